@@ -1,0 +1,162 @@
+/* CPU oracle for the mojoboost-amd GBDT training path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is a plain C++ restatement of the
+ * reference (ajhendel/mojoboost, package `mojotrees`) CPU training algorithm,
+ * used as the parity checker for the HIP path and as the CPU baseline timed by
+ * bench.py. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product library (mojoboost_amd/) never links or calls
+ * it.
+ *
+ * Every function names the reference file:line it follows in oracle.cpp.
+ * Pinning (what checks each part) is listed at the top of oracle.cpp.
+ */
+#ifndef MOJOBOOST_ORACLE_H
+#define MOJOBOOST_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_OBJ_L2 0
+#define ORC_OBJ_BINARY 1
+#define ORC_OBJ_MULTICLASS 2
+
+typedef struct {
+    int32_t objective;          /* ORC_OBJ_* */
+    int32_t num_class;          /* multiclass only */
+    int32_t num_iterations;
+    double learning_rate;
+    int32_t num_leaves;
+    int32_t min_data_in_leaf;
+    double lambda_l2;
+    double lambda_l1;
+    double min_sum_hessian;
+    int32_t max_depth;          /* <= 0: unlimited */
+    double feature_fraction;
+    int32_t feature_fraction_seed;
+    double bagging_fraction;
+    int32_t bagging_freq;
+    int32_t bagging_seed;
+    int32_t use_quantized_grad;
+    int32_t num_grad_quant_bins;
+    int32_t stochastic_rounding;
+    int32_t quant_seed;
+    int32_t goss;
+    double top_rate;
+    double other_rate;
+    int32_t goss_seed;
+    int32_t n_threads;          /* <= 0: hardware concurrency */
+    int32_t fused_score_update; /* 1: raw = fma(lr, v, raw) (reference default) */
+    int32_t fused_predict;      /* 1: prediction sums with fma */
+    int32_t totals_tree_reduce; /* 1: SIMD totals reduced pairwise (Mojo reduce) */
+    int32_t use_init_base;      /* 1: start every row at init_base (single output) */
+    double init_base;
+} orc_params;
+
+/* A trained model in flat arrays. Trees are laid out one after another;
+ * tree t owns nodes [node_offset[t], node_offset[t + 1]). */
+typedef struct orc_model orc_model;
+
+/* -------------------------------------------------------------- arithmetic */
+uint64_t orc_splitmix64(uint64_t state);
+double orc_uniform(uint64_t counter);
+double orc_exp(double x);
+double orc_log(double x);
+double orc_sigmoid(double x);
+uint64_t orc_quant_stream(int64_t seed, int64_t round_index,
+                          int64_t class_index, int64_t plane);
+
+/* ---------------------------------------------------------------- binning */
+int32_t orc_bin_equal_width(const double *x, int64_t n_rows,
+                            int32_t n_features, int32_t n_bins,
+                            uint8_t *out_bins);
+/* fit_bins + transform. out_edges is n_features * max_bins doubles,
+ * out_n_edges and out_missing_bin n_features each. Returns 0 on success. */
+int32_t orc_fit_bins(const double *x, int64_t n_rows, int32_t n_features,
+                     int32_t max_bins, int32_t min_data_in_bin,
+                     int32_t use_missing, int64_t sample_cnt, int64_t seed,
+                     double *out_edges, int32_t *out_n_edges,
+                     int32_t *out_missing_bin);
+int32_t orc_transform(const double *x, int64_t n_rows, int32_t n_features,
+                      int32_t max_bins, const double *edges,
+                      const int32_t *n_edges, const int32_t *missing_bin,
+                      uint8_t *out_bins);
+
+/* ------------------------------------------------------------- objectives */
+/* Per-row narrowed derivatives. labels are class ids for multiclass. */
+int32_t orc_grad_hess(int32_t objective, const double *raw,
+                      const double *labels, int64_t n_rows,
+                      int32_t num_class, int32_t class_k, double *grad,
+                      double *hess);
+
+/* ----------------------------------------------------------- quantization */
+/* gradient_stats + derive_scales (max-abs rule) + per-row rounding.
+ * rows may be NULL (every row). Writes q_grad/q_hess (all n rows) and
+ * out_scales[0..1] = grad_units, hess_units; out_limits = max units. */
+int32_t orc_quantize(const double *grad, const double *hess, int64_t n_rows,
+                     const int32_t *rows, int64_t n_sel, int32_t quant_bins,
+                     int32_t stochastic, int64_t seed, int64_t round_index,
+                     int64_t class_index, int32_t const_hessian,
+                     int8_t *q_grad, int8_t *q_hess, double *out_scales);
+
+/* ------------------------------------------------------------ histograms */
+/* Integer histogram over `rows` (or all rows when rows == NULL):
+ * out is n_features * n_bins cells of int64 {grad, hess, count}. */
+int32_t orc_hist_quantized(const uint8_t *bins, int64_t n_rows,
+                           int32_t n_features, int32_t n_bins,
+                           const int8_t *q_grad, const int8_t *q_hess,
+                           const int32_t *rows, int64_t n_sel,
+                           int64_t *out);
+/* Float64 histogram (reference order), cells {grad, hess} + counts. */
+int32_t orc_hist_float(const uint8_t *bins, int64_t n_rows,
+                       int32_t n_features, int32_t n_bins,
+                       const double *grad, const double *hess,
+                       const int32_t *rows, int64_t n_sel,
+                       int32_t row_blocks, double *out_gh,
+                       int64_t *out_count);
+
+/* ----------------------------------------------------------- split search */
+/* Best split of one node from an integer histogram. Returns found (0/1);
+ * out_feature, out_bin, out_default_left, out_gain. */
+int32_t orc_split_quantized(const int64_t *hist, int32_t n_features,
+                            int32_t n_bins, const int32_t *missing_bin,
+                            const int32_t *widths, double grad_units,
+                            double hess_units, double lambda_l1,
+                            double lambda_l2, double min_sum_hessian,
+                            int32_t min_data_in_leaf, int32_t *out_feature,
+                            int32_t *out_bin, int32_t *out_default_left,
+                            double *out_gain);
+
+/* --------------------------------------------------------------- training */
+orc_model *orc_train(const uint8_t *bins, int64_t n_rows, int32_t n_features,
+                     int32_t n_bins, const int32_t *missing_bin,
+                     const double *labels, const orc_params *params,
+                     char *err, int32_t err_len);
+void orc_model_free(orc_model *model);
+int32_t orc_model_num_trees(const orc_model *model);
+int32_t orc_model_num_class(const orc_model *model);
+int64_t orc_model_total_nodes(const orc_model *model);
+/* base has num_class entries. node_offset has num_trees + 1 entries. */
+void orc_model_arrays(const orc_model *model, double *base,
+                      int64_t *node_offset, int32_t *feature,
+                      int32_t *threshold_bin, int32_t *left, int32_t *right,
+                      double *value, int32_t *default_left,
+                      int32_t *missing_bin, double *split_gain,
+                      double *count);
+/* Training-time raw scores after the last round, row-major n * num_class. */
+void orc_model_train_raw(const orc_model *model, double *out);
+/* Per-round wall seconds, num_iterations entries (0 for rounds not run). */
+void orc_model_round_seconds(const orc_model *model, double *out);
+
+/* Prediction over a binned matrix: raw (row-major n * k) and response. */
+int32_t orc_predict_binned(const orc_model *model, const uint8_t *bins,
+                           int64_t n_rows, int32_t n_features, double *raw,
+                           double *response);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOJOBOOST_ORACLE_H */

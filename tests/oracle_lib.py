@@ -1,0 +1,271 @@
+"""ctypes binding to the CPU oracle (oracle/_build/liboracle.so).
+
+Test infrastructure only: the oracle is the parity checker and the CPU
+baseline, never part of the product path.
+"""
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = ROOT / "oracle" / "_build" / "liboracle.so"
+
+OBJ_L2, OBJ_BINARY, OBJ_MULTICLASS = 0, 1, 2
+
+
+class Params(C.Structure):
+    _fields_ = [
+        ("objective", C.c_int32),
+        ("num_class", C.c_int32),
+        ("num_iterations", C.c_int32),
+        ("learning_rate", C.c_double),
+        ("num_leaves", C.c_int32),
+        ("min_data_in_leaf", C.c_int32),
+        ("lambda_l2", C.c_double),
+        ("lambda_l1", C.c_double),
+        ("min_sum_hessian", C.c_double),
+        ("max_depth", C.c_int32),
+        ("feature_fraction", C.c_double),
+        ("feature_fraction_seed", C.c_int32),
+        ("bagging_fraction", C.c_double),
+        ("bagging_freq", C.c_int32),
+        ("bagging_seed", C.c_int32),
+        ("use_quantized_grad", C.c_int32),
+        ("num_grad_quant_bins", C.c_int32),
+        ("stochastic_rounding", C.c_int32),
+        ("quant_seed", C.c_int32),
+        ("goss", C.c_int32),
+        ("top_rate", C.c_double),
+        ("other_rate", C.c_double),
+        ("goss_seed", C.c_int32),
+        ("n_threads", C.c_int32),
+        ("fused_score_update", C.c_int32),
+        ("fused_predict", C.c_int32),
+        ("totals_tree_reduce", C.c_int32),
+        ("use_init_base", C.c_int32),
+        ("init_base", C.c_double),
+    ]
+
+
+def default_params(**kw) -> Params:
+    p = Params(
+        objective=OBJ_L2, num_class=1, num_iterations=100, learning_rate=0.1,
+        num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0, lambda_l1=0.0,
+        min_sum_hessian=1e-3, max_depth=-1, feature_fraction=1.0,
+        feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
+        bagging_seed=3, use_quantized_grad=0, num_grad_quant_bins=4,
+        stochastic_rounding=1, quant_seed=11, goss=0, top_rate=0.2,
+        other_rate=0.1, goss_seed=3, n_threads=0, fused_score_update=1,
+        fused_predict=1, totals_tree_reduce=1, use_init_base=0, init_base=0.0,
+    )
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"oracle not built: {LIB_PATH} (run __graft_entry__.build())")
+        L = C.CDLL(str(LIB_PATH))
+        P = C.POINTER
+        L.orc_splitmix64.restype = C.c_uint64
+        L.orc_splitmix64.argtypes = [C.c_uint64]
+        L.orc_uniform.restype = C.c_double
+        L.orc_uniform.argtypes = [C.c_uint64]
+        L.orc_exp.restype = C.c_double
+        L.orc_exp.argtypes = [C.c_double]
+        L.orc_log.restype = C.c_double
+        L.orc_log.argtypes = [C.c_double]
+        L.orc_sigmoid.restype = C.c_double
+        L.orc_sigmoid.argtypes = [C.c_double]
+        L.orc_quant_stream.restype = C.c_uint64
+        L.orc_quant_stream.argtypes = [C.c_int64] * 4
+        L.orc_train.restype = C.c_void_p
+        L.orc_train.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_void_p,
+                                C.c_void_p, P(Params), C.c_char_p, C.c_int32]
+        L.orc_model_free.argtypes = [C.c_void_p]
+        L.orc_model_num_trees.restype = C.c_int32
+        L.orc_model_num_trees.argtypes = [C.c_void_p]
+        L.orc_model_num_class.restype = C.c_int32
+        L.orc_model_num_class.argtypes = [C.c_void_p]
+        L.orc_model_total_nodes.restype = C.c_int64
+        L.orc_model_total_nodes.argtypes = [C.c_void_p]
+        L.orc_model_arrays.argtypes = [C.c_void_p] + [C.c_void_p] * 11
+        L.orc_model_train_raw.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_model_round_seconds.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_predict_binned.restype = C.c_int32
+        L.orc_predict_binned.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                         C.c_void_p, C.c_void_p]
+        L.orc_bin_equal_width.restype = C.c_int32
+        L.orc_bin_equal_width.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_void_p]
+        L.orc_fit_bins.restype = C.c_int32
+        L.orc_fit_bins.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_int32,
+                                   C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
+                                   C.c_void_p]
+        L.orc_transform.restype = C.c_int32
+        L.orc_transform.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_void_p,
+                                    C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_grad_hess.restype = C.c_int32
+        L.orc_grad_hess.argtypes = [C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                    C.c_int32, C.c_void_p, C.c_void_p]
+        L.orc_quantize.restype = C.c_int32
+        L.orc_quantize.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                   C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64,
+                                   C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_hist_quantized.restype = C.c_int32
+        L.orc_hist_quantized.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
+                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                         C.c_void_p]
+        L.orc_hist_float.restype = C.c_int32
+        L.orc_hist_float.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_void_p,
+                                     C.c_void_p]
+        L.orc_split_quantized.restype = C.c_int32
+        L.orc_split_quantized.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                          C.c_void_p, C.c_double, C.c_double, C.c_double,
+                                          C.c_double, C.c_double, C.c_int32, C.c_void_p,
+                                          C.c_void_p, C.c_void_p, C.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Model:
+    """Flat-array view of an oracle model."""
+
+    def __init__(self, handle):
+        L = lib()
+        self.h = handle
+        self.n_trees = L.orc_model_num_trees(handle)
+        self.num_class = L.orc_model_num_class(handle)
+        nn = L.orc_model_total_nodes(handle)
+        self.base = np.zeros(self.num_class)
+        self.off = np.zeros(self.n_trees + 1, np.int64)
+        i32 = lambda: np.zeros(nn, np.int32)
+        f64 = lambda: np.zeros(nn, np.float64)
+        self.feature, self.threshold, self.left, self.right = i32(), i32(), i32(), i32()
+        self.value, self.default_left, self.missing_bin = f64(), i32(), i32()
+        self.gain, self.count = f64(), f64()
+        L.orc_model_arrays(handle, _ptr(self.base), _ptr(self.off), _ptr(self.feature),
+                           _ptr(self.threshold), _ptr(self.left), _ptr(self.right),
+                           _ptr(self.value), _ptr(self.default_left), _ptr(self.missing_bin),
+                           _ptr(self.gain), _ptr(self.count))
+
+    def tree(self, t):
+        a, b = self.off[t], self.off[t + 1]
+        return {k: getattr(self, k)[a:b] for k in
+                ("feature", "threshold", "left", "right", "value", "default_left",
+                 "missing_bin", "gain", "count")}
+
+    def train_raw(self, n_rows):
+        out = np.zeros(n_rows * self.num_class)
+        lib().orc_model_train_raw(self.h, _ptr(out))
+        return out
+
+    def round_seconds(self, n_iter):
+        out = np.zeros(n_iter)
+        lib().orc_model_round_seconds(self.h, _ptr(out))
+        return out
+
+    def predict_binned(self, bins_cm, n_rows, n_features):
+        raw = np.zeros(n_rows * self.num_class)
+        resp = np.zeros(n_rows * self.num_class)
+        lib().orc_predict_binned(self.h, _ptr(bins_cm), n_rows, n_features, _ptr(raw), _ptr(resp))
+        return raw, resp
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.orc_model_free(self.h)
+            self.h = None
+
+
+def train(bins_cm, n_rows, n_features, n_bins, labels, params, missing_bin=None):
+    bins_cm = np.ascontiguousarray(bins_cm, dtype=np.uint8)
+    labels = np.ascontiguousarray(labels, dtype=np.float64)
+    mb = None if missing_bin is None else np.ascontiguousarray(missing_bin, dtype=np.int32)
+    err = C.create_string_buffer(512)
+    h = lib().orc_train(_ptr(bins_cm), n_rows, n_features, n_bins, _ptr(mb), _ptr(labels),
+                        C.byref(params), err, 512)
+    if not h:
+        raise RuntimeError("oracle training failed: " + err.value.decode())
+    return Model(h)
+
+
+def bin_equal_width(x_cm, n_rows, n_features, n_bins):
+    out = np.zeros(n_rows * n_features, np.uint8)
+    rc = lib().orc_bin_equal_width(_ptr(np.ascontiguousarray(x_cm, np.float64)), n_rows,
+                                   n_features, n_bins, _ptr(out))
+    assert rc == 0
+    return out
+
+
+def fit_transform(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_missing=1,
+                  sample_cnt=200_000, seed=1):
+    x_cm = np.ascontiguousarray(x_cm, np.float64)
+    edges = np.zeros(n_features * max_bins)
+    n_edges = np.zeros(n_features, np.int32)
+    mb = np.zeros(n_features, np.int32)
+    rc = lib().orc_fit_bins(_ptr(x_cm), n_rows, n_features, max_bins, min_data_in_bin,
+                            use_missing, sample_cnt, seed, _ptr(edges), _ptr(n_edges), _ptr(mb))
+    assert rc == 0, rc
+    bins = np.zeros(n_rows * n_features, np.uint8)
+    lib().orc_transform(_ptr(x_cm), n_rows, n_features, max_bins, _ptr(edges), _ptr(n_edges),
+                        _ptr(mb), _ptr(bins))
+    return bins, edges.reshape(n_features, max_bins), n_edges, mb
+
+
+def grad_hess(objective, raw, labels, num_class=1, class_k=0):
+    n = len(labels)
+    g = np.zeros(n)
+    h = np.zeros(n)
+    lib().orc_grad_hess(objective, _ptr(np.ascontiguousarray(raw, np.float64)),
+                        _ptr(np.ascontiguousarray(labels, np.float64)), n, num_class, class_k,
+                        _ptr(g), _ptr(h))
+    return g, h
+
+
+def quantize(grad, hess, rows=None, quant_bins=4, stochastic=1, seed=11, round_index=0,
+             class_index=0, const_hessian=0):
+    n = len(grad)
+    qg = np.zeros(n, np.int8)
+    qh = np.zeros(n, np.int8)
+    sc = np.zeros(4)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    lib().orc_quantize(_ptr(np.ascontiguousarray(grad, np.float64)),
+                       _ptr(np.ascontiguousarray(hess, np.float64)), n, _ptr(r),
+                       0 if r is None else len(r), quant_bins, stochastic, seed, round_index,
+                       class_index, const_hessian, _ptr(qg), _ptr(qh), _ptr(sc))
+    return qg, qh, sc
+
+
+def hist_quantized(bins_cm, n_rows, n_features, n_bins, qg, qh, rows=None):
+    out = np.zeros(n_features * n_bins * 3, np.int64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    lib().orc_hist_quantized(_ptr(np.ascontiguousarray(bins_cm, np.uint8)), n_rows,
+                             n_features, n_bins, _ptr(np.ascontiguousarray(qg, np.int8)),
+                             _ptr(np.ascontiguousarray(qh, np.int8)), _ptr(r),
+                             0 if r is None else len(r), _ptr(out))
+    return out.reshape(n_features, n_bins, 3)
+
+
+def split_quantized(hist, missing_bin, widths, gu, hu, l1=0.0, l2=1.0, min_hess=1e-3,
+                    min_data=20):
+    nf, nb, _ = hist.shape
+    of, ob, odl = C.c_int32(), C.c_int32(), C.c_int32()
+    og = C.c_double()
+    mb = np.ascontiguousarray(missing_bin, np.int32)
+    w = None if widths is None else np.ascontiguousarray(widths, np.int32)
+    found = lib().orc_split_quantized(_ptr(np.ascontiguousarray(hist, np.int64)), nf, nb,
+                                      _ptr(mb), _ptr(w), gu, hu, l1, l2, min_hess, min_data,
+                                      C.byref(of), C.byref(ob), C.byref(odl), C.byref(og))
+    return bool(found), of.value, ob.value, bool(odl.value), og.value
