@@ -1,0 +1,130 @@
+/* mojoboost-amd device-level C ABI.
+ *
+ * The training hot path of the `mojotrees` GPU trainer, re-built for one
+ * AMD Instinct MI355X (gfx950): the binned matrix stays resident in HBM and
+ * each boosting round runs as a sequence of HIP kernels that grow the tree
+ * on the device. `mojotrees.h` (the reference's public ABI) is implemented on
+ * top of these calls; they are exported separately so benchmarks and parity
+ * tests can keep inputs resident and call individual stages.
+ *
+ * Reference interfaces these replace (ajhendel/mojoboost):
+ *   mbh_dataset_create    GpuHistogramBuilder(data) bin upload
+ *                         (src/mojotrees/histogram_gpu.mojo:591-606)
+ *   mbh_train             train_gpu / _train_gpu_rounds
+ *                         (src/mojotrees/train_gpu.mojo:5098-5168, :4235-5095)
+ *   mbh_objective_quantize  fill_gradients_device + the quantizer
+ *                         (histogram_gpu.mojo:1697-1712,
+ *                          quantized_gradient.mojo:2487-2565)
+ *   mbh_histogram         GpuActiveRows.enqueue_range_histogram
+ *                         (src/mojotrees/gpu_active_rows.mojo:8586)
+ *   mbh_exp_sigmoid       the device objective's sigmoid
+ *                         (src/mojotrees/gpu_objectives_native.mojo:417-436)
+ *
+ * Conventions: every fallible call returns 0 on success or a negative
+ * MOJOTREES_ERROR_* code and writes a NUL-terminated message into `err`
+ * (err_len bytes, may be NULL). Host buffers are the caller's and are not
+ * retained. Binned matrices are column-major uint8, bins[f * n_rows + r].
+ */
+#ifndef MOJOBOOST_HIP_H
+#define MOJOBOOST_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MBH_OBJ_REGRESSION 0
+#define MBH_OBJ_BINARY 1
+#define MBH_OBJ_MULTICLASS 2
+
+typedef struct mbh_dataset mbh_dataset;
+typedef struct mbh_fit mbh_fit;
+
+typedef struct {
+    int32_t objective;
+    int32_t num_class;
+    int32_t num_iterations;
+    double learning_rate;
+    int32_t num_leaves;
+    int32_t min_data_in_leaf;
+    double lambda_l1;
+    double lambda_l2;
+    double min_sum_hessian;
+    int32_t max_depth;
+    double feature_fraction;
+    int32_t feature_fraction_seed;
+    double bagging_fraction;
+    int32_t bagging_freq;
+    int32_t bagging_seed;
+    int32_t num_grad_quant_bins;
+    int32_t stochastic_rounding;
+    int32_t quant_seed;
+    int32_t time_histograms; /* 1: bracket each histogram launch with events */
+} mbh_params;
+
+/* Number of usable gfx950 devices (0 without a GPU or runtime). */
+int32_t mbh_device_count(void);
+
+/* Upload a binned matrix and its labels; builds the per-row records
+ * (F bin bytes + 2 gradient bytes, padded to a power of two). */
+int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n_rows,
+                           int32_t n_features, int32_t n_bins,
+                           const int32_t *missing_bin, const double *labels,
+                           mbh_dataset **out, char *err, int32_t err_len);
+void mbh_dataset_free(mbh_dataset *ds);
+
+/* Train on a resident dataset (quantized gradients, int32 histograms). */
+int32_t mbh_train(mbh_dataset *ds, const mbh_params *params, mbh_fit **out,
+                  char *err, int32_t err_len);
+void mbh_fit_free(mbh_fit *fit);
+int32_t mbh_fit_num_trees(const mbh_fit *fit);
+int32_t mbh_fit_num_class(const mbh_fit *fit);
+int64_t mbh_fit_total_nodes(const mbh_fit *fit);
+void mbh_fit_arrays(const mbh_fit *fit, double *base, int64_t *node_offset,
+                    int32_t *feature, int32_t *threshold_bin, int32_t *left,
+                    int32_t *right, double *value, int32_t *default_left,
+                    int32_t *missing_bin, double *split_gain, double *count);
+/* Final raw scores of the training rows, row-major n_rows * num_class. */
+int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
+                          int32_t err_len);
+/* out[0] wall seconds of the training loop (enqueue to final sync),
+ * out[1] summed histogram-kernel milliseconds (time_histograms only),
+ * out[2] histogram algorithmic bytes (sum over builds of rows * (F + 2)),
+ * out[3] histogram rows * features, out[4] histogram launches that built,
+ * out[5] root-build algorithmic bytes, out[6] root-build milliseconds,
+ * out[7] trees grown. */
+void mbh_fit_stats(const mbh_fit *fit, double *out);
+
+/* ------------------------------------------- stage-level (parity, bench) */
+/* Device exp and sigmoid of x[0..n). */
+int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp,
+                        double *out_sigmoid, char *err, int32_t err_len);
+
+/* One round's gradient pass and quantizer on a resident dataset, from the
+ * given raw scores (n_rows): writes narrowed grad/hess, int8 q_grad/q_hess and
+ * scales[0..1] = grad units, hess units. */
+int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *params,
+                               const double *raw, int64_t round_index,
+                               float *grad, float *hess, int8_t *q_grad,
+                               int8_t *q_hess, double *scales, char *err,
+                               int32_t err_len);
+
+/* Histogram of the rows `rows[0..n_sel)` (all rows when rows is NULL) with the
+ * given int8 q_grad/q_hess: out is n_features * n_bins * 3 int32
+ * {grad, hess, count}. */
+int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad,
+                      const int8_t *q_hess, const int32_t *rows,
+                      int64_t n_sel, int32_t num_grad_quant_bins,
+                      int32_t *out, char *err, int32_t err_len);
+
+/* Root histogram of all rows, `reps` times back to back on resident data:
+ * out_ms[0] mean kernel milliseconds (HIP events), out_ms[1] min. */
+int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps,
+                                 double *out_ms, char *err, int32_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOJOBOOST_HIP_H */

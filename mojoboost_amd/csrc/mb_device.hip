@@ -1,0 +1,698 @@
+// Host control plane of the device-resident trainer: dataset residency, the
+// per-round kernel sequence, tree download, and the stage-level entry points
+// of include/mojoboost_hip.h.
+//
+// A round enqueues, per tree: objective, quantize, root histogram, root split,
+// then (num_leaves - 1) x [partition, histogram, split], score update and
+// round end. No call reads device memory back until the last tree is
+// enqueued; kernels whose step is inactive (the tree stopped early) return
+// at once.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/mojoboost_hip.h"
+#include "../../include/mojotrees.h"
+#include "mb_kernels.h"
+#include "mb_math.h"
+#include "mb_state.h"
+
+namespace {
+
+struct Error {
+    int32_t code;
+    std::string msg;
+};
+
+void set_err(char *err, int32_t len, const std::string &m) {
+    if (err && len > 0) std::snprintf(err, (size_t)len, "%s", m.c_str());
+}
+
+#define HIPX(expr)                                                                        \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            throw Error{MOJOTREES_ERROR_TRAINING,                                         \
+                        std::string("HIP error in ") + #expr + ": " + hipGetErrorString(e_)}; \
+    } while (0)
+
+template <class T>
+T *dalloc(size_t count, std::vector<void *> &owned) {
+    void *p = nullptr;
+    size_t bytes = count * sizeof(T);
+    if (bytes == 0) bytes = sizeof(T);
+    HIPX(hipMalloc(&p, bytes));
+    owned.push_back(p);
+    return (T *)p;
+}
+
+int device_count_gfx950() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    int good = 0;
+    for (int i = 0; i < n; ++i) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) != hipSuccess) continue;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++good;
+    }
+    return good;
+}
+
+// sampling.select_tree_features (src/mojotrees/sampling.mojo:319-465):
+// selection sampling of round(F * fraction + 0.5) features (at least 2),
+// keyed by (seed, tree index).
+std::vector<uint8_t> tree_feature_mask(int F, double fraction, int64_t seed, int64_t tree_index) {
+    std::vector<uint8_t> mask(F, 1);
+    if (fraction >= 1.0) return mask;
+    int count = (int)((double)F * fraction + 0.5);
+    int floor_count = F >= 2 ? 2 : F;
+    if (count < floor_count) count = floor_count;
+    if (count > F) count = F;
+    uint64_t h = mb::splitmix64((uint64_t)(seed & 0x7FFFFFFFFFFFFFFFLL));
+    h = mb::splitmix64(h ^ (uint64_t)(tree_index & 0x7FFFFFFFFFFFFFFFLL));
+    uint64_t stream = mb::splitmix64(h ^ 0ULL);
+    std::fill(mask.begin(), mask.end(), 0);
+    int chosen = 0;
+    for (int i = 0; i < F && chosen < count; ++i) {
+        double prob = (double)(count - chosen) / (double)(F - i);
+        if (mb::uniform53(stream + (uint64_t)i) < prob) {
+            mask[i] = 1;
+            ++chosen;
+        }
+    }
+    return mask;
+}
+
+}  // namespace
+
+struct mbh_dataset {
+    int64_t n = 0;
+    int F = 0, nb = 0, rec = 0, lds_stride = 0;
+    int device = 0;
+    int n_cu = 0;
+    uint8_t *d_records = nullptr, *d_bins_cm = nullptr;
+    double *d_labels = nullptr;
+    int32_t *d_missing = nullptr, *d_widths = nullptr;
+    std::vector<int32_t> missing, widths;
+    double label_sum = 0.0;  // sequential sum, for the base score
+    std::vector<double> class_count;
+    double label_min = 0.0, label_max = 0.0;
+    std::vector<void *> owned;
+    ~mbh_dataset() {
+        for (void *p : owned) (void)hipFree(p);
+    }
+};
+
+struct mbh_fit {
+    int num_class = 1;
+    int objective = 0;
+    int n_features = 0;
+    double learning_rate = 0.1;
+    std::vector<double> base;
+    std::vector<int64_t> offsets{0};
+    std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
+    std::vector<double> value, gain, count;
+    std::vector<double> train_raw;
+    double stats[8] = {0};
+};
+
+namespace {
+
+struct Run {
+    std::vector<void *> owned;
+    ~Run() {
+        for (void *p : owned) (void)hipFree(p);
+    }
+};
+
+int64_t chunk_limit_for(int B) {
+    // rows per LDS accumulation so no packed field overflows:
+    // count < 2^20, hess sum < 2^22 (|h| <= B + 1), |grad sum| < 2^21
+    // (|g| <= B/2 + 1; +1 covers the rounding edge at the clamp).
+    int64_t lim = (1 << 20) - 1;
+    lim = std::min<int64_t>(lim, ((1 << 22) - 1) / (B + 1));
+    lim = std::min<int64_t>(lim, ((1 << 21) - 1) / (B / 2 + 1));
+    return lim;
+}
+
+void check_params(const mbh_dataset *ds, const mbh_params *p) {
+    auto bad = [](const std::string &m) { throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, m}; };
+    auto unsup = [](const std::string &m) { throw Error{MOJOTREES_ERROR_UNSUPPORTED, m}; };
+    if (p->objective != MBH_OBJ_REGRESSION && p->objective != MBH_OBJ_BINARY) {
+        if (p->objective == MBH_OBJ_MULTICLASS)
+            unsup("multiclass training is not built on the device path yet");
+        bad("unknown objective");
+    }
+    if (p->num_iterations < 0) bad("num_iterations must be nonnegative");
+    if (p->num_leaves < 1 || p->num_leaves > 4096) bad("num_leaves must be in [1, 4096]");
+    if (p->min_data_in_leaf < 0) bad("min_data_in_leaf must be nonnegative");
+    if (!(p->learning_rate > 0.0)) bad("learning_rate must be positive");
+    if (!(p->lambda_l2 >= 0.0) || !(p->lambda_l1 >= 0.0)) bad("lambda_l1 and lambda_l2 must be nonnegative");
+    if (!(p->min_sum_hessian >= 0.0)) bad("min_sum_hessian_in_leaf must be nonnegative");
+    if (!(p->feature_fraction > 0.0 && p->feature_fraction <= 1.0)) bad("feature_fraction must be in (0, 1]");
+    if (!(p->bagging_fraction > 0.0 && p->bagging_fraction <= 1.0)) bad("bagging_fraction must be in (0, 1]");
+    if (p->bagging_freq < 0) bad("bagging_freq must be nonnegative");
+    const int B = p->num_grad_quant_bins;
+    if (B < 2 || B > 126 || B % 2 != 0)
+        unsup("num_grad_quant_bins must be even and in [2, 126] (int8 gradient storage)");
+    if ((double)ds->n * (double)(B + 1) >= 2147483647.0)
+        unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
+    if (p->objective == MBH_OBJ_BINARY && (ds->label_min < 0.0 || ds->label_max > 1.0))
+        bad("binary labels must be in [0, 1]");
+}
+
+double base_score_for(const mbh_dataset *ds, int objective) {
+    // boosting._base_score (src/mojotrees/boosting.mojo:521-568): the
+    // sequential label mean; binary takes the clamped log-odds.
+    double mean = ds->label_sum / (double)ds->n;
+    if (objective == MBH_OBJ_BINARY) {
+        double p = mean;
+        if (p < 1e-15) p = 1e-15;
+        if (p > 1.0 - 1e-15) p = 1.0 - 1e-15;
+        return mb::ref_log(p / (1.0 - p));
+    }
+    return mean;
+}
+
+struct TrainBuffers {
+    mb::DevState s{};
+    int T = 0, L = 0, max_nodes = 0;
+};
+
+TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
+    TrainBuffers tb;
+    const int K = 1;
+    const int L = p->num_leaves;
+    const int T = std::max(1, p->num_iterations * K);
+    const int max_nodes = 2 * L - 1;
+    const int F = ds->F;
+    mb::DevState &s = tb.s;
+    s.records = ds->d_records;
+    s.records_w = ds->d_records;
+    s.bins_cm = ds->d_bins_cm;
+    s.labels = ds->d_labels;
+    s.missing_bin = ds->d_missing;
+    s.widths = ds->d_widths;
+    s.n = ds->n;
+    s.n_features = F;
+    s.n_bins = ds->nb;
+    s.rec_bytes = ds->rec;
+    s.lds_stride = ds->lds_stride;
+    s.raw = dalloc<double>((size_t)ds->n * K, run.owned);
+    s.grad = dalloc<float>(ds->n, run.owned);
+    s.hess = dalloc<float>(ds->n, run.owned);
+    s.stats = dalloc<uint32_t>(4, run.owned);
+    s.round = dalloc<mb::Round>(1, run.owned);
+    s.rows0 = dalloc<int32_t>(ds->n, run.owned);
+    s.rows1 = dalloc<int32_t>(ds->n, run.owned);
+    s.hist = dalloc<int32_t>((size_t)L * F * ds->nb * 3, run.owned);
+    s.step = dalloc<mb::Step>(1, run.owned);
+    s.slots = dalloc<mb::Slot>(L, run.owned);
+    s.scan = dalloc<mb::ScanResult>(2 * (size_t)F, run.owned);
+    s.ticket = dalloc<uint32_t>(1, run.owned);
+    s.cursor = dalloc<int64_t>(2, run.owned);
+    s.error = dalloc<int32_t>(1, run.owned);
+    s.t_feature = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_threshold = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_left = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_right = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_default_left = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_missing_bin = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_value = dalloc<double>(max_nodes, run.owned);
+    s.t_gain = dalloc<double>(max_nodes, run.owned);
+    s.t_count = dalloc<double>(max_nodes, run.owned);
+    s.t_meta = dalloc<int32_t>(2, run.owned);
+    s.arc_int = dalloc<int32_t>((size_t)T * (6 * max_nodes + 2), run.owned);
+    s.arc_dbl = dalloc<double>((size_t)T * 3 * max_nodes, run.owned);
+    s.arc_rows = dalloc<int64_t>((size_t)T * L, run.owned);
+    s.max_nodes = max_nodes;
+    uint8_t *fmask = dalloc<uint8_t>((size_t)T * F, run.owned);
+    s.feature_mask = fmask;
+    mb::HyperParams &hp = s.hp;
+    hp.objective = p->objective;
+    hp.num_class = K;
+    hp.num_leaves = L;
+    hp.min_data_in_leaf = p->min_data_in_leaf;
+    hp.max_depth = p->max_depth;
+    hp.quant_bins = p->num_grad_quant_bins;
+    hp.stochastic = p->stochastic_rounding;
+    hp.quant_seed = p->quant_seed;
+    // boosting.round_has_constant_hessian: squared error without weights.
+    hp.const_hessian = p->objective == MBH_OBJ_REGRESSION ? 1 : 0;
+    hp.bagging = (p->bagging_freq > 0 && p->bagging_fraction < 1.0) ? 1 : 0;
+    hp.bagging_freq = p->bagging_freq;
+    hp.bagging_seed = p->bagging_seed;
+    hp.bagging_fraction = p->bagging_fraction;
+    hp.learning_rate = p->learning_rate;
+    hp.lambda_l1 = p->lambda_l1;
+    hp.lambda_l2 = p->lambda_l2;
+    hp.min_sum_hessian = p->min_sum_hessian;
+
+    HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
+    HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
+    HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
+    HIPX(hipMemset(s.step, 0, sizeof(mb::Step)));
+    HIPX(hipMemset(s.ticket, 0, sizeof(uint32_t)));
+    HIPX(hipMemset(s.cursor, 0, 2 * sizeof(int64_t)));
+    HIPX(hipMemset(s.error, 0, sizeof(int32_t)));
+    HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));
+    HIPX(hipMemset(s.arc_rows, 0, (size_t)T * L * sizeof(int64_t)));
+    HIPX(hipMemset(s.arc_int, 0, (size_t)T * (6 * max_nodes + 2) * sizeof(int32_t)));
+    mb::Round r0{};
+    HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
+    std::vector<uint8_t> masks((size_t)T * F);
+    for (int t = 0; t < T; ++t) {
+        std::vector<uint8_t> m = tree_feature_mask(F, p->feature_fraction, p->feature_fraction_seed, t);
+        std::memcpy(masks.data() + (size_t)t * F, m.data(), F);
+    }
+    HIPX(hipMemcpy(fmask, masks.data(), masks.size(), hipMemcpyHostToDevice));
+    tb.T = T;
+    tb.L = L;
+    tb.max_nodes = max_nodes;
+    return tb;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t mbh_device_count(void) { return device_count_gfx950(); }
+
+int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t nb,
+                           const int32_t *missing_bin, const double *labels, mbh_dataset **out,
+                           char *err, int32_t err_len) {
+    if (!bins_cm || !labels || !out || n <= 0 || F <= 0 || nb < 2 || nb > 256) {
+        set_err(err, err_len, "invalid dataset arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    if (n >= (int64_t)1 << 31) {
+        set_err(err, err_len, "n_rows must be below 2^31 (int32 row ids)");
+        return MOJOTREES_ERROR_UNSUPPORTED;
+    }
+    if (device_count_gfx950() == 0) {
+        set_err(err, err_len, "no gfx950 (MI355X) device is available to this process");
+        return MOJOTREES_ERROR_UNSUPPORTED;
+    }
+    auto *ds = new mbh_dataset();
+    try {
+        ds->n = n;
+        ds->F = F;
+        ds->nb = nb;
+        int rec = 16;
+        while (rec < F + 2) rec *= 2;
+        if (rec > 128)
+            throw Error{MOJOTREES_ERROR_UNSUPPORTED,
+                        "more than 126 features needs the feature-tiled histogram, not built yet"};
+        ds->rec = rec;
+        ds->lds_stride = nb | 1;
+        if ((size_t)F * ds->lds_stride * 8 > 160 * 1024)
+            throw Error{MOJOTREES_ERROR_UNSUPPORTED,
+                        "n_features * n_bins exceeds one workgroup's LDS (160 KiB of packed counters)"};
+        // validate bins and derive the realized widths (binning.histogram_widths)
+        ds->missing.assign(F, -1);
+        if (missing_bin)
+            for (int f = 0; f < F; ++f) ds->missing[f] = missing_bin[f];
+        ds->widths.assign(F, 1);
+        for (int f = 0; f < F; ++f) {
+            const uint8_t *col = bins_cm + (size_t)f * n;
+            int mx = 0;
+            for (int64_t r = 0; r < n; ++r) mx = std::max(mx, (int)col[r]);
+            if (mx >= nb) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "a bin id is >= n_bins"};
+            if (ds->missing[f] >= nb) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "missing bin out of range"};
+            int w = std::max(1, mx + 1);
+            w = std::max(w, ds->missing[f] + 1);
+            ds->widths[f] = std::min(w, nb);
+        }
+        double sum = 0.0, lo = labels[0], hi = labels[0];
+        for (int64_t r = 0; r < n; ++r) {
+            const double y = labels[r];
+            if (!std::isfinite(y)) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "labels must be finite"};
+            sum += 1.0 * y;
+            lo = std::min(lo, y);
+            hi = std::max(hi, y);
+        }
+        ds->label_sum = sum;
+        ds->label_min = lo;
+        ds->label_max = hi;
+        HIPX(hipGetDevice(&ds->device));
+        hipDeviceProp_t prop;
+        HIPX(hipGetDeviceProperties(&prop, ds->device));
+        ds->n_cu = prop.multiProcessorCount;
+        ds->d_bins_cm = dalloc<uint8_t>((size_t)F * n, ds->owned);
+        ds->d_records = dalloc<uint8_t>((size_t)rec * n, ds->owned);
+        ds->d_labels = dalloc<double>(n, ds->owned);
+        ds->d_missing = dalloc<int32_t>(F, ds->owned);
+        ds->d_widths = dalloc<int32_t>(F, ds->owned);
+        HIPX(hipMemcpy(ds->d_bins_cm, bins_cm, (size_t)F * n, hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(ds->d_labels, labels, (size_t)n * sizeof(double), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(ds->d_missing, ds->missing.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(ds->d_widths, ds->widths.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
+        HIPX(mb::launch_build_records(ds->d_bins_cm, ds->d_records, n, F, rec, 4 * ds->n_cu, nullptr));
+        HIPX(hipDeviceSynchronize());
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        delete ds;
+        return e.code;
+    }
+    *out = ds;
+    return MOJOTREES_OK;
+}
+
+void mbh_dataset_free(mbh_dataset *ds) { delete ds; }
+
+int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err, int32_t err_len) {
+    if (!ds || !p || !out) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    auto *fit = new mbh_fit();
+    std::vector<hipEvent_t> events;
+    try {
+        check_params(ds, p);
+        Run run;
+        TrainBuffers tb = setup_state(ds, p, run);
+        mb::DevState &s = tb.s;
+        const int K = 1;
+        fit->num_class = K;
+        fit->objective = p->objective;
+        fit->n_features = ds->F;
+        fit->learning_rate = p->learning_rate;
+        fit->base.assign(K, base_score_for(ds, p->objective));
+        double *d_base = dalloc<double>(K, run.owned);
+        HIPX(hipMemcpy(d_base, fit->base.data(), K * sizeof(double), hipMemcpyHostToDevice));
+        const int grid_rows = 8 * ds->n_cu;
+        HIPX(mb::launch_fill_f64(s.raw, ds->n, K, d_base, grid_rows, nullptr));
+        HIPX(mb::prepare_hist(s));
+        HIPX(hipDeviceSynchronize());
+        const int64_t climit = chunk_limit_for(p->num_grad_quant_bins);
+        const int grid_hist = 2 * ds->n_cu;
+        const int grid_part = 4 * ds->n_cu;
+        const int L = tb.L;
+        const int T = p->num_iterations * K;
+        const bool timed = p->time_histograms != 0;
+        hipStream_t st = nullptr;
+        if (timed) events.resize((size_t)2 * L);
+        for (auto &e : events) HIPX(hipEventCreate(&e));
+        double hist_ms = 0.0, root_ms = 0.0;
+        auto t0 = std::chrono::steady_clock::now();
+        for (int t = 0; t < T; ++t) {
+            HIPX(mb::launch_objective(s, grid_rows, st));
+            HIPX(mb::launch_quantize(s, grid_rows, st));
+            if (timed) HIPX(hipEventRecord(events[0], st));
+            HIPX(mb::launch_hist(s, 1, grid_hist, climit, st));
+            if (timed) HIPX(hipEventRecord(events[1], st));
+            HIPX(mb::launch_split(s, 1, st));
+            for (int k = 1; k < L; ++k) {
+                HIPX(mb::launch_partition(s, grid_part, st));
+                if (timed) HIPX(hipEventRecord(events[2 * k], st));
+                HIPX(mb::launch_hist(s, 0, grid_hist, climit, st));
+                if (timed) HIPX(hipEventRecord(events[2 * k + 1], st));
+                HIPX(mb::launch_split(s, 0, st));
+            }
+            HIPX(mb::launch_score(s, grid_rows, st));
+            HIPX(mb::launch_round_end(s, st));
+            if (timed) {
+                HIPX(hipStreamSynchronize(st));
+                for (int k = 0; k < L; ++k) {
+                    float ms = 0.f;
+                    HIPX(hipEventElapsedTime(&ms, events[2 * k], events[2 * k + 1]));
+                    hist_ms += ms;
+                    if (k == 0) root_ms += ms;
+                }
+            }
+        }
+        HIPX(hipStreamSynchronize(st));
+        auto t1 = std::chrono::steady_clock::now();
+        int32_t h_error = 0;
+        HIPX(hipMemcpy(&h_error, s.error, sizeof(int32_t), hipMemcpyDeviceToHost));
+        if (h_error) throw Error{MOJOTREES_ERROR_TRAINING, "device partition overflowed its range (internal error)"};
+        const int mn = tb.max_nodes;
+        std::vector<int32_t> ai((size_t)tb.T * (6 * mn + 2));
+        std::vector<double> ad((size_t)tb.T * 3 * mn);
+        std::vector<int64_t> ar((size_t)tb.T * L);
+        HIPX(hipMemcpy(ai.data(), s.arc_int, ai.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(ad.data(), s.arc_dbl, ad.size() * sizeof(double), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(ar.data(), s.arc_rows, ar.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
+        fit->train_raw.resize((size_t)ds->n * K);
+        HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
+                       hipMemcpyDeviceToHost));
+        const bool bagging = s.hp.bagging != 0;
+        double bytes = 0.0, rowsfeat = 0.0, builds = 0.0, root_bytes = 0.0;
+        int grown = 0;
+        for (int t = 0; t < T; ++t) {
+            const int32_t *ti = ai.data() + (size_t)t * (6 * mn + 2);
+            const double *td = ad.data() + (size_t)t * 3 * mn;
+            const int nn = ti[6 * mn], nl = ti[6 * mn + 1];
+            for (int k = 0; k < L; ++k) {
+                const int64_t rows = ar[(size_t)t * L + k];
+                if (k > 0 && k >= nl) break;
+                bytes += (double)rows * (ds->F + 2);
+                rowsfeat += (double)rows * ds->F;
+                builds += 1;
+                if (k == 0) root_bytes += (double)rows * (ds->F + 2);
+            }
+            // boosting._boost_rounds stopping rule (boosting.mojo:2898-2907)
+            if (nl == 1 && std::fabs(td[0]) < 1e-12) {
+                if (bagging) continue;
+                break;
+            }
+            for (int i = 0; i < nn; ++i) {
+                fit->feature.push_back(ti[6 * i + 0]);
+                fit->threshold.push_back(ti[6 * i + 1]);
+                fit->left.push_back(ti[6 * i + 2]);
+                fit->right.push_back(ti[6 * i + 3]);
+                fit->default_left.push_back(ti[6 * i + 4]);
+                fit->missing_bin.push_back(ti[6 * i + 5]);
+                fit->value.push_back(td[3 * i + 0]);
+                fit->gain.push_back(td[3 * i + 1]);
+                fit->count.push_back(td[3 * i + 2]);
+            }
+            fit->offsets.push_back((int64_t)fit->feature.size());
+            ++grown;
+        }
+        fit->stats[0] = std::chrono::duration<double>(t1 - t0).count();
+        fit->stats[1] = hist_ms;
+        fit->stats[2] = bytes;
+        fit->stats[3] = rowsfeat;
+        fit->stats[4] = builds;
+        fit->stats[5] = root_bytes;
+        fit->stats[6] = root_ms;
+        fit->stats[7] = grown;
+        for (auto &e : events) (void)hipEventDestroy(e);
+        events.clear();
+    } catch (const Error &e) {
+        for (auto &ev : events) (void)hipEventDestroy(ev);
+        set_err(err, err_len, e.msg);
+        delete fit;
+        return e.code;
+    }
+    *out = fit;
+    return MOJOTREES_OK;
+}
+
+void mbh_fit_free(mbh_fit *fit) { delete fit; }
+int32_t mbh_fit_num_trees(const mbh_fit *fit) { return (int32_t)fit->offsets.size() - 1; }
+int32_t mbh_fit_num_class(const mbh_fit *fit) { return fit->num_class; }
+int64_t mbh_fit_total_nodes(const mbh_fit *fit) { return (int64_t)fit->feature.size(); }
+void mbh_fit_arrays(const mbh_fit *fit, double *base, int64_t *off, int32_t *feature, int32_t *thr,
+                    int32_t *left, int32_t *right, double *value, int32_t *dl, int32_t *mb_,
+                    double *gain, double *count) {
+    for (int k = 0; k < fit->num_class; ++k) base[k] = fit->base[k];
+    std::memcpy(off, fit->offsets.data(), fit->offsets.size() * sizeof(int64_t));
+    const size_t nn = fit->feature.size();
+    std::memcpy(feature, fit->feature.data(), nn * sizeof(int32_t));
+    std::memcpy(thr, fit->threshold.data(), nn * sizeof(int32_t));
+    std::memcpy(left, fit->left.data(), nn * sizeof(int32_t));
+    std::memcpy(right, fit->right.data(), nn * sizeof(int32_t));
+    std::memcpy(value, fit->value.data(), nn * sizeof(double));
+    std::memcpy(dl, fit->default_left.data(), nn * sizeof(int32_t));
+    std::memcpy(mb_, fit->missing_bin.data(), nn * sizeof(int32_t));
+    std::memcpy(gain, fit->gain.data(), nn * sizeof(double));
+    std::memcpy(count, fit->count.data(), nn * sizeof(double));
+}
+int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err, int32_t err_len) {
+    if (!fit || !out) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    std::memcpy(out, fit->train_raw.data(), fit->train_raw.size() * sizeof(double));
+    return MOJOTREES_OK;
+}
+void mbh_fit_stats(const mbh_fit *fit, double *out) {
+    for (int i = 0; i < 8; ++i) out[i] = fit->stats[i];
+}
+
+int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out_sig, char *err,
+                        int32_t err_len) {
+    if (!x || !out_exp || !out_sig || n <= 0) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    if (device_count_gfx950() == 0) {
+        set_err(err, err_len, "no gfx950 device");
+        return MOJOTREES_ERROR_UNSUPPORTED;
+    }
+    Run run;
+    try {
+        double *dx = dalloc<double>(n, run.owned), *de = dalloc<double>(n, run.owned),
+               *dsg = dalloc<double>(n, run.owned);
+        HIPX(hipMemcpy(dx, x, n * sizeof(double), hipMemcpyHostToDevice));
+        HIPX(mb::launch_exp_sigmoid(dx, de, dsg, n, nullptr));
+        HIPX(hipMemcpy(out_exp, de, n * sizeof(double), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(out_sig, dsg, n * sizeof(double), hipMemcpyDeviceToHost));
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const double *raw,
+                               int64_t round_index, float *grad, float *hess, int8_t *q_grad,
+                               int8_t *q_hess, double *scales, char *err, int32_t err_len) {
+    if (!ds || !p || !raw || !grad || !hess || !q_grad || !q_hess || !scales) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        check_params(ds, p);
+        Run run;
+        mbh_params p1 = *p;
+        p1.num_iterations = 1;
+        TrainBuffers tb = setup_state(ds, &p1, run);
+        mb::DevState &s = tb.s;
+        mb::Round r0{};
+        r0.round = round_index;
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(s.raw, raw, ds->n * sizeof(double), hipMemcpyHostToDevice));
+        const int grid = 8 * ds->n_cu;
+        HIPX(mb::launch_objective(s, grid, nullptr));
+        HIPX(mb::launch_quantize(s, grid, nullptr));
+        HIPX(hipDeviceSynchronize());
+        HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
+        HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < ds->n; ++r) {
+            q_grad[r] = (int8_t)rec[(size_t)r * ds->rec + ds->rec - 2];
+            q_hess[r] = (int8_t)rec[(size_t)r * ds->rec + ds->rec - 1];
+        }
+        mb::Round rr;
+        HIPX(hipMemcpy(&rr, s.round, sizeof(rr), hipMemcpyDeviceToHost));
+        scales[0] = rr.grad_units;
+        scales[1] = rr.hess_units;
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hess,
+                      const int32_t *rows, int64_t n_sel, int32_t B, int32_t *out, char *err,
+                      int32_t err_len) {
+    if (!ds || !q_grad || !q_hess || !out || (rows && n_sel <= 0)) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        if (rows)
+            for (int64_t i = 0; i < n_sel; ++i)
+                if (rows[i] < 0 || rows[i] >= ds->n)
+                    throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "row id out of range"};
+        for (int64_t r = 0; r < ds->n; ++r)
+            if (q_grad[r] < -(B / 2 + 1) || q_grad[r] > B / 2 + 1 || q_hess[r] < -(B + 1) || q_hess[r] > B + 1)
+                throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "quantized value outside the lattice"};
+        Run run;
+        mbh_params p{};
+        p.objective = MBH_OBJ_BINARY;
+        p.num_iterations = 1;
+        p.num_leaves = 2;
+        p.learning_rate = 0.1;
+        p.feature_fraction = 1.0;
+        p.bagging_fraction = 1.0;
+        p.num_grad_quant_bins = B;
+        TrainBuffers tb = setup_state(ds, &p, run);
+        mb::DevState &s = tb.s;
+        // place the int8 pairs into the records
+        std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
+        HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < ds->n; ++r) {
+            rec[(size_t)r * ds->rec + ds->rec - 2] = (uint8_t)q_grad[r];
+            rec[(size_t)r * ds->rec + ds->rec - 1] = (uint8_t)q_hess[r];
+        }
+        HIPX(hipMemcpy(ds->d_records, rec.data(), rec.size(), hipMemcpyHostToDevice));
+        const size_t cells = (size_t)ds->F * ds->nb * 3;
+        HIPX(hipMemset(s.hist, 0, cells * sizeof(int32_t)));
+        if (rows) {
+            s.hp.bagging = 1;  // root range = rows0[0 .. cursor[0])
+            HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
+            int64_t c[2] = {n_sel, 0};
+            HIPX(hipMemcpy(s.cursor, c, sizeof(c), hipMemcpyHostToDevice));
+        }
+        HIPX(mb::prepare_hist(s));
+        HIPX(mb::launch_hist(s, 1, 2 * ds->n_cu, chunk_limit_for(B), nullptr));
+        HIPX(hipDeviceSynchronize());
+        HIPX(hipMemcpy(out, s.hist, cells * sizeof(int32_t), hipMemcpyDeviceToHost));
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, char *err,
+                                 int32_t err_len) {
+    if (!ds || reps <= 0 || !out_ms) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    std::vector<hipEvent_t> ev((size_t)2 * reps);
+    try {
+        Run run;
+        mbh_params p{};
+        p.objective = MBH_OBJ_BINARY;
+        p.num_iterations = 1;
+        p.num_leaves = 2;
+        p.learning_rate = 0.1;
+        p.feature_fraction = 1.0;
+        p.bagging_fraction = 1.0;
+        p.num_grad_quant_bins = 4;
+        TrainBuffers tb = setup_state(ds, &p, run);
+        mb::DevState &s = tb.s;
+        HIPX(mb::prepare_hist(s));
+        for (auto &e : ev) HIPX(hipEventCreate(&e));
+        const int64_t climit = chunk_limit_for(4);
+        for (int i = 0; i < reps; ++i) {
+            HIPX(hipEventRecord(ev[2 * i], nullptr));
+            HIPX(mb::launch_hist(s, 1, 2 * ds->n_cu, climit, nullptr));
+            HIPX(hipEventRecord(ev[2 * i + 1], nullptr));
+        }
+        HIPX(hipDeviceSynchronize());
+        double sum = 0.0, mn = 1e30;
+        for (int i = 0; i < reps; ++i) {
+            float ms = 0.f;
+            HIPX(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+            sum += ms;
+            mn = std::min(mn, (double)ms);
+        }
+        out_ms[0] = sum / reps;
+        out_ms[1] = mn;
+        for (auto &e : ev) (void)hipEventDestroy(e);
+    } catch (const Error &e) {
+        for (auto &x : ev)
+            if (x) (void)hipEventDestroy(x);
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,416 @@
+// Binning, prediction and the model file format (host side).
+#include "mb_host.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <stdexcept>
+#include <thread>
+
+#include "mb_math.h"
+
+namespace mb {
+
+namespace {
+
+template <class Fn>
+void parallel_for(int64_t n_tasks, Fn fn) {
+    int hw = (int)std::max(1u, std::thread::hardware_concurrency());
+    int nt = (int)std::min<int64_t>(n_tasks, std::min(hw, 16));
+    if (nt <= 1) {
+        for (int64_t i = 0; i < n_tasks; ++i) fn(i);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; ++t)
+        th.emplace_back([&, t] {
+            for (int64_t i = t; i < n_tasks; i += nt) fn(i);
+        });
+    for (auto &x : th) x.join();
+}
+
+std::string bits(double x) {
+    uint64_t u;
+    std::memcpy(&u, &x, 8);
+    return std::to_string(u);
+}
+
+double from_bits(const std::string &tok) {
+    uint64_t u = std::stoull(tok);
+    double d;
+    std::memcpy(&d, &u, 8);
+    return d;
+}
+
+}  // namespace
+
+int BinMapper::bin_of(int f, double v) const {
+    if (v != v) {
+        if (missing_bin[f] >= 0) return missing_bin[f];
+        v = 0.0;
+    }
+    const double *e = edges.data() + edge_offsets[f];
+    int64_t lo = 0, hi = edge_offsets[f + 1] - edge_offsets[f];
+    while (lo < hi) {
+        int64_t mid = (lo + hi) / 2;
+        if (v <= e[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    return (int)lo;
+}
+
+void BinMapper::transform(const double *x, int64_t n, uint8_t *out) const {
+    const int64_t blocks_per_col = (n + 262143) / 262144;
+    parallel_for((int64_t)n_features * blocks_per_col, [&](int64_t task) {
+        const int f = (int)(task / blocks_per_col);
+        const int64_t b = task % blocks_per_col;
+        const int64_t lo = b * 262144, hi = std::min(n, lo + 262144);
+        for (int64_t r = lo; r < hi; ++r)
+            out[(size_t)f * n + r] = (uint8_t)bin_of(f, x[(size_t)f * n + r]);
+    });
+}
+
+BinMapper fit_bins(const double *x, int64_t n, int nf, int max_bins, int min_data_in_bin,
+                   bool use_missing, int64_t sample_cnt, int64_t seed) {
+    if (max_bins < 2 || max_bins > 256) throw std::invalid_argument("max_bin must be in [2, 256]");
+    if (min_data_in_bin < 1) throw std::invalid_argument("min_data_in_bin must be positive");
+    // bin_construct_sample_rows (binning.mojo:1745): sequential selection
+    // sampling keyed by the data seed.
+    std::vector<int64_t> sample;
+    if (!(sample_cnt <= 0 || sample_cnt >= n)) {
+        uint64_t base = (uint64_t)seed * kGolden;
+        int64_t need = sample_cnt;
+        for (int64_t r = 0; r < n && need > 0; ++r) {
+            int64_t left = n - r;
+            if (need >= left || uniform53(base + (uint64_t)r) * (double)left < (double)need) {
+                sample.push_back(r);
+                --need;
+            }
+        }
+    }
+    const bool sampled = !sample.empty();
+    const int64_t n_sample = sampled ? (int64_t)sample.size() : n;
+    std::vector<std::vector<double>> per(nf);
+    std::vector<int32_t> missing(nf, -1);
+    parallel_for(nf, [&](int64_t fi) {
+        const int f = (int)fi;
+        const double *colp = x + (size_t)f * n;
+        std::vector<double> col;
+        col.reserve(n_sample);
+        for (int64_t i = 0; i < n_sample; ++i) {
+            double v = colp[sampled ? sample[i] : i];
+            if (v == v) col.push_back(v);
+        }
+        const int64_t n_valid = (int64_t)col.size();
+        const bool reserve = use_missing && n_valid < n_sample;
+        const int n_ordinary = reserve ? max_bins - 1 : max_bins;
+        std::sort(col.begin(), col.end());
+        std::vector<double> below, above;
+        // few distinct levels: edges between levels, merging levels until a
+        // bin holds min_data_in_bin rows (collect_distinct, binning.mojo:1531)
+        std::vector<double> lv;
+        std::vector<int64_t> lc;
+        bool few = true;
+        for (int64_t i = 0; i < n_valid;) {
+            int64_t j = i;
+            while (j < n_valid && col[j] == col[i]) ++j;
+            lv.push_back(col[i]);
+            lc.push_back(j - i);
+            if ((int64_t)lv.size() > n_ordinary) {
+                few = false;
+                break;
+            }
+            i = j;
+        }
+        if (few) {
+            int64_t acc = 0;
+            for (size_t j = 0; j + 1 < lv.size(); ++j) {
+                acc += lc[j];
+                if (min_data_in_bin <= 1 || acc >= min_data_in_bin) {
+                    below.push_back(lv[j]);
+                    above.push_back(lv[j + 1]);
+                    acc = 0;
+                }
+            }
+        } else {
+            // quantile boundaries (quantile_boundary_indices, :558)
+            int64_t n_ord = n_ordinary;
+            if (min_data_in_bin > 1) n_ord = std::min<int64_t>(n_ord, std::max<int64_t>(1, n_valid / min_data_in_bin));
+            for (int64_t b = 1; b < n_ord; ++b) {
+                const int64_t idx = b * n_valid / n_ord;
+                if (idx <= 0 || idx >= n_valid) continue;
+                const double w = col[idx - 1];
+                const int64_t e = std::upper_bound(col.begin() + idx, col.end(), w) - col.begin();
+                below.push_back(w);
+                above.push_back(e < n_valid ? col[e] : w);
+            }
+        }
+        // emit_quantile_edges (:583): midpoints, strictly increasing, clamped
+        std::vector<double> &out = per[f];
+        for (size_t j = 0; j < below.size(); ++j) {
+            const double lo = below[j], hi = above[j];
+            if (hi <= lo) continue;
+            double edge = (lo + hi) / 2.0;
+            if (edge != edge) edge = 0.0;
+            else if (edge >= 1e300) edge = 1e300;
+            else if (edge <= -1e300) edge = -1e300;
+            if (!out.empty() && edge <= out.back()) continue;
+            out.push_back(edge);
+        }
+        missing[f] = reserve ? (int32_t)out.size() + 1 : -1;
+    });
+    BinMapper m;
+    m.n_features = nf;
+    m.n_bins = max_bins;
+    m.missing_bin = missing;
+    m.edge_offsets.assign(1, 0);
+    for (int f = 0; f < nf; ++f) {
+        m.edges.insert(m.edges.end(), per[f].begin(), per[f].end());
+        m.edge_offsets.push_back((int64_t)m.edges.size());
+    }
+    return m;
+}
+
+void Model::predict_raw(const double *x, int64_t n, int64_t it0, int64_t it1, double *out) const {
+    const int K = num_class;
+    const int64_t t0 = it0 * K, t1 = std::min<int64_t>(it1 * K, num_trees());
+    const int64_t blocks = (n + 4095) / 4096;
+    parallel_for(blocks, [&](int64_t b) {
+        const int64_t lo = b * 4096, hi = std::min(n, lo + 4096);
+        for (int64_t r = lo; r < hi; ++r) {
+            for (int k = 0; k < K; ++k) out[r * K + k] = it0 == 0 ? base[k] : 0.0;
+            for (int64_t t = t0; t < t1; ++t) {
+                const int64_t o = offsets[t];
+                int node = 0;
+                while (feature[o + node] >= 0) {
+                    const int f = feature[o + node];
+                    const int bn = mapper.bin_of(f, x[(size_t)f * n + r]);
+                    bool go_left = (bn == missing_bin[o + node]) ? default_left[o + node] != 0
+                                                                 : bn <= threshold[o + node];
+                    node = go_left ? left[o + node] : right[o + node];
+                }
+                double &s = out[r * K + (int)(t % K)];
+                s = fma(learning_rate, value[o + node], s);  // predict_raw_row, fused
+            }
+        }
+    });
+}
+
+void Model::response(double *raw, int64_t n) const {
+    if (num_class == 1) {
+        if (objective == 1)
+            for (int64_t r = 0; r < n; ++r) raw[r] = sigmoid(raw[r]);
+        return;
+    }
+    const int K = num_class;
+    for (int64_t r = 0; r < n; ++r) {
+        double *p = raw + r * K;
+        double m = p[0];
+        for (int k = 1; k < K; ++k) m = std::max(m, p[k]);
+        double tot = 0.0;
+        for (int k = 0; k < K; ++k) {
+            p[k] = ref_exp(p[k] - m);
+            tot += p[k];
+        }
+        for (int k = 0; k < K; ++k) p[k] = p[k] / tot;
+    }
+}
+
+// The reference's v4 text model format (src/mojotrees/serialize.mojo:184-545,
+// :999-1121): whitespace-separated tokens, floats as the decimal of their
+// IEEE-754 bits, numerical features only.
+void Model::save(const std::string &path) const {
+    std::ostringstream o;
+    o << "mojotrees v4\n";
+    if (num_class == 1) {
+        o << "objective " << objective << "\n";
+        o << "learning_rate " << bits(learning_rate) << "\n";
+        o << "base_score " << bits(base[0]) << "\n";
+    } else {
+        o << "multiclass " << num_class << "\n";
+        o << "learning_rate " << bits(learning_rate) << "\n";
+        o << "base_scores";
+        for (int k = 0; k < num_class; ++k) o << " " << bits(base[k]);
+        o << "\n";
+    }
+    o << "mapper " << mapper.n_features << " " << mapper.n_bins << " " << mapper.edges.size() << "\n";
+    for (double e : mapper.edges) o << bits(e) << " ";
+    o << "\n";
+    for (int64_t v : mapper.edge_offsets) o << v << " ";
+    o << "\n";
+    for (int32_t v : mapper.missing_bin) o << v << " ";
+    o << "\n";
+    o << "trees " << num_trees() << "\n";
+    for (int64_t t = 0; t < num_trees(); ++t) {
+        const int64_t a = offsets[t], b = offsets[t + 1];
+        o << "tree " << (b - a) << " " << n_leaves[t] << "\n";
+        auto ints = [&](const std::vector<int32_t> &v) {
+            for (int64_t i = a; i < b; ++i) o << v[i] << " ";
+            o << "\n";
+        };
+        auto dbls = [&](const std::vector<double> &v) {
+            for (int64_t i = a; i < b; ++i) o << bits(v[i]) << " ";
+            o << "\n";
+        };
+        ints(feature);
+        ints(threshold);
+        ints(left);
+        ints(right);
+        dbls(value);
+        ints(default_left);
+        ints(missing_bin);
+        bool covers = true, gains = false;
+        for (int64_t i = a; i < b; ++i) {
+            covers = covers && count[i] > 0.0;
+            gains = gains || gain[i] > 0.0;
+        }
+        o << "counts " << (covers ? 1 : 0) << "\n";
+        if (covers) dbls(count);
+        o << "gains " << (gains ? 1 : 0) << "\n";
+        if (gains) dbls(gain);
+    }
+    std::ofstream f(path);
+    if (!f) throw std::runtime_error("cannot open '" + path + "' for writing");
+    f << o.str();
+    if (!f) throw std::runtime_error("cannot write '" + path + "'");
+}
+
+Model Model::load(const std::string &path) {
+    std::ifstream f(path);
+    if (!f) throw std::runtime_error("cannot open '" + path + "'");
+    std::vector<std::string> tok;
+    for (std::string s; f >> s;) tok.push_back(s);
+    size_t i = 0;
+    auto next = [&]() -> const std::string & {
+        if (i >= tok.size()) throw std::runtime_error("truncated model file");
+        return tok[i++];
+    };
+    auto expect = [&](const char *w) {
+        if (next() != w) throw std::runtime_error(std::string("malformed model file: expected '") + w + "'");
+    };
+    auto geti = [&]() { return std::stoll(next()); };
+    Model m;
+    expect("mojotrees");
+    const std::string ver = next();
+    if (ver != "v4" && ver != "v3" && ver != "v2")
+        throw std::runtime_error("unsupported model file version '" + ver + "'");
+    const std::string kind = next();
+    if (kind == "objective") {
+        m.objective = (int)geti();
+        if (m.objective != 0 && m.objective != 1)
+            throw std::runtime_error("objective " + std::to_string(m.objective) + " is not served by this library");
+        expect("learning_rate");
+        m.learning_rate = from_bits(next());
+        expect("base_score");
+        m.base.push_back(from_bits(next()));
+    } else if (kind == "multiclass") {
+        m.objective = -1;
+        m.num_class = (int)geti();
+        if (m.num_class < 2) throw std::runtime_error("multiclass needs at least 2 classes");
+        expect("learning_rate");
+        m.learning_rate = from_bits(next());
+        expect("base_scores");
+        for (int k = 0; k < m.num_class; ++k) m.base.push_back(from_bits(next()));
+    } else {
+        throw std::runtime_error("unsupported model section '" + kind + "'");
+    }
+    expect("mapper");
+    m.mapper.n_features = (int)geti();
+    m.mapper.n_bins = (int)geti();
+    const int64_t ne = geti();
+    for (int64_t k = 0; k < ne; ++k) m.mapper.edges.push_back(from_bits(next()));
+    m.mapper.edge_offsets.clear();
+    for (int k = 0; k <= m.mapper.n_features; ++k) m.mapper.edge_offsets.push_back(geti());
+    for (int k = 0; k < m.mapper.n_features; ++k) m.mapper.missing_bin.push_back((int32_t)geti());
+    if (m.mapper.edge_offsets.back() != ne) throw std::runtime_error("mapper offsets disagree with edges");
+    const std::string tr = next();
+    if (tr != "trees") throw std::runtime_error("section '" + tr + "' is not served by this library");
+    const int64_t nt = geti();
+    for (int64_t t = 0; t < nt; ++t) {
+        expect("tree");
+        const int64_t nn = geti();
+        m.n_leaves.push_back((int32_t)geti());
+        auto ints = [&](std::vector<int32_t> &v) {
+            for (int64_t k = 0; k < nn; ++k) v.push_back((int32_t)geti());
+        };
+        auto dbls = [&](std::vector<double> &v) {
+            for (int64_t k = 0; k < nn; ++k) v.push_back(from_bits(next()));
+        };
+        ints(m.feature);
+        ints(m.threshold);
+        ints(m.left);
+        ints(m.right);
+        dbls(m.value);
+        ints(m.default_left);
+        ints(m.missing_bin);
+        expect("counts");
+        if (geti()) dbls(m.count);
+        else m.count.insert(m.count.end(), (size_t)nn, 0.0);
+        expect("gains");
+        if (geti()) dbls(m.gain);
+        else m.gain.insert(m.gain.end(), (size_t)nn, 0.0);
+        m.offsets.push_back((int64_t)m.feature.size());
+        for (int64_t k = m.offsets[t]; k < m.offsets[t + 1]; ++k) {
+            const int fe = m.feature[k];
+            if (fe >= m.mapper.n_features) throw std::runtime_error("node feature out of range");
+            if (fe >= 0 && (m.left[k] < 0 || m.left[k] >= nn || m.right[k] < 0 || m.right[k] >= nn))
+                throw std::runtime_error("node child out of range");
+        }
+    }
+    if (i != tok.size()) throw std::runtime_error("unexpected trailing section in model file");
+    if (m.num_trees() % m.num_class != 0) throw std::runtime_error("tree count is not a multiple of the class count");
+    return m;
+}
+
+std::string Model::dump_json() const {
+    std::ostringstream o;
+    o.precision(17);
+    o << "{\"format\":\"mojotrees-inspection\",\"num_class\":" << num_class
+      << ",\"objective\":" << objective << ",\"learning_rate\":" << learning_rate
+      << ",\"num_features\":" << mapper.n_features << ",\"num_trees\":" << num_trees()
+      << ",\"num_iterations\":" << num_iterations() << ",\"base_score\":[";
+    for (int k = 0; k < num_class; ++k) o << (k ? "," : "") << base[k];
+    o << "],\"feature_names\":[";
+    for (int f = 0; f < mapper.n_features; ++f) o << (f ? "," : "") << "\"Column_" << f << "\"";
+    bool any_gain = false;
+    for (double g : gain) any_gain = any_gain || g > 0.0;
+    o << "],\"has_split_gain\":" << (any_gain ? "true" : "false") << ",\"bin_mapper\":[";
+    for (int f = 0; f < mapper.n_features; ++f) {
+        o << (f ? "," : "") << "{\"feature\":" << f << ",\"missing_bin\":" << mapper.missing_bin[f]
+          << ",\"upper_edges\":[";
+        for (int64_t e = mapper.edge_offsets[f]; e < mapper.edge_offsets[f + 1]; ++e)
+            o << (e > mapper.edge_offsets[f] ? "," : "") << mapper.edges[e];
+        o << "]}";
+    }
+    o << "],\"trees\":[";
+    for (int64_t t = 0; t < num_trees(); ++t) {
+        const int64_t a = offsets[t], b = offsets[t + 1];
+        o << (t ? "," : "") << "{\"tree_index\":" << t << ",\"class\":" << (t % num_class)
+          << ",\"num_leaves\":" << n_leaves[t] << ",\"nodes\":[";
+        for (int64_t k = a; k < b; ++k) {
+            o << (k > a ? "," : "") << "{\"id\":" << (k - a);
+            if (feature[k] >= 0) {
+                const int f = feature[k];
+                const int bn = threshold[k];
+                const int64_t eo = mapper.edge_offsets[f];
+                const int64_t ne = mapper.edge_offsets[f + 1] - eo;
+                o << ",\"split_feature\":" << f << ",\"threshold_bin\":" << bn;
+                if (bn < ne) o << ",\"threshold\":" << mapper.edges[eo + bn];
+                else o << ",\"threshold\":1e300";
+                o << ",\"default_left\":" << (default_left[k] ? "true" : "false")
+                  << ",\"left\":" << left[k] << ",\"right\":" << right[k] << ",\"split_gain\":" << gain[k];
+            } else {
+                o << ",\"leaf_value\":" << value[k];
+            }
+            o << ",\"count\":" << count[k] << "}";
+        }
+        o << "]}";
+    }
+    o << "]}";
+    return o.str();
+}
+
+}  // namespace mb

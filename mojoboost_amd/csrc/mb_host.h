@@ -1,0 +1,58 @@
+// Host-side pieces of the library: binning, the model container, prediction
+// and the model file format. Everything here runs on the CPU around the GPU
+// training path (the reference does the same: binning and the tree walk are
+// host work, docs/ARCHITECTURE.md:167-195).
+#pragma once
+
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+namespace mb {
+
+// A fitted bin mapper (binning.BinMapper, src/mojotrees/binning.mojo:2974):
+// per feature, ascending upper edges; a value v lands in the first bin whose
+// edge is >= v; NaN lands in the feature's reserved missing bin, or in the bin
+// of 0.0 when it has none.
+struct BinMapper {
+    int n_features = 0;
+    int n_bins = 255;
+    std::vector<double> edges;         // concatenated
+    std::vector<int64_t> edge_offsets; // n_features + 1
+    std::vector<int32_t> missing_bin;  // -1: none
+
+    int bin_of(int f, double v) const;
+    // Column-major doubles -> column-major uint8 bins (threads over columns).
+    void transform(const double *x, int64_t n_rows, uint8_t *out) const;
+};
+
+// binning.fit_bins with the quantile border type
+// (src/mojotrees/binning.mojo:3565-4047).
+BinMapper fit_bins(const double *x, int64_t n_rows, int n_features, int max_bins,
+                   int min_data_in_bin, bool use_missing, int64_t sample_cnt, int64_t seed);
+
+struct Model {
+    int objective = 0;  // 0 regression (squared error), 1 binary, -1 multiclass
+    int num_class = 1;
+    double learning_rate = 0.1;
+    std::vector<double> base;  // num_class
+    BinMapper mapper;
+    // trees, one after another; tree t owns nodes [offsets[t], offsets[t+1])
+    std::vector<int64_t> offsets{0};
+    std::vector<int32_t> n_leaves;
+    std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
+    std::vector<double> value, gain, count;
+
+    int64_t num_trees() const { return (int64_t)offsets.size() - 1; }
+    int64_t num_iterations() const { return num_trees() / num_class; }
+    // raw scores for rows of a column-major matrix, iterations [it0, it1)
+    void predict_raw(const double *x, int64_t n_rows, int64_t it0, int64_t it1, double *out) const;
+    void response(double *raw, int64_t n_rows) const;
+
+    void save(const std::string &path) const;  // throws std::runtime_error
+    static Model load(const std::string &path);
+    std::string dump_json() const;
+};
+
+}  // namespace mb

@@ -1,0 +1,25 @@
+// Launchers for the kernels in mb_kernels.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mb_state.h"
+
+namespace mb {
+
+hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
+hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
+hipError_t prepare_hist(const DevState &s);
+size_t hist_lds_bytes(const DevState &s);
+hipError_t launch_hist(const DevState &s, int root_mode, int grid, int64_t chunk_limit, hipStream_t st);
+hipError_t launch_partition(const DevState &s, int grid, hipStream_t st);
+hipError_t launch_split(const DevState &s, int root_mode, hipStream_t st);
+size_t score_lds_bytes(const DevState &s);
+hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
+hipError_t launch_round_end(const DevState &s, hipStream_t st);
+hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
+                                int grid, hipStream_t st);
+hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st);
+hipError_t launch_exp_sigmoid(const double *x, double *e, double *sg, int64_t n, hipStream_t st);
+
+}  // namespace mb

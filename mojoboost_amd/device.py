@@ -1,0 +1,139 @@
+"""Device-level API: a binned matrix resident in HBM and the trainer on it.
+
+Thin Python over include/mojoboost_hip.h (ctypes). Used by the benchmark and
+the parity tests, which keep inputs resident between calls.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib, ptr
+
+
+def device_count() -> int:
+    return int(lib().mbh_device_count())
+
+
+class Dataset:
+    """A column-major uint8 binned matrix and its labels, uploaded once."""
+
+    def __init__(self, bins_cm, n_rows, n_features, n_bins, labels, missing_bin=None):
+        L = lib()
+        self.n_rows, self.n_features, self.n_bins = int(n_rows), int(n_features), int(n_bins)
+        bins_cm = np.ascontiguousarray(bins_cm, dtype=np.uint8).ravel()
+        labels = np.ascontiguousarray(labels, dtype=np.float64)
+        if bins_cm.size != self.n_rows * self.n_features or labels.size != self.n_rows:
+            raise ValueError("bins must be n_rows * n_features and labels n_rows")
+        mb = None if missing_bin is None else np.ascontiguousarray(missing_bin, np.int32)
+        h = C.c_void_p()
+        err = C.create_string_buffer(1024)
+        check(L.mbh_dataset_create(ptr(bins_cm), self.n_rows, self.n_features, self.n_bins,
+                                   ptr(mb), ptr(labels), C.byref(h), err, 1024), err)
+        self.h = h
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().mbh_dataset_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def train(self, **params):
+        p = _lib.mbh_params(**params)
+        f = C.c_void_p()
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_train(self.h, C.byref(p), C.byref(f), err, 1024), err)
+        return Fit(f, self.n_rows)
+
+    def objective_quantize(self, raw, round_index=0, **params):
+        n = self.n_rows
+        p = _lib.mbh_params(**params)
+        g = np.zeros(n, np.float32)
+        h = np.zeros(n, np.float32)
+        qg = np.zeros(n, np.int8)
+        qh = np.zeros(n, np.int8)
+        sc = np.zeros(2)
+        err = C.create_string_buffer(1024)
+        raw = np.ascontiguousarray(raw, np.float64)
+        check(lib().mbh_objective_quantize(self.h, C.byref(p), ptr(raw), round_index, ptr(g),
+                                           ptr(h), ptr(qg), ptr(qh), ptr(sc), err, 1024), err)
+        return g, h, qg, qh, sc
+
+    def histogram(self, q_grad, q_hess, rows=None, quant_bins=4):
+        out = np.zeros(self.n_features * self.n_bins * 3, np.int32)
+        r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_histogram(self.h, ptr(np.ascontiguousarray(q_grad, np.int8)),
+                                  ptr(np.ascontiguousarray(q_hess, np.int8)), ptr(r),
+                                  0 if r is None else len(r), quant_bins, ptr(out), err, 1024), err)
+        return out.reshape(self.n_features, self.n_bins, 3)
+
+    def bench_root_histogram(self, reps=20):
+        out = np.zeros(2)
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_bench_root_histogram(self.h, reps, ptr(out), err, 1024), err)
+        return float(out[0]), float(out[1])
+
+
+class Fit:
+    """Trees grown by mbh_train, as flat arrays."""
+
+    def __init__(self, handle, n_rows):
+        L = lib()
+        self.h = handle
+        self.n_rows = n_rows
+        self.n_trees = int(L.mbh_fit_num_trees(handle))
+        self.num_class = int(L.mbh_fit_num_class(handle))
+        nn = int(L.mbh_fit_total_nodes(handle))
+        self.base = np.zeros(self.num_class)
+        self.off = np.zeros(self.n_trees + 1, np.int64)
+        i32 = lambda: np.zeros(nn, np.int32)
+        f64 = lambda: np.zeros(nn, np.float64)
+        self.feature, self.threshold, self.left, self.right = i32(), i32(), i32(), i32()
+        self.value, self.default_left, self.missing_bin = f64(), i32(), i32()
+        self.gain, self.count = f64(), f64()
+        L.mbh_fit_arrays(handle, ptr(self.base), ptr(self.off), ptr(self.feature),
+                         ptr(self.threshold), ptr(self.left), ptr(self.right), ptr(self.value),
+                         ptr(self.default_left), ptr(self.missing_bin), ptr(self.gain),
+                         ptr(self.count))
+        st = np.zeros(8)
+        L.mbh_fit_stats(handle, ptr(st))
+        self.stats = {
+            "train_seconds": st[0], "hist_ms": st[1], "hist_bytes": st[2],
+            "hist_rows_features": st[3], "hist_builds": st[4], "root_bytes": st[5],
+            "root_ms": st[6], "trees_grown": st[7],
+        }
+
+    def tree(self, t):
+        a, b = self.off[t], self.off[t + 1]
+        return {k: getattr(self, k)[a:b] for k in
+                ("feature", "threshold", "left", "right", "value", "default_left",
+                 "missing_bin", "gain", "count")}
+
+    def train_raw(self):
+        out = np.zeros(self.n_rows * self.num_class)
+        err = C.create_string_buffer(256)
+        check(lib().mbh_fit_train_raw(self.h, ptr(out), err, 256), err)
+        return out
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                lib().mbh_fit_free(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def exp_sigmoid(x):
+    x = np.ascontiguousarray(x, np.float64)
+    e = np.zeros_like(x)
+    s = np.zeros_like(x)
+    err = C.create_string_buffer(512)
+    check(lib().mbh_exp_sigmoid(ptr(x), x.size, ptr(e), ptr(s), err, 512), err)
+    return e, s

@@ -1,0 +1,242 @@
+"""scikit-learn-style estimators over the mojotrees C ABI.
+
+Same names and call shapes as the reference's estimators
+(python/mojotrees/sklearn.py: MojoTreesRegressor :5319, MojoTreesClassifier
+:6178; fit :5548/:6412, predict :6016/:6898, predict_proba :6913, save/load
+:6140-6162). Training goes through `mojotrees_train_dense` into the HIP
+library (column-major float64 X by address, as bindings/_mojotrees.mojo:2102
+takes it); device="gpu" never falls back to a CPU trainer.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import MojoTreesError, lib, ptr
+
+
+class _Error:
+    def __init__(self):
+        self.h = lib().mojotrees_error_create()
+
+    def message(self):
+        m = lib().mojotrees_error_message(self.h)
+        return m.decode(errors="replace") if m else ""
+
+    def check(self, rc):
+        if rc != _lib.OK:
+            raise MojoTreesError(rc, self.message())
+
+    def __del__(self):
+        try:
+            lib().mojotrees_error_free(self.h)
+        except Exception:
+            pass
+
+
+def _colmajor(X):
+    X = np.asarray(X, dtype=np.float64)
+    if X.ndim != 2:
+        raise ValueError("X must be 2-dimensional")
+    return np.asfortranarray(X), X.shape[0], X.shape[1]
+
+
+class _Booster:
+    """An owned model handle."""
+
+    def __init__(self, handle):
+        self.h = handle
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().mojotrees_model_free(self.h)
+        except Exception:
+            pass
+
+    def _count(self, fn):
+        v = C.c_int64()
+        e = _Error()
+        e.check(getattr(lib(), fn)(self.h, C.byref(v), e.h))
+        return int(v.value)
+
+    @property
+    def num_features(self):
+        return self._count("mojotrees_model_num_features")
+
+    @property
+    def num_classes(self):
+        return self._count("mojotrees_model_num_classes")
+
+    @property
+    def num_trees(self):
+        return self._count("mojotrees_model_num_trees")
+
+    @property
+    def num_iterations(self):
+        return self._count("mojotrees_model_num_iterations")
+
+    def predict(self, X, raw=False, start_iteration=0, num_iteration=0):
+        Xf, n, f = _colmajor(X)
+        k = self.num_classes
+        out = np.zeros(n * k)
+        e = _Error()
+        flags = _lib.PREDICT_RAW if raw else _lib.PREDICT_RESPONSE
+        e.check(lib().mojotrees_predict_ex(self.h, ptr(Xf.ravel(order="K")), n, f,
+                                           start_iteration, num_iteration, flags,
+                                           _lib.DEVICE_CPU, ptr(out), out.size, e.h))
+        return out.reshape(n, k) if k > 1 else out
+
+    def save(self, path):
+        e = _Error()
+        e.check(lib().mojotrees_save_model(self.h, str(path).encode(), e.h))
+
+    @staticmethod
+    def load(path):
+        h = C.c_void_p()
+        e = _Error()
+        e.check(lib().mojotrees_load_model(str(path).encode(), C.byref(h), e.h))
+        return _Booster(h)
+
+    def dump_json(self):
+        out = C.c_char_p()
+        e = _Error()
+        e.check(lib().mojotrees_model_dump_json(self.h, C.byref(out), e.h))
+        try:
+            return out.value.decode()
+        finally:
+            lib().mojotrees_string_free(out)
+
+    def feature_importance(self, importance_type="split"):
+        t = _lib.IMPORTANCE_GAIN if importance_type == "gain" else _lib.IMPORTANCE_SPLIT
+        out = np.zeros(self.num_features)
+        e = _Error()
+        e.check(lib().mojotrees_feature_importance(self.h, t, ptr(out), out.size, e.h))
+        return out
+
+
+def _train(X, y, params: str):
+    Xf, n, f = _colmajor(X)
+    y = np.ascontiguousarray(y, dtype=np.float64)
+    if y.shape[0] != n:
+        raise ValueError("y must have one entry per row of X")
+    h = C.c_void_p()
+    e = _Error()
+    e.check(lib().mojotrees_train_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), None,
+                                        params.encode(), C.byref(h), e.h))
+    return _Booster(h)
+
+
+class _Base:
+    _objective = "regression"
+
+    def __init__(self, n_estimators=100, learning_rate=0.1, num_leaves=31, max_depth=-1,
+                 min_child_samples=20, min_child_weight=1e-3, reg_alpha=0.0, reg_lambda=1.0,
+                 colsample_bytree=1.0, subsample=1.0, subsample_freq=0, max_bin=255,
+                 random_state=None, device="gpu", use_quantized_grad=True,
+                 num_grad_quant_bins=4, stochastic_rounding=True):
+        self.n_estimators = n_estimators
+        self.learning_rate = learning_rate
+        self.num_leaves = num_leaves
+        self.max_depth = max_depth
+        self.min_child_samples = min_child_samples
+        self.min_child_weight = min_child_weight
+        self.reg_alpha = reg_alpha
+        self.reg_lambda = reg_lambda
+        self.colsample_bytree = colsample_bytree
+        self.subsample = subsample
+        self.subsample_freq = subsample_freq
+        self.max_bin = max_bin
+        self.random_state = random_state
+        self.device = device
+        self.use_quantized_grad = use_quantized_grad
+        self.num_grad_quant_bins = num_grad_quant_bins
+        self.stochastic_rounding = stochastic_rounding
+        self.booster_ = None
+
+    def _params(self, extra=""):
+        if self.device not in ("gpu", "auto", "cpu"):
+            raise ValueError("device must be 'gpu', 'auto' or 'cpu'")
+        p = [f"objective={self._objective}", f"num_iterations={self.n_estimators}",
+             f"learning_rate={self.learning_rate!r}", f"num_leaves={self.num_leaves}",
+             f"max_depth={self.max_depth}", f"min_data_in_leaf={self.min_child_samples}",
+             f"min_sum_hessian_in_leaf={self.min_child_weight!r}",
+             f"lambda_l1={self.reg_alpha!r}", f"lambda_l2={self.reg_lambda!r}",
+             f"feature_fraction={self.colsample_bytree!r}",
+             f"bagging_fraction={self.subsample!r}", f"bagging_freq={self.subsample_freq}",
+             f"max_bin={self.max_bin}", f"device={self.device}",
+             f"use_quantized_grad={'true' if self.use_quantized_grad else 'false'}",
+             f"num_grad_quant_bins={self.num_grad_quant_bins}",
+             f"stochastic_rounding={'true' if self.stochastic_rounding else 'false'}"]
+        if self.random_state is not None:
+            p += [f"feature_fraction_seed={int(self.random_state)}",
+                  f"bagging_seed={int(self.random_state)}"]
+        return " ".join(p) + (" " + extra if extra else "")
+
+    def save(self, path):
+        self._check_fitted()
+        self.booster_.save(path)
+
+    def _check_fitted(self):
+        if self.booster_ is None:
+            raise RuntimeError("estimator is not fitted")
+
+    @property
+    def n_features_in_(self):
+        self._check_fitted()
+        return self.booster_.num_features
+
+    def feature_importances(self, importance_type="split"):
+        self._check_fitted()
+        return self.booster_.feature_importance(importance_type)
+
+
+class MojoTreesRegressor(_Base):
+    _objective = "regression"
+
+    def fit(self, X, y):
+        self.booster_ = _train(X, y, self._params())
+        return self
+
+    def predict(self, X, raw_score=False):
+        self._check_fitted()
+        return self.booster_.predict(X, raw=raw_score)
+
+    @classmethod
+    def load(cls, path):
+        est = cls()
+        est.booster_ = _Booster.load(path)
+        return est
+
+
+class MojoTreesClassifier(_Base):
+    _objective = "binary"
+
+    def fit(self, X, y):
+        y = np.asarray(y)
+        self.classes_ = np.unique(y)
+        if len(self.classes_) != 2:
+            raise MojoTreesError(_lib.ERROR_UNSUPPORTED,
+                                 "only binary classification is served by the device path")
+        yb = (y == self.classes_[1]).astype(np.float64)
+        self.booster_ = _train(X, yb, self._params())
+        return self
+
+    def predict_proba(self, X):
+        self._check_fitted()
+        p1 = self.booster_.predict(X)
+        return np.column_stack([1.0 - p1, p1])
+
+    def predict(self, X):
+        return self.classes_[(self.predict_proba(X)[:, 1] > 0.5).astype(int)]
+
+    def decision_function(self, X):
+        self._check_fitted()
+        return self.booster_.predict(X, raw=True)
+
+    @classmethod
+    def load(cls, path):
+        est = cls()
+        est.booster_ = _Booster.load(path)
+        est.classes_ = np.array([0, 1])
+        return est

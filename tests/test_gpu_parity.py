@@ -1,0 +1,164 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+Bar: quantized-gradient histograms, split
+choices, trees and raw scores bit-exact. Every comparison below is on
+integers or on IEEE-754 bit patterns.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from mojoboost_amd import device
+
+    if device.device_count() < 1:
+        pytest.fail("no gfx950 device visible to the HIP library")
+    return device
+
+
+def bits(a):
+    return np.asarray(a, np.float64).view(np.uint64)
+
+
+def c2_like(n, f=28, seed=1, nb=255):
+    """C2-shaped data at a reduced row count:
+    21 N(0,1) columns, 7 derived (products and abs of pairs), label
+    Bernoulli(sigmoid(sum of 8 pairwise terms))."""
+    rng = np.random.default_rng(seed)
+    base = rng.normal(size=(21, n))
+    derived = [base[0] * base[1], np.abs(base[2]), base[3] * base[4], np.abs(base[5] * base[6]),
+               base[7] * base[8], np.abs(base[9]) * base[10], base[11] * base[12]]
+    x = np.vstack([base] + derived)[:f]
+    pairs = rng.integers(0, 21, size=(8, 2))
+    w = rng.uniform(-1, 1, size=8)
+    logit = 0.3 + sum(w[i] * base[a] * base[b] for i, (a, b) in enumerate(pairs))
+    y = (rng.uniform(size=n) < 1 / (1 + np.exp(-logit))).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=nb)
+    return bins, y, mb, nb
+
+
+def test_exp_sigmoid_bit_exact(dev):
+    L = O.lib()
+    x = np.concatenate([np.linspace(-750, 750, 30001), np.random.default_rng(3).normal(0, 5, 20000),
+                        [0.0, -0.0, 1e-300, -1e-300, 709.0, -709.5, 745.0]])
+    e, s = dev.exp_sigmoid(x)
+    want_e = np.array([L.orc_exp(float(v)) for v in x])
+    want_s = np.array([L.orc_sigmoid(float(v)) for v in x])
+    assert np.array_equal(bits(e), bits(want_e))
+    assert np.array_equal(bits(s), bits(want_s))
+
+
+@pytest.mark.parametrize("objective", [0, 1])
+def test_objective_and_quantizer_bit_exact(dev, objective):
+    n, f = 50_000, 6
+    rng = np.random.default_rng(7 + objective)
+    bins = rng.integers(0, 32, size=(f, n), dtype=np.uint8)
+    y = (rng.uniform(size=n) < 0.4).astype(np.float64) if objective == 1 else rng.normal(size=n)
+    raw = rng.normal(0, 2, size=n)
+    ds = dev.Dataset(bins, n, f, 32, y)
+    for rnd in (0, 5):
+        g, h, qg, qh, sc = ds.objective_quantize(raw, round_index=rnd, objective=objective)
+        og, oh = O.grad_hess(objective, raw, y)
+        assert np.array_equal(g.astype(np.float64), og)
+        assert np.array_equal(h.astype(np.float64), oh)
+        oqg, oqh, osc = O.quantize(og, oh, quant_bins=4, stochastic=1, seed=11, round_index=rnd,
+                                   const_hessian=1 if objective == 0 else 0)
+        assert sc[0] == osc[0] and sc[1] == osc[1]
+        assert np.array_equal(qg, oqg)
+        assert np.array_equal(qh, oqh)
+
+
+@pytest.mark.parametrize("subset", [False, True])
+def test_histogram_bit_exact(dev, subset):
+    n, f, nb = 300_000, 28, 255
+    rng = np.random.default_rng(11)
+    bins = rng.integers(0, nb, size=(f, n), dtype=np.uint8)
+    bins[3] = bins[3] % 7          # a low-cardinality feature: hot bins
+    qg = rng.integers(-2, 3, size=n).astype(np.int8)
+    qh = rng.integers(0, 5, size=n).astype(np.int8)
+    ds = dev.Dataset(bins, n, f, nb, np.zeros(n))
+    rows = np.sort(rng.choice(n, 77_777, replace=False)).astype(np.int32) if subset else None
+    got = ds.histogram(qg, qh, rows, quant_bins=4)
+    want = O.hist_quantized(bins.ravel(), n, f, nb, qg, qh, rows)
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+def _compare_fit(fit, ref, n):
+    assert fit.n_trees == ref.n_trees, (fit.n_trees, ref.n_trees)
+    assert np.array_equal(fit.off, ref.off)
+    for k in ("feature", "threshold", "left", "right", "default_left", "missing_bin"):
+        assert np.array_equal(getattr(fit, k), getattr(ref, k)), k
+    for k in ("value", "gain", "count"):
+        assert np.array_equal(bits(getattr(fit, k)), bits(getattr(ref, k))), k
+    assert np.array_equal(bits(fit.base), bits(ref.base))
+    assert np.array_equal(bits(fit.train_raw()), bits(ref.train_raw(n)))
+
+
+def test_training_c2_shape_bit_exact(dev):
+    """C2 workload shape (255 bins, 255 leaves, logistic, int8 g/h) at
+    200k rows x 28 features, 12 trees: every tree and raw score identical."""
+    n = 200_000
+    bins, y, mb, nb = c2_like(n)
+    kw = dict(objective=1, num_iterations=12, num_leaves=255, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, 28, nb, y, missing_bin=mb)
+    fit = ds.train(**kw)
+    ref = O.train(bins, n, 28, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
+def test_training_regression_const_hessian(dev):
+    n, f, nb = 60_000, 10, 63
+    rng = np.random.default_rng(21)
+    x = rng.normal(size=(f, n))
+    y = x[0] - 2 * x[1] * x[2] + 0.1 * rng.normal(size=n)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=nb)
+    kw = dict(objective=0, num_iterations=8, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1, max_depth=6)
+    fit = dev.Dataset(bins, n, f, nb, y, missing_bin=mb).train(**kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
+def test_training_bagging_and_feature_fraction(dev):
+    n = 50_000
+    bins, y, mb, nb = c2_like(n, f=20, seed=5, nb=63)
+    kw = dict(objective=1, num_iterations=6, num_leaves=63, min_data_in_leaf=10, lambda_l2=0.5,
+              learning_rate=0.2, bagging_fraction=0.7, bagging_freq=2, bagging_seed=9,
+              feature_fraction=0.6, feature_fraction_seed=4)
+    fit = dev.Dataset(bins, n, 20, nb, y, missing_bin=mb).train(**kw)
+    ref = O.train(bins, n, 20, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
+def test_training_missing_values_and_tiny_leaves(dev):
+    """NaNs reserve a missing bin: both routing directions are scanned."""
+    n, f = 20_000, 5
+    rng = np.random.default_rng(33)
+    x = rng.normal(size=(f, n))
+    x[1, rng.uniform(size=n) < 0.2] = np.nan
+    x[3, rng.uniform(size=n) < 0.05] = np.nan
+    y = (np.nan_to_num(x[1], nan=1.5) + x[0] > 0.3).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=32)
+    assert (mb >= 0).sum() == 2
+    kw = dict(objective=1, num_iterations=5, num_leaves=127, min_data_in_leaf=2, lambda_l2=0.0,
+              min_sum_hessian=1e-3, learning_rate=0.3)
+    fit = dev.Dataset(bins, n, f, 32, y, missing_bin=mb).train(**kw)
+    ref = O.train(bins, n, f, 32, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
+def test_training_is_deterministic(dev):
+    n = 100_000
+    bins, y, mb, nb = c2_like(n, seed=8)
+    ds = dev.Dataset(bins, n, 28, nb, y, missing_bin=mb)
+    kw = dict(objective=1, num_iterations=4, num_leaves=255)
+    a, b = ds.train(**kw), ds.train(**kw)
+    for k in ("feature", "threshold", "value", "gain"):
+        assert np.array_equal(getattr(a, k), getattr(b, k))
+    assert np.array_equal(bits(a.train_raw()), bits(b.train_raw()))
