@@ -63,6 +63,16 @@ typedef struct {
     int32_t time_histograms; /* 1: bracket each histogram launch with events */
 } mbh_params;
 
+/* Host binning of a column-major double matrix (NaN = missing) with the
+ * reference's quantile rule (binning.fit_bins + BinMapper.transform,
+ * src/mojotrees/binning.mojo:3565-4047, :3264): out_bins is n_features *
+ * n_rows uint8, out_missing_bin n_features (-1: none reserved). */
+int32_t mbh_bin_dense(const double *data, int64_t n_rows, int32_t n_features,
+                      int32_t max_bins, int32_t min_data_in_bin,
+                      int32_t use_missing, int64_t sample_cnt, int64_t seed,
+                      uint8_t *out_bins, int32_t *out_missing_bin, char *err,
+                      int32_t err_len);
+
 /* Number of usable gfx950 devices (0 without a GPU or runtime). */
 int32_t mbh_device_count(void);
 
@@ -93,7 +103,9 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  * out[2] histogram algorithmic bytes (sum over builds of rows * (F + 2)),
  * out[3] histogram rows * features, out[4] histogram launches that built,
  * out[5] root-build algorithmic bytes, out[6] root-build milliseconds,
- * out[7] trees grown. */
+ * out[7] trees grown, out[8] summed milliseconds of histogram + split
+ * kernels (the split kernel merges the histogram's block partials),
+ * out[9] the same for the root builds. out has 10 entries. */
 void mbh_fit_stats(const mbh_fit *fit, double *out);
 
 /* ------------------------------------------- stage-level (parity, bench) */
@@ -118,8 +130,10 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad,
                       int64_t n_sel, int32_t num_grad_quant_bins,
                       int32_t *out, char *err, int32_t err_len);
 
-/* Root histogram of all rows, `reps` times back to back on resident data:
- * out_ms[0] mean kernel milliseconds (HIP events), out_ms[1] min. */
+/* Root histogram of all rows, `reps` times back to back on resident data
+ * (HIP events): out_ms[0] mean histogram-kernel milliseconds, out_ms[1] its
+ * min, out_ms[2] mean milliseconds of histogram + the split kernel that
+ * merges its partials. out_ms has 3 entries. */
 int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps,
                                  double *out_ms, char *err, int32_t err_len);
 

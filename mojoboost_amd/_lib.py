@@ -31,7 +31,7 @@ MOJOTREES_SYMBOLS = [
     "mojotrees_parameter_keys", "mojotrees_string_free", "mojotrees_model_free",
 ]
 MBH_SYMBOLS = [
-    "mbh_device_count", "mbh_dataset_create", "mbh_dataset_free", "mbh_train",
+    "mbh_bin_dense", "mbh_device_count", "mbh_dataset_create", "mbh_dataset_free", "mbh_train",
     "mbh_fit_free", "mbh_fit_num_trees", "mbh_fit_num_class", "mbh_fit_total_nodes",
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
     "mbh_objective_quantize", "mbh_histogram", "mbh_bench_root_histogram",
@@ -117,6 +117,7 @@ def lib():
         "mojotrees_parameter_keys": (I32, [V, V]),
         "mojotrees_string_free": (None, [V]),
         "mojotrees_model_free": (None, [V]),
+        "mbh_bin_dense": (I32, [V, I64, I32, I32, I32, I32, I64, I64, V, V, C.c_char_p, I32]),
         "mbh_device_count": (I32, []),
         "mbh_dataset_create": (I32, [V, I64, I32, I32, V, V, V, C.c_char_p, I32]),
         "mbh_dataset_free": (None, [V]),

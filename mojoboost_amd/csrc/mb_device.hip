@@ -20,6 +20,7 @@
 
 #include "../../include/mojoboost_hip.h"
 #include "../../include/mojotrees.h"
+#include "mb_host.h"
 #include "mb_kernels.h"
 #include "mb_math.h"
 #include "mb_state.h"
@@ -120,7 +121,7 @@ struct mbh_fit {
     std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
     std::vector<double> value, gain, count;
     std::vector<double> train_raw;
-    double stats[8] = {0};
+    double stats[10] = {0};
 };
 
 namespace {
@@ -151,7 +152,9 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         bad("unknown objective");
     }
     if (p->num_iterations < 0) bad("num_iterations must be nonnegative");
-    if (p->num_leaves < 1 || p->num_leaves > 4096) bad("num_leaves must be in [1, 4096]");
+    if (p->num_leaves < 1) bad("num_leaves must be positive");
+    if (p->num_leaves > 2048)
+        unsup("num_leaves above 2048: the score-update kernel keeps the tree in LDS (160 KB)");
     if (p->min_data_in_leaf < 0) bad("min_data_in_leaf must be nonnegative");
     if (!(p->learning_rate > 0.0)) bad("learning_rate must be positive");
     if (!(p->lambda_l2 >= 0.0) || !(p->lambda_l1 >= 0.0)) bad("lambda_l1 and lambda_l2 must be nonnegative");
@@ -166,6 +169,24 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
     if (p->objective == MBH_OBJ_BINARY && (ds->label_min < 0.0 || ds->label_max > 1.0))
         bad("binary labels must be in [0, 1]");
+}
+
+// Histogram launch geometry and the partial buffer. A build of m rows runs
+// ceil(m / chunk) blocks with chunk = clamp(ceil(m / grid), chunk_min,
+// chunk_limit); the grid is widened when needed so grid * chunk_limit covers
+// every row.
+constexpr int64_t kHistChunkMin = 8192;
+
+void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
+    const int64_t limit = chunk_limit_for(B);
+    int64_t grid = 2 * (int64_t)ds->n_cu;
+    const int64_t need = (ds->n + limit - 1) / limit;
+    if (grid < need) grid = need;
+    s.hist_grid = (int32_t)grid;
+    s.part_stride = (ds->nb + 1) & ~1;
+    s.hist_chunk_min = std::min<int64_t>(kHistChunkMin, limit);
+    s.hist_chunk_limit = limit;
+    s.part = dalloc<unsigned long long>((size_t)grid * ds->F * s.part_stride, run.owned);
 }
 
 double base_score_for(const mbh_dataset *ds, int objective) {
@@ -213,6 +234,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.rows0 = dalloc<int32_t>(ds->n, run.owned);
     s.rows1 = dalloc<int32_t>(ds->n, run.owned);
     s.hist = dalloc<int32_t>((size_t)L * F * ds->nb * 3, run.owned);
+    configure_hist(s, ds, p->num_grad_quant_bins, run);
     s.step = dalloc<mb::Step>(1, run.owned);
     s.slots = dalloc<mb::Slot>(L, run.owned);
     s.scan = dalloc<mb::ScanResult>(2 * (size_t)F, run.owned);
@@ -284,6 +306,24 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
 extern "C" {
 
 int32_t mbh_device_count(void) { return device_count_gfx950(); }
+
+int32_t mbh_bin_dense(const double *data, int64_t n, int32_t F, int32_t max_bins, int32_t min_data_in_bin,
+                      int32_t use_missing, int64_t sample_cnt, int64_t seed, uint8_t *out_bins,
+                      int32_t *out_missing, char *err, int32_t err_len) {
+    if (!data || !out_bins || !out_missing || n <= 0 || F <= 0) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        mb::BinMapper m = mb::fit_bins(data, n, F, max_bins, min_data_in_bin, use_missing != 0, sample_cnt, seed);
+        m.transform(data, n, out_bins);
+        for (int f = 0; f < F; ++f) out_missing[f] = m.missing_bin[f];
+    } catch (const std::exception &e) {
+        set_err(err, err_len, e.what());
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    return MOJOTREES_OK;
+}
 
 int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t nb,
                            const int32_t *missing_bin, const double *labels, mbh_dataset **out,
@@ -391,40 +431,47 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         HIPX(mb::launch_fill_f64(s.raw, ds->n, K, d_base, grid_rows, nullptr));
         HIPX(mb::prepare_hist(s));
         HIPX(hipDeviceSynchronize());
-        const int64_t climit = chunk_limit_for(p->num_grad_quant_bins);
-        const int grid_hist = 2 * ds->n_cu;
-        const int grid_part = 4 * ds->n_cu;
+        const int grid_part = 2 * ds->n_cu;
         const int L = tb.L;
         const int T = p->num_iterations * K;
         const bool timed = p->time_histograms != 0;
         hipStream_t st = nullptr;
-        if (timed) events.resize((size_t)2 * L);
+        // per build: before the histogram, after it, after the split kernel
+        // (which merges the partials)
+        if (timed) events.resize((size_t)3 * L);
         for (auto &e : events) HIPX(hipEventCreate(&e));
-        double hist_ms = 0.0, root_ms = 0.0;
+        double hist_ms = 0.0, root_ms = 0.0, merged_ms = 0.0, root_merged_ms = 0.0;
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
             HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
             if (timed) HIPX(hipEventRecord(events[0], st));
-            HIPX(mb::launch_hist(s, 1, grid_hist, climit, st));
+            HIPX(mb::launch_hist(s, 1, st));
             if (timed) HIPX(hipEventRecord(events[1], st));
             HIPX(mb::launch_split(s, 1, st));
+            if (timed) HIPX(hipEventRecord(events[2], st));
             for (int k = 1; k < L; ++k) {
                 HIPX(mb::launch_partition(s, grid_part, st));
-                if (timed) HIPX(hipEventRecord(events[2 * k], st));
-                HIPX(mb::launch_hist(s, 0, grid_hist, climit, st));
-                if (timed) HIPX(hipEventRecord(events[2 * k + 1], st));
+                if (timed) HIPX(hipEventRecord(events[3 * k], st));
+                HIPX(mb::launch_hist(s, 0, st));
+                if (timed) HIPX(hipEventRecord(events[3 * k + 1], st));
                 HIPX(mb::launch_split(s, 0, st));
+                if (timed) HIPX(hipEventRecord(events[3 * k + 2], st));
             }
             HIPX(mb::launch_score(s, grid_rows, st));
             HIPX(mb::launch_round_end(s, st));
             if (timed) {
                 HIPX(hipStreamSynchronize(st));
                 for (int k = 0; k < L; ++k) {
-                    float ms = 0.f;
-                    HIPX(hipEventElapsedTime(&ms, events[2 * k], events[2 * k + 1]));
+                    float ms = 0.f, ms2 = 0.f;
+                    HIPX(hipEventElapsedTime(&ms, events[3 * k], events[3 * k + 1]));
+                    HIPX(hipEventElapsedTime(&ms2, events[3 * k], events[3 * k + 2]));
                     hist_ms += ms;
-                    if (k == 0) root_ms += ms;
+                    merged_ms += ms2;
+                    if (k == 0) {
+                        root_ms += ms;
+                        root_merged_ms += ms2;
+                    }
                 }
             }
         }
@@ -485,6 +532,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         fit->stats[5] = root_bytes;
         fit->stats[6] = root_ms;
         fit->stats[7] = grown;
+        fit->stats[8] = merged_ms;
+        fit->stats[9] = root_merged_ms;
         for (auto &e : events) (void)hipEventDestroy(e);
         events.clear();
     } catch (const Error &e) {
@@ -526,7 +575,7 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err, int32_t er
     return MOJOTREES_OK;
 }
 void mbh_fit_stats(const mbh_fit *fit, double *out) {
-    for (int i = 0; i < 8; ++i) out[i] = fit->stats[i];
+    for (int i = 0; i < 10; ++i) out[i] = fit->stats[i];
 }
 
 int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out_sig, char *err,
@@ -630,7 +679,12 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
         }
         HIPX(hipMemcpy(ds->d_records, rec.data(), rec.size(), hipMemcpyHostToDevice));
         const size_t cells = (size_t)ds->F * ds->nb * 3;
-        HIPX(hipMemset(s.hist, 0, cells * sizeof(int32_t)));
+        // unit lattice scales: the root split's gains are not read here, only
+        // the histogram it merges into buffer 0
+        mb::Round r0{};
+        r0.grad_units = 1.0;
+        r0.hess_units = 1.0;
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
         if (rows) {
             s.hp.bagging = 1;  // root range = rows0[0 .. cursor[0])
             HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
@@ -638,7 +692,8 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
             HIPX(hipMemcpy(s.cursor, c, sizeof(c), hipMemcpyHostToDevice));
         }
         HIPX(mb::prepare_hist(s));
-        HIPX(mb::launch_hist(s, 1, 2 * ds->n_cu, chunk_limit_for(B), nullptr));
+        HIPX(mb::launch_hist(s, 1, nullptr));
+        HIPX(mb::launch_split(s, 1, nullptr));
         HIPX(hipDeviceSynchronize());
         HIPX(hipMemcpy(out, s.hist, cells * sizeof(int32_t), hipMemcpyDeviceToHost));
     } catch (const Error &e) {
@@ -654,7 +709,7 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         set_err(err, err_len, "invalid arguments");
         return MOJOTREES_ERROR_INVALID_ARGUMENT;
     }
-    std::vector<hipEvent_t> ev((size_t)2 * reps);
+    std::vector<hipEvent_t> ev((size_t)3 * reps);
     try {
         Run run;
         mbh_params p{};
@@ -667,24 +722,32 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         p.num_grad_quant_bins = 4;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
+        mb::Round r0{};
+        r0.grad_units = 1.0;
+        r0.hess_units = 1.0;
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
         HIPX(mb::prepare_hist(s));
         for (auto &e : ev) HIPX(hipEventCreate(&e));
-        const int64_t climit = chunk_limit_for(4);
         for (int i = 0; i < reps; ++i) {
-            HIPX(hipEventRecord(ev[2 * i], nullptr));
-            HIPX(mb::launch_hist(s, 1, 2 * ds->n_cu, climit, nullptr));
-            HIPX(hipEventRecord(ev[2 * i + 1], nullptr));
+            HIPX(hipEventRecord(ev[3 * i], nullptr));
+            HIPX(mb::launch_hist(s, 1, nullptr));
+            HIPX(hipEventRecord(ev[3 * i + 1], nullptr));
+            HIPX(mb::launch_split(s, 1, nullptr));
+            HIPX(hipEventRecord(ev[3 * i + 2], nullptr));
         }
         HIPX(hipDeviceSynchronize());
-        double sum = 0.0, mn = 1e30;
+        double sum = 0.0, mn = 1e30, sum2 = 0.0;
         for (int i = 0; i < reps; ++i) {
-            float ms = 0.f;
-            HIPX(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+            float ms = 0.f, ms2 = 0.f;
+            HIPX(hipEventElapsedTime(&ms, ev[3 * i], ev[3 * i + 1]));
+            HIPX(hipEventElapsedTime(&ms2, ev[3 * i], ev[3 * i + 2]));
             sum += ms;
+            sum2 += ms2;
             mn = std::min(mn, (double)ms);
         }
         out_ms[0] = sum / reps;
         out_ms[1] = mn;
+        out_ms[2] = sum2 / reps;
         for (auto &e : ev) (void)hipEventDestroy(e);
     } catch (const Error &e) {
         for (auto &x : ev)

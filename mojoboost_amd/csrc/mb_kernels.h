@@ -11,7 +11,7 @@ hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 hipError_t prepare_hist(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
-hipError_t launch_hist(const DevState &s, int root_mode, int grid, int64_t chunk_limit, hipStream_t st);
+hipError_t launch_hist(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_partition(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_split(const DevState &s, int root_mode, hipStream_t st);
 size_t score_lds_bytes(const DevState &s);

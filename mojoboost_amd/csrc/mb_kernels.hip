@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
 // quantize_scalar per row (:1479-1545). Every row is quantized, sampled or
 // not, with the row id as the stream counter. The int8 pair lands in the
 // last two bytes of the row's record, next to its bins. The root row list
-// (identity, or the bag) and the root histogram buffer are prepared here.
+// (the bag) is gathered here; without bagging the root reads rows directly.
 __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const Round rd = *s.round;
     const HyperParams &hp = s.hp;
@@ -205,38 +205,47 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
             }
         }
     }
-    const size_t cells = (size_t)s.n_features * s.n_bins * 3;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < cells; i += stride) s.hist[i] = 0;
 }
 
 // --------------------------------------------------------------- histogram
-// One leaf's histogram. Rows are split into contiguous chunks, one chunk per
-// block; a block accumulates its rows into LDS-private packed counters and
-// merges the non-empty cells into the global int32 histogram. A row's record
-// is D dwords: the D lanes of a row group each read one dword (4 features)
-// and the g/h pair comes from the last dword by a lane shuffle.
+// Rows of a node with m rows handled by each histogram block. The split
+// kernel recomputes it to know how many block partials a build left.
+__device__ __forceinline__ int64_t hist_chunk(const DevState &s, int64_t m) {
+    const int64_t g = s.hist_grid;
+    int64_t chunk = (m + g - 1) / g;
+    if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+    if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
+    return chunk;
+}
+
+// One leaf's histogram, accumulation pass. Rows are split into contiguous
+// chunks, one per block; a block accumulates its rows into LDS-private
+// packed counters and stores them, all cells, as its partial. The split
+// kernel merges the partials. A row's record is LPR x 16 bytes: each of the
+// LPR lanes of a row group loads 16 bytes (16 features) and the int8 g/h pair
+// (the record's last two bytes) reaches the group by a lane shuffle. Each
+// lane keeps kHistUnroll row loads in flight.
 //
 // Packed counter (64 bits): count in bits [0,20), hess sum in [20,42), grad
-// sum (signed) in [42,64). Adding packed values adds the three fields as
-// long as no field overflows, which kHistRowsPerChunk guarantees for the
-// lattice in use (host-checked).
-template <int D>
-__global__ __launch_bounds__(512) void k_hist(DevState s, int root_mode, int64_t chunk_limit) {
+// sum (signed) in [42,64). Adding packed values adds the three fields while
+// no field overflows, which hist_chunk_limit guarantees for the lattice in
+// use (host-checked).
+constexpr int kHistUnroll = 4;
+
+template <int LPR>
+__global__ __launch_bounds__(1024) void k_hist(DevState s, int root_mode) {
     extern __shared__ unsigned long long lds[];
-    int64_t beg, m;
+    int64_t m;
     const int32_t *rows;
     bool direct;
-    int32_t out_buf;
     if (root_mode) {
-        const HyperParams &hp = s.hp;
-        m = hp.bagging ? s.cursor[0] : s.n;
-        beg = 0;
+        m = s.hp.bagging ? s.cursor[0] : s.n;
         rows = s.rows0;
-        direct = !hp.bagging;
-        out_buf = 0;
+        direct = !s.hp.bagging;
     } else {
         const Step st = *s.step;
         if (!st.active) return;
+        int64_t beg;
         if (st.builds_left) {
             beg = st.begin;
             m = st.n_left;
@@ -246,55 +255,60 @@ __global__ __launch_bounds__(512) void k_hist(DevState s, int root_mode, int64_t
         }
         rows = (st.src_buf ? s.rows0 : s.rows1) + beg;
         direct = false;
-        out_buf = st.child_hist;
     }
     if (m <= 0) return;
-    int64_t chunk = (m + gridDim.x - 1) / gridDim.x;
-    if (chunk < 1024) chunk = 1024;
-    if (chunk > chunk_limit) chunk = chunk_limit;
-    const int F = s.n_features;
-    const int nb = s.n_bins;
-    const int ls = s.lds_stride;
-    const int cells = F * ls;
-    int32_t *out = s.hist + (size_t)out_buf * F * nb * 3;
-    const int sub = threadIdx.x % D;
-    const int rr = threadIdx.x / D;
-    const int rows_per_iter = blockDim.x / D;
-    const int src_lane = (lane_id() & ~(D - 1)) + (D - 1);
-    const uint32_t *rec32 = (const uint32_t *)s.records;
-    for (int64_t c0 = (int64_t)blockIdx.x * chunk; c0 < m; c0 += (int64_t)gridDim.x * chunk) {
-        const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
-        for (int i = threadIdx.x; i < cells; i += blockDim.x) lds[i] = 0ULL;
-        __syncthreads();
-        for (int64_t i = c0 + rr; i < c1; i += rows_per_iter) {
-            int64_t row = direct ? i : (int64_t)rows[i];
-            if ((uint64_t)row >= (uint64_t)s.n) row = 0;  // never taken: ids come from the row lists
-            const uint32_t w = rec32[row * D + sub];
-            const uint32_t gh = __shfl(w, src_lane, 64);
+    const int64_t chunk = hist_chunk(s, m);
+    const int64_t c0 = (int64_t)blockIdx.x * chunk;
+    if (c0 >= m) return;
+    const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
+    const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride;
+    for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
+    __syncthreads();
+    const int lane = lane_id();
+    const int sub = threadIdx.x % LPR;
+    const int rr = threadIdx.x / LPR;
+    const int rpp = blockDim.x / LPR;
+    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
+    const uint4 *rec = (const uint4 *)s.records;
+    for (int64_t i0 = c0; i0 < c1; i0 += (int64_t)kHistUnroll * rpp) {
+        uint4 w[kHistUnroll];
+        bool ok[kHistUnroll];
+#pragma unroll
+        for (int u = 0; u < kHistUnroll; ++u) {
+            const int64_t i = i0 + (int64_t)u * rpp + rr;
+            ok[u] = i < c1;
+            int64_t row = 0;
+            if (ok[u]) {
+                row = direct ? i : (int64_t)rows[i];
+                if ((uint64_t)row >= (uint64_t)s.n) row = 0;  // never taken: ids come from the row lists
+            }
+            w[u] = ok[u] ? rec[row * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < kHistUnroll; ++u) {
+            const uint32_t gh = __shfl(w[u].w, src_lane, 64);
+            if (!ok[u]) continue;
             const int g = (int)(int8_t)(gh >> 16);
             const int h = (int)(int8_t)(gh >> 24);
-            const unsigned long long packed = (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
+            const unsigned long long packed =
+                (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
+            const uint32_t d[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int f = sub * 4 + j;
-                if (f < F) atomicAdd(&lds[f * ls + ((w >> (8 * j)) & 255u)], packed);
-            }
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int f = sub * 16 + q * 4 + j;
+                    if (f < F) atomicAdd(&lds[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
+                }
         }
-        __syncthreads();
-        for (int c = threadIdx.x; c < cells; c += blockDim.x) {
-            const unsigned long long v = lds[c];
-            if (v == 0ULL) continue;
-            const int f = c / ls;
-            const int b = c - f * ls;
-            const int cnt = (int)(v & 0xFFFFFULL);
-            const int hs = (int)((v >> 20) & 0x3FFFFFULL);
-            const int gs = (int)((long long)v >> 42);
-            int32_t *o = out + ((size_t)f * nb + b) * 3;
-            if (gs) atomicAdd(o + 0, gs);
-            if (hs) atomicAdd(o + 1, hs);
-            atomicAdd(o + 2, cnt);
-        }
-        __syncthreads();
+    }
+    __syncthreads();
+    const int ps = s.part_stride;
+    unsigned long long *out = s.part + (size_t)blockIdx.x * F * ps;
+    for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
+        const int f = c / ps;
+        const int b = c - f * ps;
+        out[c] = b < nb ? lds[f * ls + b] : 0ULL;
     }
 }
 
@@ -303,26 +317,22 @@ __global__ __launch_bounds__(512) void k_hist(DevState s, int root_mode, int64_t
 // bin follows default_left, otherwise bin <= threshold goes left) into the
 // other row buffer: left rows fill [begin, begin + n_left), right rows the
 // rest. Each block counts its chunk, reserves its output with one atomic per
-// side, and scatters with ballot ranks. The order inside a child is not the
+// side, and scatters tile by tile with ballot ranks; each thread keeps
+// kPartUnroll rows in flight. The order inside a child is not the
 // reference's (blocks land in reservation order); every consumer is
-// order-free because histograms are integer sums. The block also zeroes the
-// histogram buffer the built child accumulates into.
+// order-free because histograms are integer sums.
+constexpr int kPartUnroll = 8;
+
 __global__ __launch_bounds__(256) void k_partition(DevState s) {
-    __shared__ int wave_l[4], wave_r[4];
+    __shared__ int wave_l[kPartUnroll][4], wave_r[kPartUnroll][4];
+    __shared__ int red[4];
     __shared__ long long base_l, base_r;
     const Step st = *s.step;
     if (!st.active) return;
-    {
-        const size_t cells = (size_t)s.n_features * s.n_bins * 3;
-        int32_t *ch = s.hist + (size_t)st.child_hist * cells;
-        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < cells;
-             i += (size_t)gridDim.x * blockDim.x)
-            ch[i] = 0;
-    }
     const int64_t m = st.end - st.begin;
     int64_t chunk = (m + gridDim.x - 1) / gridDim.x;
+    if (chunk < 2048) chunk = 2048;
     chunk = (chunk + 255) / 256 * 256;
-    if (chunk < 256) chunk = 256;
     const int64_t c0 = (int64_t)blockIdx.x * chunk;
     if (c0 >= m) return;
     const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
@@ -331,74 +341,97 @@ __global__ __launch_bounds__(256) void k_partition(DevState s) {
     const uint8_t *col = s.bins_cm + (size_t)st.feature * s.n;
     const int mb = st.missing_bin, thr = st.bin, dl = st.default_left;
     const int lane = lane_id(), w = threadIdx.x >> 6;
-    // pass 1: count
+    const int64_t tile = (int64_t)blockDim.x * kPartUnroll;
+    // pass 1: count rows going left
     int my_l = 0;
-    for (int64_t i = c0 + threadIdx.x; i < c1; i += blockDim.x) {
-        int32_t row = src[i];
-        if ((uint64_t)row >= (uint64_t)s.n) row = 0;
-        int b = col[row];
-        my_l += (b == mb) ? dl : (b <= thr);
+    for (int64_t t0 = c0; t0 < c1; t0 += tile) {
+        int32_t r[kPartUnroll];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) {
+            const int64_t i = t0 + (int64_t)u * blockDim.x + threadIdx.x;
+            r[u] = i < c1 ? src[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) {
+            if (r[u] < 0) continue;
+            const int32_t row = (uint64_t)r[u] < (uint64_t)s.n ? r[u] : 0;
+            const int b = col[row];
+            my_l += (b == mb) ? dl : (b <= thr);
+        }
     }
-    long long tl = wave_sum_ll(my_l);
-    if (lane == 0) wave_l[w] = (int)tl;
+    const long long tl = wave_sum_ll(my_l);
+    if (lane == 0) red[w] = (int)tl;
     __syncthreads();
     if (threadIdx.x == 0) {
         long long nl = 0;
-        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) nl += wave_l[i];
-        long long nr = (c1 - c0) - nl;
+        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) nl += red[i];
+        const long long nr = (c1 - c0) - nl;
         base_l = nl ? (long long)atomicAdd((unsigned long long *)&s.cursor[0], (unsigned long long)nl) : 0;
         base_r = nr ? (long long)atomicAdd((unsigned long long *)&s.cursor[1], (unsigned long long)nr) : 0;
     }
     __syncthreads();
     long long run_l = base_l, run_r = base_r;
     const int64_t n_left = st.n_left;
-    // pass 2: scatter, tile by tile in order
-    for (int64_t t0 = c0; t0 < c1; t0 += blockDim.x) {
-        const int64_t i = t0 + threadIdx.x;
-        const bool valid = i < c1;
-        int32_t row = 0;
-        bool left = false;
-        if (valid) {
-            row = src[i];
-            if ((uint64_t)row >= (uint64_t)s.n) row = 0;
-            int b = col[row];
-            left = (b == mb) ? (dl != 0) : (b <= thr);
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    // pass 2: scatter; a tile is kPartUnroll sub-tiles of blockDim rows
+    for (int64_t t0 = c0; t0 < c1; t0 += tile) {
+        int32_t r[kPartUnroll];
+        bool left[kPartUnroll], right[kPartUnroll];
+        unsigned long long lm[kPartUnroll], rm[kPartUnroll];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) {
+            const int64_t i = t0 + (int64_t)u * blockDim.x + threadIdx.x;
+            r[u] = i < c1 ? src[i] : -1;
         }
-        const bool right = valid && !left;
-        const unsigned long long lm = __ballot(left), rm = __ballot(right);
-        const unsigned long long below = (1ULL << lane) - 1ULL;
-        if (lane == 0) {
-            wave_l[w] = __popcll(lm);
-            wave_r[w] = __popcll(rm);
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) {
+            left[u] = right[u] = false;
+            if (r[u] >= 0) {
+                const int32_t row = (uint64_t)r[u] < (uint64_t)s.n ? r[u] : 0;
+                const int b = col[row];
+                left[u] = (b == mb) ? (dl != 0) : (b <= thr);
+                right[u] = !left[u];
+            }
+            lm[u] = __ballot(left[u]);
+            rm[u] = __ballot(right[u]);
+            if (lane == 0) {
+                wave_l[u][w] = __popcll(lm[u]);
+                wave_r[u][w] = __popcll(rm[u]);
+            }
         }
         __syncthreads();
-        long long off_l = 0, off_r = 0, tot_l = 0, tot_r = 0;
-        for (int k = 0; k < (int)(blockDim.x >> 6); ++k) {
-            if (k < w) {
-                off_l += wave_l[k];
-                off_r += wave_r[k];
+#pragma unroll
+        for (int u = 0; u < kPartUnroll; ++u) {
+            long long off_l = 0, off_r = 0, tot_l = 0, tot_r = 0;
+            for (int k = 0; k < (int)(blockDim.x >> 6); ++k) {
+                if (k < w) {
+                    off_l += wave_l[u][k];
+                    off_r += wave_r[u][k];
+                }
+                tot_l += wave_l[u][k];
+                tot_r += wave_r[u][k];
             }
-            tot_l += wave_l[k];
-            tot_r += wave_r[k];
+            if (left[u]) {
+                const long long p = run_l + off_l + __popcll(lm[u] & below);
+                if (p < n_left) dst[p] = r[u];
+                else atomicOr(s.error, 1);
+            } else if (right[u]) {
+                const long long p = n_left + run_r + off_r + __popcll(rm[u] & below);
+                if (p < m) dst[p] = r[u];
+                else atomicOr(s.error, 1);
+            }
+            run_l += tot_l;
+            run_r += tot_r;
         }
-        if (left) {
-            long long p = run_l + off_l + __popcll(lm & below);
-            if (p < n_left) dst[p] = row;
-            else atomicOr(s.error, 1);
-        } else if (right) {
-            long long p = n_left + run_r + off_r + __popcll(rm & below);
-            if (p < m) dst[p] = row;
-            else atomicOr(s.error, 1);
-        }
-        run_l += tot_l;
-        run_r += tot_r;
         __syncthreads();
     }
 }
 
 // ------------------------------------------------------------------- split
-// One wave per (child, feature). Child 0 is the built child; child 1 is the
-// sibling, parent - built, written back over the parent's buffer. The scan
+// One block (8 waves) per feature. First the built child's histogram is
+// merged from the block partials of its build and stored; the sibling is
+// parent - built, written back over the parent's buffer. Then waves 0-3 scan
+// the built child and waves 4-7 the sibling, one bin per thread. The scan
 // follows split.find_best_split (src/mojotrees/split.mojo:601-1360) with the
 // sums kept as integers and each candidate scored by quantized_split_gain
 // (quantized_gradient.mojo:3283-3310): ascending bins, missing-left scored
@@ -407,13 +440,22 @@ __global__ __launch_bounds__(256) void k_partition(DevState s) {
 //
 // The last block to finish folds the features of each child (strict '>',
 // lowest feature on ties), computes the children's leaf values
-// (quantized_leaf_output), records the nodes in the tree arrays, replaces
-// the parent's frontier slot with the left child and appends the right one,
-// then picks the next leaf (max gain, lowest slot on ties;
-// growth_policy.mojo:659-677) and writes the next step descriptor with the
-// left count read from the parent's histogram.
-__global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
-    const int lane = lane_id();
+// (quantized_leaf_output), records the nodes, replaces the parent's frontier
+// slot with the left child and appends the right one, then picks the next
+// leaf (max gain, lowest slot on ties; growth_policy.mojo:659-677) and writes
+// the next step with the left count read from that leaf's histogram.
+constexpr int kSplitThreads = 512;
+constexpr int kMaxScan = 256;  // 2 x max features
+
+__global__ __launch_bounds__(kSplitThreads) void k_split(DevState s, int root_mode) {
+    __shared__ long long cgs[2][256], chs[2][256], ccs[2][256];
+    __shared__ long long wtot[8][3];
+    __shared__ double wgain[8];
+    __shared__ int word_[8];
+    __shared__ unsigned int s_ticket;
+    __shared__ ScanResult sres[kMaxScan];
+    __shared__ long long part_acc[3][256];
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const HyperParams &hp = s.hp;
     const int F = s.n_features, nb = s.n_bins;
     const size_t hsz = (size_t)F * nb * 3;
@@ -424,131 +466,150 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
     }
     const Round rd = *s.round;
     const double gu = rd.grad_units, hu = rd.hess_units;
-    const int nchild = root_mode ? 1 : 2;
-    const int blk = blockIdx.x;
-    const int child = blk / F;
-    const int f = blk - child * F;
-
-    int64_t n_child;
-    int depth_child;
-    const int32_t *cells_a;
-    const int32_t *cells_b = nullptr;
-    int32_t *write_back = nullptr;
+    const int f = blockIdx.x;
+    int64_t m_built, m_sib = 0;
+    int built_buf, depth_child;
     if (root_mode) {
-        n_child = hp.bagging ? s.cursor[0] : s.n;
+        m_built = hp.bagging ? s.cursor[0] : s.n;
+        built_buf = 0;
         depth_child = 0;
-        cells_a = s.hist + (size_t)f * nb * 3;
     } else {
         const int64_t m = st.end - st.begin;
-        const int64_t n_built = st.builds_left ? st.n_left : m - st.n_left;
-        const int32_t *built = s.hist + (size_t)st.child_hist * hsz + (size_t)f * nb * 3;
-        int32_t *par = s.hist + (size_t)st.parent_hist * hsz + (size_t)f * nb * 3;
+        m_built = st.builds_left ? st.n_left : m - st.n_left;
+        m_sib = m - m_built;
+        built_buf = st.child_hist;
         depth_child = st.depth + 1;
-        if (child == 0) {
-            n_child = n_built;
-            cells_a = built;
-        } else {
-            n_child = m - n_built;
-            cells_a = par;
-            cells_b = built;
-            write_back = par;
-        }
     }
-    // 4 consecutive bins per lane
-    long long g[4], h[4], c[4];
+    // ---- merge the built child's partials: thread -> (bin, half of the parts)
+    const int64_t chunk = hist_chunk(s, m_built);
+    const int64_t nparts = m_built > 0 ? (m_built + chunk - 1) / chunk : 0;
+    {
+        const int bin = tid & 255, half = tid >> 8;
+        long long g = 0, h = 0, c = 0;
+        if (bin < nb) {
+            const size_t pstride = (size_t)F * s.part_stride;
+            const unsigned long long *p = s.part + (size_t)f * s.part_stride + bin;
+            int64_t b = half;
+            for (; b + 14 < nparts; b += 16) {
+                unsigned long long v[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = lane * 4 + j;
-        if (b < nb) {
-            long long vg = cells_a[3 * b], vh = cells_a[3 * b + 1], vc = cells_a[3 * b + 2];
-            if (cells_b) {
-                vg -= cells_b[3 * b];
-                vh -= cells_b[3 * b + 1];
-                vc -= cells_b[3 * b + 2];
-                write_back[3 * b] = (int32_t)vg;
-                write_back[3 * b + 1] = (int32_t)vh;
-                write_back[3 * b + 2] = (int32_t)vc;
+                for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(b + 2 * u) * pstride];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    c += (long long)(v[u] & 0xFFFFFULL);
+                    h += (long long)((v[u] >> 20) & 0x3FFFFFULL);
+                    g += (long long)v[u] >> 42;
+                }
             }
-            g[j] = vg;
-            h[j] = vh;
-            c[j] = vc;
-        } else {
-            g[j] = h[j] = c[j] = 0;
+            for (; b < nparts; b += 2) {
+                const unsigned long long v = p[(size_t)b * pstride];
+                c += (long long)(v & 0xFFFFFULL);
+                h += (long long)((v >> 20) & 0x3FFFFFULL);
+                g += (long long)v >> 42;
+            }
         }
+        if (half == 1) {
+            part_acc[0][bin] = g;
+            part_acc[1][bin] = h;
+            part_acc[2][bin] = c;
+        }
+        __syncthreads();
+        if (half == 0) {
+            g += part_acc[0][bin];
+            h += part_acc[1][bin];
+            c += part_acc[2][bin];
+            cgs[0][bin] = g;
+            chs[0][bin] = h;
+            ccs[0][bin] = c;
+            long long sgv = 0, shv = 0, scv = 0;
+            if (bin < nb) {
+                int32_t *ob = s.hist + (size_t)built_buf * hsz + ((size_t)f * nb + bin) * 3;
+                ob[0] = (int32_t)g;
+                ob[1] = (int32_t)h;
+                ob[2] = (int32_t)c;
+                if (!root_mode) {
+                    int32_t *pp = s.hist + (size_t)st.parent_hist * hsz + ((size_t)f * nb + bin) * 3;
+                    sgv = (long long)pp[0] - g;
+                    shv = (long long)pp[1] - h;
+                    scv = (long long)pp[2] - c;
+                    pp[0] = (int32_t)sgv;
+                    pp[1] = (int32_t)shv;
+                    pp[2] = (int32_t)scv;
+                }
+            }
+            cgs[1][bin] = sgv;
+            chs[1][bin] = shv;
+            ccs[1][bin] = scv;
+        }
+        __syncthreads();
     }
-    // prefix sums
-#pragma unroll
-    for (int j = 1; j < 4; ++j) {
-        g[j] += g[j - 1];
-        h[j] += h[j - 1];
-        c[j] += c[j - 1];
+    // ---- scan: waves 0-3 the built child, waves 4-7 the sibling; one bin each
+    const int child = tid >> 8;
+    const int bin = tid & 255;
+    const int cw = wv & 3;  // wave within the child
+    const long long vg = cgs[child][bin], vh = chs[child][bin], vc = ccs[child][bin];
+    const long long ig = wave_incl_scan(vg), ih = wave_incl_scan(vh), ic = wave_incl_scan(vc);
+    if (lane == 63) {
+        wtot[wv][0] = ig;
+        wtot[wv][1] = ih;
+        wtot[wv][2] = ic;
     }
-    const long long ig = wave_incl_scan(g[3]), ih = wave_incl_scan(h[3]), ic = wave_incl_scan(c[3]);
-    const long long eg = ig - g[3], eh = ih - h[3], ec = ic - c[3];
-    const long long TG = __shfl(ig, 63, 64), TH = __shfl(ih, 63, 64), TC = __shfl(ic, 63, 64);
+    __syncthreads();
+    long long pg = 0, ph = 0, pc = 0, TG = 0, TH = 0, TC = 0;
+    for (int k = 0; k < 4; ++k) {
+        const int ww = (child << 2) + k;
+        if (k < cw) {
+            pg += wtot[ww][0];
+            ph += wtot[ww][1];
+            pc += wtot[ww][2];
+        }
+        TG += wtot[ww][0];
+        TH += wtot[ww][1];
+        TC += wtot[ww][2];
+    }
+    const long long lg = pg + ig, lh = ph + ih, lc = pc + ic;  // inclusive prefix at `bin`
+    const int64_t n_child = child == 0 ? m_built : m_sib;
     const int mb = s.missing_bin[f];
-    long long mg = 0, mh = 0, mc = 0;
-    if (mb >= 0) {
-        // bin mb's own values: inclusive(mb) - inclusive(mb - 1)
-        const int ln = mb >> 2, jj = mb & 3;
-        long long pg = (jj ? g[jj - 1] : 0), ph = (jj ? h[jj - 1] : 0), pc = (jj ? c[jj - 1] : 0);
-        long long cg = 0, chh = 0, cc = 0;
-        // select this lane's j-th element without dynamic register indexing
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (j == jj) {
-                cg = g[j];
-                chh = h[j];
-                cc = c[j];
-            }
-        long long vg = cg - pg, vh = chh - ph, vc = cc - pc;
-        mg = __shfl(vg, ln, 64);
-        mh = __shfl(vh, ln, 64);
-        mc = __shfl(vc, ln, 64);
-    }
-    const bool gated = (hp.max_depth > 0 && depth_child >= hp.max_depth) ||
+    const bool gated = (root_mode && child == 1) || (hp.max_depth > 0 && depth_child >= hp.max_depth) ||
                        n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
                        !s.feature_mask[(size_t)rd.tree_index * F + f];
     double best_gain = 0.0;
     int best_order = 0x7FFFFFFF;
     if (!gated) {
+        const long long mg = mb >= 0 ? cgs[child][mb] : 0, mh = mb >= 0 ? chs[child][mb] : 0,
+                        mc = mb >= 0 ? ccs[child][mb] : 0;
         const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
-        // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
-        long long hmin = 0;
+        long long hmin = 0;  // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
         if (hp.min_sum_hessian > 0.0) {
-            double u = hp.min_sum_hessian * hu;
+            const double u = hp.min_sum_hessian * hu;
             double fl = floor(u);
             if (fl < u) fl += 1.0;
             hmin = (long long)fl;
         }
         const long long min_c = hp.min_data_in_leaf;
-        const double parent = qscore(TG, TH, gu, hu, l1, l2);
         const int n_scan = mb >= 0 ? mb : nb;
         int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
         if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int b = lane * 4 + j;
-            if (b >= lim) continue;
-            const long long lg = eg + g[j], lh = eh + h[j], lc = ec + c[j];
+        if (bin < lim) {
+            const double parent = qscore(TG, TH, gu, hu, l1, l2);
             if (mb >= 0) {
                 const long long ag = lg + mg, ah = lh + mh, ac = lc + mc;
                 const long long rg = TG - ag, rh = TH - ah, rc = TC - ac;
                 if (!(ah < hmin || rh < hmin || ac < min_c || rc < min_c)) {
-                    double gain = qscore(ag, ah, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                    const double gain = qscore(ag, ah, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
                     if (gain > best_gain) {
                         best_gain = gain;
-                        best_order = 2 * b;
+                        best_order = 2 * bin;
                     }
                 }
             }
             if (mb < 0 || mc > 0) {
                 const long long rg = TG - lg, rh = TH - lh, rc = TC - lc;
                 if (!(lh < hmin || rh < hmin || lc < min_c || rc < min_c)) {
-                    double gain = qscore(lg, lh, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                    const double gain = qscore(lg, lh, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
                     if (gain > best_gain) {
                         best_gain = gain;
-                        best_order = 2 * b + 1;
+                        best_order = 2 * bin + 1;
                     }
                 }
             }
@@ -556,54 +617,86 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
     }
     wave_argmax(best_gain, best_order);
     if (lane == 0) {
-        ScanResult r;
-        r.gain = best_gain;
-        r.found = best_order != 0x7FFFFFFF;
-        r.bin = r.found ? best_order >> 1 : -1;
-        r.default_left = r.found ? ((best_order & 1) == 0) : 0;
-        r.pad_ = 0;
-        r.tot_g = TG;
-        r.tot_h = TH;
-        r.tot_c = TC;
-        s.scan[blk] = r;
+        wgain[wv] = best_gain;
+        word_[wv] = best_order;
+    }
+    __syncthreads();
+    if (tid == 0 || tid == 256) {
+        double bg = wgain[child << 2];
+        int bo = word_[child << 2];
+        for (int k = 1; k < 4; ++k) {
+            const double og = wgain[(child << 2) + k];
+            const int oo = word_[(child << 2) + k];
+            if (og > bg || (og == bg && oo < bo)) {
+                bg = og;
+                bo = oo;
+            }
+        }
+        if (!(root_mode && child == 1)) {
+            ScanResult r;
+            r.gain = bg;
+            r.found = bo != 0x7FFFFFFF;
+            r.bin = r.found ? bo >> 1 : -1;
+            r.default_left = r.found ? ((bo & 1) == 0) : 0;
+            r.pad_ = 0;
+            r.tot_g = TG;
+            r.tot_h = TH;
+            r.tot_c = TC;
+            s.scan[child * F + f] = r;
+        }
     }
     __threadfence();
-    unsigned int ticket = 0;
-    if (lane == 0) ticket = atomicAdd(s.ticket, 1u);
-    ticket = __shfl(ticket, 0, 64);
-    if (ticket != (unsigned int)(nchild * F - 1)) return;
+    __syncthreads();
+    if (tid == 0) s_ticket = atomicAdd(s.ticket, 1u);
+    __syncthreads();
+    if (s_ticket != (unsigned int)(F - 1)) return;
     __threadfence();
 
     // ------------------------------------------------ last block: fold + pick
-    double cg_[2];
-    int cf_[2];
-    for (int ch = 0; ch < nchild; ++ch) {
+    const int nchild = root_mode ? 1 : 2;
+    for (int i = tid; i < nchild * F; i += blockDim.x) {
+        const ScanResult *p = &s.scan[i];
+        ScanResult r;
+        r.found = load_agent(&p->found);
+        r.gain = load_agent_f64(&p->gain);
+        r.bin = load_agent(&p->bin);
+        r.default_left = load_agent(&p->default_left);
+        r.pad_ = 0;
+        r.tot_g = load_agent(&p->tot_g);
+        r.tot_h = load_agent(&p->tot_h);
+        r.tot_c = load_agent(&p->tot_c);
+        sres[i] = r;
+    }
+    __syncthreads();
+    if (wv < nchild) {
         double bg = 0.0;
         int bf = 0x7FFFFFFF;
         for (int ff = lane; ff < F; ff += 64) {
-            const ScanResult *p = &s.scan[ch * F + ff];
-            const int found = load_agent(&p->found);
-            const double gg = load_agent_f64(&p->gain);
-            if (found && gg > bg) {
-                bg = gg;
+            const ScanResult &r = sres[wv * F + ff];
+            if (r.found && r.gain > bg) {
+                bg = r.gain;
                 bf = ff;
             }
         }
         wave_argmax(bg, bf);
-        cg_[ch] = bg;
-        cf_[ch] = bf;
+        if (lane == 0) {
+            wgain[wv] = bg;
+            word_[wv] = bf;
+        }
     }
-    if (lane == 0) {
+    __syncthreads();
+    if (tid == 0) {
         int32_t *meta = s.t_meta;
         const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
         auto fill_slot = [&](Slot &sl, int ch) {
-            sl.found = cf_[ch] != 0x7FFFFFFF;
+            const int bf = word_[ch];
+            sl.found = bf != 0x7FFFFFFF;
             if (sl.found) {
-                const ScanResult *p = &s.scan[ch * F + cf_[ch]];
-                sl.feature = cf_[ch];
-                sl.bin = load_agent(&p->bin);
-                sl.default_left = load_agent(&p->default_left);
-                sl.gain = cg_[ch];
+                const ScanResult &r = sres[ch * F + bf];
+                sl.feature = bf;
+                sl.bin = r.bin;
+                sl.default_left = r.default_left;
+                sl.gain = wgain[ch];
             } else {
                 sl.feature = -1;
                 sl.bin = -1;
@@ -623,31 +716,28 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
             s.t_count[id] = cnt;
         };
         if (root_mode) {
-            const ScanResult *p = &s.scan[0];
-            const long long G = load_agent(&p->tot_g), H = load_agent(&p->tot_h), C = load_agent(&p->tot_c);
-            new_node(0, qleaf(G, H, gu, hu, l1, l2), (double)C);
+            const ScanResult &r = sres[0];
+            new_node(0, qleaf(r.tot_g, r.tot_h, gu, hu, l1, l2), (double)r.tot_c);
             meta[0] = 1;
             meta[1] = 1;
             Slot sl;
             sl.begin = 0;
-            sl.end = C;
+            sl.end = r.tot_c;
             sl.node = 0;
             sl.buf = 0;
             sl.hist = 0;
             sl.depth = 0;
             fill_slot(sl, 0);
             s.slots[0] = sl;
-            s.arc_rows[(size_t)rd.tree_index * hp.num_leaves + 0] = C;
+            s.arc_rows[(size_t)rd.tree_index * hp.num_leaves + 0] = r.tot_c;
         } else {
-            const ScanResult *pb = &s.scan[0];
-            const ScanResult *ps = &s.scan[F];
-            const long long bG = load_agent(&pb->tot_g), bH = load_agent(&pb->tot_h), bC = load_agent(&pb->tot_c);
-            const long long sG = load_agent(&ps->tot_g), sH = load_agent(&ps->tot_h), sC = load_agent(&ps->tot_c);
+            const ScanResult &b = sres[0];
+            const ScanResult &sb = sres[F];
             const bool bl = st.builds_left != 0;
-            const long long LG = bl ? bG : sG, LH = bl ? bH : sH, LC = bl ? bC : sC;
-            const long long RG = bl ? sG : bG, RH = bl ? sH : bH, RC = bl ? sC : bC;
-            new_node(st.node_left, qleaf(LG, LH, gu, hu, l1, l2), (double)LC);
-            new_node(st.node_right, qleaf(RG, RH, gu, hu, l1, l2), (double)RC);
+            const ScanResult &Lr = bl ? b : sb;
+            const ScanResult &Rr = bl ? sb : b;
+            new_node(st.node_left, qleaf(Lr.tot_g, Lr.tot_h, gu, hu, l1, l2), (double)Lr.tot_c);
+            new_node(st.node_right, qleaf(Rr.tot_g, Rr.tot_h, gu, hu, l1, l2), (double)Rr.tot_c);
             const int pn = st.parent_node;
             s.t_feature[pn] = st.feature;
             s.t_threshold[pn] = st.bin;
@@ -676,41 +766,53 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
         }
     }
     __syncthreads();
-    // pick the next leaf
-    const int n_leaves = s.t_meta[1];
-    const int n_nodes = s.t_meta[0];
-    double bg = 0.0;
-    int bi = 0x7FFFFFFF;
-    if (n_leaves < hp.num_leaves) {
-        for (int i = lane; i < n_leaves; i += 64) {
-            const Slot &sl = s.slots[i];
-            if (sl.found && sl.gain > 0.0 && sl.gain > bg) {
-                bg = sl.gain;
-                bi = i;
+    // pick the next leaf (wave 0)
+    __shared__ int s_pick;
+    __shared__ Slot s_slot;
+    if (wv == 0) {
+        const int n_leaves = s.t_meta[1];
+        double bg = 0.0;
+        int bi = 0x7FFFFFFF;
+        if (n_leaves < hp.num_leaves) {
+            for (int i = lane; i < n_leaves; i += 64) {
+                const Slot &sl = s.slots[i];
+                if (sl.found && sl.gain > 0.0 && sl.gain > bg) {
+                    bg = sl.gain;
+                    bi = i;
+                }
             }
         }
-    }
-    wave_argmax(bg, bi);
-    if (bi == 0x7FFFFFFF) {
+        wave_argmax(bg, bi);
         if (lane == 0) {
+            s_pick = bi;
+            if (bi != 0x7FFFFFFF) s_slot = s.slots[bi];
+        }
+    }
+    __syncthreads();
+    const int bi = s_pick;
+    if (bi == 0x7FFFFFFF) {
+        if (tid == 0) {
             s.step->active = 0;
             *s.ticket = 0u;
         }
         return;
     }
-    const Slot sl = s.slots[bi];
-    const int32_t *ph = s.hist + (size_t)sl.hist * hsz + (size_t)sl.feature * nb * 3;
+    const Slot sl = s_slot;
+    const int32_t *pick_h = s.hist + (size_t)sl.hist * hsz + (size_t)sl.feature * nb * 3;
     const int fmb = s.missing_bin[sl.feature];
     long long nl = 0;
-    for (int j = 0; j < 4; ++j) {
-        const int b = lane * 4 + j;
-        if (b < nb) {
-            const bool goes_left = (b == fmb) ? (sl.default_left != 0) : (b <= sl.bin);
-            if (goes_left) nl += load_agent(&ph[3 * b + 2]);
-        }
+    if (tid < nb) {
+        const bool goes_left = (tid == fmb) ? (sl.default_left != 0) : (tid <= sl.bin);
+        if (goes_left) nl = load_agent(&pick_h[3 * tid + 2]);
     }
     nl = wave_sum_ll(nl);
-    if (lane == 0) {
+    if (lane == 0) wtot[wv][0] = nl;
+    __syncthreads();
+    if (tid == 0) {
+        long long tot = 0;
+        for (int k = 0; k < 8; ++k) tot += wtot[k][0];
+        const int n_leaves = s.t_meta[1];
+        const int n_nodes = s.t_meta[0];
         Step ns;
         ns.active = 1;
         ns.parent_slot = bi;
@@ -722,8 +824,8 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
         ns.src_buf = sl.buf;
         ns.begin = sl.begin;
         ns.end = sl.end;
-        ns.n_left = nl;
-        ns.builds_left = nl <= (sl.end - sl.begin) - nl;
+        ns.n_left = tot;
+        ns.builds_left = tot <= (sl.end - sl.begin) - tot;
         ns.parent_hist = sl.hist;
         ns.child_hist = n_leaves;
         ns.depth = sl.depth;
@@ -736,7 +838,7 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
         s.cursor[0] = 0;
         s.cursor[1] = 0;
         s.arc_rows[(size_t)rd.tree_index * hp.num_leaves + n_leaves] =
-            ns.builds_left ? nl : (sl.end - sl.begin) - nl;
+            ns.builds_left ? tot : (sl.end - sl.begin) - tot;
         *s.ticket = 0u;
     }
 }
@@ -744,12 +846,12 @@ __global__ __launch_bounds__(64) void k_split(DevState s, int root_mode) {
 // ------------------------------------------------------------- score update
 // raw[r] += lr * value(leaf of r), fused (boosting._add_by_leaf,
 // src/mojotrees/boosting.mojo:1991-2112), by walking the tree for every row
-// so sampled-out rows are covered too (the traversal route, :1947). A
-// single-leaf tree whose value is below 1e-12 is the reference's stopping
-// condition (:2898-2907) and adds nothing.
+// over the row's record (its bins are contiguous), so sampled-out rows are
+// covered too (the traversal route, :1947). A single-leaf tree whose value is
+// below 1e-12 is the reference's stopping condition (:2898-2907) and adds
+// nothing.
 __global__ __launch_bounds__(256) void k_score(DevState s) {
     extern __shared__ int32_t tnode[];  // 5 ints per node
-    __shared__ double tval[1];
     const int n_nodes = s.t_meta[0];
     const int n_leaves = s.t_meta[1];
     if (n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
@@ -762,22 +864,23 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
         tnode[5 * i + 4] = s.t_missing_bin[i] * 2 + (s.t_default_left[i] ? 1 : 0);
         vals[i] = s.t_value[i];
     }
-    (void)tval;
     __syncthreads();
     const double lr = s.hp.learning_rate;
     const int K = s.hp.num_class;
     const int k = s.round->class_k;
+    const int rec = s.rec_bytes;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
+        const uint8_t *rb = s.records + r * rec;
         int node = 0;
         // children always have larger ids than their parent, so a walk ends
         // within n_nodes steps
         for (int d = 0; d < n_nodes && tnode[5 * node] >= 0; ++d) {
             const int f = tnode[5 * node];
-            const int b = s.bins_cm[(size_t)f * s.n + r];
+            const int b = rb[f];
             const int md = tnode[5 * node + 4];
             const int mbin = md >> 1;  // arithmetic shift keeps -1
-            bool left = (b == mbin) ? (md & 1) : (b <= tnode[5 * node + 1]);
+            const bool left = (b == mbin) ? (md & 1) : (b <= tnode[5 * node + 1]);
             node = left ? tnode[5 * node + 2] : tnode[5 * node + 3];
             if ((unsigned)node >= (unsigned)n_nodes) node = 0;
         }
@@ -853,26 +956,32 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
+size_t score_lds_bytes(const DevState &s) {
+    return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
+}
 size_t hist_lds_bytes(const DevState &s) { return (size_t)s.n_features * s.lds_stride * 8; }
 hipError_t prepare_hist(const DevState &s) {
-    int bytes = (int)hist_lds_bytes(s);
-    hipError_t e = hipSuccess;
+    const int bytes = (int)hist_lds_bytes(s);
+    hipError_t e = hipFuncSetAttribute((const void *)k_hist<1>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void *)k_hist<2>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void *)k_score, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)score_lds_bytes(s));
+    if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void *)k_hist<4>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_hist<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_hist<16>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_hist<32>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return hipFuncSetAttribute((const void *)k_hist<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
-hipError_t launch_hist(const DevState &s, int root_mode, int grid, int64_t chunk_limit, hipStream_t st) {
+hipError_t launch_hist(const DevState &s, int root_mode, hipStream_t st) {
     const size_t lds = hist_lds_bytes(s);
-    const int D = s.rec_bytes / 4;
-    switch (D) {
-    case 4: hipLaunchKernelGGL(k_hist<4>, dim3(grid), dim3(512), lds, st, s, root_mode, chunk_limit); break;
-    case 8: hipLaunchKernelGGL(k_hist<8>, dim3(grid), dim3(512), lds, st, s, root_mode, chunk_limit); break;
-    case 16: hipLaunchKernelGGL(k_hist<16>, dim3(grid), dim3(512), lds, st, s, root_mode, chunk_limit); break;
-    case 32: hipLaunchKernelGGL(k_hist<32>, dim3(grid), dim3(512), lds, st, s, root_mode, chunk_limit); break;
+    const int lpr = s.rec_bytes / 16;
+    const dim3 grid(s.hist_grid), block(1024);
+    switch (lpr) {
+    case 1: hipLaunchKernelGGL(k_hist<1>, grid, block, lds, st, s, root_mode); break;
+    case 2: hipLaunchKernelGGL(k_hist<2>, grid, block, lds, st, s, root_mode); break;
+    case 4: hipLaunchKernelGGL(k_hist<4>, grid, block, lds, st, s, root_mode); break;
+    case 8: hipLaunchKernelGGL(k_hist<8>, grid, block, lds, st, s, root_mode); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -882,12 +991,8 @@ hipError_t launch_partition(const DevState &s, int grid, hipStream_t st) {
     return hipGetLastError();
 }
 hipError_t launch_split(const DevState &s, int root_mode, hipStream_t st) {
-    const int blocks = (root_mode ? 1 : 2) * s.n_features;
-    hipLaunchKernelGGL(k_split, dim3(blocks), dim3(64), 0, st, s, root_mode);
+    hipLaunchKernelGGL(k_split, dim3(s.n_features), dim3(kSplitThreads), 0, st, s, root_mode);
     return hipGetLastError();
-}
-size_t score_lds_bytes(const DevState &s) {
-    return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
 }
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_score, dim3(grid), dim3(256), score_lds_bytes(s), st, s);

@@ -107,6 +107,11 @@ struct DevState {
     // rows and histograms
     int32_t *rows0, *rows1;
     int32_t *hist;         // num_leaves x F x n_bins x 3 (grad, hess, count)
+    unsigned long long *part;  // hist_grid x F x n_bins packed per-block partials
+    int32_t hist_grid;         // blocks of a histogram launch
+    int32_t part_stride;       // per-feature stride of a partial (even, >= n_bins)
+    int64_t hist_chunk_min;    // fewest rows a histogram block takes
+    int64_t hist_chunk_limit;  // most rows a block may pack (field bounds)
     // growth
     Step *step;
     Slot *slots;

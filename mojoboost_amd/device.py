@@ -15,6 +15,20 @@ def device_count() -> int:
     return int(lib().mbh_device_count())
 
 
+def bin_dense(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_missing=True,
+              sample_cnt=200_000, seed=1):
+    """Quantile-bin a column-major float64 matrix on the host (the library's
+    binning, not the oracle's). Returns (bins_cm uint8, missing_bin int32)."""
+    x_cm = np.ascontiguousarray(x_cm, np.float64).ravel()
+    bins = np.zeros(n_rows * n_features, np.uint8)
+    mb = np.zeros(n_features, np.int32)
+    err = C.create_string_buffer(512)
+    check(lib().mbh_bin_dense(ptr(x_cm), n_rows, n_features, max_bins, min_data_in_bin,
+                              1 if use_missing else 0, sample_cnt, seed, ptr(bins), ptr(mb),
+                              err, 512), err)
+    return bins, mb
+
+
 class Dataset:
     """A column-major uint8 binned matrix and its labels, uploaded once."""
 
@@ -74,10 +88,12 @@ class Dataset:
         return out.reshape(self.n_features, self.n_bins, 3)
 
     def bench_root_histogram(self, reps=20):
-        out = np.zeros(2)
+        """(mean, min) histogram-kernel ms and mean histogram + merge ms of a
+        root build over all rows."""
+        out = np.zeros(3)
         err = C.create_string_buffer(1024)
         check(lib().mbh_bench_root_histogram(self.h, reps, ptr(out), err, 1024), err)
-        return float(out[0]), float(out[1])
+        return float(out[0]), float(out[1]), float(out[2])
 
 
 class Fit:
@@ -101,12 +117,13 @@ class Fit:
                          ptr(self.threshold), ptr(self.left), ptr(self.right), ptr(self.value),
                          ptr(self.default_left), ptr(self.missing_bin), ptr(self.gain),
                          ptr(self.count))
-        st = np.zeros(8)
+        st = np.zeros(10)
         L.mbh_fit_stats(handle, ptr(st))
         self.stats = {
             "train_seconds": st[0], "hist_ms": st[1], "hist_bytes": st[2],
             "hist_rows_features": st[3], "hist_builds": st[4], "root_bytes": st[5],
-            "root_ms": st[6], "trees_grown": st[7],
+            "root_ms": st[6], "trees_grown": st[7], "hist_merged_ms": st[8],
+            "root_merged_ms": st[9],
         }
 
     def tree(self, t):
