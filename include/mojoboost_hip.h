@@ -98,15 +98,24 @@ void mbh_fit_arrays(const mbh_fit *fit, double *base, int64_t *node_offset,
 /* Final raw scores of the training rows, row-major n_rows * num_class. */
 int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
                           int32_t err_len);
-/* out[0] wall seconds of the training loop (enqueue to final sync),
- * out[1] summed histogram-kernel milliseconds (time_histograms only),
- * out[2] histogram algorithmic bytes (sum over builds of rows * (F + 2)),
- * out[3] histogram rows * features, out[4] histogram launches that built,
- * out[5] root-build algorithmic bytes, out[6] root-build milliseconds,
- * out[7] trees grown, out[8] summed milliseconds of histogram + split
- * kernels (the split kernel merges the histogram's block partials),
- * out[9] the same for the root builds. out has 10 entries. */
-void mbh_fit_stats(const mbh_fit *fit, double *out);
+/* Training statistics. Writes min(n_out, count) values and returns count
+ * (17). Milliseconds are summed HIP-event times and are filled only with
+ * time_histograms=1.
+ *   [0] wall seconds of the training loop (enqueue to final sync)
+ *   [1] ms of the histogram-accumulating kernels (root build + expansions)
+ *   [2] histogram algorithmic bytes of the committed trees: (root rows + the
+ *       smaller child of every split) * (n_features + 2)
+ *   [3] the same rows * n_features    [4] builds of the committed trees
+ *   [5] root-build algorithmic bytes  [6] root-build ms   [7] trees grown
+ *   [8] ms of every growth kernel (accumulation + merge/scan/plan)
+ *   [9] the same for the root build
+ *   [10] expansion launches that did work   [11] leaves expanded (including
+ *        speculative expansions the best-first replay discarded)
+ *   [12] rows accumulated by expansions     [13] parent rows partitioned
+ *   [14] expansion launches enqueued        [15] ms of those launches
+ *   [16] their algorithmic bytes: [13] * 9 (row id in, bin, row id out)
+ *        + [12] * (n_features + 2) */
+int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
 /* ------------------------------------------- stage-level (parity, bench) */
 /* Device exp and sigmoid of x[0..n). */
@@ -132,7 +141,7 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad,
 
 /* Root histogram of all rows, `reps` times back to back on resident data
  * (HIP events): out_ms[0] mean histogram-kernel milliseconds, out_ms[1] its
- * min, out_ms[2] mean milliseconds of histogram + the split kernel that
+ * min, out_ms[2] mean milliseconds of histogram + the scan kernel that
  * merges its partials. out_ms has 3 entries. */
 int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps,
                                  double *out_ms, char *err, int32_t err_len);

@@ -128,7 +128,7 @@ def lib():
         "mbh_fit_total_nodes": (I64, [V]),
         "mbh_fit_arrays": (None, [V] * 12),
         "mbh_fit_train_raw": (I32, [V, V, C.c_char_p, I32]),
-        "mbh_fit_stats": (None, [V, V]),
+        "mbh_fit_stats": (I32, [V, V, I32]),
         "mbh_exp_sigmoid": (I32, [V, I64, V, V, C.c_char_p, I32]),
         "mbh_objective_quantize": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),

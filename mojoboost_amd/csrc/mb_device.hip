@@ -2,11 +2,13 @@
 // per-round kernel sequence, tree download, and the stage-level entry points
 // of include/mojoboost_hip.h.
 //
-// A round enqueues, per tree: objective, quantize, root histogram, root split,
-// then (num_leaves - 1) x [partition, histogram, split], score update and
-// round end. No call reads device memory back until the last tree is
-// enqueued; kernels whose step is inactive (the tree stopped early) return
-// at once.
+// A round enqueues, per tree: objective, quantize, root histogram, root scan
+// (which plans the first batch), then groups of kIterChunk x [partition +
+// histogram, scan] until the device reports the tree done, then the score
+// update and round end. The host reads back only the done flag, one group
+// behind: it enqueues group k + 1 before waiting for group k's flag, so the
+// device does not idle while the host decides; launches after the tree is
+// done find an empty batch and return at once.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -111,6 +113,8 @@ struct mbh_dataset {
     }
 };
 
+constexpr int kNumStats = 17;
+
 struct mbh_fit {
     int num_class = 1;
     int objective = 0;
@@ -121,7 +125,7 @@ struct mbh_fit {
     std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
     std::vector<double> value, gain, count;
     std::vector<double> train_raw;
-    double stats[10] = {0};
+    double stats[kNumStats] = {0};
 };
 
 namespace {
@@ -132,6 +136,21 @@ struct Run {
         for (void *p : owned) (void)hipFree(p);
     }
 };
+
+struct PinnedFlags {
+    int32_t *p = nullptr;
+    ~PinnedFlags() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+// LDS row list of the partition+histogram kernel (one tile of row ids).
+constexpr size_t kPbListBytes = 4096 * 4;
+// Leaves expanded per launch, at most (the best-first replay of C2-shaped
+// trees reaches the tree's depth in iterations with 32).
+constexpr int kMaxBatch = 32;
+// [partition + histogram, scan] pairs enqueued between done-flag reads.
+constexpr int kIterChunk = 4;
 
 int64_t chunk_limit_for(int B) {
     // rows per LDS accumulation so no packed field overflows:
@@ -153,8 +172,8 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     }
     if (p->num_iterations < 0) bad("num_iterations must be nonnegative");
     if (p->num_leaves < 1) bad("num_leaves must be positive");
-    if (p->num_leaves > 2048)
-        unsup("num_leaves above 2048: the score-update kernel keeps the tree in LDS (160 KB)");
+    if (p->num_leaves > 1024)
+        unsup("num_leaves above 1024: the planner keeps the explored tree in LDS");
     if (p->min_data_in_leaf < 0) bad("min_data_in_leaf must be nonnegative");
     if (!(p->learning_rate > 0.0)) bad("learning_rate must be positive");
     if (!(p->lambda_l2 >= 0.0) || !(p->lambda_l1 >= 0.0)) bad("lambda_l1 and lambda_l2 must be nonnegative");
@@ -171,10 +190,13 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         bad("binary labels must be in [0, 1]");
 }
 
-// Histogram launch geometry and the partial buffer. A build of m rows runs
-// ceil(m / chunk) blocks with chunk = clamp(ceil(m / grid), chunk_min,
+// Histogram launch geometry and the partial buffer. The root build of m rows
+// runs ceil(m / chunk) blocks with chunk = clamp(ceil(m / grid), chunk_min,
 // chunk_limit); the grid is widened when needed so grid * chunk_limit covers
-// every row.
+// every row. An expansion launch gives each leaf of m rows ceil(m / chunk)
+// blocks with chunk = clamp(ceil(m / 256), chunk_min, chunk_limit); the
+// leaves of a batch are disjoint, so n / chunk_min + (batch size) blocks
+// always suffice.
 constexpr int64_t kHistChunkMin = 8192;
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
@@ -186,7 +208,12 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
     s.part_stride = (ds->nb + 1) & ~1;
     s.hist_chunk_min = std::min<int64_t>(kHistChunkMin, limit);
     s.hist_chunk_limit = limit;
-    s.part = dalloc<unsigned long long>((size_t)grid * ds->F * s.part_stride, run.owned);
+    s.kmax = kMaxBatch;
+    s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + kMaxBatch);
+    s.scan_grid = std::min(kMaxBatch * ds->F, 4 * ds->n_cu);
+    const int64_t parts = std::max<int64_t>(grid, s.pb_grid);
+    s.part = dalloc<unsigned long long>((size_t)parts * ds->F * s.part_stride, run.owned);
+    s.pb_desc = dalloc<mb::PbDesc>(s.pb_grid, run.owned);
 }
 
 double base_score_for(const mbh_dataset *ds, int objective) {
@@ -233,13 +260,21 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.round = dalloc<mb::Round>(1, run.owned);
     s.rows0 = dalloc<int32_t>(ds->n, run.owned);
     s.rows1 = dalloc<int32_t>(ds->n, run.owned);
-    s.hist = dalloc<int32_t>((size_t)L * F * ds->nb * 3, run.owned);
+    const int max_exp = 2 * L - 1;
+    s.max_exp = max_exp;
+    s.e_cap = 1 + 2 * max_exp;
+    s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
     configure_hist(s, ds, p->num_grad_quant_bins, run);
-    s.step = dalloc<mb::Step>(1, run.owned);
-    s.slots = dalloc<mb::Slot>(L, run.owned);
-    s.scan = dalloc<mb::ScanResult>(2 * (size_t)F, run.owned);
-    s.ticket = dalloc<uint32_t>(1, run.owned);
-    s.cursor = dalloc<int64_t>(2, run.owned);
+    s.enodes = dalloc<mb::ENode>(s.e_cap, run.owned);
+    s.items = dalloc<mb::Item>(s.kmax, run.owned);
+    s.batch = dalloc<mb::Batch>(1, run.owned);
+    s.grow = dalloc<mb::Grow>(1, run.owned);
+    s.slot_e = dalloc<int32_t>(L, run.owned);
+    s.slot_fid = dalloc<int32_t>(L, run.owned);
+    s.scan = dalloc<mb::ScanResult>((size_t)s.kmax * 2 * F, run.owned);
+    s.e_gain = dalloc<double>(s.e_cap, run.owned);
+    s.e_left = dalloc<int32_t>(s.e_cap, run.owned);
+    s.cursor = dalloc<int64_t>(2 + 2 * (size_t)s.kmax, run.owned);
     s.error = dalloc<int32_t>(1, run.owned);
     s.t_feature = dalloc<int32_t>(max_nodes, run.owned);
     s.t_threshold = dalloc<int32_t>(max_nodes, run.owned);
@@ -253,7 +288,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.t_meta = dalloc<int32_t>(2, run.owned);
     s.arc_int = dalloc<int32_t>((size_t)T * (6 * max_nodes + 2), run.owned);
     s.arc_dbl = dalloc<double>((size_t)T * 3 * max_nodes, run.owned);
-    s.arc_rows = dalloc<int64_t>((size_t)T * L, run.owned);
+    s.arc_aux = dalloc<int64_t>((size_t)T * 4, run.owned);
     s.max_nodes = max_nodes;
     uint8_t *fmask = dalloc<uint8_t>((size_t)T * F, run.owned);
     s.feature_mask = fmask;
@@ -277,15 +312,19 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.lambda_l2 = p->lambda_l2;
     hp.min_sum_hessian = p->min_sum_hessian;
 
+    if (mb::plan_lds_bytes(s) > 160 * 1024)
+        throw Error{MOJOTREES_ERROR_UNSUPPORTED,
+                    "num_leaves * n_features too large for the planner's LDS (160 KiB)"};
     HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
-    HIPX(hipMemset(s.step, 0, sizeof(mb::Step)));
-    HIPX(hipMemset(s.ticket, 0, sizeof(uint32_t)));
-    HIPX(hipMemset(s.cursor, 0, 2 * sizeof(int64_t)));
+    HIPX(hipMemset(s.batch, 0, sizeof(mb::Batch)));
+    HIPX(hipMemset(s.grow, 0, sizeof(mb::Grow)));
+    HIPX(hipMemset(s.pb_desc, 0, (size_t)s.pb_grid * sizeof(mb::PbDesc)));
+    HIPX(hipMemset(s.cursor, 0, (2 + 2 * (size_t)s.kmax) * sizeof(int64_t)));
     HIPX(hipMemset(s.error, 0, sizeof(int32_t)));
     HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));
-    HIPX(hipMemset(s.arc_rows, 0, (size_t)T * L * sizeof(int64_t)));
+    HIPX(hipMemset(s.arc_aux, 0, (size_t)T * 4 * sizeof(int64_t)));
     HIPX(hipMemset(s.arc_int, 0, (size_t)T * (6 * max_nodes + 2) * sizeof(int32_t)));
     mb::Round r0{};
     HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
@@ -352,9 +391,10 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
                         "more than 126 features needs the feature-tiled histogram, not built yet"};
         ds->rec = rec;
         ds->lds_stride = nb | 1;
-        if ((size_t)F * ds->lds_stride * 8 > 160 * 1024)
+        if ((size_t)F * ds->lds_stride * 8 + kPbListBytes > 160 * 1024)
             throw Error{MOJOTREES_ERROR_UNSUPPORTED,
-                        "n_features * n_bins exceeds one workgroup's LDS (160 KiB of packed counters)"};
+                        "n_features * n_bins exceeds one workgroup's LDS (160 KiB: packed counters "
+                        "plus the partition's row list)"};
         // validate bins and derive the realized widths (binning.histogram_widths)
         ds->missing.assign(F, -1);
         if (missing_bin)
@@ -429,82 +469,127 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         HIPX(hipMemcpy(d_base, fit->base.data(), K * sizeof(double), hipMemcpyHostToDevice));
         const int grid_rows = 8 * ds->n_cu;
         HIPX(mb::launch_fill_f64(s.raw, ds->n, K, d_base, grid_rows, nullptr));
-        HIPX(mb::prepare_hist(s));
+        HIPX(mb::prepare_kernels(s));
         HIPX(hipDeviceSynchronize());
-        const int grid_part = 2 * ds->n_cu;
         const int L = tb.L;
         const int T = p->num_iterations * K;
         const bool timed = p->time_histograms != 0;
         hipStream_t st = nullptr;
-        // per build: before the histogram, after it, after the split kernel
-        // (which merges the partials)
-        if (timed) events.resize((size_t)3 * L);
-        for (auto &e : events) HIPX(hipEventCreate(&e));
-        double hist_ms = 0.0, root_ms = 0.0, merged_ms = 0.0, root_merged_ms = 0.0;
+        PinnedFlags done_flags;
+        HIPX(hipHostMalloc((void **)&done_flags.p, 2 * sizeof(int32_t), hipHostMallocDefault));
+        // events: [0..1] done-flag markers of the two in-flight groups; when
+        // timed, [2..4] the root build and per group slot kIterChunk x 3
+        // (before the expansion, after it, after the scan)
+        const int n_ev = 2 + (timed ? 3 + 2 * kIterChunk * 3 : 0);
+        events.resize(n_ev);
+        for (int i = 0; i < n_ev; ++i)
+            HIPX(hipEventCreateWithFlags(&events[i], i < 2 ? hipEventDisableTiming : hipEventDefault));
+        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kIterChunk + c) * 3 + k]; };
+        double t_acc = 0.0, t_root = 0.0, t_root_scan = 0.0, t_pb = 0.0, t_scan = 0.0;
+        double pb_launches = 0.0;
+        auto add_group = [&](int slot) {
+            for (int c = 0; c < kIterChunk; ++c) {
+                float a = 0.f, b = 0.f;
+                HIPX(hipEventElapsedTime(&a, ev_group(slot, c, 0), ev_group(slot, c, 1)));
+                HIPX(hipEventElapsedTime(&b, ev_group(slot, c, 1), ev_group(slot, c, 2)));
+                t_pb += a;
+                t_scan += b;
+            }
+        };
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
             HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
-            if (timed) HIPX(hipEventRecord(events[0], st));
-            HIPX(mb::launch_hist(s, 1, st));
-            if (timed) HIPX(hipEventRecord(events[1], st));
-            HIPX(mb::launch_split(s, 1, st));
             if (timed) HIPX(hipEventRecord(events[2], st));
-            for (int k = 1; k < L; ++k) {
-                HIPX(mb::launch_partition(s, grid_part, st));
-                if (timed) HIPX(hipEventRecord(events[3 * k], st));
-                HIPX(mb::launch_hist(s, 0, st));
-                if (timed) HIPX(hipEventRecord(events[3 * k + 1], st));
-                HIPX(mb::launch_split(s, 0, st));
-                if (timed) HIPX(hipEventRecord(events[3 * k + 2], st));
+            HIPX(mb::launch_hist(s, st));
+            if (timed) HIPX(hipEventRecord(events[3], st));
+            HIPX(mb::launch_scan(s, 1, st));
+            HIPX(mb::launch_plan(s, 1, st));
+            if (timed) HIPX(hipEventRecord(events[4], st));
+            int iters = 0;
+            for (int k = 0;; ++k) {
+                const int slot = k & 1;
+                for (int c = 0; c < kIterChunk; ++c) {
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 0), st));
+                    HIPX(mb::launch_part_hist(s, st));
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 1), st));
+                    HIPX(mb::launch_scan(s, 0, st));
+                    HIPX(mb::launch_plan(s, 0, st));
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 2), st));
+                }
+                pb_launches += kIterChunk;
+                iters += kIterChunk;
+                HIPX(hipMemcpyAsync(&done_flags.p[slot], &s.batch->done, sizeof(int32_t),
+                                    hipMemcpyDeviceToHost, st));
+                HIPX(hipEventRecord(events[slot], st));
+                if (k == 0) continue;
+                HIPX(hipEventSynchronize(events[1 - slot]));
+                if (timed) add_group(1 - slot);
+                if (done_flags.p[1 - slot]) {
+                    if (timed) {
+                        HIPX(hipEventSynchronize(events[slot]));
+                        add_group(slot);
+                    }
+                    break;
+                }
+                // every iteration commits at least one split once the first
+                // batch is planned, so a tree ends within num_leaves + 1
+                if (iters > L + 2 * kIterChunk + 2)
+                    throw Error{MOJOTREES_ERROR_TRAINING, "tree growth did not finish (internal error)"};
+            }
+            if (timed) {
+                float a = 0.f, b = 0.f;
+                HIPX(hipEventElapsedTime(&a, events[2], events[3]));
+                HIPX(hipEventElapsedTime(&b, events[3], events[4]));
+                t_root += a;
+                t_root_scan += b;
             }
             HIPX(mb::launch_score(s, grid_rows, st));
             HIPX(mb::launch_round_end(s, st));
-            if (timed) {
-                HIPX(hipStreamSynchronize(st));
-                for (int k = 0; k < L; ++k) {
-                    float ms = 0.f, ms2 = 0.f;
-                    HIPX(hipEventElapsedTime(&ms, events[3 * k], events[3 * k + 1]));
-                    HIPX(hipEventElapsedTime(&ms2, events[3 * k], events[3 * k + 2]));
-                    hist_ms += ms;
-                    merged_ms += ms2;
-                    if (k == 0) {
-                        root_ms += ms;
-                        root_merged_ms += ms2;
-                    }
-                }
-            }
         }
         HIPX(hipStreamSynchronize(st));
         auto t1 = std::chrono::steady_clock::now();
+        t_acc = t_root + t_pb;
         int32_t h_error = 0;
         HIPX(hipMemcpy(&h_error, s.error, sizeof(int32_t), hipMemcpyDeviceToHost));
-        if (h_error) throw Error{MOJOTREES_ERROR_TRAINING, "device partition overflowed its range (internal error)"};
+        if (h_error)
+            throw Error{MOJOTREES_ERROR_TRAINING,
+                        std::string("device growth check failed (internal error, code ") +
+                            std::to_string(h_error) + ")"};
         const int mn = tb.max_nodes;
         std::vector<int32_t> ai((size_t)tb.T * (6 * mn + 2));
         std::vector<double> ad((size_t)tb.T * 3 * mn);
-        std::vector<int64_t> ar((size_t)tb.T * L);
+        std::vector<int64_t> ax((size_t)tb.T * 4);
         HIPX(hipMemcpy(ai.data(), s.arc_int, ai.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(ad.data(), s.arc_dbl, ad.size() * sizeof(double), hipMemcpyDeviceToHost));
-        HIPX(hipMemcpy(ar.data(), s.arc_rows, ar.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(ax.data(), s.arc_aux, ax.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
         fit->train_raw.resize((size_t)ds->n * K);
         HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
                        hipMemcpyDeviceToHost));
         const bool bagging = s.hp.bagging != 0;
-        double bytes = 0.0, rowsfeat = 0.0, builds = 0.0, root_bytes = 0.0;
+        const double rb = ds->F + 2;
+        double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
+        double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
         int grown = 0;
         for (int t = 0; t < T; ++t) {
             const int32_t *ti = ai.data() + (size_t)t * (6 * mn + 2);
             const double *td = ad.data() + (size_t)t * 3 * mn;
             const int nn = ti[6 * mn], nl = ti[6 * mn + 1];
-            for (int k = 0; k < L; ++k) {
-                const int64_t rows = ar[(size_t)t * L + k];
-                if (k > 0 && k >= nl) break;
-                bytes += (double)rows * (ds->F + 2);
-                rowsfeat += (double)rows * ds->F;
+            // builds of the committed tree: the root, then the smaller child
+            // of every split
+            root_rows += td[2];
+            useful_rows += td[2];
+            builds += 1;
+            for (int i = 0; i < nn; ++i) {
+                if (ti[6 * i] < 0) continue;
+                const double cl = td[3 * ti[6 * i + 2] + 2], cr = td[3 * ti[6 * i + 3] + 2];
+                useful_rows += std::min(cl, cr);
                 builds += 1;
-                if (k == 0) root_bytes += (double)rows * (ds->F + 2);
             }
+            rows_built += (double)ax[(size_t)t * 4 + 0];
+            iters_total += (double)ax[(size_t)t * 4 + 1];
+            exps += (double)ax[(size_t)t * 4 + 2];
+            rows_parted += (double)ax[(size_t)t * 4 + 3];
             // boosting._boost_rounds stopping rule (boosting.mojo:2898-2907)
             if (nl == 1 && std::fabs(td[0]) < 1e-12) {
                 if (bagging) continue;
@@ -524,16 +609,24 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             fit->offsets.push_back((int64_t)fit->feature.size());
             ++grown;
         }
-        fit->stats[0] = std::chrono::duration<double>(t1 - t0).count();
-        fit->stats[1] = hist_ms;
-        fit->stats[2] = bytes;
-        fit->stats[3] = rowsfeat;
-        fit->stats[4] = builds;
-        fit->stats[5] = root_bytes;
-        fit->stats[6] = root_ms;
-        fit->stats[7] = grown;
-        fit->stats[8] = merged_ms;
-        fit->stats[9] = root_merged_ms;
+        double *o = fit->stats;
+        o[0] = std::chrono::duration<double>(t1 - t0).count();
+        o[1] = t_acc;
+        o[2] = useful_rows * rb;
+        o[3] = useful_rows * ds->F;
+        o[4] = builds;
+        o[5] = root_rows * rb;
+        o[6] = t_root;
+        o[7] = grown;
+        o[8] = t_root + t_root_scan + t_pb + t_scan;
+        o[9] = t_root + t_root_scan;
+        o[10] = iters_total;
+        o[11] = exps;
+        o[12] = rows_built;
+        o[13] = rows_parted;
+        o[14] = pb_launches;
+        o[15] = t_pb;
+        o[16] = rows_parted * 9.0 + rows_built * rb;
         for (auto &e : events) (void)hipEventDestroy(e);
         events.clear();
     } catch (const Error &e) {
@@ -574,8 +667,10 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err, int32_t er
     std::memcpy(out, fit->train_raw.data(), fit->train_raw.size() * sizeof(double));
     return MOJOTREES_OK;
 }
-void mbh_fit_stats(const mbh_fit *fit, double *out) {
-    for (int i = 0; i < 10; ++i) out[i] = fit->stats[i];
+int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out) {
+    if (fit && out)
+        for (int i = 0; i < kNumStats && i < n_out; ++i) out[i] = fit->stats[i];
+    return kNumStats;
 }
 
 int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out_sig, char *err,
@@ -691,9 +786,9 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
             int64_t c[2] = {n_sel, 0};
             HIPX(hipMemcpy(s.cursor, c, sizeof(c), hipMemcpyHostToDevice));
         }
-        HIPX(mb::prepare_hist(s));
-        HIPX(mb::launch_hist(s, 1, nullptr));
-        HIPX(mb::launch_split(s, 1, nullptr));
+        HIPX(mb::prepare_kernels(s));
+        HIPX(mb::launch_hist(s, nullptr));
+        HIPX(mb::launch_scan(s, 1, nullptr));
         HIPX(hipDeviceSynchronize());
         HIPX(hipMemcpy(out, s.hist, cells * sizeof(int32_t), hipMemcpyDeviceToHost));
     } catch (const Error &e) {
@@ -726,13 +821,14 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         r0.grad_units = 1.0;
         r0.hess_units = 1.0;
         HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
-        HIPX(mb::prepare_hist(s));
+        HIPX(mb::prepare_kernels(s));
         for (auto &e : ev) HIPX(hipEventCreate(&e));
         for (int i = 0; i < reps; ++i) {
             HIPX(hipEventRecord(ev[3 * i], nullptr));
-            HIPX(mb::launch_hist(s, 1, nullptr));
+            HIPX(mb::launch_hist(s, nullptr));
             HIPX(hipEventRecord(ev[3 * i + 1], nullptr));
-            HIPX(mb::launch_split(s, 1, nullptr));
+            HIPX(mb::launch_scan(s, 1, nullptr));
+            HIPX(mb::launch_plan(s, 1, nullptr));
             HIPX(hipEventRecord(ev[3 * i + 2], nullptr));
         }
         HIPX(hipDeviceSynchronize());

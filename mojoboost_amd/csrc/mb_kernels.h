@@ -9,12 +9,16 @@ namespace mb {
 
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
-hipError_t prepare_hist(const DevState &s);
+// Raises the dynamic LDS limits of the kernels that need more than 64 KB.
+hipError_t prepare_kernels(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
-hipError_t launch_hist(const DevState &s, int root_mode, hipStream_t st);
-hipError_t launch_partition(const DevState &s, int grid, hipStream_t st);
-hipError_t launch_split(const DevState &s, int root_mode, hipStream_t st);
+size_t pb_lds_bytes(const DevState &s);
+size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
+hipError_t launch_hist(const DevState &s, hipStream_t st);
+hipError_t launch_part_hist(const DevState &s, hipStream_t st);
+hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
+hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_round_end(const DevState &s, hipStream_t st);
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,

@@ -4,16 +4,18 @@
 //   k_objective   fused gradient/hessian of the round + max |g|, |h| of the
 //                 sampled rows (one pass over raw scores and labels)
 //   k_quantize    max-abs lattice + stochastic rounding to int8 g/h, written
-//                 into each row's record; root row list and root histogram
-//                 reset
-//   k_hist        per-leaf histogram: LDS-privatized packed 64-bit counters
-//                 (grad | hess | count in one ds_add_u64), merged into the
-//                 global int32 histogram with integer atomics
-//   k_partition   row partition of the chosen leaf's range: wave ballot +
-//                 popcount ranks, one atomic cursor reservation per block
-//   k_split       sibling subtraction + per-feature integer prefix scan with
-//                 fp64 gains + argmax; the last block folds features, writes
-//                 the tree nodes and frontier slots, and picks the next leaf
+//                 into each row's record; root row list
+//   k_hist        root histogram: LDS-privatized packed 64-bit counters
+//                 (grad | hess | count in one ds_add_u64) per block, stored
+//                 as block partials
+//   k_part_hist   expansion of a batch of leaves: row partition (wave ballot
+//                 ranks, one atomic reservation per tile and side) fused with
+//                 the smaller child's histogram accumulation
+//   k_scan        partial merge + sibling subtraction + per-feature integer
+//                 prefix scan with fp64 gains + argmax, per (leaf, feature)
+//   k_plan        one block: folds features into each new leaf's best split,
+//                 replays the best-first order, commits the reference's
+//                 splits and selects the next batch
 //   k_score       raw += lr * tree(row) by tree walk, fused multiply-add
 //   k_round_end   archives the finished tree and advances the round state
 //
@@ -208,8 +210,8 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
 }
 
 // --------------------------------------------------------------- histogram
-// Rows of a node with m rows handled by each histogram block. The split
-// kernel recomputes it to know how many block partials a build left.
+// Rows of the root build handled by each block. The scan kernel recomputes it
+// to know how many block partials the build left.
 __device__ __forceinline__ int64_t hist_chunk(const DevState &s, int64_t m) {
     const int64_t g = s.hist_grid;
     int64_t chunk = (m + g - 1) / g;
@@ -218,50 +220,66 @@ __device__ __forceinline__ int64_t hist_chunk(const DevState &s, int64_t m) {
     return chunk;
 }
 
-// One leaf's histogram, accumulation pass. Rows are split into contiguous
-// chunks, one per block; a block accumulates its rows into LDS-private
-// packed counters and stores them, all cells, as its partial. The split
-// kernel merges the partials. A row's record is LPR x 16 bytes: each of the
-// LPR lanes of a row group loads 16 bytes (16 features) and the int8 g/h pair
-// (the record's last two bytes) reaches the group by a lane shuffle. Each
-// lane keeps kHistUnroll row loads in flight.
-//
+__device__ __forceinline__ int64_t root_rows(const DevState &s) {
+    return s.hp.bagging ? load_agent(&s.cursor[0]) : s.n;
+}
+
 // Packed counter (64 bits): count in bits [0,20), hess sum in [20,42), grad
 // sum (signed) in [42,64). Adding packed values adds the three fields while
 // no field overflows, which hist_chunk_limit guarantees for the lattice in
-// use (host-checked).
+// use (host-checked): a block never packs more rows than that.
+__device__ __forceinline__ unsigned long long pack_gh(uint32_t gh_word) {
+    const int g = (int)(int8_t)(gh_word >> 16);
+    const int h = (int)(int8_t)(gh_word >> 24);
+    return (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
+}
+
+// Accumulates one record (this lane's 16-byte slice, features sub*16 ..) into
+// the block's LDS histogram.
+__device__ __forceinline__ void lds_accumulate(unsigned long long *lds, const uint4 &w, int sub, int F,
+                                               int ls, unsigned long long packed) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = sub * 16 + q * 4 + j;
+            if (f < F) atomicAdd(&lds[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
+        }
+}
+
+// Stores the block's LDS histogram, every cell, as its partial.
+__device__ __forceinline__ void store_partial(const DevState &s, const unsigned long long *lds, int blk) {
+    const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
+    unsigned long long *out = s.part + (size_t)blk * F * ps;
+    for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
+        const int f = c / ps;
+        const int b = c - f * ps;
+        out[c] = b < nb ? lds[f * ls + b] : 0ULL;
+    }
+}
+
+// Root histogram, accumulation pass. Rows are split into contiguous chunks,
+// one per block; a block accumulates its rows into LDS-private packed
+// counters and stores them as its partial; the scan kernel merges the
+// partials. A row's record is LPR x 16 bytes: each of the LPR lanes of a row
+// group loads 16 bytes (16 features) and the int8 g/h pair (the record's last
+// two bytes) reaches the group by a lane shuffle. Each lane keeps
+// kHistUnroll row loads in flight.
 constexpr int kHistUnroll = 4;
 
 template <int LPR>
-__global__ __launch_bounds__(1024) void k_hist(DevState s, int root_mode) {
+__global__ __launch_bounds__(1024) void k_hist(DevState s) {
     extern __shared__ unsigned long long lds[];
-    int64_t m;
-    const int32_t *rows;
-    bool direct;
-    if (root_mode) {
-        m = s.hp.bagging ? s.cursor[0] : s.n;
-        rows = s.rows0;
-        direct = !s.hp.bagging;
-    } else {
-        const Step st = *s.step;
-        if (!st.active) return;
-        int64_t beg;
-        if (st.builds_left) {
-            beg = st.begin;
-            m = st.n_left;
-        } else {
-            beg = st.begin + st.n_left;
-            m = st.end - beg;
-        }
-        rows = (st.src_buf ? s.rows0 : s.rows1) + beg;
-        direct = false;
-    }
+    const int64_t m = root_rows(s);
+    const int32_t *rows = s.rows0;
+    const bool direct = !s.hp.bagging;
     if (m <= 0) return;
     const int64_t chunk = hist_chunk(s, m);
     const int64_t c0 = (int64_t)blockIdx.x * chunk;
     if (c0 >= m) return;
     const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
-    const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride;
+    const int F = s.n_features, ls = s.lds_stride;
     for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
     __syncthreads();
     const int lane = lane_id();
@@ -287,559 +305,904 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s, int root_mode) {
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (!ok[u]) continue;
-            const int g = (int)(int8_t)(gh >> 16);
-            const int h = (int)(int8_t)(gh >> 24);
-            const unsigned long long packed =
-                (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
-            const uint32_t d[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int f = sub * 16 + q * 4 + j;
-                    if (f < F) atomicAdd(&lds[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
-                }
+            if (ok[u]) lds_accumulate(lds, w[u], sub, F, ls, pack_gh(gh));
         }
     }
     __syncthreads();
-    const int ps = s.part_stride;
-    unsigned long long *out = s.part + (size_t)blockIdx.x * F * ps;
-    for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
-        const int f = c / ps;
-        const int b = c - f * ps;
-        out[c] = b < nb ? lds[f * ls + b] : 0ULL;
-    }
+    store_partial(s, lds, blockIdx.x);
 }
 
-// --------------------------------------------------------------- partition
-// Routes the parent's rows (tree.partition_rows_into semantics: the missing
-// bin follows default_left, otherwise bin <= threshold goes left) into the
-// other row buffer: left rows fill [begin, begin + n_left), right rows the
-// rest. Each block counts its chunk, reserves its output with one atomic per
-// side, and scatters tile by tile with ballot ranks; each thread keeps
-// kPartUnroll rows in flight. The order inside a child is not the
-// reference's (blocks land in reservation order); every consumer is
-// order-free because histograms are integer sums.
-constexpr int kPartUnroll = 8;
-
-__global__ __launch_bounds__(256) void k_partition(DevState s) {
-    __shared__ int wave_l[kPartUnroll][4], wave_r[kPartUnroll][4];
-    __shared__ int red[4];
-    __shared__ long long base_l, base_r;
-    const Step st = *s.step;
-    if (!st.active) return;
-    const int64_t m = st.end - st.begin;
-    int64_t chunk = (m + gridDim.x - 1) / gridDim.x;
-    if (chunk < 2048) chunk = 2048;
-    chunk = (chunk + 255) / 256 * 256;
-    const int64_t c0 = (int64_t)blockIdx.x * chunk;
-    if (c0 >= m) return;
-    const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
-    const int32_t *src = (st.src_buf ? s.rows1 : s.rows0) + st.begin;
-    int32_t *dst = (st.src_buf ? s.rows0 : s.rows1) + st.begin;
-    const uint8_t *col = s.bins_cm + (size_t)st.feature * s.n;
-    const int mb = st.missing_bin, thr = st.bin, dl = st.default_left;
-    const int lane = lane_id(), w = threadIdx.x >> 6;
-    const int64_t tile = (int64_t)blockDim.x * kPartUnroll;
-    // pass 1: count rows going left
-    int my_l = 0;
-    for (int64_t t0 = c0; t0 < c1; t0 += tile) {
-        int32_t r[kPartUnroll];
-#pragma unroll
-        for (int u = 0; u < kPartUnroll; ++u) {
-            const int64_t i = t0 + (int64_t)u * blockDim.x + threadIdx.x;
-            r[u] = i < c1 ? src[i] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < kPartUnroll; ++u) {
-            if (r[u] < 0) continue;
-            const int32_t row = (uint64_t)r[u] < (uint64_t)s.n ? r[u] : 0;
-            const int b = col[row];
-            my_l += (b == mb) ? dl : (b <= thr);
-        }
-    }
-    const long long tl = wave_sum_ll(my_l);
-    if (lane == 0) red[w] = (int)tl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        long long nl = 0;
-        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) nl += red[i];
-        const long long nr = (c1 - c0) - nl;
-        base_l = nl ? (long long)atomicAdd((unsigned long long *)&s.cursor[0], (unsigned long long)nl) : 0;
-        base_r = nr ? (long long)atomicAdd((unsigned long long *)&s.cursor[1], (unsigned long long)nr) : 0;
-    }
-    __syncthreads();
-    long long run_l = base_l, run_r = base_r;
-    const int64_t n_left = st.n_left;
-    const unsigned long long below = (1ULL << lane) - 1ULL;
-    // pass 2: scatter; a tile is kPartUnroll sub-tiles of blockDim rows
-    for (int64_t t0 = c0; t0 < c1; t0 += tile) {
-        int32_t r[kPartUnroll];
-        bool left[kPartUnroll], right[kPartUnroll];
-        unsigned long long lm[kPartUnroll], rm[kPartUnroll];
-#pragma unroll
-        for (int u = 0; u < kPartUnroll; ++u) {
-            const int64_t i = t0 + (int64_t)u * blockDim.x + threadIdx.x;
-            r[u] = i < c1 ? src[i] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < kPartUnroll; ++u) {
-            left[u] = right[u] = false;
-            if (r[u] >= 0) {
-                const int32_t row = (uint64_t)r[u] < (uint64_t)s.n ? r[u] : 0;
-                const int b = col[row];
-                left[u] = (b == mb) ? (dl != 0) : (b <= thr);
-                right[u] = !left[u];
-            }
-            lm[u] = __ballot(left[u]);
-            rm[u] = __ballot(right[u]);
-            if (lane == 0) {
-                wave_l[u][w] = __popcll(lm[u]);
-                wave_r[u][w] = __popcll(rm[u]);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < kPartUnroll; ++u) {
-            long long off_l = 0, off_r = 0, tot_l = 0, tot_r = 0;
-            for (int k = 0; k < (int)(blockDim.x >> 6); ++k) {
-                if (k < w) {
-                    off_l += wave_l[u][k];
-                    off_r += wave_r[u][k];
-                }
-                tot_l += wave_l[u][k];
-                tot_r += wave_r[u][k];
-            }
-            if (left[u]) {
-                const long long p = run_l + off_l + __popcll(lm[u] & below);
-                if (p < n_left) dst[p] = r[u];
-                else atomicOr(s.error, 1);
-            } else if (right[u]) {
-                const long long p = n_left + run_r + off_r + __popcll(rm[u] & below);
-                if (p < m) dst[p] = r[u];
-                else atomicOr(s.error, 1);
-            }
-            run_l += tot_l;
-            run_r += tot_r;
-        }
-        __syncthreads();
-    }
-}
-
-// ------------------------------------------------------------------- split
-// One block (8 waves) per feature. First the built child's histogram is
-// merged from the block partials of its build and stored; the sibling is
-// parent - built, written back over the parent's buffer. Then waves 0-3 scan
-// the built child and waves 4-7 the sibling, one bin per thread. The scan
-// follows split.find_best_split (src/mojotrees/split.mojo:601-1360) with the
-// sums kept as integers and each candidate scored by quantized_split_gain
-// (quantized_gradient.mojo:3283-3310): ascending bins, missing-left scored
-// before missing-right, strict '>' keeps the first maximum; the hessian guard
-// compares against hessian_units_at_least (:3336).
+// ------------------------------------------------- partition + histogram
+// One launch expands every leaf of the batch: each block takes a chunk of
+// one leaf's rows (its descriptor, written by the planner), routes them to
+// the children (tree.partition_rows_into semantics: the missing bin follows
+// default_left, otherwise bin <= threshold goes left) in the other row
+// buffer -- left rows fill [begin, begin + n_left), right rows the rest --
+// and accumulates the rows of the smaller child into its LDS histogram,
+// stored as the block's partial.
 //
-// The last block to finish folds the features of each child (strict '>',
-// lowest feature on ties), computes the children's leaf values
-// (quantized_leaf_output), records the nodes, replaces the parent's frontier
-// slot with the left child and appends the right one, then picks the next
-// leaf (max gain, lowest slot on ties; growth_policy.mojo:659-677) and writes
-// the next step with the left count read from that leaf's histogram.
-constexpr int kSplitThreads = 512;
-constexpr int kMaxScan = 256;  // 2 x max features
+// A tile is kPbUnroll x 1024 rows. Per tile: row ids and the split feature's
+// bins are loaded, wave ballots rank the rows, wave 0 scans the per-wave
+// counts and reserves the tile's output with one atomic per side, rows are
+// scattered, and the smaller child's rows are listed in LDS; then the
+// accumulation pass reads their records (LPR lanes per row). The order of
+// rows inside a child is not the reference's (tiles land in reservation
+// order); every consumer is order-free because histograms are integer sums.
+constexpr int kPbThreads = 1024;
+constexpr int kPbUnroll = 4;
+constexpr int kPbTile = kPbThreads * kPbUnroll;
 
-__global__ __launch_bounds__(kSplitThreads) void k_split(DevState s, int root_mode) {
-    __shared__ long long cgs[2][256], chs[2][256], ccs[2][256];
-    __shared__ long long wtot[8][3];
+size_t pb_lds_bytes_of(int F, int ls) { return (size_t)F * ls * 8 + (size_t)kPbTile * 4; }
+
+template <int LPR>
+__global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
+    extern __shared__ unsigned long long lds[];
+    __shared__ int cnt_l[kPbUnroll * 16], cnt_r[kPbUnroll * 16];
+    __shared__ long long off_l[kPbUnroll * 16], off_r[kPbUnroll * 16], off_b[kPbUnroll * 16];
+    __shared__ int s_nbuilt;
+    const int n_blocks = s.batch->n_blocks;
+    const PbDesc d = s.pb_desc[blockIdx.x];  // in bounds: the grid is pb_grid
+    if ((int)blockIdx.x >= n_blocks) return;
+    const int F = s.n_features, ls = s.lds_stride;
+    int32_t *list = (int32_t *)(lds + (size_t)F * ls);
+    for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
+    const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
+    int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
+    const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
+    const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
+    const bool bl = d.builds_left != 0;
+    unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item];
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    const int sub = threadIdx.x % LPR;
+    const int rr = threadIdx.x / LPR;
+    const int rpp = kPbThreads / LPR;
+    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
+    const uint4 *rec = (const uint4 *)s.records;
+    for (int64_t t0 = d.c0; t0 < d.c1; t0 += kPbTile) {
+        int32_t r[kPbUnroll];
+        bool left[kPbUnroll], valid[kPbUnroll];
+        unsigned long long lm[kPbUnroll], rm[kPbUnroll];
+#pragma unroll
+        for (int u = 0; u < kPbUnroll; ++u) {
+            const int64_t i = t0 + (int64_t)u * kPbThreads + threadIdx.x;
+            valid[u] = i < d.c1;
+            r[u] = valid[u] ? src[i] : 0;
+            if ((uint32_t)r[u] >= (uint64_t)s.n) r[u] = 0;  // never taken: ids come from the row lists
+        }
+#pragma unroll
+        for (int u = 0; u < kPbUnroll; ++u) {
+            const int b = valid[u] ? (int)col[r[u]] : 0;
+            left[u] = (b == mb) ? (dl != 0) : (b <= thr);
+            lm[u] = __ballot(valid[u] && left[u]);
+            rm[u] = __ballot(valid[u] && !left[u]);
+            if (lane == 0) {
+                cnt_l[u * 16 + w] = __popcll(lm[u]);
+                cnt_r[u * 16 + w] = __popcll(rm[u]);
+            }
+        }
+        __syncthreads();
+        if (w == 0) {
+            // entry k = u * 16 + wave, in tile order
+            const long long vl = cnt_l[lane], vr = cnt_r[lane];
+            const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
+            const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
+            long long bl_base = 0, br_base = 0;
+            if (lane == 0) {
+                bl_base = tl ? (long long)atomicAdd(&cur[0], (unsigned long long)tl) : 0;
+                br_base = tr ? (long long)atomicAdd(&cur[1], (unsigned long long)tr) : 0;
+            }
+            bl_base = __shfl(bl_base, 0, 64);
+            br_base = __shfl(br_base, 0, 64);
+            off_l[lane] = bl_base + il - vl;
+            off_r[lane] = br_base + ir - vr;
+            off_b[lane] = bl ? il - vl : ir - vr;
+            if (lane == 0) s_nbuilt = (int)(bl ? tl : tr);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kPbUnroll; ++u) {
+            if (!valid[u]) continue;
+            const int k = u * 16 + w;
+            long long rank;
+            if (left[u]) {
+                rank = __popcll(lm[u] & below);
+                const long long p = off_l[k] + rank;
+                if (p < d.n_left) dst[p] = r[u];
+                else atomicOr(s.error, 1);
+            } else {
+                rank = __popcll(rm[u] & below);
+                const long long p = d.n_left + off_r[k] + rank;
+                if (p < d.m) dst[p] = r[u];
+                else atomicOr(s.error, 1);
+            }
+            if (left[u] == bl) list[off_b[k] + rank] = r[u];
+        }
+        __syncthreads();
+        const int nbt = s_nbuilt;
+        for (int k0 = 0; k0 < nbt; k0 += kHistUnroll * rpp) {
+            uint4 v[kHistUnroll];
+            bool ok[kHistUnroll];
+#pragma unroll
+            for (int u = 0; u < kHistUnroll; ++u) {
+                const int k = k0 + u * rpp + rr;
+                ok[u] = k < nbt;
+                v[u] = ok[u] ? rec[(int64_t)list[k] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < kHistUnroll; ++u) {
+                const uint32_t gh = __shfl(v[u].w, src_lane, 64);
+                if (ok[u]) lds_accumulate(lds, v[u], sub, F, ls, pack_gh(gh));
+            }
+        }
+        __syncthreads();
+    }
+    __syncthreads();
+    store_partial(s, lds, blockIdx.x);
+}
+
+// ------------------------------------------------------------------- scan
+// Tasks (item, feature), grid-strided, 512 threads each. The accumulated
+// child's histogram is merged from its block partials (two threads per bin)
+// and stored; the sibling is parent - accumulated, written over the parent's
+// buffer. Threads 0-255 then scan the accumulated child and 256-511 the
+// sibling, one bin per thread, with int32 sums (node totals stay below
+// 2^31: n_rows * (num_grad_quant_bins + 1) < 2^31 is checked on the host).
+// The scan follows split.find_best_split (src/mojotrees/split.mojo:601-1360)
+// with each candidate scored by quantized_split_gain
+// (quantized_gradient.mojo:3283-3310): ascending bins, missing-left scored
+// before missing-right, strict '>' keeps the first maximum; the hessian
+// guard compares against hessian_units_at_least (:3336). Each task writes one
+// ScanResult per child; the planner folds them.
+constexpr int kScanThreads = 512;
+
+__device__ __forceinline__ int wave_incl_scan_i(int v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(v, d, 64);
+        if (lane >= d) v += t;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode) {
+    __shared__ int cg[2][256], ch[2][256], cc[2][256];
+    __shared__ int acc[3][256];
+    __shared__ int wtot[8][3];
     __shared__ double wgain[8];
-    __shared__ int word_[8];
-    __shared__ unsigned int s_ticket;
-    __shared__ ScanResult sres[kMaxScan];
-    __shared__ long long part_acc[3][256];
+    __shared__ int word[8];
+    __shared__ long long wleft[8];
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const HyperParams &hp = s.hp;
     const int F = s.n_features, nb = s.n_bins;
     const size_t hsz = (size_t)F * nb * 3;
-    Step st;
-    if (!root_mode) {
-        st = *s.step;
-        if (!st.active) return;
-    }
+    const int n_items = root_mode ? 1 : s.batch->n_items;
+    const int n_tasks = n_items * F;
+    if ((int)blockIdx.x >= n_tasks) return;
     const Round rd = *s.round;
     const double gu = rd.grad_units, hu = rd.hess_units;
-    const int f = blockIdx.x;
-    int64_t m_built, m_sib = 0;
-    int built_buf, depth_child;
-    if (root_mode) {
-        m_built = hp.bagging ? s.cursor[0] : s.n;
-        built_buf = 0;
-        depth_child = 0;
-    } else {
-        const int64_t m = st.end - st.begin;
-        m_built = st.builds_left ? st.n_left : m - st.n_left;
-        m_sib = m - m_built;
-        built_buf = st.child_hist;
-        depth_child = st.depth + 1;
+    const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
+    long long hmin = 0;  // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
+    if (hp.min_sum_hessian > 0.0) {
+        const double u = hp.min_sum_hessian * hu;
+        double fl = floor(u);
+        if (fl < u) fl += 1.0;
+        hmin = (long long)fl;
     }
-    // ---- merge the built child's partials: thread -> (bin, half of the parts)
-    const int64_t chunk = hist_chunk(s, m_built);
-    const int64_t nparts = m_built > 0 ? (m_built + chunk - 1) / chunk : 0;
-    {
-        const int bin = tid & 255, half = tid >> 8;
-        long long g = 0, h = 0, c = 0;
-        if (bin < nb) {
-            const size_t pstride = (size_t)F * s.part_stride;
-            const unsigned long long *p = s.part + (size_t)f * s.part_stride + bin;
-            int64_t b = half;
-            for (; b + 14 < nparts; b += 16) {
-                unsigned long long v[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(b + 2 * u) * pstride];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    c += (long long)(v[u] & 0xFFFFFULL);
-                    h += (long long)((v[u] >> 20) & 0x3FFFFFULL);
-                    g += (long long)v[u] >> 42;
-                }
-            }
-            for (; b < nparts; b += 2) {
-                const unsigned long long v = p[(size_t)b * pstride];
-                c += (long long)(v & 0xFFFFFULL);
-                h += (long long)((v >> 20) & 0x3FFFFFULL);
-                g += (long long)v >> 42;
-            }
+    for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
+        const int j = task / F;
+        const int f = task - j * F;
+        Item it;
+        int64_t m_built, m_sib;
+        if (root_mode) {
+            m_built = root_rows(s);
+            m_sib = 0;
+            it.part_off = 0;
+            const int64_t chk = hist_chunk(s, m_built);
+            it.part_cnt = m_built > 0 ? (int)((m_built + chk - 1) / chk) : 0;
+            it.hist_built = 0;
+            it.hist_sib = 0;
+            it.depth_child = 0;
+        } else {
+            it = s.items[j];
+            const int64_t m = it.end - it.begin;
+            m_built = it.builds_left ? it.n_left : m - it.n_left;
+            m_sib = m - m_built;
         }
-        if (half == 1) {
-            part_acc[0][bin] = g;
-            part_acc[1][bin] = h;
-            part_acc[2][bin] = c;
-        }
-        __syncthreads();
-        if (half == 0) {
-            g += part_acc[0][bin];
-            h += part_acc[1][bin];
-            c += part_acc[2][bin];
-            cgs[0][bin] = g;
-            chs[0][bin] = h;
-            ccs[0][bin] = c;
-            long long sgv = 0, shv = 0, scv = 0;
+        // ---- merge the accumulated child's partials: thread -> (bin, half)
+        {
+            const int bin = tid & 255, half = tid >> 8;
+            int g = 0, h = 0, c = 0;
             if (bin < nb) {
-                int32_t *ob = s.hist + (size_t)built_buf * hsz + ((size_t)f * nb + bin) * 3;
-                ob[0] = (int32_t)g;
-                ob[1] = (int32_t)h;
-                ob[2] = (int32_t)c;
-                if (!root_mode) {
-                    int32_t *pp = s.hist + (size_t)st.parent_hist * hsz + ((size_t)f * nb + bin) * 3;
-                    sgv = (long long)pp[0] - g;
-                    shv = (long long)pp[1] - h;
-                    scv = (long long)pp[2] - c;
-                    pp[0] = (int32_t)sgv;
-                    pp[1] = (int32_t)shv;
-                    pp[2] = (int32_t)scv;
+                const size_t pstride = (size_t)F * s.part_stride;
+                const unsigned long long *p =
+                    s.part + (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
+                const int np = it.part_cnt;
+                int b = half;
+                for (; b + 14 < np; b += 16) {
+                    unsigned long long vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) vv[u] = p[(size_t)(b + 2 * u) * pstride];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        c += (int)(vv[u] & 0xFFFFFULL);
+                        h += (int)((vv[u] >> 20) & 0x3FFFFFULL);
+                        g += (int)((long long)vv[u] >> 42);
+                    }
+                }
+                for (; b < np; b += 2) {
+                    const unsigned long long vv = p[(size_t)b * pstride];
+                    c += (int)(vv & 0xFFFFFULL);
+                    h += (int)((vv >> 20) & 0x3FFFFFULL);
+                    g += (int)((long long)vv >> 42);
                 }
             }
-            cgs[1][bin] = sgv;
-            chs[1][bin] = shv;
-            ccs[1][bin] = scv;
+            if (half == 1) {
+                acc[0][bin] = g;
+                acc[1][bin] = h;
+                acc[2][bin] = c;
+            }
+            __syncthreads();
+            if (half == 0) {
+                g += acc[0][bin];
+                h += acc[1][bin];
+                c += acc[2][bin];
+                cg[0][bin] = g;
+                ch[0][bin] = h;
+                cc[0][bin] = c;
+                int sgv = 0, shv = 0, scv = 0;
+                if (bin < nb) {
+                    int32_t *ob = s.hist + (size_t)it.hist_built * hsz + ((size_t)f * nb + bin) * 3;
+                    ob[0] = g;
+                    ob[1] = h;
+                    ob[2] = c;
+                    if (!root_mode) {
+                        int32_t *pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
+                        sgv = pp[0] - g;
+                        shv = pp[1] - h;
+                        scv = pp[2] - c;
+                        pp[0] = sgv;
+                        pp[1] = shv;
+                        pp[2] = scv;
+                    }
+                }
+                cg[1][bin] = sgv;
+                ch[1][bin] = shv;
+                cc[1][bin] = scv;
+            }
+            __syncthreads();
+        }
+        // ---- scan: threads 0-255 the accumulated child, 256-511 the sibling
+        const int child = tid >> 8;
+        const int bin = tid & 255;
+        const int cw = wv & 3;
+        const int vg = cg[child][bin], vh = ch[child][bin], vc = cc[child][bin];
+        const int ig = wave_incl_scan_i(vg), ih = wave_incl_scan_i(vh), ic = wave_incl_scan_i(vc);
+        if (lane == 63) {
+            wtot[wv][0] = ig;
+            wtot[wv][1] = ih;
+            wtot[wv][2] = ic;
+        }
+        __syncthreads();
+        int pg = 0, ph = 0, pc = 0, TG = 0, TH = 0, TC = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int ww = (child << 2) + k;
+            if (k < cw) {
+                pg += wtot[ww][0];
+                ph += wtot[ww][1];
+                pc += wtot[ww][2];
+            }
+            TG += wtot[ww][0];
+            TH += wtot[ww][1];
+            TC += wtot[ww][2];
+        }
+        const int lg = pg + ig, lh = ph + ih, lc = pc + ic;  // inclusive prefix at `bin`
+        const int64_t n_child = child == 0 ? m_built : m_sib;
+        const int mbf = s.missing_bin[f];
+        const bool gated = (root_mode && child == 1) ||
+                           (hp.max_depth > 0 && it.depth_child >= hp.max_depth) ||
+                           n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
+                           !s.feature_mask[(size_t)rd.tree_index * F + f];
+        double best_gain = 0.0;
+        int best_order = 0x7FFFFFFF;
+        int best_left = 0;
+        if (!gated) {
+            const int mg = mbf >= 0 ? cg[child][mbf] : 0, mh = mbf >= 0 ? ch[child][mbf] : 0,
+                      mc = mbf >= 0 ? cc[child][mbf] : 0;
+            const long long min_c = hp.min_data_in_leaf;
+            const int n_scan = mbf >= 0 ? mbf : nb;
+            int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
+            if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
+            if (bin < lim) {
+                const double parent = qscore(TG, TH, gu, hu, l1, l2);
+                if (mbf >= 0) {
+                    const int ag = lg + mg, ah = lh + mh, ac = lc + mc;
+                    const int rg = TG - ag, rh = TH - ah, rc = TC - ac;
+                    if (!(ah < hmin || rh < hmin || ac < min_c || rc < min_c)) {
+                        const double gain =
+                            qscore(ag, ah, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                        if (gain > best_gain) {
+                            best_gain = gain;
+                            best_order = 2 * bin;
+                            best_left = ac;
+                        }
+                    }
+                }
+                if (mbf < 0 || mc > 0) {
+                    const int rg = TG - lg, rh = TH - lh, rc = TC - lc;
+                    if (!(lh < hmin || rh < hmin || lc < min_c || rc < min_c)) {
+                        const double gain =
+                            qscore(lg, lh, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                        if (gain > best_gain) {
+                            best_gain = gain;
+                            best_order = 2 * bin + 1;
+                            best_left = lc;
+                        }
+                    }
+                }
+            }
+        }
+        {
+            // argmax carrying the winner's left count (orders are distinct
+            // per lane, so the winner is the lane that held the final order)
+            const int mine = best_order;
+            wave_argmax(best_gain, best_order);
+            const unsigned long long wins = __ballot(mine == best_order && best_order != 0x7FFFFFFF);
+            const int srcl = wins ? (int)__ffsll((long long)wins) - 1 : 0;
+            best_left = __shfl(best_left, srcl, 64);
+        }
+        if (lane == 0) {
+            wgain[wv] = best_gain;
+            word[wv] = best_order;
+            wleft[wv] = best_left;
+        }
+        __syncthreads();
+        if ((tid & 255) == 0 && !(root_mode && child == 1)) {
+            double bgn = wgain[child << 2];
+            int bo = word[child << 2];
+            long long bleft = wleft[child << 2];
+            for (int k = 1; k < 4; ++k) {
+                const double og = wgain[(child << 2) + k];
+                const int oo = word[(child << 2) + k];
+                if (og > bgn || (og == bgn && oo < bo)) {
+                    bgn = og;
+                    bo = oo;
+                    bleft = wleft[(child << 2) + k];
+                }
+            }
+            ScanResult rs;
+            rs.gain = bgn;
+            rs.found = bo != 0x7FFFFFFF;
+            rs.bin = rs.found ? bo >> 1 : -1;
+            rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
+            rs.pad_ = 0;
+            rs.tot_g = TG;
+            rs.tot_h = TH;
+            rs.tot_c = TC;
+            rs.n_left = rs.found ? bleft : 0;
+            s.scan[(size_t)(j * 2 + child) * F + f] = rs;
         }
         __syncthreads();
     }
-    // ---- scan: waves 0-3 the built child, waves 4-7 the sibling; one bin each
-    const int child = tid >> 8;
-    const int bin = tid & 255;
-    const int cw = wv & 3;  // wave within the child
-    const long long vg = cgs[child][bin], vh = chs[child][bin], vc = ccs[child][bin];
-    const long long ig = wave_incl_scan(vg), ih = wave_incl_scan(vh), ic = wave_incl_scan(vc);
-    if (lane == 63) {
-        wtot[wv][0] = ig;
-        wtot[wv][1] = ih;
-        wtot[wv][2] = ic;
-    }
-    __syncthreads();
-    long long pg = 0, ph = 0, pc = 0, TG = 0, TH = 0, TC = 0;
-    for (int k = 0; k < 4; ++k) {
-        const int ww = (child << 2) + k;
-        if (k < cw) {
-            pg += wtot[ww][0];
-            ph += wtot[ww][1];
-            pc += wtot[ww][2];
-        }
-        TG += wtot[ww][0];
-        TH += wtot[ww][1];
-        TC += wtot[ww][2];
-    }
-    const long long lg = pg + ig, lh = ph + ih, lc = pc + ic;  // inclusive prefix at `bin`
-    const int64_t n_child = child == 0 ? m_built : m_sib;
-    const int mb = s.missing_bin[f];
-    const bool gated = (root_mode && child == 1) || (hp.max_depth > 0 && depth_child >= hp.max_depth) ||
-                       n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
-                       !s.feature_mask[(size_t)rd.tree_index * F + f];
-    double best_gain = 0.0;
-    int best_order = 0x7FFFFFFF;
-    if (!gated) {
-        const long long mg = mb >= 0 ? cgs[child][mb] : 0, mh = mb >= 0 ? chs[child][mb] : 0,
-                        mc = mb >= 0 ? ccs[child][mb] : 0;
-        const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
-        long long hmin = 0;  // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
-        if (hp.min_sum_hessian > 0.0) {
-            const double u = hp.min_sum_hessian * hu;
-            double fl = floor(u);
-            if (fl < u) fl += 1.0;
-            hmin = (long long)fl;
-        }
-        const long long min_c = hp.min_data_in_leaf;
-        const int n_scan = mb >= 0 ? mb : nb;
-        int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
-        if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
-        if (bin < lim) {
-            const double parent = qscore(TG, TH, gu, hu, l1, l2);
-            if (mb >= 0) {
-                const long long ag = lg + mg, ah = lh + mh, ac = lc + mc;
-                const long long rg = TG - ag, rh = TH - ah, rc = TC - ac;
-                if (!(ah < hmin || rh < hmin || ac < min_c || rc < min_c)) {
-                    const double gain = qscore(ag, ah, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
-                    if (gain > best_gain) {
-                        best_gain = gain;
-                        best_order = 2 * bin;
-                    }
-                }
-            }
-            if (mb < 0 || mc > 0) {
-                const long long rg = TG - lg, rh = TH - lh, rc = TC - lc;
-                if (!(lh < hmin || rh < hmin || lc < min_c || rc < min_c)) {
-                    const double gain = qscore(lg, lh, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
-                    if (gain > best_gain) {
-                        best_gain = gain;
-                        best_order = 2 * bin + 1;
-                    }
-                }
-            }
-        }
-    }
-    wave_argmax(best_gain, best_order);
-    if (lane == 0) {
-        wgain[wv] = best_gain;
-        word_[wv] = best_order;
-    }
-    __syncthreads();
-    if (tid == 0 || tid == 256) {
-        double bg = wgain[child << 2];
-        int bo = word_[child << 2];
-        for (int k = 1; k < 4; ++k) {
-            const double og = wgain[(child << 2) + k];
-            const int oo = word_[(child << 2) + k];
-            if (og > bg || (og == bg && oo < bo)) {
-                bg = og;
-                bo = oo;
-            }
-        }
-        if (!(root_mode && child == 1)) {
-            ScanResult r;
-            r.gain = bg;
-            r.found = bo != 0x7FFFFFFF;
-            r.bin = r.found ? bo >> 1 : -1;
-            r.default_left = r.found ? ((bo & 1) == 0) : 0;
-            r.pad_ = 0;
-            r.tot_g = TG;
-            r.tot_h = TH;
-            r.tot_c = TC;
-            s.scan[child * F + f] = r;
-        }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_ticket = atomicAdd(s.ticket, 1u);
-    __syncthreads();
-    if (s_ticket != (unsigned int)(F - 1)) return;
-    __threadfence();
+}
 
-    // ------------------------------------------------ last block: fold + pick
-    const int nchild = root_mode ? 1 : 2;
-    for (int i = tid; i < nchild * F; i += blockDim.x) {
-        const ScanResult *p = &s.scan[i];
-        ScanResult r;
-        r.found = load_agent(&p->found);
-        r.gain = load_agent_f64(&p->gain);
-        r.bin = load_agent(&p->bin);
-        r.default_left = load_agent(&p->default_left);
-        r.pad_ = 0;
-        r.tot_g = load_agent(&p->tot_g);
-        r.tot_h = load_agent(&p->tot_h);
-        r.tot_c = load_agent(&p->tot_c);
-        sres[i] = r;
+// ------------------------------------------------------------------ planner
+// Single block of kPlanThreads, after every scan launch.
+//
+// 1. Fold: for each child of each expanded item, the feature of largest gain
+//    (strict '>', lowest feature on ties, gain > 0) becomes the child's best
+//    split; with the child's totals and leaf value (quantized_leaf_output)
+//    it is stored in the child's explored node.
+// 2. Replay: the reference's best-first order (tree.grow_tree_leaves_profiled;
+//    growth_policy.GrowthSchedule.next_leaf, src/mojotrees/growth_policy.mojo:
+//    659-677: the frontier slot of largest gain wins, lowest slot on ties,
+//    gain must be > 0, stop at num_leaves) over the explored nodes: each pick
+//    whose leaf is already expanded is committed -- node ids left = n_nodes,
+//    right = n_nodes + 1, the left child keeps the parent's slot, the right
+//    one takes slot n_leaves -- until a pick needs an unexpanded leaf or the
+//    tree is complete.
+// 3. Selection: best-first continues over the explored tree as if every
+//    expanded leaf were committed; each pick that is not expanded joins the
+//    next batch and counts as one split, until num_leaves would be reached
+//    or the batch holds min(kmax, remaining splits, free expansions -
+//    (remaining splits - 1)) leaves. The first pick is the leaf the replay
+//    waits for; the budget rule leaves an expansion for every split the
+//    replay can still need. Expanding ahead this way follows the order the
+//    replay will take, so speculative expansions are mostly used.
+constexpr int kPlanThreads = 1024;
+
+// LDS layout of the planner (byte offsets), shared by the host's size query
+// and the kernel.
+struct PlanLayout {
+    size_t fg, wg, eg, sg, wf, el, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
+    size_t total;
+};
+
+__host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
+    PlanLayout p;
+    size_t o = 0;
+    auto take = [&o](size_t bytes, size_t align) {
+        o = (o + align - 1) & ~(align - 1);
+        const size_t at = o;
+        o += bytes;
+        return at;
+    };
+    p.fg = take((size_t)8 * 2 * K * F, 16);  // (pair, feature) gain, -1 if none
+    p.wg = take((size_t)8 * 2 * K, 8);       // pair's best gain
+    p.eg = take((size_t)8 * E, 8);           // explored node's gain view
+    p.sg = take((size_t)8 * L, 8);           // frontier slot's gain
+    p.wf = take((size_t)4 * 2 * K, 4);       // pair's best feature
+    p.el = take((size_t)4 * E, 4);           // explored node's left child
+    p.sl_e = take((size_t)4 * L, 4);
+    p.sl_fid = take((size_t)4 * L, 4);
+    p.cm_e = take((size_t)4 * L, 4);
+    p.cm_fid = take((size_t)4 * L, 4);
+    p.cm_lf = take((size_t)4 * L, 4);
+    p.sel_e = take((size_t)4 * K, 4);
+    p.pcnt = take((size_t)4 * K, 4);
+    p.poff = take((size_t)4 * (K + 1), 4);
+    p.it = take(sizeof(Item) * K, 16);
+    p.total = o;
+    return p;
+}
+
+struct PlanView {
+    double *fg, *wg, *eg, *sg;
+    int32_t *wf, *el, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff;
+    Item *it;
+};
+
+__device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
+    const PlanLayout p = plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features);
+    PlanView v;
+    v.fg = (double *)(smem + p.fg);
+    v.wg = (double *)(smem + p.wg);
+    v.eg = (double *)(smem + p.eg);
+    v.sg = (double *)(smem + p.sg);
+    v.wf = (int32_t *)(smem + p.wf);
+    v.el = (int32_t *)(smem + p.el);
+    v.sl_e = (int32_t *)(smem + p.sl_e);
+    v.sl_fid = (int32_t *)(smem + p.sl_fid);
+    v.cm_e = (int32_t *)(smem + p.cm_e);
+    v.cm_fid = (int32_t *)(smem + p.cm_fid);
+    v.cm_lf = (int32_t *)(smem + p.cm_lf);
+    v.sel_e = (int32_t *)(smem + p.sel_e);
+    v.pcnt = (int32_t *)(smem + p.pcnt);
+    v.poff = (int32_t *)(smem + p.poff);
+    v.it = (Item *)(smem + p.it);
+    return v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode) {
+    extern __shared__ unsigned char plan_smem[];
+    __shared__ Grow g;
+    __shared__ int s_nc, s_done, s_ncand, s_total, s_x;
+    __shared__ unsigned long long s_rows_built, s_rows_parted;
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
+    const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
+    const int L = s.hp.num_leaves, F = s.n_features;
+    const HyperParams &hp = s.hp;
+    const int n_items = root_mode ? 1 : s.batch->n_items;
+    if (n_items <= 0) return;  // the tree is complete
+    PlanView v = plan_view(s, plan_smem);
+    const Round rd = *s.round;
+    const double gu = rd.grad_units, hu = rd.hess_units;
+    if (tid == 0) {
+        if (root_mode) {
+            g.n_leaves = 1;
+            g.n_nodes = 1;
+            g.n_explored = 1;
+            g.n_hist = 1;
+            g.expansions = 0;
+            g.iterations = 0;
+            g.rows_built = 0;
+            g.rows_parted = 0;
+        } else {
+            g = *s.grow;
+        }
+        s_rows_built = 0;
+        s_rows_parted = 0;
+        s_ncand = 0;
     }
+    // ---- 1. fold (loads of every (pair, feature) gain, then one wave per pair)
+    const int n_pairs = root_mode ? 1 : 2 * n_items;
+    for (int i = tid; i < n_pairs * F; i += nthr) {
+        const ScanResult &q = s.scan[i];
+        v.fg[i] = q.found ? q.gain : -1.0;
+    }
+    if (!root_mode)
+        for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
     __syncthreads();
-    if (wv < nchild) {
+    const int ne = g.n_explored, nl0 = g.n_leaves;
+    for (int i = tid; i < ne; i += nthr) {
+        v.eg[i] = s.e_gain[i];
+        v.el[i] = s.e_left[i];
+    }
+    if (!root_mode)
+        for (int i = tid; i < nl0; i += nthr) {
+            v.sl_e[i] = s.slot_e[i];
+            v.sl_fid[i] = s.slot_fid[i];
+        }
+    for (int pr = wv; pr < n_pairs; pr += nwaves) {
         double bg = 0.0;
         int bf = 0x7FFFFFFF;
         for (int ff = lane; ff < F; ff += 64) {
-            const ScanResult &r = sres[wv * F + ff];
-            if (r.found && r.gain > bg) {
-                bg = r.gain;
+            const double q = v.fg[pr * F + ff];
+            if (q > bg) {
+                bg = q;
                 bf = ff;
             }
         }
         wave_argmax(bg, bf);
         if (lane == 0) {
-            wgain[wv] = bg;
-            word_[wv] = bf;
+            v.wg[pr] = bg;
+            v.wf[pr] = bf;
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        int32_t *meta = s.t_meta;
-        const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
-        auto fill_slot = [&](Slot &sl, int ch) {
-            const int bf = word_[ch];
-            sl.found = bf != 0x7FFFFFFF;
-            if (sl.found) {
-                const ScanResult &r = sres[ch * F + bf];
-                sl.feature = bf;
-                sl.bin = r.bin;
-                sl.default_left = r.default_left;
-                sl.gain = wgain[ch];
-            } else {
-                sl.feature = -1;
-                sl.bin = -1;
-                sl.default_left = 0;
-                sl.gain = 0.0;
-            }
-        };
-        auto new_node = [&](int id, double v, double cnt) {
-            s.t_feature[id] = -1;
-            s.t_threshold[id] = -1;
-            s.t_left[id] = -1;
-            s.t_right[id] = -1;
-            s.t_default_left[id] = 0;
-            s.t_missing_bin[id] = -1;
-            s.t_value[id] = v;
-            s.t_gain[id] = 0.0;
-            s.t_count[id] = cnt;
-        };
+    for (int pr = tid; pr < n_pairs; pr += nthr) {
+        int e_id = 0;
+        if (!root_mode) {
+            const Item &it = v.it[pr >> 1];
+            const bool built = (pr & 1) == 0;
+            e_id = (built == (it.builds_left != 0)) ? it.left_e : it.left_e + 1;
+        }
+        const ScanResult *base = &s.scan[(size_t)pr * F];
+        const long long G = base->tot_g, H = base->tot_h, C = base->tot_c;
+        ENode *e = &s.enodes[e_id];
         if (root_mode) {
-            const ScanResult &r = sres[0];
-            new_node(0, qleaf(r.tot_g, r.tot_h, gu, hu, l1, l2), (double)r.tot_c);
-            meta[0] = 1;
-            meta[1] = 1;
-            Slot sl;
-            sl.begin = 0;
-            sl.end = r.tot_c;
-            sl.node = 0;
-            sl.buf = 0;
-            sl.hist = 0;
-            sl.depth = 0;
-            fill_slot(sl, 0);
-            s.slots[0] = sl;
-            s.arc_rows[(size_t)rd.tree_index * hp.num_leaves + 0] = r.tot_c;
+            e->begin = 0;
+            e->end = C;
+            e->buf = 0;
+            e->hist = 0;
+            e->depth = 0;
+            e->left_e = -1;
+            e->right_e = -1;
+            e->pad_ = 0;
+            s.t_value[0] = qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2);
+            s.t_count[0] = (double)C;
+        }
+        e->tot_g = G;
+        e->tot_h = H;
+        e->tot_c = C;
+        e->value = qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2);
+        const int bf = v.wf[pr];
+        const bool found = bf != 0x7FFFFFFF;
+        e->found = found ? 1 : 0;
+        if (found) {
+            const ScanResult &q = base[bf];
+            e->gain = v.wg[pr];
+            e->feature = bf;
+            e->bin = q.bin;
+            e->default_left = q.default_left;
+            e->n_left = q.n_left;
         } else {
-            const ScanResult &b = sres[0];
-            const ScanResult &sb = sres[F];
-            const bool bl = st.builds_left != 0;
-            const ScanResult &Lr = bl ? b : sb;
-            const ScanResult &Rr = bl ? sb : b;
-            new_node(st.node_left, qleaf(Lr.tot_g, Lr.tot_h, gu, hu, l1, l2), (double)Lr.tot_c);
-            new_node(st.node_right, qleaf(Rr.tot_g, Rr.tot_h, gu, hu, l1, l2), (double)Rr.tot_c);
-            const int pn = st.parent_node;
-            s.t_feature[pn] = st.feature;
-            s.t_threshold[pn] = st.bin;
-            s.t_left[pn] = st.node_left;
-            s.t_right[pn] = st.node_right;
-            s.t_default_left[pn] = st.default_left;
-            s.t_missing_bin[pn] = st.missing_bin;
-            s.t_gain[pn] = st.gain;
-            Slot L, R;
-            L.begin = st.begin;
-            L.end = st.begin + st.n_left;
-            R.begin = L.end;
-            R.end = st.end;
-            L.node = st.node_left;
-            R.node = st.node_right;
-            L.buf = R.buf = 1 - st.src_buf;
-            L.hist = bl ? st.child_hist : st.parent_hist;
-            R.hist = bl ? st.parent_hist : st.child_hist;
-            L.depth = R.depth = st.depth + 1;
-            fill_slot(L, bl ? 0 : 1);
-            fill_slot(R, bl ? 1 : 0);
-            s.slots[st.parent_slot] = L;
-            s.slots[st.new_slot] = R;
-            meta[0] += 2;
-            meta[1] += 1;
+            e->gain = 0.0;
+            e->feature = -1;
+            e->bin = -1;
+            e->default_left = 0;
+            e->n_left = 0;
+        }
+        const double eg = found ? v.wg[pr] : -1.0;  // a found split has gain > 0
+        v.eg[e_id] = eg;
+        s.e_gain[e_id] = eg;
+        if (root_mode) {
+            v.el[0] = -1;
+            s.e_left[0] = -1;
         }
     }
+    if (root_mode && tid == 0) {
+        v.sl_e[0] = 0;
+        v.sl_fid[0] = 0;
+    }
     __syncthreads();
-    // pick the next leaf (wave 0)
-    __shared__ int s_pick;
-    __shared__ Slot s_slot;
-    if (wv == 0) {
-        const int n_leaves = s.t_meta[1];
-        double bg = 0.0;
-        int bi = 0x7FFFFFFF;
-        if (n_leaves < hp.num_leaves) {
-            for (int i = lane; i < n_leaves; i += 64) {
-                const Slot &sl = s.slots[i];
-                if (sl.found && sl.gain > 0.0 && sl.gain > bg) {
-                    bg = sl.gain;
-                    bi = i;
+    for (int i = tid; i < nl0; i += nthr) v.sg[i] = v.eg[v.sl_e[i]];
+    __syncthreads();
+    // ---- 2. replay (wave 0). The frontier lives in LDS; lane l owns slots
+    // l, l + 64, ... and keeps the best (gain, slot) of its own slots in
+    // registers, so a pick is one wave reduction. Every lane writes the same
+    // values to the shared arrays, so each lane reads back its own writes.
+    if (tid < 64) {
+        double lbg = 0.0;
+        int lbi = 0x7FFFFFFF;
+        auto own_best = [&](int nslots) {
+            lbg = 0.0;
+            lbi = 0x7FFFFFFF;
+            for (int i = lane; i < nslots; i += 64) {
+                const double gi = v.sg[i];
+                if (gi > lbg) {
+                    lbg = gi;
+                    lbi = i;
                 }
             }
+        };
+        auto pick = [&](int &bi) {
+            double bg = lbg;
+            bi = lbi;
+            wave_argmax(bg, bi);
+            return bi != 0x7FFFFFFF;
+        };
+        int nl = nl0, nn = g.n_nodes, nc = 0, done = 0, x = -1;
+        own_best(nl);
+        for (;;) {
+            int bi;
+            if (nl >= L || !pick(bi)) {
+                done = 1;
+                break;
+            }
+            const int X = v.sl_e[bi];
+            const int le = v.el[X];
+            if (le < 0) {
+                x = X;
+                break;
+            }
+            v.cm_e[nc] = X;
+            v.cm_fid[nc] = v.sl_fid[bi];
+            v.cm_lf[nc] = nn;
+            v.sl_e[bi] = le;
+            v.sl_fid[bi] = nn;
+            v.sg[bi] = v.eg[le];
+            v.sl_e[nl] = le + 1;
+            v.sl_fid[nl] = nn + 1;
+            v.sg[nl] = v.eg[le + 1];
+            if (lane == (bi & 63) || lane == (nl & 63)) own_best(nl + 1);
+            ++nl;
+            nn += 2;
+            ++nc;
         }
-        wave_argmax(bg, bi);
         if (lane == 0) {
-            s_pick = bi;
-            if (bi != 0x7FFFFFFF) s_slot = s.slots[bi];
+            s_nc = nc;
+            s_done = done;
+            s_x = x;
+            g.n_leaves = nl;
+            g.n_nodes = nn;
         }
     }
     __syncthreads();
-    const int bi = s_pick;
-    if (bi == 0x7FFFFFFF) {
+    const int nc = s_nc, nl = g.n_leaves, nn = g.n_nodes;
+    // committed splits -> tree arrays
+    for (int c = tid; c < nc; c += nthr) {
+        const ENode *e = &s.enodes[v.cm_e[c]];
+        const int fx = v.cm_fid[c], lf = v.cm_lf[c];
+        const int feat = e->feature;
+        const int le = v.el[v.cm_e[c]];
+        s.t_feature[fx] = feat;
+        s.t_threshold[fx] = e->bin;
+        s.t_left[fx] = lf;
+        s.t_right[fx] = lf + 1;
+        s.t_default_left[fx] = e->default_left;
+        s.t_missing_bin[fx] = s.missing_bin[feat];
+        s.t_gain[fx] = e->gain;
+        s.t_value[lf] = s.enodes[le].value;
+        s.t_count[lf] = (double)s.enodes[le].tot_c;
+        s.t_value[lf + 1] = s.enodes[le + 1].value;
+        s.t_count[lf + 1] = (double)s.enodes[le + 1].tot_c;
+    }
+    auto finish = [&](int err_code) {
         if (tid == 0) {
-            s.step->active = 0;
-            *s.ticket = 0u;
+            if (err_code) atomicOr(s.error, err_code);
+            s.t_meta[0] = nn;
+            s.t_meta[1] = nl;
+            *s.grow = g;
+            Batch b;
+            b.n_items = 0;
+            b.n_blocks = 0;
+            b.done = 1;
+            b.root = 0;
+            *s.batch = b;
         }
+    };
+    if (s_done) {
+        for (int i = tid; i < nl; i += nthr) {
+            const int fid = v.sl_fid[i];
+            s.t_feature[fid] = -1;
+            s.t_threshold[fid] = -1;
+            s.t_left[fid] = -1;
+            s.t_right[fid] = -1;
+            s.t_default_left[fid] = 0;
+            s.t_missing_bin[fid] = -1;
+            s.t_gain[fid] = 0.0;
+        }
+        finish(0);
         return;
     }
-    const Slot sl = s_slot;
-    const int32_t *pick_h = s.hist + (size_t)sl.hist * hsz + (size_t)sl.feature * nb * 3;
-    const int fmb = s.missing_bin[sl.feature];
-    long long nl = 0;
-    if (tid < nb) {
-        const bool goes_left = (tid == fmb) ? (sl.default_left != 0) : (tid <= sl.bin);
-        if (goes_left) nl = load_agent(&pick_h[3 * tid + 2]);
+    // the committed frontier is kept before the speculative pass reuses it
+    for (int i = tid; i < nl; i += nthr) {
+        s.slot_e[i] = v.sl_e[i];
+        s.slot_fid[i] = v.sl_fid[i];
     }
-    nl = wave_sum_ll(nl);
-    if (lane == 0) wtot[wv][0] = nl;
+    __syncthreads();
+    // ---- 3. selection: continue best-first over the explored tree as if
+    // every leaf already expanded were committed; a pick that is not
+    // expanded joins the batch and counts as a split. The first pick is the
+    // leaf the replay waits for.
+    const int r = L - nl;
+    int cap = r < s.kmax ? r : s.kmax;
+    const int room = (s.max_exp - g.expansions) - (r - 1);
+    if (room < cap) cap = room;
+    if (tid < 64) {
+        double lbg = 0.0;
+        int lbi = 0x7FFFFFFF;
+        auto own_best = [&](int nslots) {
+            lbg = 0.0;
+            lbi = 0x7FFFFFFF;
+            for (int i = lane; i < nslots; i += 64) {
+                const double gi = v.sg[i];
+                if (gi > lbg) {
+                    lbg = gi;
+                    lbi = i;
+                }
+            }
+        };
+        int nslots = nl, nsim = nl, nsel = 0;
+        own_best(nslots);
+        while (nsim < L && nsel < cap) {
+            double bg = lbg;
+            int bi = lbi;
+            wave_argmax(bg, bi);
+            if (bi == 0x7FFFFFFF) break;
+            const int Y = v.sl_e[bi];
+            const int le = v.el[Y];
+            if (le < 0) {
+                v.sel_e[nsel] = Y;
+                ++nsel;
+                v.sg[bi] = -1.0;
+                if (lane == (bi & 63)) own_best(nslots);
+            } else {
+                v.sl_e[bi] = le;
+                v.sg[bi] = v.eg[le];
+                v.sl_e[nslots] = le + 1;
+                v.sg[nslots] = v.eg[le + 1];
+                if (lane == (bi & 63) || lane == (nslots & 63)) own_best(nslots + 1);
+                ++nslots;
+            }
+            ++nsim;
+        }
+        if (lane == 0) s_ncand = nsel;
+    }
+    __syncthreads();
+    const int nsel = s_ncand;
+    {
+        // unreachable while the expansion budget holds; each check has its
+        // own code in the sticky error word
+        const int bad = (cap <= 0 ? 8 : 0) | (nsel <= 0 ? 16 : 0) | (v.sel_e[0] != s_x ? 32 : 0) |
+                        (ne + 2 * nsel > s.e_cap ? 64 : 0) | (g.n_hist + nsel > 1 + s.max_exp ? 128 : 0);
+        if (bad) {
+            finish(bad);
+            return;
+        }
+    }
+    // rows per block: at least hist_chunk_min, at most 256 blocks per leaf
+    for (int jj = tid; jj < nsel; jj += nthr) {
+        const ENode *e = &s.enodes[v.sel_e[jj]];
+        const int64_t m = e->end - e->begin;
+        int64_t chunk = (m + 255) / 256;
+        if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+        if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
+        v.pcnt[jj] = (int)((m + chunk - 1) / chunk);
+    }
     __syncthreads();
     if (tid == 0) {
-        long long tot = 0;
-        for (int k = 0; k < 8; ++k) tot += wtot[k][0];
-        const int n_leaves = s.t_meta[1];
-        const int n_nodes = s.t_meta[0];
-        Step ns;
-        ns.active = 1;
-        ns.parent_slot = bi;
-        ns.new_slot = n_leaves;
-        ns.feature = sl.feature;
-        ns.bin = sl.bin;
-        ns.default_left = sl.default_left;
-        ns.missing_bin = fmb;
-        ns.src_buf = sl.buf;
-        ns.begin = sl.begin;
-        ns.end = sl.end;
-        ns.n_left = tot;
-        ns.builds_left = tot <= (sl.end - sl.begin) - tot;
-        ns.parent_hist = sl.hist;
-        ns.child_hist = n_leaves;
-        ns.depth = sl.depth;
-        ns.parent_node = sl.node;
-        ns.node_left = n_nodes;
-        ns.node_right = n_nodes + 1;
-        ns.pad_ = 0;
-        ns.gain = sl.gain;
-        *s.step = ns;
-        s.cursor[0] = 0;
-        s.cursor[1] = 0;
-        s.arc_rows[(size_t)rd.tree_index * hp.num_leaves + n_leaves] =
-            ns.builds_left ? tot : (sl.end - sl.begin) - tot;
-        *s.ticket = 0u;
+        int a = 0;
+        for (int jj = 0; jj < nsel; ++jj) {
+            v.poff[jj] = a;
+            a += v.pcnt[jj];
+        }
+        v.poff[nsel] = a;
+        s_total = a;
+    }
+    __syncthreads();
+    const int total = s_total;
+    if (total > s.pb_grid) {  // the leaves of a batch are disjoint, so never
+        finish(4);
+        return;
+    }
+    for (int jj = tid; jj < nsel; jj += nthr) {
+        const int Xs = v.sel_e[jj];
+        ENode *e = &s.enodes[Xs];
+        const int64_t b0 = e->begin, e0 = e->end, nlft = e->n_left;
+        const int64_t m = e0 - b0;
+        const int ebuf = e->buf, ehist = e->hist, edep = e->depth;
+        const bool bl = nlft <= m - nlft;
+        const int le = ne + 2 * jj, hb = g.n_hist + jj;
+        Item it;
+        it.begin = b0;
+        it.end = e0;
+        it.n_left = nlft;
+        it.parent_e = Xs;
+        it.left_e = le;
+        it.src_buf = ebuf;
+        it.builds_left = bl ? 1 : 0;
+        it.hist_built = hb;
+        it.hist_sib = ehist;
+        it.depth_child = edep + 1;
+        it.part_off = v.poff[jj];
+        it.part_cnt = v.pcnt[jj];
+        it.pad_ = 0;
+        s.items[jj] = it;
+        v.it[jj] = it;
+        ENode c;
+        c.n_left = 0;
+        c.tot_g = c.tot_h = c.tot_c = 0;
+        c.gain = 0.0;
+        c.value = 0.0;
+        c.buf = 1 - ebuf;
+        c.depth = edep + 1;
+        c.found = 0;
+        c.feature = -1;
+        c.bin = -1;
+        c.default_left = 0;
+        c.left_e = -1;
+        c.right_e = -1;
+        c.pad_ = 0;
+        c.begin = b0;
+        c.end = b0 + nlft;
+        c.hist = bl ? hb : ehist;
+        s.enodes[le] = c;
+        c.begin = b0 + nlft;
+        c.end = e0;
+        c.hist = bl ? ehist : hb;
+        s.enodes[le + 1] = c;
+        s.e_gain[le] = -1.0;
+        s.e_gain[le + 1] = -1.0;
+        s.e_left[le] = -1;
+        s.e_left[le + 1] = -1;
+        e->left_e = le;
+        e->right_e = le + 1;
+        s.e_left[Xs] = le;
+        s.cursor[2 + 2 * jj] = 0;
+        s.cursor[3 + 2 * jj] = 0;
+        atomicAdd(&s_rows_built, (unsigned long long)(bl ? nlft : m - nlft));
+        atomicAdd(&s_rows_parted, (unsigned long long)m);
+    }
+    __syncthreads();
+    // block descriptors
+    for (int b = tid; b < total; b += nthr) {
+        int lo = 0, hi = nsel - 1;  // last item with poff <= b
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (v.poff[mid] <= b) lo = mid;
+            else hi = mid - 1;
+        }
+        const Item &it = v.it[lo];
+        const ENode &pe = s.enodes[it.parent_e];
+        const int64_t m = it.end - it.begin;
+        int64_t chunk = (m + 255) / 256;
+        if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+        if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
+        PbDesc d;
+        d.begin = it.begin;
+        d.n_left = it.n_left;
+        d.m = m;
+        d.c0 = (int64_t)(b - v.poff[lo]) * chunk;
+        d.c1 = d.c0 + chunk < m ? d.c0 + chunk : m;
+        d.item = lo;
+        d.src_buf = it.src_buf;
+        d.feature = pe.feature;
+        d.bin = pe.bin;
+        d.default_left = pe.default_left;
+        d.missing_bin = s.missing_bin[pe.feature];
+        d.builds_left = it.builds_left;
+        d.pad_ = 0;
+        s.pb_desc[b] = d;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        g.n_explored = ne + 2 * nsel;
+        g.n_hist += nsel;
+        g.expansions += nsel;
+        g.iterations += 1;
+        g.rows_built += (int64_t)s_rows_built;
+        g.rows_parted += (int64_t)s_rows_parted;
+        *s.grow = g;
+        Batch b;
+        b.n_items = nsel;
+        b.n_blocks = total;
+        b.done = 0;
+        b.root = 0;
+        *s.batch = b;
     }
 }
 
@@ -911,6 +1274,12 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
     if (threadIdx.x == 0) {
         ai[6 * mn + 0] = n_nodes;
         ai[6 * mn + 1] = s.t_meta[1];
+        const Grow g = *s.grow;
+        int64_t *ax = s.arc_aux + (size_t)rd.tree_index * 4;
+        ax[0] = g.rows_built;
+        ax[1] = g.iterations;
+        ax[2] = g.expansions;
+        ax[3] = g.rows_parted;
         Round nr = rd;
         nr.tree_index = rd.tree_index + 1;
         nr.class_k = rd.class_k + 1;
@@ -960,38 +1329,63 @@ size_t score_lds_bytes(const DevState &s) {
     return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
 }
 size_t hist_lds_bytes(const DevState &s) { return (size_t)s.n_features * s.lds_stride * 8; }
-hipError_t prepare_hist(const DevState &s) {
-    const int bytes = (int)hist_lds_bytes(s);
-    hipError_t e = hipFuncSetAttribute((const void *)k_hist<1>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_hist<2>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_score, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)score_lds_bytes(s));
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_hist<4>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_hist<8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+size_t pb_lds_bytes(const DevState &s) { return pb_lds_bytes_of(s.n_features, s.lds_stride); }
+size_t plan_lds_bytes(const DevState &s) {
+    return plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features).total;
 }
-hipError_t launch_hist(const DevState &s, int root_mode, hipStream_t st) {
+
+#define MB_SET_LDS(fn, bytes)                                                                     \
+    do {                                                                                          \
+        hipError_t e_ = hipFuncSetAttribute((const void *)(fn), hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                            (int)(bytes));                                        \
+        if (e_ != hipSuccess) return e_;                                                          \
+    } while (0)
+
+hipError_t prepare_kernels(const DevState &s) {
+    const size_t h = hist_lds_bytes(s), pb = pb_lds_bytes(s);
+    MB_SET_LDS(k_hist<1>, h);
+    MB_SET_LDS(k_hist<2>, h);
+    MB_SET_LDS(k_hist<4>, h);
+    MB_SET_LDS(k_hist<8>, h);
+    MB_SET_LDS(k_part_hist<1>, pb);
+    MB_SET_LDS(k_part_hist<2>, pb);
+    MB_SET_LDS(k_part_hist<4>, pb);
+    MB_SET_LDS(k_part_hist<8>, pb);
+    MB_SET_LDS(k_plan, plan_lds_bytes(s));
+    MB_SET_LDS(k_score, score_lds_bytes(s));
+    return hipSuccess;
+}
+hipError_t launch_hist(const DevState &s, hipStream_t st) {
     const size_t lds = hist_lds_bytes(s);
-    const int lpr = s.rec_bytes / 16;
     const dim3 grid(s.hist_grid), block(1024);
-    switch (lpr) {
-    case 1: hipLaunchKernelGGL(k_hist<1>, grid, block, lds, st, s, root_mode); break;
-    case 2: hipLaunchKernelGGL(k_hist<2>, grid, block, lds, st, s, root_mode); break;
-    case 4: hipLaunchKernelGGL(k_hist<4>, grid, block, lds, st, s, root_mode); break;
-    case 8: hipLaunchKernelGGL(k_hist<8>, grid, block, lds, st, s, root_mode); break;
+    switch (s.rec_bytes / 16) {
+    case 1: hipLaunchKernelGGL(k_hist<1>, grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL(k_hist<2>, grid, block, lds, st, s); break;
+    case 4: hipLaunchKernelGGL(k_hist<4>, grid, block, lds, st, s); break;
+    case 8: hipLaunchKernelGGL(k_hist<8>, grid, block, lds, st, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
-hipError_t launch_partition(const DevState &s, int grid, hipStream_t st) {
-    hipLaunchKernelGGL(k_partition, dim3(grid), dim3(256), 0, st, s);
+hipError_t launch_part_hist(const DevState &s, hipStream_t st) {
+    const size_t lds = pb_lds_bytes(s);
+    const dim3 grid(s.pb_grid), block(kPbThreads);
+    switch (s.rec_bytes / 16) {
+    case 1: hipLaunchKernelGGL(k_part_hist<1>, grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL(k_part_hist<2>, grid, block, lds, st, s); break;
+    case 4: hipLaunchKernelGGL(k_part_hist<4>, grid, block, lds, st, s); break;
+    case 8: hipLaunchKernelGGL(k_part_hist<8>, grid, block, lds, st, s); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
-hipError_t launch_split(const DevState &s, int root_mode, hipStream_t st) {
-    hipLaunchKernelGGL(k_split, dim3(s.n_features), dim3(kSplitThreads), 0, st, s, root_mode);
+hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
+    const int grid = root_mode ? s.n_features : s.scan_grid;
+    hipLaunchKernelGGL(k_scan, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    return hipGetLastError();
+}
+hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st) {
+    hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanThreads), plan_lds_bytes(s), st, s, root_mode);
     return hipGetLastError();
 }
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st) {

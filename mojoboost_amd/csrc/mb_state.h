@@ -1,10 +1,11 @@
 // Device-resident state of one training run on one GPU.
 //
 // The tree grows entirely on the device: every kernel reads what it needs
-// (which leaf to split, its row range, the split) from a step descriptor that
-// the previous split kernel wrote, so the host enqueues a whole tree without
-// reading anything back. The host downloads the finished trees once, at the
-// end of training.
+// (the leaves to expand, their row ranges and splits) from descriptors that
+// the previous scan kernel's planning block wrote, so the host enqueues a
+// tree without reading anything back except a done flag between groups of
+// launches. The host downloads the finished trees once, at the end of
+// training.
 #pragma once
 
 #include <stdint.h>
@@ -15,36 +16,67 @@ constexpr int kObjL2 = 0;
 constexpr int kObjBinary = 1;
 constexpr int kObjMulticlass = 2;
 
-// One split of the leaf-wise growth loop. Written by the last block of the
-// split kernel (the "pick"), read by the partition, histogram and split
-// kernels of the next step.
-struct Step {
-    int32_t active;        // 0: the tree is finished, every kernel returns
-    int32_t parent_slot;   // frontier slot being split; the left child keeps it
-    int32_t new_slot;      // frontier slot of the right child (= leaves so far)
-    int32_t feature;
-    int32_t bin;           // inclusive left threshold
-    int32_t default_left;  // direction of the feature's missing bin
-    int32_t missing_bin;   // -1: none
-    int32_t src_buf;       // row buffer holding the parent's range
-    int64_t begin, end;    // parent's range in the row buffers
-    int64_t n_left;        // rows routed left, from the parent's histogram
-    int32_t builds_left;   // the smaller child (left on ties) is built
-    int32_t parent_hist;   // histogram buffer of the parent (sibling lands here)
-    int32_t child_hist;    // histogram buffer the built child accumulates into
-    int32_t depth;         // parent depth
-    int32_t parent_node;
-    int32_t node_left, node_right;
+// Leaf-wise growth, batched. The reference grows a tree best-first: split the
+// frontier leaf of largest gain, score both children, repeat. A leaf's best
+// split depends only on its own rows and depth, so the tree it produces is
+// fixed by the set of leaves' best splits alone; the order only decides which
+// splits make the num_leaves cut and how nodes are numbered. Here several
+// frontier leaves are expanded per launch (the highest-gain ones, some of
+// them speculatively), and a single-block replay of the best-first order over
+// the expanded leaves commits splits in the reference's order, assigning its
+// node ids and frontier slots. Expansions the replay never reaches are
+// discarded; the tree is the reference's.
+
+// A node of the explored tree (every leaf ever created in this tree).
+struct ENode {
+    int64_t begin, end;          // row range in row buffer `buf`
+    int64_t n_left;              // rows on the left side of the best split
+    int64_t tot_g, tot_h, tot_c; // integer sums of the node's rows
+    double gain;                 // best split gain (valid when found)
+    double value;                // leaf output
+    int32_t buf, hist, depth;
+    int32_t found, feature, bin, default_left;
+    int32_t left_e, right_e;     // explored children, -1 until expanded
     int32_t pad_;
-    double gain;
 };
 
-// One leaf of the frontier.
-struct Slot {
-    int64_t begin, end;
-    int32_t node, buf, hist, depth;
-    int32_t found, feature, bin, default_left;
-    double gain;
+// One leaf expanded by a launch of the partition+histogram and scan kernels.
+struct Item {
+    int64_t begin, end;     // the parent's range in row buffer src_buf
+    int64_t n_left;         // rows routed left (exact, from the parent's scan)
+    int32_t parent_e, left_e;   // right child = left_e + 1
+    int32_t src_buf;        // children land in the other buffer, same range
+    int32_t builds_left;    // the smaller child (left on ties) is accumulated
+    int32_t hist_built;     // histogram buffer of the accumulated child (new)
+    int32_t hist_sib;       // the parent's buffer; the sibling is written over it
+    int32_t depth_child;
+    int32_t part_off, part_cnt;  // block partials of the accumulated child
+    int32_t pad_;
+};
+
+// Work of one partition+histogram block: a chunk [c0, c1) of an item's
+// parent range (offsets relative to begin).
+struct PbDesc {
+    int64_t begin, n_left, m, c0, c1;
+    int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left, pad_;
+};
+
+struct Batch {
+    int32_t n_items;   // 0: nothing to do this iteration
+    int32_t n_blocks;  // partition+histogram blocks in use
+    int32_t done;      // the tree is complete (read by the host between launches)
+    int32_t root;      // the scan kernel's item 0 is the root build
+};
+
+// Replay state of the best-first order (touched by the planning block only).
+struct Grow {
+    int32_t n_leaves, n_nodes;  // of the committed (reference) tree
+    int32_t n_explored;         // ENode entries in use
+    int32_t n_hist;             // histogram buffers in use
+    int32_t expansions;
+    int32_t iterations;
+    int64_t rows_built;         // rows accumulated by this tree's expansions
+    int64_t rows_parted;        // parent rows routed by this tree's expansions
 };
 
 // Best candidate of one (child, feature) scan.
@@ -52,6 +84,7 @@ struct ScanResult {
     double gain;
     int32_t bin, default_left, found, pad_;
     int64_t tot_g, tot_h, tot_c;
+    int64_t n_left;  // rows left of the candidate
 };
 
 // Per-round values shared by the kernels of one tree, advanced on the device
@@ -106,19 +139,31 @@ struct DevState {
     Round *round;
     // rows and histograms
     int32_t *rows0, *rows1;
-    int32_t *hist;         // num_leaves x F x n_bins x 3 (grad, hess, count)
-    unsigned long long *part;  // hist_grid x F x n_bins packed per-block partials
+    int32_t *hist;         // (1 + max_exp) x F x n_bins x 3 (grad, hess, count)
+    unsigned long long *part;  // max(hist_grid, pb_grid) x F x part_stride packed partials
     int32_t hist_grid;         // blocks of a histogram launch
     int32_t part_stride;       // per-feature stride of a partial (even, >= n_bins)
     int64_t hist_chunk_min;    // fewest rows a histogram block takes
     int64_t hist_chunk_limit;  // most rows a block may pack (field bounds)
     // growth
-    Step *step;
-    Slot *slots;
-    ScanResult *scan;      // 2 x F
-    uint32_t *ticket;      // last-block counter of the split kernel
-    int64_t *cursor;       // [2]: partition output cursors
+    ENode *enodes;         // e_cap
+    double *e_gain;        // e_cap: best gain when > 0 and found, else -1 (planner's view)
+    int32_t *e_left;       // e_cap: left child (right = left + 1), -1 while unexpanded
+    Item *items;           // kmax
+    PbDesc *pb_desc;       // pb_grid
+    Batch *batch;
+    Grow *grow;
+    int32_t *slot_e;       // num_leaves: explored node of each frontier slot
+    int32_t *slot_fid;     // num_leaves: its node id in the committed tree
+    ScanResult *scan;      // kmax x 2 x F
+    int64_t *cursor;       // [0] root bag size; [2 + 2j], [3 + 2j]: item j's output cursors
     int32_t *error;        // sticky error flag (partition overflow)
+    int32_t kmax;          // most leaves expanded per launch
+    int32_t max_exp;       // most expansions per tree (2 num_leaves - 1)
+    int32_t e_cap;         // ENode capacity (1 + 2 max_exp)
+    int32_t pb_grid;       // blocks of a partition+histogram launch
+    int32_t scan_grid;     // blocks of a scan launch
+    int32_t pad2_;
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;
@@ -126,7 +171,7 @@ struct DevState {
     // archive of finished trees (downloaded at the end)
     int32_t *arc_int;      // per tree: max_nodes x 6 ints + 2 meta
     double *arc_dbl;       // per tree: max_nodes x 3 doubles
-    int64_t *arc_rows;     // per tree: rows of every histogram build (max num_leaves)
+    int64_t *arc_aux;      // per tree: rows accumulated, iterations, expansions, 0
     int32_t max_nodes;
     HyperParams hp;
 };

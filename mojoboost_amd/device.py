@@ -117,14 +117,14 @@ class Fit:
                          ptr(self.threshold), ptr(self.left), ptr(self.right), ptr(self.value),
                          ptr(self.default_left), ptr(self.missing_bin), ptr(self.gain),
                          ptr(self.count))
-        st = np.zeros(10)
-        L.mbh_fit_stats(handle, ptr(st))
-        self.stats = {
-            "train_seconds": st[0], "hist_ms": st[1], "hist_bytes": st[2],
-            "hist_rows_features": st[3], "hist_builds": st[4], "root_bytes": st[5],
-            "root_ms": st[6], "trees_grown": st[7], "hist_merged_ms": st[8],
-            "root_merged_ms": st[9],
-        }
+        names = ("train_seconds", "hist_ms", "hist_bytes", "hist_rows_features",
+                 "hist_builds", "root_bytes", "root_ms", "trees_grown", "growth_ms",
+                 "root_growth_ms", "iterations", "expansions", "rows_built", "rows_parted",
+                 "expand_launches", "expand_ms", "expand_bytes")
+        st = np.zeros(len(names))
+        count = L.mbh_fit_stats(handle, ptr(st), len(names))
+        assert count == len(names), count
+        self.stats = dict(zip(names, (float(v) for v in st)))
 
     def tree(self, t):
         a, b = self.off[t], self.off[t + 1]
