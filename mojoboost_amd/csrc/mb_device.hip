@@ -3,12 +3,13 @@
 // of include/mojoboost_hip.h.
 //
 // A round enqueues, per tree: objective, quantize, root histogram, root scan
-// (which plans the first batch), then groups of kIterChunk x [partition +
-// histogram, scan] until the device reports the tree done, then the score
-// update and round end. The host reads back only the done flag, one group
-// behind: it enqueues group k + 1 before waiting for group k's flag, so the
-// device does not idle while the host decides; launches after the tree is
-// done find an empty batch and return at once.
+// and plan (which plans the first batch), then groups of [partition +
+// histogram, scan, plan] iterations until the device reports the tree done,
+// then the score update and round end. The host reads back only the batch
+// header (done flag, iteration count), one group behind: it enqueues group
+// k + 1 before waiting for group k's header, so the device does not idle
+// while the host decides; launches after the tree is done find an empty
+// batch and return at once.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -138,7 +139,7 @@ struct Run {
 };
 
 struct PinnedFlags {
-    int32_t *p = nullptr;
+    mb::Batch *p = nullptr;
     ~PinnedFlags() {
         if (p) (void)hipHostFree(p);
     }
@@ -149,8 +150,13 @@ constexpr size_t kPbListBytes = 4096 * 4;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
 // trees reaches the tree's depth in iterations with 32).
 constexpr int kMaxBatch = 32;
-// [partition + histogram, scan] pairs enqueued between done-flag reads.
-constexpr int kIterChunk = 4;
+// Expansion iterations ([partition + histogram, scan, plan]) per group of
+// launches between done-flag reads: the first group of a tree is as long as
+// the previous tree needed (kFirstGroup for the first tree), later ones
+// kNextGroup.
+constexpr int kFirstGroup = 8;
+constexpr int kNextGroup = 2;
+constexpr int kMaxGroup = 64;
 
 int64_t chunk_limit_for(int B) {
     // rows per LDS accumulation so no packed field overflows:
@@ -211,6 +217,7 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
     s.kmax = kMaxBatch;
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + kMaxBatch);
     s.scan_grid = std::min(kMaxBatch * ds->F, 4 * ds->n_cu);
+    s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);
     const int64_t parts = std::max<int64_t>(grid, s.pb_grid);
     s.part = dalloc<unsigned long long>((size_t)parts * ds->F * s.part_stride, run.owned);
     s.pb_desc = dalloc<mb::PbDesc>(s.pb_grid, run.owned);
@@ -274,6 +281,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.scan = dalloc<mb::ScanResult>((size_t)s.kmax * 2 * F, run.owned);
     s.e_gain = dalloc<double>(s.e_cap, run.owned);
     s.e_left = dalloc<int32_t>(s.e_cap, run.owned);
+    s.e_parent = dalloc<int32_t>(s.e_cap, run.owned);
     s.cursor = dalloc<int64_t>(2 + 2 * (size_t)s.kmax, run.owned);
     s.error = dalloc<int32_t>(1, run.owned);
     s.t_feature = dalloc<int32_t>(max_nodes, run.owned);
@@ -475,20 +483,20 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         const int T = p->num_iterations * K;
         const bool timed = p->time_histograms != 0;
         hipStream_t st = nullptr;
-        PinnedFlags done_flags;
-        HIPX(hipHostMalloc((void **)&done_flags.p, 2 * sizeof(int32_t), hipHostMallocDefault));
-        // events: [0..1] done-flag markers of the two in-flight groups; when
-        // timed, [2..4] the root build and per group slot kIterChunk x 3
-        // (before the expansion, after it, after the scan)
-        const int n_ev = 2 + (timed ? 3 + 2 * kIterChunk * 3 : 0);
+        PinnedFlags flags;
+        HIPX(hipHostMalloc((void **)&flags.p, 2 * sizeof(mb::Batch), hipHostMallocDefault));
+        // events: [0..1] flag markers of the two in-flight groups; when
+        // timed, [2..4] the root build and per group slot kMaxGroup x 3
+        // (before the expansion, after it, after scan + plan)
+        const int n_ev = 2 + (timed ? 3 + 2 * kMaxGroup * 3 : 0);
         events.resize(n_ev);
         for (int i = 0; i < n_ev; ++i)
             HIPX(hipEventCreateWithFlags(&events[i], i < 2 ? hipEventDisableTiming : hipEventDefault));
-        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kIterChunk + c) * 3 + k]; };
+        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kMaxGroup + c) * 3 + k]; };
         double t_acc = 0.0, t_root = 0.0, t_root_scan = 0.0, t_pb = 0.0, t_scan = 0.0;
         double pb_launches = 0.0;
-        auto add_group = [&](int slot) {
-            for (int c = 0; c < kIterChunk; ++c) {
+        auto add_group = [&](int slot, int n) {
+            for (int c = 0; c < n; ++c) {
                 float a = 0.f, b = 0.f;
                 HIPX(hipEventElapsedTime(&a, ev_group(slot, c, 0), ev_group(slot, c, 1)));
                 HIPX(hipEventElapsedTime(&b, ev_group(slot, c, 1), ev_group(slot, c, 2)));
@@ -496,6 +504,9 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 t_scan += b;
             }
         };
+        // expansion launches the previous tree needed: the first group of a
+        // tree is that long, later groups kNextGroup
+        int est = kFirstGroup;
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
             HIPX(mb::launch_objective(s, grid_rows, st));
@@ -507,9 +518,12 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             HIPX(mb::launch_plan(s, 1, st));
             if (timed) HIPX(hipEventRecord(events[4], st));
             int iters = 0;
+            int group_size[2] = {0, 0};
             for (int k = 0;; ++k) {
                 const int slot = k & 1;
-                for (int c = 0; c < kIterChunk; ++c) {
+                const int n = k == 0 ? std::max(1, std::min(est, kMaxGroup)) : kNextGroup;
+                group_size[slot] = n;
+                for (int c = 0; c < n; ++c) {
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 0), st));
                     HIPX(mb::launch_part_hist(s, st));
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 1), st));
@@ -517,24 +531,24 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                     HIPX(mb::launch_plan(s, 0, st));
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 2), st));
                 }
-                pb_launches += kIterChunk;
-                iters += kIterChunk;
-                HIPX(hipMemcpyAsync(&done_flags.p[slot], &s.batch->done, sizeof(int32_t),
-                                    hipMemcpyDeviceToHost, st));
+                pb_launches += n;
+                iters += n;
+                HIPX(hipMemcpyAsync(&flags.p[slot], s.batch, sizeof(mb::Batch), hipMemcpyDeviceToHost, st));
                 HIPX(hipEventRecord(events[slot], st));
                 if (k == 0) continue;
                 HIPX(hipEventSynchronize(events[1 - slot]));
-                if (timed) add_group(1 - slot);
-                if (done_flags.p[1 - slot]) {
+                if (timed) add_group(1 - slot, group_size[1 - slot]);
+                if (flags.p[1 - slot].done) {
+                    est = flags.p[1 - slot].iters;
                     if (timed) {
                         HIPX(hipEventSynchronize(events[slot]));
-                        add_group(slot);
+                        add_group(slot, n);
                     }
                     break;
                 }
                 // every iteration commits at least one split once the first
                 // batch is planned, so a tree ends within num_leaves + 1
-                if (iters > L + 2 * kIterChunk + 2)
+                if (iters > L + kMaxGroup + 2)
                     throw Error{MOJOTREES_ERROR_TRAINING, "tree growth did not finish (internal error)"};
             }
             if (timed) {

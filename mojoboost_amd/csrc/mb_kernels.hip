@@ -72,18 +72,54 @@ __device__ __forceinline__ long long wave_incl_scan(long long v) {
     return v;
 }
 
-// (gain, order) argmax across the wave: larger gain wins, equal gains go to
-// the smaller order, so the result is the first maximum in scan order.
+// Cross-lane moves through DPP (data-parallel primitives): a VALU operand
+// modifier, so a reduction step costs a few cycles instead of an LDS
+// crossbar round trip. Lanes a control does not cover keep their own value,
+// which every reduction below treats as its identity.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned dpp_u32(unsigned x) {
+    return (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Max / min of a 32-bit value over the 64 lanes (every lane active),
+// returned wave-uniform: quad swaps, half-row and row mirrors fold each row
+// of 16 lanes, then row broadcasts 15 and 31 fold the rows into lane 63.
+__device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
+    x = max(x, dpp_u32<0xB1, 0xF>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp_u32<0x4E, 0xF>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp_u32<0x141, 0xF>(x));  // row_half_mirror
+    x = max(x, dpp_u32<0x140, 0xF>(x));  // row_mirror
+    x = max(x, dpp_u32<0x142, 0xA>(x));  // row_bcast:15 into rows 1, 3
+    x = max(x, dpp_u32<0x143, 0xC>(x));  // row_bcast:31 into rows 2, 3
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+__device__ __forceinline__ unsigned wave_min_u32(unsigned x) {
+    x = min(x, dpp_u32<0xB1, 0xF>(x));
+    x = min(x, dpp_u32<0x4E, 0xF>(x));
+    x = min(x, dpp_u32<0x141, 0xF>(x));
+    x = min(x, dpp_u32<0x140, 0xF>(x));
+    x = min(x, dpp_u32<0x142, 0xA>(x));
+    x = min(x, dpp_u32<0x143, 0xC>(x));
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// (gain, order) argmax across the wave, result on every lane: larger gain
+// wins, equal gains go to the smaller order, so the result is the first
+// maximum in scan order. Gains must be >= 0 (a lane with nothing to offer
+// holds 0.0); non-negative binary64 values order like their bit patterns,
+// so the maximum is found on the high word, then the low word among lanes
+// tied on it, then the smallest order among lanes holding the maximum.
+// Orders are non-negative.
 __device__ __forceinline__ void wave_argmax(double &gain, int &order) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        double og = __shfl_xor(gain, d, 64);
-        int oo = __shfl_xor(order, d, 64);
-        if (og > gain || (og == gain && oo < order)) {
-            gain = og;
-            order = oo;
-        }
-    }
+    const unsigned long long bits = gain > 0.0 ? (unsigned long long)__double_as_longlong(gain) : 0ULL;
+    const unsigned hi = (unsigned)(bits >> 32), lo = (unsigned)bits;
+    const unsigned mhi = wave_max_u32(hi);
+    const unsigned mlo = wave_max_u32(hi == mhi ? lo : 0u);
+    const bool top = hi == mhi && lo == mlo;
+    const unsigned mord = wave_min_u32(top ? (unsigned)order : 0xFFFFFFFFu);
+    gain = __longlong_as_double((long long)(((unsigned long long)mhi << 32) | mlo));
+    order = (int)mord;
 }
 
 __device__ __forceinline__ bool in_bag(const HyperParams &hp, uint64_t bag_stream, int64_t r) {
@@ -341,17 +377,8 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     __shared__ long long off_l[kPbUnroll * 16], off_r[kPbUnroll * 16], off_b[kPbUnroll * 16];
     __shared__ int s_nbuilt;
     const int n_blocks = s.batch->n_blocks;
-    const PbDesc d = s.pb_desc[blockIdx.x];  // in bounds: the grid is pb_grid
-    if ((int)blockIdx.x >= n_blocks) return;
     const int F = s.n_features, ls = s.lds_stride;
     int32_t *list = (int32_t *)(lds + (size_t)F * ls);
-    for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
-    const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
-    int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
-    const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
-    const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
-    const bool bl = d.builds_left != 0;
-    unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item];
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const unsigned long long below = (1ULL << lane) - 1ULL;
     const int sub = threadIdx.x % LPR;
@@ -359,86 +386,99 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     const int rpp = kPbThreads / LPR;
     const int src_lane = (lane / LPR) * LPR + (LPR - 1);
     const uint4 *rec = (const uint4 *)s.records;
-    for (int64_t t0 = d.c0; t0 < d.c1; t0 += kPbTile) {
-        int32_t r[kPbUnroll];
-        bool left[kPbUnroll], valid[kPbUnroll];
-        unsigned long long lm[kPbUnroll], rm[kPbUnroll];
+    // a block takes descriptors blockIdx.x, + gridDim.x, ...; each one is a
+    // whole accumulation (zeroed LDS, stored partial)
+    for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const PbDesc d = s.pb_desc[blk];
+        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
+        const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
+        int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
+        const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
+        const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
+        const bool bl = d.builds_left != 0;
+        unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item];
+        for (int64_t t0 = d.c0; t0 < d.c1; t0 += kPbTile) {
+            int32_t r[kPbUnroll];
+            bool left[kPbUnroll], valid[kPbUnroll];
+            unsigned long long lm[kPbUnroll], rm[kPbUnroll];
 #pragma unroll
-        for (int u = 0; u < kPbUnroll; ++u) {
-            const int64_t i = t0 + (int64_t)u * kPbThreads + threadIdx.x;
-            valid[u] = i < d.c1;
-            r[u] = valid[u] ? src[i] : 0;
-            if ((uint32_t)r[u] >= (uint64_t)s.n) r[u] = 0;  // never taken: ids come from the row lists
-        }
-#pragma unroll
-        for (int u = 0; u < kPbUnroll; ++u) {
-            const int b = valid[u] ? (int)col[r[u]] : 0;
-            left[u] = (b == mb) ? (dl != 0) : (b <= thr);
-            lm[u] = __ballot(valid[u] && left[u]);
-            rm[u] = __ballot(valid[u] && !left[u]);
-            if (lane == 0) {
-                cnt_l[u * 16 + w] = __popcll(lm[u]);
-                cnt_r[u * 16 + w] = __popcll(rm[u]);
+            for (int u = 0; u < kPbUnroll; ++u) {
+                const int64_t i = t0 + (int64_t)u * kPbThreads + threadIdx.x;
+                valid[u] = i < d.c1;
+                r[u] = valid[u] ? src[i] : 0;
+                if ((uint32_t)r[u] >= (uint64_t)s.n) r[u] = 0;  // never taken: ids come from the row lists
             }
+#pragma unroll
+            for (int u = 0; u < kPbUnroll; ++u) {
+                const int b = valid[u] ? (int)col[r[u]] : 0;
+                left[u] = (b == mb) ? (dl != 0) : (b <= thr);
+                lm[u] = __ballot(valid[u] && left[u]);
+                rm[u] = __ballot(valid[u] && !left[u]);
+                if (lane == 0) {
+                    cnt_l[u * 16 + w] = __popcll(lm[u]);
+                    cnt_r[u * 16 + w] = __popcll(rm[u]);
+                }
+            }
+            __syncthreads();
+            if (w == 0) {
+                // entry k = u * 16 + wave, in tile order
+                const long long vl = cnt_l[lane], vr = cnt_r[lane];
+                const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
+                const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
+                long long bl_base = 0, br_base = 0;
+                if (lane == 0) {
+                    bl_base = tl ? (long long)atomicAdd(&cur[0], (unsigned long long)tl) : 0;
+                    br_base = tr ? (long long)atomicAdd(&cur[1], (unsigned long long)tr) : 0;
+                }
+                bl_base = __shfl(bl_base, 0, 64);
+                br_base = __shfl(br_base, 0, 64);
+                off_l[lane] = bl_base + il - vl;
+                off_r[lane] = br_base + ir - vr;
+                off_b[lane] = bl ? il - vl : ir - vr;
+                if (lane == 0) s_nbuilt = (int)(bl ? tl : tr);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < kPbUnroll; ++u) {
+                if (!valid[u]) continue;
+                const int k = u * 16 + w;
+                long long rank;
+                if (left[u]) {
+                    rank = __popcll(lm[u] & below);
+                    const long long p = off_l[k] + rank;
+                    if (p < d.n_left) dst[p] = r[u];
+                    else atomicOr(s.error, 1);
+                } else {
+                    rank = __popcll(rm[u] & below);
+                    const long long p = d.n_left + off_r[k] + rank;
+                    if (p < d.m) dst[p] = r[u];
+                    else atomicOr(s.error, 1);
+                }
+                if (left[u] == bl) list[off_b[k] + rank] = r[u];
+            }
+            __syncthreads();
+            const int nbt = s_nbuilt;
+            for (int k0 = 0; k0 < nbt; k0 += kHistUnroll * rpp) {
+                uint4 v[kHistUnroll];
+                bool ok[kHistUnroll];
+#pragma unroll
+                for (int u = 0; u < kHistUnroll; ++u) {
+                    const int k = k0 + u * rpp + rr;
+                    ok[u] = k < nbt;
+                    v[u] = ok[u] ? rec[(int64_t)list[k] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
+                }
+#pragma unroll
+                for (int u = 0; u < kHistUnroll; ++u) {
+                    const uint32_t gh = __shfl(v[u].w, src_lane, 64);
+                    if (ok[u]) lds_accumulate(lds, v[u], sub, F, ls, pack_gh(gh));
+                }
+            }
+            __syncthreads();
         }
         __syncthreads();
-        if (w == 0) {
-            // entry k = u * 16 + wave, in tile order
-            const long long vl = cnt_l[lane], vr = cnt_r[lane];
-            const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
-            const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
-            long long bl_base = 0, br_base = 0;
-            if (lane == 0) {
-                bl_base = tl ? (long long)atomicAdd(&cur[0], (unsigned long long)tl) : 0;
-                br_base = tr ? (long long)atomicAdd(&cur[1], (unsigned long long)tr) : 0;
-            }
-            bl_base = __shfl(bl_base, 0, 64);
-            br_base = __shfl(br_base, 0, 64);
-            off_l[lane] = bl_base + il - vl;
-            off_r[lane] = br_base + ir - vr;
-            off_b[lane] = bl ? il - vl : ir - vr;
-            if (lane == 0) s_nbuilt = (int)(bl ? tl : tr);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < kPbUnroll; ++u) {
-            if (!valid[u]) continue;
-            const int k = u * 16 + w;
-            long long rank;
-            if (left[u]) {
-                rank = __popcll(lm[u] & below);
-                const long long p = off_l[k] + rank;
-                if (p < d.n_left) dst[p] = r[u];
-                else atomicOr(s.error, 1);
-            } else {
-                rank = __popcll(rm[u] & below);
-                const long long p = d.n_left + off_r[k] + rank;
-                if (p < d.m) dst[p] = r[u];
-                else atomicOr(s.error, 1);
-            }
-            if (left[u] == bl) list[off_b[k] + rank] = r[u];
-        }
-        __syncthreads();
-        const int nbt = s_nbuilt;
-        for (int k0 = 0; k0 < nbt; k0 += kHistUnroll * rpp) {
-            uint4 v[kHistUnroll];
-            bool ok[kHistUnroll];
-#pragma unroll
-            for (int u = 0; u < kHistUnroll; ++u) {
-                const int k = k0 + u * rpp + rr;
-                ok[u] = k < nbt;
-                v[u] = ok[u] ? rec[(int64_t)list[k] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
-            }
-#pragma unroll
-            for (int u = 0; u < kHistUnroll; ++u) {
-                const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                if (ok[u]) lds_accumulate(lds, v[u], sub, F, ls, pack_gh(gh));
-            }
-        }
-        __syncthreads();
+        store_partial(s, lds, blk);
+        __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
     }
-    __syncthreads();
-    store_partial(s, lds, blockIdx.x);
 }
 
 // ------------------------------------------------------------------- scan
@@ -716,7 +756,7 @@ constexpr int kPlanThreads = 1024;
 // LDS layout of the planner (byte offsets), shared by the host's size query
 // and the kernel.
 struct PlanLayout {
-    size_t fg, wg, eg, sg, wf, el, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
+    size_t fg, wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
     size_t total;
 };
 
@@ -733,8 +773,12 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
     p.wg = take((size_t)8 * 2 * K, 8);       // pair's best gain
     p.eg = take((size_t)8 * E, 8);           // explored node's gain view
     p.sg = take((size_t)8 * L, 8);           // frontier slot's gain
+    p.cb = take((size_t)8 * E, 8);           // candidates' bottleneck values
     p.wf = take((size_t)4 * 2 * K, 4);       // pair's best feature
     p.el = take((size_t)4 * E, 4);           // explored node's left child
+    p.ep = take((size_t)4 * E, 4);           // explored node's parent
+    p.fr = take((size_t)4 * E, 4);           // in the committed frontier
+    p.ci = take((size_t)4 * E, 4);           // candidates' node ids
     p.sl_e = take((size_t)4 * L, 4);
     p.sl_fid = take((size_t)4 * L, 4);
     p.cm_e = take((size_t)4 * L, 4);
@@ -749,8 +793,8 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
 }
 
 struct PlanView {
-    double *fg, *wg, *eg, *sg;
-    int32_t *wf, *el, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff;
+    double *fg, *wg, *eg, *sg, *cb;
+    int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff;
     Item *it;
 };
 
@@ -761,8 +805,12 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.wg = (double *)(smem + p.wg);
     v.eg = (double *)(smem + p.eg);
     v.sg = (double *)(smem + p.sg);
+    v.cb = (double *)(smem + p.cb);
     v.wf = (int32_t *)(smem + p.wf);
     v.el = (int32_t *)(smem + p.el);
+    v.ep = (int32_t *)(smem + p.ep);
+    v.fr = (int32_t *)(smem + p.fr);
+    v.ci = (int32_t *)(smem + p.ci);
     v.sl_e = (int32_t *)(smem + p.sl_e);
     v.sl_fid = (int32_t *)(smem + p.sl_fid);
     v.cm_e = (int32_t *)(smem + p.cm_e);
@@ -778,7 +826,7 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
 __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode) {
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
-    __shared__ int s_nc, s_done, s_ncand, s_total, s_x;
+    __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x;
     __shared__ unsigned long long s_rows_built, s_rows_parted;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
@@ -819,6 +867,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     for (int i = tid; i < ne; i += nthr) {
         v.eg[i] = s.e_gain[i];
         v.el[i] = s.e_left[i];
+        v.ep[i] = s.e_parent[i];
     }
     if (!root_mode)
         for (int i = tid; i < nl0; i += nthr) {
@@ -890,7 +939,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.e_gain[e_id] = eg;
         if (root_mode) {
             v.el[0] = -1;
+            v.ep[0] = -1;
             s.e_left[0] = -1;
+            s.e_parent[0] = -1;
         }
     }
     if (root_mode && tid == 0) {
@@ -990,7 +1041,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.n_items = 0;
             b.n_blocks = 0;
             b.done = 1;
-            b.root = 0;
+            b.iters = g.iterations;
             *s.batch = b;
         }
     };
@@ -1014,61 +1065,87 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.slot_fid[i] = v.sl_fid[i];
     }
     __syncthreads();
-    // ---- 3. selection: continue best-first over the explored tree as if
-    // every leaf already expanded were committed; a pick that is not
-    // expanded joins the batch and counts as a split. The first pick is the
-    // leaf the replay waits for.
+    // ---- 3. selection. Best-first over a tree pops nodes in non-increasing
+    // order of their bottleneck value b(v) = the smallest gain on the path
+    // from the committed frontier down to v; continuing the replay as if
+    // every expanded leaf were committed therefore visits the explored nodes
+    // of largest b first. A visited node that is not expanded joins the
+    // batch. The visit stops after num_leaves - n_leaves splits (each visit
+    // adds one leaf) or when the batch holds `cap` leaves. Ties are broken
+    // by node index; the selection only steers speed, never the tree.
     const int r = L - nl;
     int cap = r < s.kmax ? r : s.kmax;
     const int room = (s.max_exp - g.expansions) - (r - 1);
     if (room < cap) cap = room;
-    if (tid < 64) {
-        double lbg = 0.0;
-        int lbi = 0x7FFFFFFF;
-        auto own_best = [&](int nslots) {
-            lbg = 0.0;
-            lbi = 0x7FFFFFFF;
-            for (int i = lane; i < nslots; i += 64) {
-                const double gi = v.sg[i];
-                if (gi > lbg) {
-                    lbg = gi;
-                    lbi = i;
+    for (int i = tid; i < ne; i += nthr) v.fr[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < nl; i += nthr) v.fr[v.sl_e[i]] = 1;
+    __syncthreads();
+    for (int i = tid; i < ne; i += nthr) {
+        double b = -1.0;  // outside the region below the frontier, or no split
+        if (v.eg[i] > 0.0) {
+            double m = v.eg[i];
+            int u = i;
+            bool inside = true;
+            while (!v.fr[u]) {
+                u = v.ep[u];
+                if (u < 0) {
+                    inside = false;  // a committed internal node
+                    break;
                 }
+                m = v.eg[u] < m ? v.eg[u] : m;
             }
-        };
-        int nslots = nl, nsim = nl, nsel = 0;
-        own_best(nslots);
-        while (nsim < L && nsel < cap) {
-            double bg = lbg;
-            int bi = lbi;
-            wave_argmax(bg, bi);
-            if (bi == 0x7FFFFFFF) break;
-            const int Y = v.sl_e[bi];
-            const int le = v.el[Y];
-            if (le < 0) {
-                v.sel_e[nsel] = Y;
-                ++nsel;
-                v.sg[bi] = -1.0;
-                if (lane == (bi & 63)) own_best(nslots);
-            } else {
-                v.sl_e[bi] = le;
-                v.sg[bi] = v.eg[le];
-                v.sl_e[nslots] = le + 1;
-                v.sg[nslots] = v.eg[le + 1];
-                if (lane == (bi & 63) || lane == (nslots & 63)) own_best(nslots + 1);
-                ++nslots;
-            }
-            ++nsim;
+            if (inside) b = m;
         }
-        if (lane == 0) s_ncand = nsel;
+        if (b > 0.0) {
+            // node id, with bit 31 set when the node is expanded
+            const int k = atomicAdd(&s_ncand, 1);
+            v.cb[k] = b;
+            v.ci[k] = i | (v.el[i] >= 0 ? (int)0x80000000 : 0);
+        }
     }
     __syncthreads();
-    const int nsel = s_ncand;
+    const int ncand = s_ncand;
+    if (tid == 0) s_nsel = 0;
+    __syncthreads();
+    for (int k = tid; k < ncand; k += nthr) {
+        const double bk = v.cb[k];
+        const int ck = v.ci[k];
+        if (ck < 0) continue;  // expanded: visited, not selected
+        int rank_all = 0, rank_pend = 0;
+#pragma unroll 8
+        for (int q = 0; q < ncand; ++q) {
+            const double bq = v.cb[q];
+            const int cq = v.ci[q];
+            const int iq = cq & 0x7FFFFFFF;
+            const int before = (bq > bk || (bq == bk && iq < ck)) ? 1 : 0;
+            rank_all += before;
+            rank_pend += before & (cq >= 0 ? 1 : 0);
+        }
+        if (rank_all < r && rank_pend < cap) {
+            v.sel_e[rank_pend] = ck;
+            atomicAdd(&s_nsel, 1);
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // the leaf the replay waits for is always in the batch
+        int n = s_nsel;
+        bool has = false;
+        for (int jj = 0; jj < n; ++jj) has |= v.sel_e[jj] == s_x;
+        if (!has && cap > 0) {
+            if (n < cap) ++n;
+            v.sel_e[n - 1] = s_x;
+        }
+        s_nsel = n;
+    }
+    __syncthreads();
+    const int nsel = s_nsel;
     {
         // unreachable while the expansion budget holds; each check has its
         // own code in the sticky error word
-        const int bad = (cap <= 0 ? 8 : 0) | (nsel <= 0 ? 16 : 0) | (v.sel_e[0] != s_x ? 32 : 0) |
-                        (ne + 2 * nsel > s.e_cap ? 64 : 0) | (g.n_hist + nsel > 1 + s.max_exp ? 128 : 0);
+        const int bad = (cap <= 0 ? 8 : 0) | (nsel <= 0 ? 16 : 0) | (ne + 2 * nsel > s.e_cap ? 64 : 0) |
+                        (g.n_hist + nsel > 1 + s.max_exp ? 128 : 0);
         if (bad) {
             finish(bad);
             return;
@@ -1149,6 +1226,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.e_gain[le + 1] = -1.0;
         s.e_left[le] = -1;
         s.e_left[le + 1] = -1;
+        s.e_parent[le] = Xs;
+        s.e_parent[le + 1] = Xs;
         e->left_e = le;
         e->right_e = le + 1;
         s.e_left[Xs] = le;
@@ -1201,7 +1280,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         b.n_items = nsel;
         b.n_blocks = total;
         b.done = 0;
-        b.root = 0;
+        b.iters = g.iterations;
         *s.batch = b;
     }
 }
@@ -1369,7 +1448,7 @@ hipError_t launch_hist(const DevState &s, hipStream_t st) {
 }
 hipError_t launch_part_hist(const DevState &s, hipStream_t st) {
     const size_t lds = pb_lds_bytes(s);
-    const dim3 grid(s.pb_grid), block(kPbThreads);
+    const dim3 grid(s.pb_launch), block(kPbThreads);
     switch (s.rec_bytes / 16) {
     case 1: hipLaunchKernelGGL(k_part_hist<1>, grid, block, lds, st, s); break;
     case 2: hipLaunchKernelGGL(k_part_hist<2>, grid, block, lds, st, s); break;

@@ -61,11 +61,12 @@ struct PbDesc {
     int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left, pad_;
 };
 
+// Written by the planner; the host reads it back between launch groups.
 struct Batch {
     int32_t n_items;   // 0: nothing to do this iteration
-    int32_t n_blocks;  // partition+histogram blocks in use
-    int32_t done;      // the tree is complete (read by the host between launches)
-    int32_t root;      // the scan kernel's item 0 is the root build
+    int32_t n_blocks;  // partition+histogram descriptors in use
+    int32_t done;      // the tree is complete
+    int32_t iters;     // expansion iterations planned so far in this tree
 };
 
 // Replay state of the best-first order (touched by the planning block only).
@@ -149,6 +150,7 @@ struct DevState {
     ENode *enodes;         // e_cap
     double *e_gain;        // e_cap: best gain when > 0 and found, else -1 (planner's view)
     int32_t *e_left;       // e_cap: left child (right = left + 1), -1 while unexpanded
+    int32_t *e_parent;     // e_cap: parent, -1 for the root
     Item *items;           // kmax
     PbDesc *pb_desc;       // pb_grid
     Batch *batch;
@@ -161,9 +163,9 @@ struct DevState {
     int32_t kmax;          // most leaves expanded per launch
     int32_t max_exp;       // most expansions per tree (2 num_leaves - 1)
     int32_t e_cap;         // ENode capacity (1 + 2 max_exp)
-    int32_t pb_grid;       // blocks of a partition+histogram launch
+    int32_t pb_grid;       // most partition+histogram descriptors of a batch
     int32_t scan_grid;     // blocks of a scan launch
-    int32_t pad2_;
+    int32_t pb_launch;     // blocks of a partition+histogram launch (grid-strided)
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;
