@@ -203,7 +203,7 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
 // blocks with chunk = clamp(ceil(m / 256), chunk_min, chunk_limit); the
 // leaves of a batch are disjoint, so n / chunk_min + (batch size) blocks
 // always suffice.
-constexpr int64_t kHistChunkMin = 8192;
+constexpr int64_t kHistChunkMin = 4096;
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
     const int64_t limit = chunk_limit_for(B);
@@ -215,8 +215,8 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
     s.hist_chunk_min = std::min<int64_t>(kHistChunkMin, limit);
     s.hist_chunk_limit = limit;
     s.kmax = kMaxBatch;
-    s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + kMaxBatch);
-    s.scan_grid = std::min(kMaxBatch * ds->F, 4 * ds->n_cu);
+    s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
+    s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);
     const int64_t parts = std::max<int64_t>(grid, s.pb_grid);
     s.part = dalloc<unsigned long long>((size_t)parts * ds->F * s.part_stride, run.owned);
