@@ -66,6 +66,64 @@ def c2_data(n_rows, seed=0x5EED0002):
     return x, y
 
 
+def traffic_per_launch():
+    """HBM bytes per k_part_hist launch measured by rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE passes over the same workload, calibrated against a plain
+    device copy), as committed under profiles/; None when absent."""
+    p = ROOT / "profiles" / "k_part_hist_c2_traffic.json"
+    if not p.exists():
+        return None
+    return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+
+
+def rocprof_summary(path):
+    """Markdown table of a rocprofv3 CSV: per-kernel durations from a
+    *_kernel_stats.csv, or per-kernel mean counter values per dispatch from a
+    *_counter_collection.csv."""
+    import csv
+    import collections
+    rows = list(csv.DictReader(open(path)))
+    if rows and "AverageNs" in rows[0]:
+        print("| kernel | calls | total ms | avg us | min us | max us | % |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for r in rows:
+            print(f"| `{r['Name'][:60]}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
+                  f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                  f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+        return 0
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    for r in rows:
+        key = (r.get("Kernel_Name", "")[:60], r.get("Counter_Name", ""))
+        agg[key][0] += 1
+        agg[key][1] += float(r.get("Counter_Value", 0) or 0)
+    print("| kernel | counter | dispatches | mean per dispatch |")
+    print("|---|---|---:|---:|")
+    for (k, c), (n, sm) in sorted(agg.items(), key=lambda x: -x[1][1]):
+        print(f"| `{k}` | {c} | {n} | {sm / n:.1f} |")
+    return 0
+
+
+def copy_probe(mib):
+    """One hipMemcpy device-to-device of `mib` MiB: the runtime's blit kernel
+    reads and writes exactly that many bytes, which calibrates the HBM byte
+    counters (FETCH_SIZE, WRITE_SIZE) the histogram kernels are read with."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    n = mib << 20
+    a, b = C.c_void_p(), C.c_void_p()
+    for p in (a, b):
+        if hip.hipMalloc(C.byref(p), C.c_size_t(n)) != 0:
+            print(json.dumps({"error": "hipMalloc failed"}))
+            return 1
+    hip.hipMemset(a, 1, C.c_size_t(n))
+    rc = hip.hipMemcpy(b, a, C.c_size_t(n), 3)  # hipMemcpyDeviceToDevice
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"copy_probe_mib": mib, "rc": rc}))
+    return 0 if rc == 0 else 1
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,11 +132,22 @@ def main():
     ap.add_argument("--rows", type=int, default=10_500_000)
     ap.add_argument("--cpu-trees", type=int, default=6)
     ap.add_argument("--no-instrumented", action="store_true")
+    ap.add_argument("--rocprof-summary", default=None,
+                    help="only summarize a rocprofv3 CSV (kernel_stats or counter_collection) "
+                         "as a markdown table")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run one device-to-device copy of this many MiB (the "
+                         "calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU row sharding is a "
                           "design only (see DESIGN.md), --gpus must be 1"}))
         return 2
+
+    if args.rocprof_summary:
+        return rocprof_summary(args.rocprof_summary)
+    if args.copy_probe_mib > 0:
+        return copy_probe(args.copy_probe_mib)
 
     from mojoboost_amd import device
 
@@ -209,7 +278,7 @@ def main():
         "root_hist_merged_ms": round(root_merged_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "note": note},
+                     "traffic": traffic_per_launch(), "note": note},
         "cpu_baseline": cpu,
         "parity_first_trees_bit_exact": parity,
     }

@@ -827,7 +827,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
     __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x;
-    __shared__ unsigned long long s_rows_built, s_rows_parted;
+    __shared__ unsigned long long s_rows_built, s_rows_parted, s_rows_total;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
     const int L = s.hp.num_leaves, F = s.n_features;
@@ -1151,13 +1151,23 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             return;
         }
     }
-    // rows per block: at least hist_chunk_min, at most 256 blocks per leaf
+    // Rows per block, one value for the whole batch: the batch's rows spread
+    // over about pb_launch blocks (one wave of resident blocks), at least
+    // hist_chunk_min rows each. Fewer blocks mean fewer partials to store and
+    // merge; a batch never needs more than n / hist_chunk_min + nsel blocks.
+    if (tid == 0) s_rows_total = 0;
+    __syncthreads();
+    for (int jj = tid; jj < nsel; jj += nthr) {
+        const ENode *e = &s.enodes[v.sel_e[jj]];
+        atomicAdd(&s_rows_total, (unsigned long long)(e->end - e->begin));
+    }
+    __syncthreads();
+    int64_t chunk = ((int64_t)s_rows_total + s.pb_launch - 1) / s.pb_launch;
+    if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+    if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
     for (int jj = tid; jj < nsel; jj += nthr) {
         const ENode *e = &s.enodes[v.sel_e[jj]];
         const int64_t m = e->end - e->begin;
-        int64_t chunk = (m + 255) / 256;
-        if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
-        if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
         v.pcnt[jj] = (int)((m + chunk - 1) / chunk);
     }
     __syncthreads();
@@ -1248,9 +1258,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const Item &it = v.it[lo];
         const ENode &pe = s.enodes[it.parent_e];
         const int64_t m = it.end - it.begin;
-        int64_t chunk = (m + 255) / 256;
-        if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
-        if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
         PbDesc d;
         d.begin = it.begin;
         d.n_left = it.n_left;
