@@ -219,6 +219,9 @@ def main():
     root_gbs = algo_root / (root_mean_ms * 1e-3) / 1e9
     root_merged_gbs = algo_root / (root_merged_ms * 1e-3) / 1e9
     extra = {}
+    fst = fit.stats
+    if fst["expand_launches"] > 0:
+        extra["expand_bytes_per_launch"] = round(fst["expand_bytes"] / fst["expand_launches"], 1)
     if st:
         # a histogram build = accumulation (root kernel, or the expansion
         # kernel that also partitions) + the scan kernel that merges the

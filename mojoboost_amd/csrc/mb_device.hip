@@ -155,7 +155,7 @@ constexpr int kMaxBatch = 32;
 // the previous tree needed (kFirstGroup for the first tree), later ones
 // kNextGroup.
 constexpr int kFirstGroup = 8;
-constexpr int kNextGroup = 2;
+constexpr int kNextGroup = 1;
 constexpr int kMaxGroup = 64;
 
 int64_t chunk_limit_for(int B) {
@@ -521,7 +521,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             int group_size[2] = {0, 0};
             for (int k = 0;; ++k) {
                 const int slot = k & 1;
-                const int n = k == 0 ? std::max(1, std::min(est, kMaxGroup)) : kNextGroup;
+                // a little short of the previous tree: a tree that needs more
+                // costs one more group read, one that needs fewer costs empty
+                // launches
+                const int n = k == 0 ? std::max(1, std::min(est - 2, kMaxGroup)) : kNextGroup;
                 group_size[slot] = n;
                 for (int c = 0; c < n; ++c) {
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 0), st));
