@@ -162,3 +162,45 @@ def test_training_is_deterministic(dev):
     for k in ("feature", "threshold", "value", "gain"):
         assert np.array_equal(getattr(a, k), getattr(b, k))
     assert np.array_equal(bits(a.train_raw()), bits(b.train_raw()))
+
+
+@pytest.mark.parametrize("objective", ["binary", "regression"])
+def test_estimator_through_c_abi_bit_exact(dev, tmp_path, objective):
+    """The public surface end to end: MojoTrees*(device="gpu").fit ->
+    mojotrees_train_dense -> host binning -> device training -> model ->
+    predict, against the oracle trained on the oracle's own bins of the same
+    matrix (identical bin boundaries); then save -> load -> predict."""
+    from mojoboost_amd.sklearn import MojoTreesClassifier, MojoTreesRegressor
+
+    n, f = 60_000, 8
+    rng = np.random.default_rng(11)
+    X = rng.normal(size=(n, f))
+    X[rng.uniform(size=(n, f)) < 0.02] = np.nan
+    z = X[:, 0] * X[:, 1] + np.abs(np.nan_to_num(X[:, 2])) - 0.5
+    z = np.nan_to_num(z)
+    if objective == "binary":
+        y = (rng.uniform(size=n) < 1 / (1 + np.exp(-z))).astype(np.float64)
+        est = MojoTreesClassifier(n_estimators=6, num_leaves=31, learning_rate=0.1,
+                                  max_bin=63, device="gpu")
+    else:
+        y = z + 0.1 * rng.normal(size=n)
+        est = MojoTreesRegressor(n_estimators=6, num_leaves=31, learning_rate=0.1,
+                                 max_bin=63, device="gpu")
+    est.fit(X, y)
+    raw = est.decision_function(X) if objective == "binary" else est.predict(X)
+
+    x_cm = np.ascontiguousarray(X.T).ravel()
+    bins, _, _, mb = O.fit_transform(x_cm, n, f, max_bins=63)
+    p = O.default_params(objective=1 if objective == "binary" else 0, num_iterations=6,
+                         num_leaves=31, learning_rate=0.1, min_data_in_leaf=20, lambda_l2=1.0,
+                         min_sum_hessian=1e-3, use_quantized_grad=1, num_grad_quant_bins=4,
+                         stochastic_rounding=1)
+    ref = O.train(bins, n, f, 64, y, p, missing_bin=mb)
+    want = ref.predict_binned(bins, n, f)
+    assert np.array_equal(bits(raw), bits(want))
+
+    path = tmp_path / "m.txt"
+    est.save(str(path))
+    back = type(est).load(str(path))
+    raw2 = back.decision_function(X) if objective == "binary" else back.predict(X)
+    assert np.array_equal(bits(raw2), bits(raw))
