@@ -106,7 +106,8 @@ struct mbh_dataset {
     int32_t *d_missing = nullptr, *d_widths = nullptr;
     std::vector<int32_t> missing, widths;
     double label_sum = 0.0;  // sequential sum, for the base score
-    std::vector<double> class_count;
+    std::vector<double> class_count;  // when labels are integers in [0, 1024)
+    bool labels_integral = false;
     double label_min = 0.0, label_max = 0.0;
     std::vector<void *> owned;
     ~mbh_dataset() {
@@ -155,6 +156,8 @@ constexpr int kMaxBatch = 32;
 // the previous tree needed (kFirstGroup for the first tree), later ones
 // kNextGroup.
 constexpr int kFirstGroup = 8;
+// Most classes of a multiclass objective.
+constexpr int kMaxClass = 1024;
 constexpr int kNextGroup = 1;
 constexpr int kMaxGroup = 64;
 
@@ -171,10 +174,13 @@ int64_t chunk_limit_for(int B) {
 void check_params(const mbh_dataset *ds, const mbh_params *p) {
     auto bad = [](const std::string &m) { throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, m}; };
     auto unsup = [](const std::string &m) { throw Error{MOJOTREES_ERROR_UNSUPPORTED, m}; };
-    if (p->objective != MBH_OBJ_REGRESSION && p->objective != MBH_OBJ_BINARY) {
-        if (p->objective == MBH_OBJ_MULTICLASS)
-            unsup("multiclass training is not built on the device path yet");
+    if (p->objective != MBH_OBJ_REGRESSION && p->objective != MBH_OBJ_BINARY &&
+        p->objective != MBH_OBJ_MULTICLASS)
         bad("unknown objective");
+    if (p->objective == MBH_OBJ_MULTICLASS) {
+        if (p->num_class < 2 || p->num_class > kMaxClass) bad("num_class must be in [2, 1024]");
+        if (!ds->labels_integral || ds->label_min < 0.0 || ds->label_max >= (double)p->num_class)
+            bad("multiclass labels must be integers in [0, num_class)");
     }
     if (p->num_iterations < 0) bad("num_iterations must be nonnegative");
     if (p->num_leaves < 1) bad("num_leaves must be positive");
@@ -236,6 +242,22 @@ double base_score_for(const mbh_dataset *ds, int objective) {
     return mean;
 }
 
+// Per-class base scores. boosting.train_multiclass
+// (src/mojotrees/boosting.mojo:4167-4250): log of each class's clamped share.
+std::vector<double> base_scores_for(const mbh_dataset *ds, int objective, int K) {
+    if (objective != MBH_OBJ_MULTICLASS) return {base_score_for(ds, objective)};
+    std::vector<double> b(K);
+    for (int k = 0; k < K; ++k) {
+        const double cnt = (size_t)k < ds->class_count.size() ? ds->class_count[k] : 0.0;
+        double p = cnt / (double)ds->n;
+        if (p < 1e-15) p = 1e-15;
+        if (p > 1.0 - 1e-15) p = 1.0 - 1e-15;
+        b[k] = mb::ref_log(p);
+    }
+    return b;
+}
+
+
 struct TrainBuffers {
     mb::DevState s{};
     int T = 0, L = 0, max_nodes = 0;
@@ -243,7 +265,7 @@ struct TrainBuffers {
 
 TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     TrainBuffers tb;
-    const int K = 1;
+    const int K = p->objective == MBH_OBJ_MULTICLASS ? p->num_class : 1;
     const int L = p->num_leaves;
     const int T = std::max(1, p->num_iterations * K);
     const int max_nodes = 2 * L - 1;
@@ -261,6 +283,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.rec_bytes = ds->rec;
     s.lds_stride = ds->lds_stride;
     s.raw = dalloc<double>((size_t)ds->n * K, run.owned);
+    s.prob = K > 1 ? dalloc<double>((size_t)ds->n * K, run.owned) : nullptr;
     s.grad = dalloc<float>(ds->n, run.owned);
     s.hess = dalloc<float>(ds->n, run.owned);
     s.stats = dalloc<uint32_t>(4, run.owned);
@@ -429,6 +452,14 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         ds->label_sum = sum;
         ds->label_min = lo;
         ds->label_max = hi;
+        // class counts, for a multiclass base score
+        ds->labels_integral = lo >= 0.0 && hi < (double)kMaxClass;
+        for (int64_t r = 0; r < n && ds->labels_integral; ++r)
+            if (labels[r] != std::floor(labels[r])) ds->labels_integral = false;
+        if (ds->labels_integral) {
+            ds->class_count.assign((size_t)hi + 1, 0.0);
+            for (int64_t r = 0; r < n; ++r) ds->class_count[(size_t)labels[r]] += 1.0;
+        }
         HIPX(hipGetDevice(&ds->device));
         hipDeviceProp_t prop;
         HIPX(hipGetDeviceProperties(&prop, ds->device));
@@ -467,12 +498,12 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         Run run;
         TrainBuffers tb = setup_state(ds, p, run);
         mb::DevState &s = tb.s;
-        const int K = 1;
+        const int K = s.hp.num_class;
         fit->num_class = K;
         fit->objective = p->objective;
         fit->n_features = ds->F;
         fit->learning_rate = p->learning_rate;
-        fit->base.assign(K, base_score_for(ds, p->objective));
+        fit->base = base_scores_for(ds, p->objective, K);
         double *d_base = dalloc<double>(K, run.owned);
         HIPX(hipMemcpy(d_base, fit->base.data(), K * sizeof(double), hipMemcpyHostToDevice));
         const int grid_rows = 8 * ds->n_cu;
@@ -509,6 +540,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         int est = kFirstGroup;
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
+            if (K > 1 && t % K == 0) HIPX(mb::launch_softmax(s, grid_rows, st));
             HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
             if (timed) HIPX(hipEventRecord(events[2], st));
@@ -588,43 +620,63 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
         double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
         int grown = 0;
-        for (int t = 0; t < T; ++t) {
-            const int32_t *ti = ai.data() + (size_t)t * (6 * mn + 2);
-            const double *td = ad.data() + (size_t)t * 3 * mn;
-            const int nn = ti[6 * mn], nl = ti[6 * mn + 1];
-            // builds of the committed tree: the root, then the smaller child
-            // of every split
-            root_rows += td[2];
-            useful_rows += td[2];
-            builds += 1;
-            for (int i = 0; i < nn; ++i) {
-                if (ti[6 * i] < 0) continue;
-                const double cl = td[3 * ti[6 * i + 2] + 2], cr = td[3 * ti[6 * i + 3] + 2];
-                useful_rows += std::min(cl, cr);
+        auto tree_int = [&](int t) { return ai.data() + (size_t)t * (6 * mn + 2); };
+        auto tree_dbl = [&](int t) { return ad.data() + (size_t)t * 3 * mn; };
+        auto degenerate = [&](int t) {
+            return tree_int(t)[6 * mn + 1] == 1 && std::fabs(tree_dbl(t)[0]) < 1e-12;
+        };
+        const int R = T / K;
+        for (int rr = 0; rr < R; ++rr) {
+            bool progress = false;
+            for (int k = 0; k < K; ++k) {
+                const int t = rr * K + k;
+                const int32_t *ti = tree_int(t);
+                const double *td = tree_dbl(t);
+                const int nn = ti[6 * mn];
+                // builds of the committed tree: the root, then the smaller
+                // child of every split
+                root_rows += td[2];
+                useful_rows += td[2];
                 builds += 1;
+                for (int i = 0; i < nn; ++i) {
+                    if (ti[6 * i] < 0) continue;
+                    const double cl = td[3 * ti[6 * i + 2] + 2], cr = td[3 * ti[6 * i + 3] + 2];
+                    useful_rows += std::min(cl, cr);
+                    builds += 1;
+                }
+                rows_built += (double)ax[(size_t)t * 4 + 0];
+                iters_total += (double)ax[(size_t)t * 4 + 1];
+                exps += (double)ax[(size_t)t * 4 + 2];
+                rows_parted += (double)ax[(size_t)t * 4 + 3];
+                progress |= !degenerate(t);
             }
-            rows_built += (double)ax[(size_t)t * 4 + 0];
-            iters_total += (double)ax[(size_t)t * 4 + 1];
-            exps += (double)ax[(size_t)t * 4 + 2];
-            rows_parted += (double)ax[(size_t)t * 4 + 3];
-            // boosting._boost_rounds stopping rule (boosting.mojo:2898-2907)
-            if (nl == 1 && std::fabs(td[0]) < 1e-12) {
+            // boosting._boost_rounds' stop rule (boosting.mojo:2898-2907):
+            // a round that does not move ends training, or is skipped when
+            // rows are sampled; multiclass judges the round's K trees
+            // together (:3876-4165)
+            if (!progress) {
                 if (bagging) continue;
                 break;
             }
-            for (int i = 0; i < nn; ++i) {
-                fit->feature.push_back(ti[6 * i + 0]);
-                fit->threshold.push_back(ti[6 * i + 1]);
-                fit->left.push_back(ti[6 * i + 2]);
-                fit->right.push_back(ti[6 * i + 3]);
-                fit->default_left.push_back(ti[6 * i + 4]);
-                fit->missing_bin.push_back(ti[6 * i + 5]);
-                fit->value.push_back(td[3 * i + 0]);
-                fit->gain.push_back(td[3 * i + 1]);
-                fit->count.push_back(td[3 * i + 2]);
+            for (int k = 0; k < K; ++k) {
+                const int t = rr * K + k;
+                const int32_t *ti = tree_int(t);
+                const double *td = tree_dbl(t);
+                const int nn = ti[6 * mn];
+                for (int i = 0; i < nn; ++i) {
+                    fit->feature.push_back(ti[6 * i + 0]);
+                    fit->threshold.push_back(ti[6 * i + 1]);
+                    fit->left.push_back(ti[6 * i + 2]);
+                    fit->right.push_back(ti[6 * i + 3]);
+                    fit->default_left.push_back(ti[6 * i + 4]);
+                    fit->missing_bin.push_back(ti[6 * i + 5]);
+                    fit->value.push_back(td[3 * i + 0]);
+                    fit->gain.push_back(td[3 * i + 1]);
+                    fit->count.push_back(td[3 * i + 2]);
+                }
+                fit->offsets.push_back((int64_t)fit->feature.size());
+                ++grown;
             }
-            fit->offsets.push_back((int64_t)fit->feature.size());
-            ++grown;
         }
         double *o = fit->stats;
         o[0] = std::chrono::duration<double>(t1 - t0).count();

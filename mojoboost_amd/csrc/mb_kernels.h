@@ -8,6 +8,7 @@
 namespace mb {
 
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
+hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 // Raises the dynamic LDS limits of the kernels that need more than 64 KB.
 hipError_t prepare_kernels(const DevState &s);

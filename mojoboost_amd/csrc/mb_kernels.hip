@@ -144,14 +144,26 @@ __device__ __forceinline__ uint64_t bag_stream_of(const HyperParams &hp, int64_t
 __global__ __launch_bounds__(256) void k_objective(DevState s) {
     __shared__ float red_g[4], red_h[4];
     const Round rd = *s.round;
+    if (rd.stopped) return;
     const HyperParams &hp = s.hp;
     if (blockIdx.x == 0 && threadIdx.x == 0) s.cursor[0] = 0;  // root row count
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int K = hp.num_class, ck = rd.class_k;
+    const double factor = K > 1 ? (double)K / (double)(K - 1) : 0.0;
     float mg = 0.0f, mh = 0.0f;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
         float g, h;
-        if (hp.objective == kObjBinary) {
+        if (hp.objective == kObjMulticlass) {
+            // _fill_softmax_grad_hess_at (boosting.mojo:3621-3678) on the
+            // probabilities of the round's start
+            const double p = s.prob[r * K + ck];
+            const double y = ((int)s.labels[r] == ck) ? 1.0 : 0.0;
+            g = (float)(p - y);
+            double hh = factor * p * (1.0 - p);
+            if (hh < 1e-16) hh = 1e-16;
+            h = (float)hh;
+        } else if (hp.objective == kObjBinary) {
             double p = sigmoid(s.raw[r]);
             g = (float)(p - s.labels[r]);
             double hh = p * (1.0 - p);
@@ -188,6 +200,31 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
     }
 }
 
+// ----------------------------------------------------------------- softmax
+// boosting._softmax_rows (src/mojotrees/boosting.mojo:3529-3573): per row,
+// shift by the maximum, exponentiate with the reference's exp, sum in class
+// order, divide. Run once at the start of each multiclass round; every class
+// tree of the round uses these probabilities.
+__global__ __launch_bounds__(256) void k_softmax(DevState s) {
+    if (s.round->stopped) return;
+    const int K = s.hp.num_class;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
+        const double *x = s.raw + r * K;
+        double *p = s.prob + r * K;
+        double m = x[0];
+        for (int i = 1; i < K; ++i)
+            if (x[i] > m) m = x[i];
+        double total = 0.0;
+        for (int i = 0; i < K; ++i) {
+            const double e = ref_exp(x[i] - m);
+            p[i] = e;
+            total += e;
+        }
+        for (int i = 0; i < K; ++i) p[i] = p[i] / total;
+    }
+}
+
 // ---------------------------------------------------------------- quantize
 // derive_scales (max-abs rule, quantized_gradient.mojo:1343-1453) and
 // quantize_scalar per row (:1479-1545). Every row is quantized, sampled or
@@ -196,6 +233,7 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
 // (the bag) is gathered here; without bagging the root reads rows directly.
 __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const Round rd = *s.round;
+    if (rd.stopped) return;
     const HyperParams &hp = s.hp;
     double max_g = (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
     double max_h = (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
@@ -307,6 +345,7 @@ constexpr int kHistUnroll = 4;
 template <int LPR>
 __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     extern __shared__ unsigned long long lds[];
+    if (s.round->stopped) return;
     const int64_t m = root_rows(s);
     const int32_t *rows = s.rows0;
     const bool direct = !s.hp.bagging;
@@ -521,6 +560,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
     const int n_tasks = n_items * F;
     if ((int)blockIdx.x >= n_tasks) return;
     const Round rd = *s.round;
+    if (rd.stopped) return;
     const double gu = rd.grad_units, hu = rd.hess_units;
     const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
     long long hmin = 0;  // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
@@ -836,6 +876,20 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     if (n_items <= 0) return;  // the tree is complete
     PlanView v = plan_view(s, plan_smem);
     const Round rd = *s.round;
+    if (rd.stopped) {
+        // training has stopped: an empty tree, nothing to expand
+        if (tid == 0) {
+            s.t_meta[0] = 1;
+            s.t_meta[1] = 1;
+            Batch b;
+            b.n_items = 0;
+            b.n_blocks = 0;
+            b.done = 1;
+            b.iters = 0;
+            *s.batch = b;
+        }
+        return;
+    }
     const double gu = rd.grad_units, hu = rd.hess_units;
     if (tid == 0) {
         if (root_mode) {
@@ -1303,7 +1357,11 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     extern __shared__ int32_t tnode[];  // 5 ints per node
     const int n_nodes = s.t_meta[0];
     const int n_leaves = s.t_meta[1];
-    if (n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
+    if (s.round->stopped) return;
+    // a single output stops before adding a degenerate tree; a multiclass
+    // round adds every class tree and decides afterwards
+    // (boosting.mojo:2898-2907, :3876-4165)
+    if (s.hp.num_class == 1 && n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
     double *vals = (double *)(tnode + 5 * s.max_nodes + (s.max_nodes & 1));
     for (int i = threadIdx.x; i < n_nodes; i += blockDim.x) {
         tnode[5 * i + 0] = s.t_feature[i];
@@ -1367,6 +1425,19 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
         ax[2] = g.expansions;
         ax[3] = g.rows_parted;
         Round nr = rd;
+        if (!rd.stopped) {
+            // boosting._boost_rounds' stop rule: a tree of one leaf whose
+            // value is below 1e-12 ends training unless rows are sampled;
+            // for multiclass, a round none of whose trees does better
+            const bool degenerate = s.t_meta[1] == 1 && fabs(s.t_value[0]) < 1e-12;
+            const int K = s.hp.num_class;
+            if (K == 1) {
+                if (degenerate && !s.hp.bagging) nr.stopped = 1;
+            } else {
+                nr.progress = (rd.class_k == 0 ? 0 : rd.progress) | (degenerate ? 0 : 1);
+                if (rd.class_k == K - 1 && !nr.progress && !s.hp.bagging) nr.stopped = 1;
+            }
+        }
         nr.tree_index = rd.tree_index + 1;
         nr.class_k = rd.class_k + 1;
         if (nr.class_k >= s.hp.num_class) {
@@ -1405,6 +1476,10 @@ __global__ void k_exp_sigmoid(const double *x, double *e, double *sg, int64_t n)
 // ------------------------------------------------------------------ launch
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_objective, dim3(grid), dim3(256), 0, st, s);
+    return hipGetLastError();
+}
+hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_softmax, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {

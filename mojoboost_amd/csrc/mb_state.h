@@ -95,8 +95,9 @@ struct Round {
     int32_t class_k;     // class of this tree (0 for single output)
     int32_t tree_index;  // position in the ensemble
     int32_t parity;      // which magnitude-stats pair this tree uses
+    int32_t stopped;     // training stopped (boosting._boost_rounds' stop rule): later trees do nothing
+    int32_t progress;    // a tree of the current multiclass round split or moved
     int32_t pad_;
-    int64_t n_root;      // rows in the root range (bag size, or n)
     double grad_units, hess_units;
 };
 
@@ -135,6 +136,7 @@ struct DevState {
     int32_t lds_stride;    // per-feature LDS stride (odd, >= n_bins)
     // per round
     double *raw;           // n x num_class
+    double *prob;          // n x num_class softmax of raw at the start of a round (multiclass)
     float *grad, *hess;    // n
     uint32_t *stats;       // [2 parities][2]: max |g|, max |h| as float bits
     Round *round;

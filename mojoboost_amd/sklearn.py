@@ -210,33 +210,44 @@ class MojoTreesRegressor(_Base):
 
 
 class MojoTreesClassifier(_Base):
+    """Binary (logistic) for two classes, softmax multiclass for more; class
+    labels are mapped to 0..K-1 in sorted order, as the reference's
+    classifier does (python/mojotrees/sklearn.py:6412)."""
     _objective = "binary"
 
     def fit(self, X, y):
         y = np.asarray(y)
-        self.classes_ = np.unique(y)
-        if len(self.classes_) != 2:
-            raise MojoTreesError(_lib.ERROR_UNSUPPORTED,
-                                 "only binary classification is served by the device path")
-        yb = (y == self.classes_[1]).astype(np.float64)
-        self.booster_ = _train(X, yb, self._params())
+        self.classes_, yi = np.unique(y, return_inverse=True)
+        k = len(self.classes_)
+        if k < 2:
+            raise ValueError("y needs at least two classes")
+        if k == 2:
+            self.booster_ = _train(X, yi.astype(np.float64), self._params())
+        else:
+            params = self._params().replace("objective=binary", "objective=multiclass")
+            self.booster_ = _train(X, yi.astype(np.float64), params + f" num_class={k}")
         return self
 
     def predict_proba(self, X):
         self._check_fitted()
-        p1 = self.booster_.predict(X)
-        return np.column_stack([1.0 - p1, p1])
+        p = self.booster_.predict(X)
+        if self.booster_.num_classes == 1:
+            return np.column_stack([1.0 - p, p])
+        return p.reshape(-1, self.booster_.num_classes)
 
     def predict(self, X):
-        return self.classes_[(self.predict_proba(X)[:, 1] > 0.5).astype(int)]
+        return self.classes_[np.argmax(self.predict_proba(X), axis=1)]
 
     def decision_function(self, X):
         self._check_fitted()
-        return self.booster_.predict(X, raw=True)
+        raw = self.booster_.predict(X, raw=True)
+        k = self.booster_.num_classes
+        return raw if k == 1 else raw.reshape(-1, k)
 
     @classmethod
     def load(cls, path):
         est = cls()
         est.booster_ = _Booster.load(path)
-        est.classes_ = np.array([0, 1])
+        k = est.booster_.num_classes
+        est.classes_ = np.arange(2 if k == 1 else k)
         return est

@@ -204,3 +204,87 @@ def test_estimator_through_c_abi_bit_exact(dev, tmp_path, objective):
     back = type(est).load(str(path))
     raw2 = back.decision_function(X) if objective == "binary" else back.predict(X)
     assert np.array_equal(bits(raw2), bits(raw))
+
+
+def c5_like(n, n_class=5, seed=5, nb=255):
+    """C5-shaped data at reduced size: 16
+    continuous N(0,1) columns and 4 integer columns of cardinality 4-64, the
+    class drawn as the argmax of random linear scores plus Gumbel noise."""
+    rng = np.random.default_rng(seed)
+    cont = rng.normal(size=(16, n))
+    cats = np.vstack([rng.integers(0, c, size=n) for c in (4, 9, 27, 64)]).astype(np.float64)
+    x = np.vstack([cont, cats])
+    w = rng.normal(size=(n_class, x.shape[0]))
+    scores = w @ (x - x.mean(axis=1, keepdims=True)) / 4 + rng.gumbel(size=(n_class, n))
+    y = scores.argmax(axis=0).astype(np.float64)
+    f = x.shape[0]
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=nb)
+    return bins, y, mb, nb, f
+
+
+@pytest.mark.parametrize("bagging", [False, True])
+def test_training_multiclass_bit_exact(dev, bagging):
+    """Softmax multiclass, one tree per class per round, quantized per class:
+    every tree and every training score identical to the oracle."""
+    n, K = 120_000, 5
+    bins, y, mb, nb, f = c5_like(n, K)
+    kw = dict(objective=2, num_class=K, num_iterations=4, num_leaves=63, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    if bagging:
+        kw.update(bagging_fraction=0.7, bagging_freq=1, bagging_seed=9)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    fit = ds.train(**kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    assert fit.num_class == K and fit.n_trees == 4 * K
+    _compare_fit(fit, ref, n)
+
+
+def test_estimator_multiclass_through_c_abi_bit_exact(dev, tmp_path):
+    """MojoTreesClassifier with 4 classes -> objective=multiclass through the
+    C ABI; raw scores equal the oracle's on its own bins, and survive
+    save -> load."""
+    from mojoboost_amd.sklearn import MojoTreesClassifier
+
+    n, f, K = 50_000, 6, 4
+    rng = np.random.default_rng(21)
+    X = rng.normal(size=(n, f))
+    scores = X[:, :K] * 1.5 + rng.gumbel(size=(n, K))
+    y = np.array(["a", "b", "c", "d"])[scores.argmax(axis=1)]
+    est = MojoTreesClassifier(n_estimators=3, num_leaves=15, learning_rate=0.2, max_bin=63,
+                              device="gpu").fit(X, y)
+    raw = est.decision_function(X)
+    assert raw.shape == (n, K) and list(est.classes_) == ["a", "b", "c", "d"]
+
+    x_cm = np.ascontiguousarray(X.T).ravel()
+    bins, _, _, mb = O.fit_transform(x_cm, n, f, max_bins=63)
+    yi = np.unique(y, return_inverse=True)[1].astype(np.float64)
+    p = O.default_params(objective=2, num_class=K, num_iterations=3, num_leaves=15,
+                         learning_rate=0.2, min_data_in_leaf=20, lambda_l2=1.0,
+                         min_sum_hessian=1e-3, use_quantized_grad=1, num_grad_quant_bins=4,
+                         stochastic_rounding=1)
+    ref = O.train(bins, n, f, 64, yi, p, missing_bin=mb)
+    want_raw, want_prob = ref.predict_binned(bins, n, f)
+    assert np.array_equal(bits(raw.ravel()), bits(want_raw))
+    prob = est.predict_proba(X)
+    assert np.allclose(prob.ravel(), want_prob, rtol=1e-12, atol=0)
+
+    path = tmp_path / "mc.txt"
+    est.save(str(path))
+    back = MojoTreesClassifier.load(str(path))
+    assert np.array_equal(bits(back.decision_function(X).ravel()), bits(raw.ravel()))
+
+
+def test_stop_rule_constant_labels(dev):
+    """A round that cannot split and whose leaf value is below 1e-12 ends
+    training (boosting._boost_rounds): no trees, scores stay at the base."""
+    n = 20_000
+    rng = np.random.default_rng(4)
+    bins = rng.integers(0, 16, size=(3, n), dtype=np.uint8)
+    y = np.full(n, 2.5)
+    kw = dict(objective=0, num_iterations=5, num_leaves=15, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.1)
+    ds = dev.Dataset(bins.ravel(), n, 3, 16, y)
+    fit = ds.train(**kw)
+    ref = O.train(bins.ravel(), n, 3, 16, y, O.default_params(**kw, use_quantized_grad=1))
+    assert fit.n_trees == ref.n_trees == 0
+    assert np.array_equal(bits(fit.train_raw()), bits(ref.train_raw(n)))
