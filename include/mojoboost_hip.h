@@ -61,6 +61,8 @@ typedef struct {
     int32_t stochastic_rounding;
     int32_t quant_seed;
     int32_t time_histograms; /* 1: bracket each histogram launch with events */
+    int32_t use_quantized_grad; /* 1: int8 gradients, integer histograms;
+                                   0: fp32 gradients, fp64 histogram sums */
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -84,7 +86,8 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n_rows,
                            mbh_dataset **out, char *err, int32_t err_len);
 void mbh_dataset_free(mbh_dataset *ds);
 
-/* Train on a resident dataset (quantized gradients, int32 histograms). */
+/* Train on a resident dataset: quantized gradients with integer histograms,
+ * or fp32 gradients with fp64 histogram sums (use_quantized_grad = 0). */
 int32_t mbh_train(mbh_dataset *ds, const mbh_params *params, mbh_fit **out,
                   char *err, int32_t err_len);
 void mbh_fit_free(mbh_fit *fit);
@@ -138,6 +141,15 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad,
                       const int8_t *q_hess, const int32_t *rows,
                       int64_t n_sel, int32_t num_grad_quant_bins,
                       int32_t *out, char *err, int32_t err_len);
+
+/* fp32-gradient histogram of the rows `rows[0..n_sel)` (all rows when rows
+ * is NULL) with the given fp32 grad/hess (n_rows each), summed in fp64 on the
+ * device: out_gh is n_features * n_bins * 2 doubles {grad, hess} per cell,
+ * out_count n_features * n_bins counts. The reference's Float64 histogram
+ * (histogram.mojo:1002, build_histogram_subset_into :2038). */
+int32_t mbh_histogram_fp32(mbh_dataset *ds, const float *grad, const float *hess,
+                           const int32_t *rows, int64_t n_sel, double *out_gh,
+                           int64_t *out_count, char *err, int32_t err_len);
 
 /* Root histogram of all rows, `reps` times back to back on resident data
  * (HIP events): out_ms[0] mean histogram-kernel milliseconds, out_ms[1] its

@@ -34,7 +34,7 @@ MBH_SYMBOLS = [
     "mbh_bin_dense", "mbh_device_count", "mbh_dataset_create", "mbh_dataset_free", "mbh_train",
     "mbh_fit_free", "mbh_fit_num_trees", "mbh_fit_num_class", "mbh_fit_total_nodes",
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
-    "mbh_objective_quantize", "mbh_histogram", "mbh_bench_root_histogram",
+    "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
 ]
 
 
@@ -59,6 +59,7 @@ class MbhParams(C.Structure):
         ("stochastic_rounding", C.c_int32),
         ("quant_seed", C.c_int32),
         ("time_histograms", C.c_int32),
+        ("use_quantized_grad", C.c_int32),
     ]
 
 
@@ -68,7 +69,7 @@ def mbh_params(**kw) -> MbhParams:
                   lambda_l2=1.0, min_sum_hessian=1e-3, max_depth=-1, feature_fraction=1.0,
                   feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
-                  quant_seed=11, time_histograms=0)
+                  quant_seed=11, time_histograms=0, use_quantized_grad=1)
     for k, v in kw.items():
         setattr(p, k, v)
     return p
@@ -132,6 +133,7 @@ def lib():
         "mbh_exp_sigmoid": (I32, [V, I64, V, V, C.c_char_p, I32]),
         "mbh_objective_quantize": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),
+        "mbh_histogram_fp32": (I32, [V, V, V, V, I64, V, V, C.c_char_p, I32]),
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),
     }
     for name, (res, args) in sig.items():

@@ -120,7 +120,7 @@ struct Config {
     int64_t bin_sample = 200000;
     int64_t data_seed = 1;
     bool use_missing = true;
-    bool quantized = true;
+    bool quantized = false;  // LightGBM's default; the reference trains unquantized
     int num_class = 1;
     bool saw_num_class = false;
 };
@@ -266,9 +266,7 @@ Config parse(const char *spec) {
         if (!c.saw_num_class) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "objective=multiclass needs num_class"};
         p.num_class = c.num_class;
     }
-    if (!c.quantized)
-        throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
-                       "use_quantized_grad=false (fp32 histograms) is not built on the device path yet"};
+    p.use_quantized_grad = c.quantized ? 1 : 0;
     if (c.max_bin < 2 || c.max_bin > 256) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "max_bin must be in [2, 256]"};
     return c;
 }

@@ -146,8 +146,10 @@ struct PinnedFlags {
     }
 };
 
-// LDS row list of the partition+histogram kernel (one tile of row ids).
+// LDS row list of the partition+histogram kernel (one tile of row ids), and
+// its static LDS (tile counters and offsets).
 constexpr size_t kPbListBytes = 4096 * 4;
+constexpr size_t kPbStaticLds = 2048;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
 // trees reaches the tree's depth in iterations with 32).
 constexpr int kMaxBatch = 32;
@@ -194,10 +196,12 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     if (!(p->bagging_fraction > 0.0 && p->bagging_fraction <= 1.0)) bad("bagging_fraction must be in (0, 1]");
     if (p->bagging_freq < 0) bad("bagging_freq must be nonnegative");
     const int B = p->num_grad_quant_bins;
-    if (B < 2 || B > 126 || B % 2 != 0)
-        unsup("num_grad_quant_bins must be even and in [2, 126] (int8 gradient storage)");
-    if ((double)ds->n * (double)(B + 1) >= 2147483647.0)
-        unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
+    if (p->use_quantized_grad) {
+        if (B < 2 || B > 126 || B % 2 != 0)
+            unsup("num_grad_quant_bins must be even and in [2, 126] (int8 gradient storage)");
+        if ((double)ds->n * (double)(B + 1) >= 2147483647.0)
+            unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
+    }
     if (p->objective == MBH_OBJ_BINARY && (ds->label_min < 0.0 || ds->label_max > 1.0))
         bad("binary labels must be in [0, 1]");
 }
@@ -211,7 +215,7 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
 // always suffice.
 constexpr int64_t kHistChunkMin = 4096;
 
-void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
+void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantized, Run &run) {
     const int64_t limit = chunk_limit_for(B);
     int64_t grid = 2 * (int64_t)ds->n_cu;
     const int64_t need = (ds->n + limit - 1) / limit;
@@ -225,7 +229,14 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, Run &run) {
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);
     const int64_t parts = std::max<int64_t>(grid, s.pb_grid);
-    s.part = dalloc<unsigned long long>((size_t)parts * ds->F * s.part_stride, run.owned);
+    const size_t cells = (size_t)parts * ds->F * s.part_stride;
+    if (quantized) {
+        s.part = dalloc<unsigned long long>(cells, run.owned);
+    } else {
+        s.fpart_g = dalloc<double>(cells, run.owned);
+        s.fpart_h = dalloc<double>(cells, run.owned);
+        s.fpart_c = dalloc<uint32_t>(cells, run.owned);
+    }
     s.pb_desc = dalloc<mb::PbDesc>(s.pb_grid, run.owned);
 }
 
@@ -293,8 +304,10 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     const int max_exp = 2 * L - 1;
     s.max_exp = max_exp;
     s.e_cap = 1 + 2 * max_exp;
-    s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
-    configure_hist(s, ds, p->num_grad_quant_bins, run);
+    const bool quantized = p->use_quantized_grad != 0;
+    if (quantized) s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
+    else s.histf = dalloc<mb::HistF>((size_t)(1 + max_exp) * F * ds->nb, run.owned);
+    configure_hist(s, ds, quantized ? p->num_grad_quant_bins : 4, quantized, run);
     s.enodes = dalloc<mb::ENode>(s.e_cap, run.owned);
     s.items = dalloc<mb::Item>(s.kmax, run.owned);
     s.batch = dalloc<mb::Batch>(1, run.owned);
@@ -334,6 +347,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.quant_seed = p->quant_seed;
     // boosting.round_has_constant_hessian: squared error without weights.
     hp.const_hessian = p->objective == MBH_OBJ_REGRESSION ? 1 : 0;
+    hp.quantized = p->use_quantized_grad ? 1 : 0;
     hp.bagging = (p->bagging_freq > 0 && p->bagging_fraction < 1.0) ? 1 : 0;
     hp.bagging_freq = p->bagging_freq;
     hp.bagging_seed = p->bagging_seed;
@@ -346,6 +360,11 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     if (mb::plan_lds_bytes(s) > 160 * 1024)
         throw Error{MOJOTREES_ERROR_UNSUPPORTED,
                     "num_leaves * n_features too large for the planner's LDS (160 KiB)"};
+    if (mb::pb_lds_bytes(s) + kPbStaticLds > 160 * 1024)
+        throw Error{MOJOTREES_ERROR_UNSUPPORTED,
+                    quantized ? "n_features * n_bins exceeds one workgroup's LDS"
+                              : "fp32 histograms: n_features * n_bins exceeds one workgroup's LDS "
+                                "(20 bytes per cell; use_quantized_grad=true takes 8)"};
     HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
@@ -832,6 +851,7 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
         p.feature_fraction = 1.0;
         p.bagging_fraction = 1.0;
         p.num_grad_quant_bins = B;
+        p.use_quantized_grad = 1;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
         // place the int8 pairs into the records
@@ -867,6 +887,56 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
     return MOJOTREES_OK;
 }
 
+int32_t mbh_histogram_fp32(mbh_dataset *ds, const float *grad, const float *hess, const int32_t *rows,
+                           int64_t n_sel, double *out_gh, int64_t *out_count, char *err, int32_t err_len) {
+    if (!ds || !grad || !hess || !out_gh || !out_count || (rows && n_sel <= 0)) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        if (rows)
+            for (int64_t i = 0; i < n_sel; ++i)
+                if (rows[i] < 0 || rows[i] >= ds->n)
+                    throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "row id out of range"};
+        Run run;
+        mbh_params p{};
+        p.objective = MBH_OBJ_REGRESSION;
+        p.num_iterations = 1;
+        p.num_leaves = 2;
+        p.learning_rate = 0.1;
+        p.feature_fraction = 1.0;
+        p.bagging_fraction = 1.0;
+        p.num_grad_quant_bins = 4;
+        p.use_quantized_grad = 0;
+        TrainBuffers tb = setup_state(ds, &p, run);
+        mb::DevState &s = tb.s;
+        HIPX(hipMemcpy(s.grad, grad, ds->n * sizeof(float), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(s.hess, hess, ds->n * sizeof(float), hipMemcpyHostToDevice));
+        if (rows) {
+            s.hp.bagging = 1;  // root range = rows0[0 .. cursor[0])
+            HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
+            int64_t c = n_sel;
+            HIPX(hipMemcpy(s.cursor, &c, sizeof(c), hipMemcpyHostToDevice));
+        }
+        HIPX(mb::prepare_kernels(s));
+        HIPX(mb::launch_hist(s, nullptr));
+        HIPX(mb::launch_scan(s, 1, nullptr));
+        HIPX(hipDeviceSynchronize());
+        const size_t cells = (size_t)ds->F * ds->nb;
+        std::vector<mb::HistF> h(cells);
+        HIPX(hipMemcpy(h.data(), s.histf, cells * sizeof(mb::HistF), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < cells; ++i) {
+            out_gh[2 * i] = h[i].g;
+            out_gh[2 * i + 1] = h[i].h;
+            out_count[i] = h[i].c;
+        }
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
 int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, char *err,
                                  int32_t err_len) {
     if (!ds || reps <= 0 || !out_ms) {
@@ -884,6 +954,7 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         p.feature_fraction = 1.0;
         p.bagging_fraction = 1.0;
         p.num_grad_quant_bins = 4;
+        p.use_quantized_grad = 1;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
         mb::Round r0{};

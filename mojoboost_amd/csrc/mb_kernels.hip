@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     for (int64_t r0 = (int64_t)blockIdx.x * blockDim.x; r0 < s.n; r0 += stride) {
         const int64_t r = r0 + threadIdx.x;
         const bool valid = r < s.n;
-        if (valid) {
+        if (valid && hp.quantized) {
             int32_t qg = quantize_scalar((double)s.grad[r], gu, gmax, stoch, gs + (uint64_t)r);
             int32_t qh = quantize_scalar((double)s.hess[r], hu, hmax, stoch, hs + (uint64_t)r);
             uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
@@ -298,53 +298,114 @@ __device__ __forceinline__ int64_t root_rows(const DevState &s) {
     return s.hp.bagging ? load_agent(&s.cursor[0]) : s.n;
 }
 
-// Packed counter (64 bits): count in bits [0,20), hess sum in [20,42), grad
-// sum (signed) in [42,64). Adding packed values adds the three fields while
-// no field overflows, which hist_chunk_limit guarantees for the lattice in
-// use (host-checked): a block never packs more rows than that.
-__device__ __forceinline__ unsigned long long pack_gh(uint32_t gh_word) {
-    const int g = (int)(int8_t)(gh_word >> 16);
-    const int h = (int)(int8_t)(gh_word >> 24);
-    return (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
-}
-
-// Accumulates one record (this lane's 16-byte slice, features sub*16 ..) into
-// the block's LDS histogram.
-__device__ __forceinline__ void lds_accumulate(unsigned long long *lds, const uint4 &w, int sub, int F,
-                                               int ls, unsigned long long packed) {
-    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int f = sub * 16 + q * 4 + j;
-            if (f < F) atomicAdd(&lds[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
-        }
-}
-
-// Stores the block's LDS histogram, every cell, as its partial.
-__device__ __forceinline__ void store_partial(const DevState &s, const unsigned long long *lds, int blk) {
-    const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
-    unsigned long long *out = s.part + (size_t)blk * F * ps;
-    for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
-        const int f = c / ps;
-        const int b = c - f * ps;
-        out[c] = b < nb ? lds[f * ls + b] : 0ULL;
+// Block-private LDS histograms, two kinds.
+//
+// QAcc (quantized gradients): one packed 64-bit counter per cell -- count in
+// bits [0,20), hess sum in [20,42), grad sum (signed) in [42,64) -- so a row
+// costs one ds_add_u64 per feature; the int8 pair travels in the record's
+// last two bytes. Adding packed values adds the three fields while no field
+// overflows, which hist_chunk_limit guarantees for the lattice in use
+// (host-checked): a block never packs more rows than that.
+//
+// FAcc (fp32 gradients): fp64 grad and hess sums (ds_add_f64) and a uint32
+// count per cell, summing the fp32 gradient values exactly as the
+// reference's Float64 histograms do (histogram.mojo:1002); only the order of
+// the additions differs.
+struct QAcc {
+    static constexpr int kUnroll = 4;  // partition tile: 4 x 1024 rows
+    static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 8; }
+    __device__ static void zero(unsigned char *lds, int F, int ls) {
+        unsigned long long *a = (unsigned long long *)lds;
+        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) a[i] = 0ULL;
     }
-}
+    // one record (this lane's 16-byte slice: features sub*16 ..)
+    __device__ static void add(unsigned char *lds, const DevState &, const uint4 &w, int sub, int F, int ls,
+                               int64_t, uint32_t gh_word) {
+        unsigned long long *a = (unsigned long long *)lds;
+        const int g = (int)(int8_t)(gh_word >> 16);
+        const int h = (int)(int8_t)(gh_word >> 24);
+        const unsigned long long packed =
+            (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
+        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = sub * 16 + q * 4 + j;
+                if (f < F) atomicAdd(&a[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
+            }
+    }
+    // every cell of the block's histogram as its partial
+    __device__ static void store(const DevState &s, const unsigned char *lds, int blk) {
+        const unsigned long long *a = (const unsigned long long *)lds;
+        const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
+        unsigned long long *out = s.part + (size_t)blk * F * ps;
+        for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
+            const int f = c / ps;
+            const int b = c - f * ps;
+            out[c] = b < nb ? a[f * ls + b] : 0ULL;
+        }
+    }
+};
+
+struct FAcc {
+    static constexpr int kUnroll = 2;  // partition tile: 2 x 1024 rows (LDS budget)
+    static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 20; }
+    __device__ static void zero(unsigned char *lds, int F, int ls) {
+        double *g = (double *)lds;
+        uint32_t *c = (uint32_t *)(g + 2 * (size_t)F * ls);
+        for (int i = threadIdx.x; i < 2 * F * ls; i += blockDim.x) g[i] = 0.0;
+        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) c[i] = 0u;
+    }
+    __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
+                               int64_t row, uint32_t) {
+        double *g = (double *)lds;
+        double *h = g + (size_t)F * ls;
+        uint32_t *c = (uint32_t *)(h + (size_t)F * ls);
+        const double gv = (double)s.grad[row], hv = (double)s.hess[row];
+        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = sub * 16 + q * 4 + j;
+                if (f < F) {
+                    const int cell = f * ls + (int)((d[q] >> (8 * j)) & 255u);
+                    atomicAdd(&g[cell], gv);
+                    atomicAdd(&h[cell], hv);
+                    atomicAdd(&c[cell], 1u);
+                }
+            }
+    }
+    __device__ static void store(const DevState &s, const unsigned char *lds, int blk) {
+        const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
+        const double *g = (const double *)lds;
+        const double *h = g + (size_t)F * ls;
+        const uint32_t *c = (const uint32_t *)(h + (size_t)F * ls);
+        const size_t base = (size_t)blk * F * ps;
+        for (int i = threadIdx.x; i < F * ps; i += blockDim.x) {
+            const int f = i / ps;
+            const int b = i - f * ps;
+            const bool in = b < nb;
+            s.fpart_g[base + i] = in ? g[f * ls + b] : 0.0;
+            s.fpart_h[base + i] = in ? h[f * ls + b] : 0.0;
+            s.fpart_c[base + i] = in ? c[f * ls + b] : 0u;
+        }
+    }
+};
 
 // Root histogram, accumulation pass. Rows are split into contiguous chunks,
-// one per block; a block accumulates its rows into LDS-private packed
-// counters and stores them as its partial; the scan kernel merges the
-// partials. A row's record is LPR x 16 bytes: each of the LPR lanes of a row
-// group loads 16 bytes (16 features) and the int8 g/h pair (the record's last
-// two bytes) reaches the group by a lane shuffle. Each lane keeps
-// kHistUnroll row loads in flight.
+// one per block; a block accumulates its rows into its LDS histogram and
+// stores it as its partial; the scan kernel merges the partials. A row's
+// record is LPR x 16 bytes: each of the LPR lanes of a row group loads 16
+// bytes (16 features) and the int8 g/h pair (the record's last two bytes)
+// reaches the group by a lane shuffle. Each lane keeps kHistUnroll row loads
+// in flight.
 constexpr int kHistUnroll = 4;
 
-template <int LPR>
+template <int LPR, class Acc>
 __global__ __launch_bounds__(1024) void k_hist(DevState s) {
-    extern __shared__ unsigned long long lds[];
+    extern __shared__ unsigned char lds[];
     if (s.round->stopped) return;
     const int64_t m = root_rows(s);
     const int32_t *rows = s.rows0;
@@ -355,7 +416,7 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     if (c0 >= m) return;
     const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
     const int F = s.n_features, ls = s.lds_stride;
-    for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
+    Acc::zero(lds, F, ls);
     __syncthreads();
     const int lane = lane_id();
     const int sub = threadIdx.x % LPR;
@@ -365,26 +426,27 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     const uint4 *rec = (const uint4 *)s.records;
     for (int64_t i0 = c0; i0 < c1; i0 += (int64_t)kHistUnroll * rpp) {
         uint4 w[kHistUnroll];
+        int64_t row[kHistUnroll];
         bool ok[kHistUnroll];
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const int64_t i = i0 + (int64_t)u * rpp + rr;
             ok[u] = i < c1;
-            int64_t row = 0;
+            row[u] = 0;
             if (ok[u]) {
-                row = direct ? i : (int64_t)rows[i];
-                if ((uint64_t)row >= (uint64_t)s.n) row = 0;  // never taken: ids come from the row lists
+                row[u] = direct ? i : (int64_t)rows[i];
+                if ((uint64_t)row[u] >= (uint64_t)s.n) row[u] = 0;  // never taken: ids come from the row lists
             }
-            w[u] = ok[u] ? rec[row * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
+            w[u] = ok[u] ? rec[row[u] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (ok[u]) lds_accumulate(lds, w[u], sub, F, ls, pack_gh(gh));
+            if (ok[u]) Acc::add(lds, s, w[u], sub, F, ls, row[u], gh);
         }
     }
     __syncthreads();
-    store_partial(s, lds, blockIdx.x);
+    Acc::store(s, lds, blockIdx.x);
 }
 
 // ------------------------------------------------- partition + histogram
@@ -396,28 +458,33 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
 // and accumulates the rows of the smaller child into its LDS histogram,
 // stored as the block's partial.
 //
-// A tile is kPbUnroll x 1024 rows. Per tile: row ids and the split feature's
-// bins are loaded, wave ballots rank the rows, wave 0 scans the per-wave
-// counts and reserves the tile's output with one atomic per side, rows are
-// scattered, and the smaller child's rows are listed in LDS; then the
-// accumulation pass reads their records (LPR lanes per row). The order of
-// rows inside a child is not the reference's (tiles land in reservation
-// order); every consumer is order-free because histograms are integer sums.
+// A tile is Acc::kUnroll x 1024 rows. Per tile: row ids and the split
+// feature's bins are loaded, wave ballots rank the rows, wave 0 scans the
+// per-wave counts and reserves the tile's output with one atomic per side,
+// rows are scattered, and the smaller child's rows are listed in LDS; then
+// the accumulation pass reads their records (LPR lanes per row). The order
+// of rows inside a child is not the reference's (tiles land in reservation
+// order); integer histograms are order-free, fp64 sums differ only in their
+// rounding.
 constexpr int kPbThreads = 1024;
-constexpr int kPbUnroll = 4;
-constexpr int kPbTile = kPbThreads * kPbUnroll;
+constexpr int kPbMaxUnroll = 4;
 
-size_t pb_lds_bytes_of(int F, int ls) { return (size_t)F * ls * 8 + (size_t)kPbTile * 4; }
+template <class Acc>
+__host__ __device__ size_t pb_lds_bytes_of(int F, int ls) {
+    return Acc::lds_bytes(F, ls) + (size_t)kPbThreads * Acc::kUnroll * 4;
+}
 
-template <int LPR>
+template <int LPR, class Acc>
 __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
-    extern __shared__ unsigned long long lds[];
-    __shared__ int cnt_l[kPbUnroll * 16], cnt_r[kPbUnroll * 16];
-    __shared__ long long off_l[kPbUnroll * 16], off_r[kPbUnroll * 16], off_b[kPbUnroll * 16];
+    constexpr int U = Acc::kUnroll;
+    constexpr int kTile = kPbThreads * U;
+    extern __shared__ unsigned char lds[];
+    __shared__ int cnt_l[kPbMaxUnroll * 16], cnt_r[kPbMaxUnroll * 16];
+    __shared__ long long off_l[kPbMaxUnroll * 16], off_r[kPbMaxUnroll * 16], off_b[kPbMaxUnroll * 16];
     __shared__ int s_nbuilt;
     const int n_blocks = s.batch->n_blocks;
     const int F = s.n_features, ls = s.lds_stride;
-    int32_t *list = (int32_t *)(lds + (size_t)F * ls);
+    int32_t *list = (int32_t *)(lds + Acc::lds_bytes(F, ls));
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const unsigned long long below = (1ULL << lane) - 1ULL;
     const int sub = threadIdx.x % LPR;
@@ -429,26 +496,26 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     // whole accumulation (zeroed LDS, stored partial)
     for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
         const PbDesc d = s.pb_desc[blk];
-        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) lds[i] = 0ULL;
+        Acc::zero(lds, F, ls);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
         const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
         const bool bl = d.builds_left != 0;
         unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item];
-        for (int64_t t0 = d.c0; t0 < d.c1; t0 += kPbTile) {
-            int32_t r[kPbUnroll];
-            bool left[kPbUnroll], valid[kPbUnroll];
-            unsigned long long lm[kPbUnroll], rm[kPbUnroll];
+        for (int64_t t0 = d.c0; t0 < d.c1; t0 += kTile) {
+            int32_t r[U];
+            bool left[U], valid[U];
+            unsigned long long lm[U], rm[U];
 #pragma unroll
-            for (int u = 0; u < kPbUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int64_t i = t0 + (int64_t)u * kPbThreads + threadIdx.x;
                 valid[u] = i < d.c1;
                 r[u] = valid[u] ? src[i] : 0;
                 if ((uint32_t)r[u] >= (uint64_t)s.n) r[u] = 0;  // never taken: ids come from the row lists
             }
 #pragma unroll
-            for (int u = 0; u < kPbUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int b = valid[u] ? (int)col[r[u]] : 0;
                 left[u] = (b == mb) ? (dl != 0) : (b <= thr);
                 lm[u] = __ballot(valid[u] && left[u]);
@@ -460,8 +527,8 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
             }
             __syncthreads();
             if (w == 0) {
-                // entry k = u * 16 + wave, in tile order
-                const long long vl = cnt_l[lane], vr = cnt_r[lane];
+                // entry k = u * 16 + wave, in tile order (U * 16 <= 64 entries)
+                const long long vl = lane < U * 16 ? cnt_l[lane] : 0, vr = lane < U * 16 ? cnt_r[lane] : 0;
                 const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
                 const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
                 long long bl_base = 0, br_base = 0;
@@ -478,7 +545,7 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
             }
             __syncthreads();
 #pragma unroll
-            for (int u = 0; u < kPbUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 if (!valid[u]) continue;
                 const int k = u * 16 + w;
                 long long rank;
@@ -499,23 +566,25 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
             const int nbt = s_nbuilt;
             for (int k0 = 0; k0 < nbt; k0 += kHistUnroll * rpp) {
                 uint4 v[kHistUnroll];
+                int64_t row[kHistUnroll];
                 bool ok[kHistUnroll];
 #pragma unroll
                 for (int u = 0; u < kHistUnroll; ++u) {
                     const int k = k0 + u * rpp + rr;
                     ok[u] = k < nbt;
-                    v[u] = ok[u] ? rec[(int64_t)list[k] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
+                    row[u] = ok[u] ? (int64_t)list[k] : 0;
+                    v[u] = ok[u] ? rec[row[u] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
                 }
 #pragma unroll
                 for (int u = 0; u < kHistUnroll; ++u) {
                     const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                    if (ok[u]) lds_accumulate(lds, v[u], sub, F, ls, pack_gh(gh));
+                    if (ok[u]) Acc::add(lds, s, v[u], sub, F, ls, row[u], gh);
                 }
             }
             __syncthreads();
         }
         __syncthreads();
-        store_partial(s, lds, blk);
+        Acc::store(s, lds, blk);
         __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
     }
 }
@@ -768,6 +837,252 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
     }
 }
 
+// Scan, fp32-gradient path. Same task layout as k_scan. The merge sums the
+// fp64 partials; the sibling is parent - built in fp64 (subtract_histogram,
+// histogram.mojo:3747). Then one thread per child runs the reference's
+// sequential arithmetic of split.find_best_split (split.mojo:601-1360):
+// totals over 8 interleaved lanes reduced pairwise plus the tail, the
+// running left prefix in ascending bin order, and the serial sum over all
+// bins that tree._leaf_value (tree.mojo:1961-1995) uses; every thread then
+// scores its bin's candidates from those prefixes with the reference's gain
+// expression. Given identical histograms the gains are identical; the
+// histograms themselves differ from the reference's only in the rounding of
+// their fp64 sums.
+__global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mode) {
+    __shared__ double cg[2][256], ch[2][256];
+    __shared__ int cc[2][256];
+    __shared__ double pg_[2][256], ph_[2][256];
+    __shared__ int pc_[2][256];
+    __shared__ double accg[256], acch[256];
+    __shared__ int accc[256];
+    __shared__ double s_tg[2], s_th[2], s_sg[2], s_sh[2];
+    __shared__ long long s_tc[2];
+    __shared__ double wgain[8];
+    __shared__ int word[8];
+    __shared__ long long wleft[8];
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
+    const HyperParams &hp = s.hp;
+    const int F = s.n_features, nb = s.n_bins;
+    const size_t hsz = (size_t)F * nb;
+    const int n_items = root_mode ? 1 : s.batch->n_items;
+    const int n_tasks = n_items * F;
+    if ((int)blockIdx.x >= n_tasks) return;
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const double l1 = hp.lambda_l1, l2 = hp.lambda_l2, min_h = hp.min_sum_hessian;
+    const long long min_c = hp.min_data_in_leaf;
+    for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
+        const int j = task / F;
+        const int f = task - j * F;
+        Item it;
+        int64_t m_built, m_sib;
+        if (root_mode) {
+            m_built = root_rows(s);
+            m_sib = 0;
+            it.part_off = 0;
+            const int64_t chk = hist_chunk(s, m_built);
+            it.part_cnt = m_built > 0 ? (int)((m_built + chk - 1) / chk) : 0;
+            it.hist_built = 0;
+            it.hist_sib = 0;
+            it.depth_child = 0;
+        } else {
+            it = s.items[j];
+            const int64_t m = it.end - it.begin;
+            m_built = it.builds_left ? it.n_left : m - it.n_left;
+            m_sib = m - m_built;
+        }
+        // ---- merge (thread -> (bin, half))
+        {
+            const int bin = tid & 255, half = tid >> 8;
+            double g = 0.0, h = 0.0;
+            int c = 0;
+            if (bin < nb) {
+                const size_t pstride = (size_t)F * s.part_stride;
+                const size_t base = (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
+                for (int b = half; b < it.part_cnt; b += 2) {
+                    const size_t at = base + (size_t)b * pstride;
+                    g += s.fpart_g[at];
+                    h += s.fpart_h[at];
+                    c += (int)s.fpart_c[at];
+                }
+            }
+            if (half == 1) {
+                accg[bin] = g;
+                acch[bin] = h;
+                accc[bin] = c;
+            }
+            __syncthreads();
+            if (half == 0) {
+                g += accg[bin];
+                h += acch[bin];
+                c += accc[bin];
+                cg[0][bin] = g;
+                ch[0][bin] = h;
+                cc[0][bin] = c;
+                double sgv = 0.0, shv = 0.0;
+                int scv = 0;
+                if (bin < nb) {
+                    HistF *ob = s.histf + (size_t)it.hist_built * hsz + (size_t)f * nb + bin;
+                    ob->g = g;
+                    ob->h = h;
+                    ob->c = c;
+                    if (!root_mode) {
+                        HistF *pp = s.histf + (size_t)it.hist_sib * hsz + (size_t)f * nb + bin;
+                        sgv = pp->g - g;
+                        shv = pp->h - h;
+                        scv = (int)(pp->c - c);
+                        pp->g = sgv;
+                        pp->h = shv;
+                        pp->c = scv;
+                    }
+                }
+                cg[1][bin] = sgv;
+                ch[1][bin] = shv;
+                cc[1][bin] = scv;
+            }
+            __syncthreads();
+        }
+        const int child = tid >> 8;
+        const int bin = tid & 255;
+        // ---- the reference's sequential sums, one thread per child
+        if ((tid & 255) == 0) {
+            constexpr int W = 8;
+            double lg[W], lh[W];
+            for (int k = 0; k < W; ++k) lg[k] = lh[k] = 0.0;
+            long long tc = 0;
+            int b = 0;
+            while (b + W <= nb) {
+                for (int k = 0; k < W; ++k) {
+                    lg[k] += cg[child][b + k];
+                    lh[k] += ch[child][b + k];
+                    tc += cc[child][b + k];
+                }
+                b += W;
+            }
+            for (int w2 = W / 2; w2 >= 1; w2 >>= 1)
+                for (int k = 0; k < w2; ++k) {
+                    lg[k] = lg[k] + lg[k + w2];
+                    lh[k] = lh[k] + lh[k + w2];
+                }
+            double tg = lg[0], th = lh[0];
+            for (; b < nb; ++b) {
+                tg += cg[child][b];
+                th += ch[child][b];
+                tc += cc[child][b];
+            }
+            double rg = 0.0, rh = 0.0, sg = 0.0, sh = 0.0;
+            int rc = 0;
+            for (int k = 0; k < nb; ++k) {
+                rg += cg[child][k];
+                rh += ch[child][k];
+                rc += cc[child][k];
+                pg_[child][k] = rg;
+                ph_[child][k] = rh;
+                pc_[child][k] = rc;
+                sg += cg[child][k];
+                sh += ch[child][k];
+            }
+            s_tg[child] = tg;
+            s_th[child] = th;
+            s_tc[child] = tc;
+            s_sg[child] = sg;
+            s_sh[child] = sh;
+        }
+        __syncthreads();
+        const double TG = s_tg[child], TH = s_th[child];
+        const long long TC = s_tc[child];
+        const int64_t n_child = child == 0 ? m_built : m_sib;
+        const int mbf = s.missing_bin[f];
+        const bool gated = (root_mode && child == 1) ||
+                           (hp.max_depth > 0 && it.depth_child >= hp.max_depth) ||
+                           n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
+                           !s.feature_mask[(size_t)rd.tree_index * F + f];
+        double best_gain = 0.0;
+        int best_order = 0x7FFFFFFF;
+        long long best_left = 0;
+        if (!gated) {
+            const double mg = mbf >= 0 ? cg[child][mbf] : 0.0, mh = mbf >= 0 ? ch[child][mbf] : 0.0;
+            const long long mc = mbf >= 0 ? cc[child][mbf] : 0;
+            const int n_scan = mbf >= 0 ? mbf : nb;
+            int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
+            if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
+            if (bin < lim) {
+                const double pgs = soft_threshold_l1(TG, l1);
+                const double parent_score = pgs * pgs / (TH + l2);
+                const double lgs = pg_[child][bin], lhs = ph_[child][bin];
+                const long long lcs = pc_[child][bin];
+                if (mbf >= 0) {
+                    const double a = lgs + mg, ah = lhs + mh;
+                    const long long ac = lcs + mc;
+                    const double rg = TG - a, rh = TH - ah;
+                    if (!(ah < min_h || rh < min_h || ac < min_c || TC - ac < min_c)) {
+                        const double tl = soft_threshold_l1(a, l1), tr = soft_threshold_l1(rg, l1);
+                        const double gain = tl * tl / (ah + l2) + tr * tr / (rh + l2) - parent_score;
+                        if (gain > best_gain) {
+                            best_gain = gain;
+                            best_order = 2 * bin;
+                            best_left = ac;
+                        }
+                    }
+                }
+                if (mbf < 0 || mc > 0) {
+                    const double rg = TG - lgs, rh = TH - lhs;
+                    if (!(lhs < min_h || rh < min_h || lcs < min_c || TC - lcs < min_c)) {
+                        const double tl = soft_threshold_l1(lgs, l1), tr = soft_threshold_l1(rg, l1);
+                        const double gain = tl * tl / (lhs + l2) + tr * tr / (rh + l2) - parent_score;
+                        if (gain > best_gain) {
+                            best_gain = gain;
+                            best_order = 2 * bin + 1;
+                            best_left = lcs;
+                        }
+                    }
+                }
+            }
+        }
+        {
+            const int mine = best_order;
+            wave_argmax(best_gain, best_order);
+            const unsigned long long wins = __ballot(mine == best_order && best_order != 0x7FFFFFFF);
+            const int srcl = wins ? (int)__ffsll((long long)wins) - 1 : 0;
+            best_left = __shfl(best_left, srcl, 64);
+        }
+        if (lane == 0) {
+            wgain[wv] = best_gain;
+            word[wv] = best_order;
+            wleft[wv] = best_left;
+        }
+        __syncthreads();
+        if ((tid & 255) == 0 && !(root_mode && child == 1)) {
+            double bgn = wgain[child << 2];
+            int bo = word[child << 2];
+            long long bleft = wleft[child << 2];
+            for (int k = 1; k < 4; ++k) {
+                const double og = wgain[(child << 2) + k];
+                const int oo = word[(child << 2) + k];
+                if (og > bgn || (og == bgn && oo < bo)) {
+                    bgn = og;
+                    bo = oo;
+                    bleft = wleft[(child << 2) + k];
+                }
+            }
+            ScanResult rs;
+            rs.gain = bgn;
+            rs.found = bo != 0x7FFFFFFF;
+            rs.bin = rs.found ? bo >> 1 : -1;
+            rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
+            rs.pad_ = 0;
+            rs.tot_g = 0;
+            rs.tot_h = 0;
+            rs.tot_c = TC;
+            rs.n_left = rs.found ? bleft : 0;
+            rs.fg = s_sg[child];
+            rs.fh = s_sh[child];
+            s.scan[(size_t)(j * 2 + child) * F + f] = rs;
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------ planner
 // Single block of kPlanThreads, after every scan launch.
 //
@@ -866,7 +1181,7 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
 __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode) {
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
-    __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x;
+    __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x, s_vf;
     __shared__ unsigned long long s_rows_built, s_rows_parted, s_rows_total;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
@@ -907,6 +1222,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s_rows_built = 0;
         s_rows_parted = 0;
         s_ncand = 0;
+        int vf = 0;
+        while (vf < F - 1 && !s.feature_mask[(size_t)rd.tree_index * F + vf]) ++vf;
+        s_vf = vf;
     }
     // ---- 1. fold (loads of every (pair, feature) gain, then one wave per pair)
     const int n_pairs = root_mode ? 1 : 2 * n_items;
@@ -954,6 +1272,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
         const ScanResult *base = &s.scan[(size_t)pr * F];
         const long long G = base->tot_g, H = base->tot_h, C = base->tot_c;
+        // leaf value: integer sums are the same on every feature; the fp32
+        // path sums the tree's first selected feature serially, as
+        // tree._leaf_value does (value_feature = tree_features[0])
+        const double value = hp.quantized ? qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2)
+                                          : -soft_threshold_l1(base[s_vf].fg, hp.lambda_l1) /
+                                                (base[s_vf].fh + hp.lambda_l2);
         ENode *e = &s.enodes[e_id];
         if (root_mode) {
             e->begin = 0;
@@ -964,13 +1288,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             e->left_e = -1;
             e->right_e = -1;
             e->pad_ = 0;
-            s.t_value[0] = qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2);
+            s.t_value[0] = value;
             s.t_count[0] = (double)C;
         }
         e->tot_g = G;
         e->tot_h = H;
         e->tot_c = C;
-        e->value = qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2);
+        e->value = value;
         const int bf = v.wf[pr];
         const bool found = bf != 0x7FFFFFFF;
         e->found = found ? 1 : 0;
@@ -1489,8 +1813,14 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
 size_t score_lds_bytes(const DevState &s) {
     return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
 }
-size_t hist_lds_bytes(const DevState &s) { return (size_t)s.n_features * s.lds_stride * 8; }
-size_t pb_lds_bytes(const DevState &s) { return pb_lds_bytes_of(s.n_features, s.lds_stride); }
+size_t hist_lds_bytes(const DevState &s) {
+    return s.hp.quantized ? QAcc::lds_bytes(s.n_features, s.lds_stride)
+                          : FAcc::lds_bytes(s.n_features, s.lds_stride);
+}
+size_t pb_lds_bytes(const DevState &s) {
+    return s.hp.quantized ? pb_lds_bytes_of<QAcc>(s.n_features, s.lds_stride)
+                          : pb_lds_bytes_of<FAcc>(s.n_features, s.lds_stride);
+}
 size_t plan_lds_bytes(const DevState &s) {
     return plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features).total;
 }
@@ -1504,45 +1834,67 @@ size_t plan_lds_bytes(const DevState &s) {
 
 hipError_t prepare_kernels(const DevState &s) {
     const size_t h = hist_lds_bytes(s), pb = pb_lds_bytes(s);
-    MB_SET_LDS(k_hist<1>, h);
-    MB_SET_LDS(k_hist<2>, h);
-    MB_SET_LDS(k_hist<4>, h);
-    MB_SET_LDS(k_hist<8>, h);
-    MB_SET_LDS(k_part_hist<1>, pb);
-    MB_SET_LDS(k_part_hist<2>, pb);
-    MB_SET_LDS(k_part_hist<4>, pb);
-    MB_SET_LDS(k_part_hist<8>, pb);
+    if (s.hp.quantized) {
+        MB_SET_LDS((k_hist<1, QAcc>), h);
+        MB_SET_LDS((k_hist<2, QAcc>), h);
+        MB_SET_LDS((k_hist<4, QAcc>), h);
+        MB_SET_LDS((k_hist<8, QAcc>), h);
+        MB_SET_LDS((k_part_hist<1, QAcc>), pb);
+        MB_SET_LDS((k_part_hist<2, QAcc>), pb);
+        MB_SET_LDS((k_part_hist<4, QAcc>), pb);
+        MB_SET_LDS((k_part_hist<8, QAcc>), pb);
+    } else {
+        MB_SET_LDS((k_hist<1, FAcc>), h);
+        MB_SET_LDS((k_hist<2, FAcc>), h);
+        MB_SET_LDS((k_hist<4, FAcc>), h);
+        MB_SET_LDS((k_hist<8, FAcc>), h);
+        MB_SET_LDS((k_part_hist<1, FAcc>), pb);
+        MB_SET_LDS((k_part_hist<2, FAcc>), pb);
+        MB_SET_LDS((k_part_hist<4, FAcc>), pb);
+        MB_SET_LDS((k_part_hist<8, FAcc>), pb);
+    }
     MB_SET_LDS(k_plan, plan_lds_bytes(s));
     MB_SET_LDS(k_score, score_lds_bytes(s));
     return hipSuccess;
 }
-hipError_t launch_hist(const DevState &s, hipStream_t st) {
+template <class Acc>
+hipError_t launch_hist_t(const DevState &s, hipStream_t st) {
     const size_t lds = hist_lds_bytes(s);
     const dim3 grid(s.hist_grid), block(1024);
     switch (s.rec_bytes / 16) {
-    case 1: hipLaunchKernelGGL(k_hist<1>, grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL(k_hist<2>, grid, block, lds, st, s); break;
-    case 4: hipLaunchKernelGGL(k_hist<4>, grid, block, lds, st, s); break;
-    case 8: hipLaunchKernelGGL(k_hist<8>, grid, block, lds, st, s); break;
+    case 1: hipLaunchKernelGGL((k_hist<1, Acc>), grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL((k_hist<2, Acc>), grid, block, lds, st, s); break;
+    case 4: hipLaunchKernelGGL((k_hist<4, Acc>), grid, block, lds, st, s); break;
+    case 8: hipLaunchKernelGGL((k_hist<8, Acc>), grid, block, lds, st, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+hipError_t launch_hist(const DevState &s, hipStream_t st) {
+    return s.hp.quantized ? launch_hist_t<QAcc>(s, st) : launch_hist_t<FAcc>(s, st);
+}
+template <class Acc>
+hipError_t launch_part_hist_t(const DevState &s, hipStream_t st) {
+    const size_t lds = pb_lds_bytes(s);
+    const dim3 grid(s.pb_launch), block(kPbThreads);
+    switch (s.rec_bytes / 16) {
+    case 1: hipLaunchKernelGGL((k_part_hist<1, Acc>), grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL((k_part_hist<2, Acc>), grid, block, lds, st, s); break;
+    case 4: hipLaunchKernelGGL((k_part_hist<4, Acc>), grid, block, lds, st, s); break;
+    case 8: hipLaunchKernelGGL((k_part_hist<8, Acc>), grid, block, lds, st, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 hipError_t launch_part_hist(const DevState &s, hipStream_t st) {
-    const size_t lds = pb_lds_bytes(s);
-    const dim3 grid(s.pb_launch), block(kPbThreads);
-    switch (s.rec_bytes / 16) {
-    case 1: hipLaunchKernelGGL(k_part_hist<1>, grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL(k_part_hist<2>, grid, block, lds, st, s); break;
-    case 4: hipLaunchKernelGGL(k_part_hist<4>, grid, block, lds, st, s); break;
-    case 8: hipLaunchKernelGGL(k_part_hist<8>, grid, block, lds, st, s); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    return s.hp.quantized ? launch_part_hist_t<QAcc>(s, st) : launch_part_hist_t<FAcc>(s, st);
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     const int grid = root_mode ? s.n_features : s.scan_grid;
-    hipLaunchKernelGGL(k_scan, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    if (s.hp.quantized)
+        hipLaunchKernelGGL(k_scan, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    else
+        hipLaunchKernelGGL(k_scan_f, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
     return hipGetLastError();
 }
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st) {

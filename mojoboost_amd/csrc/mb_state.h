@@ -84,8 +84,15 @@ struct Grow {
 struct ScanResult {
     double gain;
     int32_t bin, default_left, found, pad_;
-    int64_t tot_g, tot_h, tot_c;
+    int64_t tot_g, tot_h, tot_c;  // integer sums (quantized path; tot_c on both)
     int64_t n_left;  // rows left of the candidate
+    double fg, fh;   // fp64 serial sums over the feature's bins (fp32 path's leaf value)
+};
+
+// One cell of an fp64 histogram (fp32 gradient path).
+struct HistF {
+    double g, h;
+    int64_t c;
 };
 
 // Per-round values shared by the kernels of one tree, advanced on the device
@@ -112,6 +119,8 @@ struct HyperParams {
     int32_t quant_seed;
     int32_t const_hessian;
     int32_t bagging;        // 1: rows sampled per bag
+    int32_t quantized;      // 1: int8 gradients, integer histograms; 0: fp32 gradients, fp64 sums
+    int32_t pad_hp_;
     int32_t bagging_freq;
     int32_t bagging_seed;
     double bagging_fraction;
@@ -144,6 +153,9 @@ struct DevState {
     int32_t *rows0, *rows1;
     int32_t *hist;         // (1 + max_exp) x F x n_bins x 3 (grad, hess, count)
     unsigned long long *part;  // max(hist_grid, pb_grid) x F x part_stride packed partials
+    HistF *histf;              // fp32 path: (1 + max_exp) x F x n_bins cells
+    double *fpart_g, *fpart_h; // fp32 path partials, same shape as part
+    uint32_t *fpart_c;
     int32_t hist_grid;         // blocks of a histogram launch
     int32_t part_stride;       // per-feature stride of a partial (even, >= n_bins)
     int64_t hist_chunk_min;    // fewest rows a histogram block takes

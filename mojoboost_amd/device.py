@@ -87,6 +87,19 @@ class Dataset:
                                   0 if r is None else len(r), quant_bins, ptr(out), err, 1024), err)
         return out.reshape(self.n_features, self.n_bins, 3)
 
+    def histogram_fp32(self, grad, hess, rows=None):
+        """fp64 sums of fp32 grad/hess per (feature, bin), and counts."""
+        cells = self.n_features * self.n_bins
+        gh = np.zeros(2 * cells)
+        cnt = np.zeros(cells, np.int64)
+        g = np.ascontiguousarray(grad, np.float32)
+        h = np.ascontiguousarray(hess, np.float32)
+        r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_histogram_fp32(self.h, ptr(g), ptr(h), ptr(r), 0 if r is None else len(r),
+                                       ptr(gh), ptr(cnt), err, 1024), err)
+        return gh, cnt
+
     def bench_root_histogram(self, reps=20):
         """(mean, min) histogram-kernel ms and mean histogram + merge ms of a
         root build over all rows."""

@@ -133,7 +133,7 @@ class _Base:
     def __init__(self, n_estimators=100, learning_rate=0.1, num_leaves=31, max_depth=-1,
                  min_child_samples=20, min_child_weight=1e-3, reg_alpha=0.0, reg_lambda=1.0,
                  colsample_bytree=1.0, subsample=1.0, subsample_freq=0, max_bin=255,
-                 random_state=None, device="gpu", use_quantized_grad=True,
+                 random_state=None, device="gpu", use_quantized_grad=False,
                  num_grad_quant_bins=4, stochastic_rounding=True):
         self.n_estimators = n_estimators
         self.learning_rate = learning_rate

@@ -90,7 +90,6 @@ def test_train_argument_errors():
     ("device=cpu", _lib.ERROR_UNSUPPORTED),
     ("boosting=goss", _lib.ERROR_UNSUPPORTED),
     ("objective=poisson", _lib.ERROR_UNSUPPORTED),
-    ("use_quantized_grad=false", _lib.ERROR_UNSUPPORTED),
 ])
 def test_parameter_string_errors(params, code):
     rc, msg, h = _train(params)

@@ -181,11 +181,11 @@ def test_estimator_through_c_abi_bit_exact(dev, tmp_path, objective):
     if objective == "binary":
         y = (rng.uniform(size=n) < 1 / (1 + np.exp(-z))).astype(np.float64)
         est = MojoTreesClassifier(n_estimators=6, num_leaves=31, learning_rate=0.1,
-                                  max_bin=63, device="gpu")
+                                  max_bin=63, device="gpu", use_quantized_grad=True)
     else:
         y = z + 0.1 * rng.normal(size=n)
         est = MojoTreesRegressor(n_estimators=6, num_leaves=31, learning_rate=0.1,
-                                 max_bin=63, device="gpu")
+                                 max_bin=63, device="gpu", use_quantized_grad=True)
     est.fit(X, y)
     raw = est.decision_function(X) if objective == "binary" else est.predict(X)
 
@@ -251,7 +251,7 @@ def test_estimator_multiclass_through_c_abi_bit_exact(dev, tmp_path):
     scores = X[:, :K] * 1.5 + rng.gumbel(size=(n, K))
     y = np.array(["a", "b", "c", "d"])[scores.argmax(axis=1)]
     est = MojoTreesClassifier(n_estimators=3, num_leaves=15, learning_rate=0.2, max_bin=63,
-                              device="gpu").fit(X, y)
+                              device="gpu", use_quantized_grad=True).fit(X, y)
     raw = est.decision_function(X)
     assert raw.shape == (n, K) and list(est.classes_) == ["a", "b", "c", "d"]
 
@@ -288,3 +288,81 @@ def test_stop_rule_constant_labels(dev):
     ref = O.train(bins.ravel(), n, 3, 16, y, O.default_params(**kw, use_quantized_grad=1))
     assert fit.n_trees == ref.n_trees == 0
     assert np.array_equal(bits(fit.train_raw()), bits(ref.train_raw(n)))
+
+
+# ---------------------------------------------------------------- fp32 path
+# Bar: fp32 histograms within 1e-5 relative of
+# the reference's Float64 histograms, predictions after 100 trees within 1e-5
+# relative. The device sums the fp32 gradient values in fp64 with atomics, so
+# only the order (and with it the last bits) of the additions differs.
+
+def test_histogram_fp32_matches_oracle(dev):
+    n, f, nb = 300_000, 20, 64
+    rng = np.random.default_rng(31)
+    bins = rng.integers(0, nb, size=(f, n), dtype=np.uint8)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.01, 1.0, size=n).astype(np.float32)
+    ds = dev.Dataset(bins.ravel(), n, f, nb, np.zeros(n))
+    L = O.lib()
+    for rows in (None, np.sort(rng.choice(n, size=n // 3, replace=False)).astype(np.int32)):
+        gh, cnt = ds.histogram_fp32(g, h, rows)
+        want_gh = np.zeros(2 * f * nb)
+        want_c = np.zeros(f * nb, np.int64)
+        r = None if rows is None else rows
+        L.orc_hist_float(O._ptr(bins.ravel()), n, f, nb, O._ptr(g.astype(np.float64)),
+                         O._ptr(h.astype(np.float64)), O._ptr(r), 0 if r is None else len(r), 1,
+                         O._ptr(want_gh), O._ptr(want_c))
+        assert np.array_equal(cnt, want_c)
+        # per cell, the rounding of a different summation order is bounded by
+        # n_cell * eps * sum |x|; 1e-12 of the cell's magnitude is far inside
+        # the 1e-5 bar
+        scale = np.maximum(np.abs(want_gh), 1e-30)
+        rel = np.abs(gh - want_gh) / scale
+        assert rel.max() < 1e-10, rel.max()
+
+
+def _rel_err(a, b):
+    return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), 1e-12)))
+
+
+def _tree_agreement(fit, ref):
+    same = 0
+    for t in range(min(fit.n_trees, ref.n_trees)):
+        a, b = fit.tree(t), ref.tree(t)
+        same += int(all(np.array_equal(a[k], b[k]) for k in ("feature", "threshold", "left", "right")))
+    return same
+
+
+def test_training_fp32_c1(dev):
+    """C1 (the reference's CPU-runnable case):
+    100k x 28 N(0,1), y = x.w + 0.1 N(0,1), L2, 255 bins, 31 leaves, lr 0.1,
+    100 trees, fp32 gradients."""
+    n, f = 100_000, 28
+    rng = np.random.default_rng(0x5EED0001)
+    x = rng.normal(size=(f, n)).astype(np.float32).astype(np.float64)
+    w = rng.uniform(-1.0, 1.0, size=f)
+    y = w @ x + 0.1 * rng.normal(size=n)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=255)
+    kw = dict(objective=0, num_iterations=100, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, f, 255, y, missing_bin=mb)
+    fit = ds.train(use_quantized_grad=0, **kw)
+    ref = O.train(bins, n, f, 255, y, O.default_params(**kw, use_quantized_grad=0), missing_bin=mb)
+    assert fit.n_trees == ref.n_trees == 100
+    assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+    raw, _ = ref.predict_binned(bins, n, f)
+    assert _rel_err(fit.train_raw(), raw) < 1e-5
+    assert _tree_agreement(fit, ref) >= 95
+
+
+def test_training_fp32_binary_bagging(dev):
+    n = 150_000
+    bins, y, mb, nb = c2_like(n, f=16)
+    kw = dict(objective=1, num_iterations=20, num_leaves=63, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.1, bagging_fraction=0.8, bagging_freq=1, bagging_seed=5)
+    ds = dev.Dataset(bins, n, 16, nb, y, missing_bin=mb)
+    fit = ds.train(use_quantized_grad=0, **kw)
+    ref = O.train(bins, n, 16, nb, y, O.default_params(**kw, use_quantized_grad=0), missing_bin=mb)
+    assert fit.n_trees == ref.n_trees
+    assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+    assert _tree_agreement(fit, ref) >= ref.n_trees - 1
