@@ -63,6 +63,10 @@ typedef struct {
     int32_t time_histograms; /* 1: bracket each histogram launch with events */
     int32_t use_quantized_grad; /* 1: int8 gradients, integer histograms;
                                    0: fp32 gradients, fp64 histogram sums */
+    int32_t goss;               /* 1: gradient-based one-side sampling after
+                                   floor(1 / learning_rate) rounds, stream
+                                   keyed by bagging_seed */
+    double top_rate, other_rate;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the

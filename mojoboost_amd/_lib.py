@@ -60,6 +60,9 @@ class MbhParams(C.Structure):
         ("quant_seed", C.c_int32),
         ("time_histograms", C.c_int32),
         ("use_quantized_grad", C.c_int32),
+        ("goss", C.c_int32),
+        ("top_rate", C.c_double),
+        ("other_rate", C.c_double),
     ]
 
 
@@ -69,7 +72,8 @@ def mbh_params(**kw) -> MbhParams:
                   lambda_l2=1.0, min_sum_hessian=1e-3, max_depth=-1, feature_fraction=1.0,
                   feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
-                  quant_seed=11, time_histograms=0, use_quantized_grad=1)
+                  quant_seed=11, time_histograms=0, use_quantized_grad=1, goss=0,
+                  top_rate=0.2, other_rate=0.1)
     for k, v in kw.items():
         setattr(p, k, v)
     return p

@@ -154,6 +154,9 @@ Config parse(const char *spec) {
     // (src/mojotrees/boosting.mojo:1611, src/mojotrees/tree.mojo:284)
     p.objective = MBH_OBJ_REGRESSION;
     p.num_class = 1;
+    p.goss = 0;
+    p.top_rate = 0.2;    // LightGBM / GossParams defaults
+    p.other_rate = 0.1;
     p.num_iterations = 100;
     p.learning_rate = 0.1;
     p.num_leaves = 31;
@@ -247,11 +250,13 @@ Config parse(const char *spec) {
             p.bagging_seed = (int)to_int(k, val);
         } else if (k == "boosting") {
             if (val == "goss")
-                throw ApiError{MOJOTREES_ERROR_UNSUPPORTED, "boosting=goss is not built on the device path yet"};
-            if (val != "gbdt" && val != "gbrt")
+                p.goss = 1;
+            else if (val != "gbdt" && val != "gbrt")
                 throw ApiError{MOJOTREES_ERROR_UNSUPPORTED, "boosting=" + val + " is not served by this library"};
-        } else if (k == "top_rate" || k == "other_rate") {
-            (void)to_double(k, val);
+        } else if (k == "top_rate") {
+            p.top_rate = to_double(k, val);
+        } else if (k == "other_rate") {
+            p.other_rate = to_double(k, val);
         } else if (k == "min_data_in_bin") {
             c.min_data_in_bin = (int)to_int(k, val);
         } else if (k == "bin_construct_sample_cnt") {
@@ -267,6 +272,20 @@ Config parse(const char *spec) {
         p.num_class = c.num_class;
     }
     p.use_quantized_grad = c.quantized ? 1 : 0;
+    if (p.goss) {
+        // GossParams.validate (goss.mojo:129-145) and _check_goss (boosting.mojo:346-355)
+        const double tr = p.top_rate, orr = p.other_rate;
+        if (!(tr >= 0.0 && tr <= 1.0)) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss top_rate must be in [0, 1]"};
+        if (!(orr >= 0.0 && orr <= 1.0))
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss other_rate must be in [0, 1]"};
+        if (!(tr + orr <= 1.0))
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss top_rate + other_rate must not exceed 1"};
+        if (!(tr + orr > 0.0))
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss top_rate + other_rate must be positive"};
+        if (p.bagging_seed < 0) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss seed must be nonnegative"};
+        if (p.bagging_freq > 0 && p.bagging_fraction < 1.0)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "goss and bagging cannot both be enabled"};
+    }
     if (c.max_bin < 2 || c.max_bin > 256) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "max_bin must be in [2, 256]"};
     return c;
 }

@@ -202,6 +202,17 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         if ((double)ds->n * (double)(B + 1) >= 2147483647.0)
             unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
     }
+    if (p->goss) {
+        if (p->use_quantized_grad)
+            unsup("GOSS with quantized gradients is not built on the device path yet (use_quantized_grad=false)");
+        if (p->objective == MBH_OBJ_MULTICLASS) unsup("GOSS with multiclass is not built on the device path yet");
+        // GossParams.validate (goss.mojo:129-145), _check_goss (boosting.mojo:346-355)
+        if (p->bagging_freq > 0 && p->bagging_fraction < 1.0) bad("goss and bagging cannot both be enabled");
+        if (!(p->top_rate >= 0.0 && p->top_rate <= 1.0) || !(p->other_rate >= 0.0 && p->other_rate <= 1.0) ||
+            !(p->top_rate + p->other_rate <= 1.0) || !(p->top_rate + p->other_rate > 0.0))
+            bad("goss needs top_rate and other_rate in [0, 1] with 0 < top_rate + other_rate <= 1");
+        if (p->bagging_seed < 0) bad("goss seed (bagging_seed) must be nonnegative");
+    }
     if (p->objective == MBH_OBJ_BINARY && (ds->label_min < 0.0 || ds->label_max > 1.0))
         bad("binary labels must be in [0, 1]");
 }
@@ -348,6 +359,22 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     // boosting.round_has_constant_hessian: squared error without weights.
     hp.const_hessian = p->objective == MBH_OBJ_REGRESSION ? 1 : 0;
     hp.quantized = p->use_quantized_grad ? 1 : 0;
+    hp.goss = p->goss ? 1 : 0;
+    // GossParams.warmup (goss.mojo:102-157): floor(1 / learning_rate) rounds
+    hp.goss_warm = p->learning_rate > 0.0 ? (int32_t)(1.0 / p->learning_rate) : 0;
+    hp.goss_seed = p->bagging_seed;
+    hp.top_rate = p->top_rate;
+    hp.other_rate = p->other_rate;
+    if (hp.goss) {
+        s.goss_nblk = (int32_t)((ds->n + 1023) / 1024);
+        s.gst = dalloc<mb::GossState>(1, run.owned);
+        s.goss_hist = dalloc<uint32_t>(8 * 256, run.owned);
+        s.goss_kappa = dalloc<int32_t>(ds->n, run.owned);
+        s.goss_mask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
+        s.goss_blk = dalloc<int32_t>(s.goss_nblk, run.owned);
+        s.goss_other = dalloc<uint8_t>(ds->n, run.owned);
+        HIPX(hipMemset(s.goss_other, 0, ds->n));
+    }
     hp.bagging = (p->bagging_freq > 0 && p->bagging_fraction < 1.0) ? 1 : 0;
     hp.bagging_freq = p->bagging_freq;
     hp.bagging_seed = p->bagging_seed;
@@ -376,7 +403,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));
     HIPX(hipMemset(s.arc_aux, 0, (size_t)T * 4 * sizeof(int64_t)));
     HIPX(hipMemset(s.arc_int, 0, (size_t)T * (6 * max_nodes + 2) * sizeof(int32_t)));
-    mb::Round r0{};
+    mb::Round r0 = mb::initial_round();
     HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
     std::vector<uint8_t> masks((size_t)T * F);
     for (int t = 0; t < T; ++t) {
@@ -562,6 +589,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             if (K > 1 && t % K == 0) HIPX(mb::launch_softmax(s, grid_rows, st));
             HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
+            if (s.hp.goss) HIPX(mb::launch_goss(s, st));
             if (timed) HIPX(hipEventRecord(events[2], st));
             HIPX(mb::launch_hist(s, st));
             if (timed) HIPX(hipEventRecord(events[3], st));
@@ -634,7 +662,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         fit->train_raw.resize((size_t)ds->n * K);
         HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
                        hipMemcpyDeviceToHost));
-        const bool bagging = s.hp.bagging != 0;
+        const bool bagging = s.hp.bagging != 0 || s.hp.goss != 0;  // sampled rounds are skipped, not stops
         const double rb = ds->F + 2;
         double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
         double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
@@ -800,7 +828,7 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const doubl
         p1.num_iterations = 1;
         TrainBuffers tb = setup_state(ds, &p1, run);
         mb::DevState &s = tb.s;
-        mb::Round r0{};
+        mb::Round r0 = mb::initial_round();
         r0.round = round_index;
         HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(s.raw, raw, ds->n * sizeof(double), hipMemcpyHostToDevice));
@@ -865,12 +893,12 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
         const size_t cells = (size_t)ds->F * ds->nb * 3;
         // unit lattice scales: the root split's gains are not read here, only
         // the histogram it merges into buffer 0
-        mb::Round r0{};
+        mb::Round r0 = mb::initial_round();
         r0.grad_units = 1.0;
         r0.hess_units = 1.0;
+        r0.sampled = rows ? 1 : 0;  // root range = rows0[0 .. cursor[0])
         HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
         if (rows) {
-            s.hp.bagging = 1;  // root range = rows0[0 .. cursor[0])
             HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
             int64_t c[2] = {n_sel, 0};
             HIPX(hipMemcpy(s.cursor, c, sizeof(c), hipMemcpyHostToDevice));
@@ -912,8 +940,10 @@ int32_t mbh_histogram_fp32(mbh_dataset *ds, const float *grad, const float *hess
         mb::DevState &s = tb.s;
         HIPX(hipMemcpy(s.grad, grad, ds->n * sizeof(float), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(s.hess, hess, ds->n * sizeof(float), hipMemcpyHostToDevice));
+        mb::Round r0 = mb::initial_round();
+        r0.sampled = rows ? 1 : 0;  // root range = rows0[0 .. cursor[0])
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
         if (rows) {
-            s.hp.bagging = 1;  // root range = rows0[0 .. cursor[0])
             HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
             int64_t c = n_sel;
             HIPX(hipMemcpy(s.cursor, &c, sizeof(c), hipMemcpyHostToDevice));
@@ -957,7 +987,7 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         p.use_quantized_grad = 1;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
-        mb::Round r0{};
+        mb::Round r0 = mb::initial_round();
         r0.grad_units = 1.0;
         r0.hess_units = 1.0;
         HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));

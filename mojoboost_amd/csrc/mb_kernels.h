@@ -9,6 +9,8 @@ namespace mb {
 
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st);
+// The GOSS selection of the round (no-ops before the warmup ends).
+hipError_t launch_goss(const DevState &s, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 // Raises the dynamic LDS limits of the kernels that need more than 64 KB.
 hipError_t prepare_kernels(const DevState &s);

@@ -248,6 +248,8 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const bool stoch = hp.stochastic != 0;
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
+        s.round->sampled = hp.bagging;
+        s.round->goss_mult = 1.0;
         s.round->grad_units = gu;
         s.round->hess_units = hu;
         s.stats[(1 - rd.parity) * 2 + 0] = 0u;
@@ -283,6 +285,272 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     }
 }
 
+// -------------------------------------------------------------------- GOSS
+// goss_round (src/mojotrees/goss.mojo:294-396), from round floor(1 / lr) on
+// (GossParams.warmup, :102-157): importance |g h| of the fp32 derivatives in
+// fp64, the top_k-th largest importance as threshold (every row at or above
+// it is kept), then selection sampling of the other rows in row order --
+// row r is kept with probability (other_k - kept) / rest with rest =
+// (n - r) - (top_k - tops before r), drawn as uniform(stream + r) -- and
+// the kept rows' g and h weighted by (n - top_k) / other_k.
+//
+// The selection sampling is a sequential count: row r is kept iff the
+// number kept before it is below kappa_r, the least count at which the
+// reference's comparison u_r < (other_k - count) / rest fails (found from
+// the same double expression, so the decisions are the reference's). A
+// single wave then runs the count over 64 rows at a time: a row whose kappa
+// is at most the count is dropped and one whose kappa exceeds the count by
+// 64 or more is kept whatever the rows before it do, so a step costs a
+// ballot and a popcount; only steps with a kappa inside that window take the
+// 64 rows one by one.
+__device__ __forceinline__ bool goss_on(const DevState &s) {
+    const Round &rd = *s.round;
+    return s.hp.goss && !rd.stopped && rd.round >= s.hp.goss_warm;
+}
+
+__device__ __forceinline__ unsigned long long goss_key(const DevState &s, int64_t r) {
+    const double imp = fabs((double)s.grad[r] * (double)s.hess[r]);
+    return (unsigned long long)__double_as_longlong(imp);  // non-negative: ordered like its bits
+}
+
+__global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
+    if (!goss_on(s)) return;
+    for (int i = threadIdx.x; i < 8 * 256; i += blockDim.x) s.goss_hist[i] = 0u;
+    if (threadIdx.x == 0) {
+        GossState g;
+        const int64_t n = s.n;
+        int64_t top_k = (int64_t)((double)n * s.hp.top_rate);
+        if (top_k < 1) top_k = 1;
+        if (top_k > n) top_k = n;
+        int64_t other_k = (int64_t)((double)n * s.hp.other_rate);
+        if (other_k > n - top_k) other_k = n - top_k;
+        g.prefix = 0ULL;
+        g.rank = top_k - 1;
+        g.top_k = top_k;
+        g.other_k = other_k;
+        g.threshold = 0.0;
+        g.kept_other = 0;
+        g.bag_n = 0;
+        *s.gst = g;
+    }
+}
+
+// Radix select of the top_k-th largest key, 8 bits per pass from the top.
+__global__ __launch_bounds__(256) void k_goss_digits(DevState s, int pass) {
+    __shared__ uint32_t hist[256];
+    if (!goss_on(s)) return;
+    hist[threadIdx.x] = 0u;
+    __syncthreads();
+    const unsigned long long prefix = s.gst->prefix;
+    const int shift = 56 - 8 * pass;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
+        const unsigned long long key = goss_key(s, r);
+        if (pass == 0 || (key >> (shift + 8)) == (prefix >> (shift + 8)))
+            atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    const uint32_t v = hist[threadIdx.x];
+    if (v) atomicAdd(&s.goss_hist[pass * 256 + threadIdx.x], v);
+}
+
+__global__ void k_goss_pick(DevState s, int pass) {
+    if (!goss_on(s) || threadIdx.x != 0) return;
+    GossState g = *s.gst;
+    const uint32_t *h = s.goss_hist + pass * 256;
+    int64_t above = 0;
+    int d = 255;
+    for (; d > 0; --d) {
+        if (g.rank < above + (int64_t)h[d]) break;
+        above += h[d];
+    }
+    g.rank -= above;
+    g.prefix |= (unsigned long long)d << (56 - 8 * pass);
+    if (pass == 7) g.threshold = __longlong_as_double((long long)g.prefix);
+    *s.gst = g;
+}
+
+// Blocks of 1024 rows: count of top rows (mode 0) or of rows in the sample
+// (mode 1) per block.
+__device__ __forceinline__ bool goss_top(const DevState &s, int64_t r, unsigned long long thr_bits) {
+    return goss_key(s, r) >= thr_bits;
+}
+
+__global__ __launch_bounds__(1024) void k_goss_count(DevState s, int mode) {
+    __shared__ int wsum[16];
+    if (!goss_on(s)) return;
+    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    bool in = false;
+    if (r < s.n) {
+        if (mode == 0) {
+            in = goss_top(s, r, (unsigned long long)__double_as_longlong(s.gst->threshold));
+        } else {
+            in = s.goss_kappa[r] == INT_MIN || ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
+        }
+    }
+    const unsigned long long b = __ballot(in);
+    if (lane_id() == 0) wsum[threadIdx.x >> 6] = __popcll(b);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t = 0;
+        for (int i = 0; i < 16; ++i) t += wsum[i];
+        s.goss_blk[blockIdx.x] = t;
+    }
+}
+
+// Exclusive prefix of the per-block counts, in place (one block); mode 1
+// also records the sample size.
+__global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int mode) {
+    __shared__ long long part[1024];
+    if (!goss_on(s)) return;
+    const int nb = s.goss_nblk;
+    const int per = (nb + 1023) / 1024;
+    const int lo = threadIdx.x * per;
+    const int hi = lo + per < nb ? lo + per : nb;
+    long long sum = 0;
+    for (int i = lo; i < hi; ++i) sum += s.goss_blk[i];
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long acc = 0;
+        for (int i = 0; i < 1024; ++i) {
+            const long long v = part[i];
+            part[i] = acc;
+            acc += v;
+        }
+        if (mode == 1) s.gst->bag_n = acc;
+    }
+    __syncthreads();
+    long long acc = part[threadIdx.x];
+    for (int i = lo; i < hi; ++i) {
+        const int v = s.goss_blk[i];
+        s.goss_blk[i] = (int32_t)acc;
+        acc += v;
+    }
+}
+
+// In-block exclusive prefix of a flag (1024 threads, one row each).
+__device__ __forceinline__ int block_excl_prefix(bool flag, int *wsum) {
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const unsigned long long b = __ballot(flag);
+    if (lane == 0) wsum[w] = __popcll(b);
+    __syncthreads();
+    int before = 0;
+    for (int i = 0; i < w; ++i) before += wsum[i];
+    return before + __popcll(b & ((1ULL << lane) - 1ULL));
+}
+
+__global__ __launch_bounds__(1024) void k_goss_kappa(DevState s) {
+    __shared__ int wsum[16];
+    if (!goss_on(s)) return;
+    const GossState g = *s.gst;
+    const int64_t n = s.n;
+    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const unsigned long long thr = (unsigned long long)__double_as_longlong(g.threshold);
+    const bool top = r < n && goss_top(s, r, thr);
+    const int pre = block_excl_prefix(top, wsum);
+    if (r >= n) return;
+    if (top) {
+        s.goss_kappa[r] = INT_MIN;
+        return;
+    }
+    const int64_t n_top = (int64_t)s.goss_blk[blockIdx.x] + pre;
+    const int64_t rest = (n - r) - (g.top_k - n_top);
+    const int64_t K = g.other_k;
+    int64_t kappa;
+    if (rest <= 0) {
+        kappa = K;  // the reference keeps the row iff rows are still needed
+    } else {
+        const uint64_t stream = splitmix64((uint64_t)(s.hp.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
+                                           ((uint64_t)s.round->round * kGolden));
+        const double u = uniform53(stream + (uint64_t)r);
+        auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
+        int64_t c = (int64_t)floor((double)K - u * (double)rest);
+        if (c < 0) c = 0;
+        if (c > K) c = K;
+        while (c > 0 && !keep(c - 1)) --c;
+        while (c < K && keep(c)) ++c;
+        kappa = c;
+    }
+    s.goss_kappa[r] = (int32_t)kappa;
+}
+
+// One block; wave 0 runs the count while the other waves stage the next
+// tile of kappa values into LDS.
+constexpr int kGossTile = 16384;
+
+__global__ __launch_bounds__(1024) void k_goss_walk(DevState s) {
+    extern __shared__ int32_t gbuf[];  // 2 x kGossTile
+    if (!goss_on(s)) return;
+    const int64_t n = s.n;
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const int64_t tiles = (n + kGossTile - 1) / kGossTile;
+    for (int i = threadIdx.x; i < kGossTile; i += blockDim.x) gbuf[i] = i < n ? s.goss_kappa[i] : INT_MIN;
+    __syncthreads();
+    long long cnt = 0;
+    for (int64_t t = 0; t < tiles; ++t) {
+        int32_t *cur = gbuf + (t & 1) * kGossTile;
+        if (w != 0 && t + 1 < tiles) {
+            int32_t *nxt = gbuf + ((t + 1) & 1) * kGossTile;
+            const int64_t base = (t + 1) * kGossTile;
+            for (int i = threadIdx.x - 64; i < kGossTile; i += blockDim.x - 64) {
+                const int64_t r = base + i;
+                nxt[i] = r < n ? s.goss_kappa[r] : INT_MIN;
+            }
+        }
+        if (w == 0) {
+            const int64_t base = t * kGossTile;
+            for (int st = 0; st < kGossTile / 64; ++st) {
+                const int64_t row0 = base + (int64_t)st * 64;
+                if (row0 >= n) break;
+                const long long k = cur[st * 64 + lane];
+                const unsigned long long always = __ballot(k > cnt + 63);
+                const unsigned long long never = __ballot(k <= cnt);
+                unsigned long long kept;
+                if ((always | never) == ~0ULL) {
+                    kept = always;
+                    cnt += __popcll(always);
+                } else {
+                    kept = 0ULL;
+                    for (int i = 0; i < 64; ++i) {
+                        const long long ki = __builtin_amdgcn_readlane((int)k, i);
+                        if (cnt < ki) {
+                            kept |= 1ULL << i;
+                            ++cnt;
+                        }
+                    }
+                }
+                if (lane == 0) s.goss_mask[row0 >> 6] = kept;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) s.gst->kept_other = cnt;
+}
+
+__global__ __launch_bounds__(1024) void k_goss_scatter(DevState s) {
+    __shared__ int wsum[16];
+    if (!goss_on(s)) return;
+    const int64_t n = s.n;
+    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    bool top = false, other = false;
+    if (r < n) {
+        top = s.goss_kappa[r] == INT_MIN;
+        other = !top && ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
+    }
+    const int pre = block_excl_prefix(top || other, wsum);
+    if (r < n) {
+        if (top || other) s.rows0[(int64_t)s.goss_blk[blockIdx.x] + pre] = (int32_t)r;
+        s.goss_other[r] = other ? 1 : 0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const GossState g = *s.gst;
+        s.cursor[0] = g.bag_n;
+        s.round->sampled = 1;
+        s.round->goss_mult = g.other_k > 0 ? (double)(n - g.top_k) / (double)g.other_k : 1.0;
+    }
+}
+
 // --------------------------------------------------------------- histogram
 // Rows of the root build handled by each block. The scan kernel recomputes it
 // to know how many block partials the build left.
@@ -295,7 +563,7 @@ __device__ __forceinline__ int64_t hist_chunk(const DevState &s, int64_t m) {
 }
 
 __device__ __forceinline__ int64_t root_rows(const DevState &s) {
-    return s.hp.bagging ? load_agent(&s.cursor[0]) : s.n;
+    return s.round->sampled ? load_agent(&s.cursor[0]) : s.n;
 }
 
 // Block-private LDS histograms, two kinds.
@@ -320,7 +588,7 @@ struct QAcc {
     }
     // one record (this lane's 16-byte slice: features sub*16 ..)
     __device__ static void add(unsigned char *lds, const DevState &, const uint4 &w, int sub, int F, int ls,
-                               int64_t, uint32_t gh_word) {
+                               int64_t, uint32_t gh_word, double) {
         unsigned long long *a = (unsigned long long *)lds;
         const int g = (int)(int8_t)(gh_word >> 16);
         const int h = (int)(int8_t)(gh_word >> 24);
@@ -357,12 +625,18 @@ struct FAcc {
         for (int i = threadIdx.x; i < 2 * F * ls; i += blockDim.x) g[i] = 0.0;
         for (int i = threadIdx.x; i < F * ls; i += blockDim.x) c[i] = 0u;
     }
+    // goss_mult: the GOSS weight of rows the sampling kept (1 outside GOSS
+    // rounds); goss.apply_goss_scaling multiplies their g and h in fp64
     __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
-                               int64_t row, uint32_t) {
+                               int64_t row, uint32_t, double goss_mult) {
         double *g = (double *)lds;
         double *h = g + (size_t)F * ls;
         uint32_t *c = (uint32_t *)(h + (size_t)F * ls);
-        const double gv = (double)s.grad[row], hv = (double)s.hess[row];
+        double gv = (double)s.grad[row], hv = (double)s.hess[row];
+        if (goss_mult != 1.0 && s.goss_other != nullptr && s.goss_other[row]) {
+            gv *= goss_mult;
+            hv *= goss_mult;
+        }
         const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -409,7 +683,8 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     if (s.round->stopped) return;
     const int64_t m = root_rows(s);
     const int32_t *rows = s.rows0;
-    const bool direct = !s.hp.bagging;
+    const bool direct = !s.round->sampled;
+    const double goss_mult = s.round->goss_mult;
     if (m <= 0) return;
     const int64_t chunk = hist_chunk(s, m);
     const int64_t c0 = (int64_t)blockIdx.x * chunk;
@@ -442,7 +717,7 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (ok[u]) Acc::add(lds, s, w[u], sub, F, ls, row[u], gh);
+            if (ok[u]) Acc::add(lds, s, w[u], sub, F, ls, row[u], gh, goss_mult);
         }
     }
     __syncthreads();
@@ -483,6 +758,7 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     __shared__ long long off_l[kPbMaxUnroll * 16], off_r[kPbMaxUnroll * 16], off_b[kPbMaxUnroll * 16];
     __shared__ int s_nbuilt;
     const int n_blocks = s.batch->n_blocks;
+    const double goss_mult = s.round->goss_mult;
     const int F = s.n_features, ls = s.lds_stride;
     int32_t *list = (int32_t *)(lds + Acc::lds_bytes(F, ls));
     const int lane = lane_id(), w = threadIdx.x >> 6;
@@ -578,7 +854,7 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
 #pragma unroll
                 for (int u = 0; u < kHistUnroll; ++u) {
                     const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                    if (ok[u]) Acc::add(lds, s, v[u], sub, F, ls, row[u], gh);
+                    if (ok[u]) Acc::add(lds, s, v[u], sub, F, ls, row[u], gh, goss_mult);
                 }
             }
             __syncthreads();
@@ -1755,11 +2031,12 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
             // for multiclass, a round none of whose trees does better
             const bool degenerate = s.t_meta[1] == 1 && fabs(s.t_value[0]) < 1e-12;
             const int K = s.hp.num_class;
+            const bool sampling = s.hp.bagging || s.hp.goss;
             if (K == 1) {
-                if (degenerate && !s.hp.bagging) nr.stopped = 1;
+                if (degenerate && !sampling) nr.stopped = 1;
             } else {
                 nr.progress = (rd.class_k == 0 ? 0 : rd.progress) | (degenerate ? 0 : 1);
-                if (rd.class_k == K - 1 && !nr.progress && !s.hp.bagging) nr.stopped = 1;
+                if (rd.class_k == K - 1 && !nr.progress && !sampling) nr.stopped = 1;
             }
         }
         nr.tree_index = rd.tree_index + 1;
@@ -1804,6 +2081,23 @@ hipError_t launch_objective(const DevState &s, int grid, hipStream_t st) {
 }
 hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_softmax, dim3(grid), dim3(256), 0, st, s);
+    return hipGetLastError();
+}
+hipError_t launch_goss(const DevState &s, hipStream_t st) {
+    hipLaunchKernelGGL(k_goss_setup, dim3(1), dim3(256), 0, st, s);
+    const int grid = 1024;
+    for (int pass = 0; pass < 8; ++pass) {
+        hipLaunchKernelGGL(k_goss_digits, dim3(grid), dim3(256), 0, st, s, pass);
+        hipLaunchKernelGGL(k_goss_pick, dim3(1), dim3(64), 0, st, s, pass);
+    }
+    const dim3 blocks(s.goss_nblk);
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 0);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, 0);
+    hipLaunchKernelGGL(k_goss_kappa, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), (size_t)2 * kGossTile * sizeof(int32_t), st, s);
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 1);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, 1);
+    hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(1024), 0, st, s);
     return hipGetLastError();
 }
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
@@ -1854,6 +2148,7 @@ hipError_t prepare_kernels(const DevState &s) {
         MB_SET_LDS((k_part_hist<8, FAcc>), pb);
     }
     MB_SET_LDS(k_plan, plan_lds_bytes(s));
+    MB_SET_LDS(k_goss_walk, (size_t)2 * kGossTile * sizeof(int32_t));
     MB_SET_LDS(k_score, score_lds_bytes(s));
     return hipSuccess;
 }

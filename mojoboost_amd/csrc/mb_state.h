@@ -104,8 +104,26 @@ struct Round {
     int32_t parity;      // which magnitude-stats pair this tree uses
     int32_t stopped;     // training stopped (boosting._boost_rounds' stop rule): later trees do nothing
     int32_t progress;    // a tree of the current multiclass round split or moved
-    int32_t pad_;
+    int32_t sampled;     // the root range is the row list rows0[0 .. cursor[0]) (bag or GOSS sample)
     double grad_units, hess_units;
+    double goss_mult;    // GOSS weight of the sampled small-gradient rows (1 when off)
+};
+
+// The state of a run before its first tree: no sampling, unit GOSS weight.
+inline Round initial_round() {
+    Round r{};
+    r.goss_mult = 1.0;
+    return r;
+}
+
+// GOSS selection of one round (goss.mojo:294-396).
+struct GossState {
+    unsigned long long prefix;  // radix select: high bits of the threshold found so far
+    int64_t rank;               // remaining rank (0-based, descending) inside the prefix
+    int64_t top_k, other_k;
+    double threshold;           // top_k-th largest |g h|
+    int64_t kept_other;         // rows kept by the selection sampling
+    int64_t bag_n;              // top + kept rows
 };
 
 struct HyperParams {
@@ -120,7 +138,10 @@ struct HyperParams {
     int32_t const_hessian;
     int32_t bagging;        // 1: rows sampled per bag
     int32_t quantized;      // 1: int8 gradients, integer histograms; 0: fp32 gradients, fp64 sums
-    int32_t pad_hp_;
+    int32_t goss;           // 1: GOSS from round goss_warm on
+    int32_t goss_warm;
+    int32_t goss_seed;
+    double top_rate, other_rate;
     int32_t bagging_freq;
     int32_t bagging_seed;
     double bagging_fraction;
@@ -160,6 +181,15 @@ struct DevState {
     int32_t part_stride;       // per-feature stride of a partial (even, >= n_bins)
     int64_t hist_chunk_min;    // fewest rows a histogram block takes
     int64_t hist_chunk_limit;  // most rows a block may pack (field bounds)
+    // GOSS (fp32 path)
+    GossState *gst;
+    uint32_t *goss_hist;        // 8 passes x 256 digit counts
+    int32_t *goss_kappa;        // n: top row -> INT_MIN, else the count bound of the sampling
+    unsigned long long *goss_mask;  // ceil(n / 64): rows kept by the sampling
+    int32_t *goss_blk;          // per 1024-row block counts, then their exclusive prefix
+    uint8_t *goss_other;        // n: 1 when the row was kept by the sampling (weighted)
+    int32_t goss_nblk;
+    int32_t pad_goss_;
     // growth
     ENode *enodes;         // e_cap
     double *e_gain;        // e_cap: best gain when > 0 and found, else -1 (planner's view)

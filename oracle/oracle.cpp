@@ -20,8 +20,11 @@
 //        worked example y=-1.3,u=0.9 -> -2 (quantized_gradient.mojo:1502-1505)
 //   integer histogram ................ brute force + float/int agreement
 //   quantized split search ........... brute-force enumeration on tiny nodes
-//   GOSS .......... parity unpinned (no reference vector; restated from
-//        goss.mojo:294-396 only)
+//   GOSS ........... the reference's GOSS properties (tests/test_goss.mojo:
+//        counts, multiplier, top set, order, reseeding, unbiasedness, warmup,
+//        sampled leaf counts) in tests/test_oracle_goss.py; the per-row draw
+//        u(r) = uniform(splitmix64(seed ^ round * GOLDEN) + r) follows the
+//        formula of goss.mojo:67-78 and no vector of drawn rows pins it
 #include "oracle.h"
 
 #include <algorithm>
@@ -952,7 +955,8 @@ double select_kth_desc(std::vector<double> &v, int64_t k) {
 }
 
 bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
-                std::vector<double> &hess, const orc_params &p, int64_t round) {
+                std::vector<double> &hess, const orc_params &p, int64_t round,
+                std::vector<double> *scale = nullptr) {
     if (!p.goss) return false;
     int64_t warm = p.learning_rate <= 0.0 ? 0 : (int64_t)(1.0 / p.learning_rate);
     if (round < warm) return false;
@@ -971,10 +975,12 @@ bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
     uint64_t stream = splitmix64((uint64_t)(p.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
                                  ((uint64_t)round * GOLDEN));
     bag.clear();
+    if (scale) scale->clear();
     int64_t n_top = 0, n_other = 0;
     for (int64_t r = 0; r < n; ++r) {
         if (imp[r] >= threshold) {
             bag.push_back((int32_t)r);
+            if (scale) scale->push_back(1.0);
             ++n_top;
         } else {
             int64_t rest_need = other_k - n_other;
@@ -983,6 +989,7 @@ bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
                                         : (double)rest_need / (double)rest_all;
             if (uniform(stream + (uint64_t)r) < prob) {
                 bag.push_back((int32_t)r);
+                if (scale) scale->push_back(mult);
                 grad[r] *= mult;
                 hess[r] *= mult;
                 ++n_other;
@@ -1337,6 +1344,32 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
     build_float(hist, d, g, h, rows, rows ? n_sel : n, feats, pool, row_blocks);
     std::memcpy(out_gh, hist.gh.data(), hist.gh.size() * sizeof(double));
     std::memcpy(out_count, hist.c.data(), hist.c.size() * sizeof(int64_t));
+    return 0;
+}
+
+// One GOSS selection (goss_importance + goss_select + apply_goss_scaling,
+// goss.mojo:294-373) on caller arrays, warmup not applied. rows_out and
+// scale_out need n entries; grad/hess are scaled in place like the trainer's.
+int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
+                        double other_rate, int32_t seed, int64_t round_index,
+                        int32_t *rows_out, double *scale_out, int64_t *n_out) {
+    if (n <= 0 || !grad || !hess || !rows_out || !scale_out || !n_out) return -1;
+    orc_params p{};
+    p.goss = 1;
+    p.learning_rate = 0.0;  // no warmup
+    p.top_rate = top_rate;
+    p.other_rate = other_rate;
+    p.goss_seed = seed;
+    std::vector<double> g(grad, grad + n), h(hess, hess + n), sc;
+    std::vector<int32_t> bag;
+    goss_round(bag, g, h, p, round_index, &sc);
+    for (size_t i = 0; i < bag.size(); ++i) {
+        rows_out[i] = bag[i];
+        scale_out[i] = sc[i];
+    }
+    std::memcpy(grad, g.data(), n * sizeof(double));
+    std::memcpy(hess, h.data(), n * sizeof(double));
+    *n_out = (int64_t)bag.size();
     return 0;
 }
 

@@ -117,6 +117,14 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n_rows,
                        int32_t row_blocks, double *out_gh,
                        int64_t *out_count);
 
+/* ------------------------------------------------------------------ GOSS */
+/* One GOSS selection of round `round_index` (no warmup): ascending kept rows,
+ * each row's scale (1 for the top set, the multiplier for sampled rows), and
+ * grad/hess scaled in place. rows_out and scale_out hold n entries. */
+int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
+                        double other_rate, int32_t seed, int64_t round_index,
+                        int32_t *rows_out, double *scale_out, int64_t *n_out);
+
 /* ----------------------------------------------------------- split search */
 /* Best split of one node from an integer histogram. Returns found (0/1);
  * out_feature, out_bin, out_default_left, out_gain. */

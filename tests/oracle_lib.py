@@ -132,6 +132,10 @@ def lib():
                                           C.c_void_p, C.c_double, C.c_double, C.c_double,
                                           C.c_double, C.c_double, C.c_int32, C.c_void_p,
                                           C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_goss_select.restype = C.c_int32
+        L.orc_goss_select.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_double, C.c_double,
+                                      C.c_int32, C.c_int64, C.c_void_p, C.c_void_p,
+                                      P(C.c_int64)]
         _lib = L
     return _lib
 
@@ -269,3 +273,17 @@ def split_quantized(hist, missing_bin, widths, gu, hu, l1=0.0, l2=1.0, min_hess=
                                       _ptr(mb), _ptr(w), gu, hu, l1, l2, min_hess, min_data,
                                       C.byref(of), C.byref(ob), C.byref(odl), C.byref(og))
     return bool(found), of.value, ob.value, bool(odl.value), og.value
+
+
+def goss_select(grad, hess, top_rate=0.2, other_rate=0.1, seed=3, round_index=0):
+    """One GOSS selection (no warmup): (rows, scale, scaled grad, scaled hess)."""
+    g = np.array(grad, np.float64)
+    h = np.array(hess, np.float64)
+    n = len(g)
+    rows = np.zeros(n, np.int32)
+    scale = np.zeros(n)
+    cnt = C.c_int64(0)
+    rc = lib().orc_goss_select(_ptr(g), _ptr(h), n, top_rate, other_rate, seed, round_index,
+                               _ptr(rows), _ptr(scale), C.byref(cnt))
+    assert rc == 0, rc
+    return rows[:cnt.value], scale[:cnt.value], g, h

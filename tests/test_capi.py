@@ -88,8 +88,19 @@ def test_train_argument_errors():
     ("num_class=3", _lib.ERROR_INVALID_ARGUMENT),
     ("objective=nonsense", _lib.ERROR_INVALID_ARGUMENT),
     ("device=cpu", _lib.ERROR_UNSUPPORTED),
-    ("boosting=goss", _lib.ERROR_UNSUPPORTED),
+    ("boosting=dart", _lib.ERROR_UNSUPPORTED),
     ("objective=poisson", _lib.ERROR_UNSUPPORTED),
+    # GossParams.validate (goss.mojo:129-145), the cases of test_goss.mojo:217-241
+    ("boosting=goss top_rate=1.5", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss top_rate=-0.1", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss other_rate=1.5", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss other_rate=-0.1", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss top_rate=0.7 other_rate=0.4", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss top_rate=0 other_rate=0", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss bagging_seed=-1", _lib.ERROR_INVALID_ARGUMENT),
+    ("boosting=goss top_rate=0.9 other_rate=0.2", _lib.ERROR_INVALID_ARGUMENT),
+    # _check_goss (boosting.mojo:346-355): GOSS and row bagging both own the row list
+    ("boosting=goss bagging_fraction=0.5 bagging_freq=1", _lib.ERROR_INVALID_ARGUMENT),
 ])
 def test_parameter_string_errors(params, code):
     rc, msg, h = _train(params)

@@ -366,3 +366,23 @@ def test_training_fp32_binary_bagging(dev):
     assert fit.n_trees == ref.n_trees
     assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
     assert _tree_agreement(fit, ref) >= ref.n_trees - 1
+
+
+@pytest.mark.parametrize("n,f,leaves,lr,iters", [(3_000, 4, 15, 0.2, 20), (200_000, 16, 63, 0.1, 16)])
+def test_training_goss_fp32(dev, n, f, leaves, lr, iters):
+    """GOSS (goss.mojo:294-396) on the fp32 path, as in C3: warmup of
+    floor(1/lr) rounds, then the top 20 % by |g h| plus selection sampling of
+    10 % weighted by (n - top_k) / other_k. The sample is exact (the small
+    case makes the sampling's one-by-one steps frequent), so the trees follow
+    the oracle's and predictions agree within 1e-5."""
+    bins, y, mb, nb = c2_like(n, f=f, seed=13)
+    kw = dict(objective=1, num_iterations=iters, num_leaves=leaves, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=lr)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    fit = ds.train(use_quantized_grad=0, goss=1, top_rate=0.2, other_rate=0.1, **kw)
+    ref = O.train(bins, n, f, nb, y,
+                  O.default_params(**kw, use_quantized_grad=0, goss=1, top_rate=0.2, other_rate=0.1),
+                  missing_bin=mb)
+    assert fit.n_trees == ref.n_trees
+    assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+    assert _tree_agreement(fit, ref) >= ref.n_trees - 1
