@@ -98,7 +98,10 @@ std::vector<uint8_t> tree_feature_mask(int F, double fraction, int64_t seed, int
 
 struct mbh_dataset {
     int64_t n = 0;
-    int F = 0, nb = 0, rec = 0, lds_stride = 0;
+    int F = 0, nb = 0, lds_stride = 0;
+    // the records' current layout (built for the last training's histogram
+    // kind; rebuilt from d_bins_cm when another kind needs other tiles)
+    int rec = 0, tile_f = 0, n_tiles = 0;
     int device = 0;
     int n_cu = 0;
     uint8_t *d_records = nullptr, *d_bins_cm = nullptr;
@@ -146,9 +149,7 @@ struct PinnedFlags {
     }
 };
 
-// LDS row list of the partition+histogram kernel (one tile of row ids), and
-// its static LDS (tile counters and offsets).
-constexpr size_t kPbListBytes = 4096 * 4;
+// Static LDS of the partition+histogram kernel (tile counters and offsets).
 constexpr size_t kPbStaticLds = 2048;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
 // trees reaches the tree's depth in iterations with 32).
@@ -217,6 +218,53 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         bad("binary labels must be in [0, 1]");
 }
 
+// Feature tiles of the row records. A tile holds as many features as one
+// workgroup's LDS histogram takes for the histogram kind in use (8 bytes per
+// cell quantized, 20 fp32, plus the partition's row list) and a 128-byte
+// record allows (126 features and the g/h pair); the features are then
+// spread evenly over the tiles. Narrow data is one tile: each row's bins in
+// one 16..128-byte record.
+struct RecLayout {
+    int rec = 0, tile_f = 0, n_tiles = 0;
+};
+
+RecLayout record_layout(int F, int lds_stride, bool quantized) {
+    int ft_max = 126;
+    while (ft_max > 0 && mb::pb_lds_bytes_for(ft_max, lds_stride, quantized) + kPbStaticLds > 160 * 1024)
+        --ft_max;
+    if (ft_max < 1)
+        throw Error{MOJOTREES_ERROR_UNSUPPORTED, "one feature's histogram exceeds a workgroup's LDS"};
+    RecLayout l;
+    l.n_tiles = (F + ft_max - 1) / ft_max;
+    l.tile_f = (F + l.n_tiles - 1) / l.n_tiles;
+    l.rec = 16;
+    while (l.rec < l.tile_f + 2) l.rec *= 2;
+    return l;
+}
+
+// (Re)build the dataset's records for a layout; the g/h pairs start at zero.
+void ensure_records(mbh_dataset *ds, const RecLayout &l) {
+    if (ds->d_records && ds->rec == l.rec && ds->tile_f == l.tile_f && ds->n_tiles == l.n_tiles) return;
+    if (ds->d_records) {
+        HIPX(hipDeviceSynchronize());
+        for (void *&q : ds->owned)
+            if (q == ds->d_records) {
+                (void)hipFree(q);
+                q = ds->owned.back();
+                ds->owned.pop_back();
+                break;
+            }
+        ds->d_records = nullptr;
+    }
+    ds->d_records = dalloc<uint8_t>((size_t)l.rec * l.n_tiles * ds->n, ds->owned);
+    ds->rec = l.rec;
+    ds->tile_f = l.tile_f;
+    ds->n_tiles = l.n_tiles;
+    HIPX(mb::launch_build_records(ds->d_bins_cm, ds->d_records, ds->n, ds->F, l.rec, l.tile_f, l.n_tiles,
+                                  4 * ds->n_cu, nullptr));
+    HIPX(hipDeviceSynchronize());
+}
+
 // Histogram launch geometry and the partial buffer. The root build of m rows
 // runs ceil(m / chunk) blocks with chunk = clamp(ceil(m / grid), chunk_min,
 // chunk_limit); the grid is widened when needed so grid * chunk_limit covers
@@ -239,7 +287,9 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantize
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);
-    const int64_t parts = std::max<int64_t>(grid, s.pb_grid);
+    // a root build uses at most ceil(n / chunk_min) chunks
+    const int64_t parts = std::max<int64_t>(std::min<int64_t>(grid, (ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min),
+                                            s.pb_grid);
     const size_t cells = (size_t)parts * ds->F * s.part_stride;
     if (quantized) {
         s.part = dalloc<unsigned long long>(cells, run.owned);
@@ -293,6 +343,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     const int max_nodes = 2 * L - 1;
     const int F = ds->F;
     mb::DevState &s = tb.s;
+    const bool quantized = p->use_quantized_grad != 0;
+    ensure_records(ds, record_layout(F, ds->lds_stride, quantized));
     s.records = ds->d_records;
     s.records_w = ds->d_records;
     s.bins_cm = ds->d_bins_cm;
@@ -303,6 +355,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.n_features = F;
     s.n_bins = ds->nb;
     s.rec_bytes = ds->rec;
+    s.tile_f = ds->tile_f;
+    s.n_tiles = ds->n_tiles;
     s.lds_stride = ds->lds_stride;
     s.raw = dalloc<double>((size_t)ds->n * K, run.owned);
     s.prob = K > 1 ? dalloc<double>((size_t)ds->n * K, run.owned) : nullptr;
@@ -315,7 +369,6 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     const int max_exp = 2 * L - 1;
     s.max_exp = max_exp;
     s.e_cap = 1 + 2 * max_exp;
-    const bool quantized = p->use_quantized_grad != 0;
     if (quantized) s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
     else s.histf = dalloc<mb::HistF>((size_t)(1 + max_exp) * F * ds->nb, run.owned);
     configure_hist(s, ds, quantized ? p->num_grad_quant_bins : 4, quantized, run);
@@ -388,10 +441,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
         throw Error{MOJOTREES_ERROR_UNSUPPORTED,
                     "num_leaves * n_features too large for the planner's LDS (160 KiB)"};
     if (mb::pb_lds_bytes(s) + kPbStaticLds > 160 * 1024)
-        throw Error{MOJOTREES_ERROR_UNSUPPORTED,
-                    quantized ? "n_features * n_bins exceeds one workgroup's LDS"
-                              : "fp32 histograms: n_features * n_bins exceeds one workgroup's LDS "
-                                "(20 bytes per cell; use_quantized_grad=true takes 8)"};
+        throw Error{MOJOTREES_ERROR_TRAINING, "internal: the feature tile exceeds one workgroup's LDS"};
     HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
@@ -461,17 +511,7 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         ds->n = n;
         ds->F = F;
         ds->nb = nb;
-        int rec = 16;
-        while (rec < F + 2) rec *= 2;
-        if (rec > 128)
-            throw Error{MOJOTREES_ERROR_UNSUPPORTED,
-                        "more than 126 features needs the feature-tiled histogram, not built yet"};
-        ds->rec = rec;
         ds->lds_stride = nb | 1;
-        if ((size_t)F * ds->lds_stride * 8 + kPbListBytes > 160 * 1024)
-            throw Error{MOJOTREES_ERROR_UNSUPPORTED,
-                        "n_features * n_bins exceeds one workgroup's LDS (160 KiB: packed counters "
-                        "plus the partition's row list)"};
         // validate bins and derive the realized widths (binning.histogram_widths)
         ds->missing.assign(F, -1);
         if (missing_bin)
@@ -511,7 +551,6 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         HIPX(hipGetDeviceProperties(&prop, ds->device));
         ds->n_cu = prop.multiProcessorCount;
         ds->d_bins_cm = dalloc<uint8_t>((size_t)F * n, ds->owned);
-        ds->d_records = dalloc<uint8_t>((size_t)rec * n, ds->owned);
         ds->d_labels = dalloc<double>(n, ds->owned);
         ds->d_missing = dalloc<int32_t>(F, ds->owned);
         ds->d_widths = dalloc<int32_t>(F, ds->owned);
@@ -519,7 +558,6 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         HIPX(hipMemcpy(ds->d_labels, labels, (size_t)n * sizeof(double), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(ds->d_missing, ds->missing.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(ds->d_widths, ds->widths.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
-        HIPX(mb::launch_build_records(ds->d_bins_cm, ds->d_records, n, F, rec, 4 * ds->n_cu, nullptr));
         HIPX(hipDeviceSynchronize());
     } catch (const Error &e) {
         set_err(err, err_len, e.msg);
@@ -838,6 +876,7 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const doubl
         HIPX(hipDeviceSynchronize());
         HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        // the pairs of tile 0 (every tile holds the same pair)
         std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
         HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
         for (int64_t r = 0; r < ds->n; ++r) {
@@ -882,13 +921,15 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
         p.use_quantized_grad = 1;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
-        // place the int8 pairs into the records
-        std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
+        // place the int8 pairs into every tile's records
+        std::vector<uint8_t> rec((size_t)ds->n * ds->rec * ds->n_tiles);
         HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
-        for (int64_t r = 0; r < ds->n; ++r) {
-            rec[(size_t)r * ds->rec + ds->rec - 2] = (uint8_t)q_grad[r];
-            rec[(size_t)r * ds->rec + ds->rec - 1] = (uint8_t)q_hess[r];
-        }
+        for (int t = 0; t < ds->n_tiles; ++t)
+            for (int64_t r = 0; r < ds->n; ++r) {
+                const size_t at = ((size_t)t * ds->n + r) * ds->rec + ds->rec - 2;
+                rec[at] = (uint8_t)q_grad[r];
+                rec[at + 1] = (uint8_t)q_hess[r];
+            }
         HIPX(hipMemcpy(ds->d_records, rec.data(), rec.size(), hipMemcpyHostToDevice));
         const size_t cells = (size_t)ds->F * ds->nb * 3;
         // unit lattice scales: the root split's gains are not read here, only

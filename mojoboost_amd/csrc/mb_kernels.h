@@ -16,6 +16,8 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 hipError_t prepare_kernels(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
 size_t pb_lds_bytes(const DevState &s);
+// partition + histogram LDS of a tile of tile_f features
+size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized);
 size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
 hipError_t launch_hist(const DevState &s, hipStream_t st);
@@ -25,7 +27,7 @@ hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_round_end(const DevState &s, hipStream_t st);
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
-                                int grid, hipStream_t st);
+                                int tile_f, int n_tiles, int grid, hipStream_t st);
 hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st);
 hipError_t launch_exp_sigmoid(const double *x, double *e, double *sg, int64_t n, hipStream_t st);
 

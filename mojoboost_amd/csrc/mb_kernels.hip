@@ -264,7 +264,8 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
             int32_t qg = quantize_scalar((double)s.grad[r], gu, gmax, stoch, gs + (uint64_t)r);
             int32_t qh = quantize_scalar((double)s.hess[r], hu, hmax, stoch, hs + (uint64_t)r);
             uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
-            *(uint16_t *)(s.records_w + r * rec + rec - 2) = v;
+            for (int t = 0; t < s.n_tiles; ++t)
+                *(uint16_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 2) = v;
         }
         if (!hp.bagging) {
             if (valid) s.rows0[r] = (int32_t)r;
@@ -603,12 +604,13 @@ struct QAcc {
                 if (f < F) atomicAdd(&a[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
             }
     }
-    // every cell of the block's histogram as its partial
-    __device__ static void store(const DevState &s, const unsigned char *lds, int blk) {
+    // every cell of the block's histogram as its partial: features
+    // [f0, f0 + Ft) of partial blk
+    __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
         const unsigned long long *a = (const unsigned long long *)lds;
         const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
-        unsigned long long *out = s.part + (size_t)blk * F * ps;
-        for (int c = threadIdx.x; c < F * ps; c += blockDim.x) {
+        unsigned long long *out = s.part + ((size_t)blk * F + f0) * ps;
+        for (int c = threadIdx.x; c < Ft * ps; c += blockDim.x) {
             const int f = c / ps;
             const int b = c - f * ps;
             out[c] = b < nb ? a[f * ls + b] : 0ULL;
@@ -651,13 +653,13 @@ struct FAcc {
                 }
             }
     }
-    __device__ static void store(const DevState &s, const unsigned char *lds, int blk) {
+    __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
         const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
         const double *g = (const double *)lds;
-        const double *h = g + (size_t)F * ls;
-        const uint32_t *c = (const uint32_t *)(h + (size_t)F * ls);
-        const size_t base = (size_t)blk * F * ps;
-        for (int i = threadIdx.x; i < F * ps; i += blockDim.x) {
+        const double *h = g + (size_t)Ft * ls;
+        const uint32_t *c = (const uint32_t *)(h + (size_t)Ft * ls);
+        const size_t base = ((size_t)blk * F + f0) * ps;
+        for (int i = threadIdx.x; i < Ft * ps; i += blockDim.x) {
             const int f = i / ps;
             const int b = i - f * ps;
             const bool in = b < nb;
@@ -674,7 +676,8 @@ struct FAcc {
 // record is LPR x 16 bytes: each of the LPR lanes of a row group loads 16
 // bytes (16 features) and the int8 g/h pair (the record's last two bytes)
 // reaches the group by a lane shuffle. Each lane keeps kHistUnroll row loads
-// in flight.
+// in flight. blockIdx.y is the feature tile: the block reads that tile's
+// records and stores that tile's features of its partial.
 constexpr int kHistUnroll = 4;
 
 template <int LPR, class Acc>
@@ -690,15 +693,17 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     const int64_t c0 = (int64_t)blockIdx.x * chunk;
     if (c0 >= m) return;
     const int64_t c1 = c0 + chunk < m ? c0 + chunk : m;
-    const int F = s.n_features, ls = s.lds_stride;
-    Acc::zero(lds, F, ls);
+    const int ls = s.lds_stride;
+    const int f0 = (int)blockIdx.y * s.tile_f;
+    const int Ft = min(s.tile_f, s.n_features - f0);
+    Acc::zero(lds, Ft, ls);
     __syncthreads();
     const int lane = lane_id();
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
     const int rpp = blockDim.x / LPR;
     const int src_lane = (lane / LPR) * LPR + (LPR - 1);
-    const uint4 *rec = (const uint4 *)s.records;
+    const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
     for (int64_t i0 = c0; i0 < c1; i0 += (int64_t)kHistUnroll * rpp) {
         uint4 w[kHistUnroll];
         int64_t row[kHistUnroll];
@@ -717,11 +722,11 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (ok[u]) Acc::add(lds, s, w[u], sub, F, ls, row[u], gh, goss_mult);
+            if (ok[u]) Acc::add(lds, s, w[u], sub, Ft, ls, row[u], gh, goss_mult);
         }
     }
     __syncthreads();
-    Acc::store(s, lds, blockIdx.x);
+    Acc::store(s, lds, blockIdx.x, f0, Ft);
 }
 
 // ------------------------------------------------- partition + histogram
@@ -741,6 +746,12 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
 // of rows inside a child is not the reference's (tiles land in reservation
 // order); integer histograms are order-free, fp64 sums differ only in their
 // rounding.
+//
+// blockIdx.y is the feature tile. Every tile's block ranks the rows of its
+// descriptor the same way (ballots and a block-local scan are deterministic),
+// so each lists the same smaller-child rows; only tile 0's block reserves
+// output and scatters the rows, the others accumulate their tile's features
+// from the same list.
 constexpr int kPbThreads = 1024;
 constexpr int kPbMaxUnroll = 4;
 
@@ -759,20 +770,23 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     __shared__ int s_nbuilt;
     const int n_blocks = s.batch->n_blocks;
     const double goss_mult = s.round->goss_mult;
-    const int F = s.n_features, ls = s.lds_stride;
-    int32_t *list = (int32_t *)(lds + Acc::lds_bytes(F, ls));
+    const int ls = s.lds_stride, tf = s.tile_f;
+    const int f0 = (int)blockIdx.y * tf;
+    const int Ft = min(tf, s.n_features - f0);
+    const bool owner = blockIdx.y == 0;  // reserves output and scatters the rows
+    int32_t *list = (int32_t *)(lds + Acc::lds_bytes(tf, ls));
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const unsigned long long below = (1ULL << lane) - 1ULL;
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
     const int rpp = kPbThreads / LPR;
     const int src_lane = (lane / LPR) * LPR + (LPR - 1);
-    const uint4 *rec = (const uint4 *)s.records;
+    const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
     // a block takes descriptors blockIdx.x, + gridDim.x, ...; each one is a
     // whole accumulation (zeroed LDS, stored partial)
     for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
         const PbDesc d = s.pb_desc[blk];
-        Acc::zero(lds, F, ls);
+        Acc::zero(lds, Ft, ls);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
@@ -808,7 +822,7 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
                 const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
                 const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
                 long long bl_base = 0, br_base = 0;
-                if (lane == 0) {
+                if (lane == 0 && owner) {
                     bl_base = tl ? (long long)atomicAdd(&cur[0], (unsigned long long)tl) : 0;
                     br_base = tr ? (long long)atomicAdd(&cur[1], (unsigned long long)tr) : 0;
                 }
@@ -828,13 +842,17 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
                 if (left[u]) {
                     rank = __popcll(lm[u] & below);
                     const long long p = off_l[k] + rank;
-                    if (p < d.n_left) dst[p] = r[u];
-                    else atomicOr(s.error, 1);
+                    if (owner) {
+                        if (p < d.n_left) dst[p] = r[u];
+                        else atomicOr(s.error, 1);
+                    }
                 } else {
                     rank = __popcll(rm[u] & below);
                     const long long p = d.n_left + off_r[k] + rank;
-                    if (p < d.m) dst[p] = r[u];
-                    else atomicOr(s.error, 1);
+                    if (owner) {
+                        if (p < d.m) dst[p] = r[u];
+                        else atomicOr(s.error, 1);
+                    }
                 }
                 if (left[u] == bl) list[off_b[k] + rank] = r[u];
             }
@@ -854,13 +872,13 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
 #pragma unroll
                 for (int u = 0; u < kHistUnroll; ++u) {
                     const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                    if (ok[u]) Acc::add(lds, s, v[u], sub, F, ls, row[u], gh, goss_mult);
+                    if (ok[u]) Acc::add(lds, s, v[u], sub, Ft, ls, row[u], gh, goss_mult);
                 }
             }
             __syncthreads();
         }
         __syncthreads();
-        Acc::store(s, lds, blk);
+        Acc::store(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
     }
 }
@@ -1387,7 +1405,7 @@ constexpr int kPlanThreads = 1024;
 // LDS layout of the planner (byte offsets), shared by the host's size query
 // and the kernel.
 struct PlanLayout {
-    size_t fg, wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
+    size_t wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
     size_t total;
 };
 
@@ -1400,7 +1418,6 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
         o += bytes;
         return at;
     };
-    p.fg = take((size_t)8 * 2 * K * F, 16);  // (pair, feature) gain, -1 if none
     p.wg = take((size_t)8 * 2 * K, 8);       // pair's best gain
     p.eg = take((size_t)8 * E, 8);           // explored node's gain view
     p.sg = take((size_t)8 * L, 8);           // frontier slot's gain
@@ -1424,7 +1441,7 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
 }
 
 struct PlanView {
-    double *fg, *wg, *eg, *sg, *cb;
+    double *wg, *eg, *sg, *cb;
     int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff;
     Item *it;
 };
@@ -1432,7 +1449,6 @@ struct PlanView {
 __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     const PlanLayout p = plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features);
     PlanView v;
-    v.fg = (double *)(smem + p.fg);
     v.wg = (double *)(smem + p.wg);
     v.eg = (double *)(smem + p.eg);
     v.sg = (double *)(smem + p.sg);
@@ -1502,12 +1518,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         while (vf < F - 1 && !s.feature_mask[(size_t)rd.tree_index * F + vf]) ++vf;
         s_vf = vf;
     }
-    // ---- 1. fold (loads of every (pair, feature) gain, then one wave per pair)
+    // ---- 1. fold (one wave per pair over the pair's per-feature results)
     const int n_pairs = root_mode ? 1 : 2 * n_items;
-    for (int i = tid; i < n_pairs * F; i += nthr) {
-        const ScanResult &q = s.scan[i];
-        v.fg[i] = q.found ? q.gain : -1.0;
-    }
     if (!root_mode)
         for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
     __syncthreads();
@@ -1526,7 +1538,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         double bg = 0.0;
         int bf = 0x7FFFFFFF;
         for (int ff = lane; ff < F; ff += 64) {
-            const double q = v.fg[pr * F + ff];
+            const ScanResult &sr = s.scan[(size_t)pr * F + ff];
+            const double q = sr.found ? sr.gain : -1.0;
             if (q > bg) {
                 bg = q;
                 bf = ff;
@@ -1975,7 +1988,9 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     const double lr = s.hp.learning_rate;
     const int K = s.hp.num_class;
     const int k = s.round->class_k;
-    const int rec = s.rec_bytes;
+    const int rec = s.rec_bytes, tf = s.tile_f;
+    const bool tiled = s.n_tiles > 1;
+    const size_t tile_bytes = (size_t)s.n * rec;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
         const uint8_t *rb = s.records + r * rec;
@@ -1984,7 +1999,13 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
         // within n_nodes steps
         for (int d = 0; d < n_nodes && tnode[5 * node] >= 0; ++d) {
             const int f = tnode[5 * node];
-            const int b = rb[f];
+            int b;
+            if (tiled) {
+                const int t = f / tf;
+                b = rb[(size_t)t * tile_bytes + (f - t * tf)];
+            } else {
+                b = rb[f];
+            }
             const int md = tnode[5 * node + 4];
             const int mbin = md >> 1;  // arithmetic shift keeps -1
             const bool left = (b == mbin) ? (md & 1) : (b <= tnode[5 * node + 1]);
@@ -2050,13 +2071,19 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
     }
 }
 
-// Bins column-major -> per-row records (F bin bytes, zero pad).
+// Bins column-major -> tile-major row records (each tile: its features' bin
+// bytes, then zeros up to the g/h pair, which starts at zero too).
 __global__ __launch_bounds__(256) void k_build_records(const uint8_t *bins_cm, uint8_t *records,
-                                                       int64_t n, int F, int rec) {
+                                                       int64_t n, int F, int rec, int tile_f, int n_tiles) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
-        uint8_t *o = records + r * rec;
-        for (int f = 0; f < rec; ++f) o[f] = f < F ? bins_cm[(size_t)f * n + r] : 0;
+    const int64_t total = n * n_tiles;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int t = (int)(i / n);
+        const int64_t r = i - (int64_t)t * n;
+        const int f0 = t * tile_f;
+        const int ft = min(tile_f, F - f0);
+        uint8_t *o = records + i * rec;
+        for (int j = 0; j < rec; ++j) o[j] = j < ft ? bins_cm[(size_t)(f0 + j) * n + r] : 0;
     }
 }
 
@@ -2108,12 +2135,14 @@ size_t score_lds_bytes(const DevState &s) {
     return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
 }
 size_t hist_lds_bytes(const DevState &s) {
-    return s.hp.quantized ? QAcc::lds_bytes(s.n_features, s.lds_stride)
-                          : FAcc::lds_bytes(s.n_features, s.lds_stride);
+    return s.hp.quantized ? QAcc::lds_bytes(s.tile_f, s.lds_stride) : FAcc::lds_bytes(s.tile_f, s.lds_stride);
 }
 size_t pb_lds_bytes(const DevState &s) {
-    return s.hp.quantized ? pb_lds_bytes_of<QAcc>(s.n_features, s.lds_stride)
-                          : pb_lds_bytes_of<FAcc>(s.n_features, s.lds_stride);
+    return s.hp.quantized ? pb_lds_bytes_of<QAcc>(s.tile_f, s.lds_stride)
+                          : pb_lds_bytes_of<FAcc>(s.tile_f, s.lds_stride);
+}
+size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized) {
+    return quantized ? pb_lds_bytes_of<QAcc>(tile_f, lds_stride) : pb_lds_bytes_of<FAcc>(tile_f, lds_stride);
 }
 size_t plan_lds_bytes(const DevState &s) {
     return plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features).total;
@@ -2155,7 +2184,7 @@ hipError_t prepare_kernels(const DevState &s) {
 template <class Acc>
 hipError_t launch_hist_t(const DevState &s, hipStream_t st) {
     const size_t lds = hist_lds_bytes(s);
-    const dim3 grid(s.hist_grid), block(1024);
+    const dim3 grid(s.hist_grid, s.n_tiles), block(1024);
     switch (s.rec_bytes / 16) {
     case 1: hipLaunchKernelGGL((k_hist<1, Acc>), grid, block, lds, st, s); break;
     case 2: hipLaunchKernelGGL((k_hist<2, Acc>), grid, block, lds, st, s); break;
@@ -2171,7 +2200,7 @@ hipError_t launch_hist(const DevState &s, hipStream_t st) {
 template <class Acc>
 hipError_t launch_part_hist_t(const DevState &s, hipStream_t st) {
     const size_t lds = pb_lds_bytes(s);
-    const dim3 grid(s.pb_launch), block(kPbThreads);
+    const dim3 grid(s.pb_launch, s.n_tiles), block(kPbThreads);
     switch (s.rec_bytes / 16) {
     case 1: hipLaunchKernelGGL((k_part_hist<1, Acc>), grid, block, lds, st, s); break;
     case 2: hipLaunchKernelGGL((k_part_hist<2, Acc>), grid, block, lds, st, s); break;
@@ -2205,8 +2234,9 @@ hipError_t launch_round_end(const DevState &s, hipStream_t st) {
     return hipGetLastError();
 }
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
-                                int grid, hipStream_t st) {
-    hipLaunchKernelGGL(k_build_records, dim3(grid), dim3(256), 0, st, bins_cm, records, n, F, rec);
+                                int tile_f, int n_tiles, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_build_records, dim3(grid), dim3(256), 0, st, bins_cm, records, n, F, rec, tile_f,
+                       n_tiles);
     return hipGetLastError();
 }
 hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st) {

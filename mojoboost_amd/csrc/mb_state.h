@@ -152,7 +152,10 @@ struct HyperParams {
 // Everything the kernels touch, passed by value.
 struct DevState {
     // data (resident for the whole fit)
-    const uint8_t *records;  // n x rec_bytes: F bin bytes, pad, then q_grad, q_hess
+    // n_tiles x n x rec_bytes, tile-major: tile t holds features
+    // [t * tile_f, t * tile_f + tile_f) of a row, zero pad, then q_grad,
+    // q_hess in its last two bytes (every tile carries the pair)
+    const uint8_t *records;
     const uint8_t *bins_cm;  // F x n, column-major (partition, score update)
     const double *labels;    // n
     const int32_t *missing_bin;  // F
@@ -162,7 +165,9 @@ struct DevState {
     int64_t n;
     int32_t n_features;
     int32_t n_bins;        // histogram stride per feature
-    int32_t rec_bytes;
+    int32_t rec_bytes;     // bytes of one row's record in one tile (16..128)
+    int32_t tile_f;        // features per tile (the last tile may hold fewer)
+    int32_t n_tiles;
     int32_t lds_stride;    // per-feature LDS stride (odd, >= n_bins)
     // per round
     double *raw;           // n x num_class

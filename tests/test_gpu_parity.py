@@ -386,3 +386,86 @@ def test_training_goss_fp32(dev, n, f, leaves, lr, iters):
     assert fit.n_trees == ref.n_trees
     assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
     assert _tree_agreement(fit, ref) >= ref.n_trees - 1
+
+
+# ------------------------------------------------------------ wide (C4-shaped)
+def c4_like(n, f, seed=17, nb=63):
+    """C4-shaped data at a reduced size: N(0,1)
+    features, label = sign of a sparse 50-feature linear model plus noise."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(f, n))
+    k = min(50, f)
+    idx = rng.choice(f, k, replace=False)
+    w = rng.normal(size=k)
+    y = ((w @ x[idx] + 0.5 * rng.normal(size=n)) > 0).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=nb)
+    return bins, y, mb, nb
+
+
+@pytest.mark.parametrize("subset", [False, True])
+def test_histogram_wide_bit_exact(dev, subset):
+    """700 features at 63 bins: six feature tiles of 117 features, every
+    (feature, bin) cell identical to the oracle's."""
+    n, f, nb = 40_000, 700, 63
+    rng = np.random.default_rng(12)
+    bins = rng.integers(0, nb, size=(f, n), dtype=np.uint8)
+    bins[699] = bins[699] % 3
+    qg = rng.integers(-2, 3, size=n).astype(np.int8)
+    qh = rng.integers(0, 5, size=n).astype(np.int8)
+    ds = dev.Dataset(bins, n, f, nb, np.zeros(n))
+    rows = np.sort(rng.choice(n, 9_999, replace=False)).astype(np.int32) if subset else None
+    got = ds.histogram(qg, qh, rows, quant_bins=4)
+    want = O.hist_quantized(bins.ravel(), n, f, nb, qg, qh, rows)
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+def test_histogram_fp32_wide(dev):
+    """fp32 histograms at 255 bins take 20 bytes per LDS cell, so 300
+    features run as ten tiles of 30."""
+    n, f, nb = 30_000, 300, 255
+    rng = np.random.default_rng(13)
+    bins = rng.integers(0, nb, size=(f, n), dtype=np.uint8)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.01, 1.0, size=n).astype(np.float32)
+    ds = dev.Dataset(bins.ravel(), n, f, nb, np.zeros(n))
+    gh, cnt = ds.histogram_fp32(g, h)
+    want_gh = np.zeros(2 * f * nb)
+    want_c = np.zeros(f * nb, np.int64)
+    O.lib().orc_hist_float(O._ptr(bins.ravel()), n, f, nb, O._ptr(g.astype(np.float64)),
+                           O._ptr(h.astype(np.float64)), None, 0, 1, O._ptr(want_gh), O._ptr(want_c))
+    assert np.array_equal(cnt, want_c)
+    rel = np.abs(gh - want_gh) / np.maximum(np.abs(want_gh), 1e-30)
+    assert rel.max() < 1e-10, rel.max()
+
+
+def test_training_c4_shape_bit_exact(dev):
+    """C4 workload shape (2000 features, 63 bins, 127 leaves, logistic, int8
+    g/h) at 20k rows, 3 trees: sixteen feature tiles; every tree and raw score
+    identical to the oracle's."""
+    n, f = 20_000, 2000
+    bins, y, mb, nb = c4_like(n, f)
+    kw = dict(objective=1, num_iterations=3, num_leaves=127, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    fit = ds.train(use_quantized_grad=1, **kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
+def test_training_wide_fp32_and_narrow_after_wide(dev):
+    """fp32 gradients on 300 features at 255 bins (ten tiles) within 1e-5 of
+    the oracle; then the same dataset trains quantized (the records are
+    rebuilt for the other tile width) bit-exactly."""
+    n, f = 30_000, 300
+    bins, y, mb, nb = c4_like(n, f, seed=19, nb=255)
+    kw = dict(objective=1, num_iterations=6, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    fit = ds.train(use_quantized_grad=0, **kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=0), missing_bin=mb)
+    assert fit.n_trees == ref.n_trees
+    assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+    assert _tree_agreement(fit, ref) >= ref.n_trees - 1
+    fitq = ds.train(use_quantized_grad=1, **kw)
+    refq = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(fitq, refq, n)
