@@ -1,4 +1,5 @@
-"""Benchmark: GBDT training on one MI355X, BASELINE.json configs[1] (C2).
+"""Benchmark: GBDT training on one MI355X, BASELINE.json configs[1] (C2) by
+default; --workload c3|c4|c5 measures configs[2..4] the same way.
 
 Workload: 10.5M rows x 28 features (21 N(0,1), 7 products/abs of pairs),
 binary label ~ Bernoulli(sigmoid(sum of 8 random pairwise terms)), logistic
@@ -66,11 +67,86 @@ def c2_data(n_rows, seed=0x5EED0002):
     return x, y
 
 
-def traffic_per_launch():
+def c4_data(n_rows, n_features=2000, seed=0x5EED0004):
+    """C4: N(0,1) features, label = sign of a sparse 50-feature linear model
+    plus noise."""
+    rng = np.random.default_rng(seed)
+    x = np.empty((n_features, n_rows), np.float64)
+    for f in range(n_features):
+        x[f] = rng.standard_normal(n_rows, dtype=np.float32)
+    idx = rng.choice(n_features, 50, replace=False)
+    w = rng.standard_normal(50)
+    score = np.zeros(n_rows)
+    for i, f in enumerate(idx):
+        score += w[i] * x[f]
+    y = (score + 0.5 * rng.standard_normal(n_rows) > 0).astype(np.float64)
+    return x, y
+
+
+def c5_data(n_rows, n_classes=10, seed=0x5EED0005):
+    """C5: 40 N(0,1) columns and 10 integer columns of cardinality 4-64
+    (uniform); the class is the argmax of a random linear score over the
+    continuous columns plus a random effect per category value, plus Gumbel
+    noise."""
+    rng = np.random.default_rng(seed)
+    x = np.empty((50, n_rows), np.float64)
+    scores = np.zeros((n_classes, n_rows))
+    w = rng.standard_normal((n_classes, 40)) * 0.5
+    for f in range(40):
+        x[f] = rng.standard_normal(n_rows, dtype=np.float32)
+        scores += np.outer(w[:, f], x[f])
+    cards = rng.integers(4, 65, size=10)
+    for j in range(10):
+        c = rng.integers(0, cards[j], size=n_rows)
+        x[40 + j] = c
+        effect = rng.standard_normal((n_classes, cards[j])) * 0.5
+        scores += effect[:, c]
+    scores += rng.gumbel(size=(n_classes, n_rows))
+    y = np.argmax(scores, axis=0).astype(np.float64)
+    return x, y
+
+
+# BASELINE.json configs[1..4]; the driver's default line is C2 (the metric's
+# configuration), the others are measured the same way when named.
+WORKLOADS = {
+    "c2": dict(rows=10_500_000, features=28, max_bin=255, leaves=255, trees=500, classes=1,
+               gh_bytes=2, params=dict(objective=1, use_quantized_grad=1),
+               cpu_sample=6, desc="C2: 10.5M x 28 binary logistic, max_bin 255, num_leaves 255, "
+                    "quantized gradients (int8 g/h, int32 histogram bins)",
+               dtype="int8 g/h, int32 cells"),
+    "c3": dict(rows=10_500_000, features=28, max_bin=255, leaves=255, trees=500, classes=1,
+               gh_bytes=8, params=dict(objective=1, use_quantized_grad=0, goss=1, top_rate=0.2,
+                                       other_rate=0.1),
+               cpu_sample=6, desc="C3: the C2 workload with fp32 gradients (fp64 histogram sums) and GOSS "
+                    "(top_rate 0.2, other_rate 0.1, warmup 10 rounds)",
+               dtype="fp32 g/h, fp64 sums"),
+    "c4": dict(rows=400_000, features=2000, max_bin=63, leaves=127, trees=200, classes=1,
+               gh_bytes=2, params=dict(objective=1, use_quantized_grad=1),
+               cpu_sample=4, desc="C4: 400k x 2000 binary logistic (sparse linear label), max_bin 63, "
+                    "num_leaves 127, quantized gradients; 16 feature tiles",
+               dtype="int8 g/h, int32 cells"),
+    "c5": dict(rows=2_000_000, features=50, max_bin=255, leaves=63, trees=100, classes=10,
+               gh_bytes=2, params=dict(objective=2, num_class=10, use_quantized_grad=1),
+               cpu_sample=2, desc="C5: 2M x 50 (10 integer columns split as ordered bins) softmax, 10 classes, "
+                    "max_bin 255, num_leaves 63, quantized gradients per class; a step is "
+                    "one round of 10 trees",
+               dtype="int8 g/h, int32 cells"),
+}
+
+
+def workload_data(name, n_rows):
+    if name in ("c2", "c3"):
+        return c2_data(n_rows)
+    if name == "c4":
+        return c4_data(n_rows)
+    return c5_data(n_rows)
+
+
+def traffic_per_launch(workload):
     """HBM bytes per k_part_hist launch measured by rocprofv3 (FETCH_SIZE and
     WRITE_SIZE passes over the same workload, calibrated against a plain
     device copy), as committed under profiles/; None when absent."""
-    p = ROOT / "profiles" / "k_part_hist_c2_traffic.json"
+    p = ROOT / "profiles" / f"k_part_hist_{workload}_traffic.json"
     if not p.exists():
         return None
     return json.loads(p.read_text()).get("traffic_bytes_per_launch")
@@ -127,10 +203,13 @@ def copy_probe(mib):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None,
+                    help="trees (rounds for c5); default: the workload's full count")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--rows", type=int, default=10_500_000)
-    ap.add_argument("--cpu-trees", type=int, default=6)
+    ap.add_argument("--rows", type=int, default=None)
+    ap.add_argument("--cpu-trees", type=int, default=None,
+                    help="oracle sample: trees (rounds for c5); default per workload")
     ap.add_argument("--no-instrumented", action="store_true")
     ap.add_argument("--rocprof-summary", default=None,
                     help="only summarize a rocprofv3 CSV (kernel_stats or counter_collection) "
@@ -154,17 +233,25 @@ def main():
     if device.device_count() < 1:
         print(json.dumps({"error": "no gfx950 GPU visible"}))
         return 1
-    F, NB, L = 28, 255, 255
+    wl = WORKLOADS[args.workload]
+    F, NB, L, K = wl["features"], wl["max_bin"], wl["leaves"], wl["classes"]
+    GH = wl["gh_bytes"]
+    if args.rows is None:
+        args.rows = wl["rows"]
+    if args.steps is None:
+        args.steps = wl["trees"]
+    if args.cpu_trees is None:
+        args.cpu_trees = wl["cpu_sample"]
     t0 = time.perf_counter()
-    x, y = c2_data(args.rows)
+    x, y = workload_data(args.workload, args.rows)
     bins, missing = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB)
     del x
     t_data = time.perf_counter() - t0
-    print(f"[bench] data {args.rows}x{F} generated+binned in {t_data:.1f}s, "
-          f"positive rate {y.mean():.3f}", file=sys.stderr, flush=True)
+    print(f"[bench] {args.workload}: data {args.rows}x{F} generated+binned in {t_data:.1f}s, "
+          f"label mean {y.mean():.3f}", file=sys.stderr, flush=True)
     ds = device.Dataset(bins, args.rows, F, NB, y, missing_bin=missing)
-    kw = dict(objective=1, num_leaves=L, min_data_in_leaf=20, lambda_l2=1.0,
-              learning_rate=0.1, num_grad_quant_bins=4, stochastic_rounding=1)
+    kw = dict(num_leaves=L, min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1,
+              num_grad_quant_bins=4, stochastic_rounding=1, **wl["params"])
     if args.warmup > 0:
         ds.train(num_iterations=args.warmup, **kw)
     print("[bench] warmup done", file=sys.stderr, flush=True)
@@ -173,8 +260,8 @@ def main():
     fit = ds.train(num_iterations=args.steps, **kw)
     wall = time.perf_counter() - t1
     trees = fit.n_trees
-    print(f"[bench] timed: {args.steps} trees in {wall:.3f}s ({trees} kept)", file=sys.stderr,
-          flush=True)
+    print(f"[bench] timed: {args.steps} steps in {wall:.3f}s ({trees} trees kept)",
+          file=sys.stderr, flush=True)
 
     st = None
     if not args.no_instrumented:
@@ -194,28 +281,36 @@ def main():
         import oracle_lib as O
 
         cores = min(16, os.cpu_count() or 1)
-        p = O.default_params(objective=1, num_iterations=args.cpu_trees, num_leaves=L,
-                             min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1,
-                             use_quantized_grad=1, num_grad_quant_bins=4, n_threads=cores)
+        oparams = {k: v for k, v in kw.items() if k not in ("num_grad_quant_bins", "stochastic_rounding")}
+        p = O.default_params(num_iterations=args.cpu_trees, num_grad_quant_bins=4, n_threads=cores,
+                             **oparams)
         tc = time.perf_counter()
         ref = O.train(bins, args.rows, F, NB, y, p, missing_bin=missing)
         cpu_s = time.perf_counter() - tc
         k = min(ref.n_trees, fit.n_trees)
         a, b = ref.off[k], fit.off[k]
-        parity = bool(a == b and all(
+        same_shape = bool(a == b and all(
             np.array_equal(getattr(ref, f)[:a], getattr(fit, f)[:b])
-            for f in ("feature", "threshold", "left", "right", "default_left"))
-            and np.array_equal(ref.value[:a].view(np.uint64), fit.value[:b].view(np.uint64)))
-        per_tree = cpu_s / max(1, args.cpu_trees)
-        cpu = {"value": round(per_tree * 500.0, 2), "unit": "s/500 trees", "cores": cores,
+            for f in ("feature", "threshold", "left", "right", "default_left")))
+        if wl["params"].get("use_quantized_grad"):
+            parity = same_shape and bool(np.array_equal(ref.value[:a].view(np.uint64),
+                                                        fit.value[:b].view(np.uint64)))
+            how = "bit-identical"
+        else:
+            parity = same_shape and bool(np.allclose(ref.value[:a], fit.value[:b], rtol=1e-5, atol=0))
+            how = "same splits, values within 1e-5"
+        per_step = cpu_s / max(1, args.cpu_trees)
+        full = wl["trees"]
+        unit_steps = "rounds" if K > 1 else "trees"
+        cpu = {"value": round(per_step * full, 2), "unit": f"s/{full} {unit_steps}", "cores": cores,
                "kind": "port",
-               "sample": f"first {args.cpu_trees} trees of the C2 workload on all "
-                         f"{args.rows} rows ({cpu_s:.1f}s, {per_tree:.2f}s/tree, "
-                         f"extrapolated x500); trees bit-identical to GPU: {parity}"}
-        print(f"[bench] cpu oracle {args.cpu_trees} trees in {cpu_s:.1f}s", file=sys.stderr,
+               "sample": f"first {args.cpu_trees} {unit_steps} of the {args.workload.upper()} workload "
+                         f"on all {args.rows} rows ({cpu_s:.1f}s, {per_step:.2f}s each, "
+                         f"extrapolated x{full}); trees {how} to GPU: {parity}"}
+        print(f"[bench] cpu oracle {args.cpu_trees} {unit_steps} in {cpu_s:.1f}s", file=sys.stderr,
               flush=True)
 
-    algo_root = args.rows * (F + 2)
+    algo_root = args.rows * (F + GH)
     root_gbs = algo_root / (root_mean_ms * 1e-3) / 1e9
     root_merged_gbs = algo_root / (root_merged_ms * 1e-3) / 1e9
     extra = {}
@@ -240,13 +335,13 @@ def main():
             "expansion_launches_per_tree": round(st["expand_launches"] * per_tree, 2),
             "leaves_expanded_per_tree": round(st["expansions"] * per_tree, 2),
             "speculative_row_overhead": round(
-                st["rows_built"] / max(1.0, st["hist_bytes"] / (F + 2) - st["root_bytes"] / (F + 2))
+                st["rows_built"] / max(1.0, st["hist_bytes"] / (F + GH) - st["root_bytes"] / (F + GH))
                 - 1.0, 4),
             "expand_kernel_avg_ms": round(kernel_avg_ms, 5),
         }
         note = (f"dominant kernel k_part_hist (partition + smaller-child accumulation), "
                 f"algorithmic bytes per launch = parent rows * 9 (row id in, split bin, row "
-                f"id out) + accumulated rows * (F + 2), over its average launch "
+                f"id out) + accumulated rows * (F + {GH}), over its average launch "
                 f"({kernel_avg_ms * 1e3:.1f} us, {int(st['expand_launches'])} launches incl. "
                 f"empty tail launches); root build alone {root_gbs:.0f} GB/s "
                 f"({root_gbs / HBM_PEAK_GBS:.1%})")
@@ -265,14 +360,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 g/h, int32 cells",
+        "dtype": wl["dtype"],
         "data": "synthetic",
-        "config": {"workload": "C2: 10.5M x 28 binary logistic, max_bin 255, num_leaves 255, "
-                               "quantized gradients (int8 g/h, int32 histogram bins)",
-                   "rows": args.rows, "features": F, "max_bin": NB, "num_leaves": L,
-                   "trees": args.steps},
+        "config": {"workload": wl["desc"], "rows": args.rows, "features": F, "max_bin": NB,
+                   "num_leaves": L, "steps": args.steps, "trees_per_step": K},
         "train_seconds": round(wall, 3),
-        "train_sec_per_500_trees": round(wall * 500.0 / max(1, args.steps), 3),
+        f"train_sec_per_{wl['trees']}_{'rounds' if K > 1 else 'trees'}":
+            round(wall * wl["trees"] / max(1, args.steps), 3),
         "hist_frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         **extra,
         "root_hist_gbs": round(root_gbs, 1),
@@ -281,7 +375,7 @@ def main():
         "root_hist_merged_ms": round(root_merged_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_per_launch(), "note": note},
+                     "traffic": traffic_per_launch(args.workload), "note": note},
         "cpu_baseline": cpu,
         "parity_first_trees_bit_exact": parity,
     }

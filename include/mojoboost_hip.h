@@ -67,6 +67,12 @@ typedef struct {
                                    floor(1 / learning_rate) rounds, stream
                                    keyed by bagging_seed */
     double top_rate, other_rate;
+    /* GOSS count: decisions outside a band of goss_band standard deviations
+     * (+64) around the count's expectation are taken in parallel and checked
+     * exactly; goss_exact_walk = 1 always runs the full sequential count.
+     * Both give the reference's sample. Defaults 10 and 0. */
+    double goss_band;
+    int32_t goss_exact_walk;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -111,7 +117,8 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *   [0] wall seconds of the training loop (enqueue to final sync)
  *   [1] ms of the histogram-accumulating kernels (root build + expansions)
  *   [2] histogram algorithmic bytes of the committed trees: (root rows + the
- *       smaller child of every split) * (n_features + 2)
+ *       smaller child of every split) * (n_features + gh), gh = 2 for int8
+ *       g/h (use_quantized_grad=1), 8 for fp32 g/h
  *   [3] the same rows * n_features    [4] builds of the committed trees
  *   [5] root-build algorithmic bytes  [6] root-build ms   [7] trees grown
  *   [8] ms of every growth kernel (accumulation + merge/scan/plan)
@@ -121,7 +128,7 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *   [12] rows accumulated by expansions     [13] parent rows partitioned
  *   [14] expansion launches enqueued        [15] ms of those launches
  *   [16] their algorithmic bytes: [13] * 9 (row id in, bin, row id out)
- *        + [12] * (n_features + 2) */
+ *        + [12] * (n_features + gh) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
 /* ------------------------------------------- stage-level (parity, bench) */

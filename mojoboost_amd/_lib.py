@@ -63,6 +63,8 @@ class MbhParams(C.Structure):
         ("goss", C.c_int32),
         ("top_rate", C.c_double),
         ("other_rate", C.c_double),
+        ("goss_band", C.c_double),
+        ("goss_exact_walk", C.c_int32),
     ]
 
 
@@ -73,7 +75,7 @@ def mbh_params(**kw) -> MbhParams:
                   feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
                   quant_seed=11, time_histograms=0, use_quantized_grad=1, goss=0,
-                  top_rate=0.2, other_rate=0.1)
+                  top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0)
     for k, v in kw.items():
         setattr(p, k, v)
     return p

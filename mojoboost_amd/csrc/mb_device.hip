@@ -418,13 +418,26 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.goss_seed = p->bagging_seed;
     hp.top_rate = p->top_rate;
     hp.other_rate = p->other_rate;
+    hp.goss_band = p->goss_band;
+    hp.goss_exact = p->goss_exact_walk ? 1 : 0;
     if (hp.goss) {
         s.goss_nblk = (int32_t)((ds->n + 1023) / 1024);
         s.gst = dalloc<mb::GossState>(1, run.owned);
         s.goss_hist = dalloc<uint32_t>(8 * 256, run.owned);
-        s.goss_kappa = dalloc<int32_t>(ds->n, run.owned);
+        // padded to whole count tiles; the pad holds INT_MIN (never kept) and
+        // no kernel writes it
+        const int64_t padded = (ds->n + mb::kGossTileRows - 1) / mb::kGossTileRows * mb::kGossTileRows;
+        s.goss_kappa = dalloc<int32_t>(padded, run.owned);
+        if (padded > ds->n) {
+            std::vector<int32_t> pad(padded - ds->n, INT32_MIN);
+            HIPX(hipMemcpy(s.goss_kappa + ds->n, pad.data(), pad.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        }
         s.goss_mask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
         s.goss_blk = dalloc<int32_t>(s.goss_nblk, run.owned);
+        s.goss_blk_u = dalloc<int32_t>(s.goss_nblk, run.owned);
+        s.goss_ukappa = dalloc<int32_t>(padded, run.owned);  // whole count tiles
+        s.goss_urow = dalloc<int32_t>(ds->n, run.owned);
+        s.goss_umask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
         s.goss_other = dalloc<uint8_t>(ds->n, run.owned);
         HIPX(hipMemset(s.goss_other, 0, ds->n));
     }
@@ -701,7 +714,9 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
                        hipMemcpyDeviceToHost));
         const bool bagging = s.hp.bagging != 0 || s.hp.goss != 0;  // sampled rounds are skipped, not stops
-        const double rb = ds->F + 2;
+        // algorithmic bytes per accumulated row: its bins plus its g/h pair
+        // (int8 x 2 quantized, fp32 x 2 otherwise)
+        const double rb = ds->F + (s.hp.quantized ? 2 : 8);
         double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
         double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
         int grown = 0;

@@ -332,6 +332,9 @@ __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
         g.threshold = 0.0;
         g.kept_other = 0;
         g.bag_n = 0;
+        g.n_uncertain = 0;
+        g.fallback = s.hp.goss_exact ? 1 : 0;
+        g.pad_ = 0;
         *s.gst = g;
     }
 }
@@ -371,8 +374,8 @@ __global__ void k_goss_pick(DevState s, int pass) {
     *s.gst = g;
 }
 
-// Blocks of 1024 rows: count of top rows (mode 0) or of rows in the sample
-// (mode 1) per block.
+// Blocks of 1024 rows: count of top rows (mode 0), of rows in the sample
+// (mode 1) or of rows kept by the sampling (mode 2) per block.
 __device__ __forceinline__ bool goss_top(const DevState &s, int64_t r, unsigned long long thr_bits) {
     return goss_key(s, r) >= thr_bits;
 }
@@ -386,7 +389,8 @@ __global__ __launch_bounds__(1024) void k_goss_count(DevState s, int mode) {
         if (mode == 0) {
             in = goss_top(s, r, (unsigned long long)__double_as_longlong(s.gst->threshold));
         } else {
-            in = s.goss_kappa[r] == INT_MIN || ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
+            const bool other = (s.goss_mask[r >> 6] >> (r & 63)) & 1ULL;
+            in = mode == 2 ? other : (s.goss_kappa[r] == INT_MIN || other);
         }
     }
     const unsigned long long b = __ballot(in);
@@ -399,33 +403,28 @@ __global__ __launch_bounds__(1024) void k_goss_count(DevState s, int mode) {
     }
 }
 
-// Exclusive prefix of the per-block counts, in place (one block); mode 1
-// also records the sample size.
-__global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int mode) {
-    __shared__ long long part[1024];
+// Exclusive prefix of per-block counts, in place (one block); the total
+// goes to *total when given.
+__global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, int64_t *total) {
+    __shared__ long long wtot[16];
     if (!goss_on(s)) return;
     const int nb = s.goss_nblk;
     const int per = (nb + 1023) / 1024;
     const int lo = threadIdx.x * per;
     const int hi = lo + per < nb ? lo + per : nb;
     long long sum = 0;
-    for (int i = lo; i < hi; ++i) sum += s.goss_blk[i];
-    part[threadIdx.x] = sum;
+    for (int i = lo; i < hi; ++i) sum += blk[i];
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const long long inc = wave_incl_scan(sum);
+    if (lane == 63) wtot[w] = inc;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        long long acc = 0;
-        for (int i = 0; i < 1024; ++i) {
-            const long long v = part[i];
-            part[i] = acc;
-            acc += v;
-        }
-        if (mode == 1) s.gst->bag_n = acc;
-    }
-    __syncthreads();
-    long long acc = part[threadIdx.x];
+    long long before = 0;
+    for (int i = 0; i < w; ++i) before += wtot[i];
+    if (total != nullptr && threadIdx.x == 1023) *total = before + inc;
+    long long acc = before + inc - sum;
     for (int i = lo; i < hi; ++i) {
-        const int v = s.goss_blk[i];
-        s.goss_blk[i] = (int32_t)acc;
+        const int v = blk[i];
+        blk[i] = (int32_t)acc;
         acc += v;
     }
 }
@@ -441,93 +440,252 @@ __device__ __forceinline__ int block_excl_prefix(bool flag, int *wsum) {
     return before + __popcll(b & ((1ULL << lane) - 1ULL));
 }
 
+// kappa of every row, then its class against a predicted band of the count:
+// before row r the count is expected at K (1 - rest_r / N) (selection
+// sampling takes a uniform K-subset of the N = n - top_k other rows) with a
+// hypergeometric standard deviation sigma_r; with D = band * sigma_r + 64, a
+// row with kappa > expected + D is kept and one with kappa <= expected - D
+// dropped if the count stays inside the band, which the check after the
+// count verifies; the rows in between are left to the sequential count.
+// Class (in goss_other): 0 dropped, 1 kept, 2 open. Kept rows' bits go to
+// goss_mask; per block the kept (goss_blk) and open (goss_blk_u) counts.
 __global__ __launch_bounds__(1024) void k_goss_kappa(DevState s) {
-    __shared__ int wsum[16];
+    __shared__ int wsum[16], wk[16], wu[16];
     if (!goss_on(s)) return;
     const GossState g = *s.gst;
     const int64_t n = s.n;
     const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const int64_t top_before_blk = s.goss_blk[blockIdx.x];
     const unsigned long long thr = (unsigned long long)__double_as_longlong(g.threshold);
     const bool top = r < n && goss_top(s, r, thr);
     const int pre = block_excl_prefix(top, wsum);
-    if (r >= n) return;
-    if (top) {
+    int cls = 0;
+    if (r < n && !top) {
+        const int64_t n_top = top_before_blk + pre;
+        const int64_t rest = (n - r) - (g.top_k - n_top);
+        const int64_t K = g.other_k;
+        int64_t kappa;
+        if (rest <= 0) {
+            kappa = K;  // the reference keeps the row iff rows are still needed
+        } else {
+            const uint64_t stream = splitmix64((uint64_t)(s.hp.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
+                                               ((uint64_t)s.round->round * kGolden));
+            const double u = uniform53(stream + (uint64_t)r);
+            auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
+            int64_t c = (int64_t)floor((double)K - u * (double)rest);
+            if (c < 0) c = 0;
+            if (c > K) c = K;
+            while (c > 0 && !keep(c - 1)) --c;
+            while (c < K && keep(c)) ++c;
+            kappa = c;
+        }
+        s.goss_kappa[r] = (int32_t)kappa;
+        const double N = (double)(n - g.top_k);
+        double f = N > 0.0 ? 1.0 - (double)(rest > 0 ? rest : 0) / N : 1.0;
+        f = f < 0.0 ? 0.0 : (f > 1.0 ? 1.0 : f);
+        const double expect = (double)K * f;
+        const double var = N > 1.0 ? (double)K * f * (1.0 - f) * (N - (double)K) / (N - 1.0) : 0.0;
+        const double d = s.hp.goss_band * sqrt(var > 0.0 ? var : 0.0) + 64.0;
+        cls = (double)kappa > expect + d ? 1 : ((double)kappa <= expect - d ? 0 : 2);
+    } else if (r < n) {
         s.goss_kappa[r] = INT_MIN;
-        return;
     }
-    const int64_t n_top = (int64_t)s.goss_blk[blockIdx.x] + pre;
-    const int64_t rest = (n - r) - (g.top_k - n_top);
-    const int64_t K = g.other_k;
-    int64_t kappa;
-    if (rest <= 0) {
-        kappa = K;  // the reference keeps the row iff rows are still needed
-    } else {
-        const uint64_t stream = splitmix64((uint64_t)(s.hp.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
-                                           ((uint64_t)s.round->round * kGolden));
-        const double u = uniform53(stream + (uint64_t)r);
-        auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
-        int64_t c = (int64_t)floor((double)K - u * (double)rest);
-        if (c < 0) c = 0;
-        if (c > K) c = K;
-        while (c > 0 && !keep(c - 1)) --c;
-        while (c < K && keep(c)) ++c;
-        kappa = c;
+    if (r < n) s.goss_other[r] = (uint8_t)cls;
+    const unsigned long long km = __ballot(cls == 1), um = __ballot(cls == 2);
+    const int64_t r0 = (int64_t)blockIdx.x * 1024 + w * 64;
+    if (lane == 0) {
+        if (r0 < n) s.goss_mask[r0 >> 6] = km;
+        wk[w] = __popcll(km);
+        wu[w] = __popcll(um);
     }
-    s.goss_kappa[r] = (int32_t)kappa;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int tk = 0, tu = 0;
+        for (int i = 0; i < 16; ++i) {
+            tk += wk[i];
+            tu += wu[i];
+        }
+        s.goss_blk[blockIdx.x] = tk;
+        s.goss_blk_u[blockIdx.x] = tu;
+    }
 }
 
-// One block; wave 0 runs the count while the other waves stage the next
-// tile of kappa values into LDS.
-constexpr int kGossTile = 16384;
-
-__global__ __launch_bounds__(1024) void k_goss_walk(DevState s) {
-    extern __shared__ int32_t gbuf[];  // 2 x kGossTile
+// The open rows in row order, each with its kappa less the kept rows before
+// it, which turns their decisions into the same sequential count.
+__global__ __launch_bounds__(1024) void k_goss_compact(DevState s) {
+    __shared__ int wk[16], wu[16];
     if (!goss_on(s)) return;
     const int64_t n = s.n;
+    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const int cls = r < n ? (int)s.goss_other[r] : 0;
+    const int pk = block_excl_prefix(cls == 1, wk);
+    const int pu = block_excl_prefix(cls == 2, wu);
+    if (cls == 2) {
+        const int64_t pos = (int64_t)s.goss_blk_u[blockIdx.x] + pu;
+        const int64_t kept_before = (int64_t)s.goss_blk[blockIdx.x] + pk;
+        s.goss_ukappa[pos] = (int32_t)((int64_t)s.goss_kappa[r] - kept_before);
+        s.goss_urow[pos] = (int32_t)r;
+    }
+}
+
+// Decisions of the open rows into goss_mask.
+__global__ __launch_bounds__(256) void k_goss_apply(DevState s) {
+    if (!goss_on(s)) return;
+    const int64_t u = s.gst->n_uncertain;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < u; j += stride)
+        if ((s.goss_umask[j >> 6] >> (j & 63)) & 1ULL) {
+            const int32_t r = s.goss_urow[j];
+            atomicOr(&s.goss_mask[r >> 6], 1ULL << (r & 63));
+        }
+}
+
+// The check: the sequential count keeps row r iff the rows it kept before r
+// number less than kappa_r, so kept flags that satisfy this at every row are
+// its result. goss_blk holds the exclusive prefix of kept rows per block.
+__global__ __launch_bounds__(1024) void k_goss_verify(DevState s) {
+    __shared__ int wsum[16];
+    if (!goss_on(s)) return;
+    const int64_t n = s.n;
+    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const bool kept = r < n && ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
+    const int pre = block_excl_prefix(kept, wsum);
+    if (r < n) {
+        const int64_t before = (int64_t)s.goss_blk[blockIdx.x] + pre;
+        const int32_t k = s.goss_kappa[r];
+        if ((before < (int64_t)k) != kept) atomicOr(&s.gst->fallback, 1);
+    }
+}
+
+// One 64-row slice of the count: rows whose kappa exceeds the count by 64 or
+// more are kept and rows whose kappa is at most the count dropped whatever
+// the slice's other rows do; the rest are resolved in row order.
+__device__ __forceinline__ unsigned long long goss_slice(int k, int &cnt) {
+    const unsigned long long a = __ballot(k > cnt + 63);
+    const unsigned long long z = __ballot(k <= cnt);
+    unsigned long long kept = a, amb = ~(a | z);
+    while (amb) {
+        const int i = __builtin_ctzll(amb);
+        amb &= amb - 1ULL;
+        const int ki = __builtin_amdgcn_readlane(k, i);
+        if (cnt + __popcll(kept & ((1ULL << i) - 1ULL)) < ki) kept |= 1ULL << i;
+    }
+    cnt += __popcll(kept);
+    return kept;
+}
+
+constexpr int kGossTile = kGossTileRows;
+
+// One block; wave 0 runs the count while the other 15 waves stage kappa
+// tiles into LDS, one tile ahead through registers: in the iteration that
+// wave 0 walks tile t, they store tile t + 1 (loaded during the previous
+// iteration) and issue the loads of tile t + 2. The kappa buffer is padded to
+// whole tiles with INT_MIN (never kept). The count advances 256 rows per
+// step when every kappa of the step is above count + 255 or at most the
+// count (always true but for rows whose draw falls within 256 of the
+// boundary), else by 64-row slices.
+constexpr int kGossStep = 256;
+constexpr int kGossVec = kGossTile / 4;       // int4 per tile
+constexpr int kGossStagers = 1024 - 64;
+constexpr int kGossSlots = (kGossVec + kGossStagers - 1) / kGossStagers;
+
+__device__ __forceinline__ int4 goss_clip(int4 v, int64_t e, int64_t len) {
+    v.x = e < len ? v.x : INT_MIN;
+    v.y = e + 1 < len ? v.y : INT_MIN;
+    v.z = e + 2 < len ? v.z : INT_MIN;
+    v.w = e + 3 < len ? v.w : INT_MIN;
+    return v;
+}
+
+// list = 1: the count over the open rows (goss_ukappa -> goss_umask);
+// list = 0: the full count over every row (goss_kappa -> goss_mask), run
+// only when the band's decisions failed the check or were not used.
+__global__ __launch_bounds__(1024) void k_goss_walk(DevState s, int list) {
+    extern __shared__ int32_t gbuf[];  // 2 x kGossTile
+    if (!goss_on(s)) return;
+    if (!list && !s.gst->fallback) return;
+    const int64_t n = list ? s.gst->n_uncertain : s.n;
+    if (n <= 0) return;
+    unsigned long long *out = list ? s.goss_umask : s.goss_mask;
+    const int64_t n_words = (n + 63) / 64;
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const int64_t tiles = (n + kGossTile - 1) / kGossTile;
-    for (int i = threadIdx.x; i < kGossTile; i += blockDim.x) gbuf[i] = i < n ? s.goss_kappa[i] : INT_MIN;
+    const int4 *kv = (const int4 *)(list ? s.goss_ukappa : s.goss_kappa);
+    for (int i = threadIdx.x; i < kGossVec; i += blockDim.x) ((int4 *)gbuf)[i] = goss_clip(kv[i], 4 * i, n);
+    // the stagers' registers: slot j holds int4 sid + j * kGossStagers of a tile
+    static_assert(kGossSlots == 5, "staging slots are written out below");
+    const int sid = (int)threadIdx.x - 64;
+    const bool last_slot = sid + 4 * kGossStagers < kGossVec;
+    int4 r0, r1, r2, r3, r4;
+#define MB_GOSS_LOAD(tile)                                                       \
+    do {                                                                         \
+        const int64_t e_ = ((int64_t)(tile) * kGossVec + sid) * 4;               \
+        const int4 *src_ = kv + (int64_t)(tile) * kGossVec + sid;                \
+        r0 = goss_clip(src_[0], e_, n);                                          \
+        r1 = goss_clip(src_[kGossStagers], e_ + 4 * kGossStagers, n);            \
+        r2 = goss_clip(src_[2 * kGossStagers], e_ + 8 * kGossStagers, n);        \
+        r3 = goss_clip(src_[3 * kGossStagers], e_ + 12 * kGossStagers, n);       \
+        if (last_slot) r4 = goss_clip(src_[4 * kGossStagers], e_ + 16 * kGossStagers, n); \
+    } while (0)
+    if (w != 0 && tiles > 1) MB_GOSS_LOAD(1);
     __syncthreads();
-    long long cnt = 0;
+    int cnt = 0;
     for (int64_t t = 0; t < tiles; ++t) {
-        int32_t *cur = gbuf + (t & 1) * kGossTile;
-        if (w != 0 && t + 1 < tiles) {
-            int32_t *nxt = gbuf + ((t + 1) & 1) * kGossTile;
-            const int64_t base = (t + 1) * kGossTile;
-            for (int i = threadIdx.x - 64; i < kGossTile; i += blockDim.x - 64) {
-                const int64_t r = base + i;
-                nxt[i] = r < n ? s.goss_kappa[r] : INT_MIN;
+        const int32_t *cur = gbuf + (t & 1) * kGossTile;
+        if (w != 0) {
+            if (t + 1 < tiles) {
+                int4 *dst = (int4 *)(gbuf + ((t + 1) & 1) * kGossTile) + sid;
+                dst[0] = r0;
+                dst[kGossStagers] = r1;
+                dst[2 * kGossStagers] = r2;
+                dst[3 * kGossStagers] = r3;
+                if (last_slot) dst[4 * kGossStagers] = r4;
             }
+            if (t + 2 < tiles) MB_GOSS_LOAD(t + 2);
         }
         if (w == 0) {
             const int64_t base = t * kGossTile;
-            for (int st = 0; st < kGossTile / 64; ++st) {
-                const int64_t row0 = base + (int64_t)st * 64;
+            int k0 = cur[lane], k1 = cur[64 + lane], k2 = cur[128 + lane], k3 = cur[192 + lane];
+            for (int st = 0; st < kGossTile / kGossStep; ++st) {
+                const int64_t row0 = base + (int64_t)st * kGossStep;
                 if (row0 >= n) break;
-                const long long k = cur[st * 64 + lane];
-                const unsigned long long always = __ballot(k > cnt + 63);
-                const unsigned long long never = __ballot(k <= cnt);
-                unsigned long long kept;
-                if ((always | never) == ~0ULL) {
-                    kept = always;
-                    cnt += __popcll(always);
+                // the next step's kappas do not depend on the count
+                const int o = st + 1 < kGossTile / kGossStep ? (st + 1) * kGossStep : 0;
+                const int n0 = cur[o + lane], n1 = cur[o + 64 + lane], n2 = cur[o + 128 + lane],
+                          n3 = cur[o + 192 + lane];
+                const int hi = cnt + kGossStep - 1;
+                const unsigned long long a0 = __ballot(k0 > hi), a1 = __ballot(k1 > hi),
+                                         a2 = __ballot(k2 > hi), a3 = __ballot(k3 > hi);
+                const unsigned long long z0 = __ballot(k0 <= cnt), z1 = __ballot(k1 <= cnt),
+                                         z2 = __ballot(k2 <= cnt), z3 = __ballot(k3 <= cnt);
+                unsigned long long m0, m1, m2, m3;
+                if (((a0 | z0) & (a1 | z1) & (a2 | z2) & (a3 | z3)) == ~0ULL) {
+                    m0 = a0;
+                    m1 = a1;
+                    m2 = a2;
+                    m3 = a3;
+                    cnt += __popcll(a0) + __popcll(a1) + __popcll(a2) + __popcll(a3);
                 } else {
-                    kept = 0ULL;
-                    for (int i = 0; i < 64; ++i) {
-                        const long long ki = __builtin_amdgcn_readlane((int)k, i);
-                        if (cnt < ki) {
-                            kept |= 1ULL << i;
-                            ++cnt;
-                        }
-                    }
+                    m0 = goss_slice(k0, cnt);
+                    m1 = goss_slice(k1, cnt);
+                    m2 = goss_slice(k2, cnt);
+                    m3 = goss_slice(k3, cnt);
                 }
-                if (lane == 0) s.goss_mask[row0 >> 6] = kept;
+                const int64_t wd = (row0 >> 6) + lane;
+                if (lane < 4 && wd < n_words)
+                    out[wd] = lane == 0 ? m0 : lane == 1 ? m1 : lane == 2 ? m2 : m3;
+                k0 = n0;
+                k1 = n1;
+                k2 = n2;
+                k3 = n3;
             }
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) s.gst->kept_other = cnt;
+    if (threadIdx.x == 0 && !list) s.gst->kept_other = cnt;
 }
+#undef MB_GOSS_LOAD
 
 __global__ __launch_bounds__(1024) void k_goss_scatter(DevState s) {
     __shared__ int wsum[16];
@@ -2118,12 +2276,27 @@ hipError_t launch_goss(const DevState &s, hipStream_t st) {
         hipLaunchKernelGGL(k_goss_pick, dim3(1), dim3(64), 0, st, s, pass);
     }
     const dim3 blocks(s.goss_nblk);
+    const size_t walk_lds = (size_t)2 * kGossTile * sizeof(int32_t);
+    int64_t *n_unc = &s.gst->n_uncertain;
+    int64_t *bag_n = &s.gst->bag_n;
+    // top rows: counts, prefix; kappa and the band's classes
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 0);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, 0);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
     hipLaunchKernelGGL(k_goss_kappa, blocks, dim3(1024), 0, st, s);
-    hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), (size_t)2 * kGossTile * sizeof(int32_t), st, s);
+    // the open rows: list, sequential count, decisions
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk_u, n_unc);
+    hipLaunchKernelGGL(k_goss_compact, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 1);
+    hipLaunchKernelGGL(k_goss_apply, dim3(256), dim3(256), 0, st, s);
+    // the check, and the full count when it fails
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 2);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
+    hipLaunchKernelGGL(k_goss_verify, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 0);
+    // the sample: top rows and kept rows, ascending
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 1);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, 1);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, bag_n);
     hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(1024), 0, st, s);
     return hipGetLastError();
 }

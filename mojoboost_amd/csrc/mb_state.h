@@ -109,6 +109,9 @@ struct Round {
     double goss_mult;    // GOSS weight of the sampled small-gradient rows (1 when off)
 };
 
+// Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
+constexpr int kGossTileRows = 16384;
+
 // The state of a run before its first tree: no sampling, unit GOSS weight.
 inline Round initial_round() {
     Round r{};
@@ -124,6 +127,9 @@ struct GossState {
     double threshold;           // top_k-th largest |g h|
     int64_t kept_other;         // rows kept by the selection sampling
     int64_t bag_n;              // top + kept rows
+    int64_t n_uncertain;        // rows whose keep decision the predicted count band left open
+    int32_t fallback;           // 1: the band's decisions failed the check (or were not used)
+    int32_t pad_;
 };
 
 struct HyperParams {
@@ -141,6 +147,8 @@ struct HyperParams {
     int32_t goss;           // 1: GOSS from round goss_warm on
     int32_t goss_warm;
     int32_t goss_seed;
+    int32_t goss_exact;     // 1: always the full sequential count (no predicted band)
+    double goss_band;       // band half-width in standard deviations of the count
     double top_rate, other_rate;
     int32_t bagging_freq;
     int32_t bagging_seed;
@@ -192,6 +200,10 @@ struct DevState {
     int32_t *goss_kappa;        // n: top row -> INT_MIN, else the count bound of the sampling
     unsigned long long *goss_mask;  // ceil(n / 64): rows kept by the sampling
     int32_t *goss_blk;          // per 1024-row block counts, then their exclusive prefix
+    int32_t *goss_blk_u;        // per block: rows the band leaves open, then their prefix
+    int32_t *goss_ukappa;       // the open rows in row order: kappa - certain keeps before it
+    int32_t *goss_urow;         // their row ids
+    unsigned long long *goss_umask; // the open rows' decisions, one bit per list position
     uint8_t *goss_other;        // n: 1 when the row was kept by the sampling (weighted)
     int32_t goss_nblk;
     int32_t pad_goss_;

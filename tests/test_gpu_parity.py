@@ -469,3 +469,27 @@ def test_training_wide_fp32_and_narrow_after_wide(dev):
     fitq = ds.train(use_quantized_grad=1, **kw)
     refq = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
     _compare_fit(fitq, refq, n)
+
+
+def test_goss_count_paths_agree(dev):
+    """The GOSS count three ways: the default band (parallel decisions, a
+    sequential count over the open rows, the exact check), the full
+    sequential count alone, and a band so wrong that the check fails and the
+    full count runs. All three give the same sample, hence bit-identical
+    training, and the oracle's trees."""
+    n, f = 200_000, 16
+    bins, y, mb, nb = c2_like(n, f=f, seed=23)
+    kw = dict(objective=1, num_iterations=14, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    goss = dict(use_quantized_grad=0, goss=1, top_rate=0.2, other_rate=0.1)
+    a = ds.train(**goss, **kw)
+    b = ds.train(**goss, goss_exact_walk=1, **kw)
+    c = ds.train(**goss, goss_band=-1e9, **kw)
+    for other in (b, c):
+        assert np.array_equal(bits(a.train_raw()), bits(other.train_raw()))
+        assert np.array_equal(a.threshold, other.threshold)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, **goss), missing_bin=mb)
+    assert a.n_trees == ref.n_trees
+    assert _rel_err(a.train_raw(), ref.train_raw(n)) < 1e-5
+    assert _tree_agreement(a, ref) >= ref.n_trees - 1
