@@ -131,6 +131,23 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *        + [12] * (n_features + gh) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
+/* Raw scores on the device (Booster.predict_raw_row,
+ * src/mojotrees/boosting.mojo:1722-1760; the reference's device counterpart is
+ * _predict_kernel, src/mojotrees/gpu_predict.mojo:206, in Float32). bins_cm is
+ * the column-major uint8 matrix (n_rows x n_features) the model's bin mapper
+ * produced; trees [tree_begin, tree_end) of a flat ensemble laid out as
+ * mbh_fit_arrays does (tree_begin a multiple of num_class). base: num_class
+ * scores added first, or NULL for a range that starts after iteration 0. out:
+ * row-major n_rows x num_class, bit-identical to the host predictor (fused
+ * multiply-adds in ascending tree order). */
+int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n_rows, int32_t n_features,
+                           int32_t num_class, double learning_rate, const double *base,
+                           const int64_t *node_offset, int64_t tree_begin, int64_t tree_end,
+                           const int32_t *feature, const int32_t *threshold,
+                           const int32_t *left, const int32_t *right, const double *value,
+                           const int32_t *default_left, const int32_t *missing_bin,
+                           double *out, char *err, int32_t err_len);
+
 /* ------------------------------------------- stage-level (parity, bench) */
 /* Device exp and sigmoid of x[0..n). */
 int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp,

@@ -35,6 +35,7 @@ MBH_SYMBOLS = [
     "mbh_fit_free", "mbh_fit_num_trees", "mbh_fit_num_class", "mbh_fit_total_nodes",
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
+    "mbh_predict_binned",
 ]
 
 
@@ -141,6 +142,8 @@ def lib():
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),
         "mbh_histogram_fp32": (I32, [V, V, V, V, I64, V, V, C.c_char_p, I32]),
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),
+        "mbh_predict_binned": (I32, [V, I64, I32, I32, C.c_double, V, V, I64, I64, V, V, V, V, V, V, V,
+                                     V, C.c_char_p, I32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

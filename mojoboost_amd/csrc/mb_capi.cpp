@@ -312,6 +312,9 @@ void check_model(const MojoTreesModel *m) {
     if (!m) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "model is NULL"};
 }
 
+// Row x tree visits from which device=auto predicts on the GPU.
+constexpr int64_t kAutoGpuRowTrees = (int64_t)1 << 24;
+
 int32_t predict_common(const MojoTreesModel *model, const double *data, int64_t n_rows, int64_t n_features,
                        int64_t start_it, int64_t num_it, int32_t flags, int32_t device, double *out,
                        int64_t out_len, MojoTreesError *error) {
@@ -328,15 +331,32 @@ int32_t predict_common(const MojoTreesModel *model, const double *data, int64_t 
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "unknown prediction flags"};
         if (device != MOJOTREES_DEVICE_CPU && device != MOJOTREES_DEVICE_GPU && device != MOJOTREES_DEVICE_AUTO)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "unknown device"};
-        if (device == MOJOTREES_DEVICE_GPU)
-            throw ApiError{MOJOTREES_ERROR_UNSUPPORTED, "device prediction is not built yet; use CPU or AUTO"};
+        const bool have_gpu = mbh_device_count() > 0;
+        if (device == MOJOTREES_DEVICE_GPU && !have_gpu)
+            throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
+                           "no gfx950 (MI355X) GPU is available; device=gpu never falls back to the CPU"};
         const int64_t k = m.num_class;
         if (out_len < n_rows * k) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "out_len is smaller than n_rows * num_classes"};
         const int64_t total = m.num_iterations();
         int64_t s0 = start_it < 0 ? 0 : std::min(start_it, total);
         int64_t s1 = num_it <= 0 ? total : std::min(total, s0 + num_it);
         std::vector<double> tmp((size_t)(n_rows * k));
-        m.predict_raw(data, n_rows, s0, s1, tmp.data());
+        // AUTO takes the device for batches large enough to pay for the upload
+        // (both paths give the same bits)
+        const bool on_gpu = device == MOJOTREES_DEVICE_GPU ||
+                            (device == MOJOTREES_DEVICE_AUTO && have_gpu && n_rows * (s1 - s0) * k >= kAutoGpuRowTrees);
+        if (on_gpu) {
+            std::vector<uint8_t> bins((size_t)n_rows * n_features);
+            m.mapper.transform(data, n_rows, bins.data());
+            char msg[512] = {0};
+            const int32_t rc = mbh_predict_binned(
+                bins.data(), n_rows, (int32_t)n_features, (int32_t)k, m.learning_rate, s0 == 0 ? m.base.data() : nullptr,
+                m.offsets.data(), s0 * k, s1 * k, m.feature.data(), m.threshold.data(), m.left.data(), m.right.data(),
+                m.value.data(), m.default_left.data(), m.missing_bin.data(), tmp.data(), msg, sizeof(msg));
+            if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
+        } else {
+            m.predict_raw(data, n_rows, s0, s1, tmp.data());
+        }
         if (flags == MOJOTREES_PREDICT_RESPONSE) m.response(tmp.data(), n_rows);
         std::memcpy(out, tmp.data(), tmp.size() * sizeof(double));
         return MOJOTREES_OK;

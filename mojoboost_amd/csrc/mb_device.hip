@@ -867,6 +867,116 @@ int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out
     return MOJOTREES_OK;
 }
 
+int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t num_class,
+                           double learning_rate, const double *base, const int64_t *node_offset,
+                           int64_t tree_begin, int64_t tree_end, const int32_t *feature,
+                           const int32_t *threshold, const int32_t *left, const int32_t *right,
+                           const double *value, const int32_t *default_left, const int32_t *missing_bin,
+                           double *out, char *err, int32_t err_len) {
+    if (!bins_cm || !node_offset || !feature || !threshold || !left || !right || !value || !default_left ||
+        !missing_bin || !out || n <= 0 || F <= 0 || num_class <= 0 || tree_begin < 0 || tree_end < tree_begin ||
+        tree_begin % num_class != 0) {
+        set_err(err, err_len, "invalid prediction arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    if (device_count_gfx950() == 0) {
+        set_err(err, err_len, "no gfx950 (MI355X) device is available to this process");
+        return MOJOTREES_ERROR_UNSUPPORTED;
+    }
+    Run run;
+    try {
+        const int K = num_class;
+        // the trees in range, rebased: absolute child indices, validated so
+        // that every walk moves to a larger index and ends at a leaf
+        const int64_t o0 = node_offset[tree_begin], o1 = node_offset[tree_end];
+        const int64_t nn = o1 - o0;
+        if (nn < 0 || nn >= ((int64_t)1 << 31))
+            throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "invalid node offsets"};
+        std::vector<int4> nodes((size_t)std::max<int64_t>(nn, 1));
+        std::vector<int32_t> md((size_t)std::max<int64_t>(nn, 1)), root((size_t)std::max<int64_t>(tree_end - tree_begin, 1));
+        int32_t max_steps = 1;
+        for (int64_t t = tree_begin; t < tree_end; ++t) {
+            const int64_t a = node_offset[t], b = node_offset[t + 1];
+            if (b <= a || a < o0 || b > o1) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "invalid node offsets"};
+            max_steps = std::max<int32_t>(max_steps, (int32_t)(b - a));
+            root[t - tree_begin] = (int32_t)(a - o0);
+            for (int64_t i = a; i < b; ++i) {
+                const int64_t loc = i - a;
+                int4 v;
+                v.x = feature[i] >= 0 ? feature[i] : -1;
+                v.y = threshold[i];
+                v.z = (int32_t)(a - o0 + left[i]);
+                v.w = (int32_t)(a - o0 + right[i]);
+                if (feature[i] >= 0 && (feature[i] >= F || left[i] <= loc || right[i] <= loc ||
+                                        left[i] >= b - a || right[i] >= b - a))
+                    throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "malformed tree: a child index must exceed its parent's"};
+                nodes[i - o0] = v;
+                md[i - o0] = missing_bin[i] * 2 + (default_left[i] ? 1 : 0);
+            }
+        }
+        std::vector<double> vals(value + o0, value + o0 + std::max<int64_t>(nn, 0));
+        if (vals.empty()) vals.push_back(0.0);
+        int dev = 0;
+        HIPX(hipGetDevice(&dev));
+        hipDeviceProp_t prop;
+        HIPX(hipGetDeviceProperties(&prop, dev));
+        int4 *d_nodes = dalloc<int4>(nodes.size(), run.owned);
+        int32_t *d_md = dalloc<int32_t>(md.size(), run.owned);
+        int32_t *d_root = dalloc<int32_t>(root.size(), run.owned);
+        double *d_val = dalloc<double>(vals.size(), run.owned);
+        double *d_base = base ? dalloc<double>(K, run.owned) : nullptr;
+        HIPX(hipMemcpy(d_nodes, nodes.data(), nodes.size() * sizeof(int4), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(d_md, md.data(), md.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(d_root, root.data(), root.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(d_val, vals.data(), vals.size() * sizeof(double), hipMemcpyHostToDevice));
+        if (base) HIPX(hipMemcpy(d_base, base, K * sizeof(double), hipMemcpyHostToDevice));
+        // row batches bound the device copy of the matrix (bins + records)
+        RecLayout l;
+        l.n_tiles = (F + 125) / 126;
+        l.tile_f = (F + l.n_tiles - 1) / l.n_tiles;
+        l.rec = 16;
+        while (l.rec < l.tile_f + 2) l.rec *= 2;
+        const int64_t per_row = (int64_t)F + (int64_t)l.rec * l.n_tiles + 8 * K;
+        const int64_t batch = std::max<int64_t>(4096, std::min<int64_t>(n, ((int64_t)1 << 31) / per_row));
+        uint8_t *d_bins = dalloc<uint8_t>((size_t)F * batch, run.owned);
+        uint8_t *d_rec = dalloc<uint8_t>((size_t)l.rec * l.n_tiles * batch, run.owned);
+        double *d_out = dalloc<double>((size_t)batch * K, run.owned);
+        std::vector<uint8_t> stage((size_t)F * batch);
+        for (int64_t r0 = 0; r0 < n; r0 += batch) {
+            const int64_t m = std::min(batch, n - r0);
+            for (int f = 0; f < F; ++f)
+                std::memcpy(stage.data() + (size_t)f * m, bins_cm + (size_t)f * n + r0, (size_t)m);
+            HIPX(hipMemcpy(d_bins, stage.data(), (size_t)F * m, hipMemcpyHostToDevice));
+            HIPX(mb::launch_build_records(d_bins, d_rec, m, F, l.rec, l.tile_f, l.n_tiles, 4 * prop.multiProcessorCount,
+                                          nullptr));
+            mb::PredictArgs a{};
+            a.records = d_rec;
+            a.n = m;
+            a.rec_bytes = l.rec;
+            a.tile_f = l.tile_f;
+            a.n_tiles = l.n_tiles;
+            a.num_class = K;
+            a.nodes = d_nodes;
+            a.md = d_md;
+            a.value = d_val;
+            a.root = d_root;
+            a.max_steps = max_steps;
+            a.t0 = 0;
+            a.t1 = tree_end - tree_begin;
+            a.learning_rate = learning_rate;
+            a.base = d_base;
+            a.out = d_out;
+            const int grid = (int)std::min<int64_t>((m + 255) / 256, 16 * (int64_t)prop.multiProcessorCount);
+            HIPX(mb::launch_predict(a, grid, nullptr));
+            HIPX(hipMemcpy(out + r0 * K, d_out, (size_t)m * K * sizeof(double), hipMemcpyDeviceToHost));
+        }
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
 int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const double *raw,
                                int64_t round_index, float *grad, float *hess, int8_t *q_grad,
                                int8_t *q_hess, double *scales, char *err, int32_t err_len) {

@@ -31,4 +31,23 @@ hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_
 hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st);
 hipError_t launch_exp_sigmoid(const double *x, double *e, double *sg, int64_t n, hipStream_t st);
 
+// Batch prediction over row records (the training layout), one thread per
+// (row, class): trees t0 + k, t0 + k + K, ... < t1 of a flat ensemble whose
+// nodes hold absolute child indices.
+struct PredictArgs {
+    const uint8_t *records;
+    int64_t n;
+    int32_t rec_bytes, tile_f, n_tiles, num_class;
+    const int4 *nodes;        // {feature (-1: leaf), threshold bin, left, right}
+    const int32_t *md;        // missing_bin * 2 + default_left
+    const double *value;      // per node
+    const int32_t *root;      // per tree: index of its root node
+    int32_t max_steps;        // nodes of the largest tree: no walk is longer
+    int64_t t0, t1;           // trees [t0, t1); t0 a multiple of num_class
+    double learning_rate;
+    const double *base;       // num_class base scores, or null (a range after iteration 0)
+    double *out;              // n x num_class
+};
+hipError_t launch_predict(const PredictArgs &a, int grid, hipStream_t st);
+
 }  // namespace mb

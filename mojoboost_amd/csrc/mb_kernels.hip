@@ -2245,6 +2245,46 @@ __global__ __launch_bounds__(256) void k_build_records(const uint8_t *bins_cm, u
     }
 }
 
+// Raw scores of a flat ensemble (Tree.predict_row, src/mojotrees/tree.mojo:
+// 483-505; Booster.predict_raw_row, src/mojotrees/boosting.mojo:1722-1760):
+// a row's bin for a node's feature comes from its record; the missing bin
+// follows the default direction, otherwise bin <= threshold goes left. The
+// class's trees are added in ascending order as fma(learning_rate, value,
+// score), the host predictor's fused update, so the scores are its bits.
+__global__ __launch_bounds__(256) void k_predict(PredictArgs a) {
+    const int k = blockIdx.y;
+    const int K = a.num_class;
+    const int tf = a.tile_f;
+    const bool tiled = a.n_tiles > 1;
+    const size_t tile_bytes = (size_t)a.n * a.rec_bytes;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += stride) {
+        const uint8_t *rb = a.records + r * a.rec_bytes;
+        double acc = a.base ? a.base[k] : 0.0;
+        for (int64_t t = a.t0 + k; t < a.t1; t += K) {
+            int node = a.root[t];
+            int4 nd = a.nodes[node];
+            // children have larger indices than their parent (host-checked),
+            // so a walk ends within the tree's node count
+            for (int d = 0; nd.x >= 0 && d < a.max_steps; ++d) {
+                int b;
+                if (tiled) {
+                    const int tt = nd.x / tf;
+                    b = rb[(size_t)tt * tile_bytes + (nd.x - tt * tf)];
+                } else {
+                    b = rb[nd.x];
+                }
+                const int md = a.md[node];
+                const bool left = (b == (md >> 1)) ? (md & 1) : (b <= nd.y);
+                node = left ? nd.z : nd.w;
+                nd = a.nodes[node];
+            }
+            acc = fma(a.learning_rate, a.value[node], acc);
+        }
+        a.out[r * K + k] = acc;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_fill_f64(double *p, int64_t n, int K, const double *base) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n * K; i += stride)
@@ -2410,6 +2450,10 @@ hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_
                                 int tile_f, int n_tiles, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_build_records, dim3(grid), dim3(256), 0, st, bins_cm, records, n, F, rec, tile_f,
                        n_tiles);
+    return hipGetLastError();
+}
+hipError_t launch_predict(const PredictArgs &a, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_predict, dim3(grid, a.num_class), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st) {

@@ -62,7 +62,7 @@ class Dataset:
         f = C.c_void_p()
         err = C.create_string_buffer(1024)
         check(lib().mbh_train(self.h, C.byref(p), C.byref(f), err, 1024), err)
-        return Fit(f, self.n_rows)
+        return Fit(f, self.n_rows, p.learning_rate)
 
     def objective_quantize(self, raw, round_index=0, **params):
         n = self.n_rows
@@ -112,10 +112,11 @@ class Dataset:
 class Fit:
     """Trees grown by mbh_train, as flat arrays."""
 
-    def __init__(self, handle, n_rows):
+    def __init__(self, handle, n_rows, learning_rate=0.1):
         L = lib()
         self.h = handle
         self.n_rows = n_rows
+        self.learning_rate = float(learning_rate)
         self.n_trees = int(L.mbh_fit_num_trees(handle))
         self.num_class = int(L.mbh_fit_num_class(handle))
         nn = int(L.mbh_fit_total_nodes(handle))
@@ -144,6 +145,21 @@ class Fit:
         return {k: getattr(self, k)[a:b] for k in
                 ("feature", "threshold", "left", "right", "value", "default_left",
                  "missing_bin", "gain", "count")}
+
+    def predict_binned(self, bins_cm, n_rows, n_features, tree_begin=0, tree_end=None):
+        """Raw scores of trees [tree_begin, tree_end) on the device, from
+        column-major uint8 bins; the base score is added when the range
+        starts at tree 0."""
+        tree_end = self.n_trees if tree_end is None else tree_end
+        bins_cm = np.ascontiguousarray(bins_cm, np.uint8).ravel()
+        out = np.zeros(n_rows * self.num_class)
+        err = C.create_string_buffer(512)
+        check(lib().mbh_predict_binned(
+            ptr(bins_cm), n_rows, n_features, self.num_class, self.learning_rate,
+            ptr(self.base) if tree_begin == 0 else None, ptr(self.off), tree_begin, tree_end,
+            ptr(self.feature), ptr(self.threshold), ptr(self.left), ptr(self.right),
+            ptr(self.value), ptr(self.default_left), ptr(self.missing_bin), ptr(out), err, 512), err)
+        return out
 
     def train_raw(self):
         out = np.zeros(self.n_rows * self.num_class)

@@ -41,6 +41,16 @@ def _colmajor(X):
     return np.asfortranarray(X), X.shape[0], X.shape[1]
 
 
+def _predict_device(device):
+    if device is None or device == "cpu":
+        return _lib.DEVICE_CPU
+    if device == "gpu":
+        return _lib.DEVICE_GPU
+    if device == "auto":
+        return _lib.DEVICE_AUTO
+    raise ValueError(f"device must be None, 'cpu', 'gpu' or 'auto', not {device!r}")
+
+
 class _Booster:
     """An owned model handle."""
 
@@ -76,15 +86,15 @@ class _Booster:
     def num_iterations(self):
         return self._count("mojotrees_model_num_iterations")
 
-    def predict(self, X, raw=False, start_iteration=0, num_iteration=0):
+    def predict(self, X, raw=False, start_iteration=0, num_iteration=0, device=None):
         Xf, n, f = _colmajor(X)
         k = self.num_classes
         out = np.zeros(n * k)
         e = _Error()
         flags = _lib.PREDICT_RAW if raw else _lib.PREDICT_RESPONSE
         e.check(lib().mojotrees_predict_ex(self.h, ptr(Xf.ravel(order="K")), n, f,
-                                           start_iteration, num_iteration, flags,
-                                           _lib.DEVICE_CPU, ptr(out), out.size, e.h))
+                                           start_iteration, num_iteration or 0, flags,
+                                           _predict_device(device), ptr(out), out.size, e.h))
         return out.reshape(n, k) if k > 1 else out
 
     def save(self, path):
@@ -198,9 +208,13 @@ class MojoTreesRegressor(_Base):
         self.booster_ = _train(X, y, self._params())
         return self
 
-    def predict(self, X, raw_score=False):
+    def predict(self, X, raw_score=False, start_iteration=0, num_iteration=None, device=None):
+        """`device` as in the reference (python/mojotrees/sklearn.py:6016-6060):
+        None predicts on the CPU, "gpu" on the device (an error without one),
+        "auto" by the library's rule. Both give the same scores."""
         self._check_fitted()
-        return self.booster_.predict(X, raw=raw_score)
+        return self.booster_.predict(X, raw=raw_score, start_iteration=start_iteration,
+                                     num_iteration=num_iteration, device=device)
 
     @classmethod
     def load(cls, path):
@@ -228,19 +242,22 @@ class MojoTreesClassifier(_Base):
             self.booster_ = _train(X, yi.astype(np.float64), params + f" num_class={k}")
         return self
 
-    def predict_proba(self, X):
+    def predict_proba(self, X, start_iteration=0, num_iteration=None, device=None):
         self._check_fitted()
-        p = self.booster_.predict(X)
+        p = self.booster_.predict(X, start_iteration=start_iteration, num_iteration=num_iteration,
+                                  device=device)
         if self.booster_.num_classes == 1:
             return np.column_stack([1.0 - p, p])
         return p.reshape(-1, self.booster_.num_classes)
 
-    def predict(self, X):
-        return self.classes_[np.argmax(self.predict_proba(X), axis=1)]
+    def predict(self, X, start_iteration=0, num_iteration=None, device=None):
+        return self.classes_[np.argmax(self.predict_proba(X, start_iteration, num_iteration, device),
+                                       axis=1)]
 
-    def decision_function(self, X):
+    def decision_function(self, X, start_iteration=0, num_iteration=None, device=None):
         self._check_fitted()
-        raw = self.booster_.predict(X, raw=True)
+        raw = self.booster_.predict(X, raw=True, start_iteration=start_iteration,
+                                    num_iteration=num_iteration, device=device)
         k = self.booster_.num_classes
         return raw if k == 1 else raw.reshape(-1, k)
 

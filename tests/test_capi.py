@@ -115,6 +115,26 @@ def test_gpu_request_without_gpu_is_unsupported():
     assert rc == _lib.ERROR_UNSUPPORTED and "gfx950" in msg and h.value is None
 
 
+def test_gpu_predict_without_gpu_is_unsupported(tmp_path):
+    if lib().mojotrees_gpu_available():
+        pytest.skip("a GPU is present on this host")
+    L = lib()
+    path = tmp_path / "m.txt"
+    write_model(path)
+    rc, msg, h = _load(path)
+    assert rc == 0
+    x = np.zeros(12)
+    out = np.zeros(6)
+    e = L.mojotrees_error_create()
+    assert L.mojotrees_predict_ex(h, ptr(x), 6, 2, 0, 0, 1, _lib.DEVICE_GPU, ptr(out), 6, e) == \
+        _lib.ERROR_UNSUPPORTED
+    assert b"gfx950" in L.mojotrees_error_message(e)
+    # AUTO without a GPU predicts on the CPU
+    assert L.mojotrees_predict_ex(h, ptr(x), 6, 2, 0, 0, 1, _lib.DEVICE_AUTO, ptr(out), 6, e) == 0
+    L.mojotrees_error_free(e)
+    L.mojotrees_model_free(h)
+
+
 def test_parameter_keys():
     L = lib()
     out = C.c_char_p()

@@ -493,3 +493,48 @@ def test_goss_count_paths_agree(dev):
     assert a.n_trees == ref.n_trees
     assert _rel_err(a.train_raw(), ref.train_raw(n)) < 1e-5
     assert _tree_agreement(a, ref) >= ref.n_trees - 1
+
+
+# ------------------------------------------------------------- prediction
+def test_device_predict_bit_exact(dev):
+    """Device prediction (mbh_predict_binned) of a trained ensemble: the raw
+    scores of the training rows equal the trainer's own (same fused updates in
+    the same order) and the oracle's host predictor, bit for bit; an
+    iteration range without tree 0 leaves the base score out."""
+    n = 120_000
+    bins, y, mb, nb = c2_like(n, f=20, seed=29, nb=63)
+    kw = dict(objective=1, num_iterations=20, num_leaves=63, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    fit = dev.Dataset(bins, n, 20, nb, y, missing_bin=mb).train(**kw)
+    ref = O.train(bins, n, 20, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    raw = fit.predict_binned(bins, n, 20)
+    assert np.array_equal(bits(raw), bits(fit.train_raw()))
+    want, _ = ref.predict_binned(bins, n, 20)
+    assert np.array_equal(bits(raw), bits(want))
+    tail = fit.predict_binned(bins, n, 20, tree_begin=5)
+    head = fit.predict_binned(bins, n, 20, tree_begin=0, tree_end=5)
+    assert np.allclose(head + tail, raw, rtol=1e-12, atol=1e-12)
+
+
+def test_device_predict_wide_multiclass_through_c_abi(dev):
+    """mojotrees_predict_ex with device=GPU against device=CPU: multiclass
+    softmax and a 300-feature model (feature tiles), raw and response,
+    whole ensemble and iteration slices -- identical bits."""
+    from mojoboost_amd.sklearn import MojoTreesClassifier
+
+    rng = np.random.default_rng(31)
+    for n, f, k in ((40_000, 12, 4), (20_000, 300, 2)):
+        X = rng.normal(size=(n, f))
+        X[rng.uniform(size=(n, f)) < 0.01] = np.nan
+        score = np.nan_to_num(X[:, :k]) + 0.5 * rng.normal(size=(n, k))
+        y = np.argmax(score, axis=1)
+        est = MojoTreesClassifier(n_estimators=8, num_leaves=15, learning_rate=0.2, max_bin=63,
+                                  device="gpu", use_quantized_grad=True).fit(X, y)
+        for s0, num in ((0, None), (3, None), (0, 5), (2, 3)):
+            a = est.decision_function(X, start_iteration=s0, num_iteration=num)
+            b = est.decision_function(X, start_iteration=s0, num_iteration=num, device="gpu")
+            assert np.array_equal(bits(a), bits(b)), (n, f, s0, num)
+            pa = est.predict_proba(X, start_iteration=s0, num_iteration=num)
+            pb = est.predict_proba(X, start_iteration=s0, num_iteration=num, device="gpu")
+            assert np.array_equal(bits(pa), bits(pb)), (n, f, s0, num)
+        assert np.array_equal(est.predict(X, device="auto"), est.predict(X))
