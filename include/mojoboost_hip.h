@@ -37,6 +37,7 @@ extern "C" {
 #define MBH_OBJ_REGRESSION 0
 #define MBH_OBJ_BINARY 1
 #define MBH_OBJ_MULTICLASS 2
+#define MBH_OBJ_LAMBDARANK 3  /* needs query groups (mbh_dataset_set_groups) */
 
 typedef struct mbh_dataset mbh_dataset;
 typedef struct mbh_fit mbh_fit;
@@ -73,6 +74,12 @@ typedef struct {
      * Both give the reference's sample. Defaults 10 and 0. */
     double goss_band;
     int32_t goss_exact_walk;
+    /* lambdarank (LightGBM names): pairs whose better-ranked member sits
+     * within the truncation level, the pairwise logistic's scale, per-pair
+     * and per-query normalization. Defaults 30, 1.0, 1. */
+    int32_t lambdarank_truncation_level;
+    int32_t lambdarank_norm;
+    double lambdarank_sigmoid;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -130,6 +137,35 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *   [16] their algorithmic bytes: [13] * 9 (row id in, bin, row id out)
  *        + [12] * (n_features + gh) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
+
+/* Query groups of a resident dataset, for objective lambdarank: counts[q]
+ * rows per query, in row order (LightGBM's `group`,
+ * ranking.groups_from_counts, src/mojotrees/ranking.mojo:152-169); counts must
+ * be positive and sum to n_rows, and a query holds at most 2048 rows. */
+int32_t mbh_dataset_set_groups(mbh_dataset *ds, const int32_t *counts, int64_t n_queries,
+                               char *err, int32_t err_len);
+
+/* LambdaRank gradients and hessians (binary64) of one set of raw scores on
+ * the device (ranking.lambdarank_gradients, src/mojotrees/ranking.mojo:
+ * 603-654, unweighted), with the dataset's labels and groups. */
+int32_t mbh_lambdarank(mbh_dataset *ds, const mbh_params *params, const double *raw,
+                       double *grad, double *hess, char *err, int32_t err_len);
+
+/* A ranker through the C ABI's model type: bins the column-major matrix with
+ * the parameters' max_bin (as mojotrees_train_dense does), trains objective
+ * lambdarank on the device over query groups (group_counts, one row count
+ * per query) and returns a MojoTreesModel that every mojotrees_* function
+ * takes (raw-score predictions, v4 save/load with objective 7). The
+ * reference serves its ranker only from Python (MojoTreesRanker,
+ * python/mojotrees/sklearn.py:6951); this entry is what an estimator or a C
+ * caller uses here. Parameters as for mojotrees_train_dense plus
+ * lambdarank_truncation_level, sigmoid, lambdarank_norm. */
+struct MojoTreesModel;
+struct MojoTreesError;
+int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_features,
+                               const double *labels, const int32_t *group_counts,
+                               int64_t n_groups, const char *parameters,
+                               struct MojoTreesModel **out_model, struct MojoTreesError *error);
 
 /* Raw scores on the device (Booster.predict_raw_row,
  * src/mojotrees/boosting.mojo:1722-1760; the reference's device counterpart is

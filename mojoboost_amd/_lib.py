@@ -17,7 +17,7 @@ ERROR_UNSUPPORTED = -4
 DEVICE_CPU, DEVICE_GPU, DEVICE_AUTO = 0, 1, 2
 PREDICT_RESPONSE, PREDICT_RAW = 0, 1
 IMPORTANCE_SPLIT, IMPORTANCE_GAIN = 0, 1
-OBJ_REGRESSION, OBJ_BINARY, OBJ_MULTICLASS = 0, 1, 2
+OBJ_REGRESSION, OBJ_BINARY, OBJ_MULTICLASS, OBJ_LAMBDARANK = 0, 1, 2, 3
 
 # Every symbol include/mojotrees.h and include/mojoboost_hip.h declare.
 MOJOTREES_SYMBOLS = [
@@ -35,7 +35,7 @@ MBH_SYMBOLS = [
     "mbh_fit_free", "mbh_fit_num_trees", "mbh_fit_num_class", "mbh_fit_total_nodes",
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
-    "mbh_predict_binned",
+    "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
 ]
 
 
@@ -66,6 +66,9 @@ class MbhParams(C.Structure):
         ("other_rate", C.c_double),
         ("goss_band", C.c_double),
         ("goss_exact_walk", C.c_int32),
+        ("lambdarank_truncation_level", C.c_int32),
+        ("lambdarank_norm", C.c_int32),
+        ("lambdarank_sigmoid", C.c_double),
     ]
 
 
@@ -76,7 +79,8 @@ def mbh_params(**kw) -> MbhParams:
                   feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
                   quant_seed=11, time_histograms=0, use_quantized_grad=1, goss=0,
-                  top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0)
+                  top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0,
+                  lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0)
     for k, v in kw.items():
         setattr(p, k, v)
     return p
@@ -144,6 +148,9 @@ def lib():
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),
         "mbh_predict_binned": (I32, [V, I64, I32, I32, C.c_double, V, V, I64, I64, V, V, V, V, V, V, V,
                                      V, C.c_char_p, I32]),
+        "mbh_dataset_set_groups": (I32, [V, V, I64, C.c_char_p, I32]),
+        "mbh_lambdarank": (I32, [V, P(MbhParams), V, V, V, C.c_char_p, I32]),
+        "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, I64, C.c_char_p, V, V]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

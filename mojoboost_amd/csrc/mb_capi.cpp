@@ -100,6 +100,9 @@ const std::map<std::string, std::string> &aliases() {
         {"min_data_in_bin", "min_data_in_bin"},
         {"bin_construct_sample_cnt", "bin_construct_sample_cnt"},
         {"data_random_seed", "data_random_seed"},
+        {"lambdarank_truncation_level", "lambdarank_truncation_level"},
+        {"sigmoid", "sigmoid"},
+        {"lambdarank_norm", "lambdarank_norm"},
     };
     return a;
 }
@@ -110,7 +113,7 @@ const char *kPrimaryKeys =
     "feature_fraction_bynode,feature_fraction_seed,max_bin,alpha,device,use_missing,"
     "use_quantized_grad,num_grad_quant_bins,stochastic_rounding,bagging_fraction,"
     "bagging_freq,bagging_seed,boosting,top_rate,other_rate,min_data_in_bin,"
-    "bin_construct_sample_cnt,data_random_seed";
+    "bin_construct_sample_cnt,data_random_seed,lambdarank_truncation_level,sigmoid,lambdarank_norm";
 
 struct Config {
     mbh_params p{};
@@ -176,6 +179,9 @@ Config parse(const char *spec) {
     p.stochastic_rounding = 1;
     p.quant_seed = 11;
     p.time_histograms = 0;
+    p.lambdarank_truncation_level = 30;  // RankerParams.default (ranking.mojo:478-490)
+    p.lambdarank_norm = 1;
+    p.lambdarank_sigmoid = 1.0;
     if (!spec) return c;
     std::istringstream in(spec);
     std::string item;
@@ -195,6 +201,8 @@ Config parse(const char *spec) {
                 p.objective = MBH_OBJ_BINARY;
             else if (val == "multiclass" || val == "softmax")
                 p.objective = MBH_OBJ_MULTICLASS;
+            else if (val == "lambdarank")
+                p.objective = MBH_OBJ_LAMBDARANK;
             else if (val == "poisson" || val == "huber" || val == "quantile" || val == "mae" ||
                      val == "regression_l1" || val == "l1")
                 throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
@@ -265,6 +273,12 @@ Config parse(const char *spec) {
             c.bin_sample = to_int(k, val);
         } else if (k == "data_random_seed") {
             c.data_seed = to_int(k, val);
+        } else if (k == "lambdarank_truncation_level") {
+            p.lambdarank_truncation_level = (int)to_int(k, val);
+        } else if (k == "sigmoid") {
+            p.lambdarank_sigmoid = to_double(k, val);
+        } else if (k == "lambdarank_norm") {
+            p.lambdarank_norm = to_bool(k, val) ? 1 : 0;
         }
     }
     if (c.saw_num_class && p.objective != MBH_OBJ_MULTICLASS)
@@ -363,6 +377,67 @@ int32_t predict_common(const MojoTreesModel *model, const double *data, int64_t 
     });
 }
 
+// Host binning, the resident dataset, device training and the model: the
+// common body of the training entry points. groups: per-query row counts
+// (lambdarank), or null.
+MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_features, const double *labels,
+                            const int32_t *groups, int64_t n_groups, Config &c) {
+    mb::BinMapper mapper = mb::fit_bins(data, n_rows, (int)n_features, c.max_bin, c.min_data_in_bin,
+                                        c.use_missing, c.bin_sample, c.data_seed);
+    std::vector<uint8_t> bins((size_t)n_rows * n_features);
+    mapper.transform(data, n_rows, bins.data());
+    char msg[512] = {0};
+    mbh_dataset *ds = nullptr;
+    int32_t rc = mbh_dataset_create(bins.data(), n_rows, (int32_t)n_features, c.max_bin,
+                                    mapper.missing_bin.data(), labels, &ds, msg, sizeof(msg));
+    if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
+    if (groups) {
+        rc = mbh_dataset_set_groups(ds, groups, n_groups, msg, sizeof(msg));
+        if (rc != MOJOTREES_OK) {
+            mbh_dataset_free(ds);
+            throw ApiError{rc, msg};
+        }
+    }
+    mbh_fit *fit = nullptr;
+    rc = mbh_train(ds, &c.p, &fit, msg, sizeof(msg));
+    mbh_dataset_free(ds);
+    if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
+    auto *model = new MojoTreesModel();
+    mb::Model &m = model->m;
+    // model objective codes: 0 regression, 1 binary, -1 multiclass, 7
+    // lambdarank (objective_registry.mojo:289)
+    m.objective = c.p.objective == MBH_OBJ_MULTICLASS ? -1
+                  : c.p.objective == MBH_OBJ_LAMBDARANK ? 7
+                                                         : c.p.objective;
+    m.num_class = mbh_fit_num_class(fit);
+    m.learning_rate = c.p.learning_rate;
+    m.mapper = mapper;
+    const int nt = mbh_fit_num_trees(fit);
+    const int64_t nn = mbh_fit_total_nodes(fit);
+    m.base.resize(m.num_class);
+    m.offsets.resize(nt + 1);
+    m.feature.resize(nn);
+    m.threshold.resize(nn);
+    m.left.resize(nn);
+    m.right.resize(nn);
+    m.value.resize(nn);
+    m.default_left.resize(nn);
+    m.missing_bin.resize(nn);
+    m.gain.resize(nn);
+    m.count.resize(nn);
+    mbh_fit_arrays(fit, m.base.data(), m.offsets.data(), m.feature.data(), m.threshold.data(), m.left.data(),
+                   m.right.data(), m.value.data(), m.default_left.data(), m.missing_bin.data(), m.gain.data(),
+                   m.count.data());
+    mbh_fit_free(fit);
+    m.n_leaves.resize(nt);
+    for (int t = 0; t < nt; ++t) {
+        int leaves = 0;
+        for (int64_t i = m.offsets[t]; i < m.offsets[t + 1]; ++i) leaves += m.feature[i] < 0;
+        m.n_leaves[t] = leaves;
+    }
+    return model;
+}
+
 }  // namespace
 
 extern "C" {
@@ -390,6 +465,9 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
         if (n_rows <= 0 || n_features <= 0)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "n_rows and n_features must be positive"};
         Config c = parse(parameters);
+        if (c.p.objective == MBH_OBJ_LAMBDARANK)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
+                           "objective=lambdarank needs query groups: train it with mbh_train_ranker_dense"};
         if (weights)
             throw ApiError{MOJOTREES_ERROR_UNSUPPORTED, "sample weights are not served by the device training path"};
         if (c.device == MOJOTREES_DEVICE_CPU)
@@ -402,48 +480,7 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
             for (int64_t r = 0; r < n_rows; ++r)
                 if (labels[r] != 0.0 && labels[r] != 1.0)
                     throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "binary labels must be 0 or 1"};
-        mb::BinMapper mapper = mb::fit_bins(data, n_rows, (int)n_features, c.max_bin, c.min_data_in_bin,
-                                            c.use_missing, c.bin_sample, c.data_seed);
-        std::vector<uint8_t> bins((size_t)n_rows * n_features);
-        mapper.transform(data, n_rows, bins.data());
-        char msg[512] = {0};
-        mbh_dataset *ds = nullptr;
-        int32_t rc = mbh_dataset_create(bins.data(), n_rows, (int32_t)n_features, c.max_bin,
-                                        mapper.missing_bin.data(), labels, &ds, msg, sizeof(msg));
-        if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
-        mbh_fit *fit = nullptr;
-        rc = mbh_train(ds, &c.p, &fit, msg, sizeof(msg));
-        mbh_dataset_free(ds);
-        if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
-        auto *model = new MojoTreesModel();
-        mb::Model &m = model->m;
-        m.objective = c.p.objective == MBH_OBJ_MULTICLASS ? -1 : c.p.objective;
-        m.num_class = mbh_fit_num_class(fit);
-        m.learning_rate = c.p.learning_rate;
-        m.mapper = mapper;
-        const int nt = mbh_fit_num_trees(fit);
-        const int64_t nn = mbh_fit_total_nodes(fit);
-        m.base.resize(m.num_class);
-        m.offsets.resize(nt + 1);
-        m.feature.resize(nn);
-        m.threshold.resize(nn);
-        m.left.resize(nn);
-        m.right.resize(nn);
-        m.value.resize(nn);
-        m.default_left.resize(nn);
-        m.missing_bin.resize(nn);
-        m.gain.resize(nn);
-        m.count.resize(nn);
-        mbh_fit_arrays(fit, m.base.data(), m.offsets.data(), m.feature.data(), m.threshold.data(), m.left.data(),
-                       m.right.data(), m.value.data(), m.default_left.data(), m.missing_bin.data(), m.gain.data(),
-                       m.count.data());
-        mbh_fit_free(fit);
-        m.n_leaves.resize(nt);
-        for (int t = 0; t < nt; ++t) {
-            int leaves = 0;
-            for (int64_t i = m.offsets[t]; i < m.offsets[t + 1]; ++i) leaves += m.feature[i] < 0;
-            m.n_leaves[t] = leaves;
-        }
+        MojoTreesModel *model = train_model(data, n_rows, n_features, labels, nullptr, 0, c);
         *out_model = model;
         return MOJOTREES_OK;
     });
@@ -577,5 +614,30 @@ int32_t mojotrees_parameter_keys(char **out_text, MojoTreesError *error) {
 
 void mojotrees_string_free(char *text) { std::free(text); }
 void mojotrees_model_free(MojoTreesModel *model) { delete model; }
+
+int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_features, const double *labels,
+                               const int32_t *group_counts, int64_t n_groups, const char *parameters,
+                               MojoTreesModel **out_model, MojoTreesError *error) {
+    return guarded(error, [&]() -> int32_t {
+        if (!data || !labels || !group_counts || !out_model)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "data, labels, group_counts and out_model must not be NULL"};
+        if (n_rows <= 0 || n_features <= 0 || n_groups <= 0)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "n_rows, n_features and n_groups must be positive"};
+        Config c = parse(parameters);
+        c.p.objective = MBH_OBJ_LAMBDARANK;
+        if (c.device == MOJOTREES_DEVICE_CPU)
+            throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
+                           "device=cpu: this library is the MI355X training path and has no CPU trainer"};
+        if (mbh_device_count() == 0)
+            throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
+                           "no gfx950 (MI355X) GPU is available; device=gpu never falls back to the CPU"};
+        // check_labels (ranking.mojo:221-232)
+        for (int64_t r = 0; r < n_rows; ++r)
+            if (!(labels[r] >= 0.0 && labels[r] <= 30.0) || labels[r] != std::floor(labels[r]))
+                throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "relevance labels must be integers in [0, 30]"};
+        *out_model = train_model(data, n_rows, n_features, labels, group_counts, n_groups, c);
+        return MOJOTREES_OK;
+    });
+}
 
 }  // extern "C"

@@ -112,6 +112,12 @@ struct mbh_dataset {
     std::vector<double> class_count;  // when labels are integers in [0, 1024)
     bool labels_integral = false;
     double label_min = 0.0, label_max = 0.0;
+    // lambdarank: labels as relevance grades (when integers in [0, 30]) and
+    // the query boundaries set by mbh_dataset_set_groups
+    std::vector<int8_t> grades;
+    std::vector<int64_t> qstart;
+    int64_t *d_qstart = nullptr;
+    int max_query = 0;
     std::vector<void *> owned;
     ~mbh_dataset() {
         for (void *p : owned) (void)hipFree(p);
@@ -178,8 +184,18 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     auto bad = [](const std::string &m) { throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, m}; };
     auto unsup = [](const std::string &m) { throw Error{MOJOTREES_ERROR_UNSUPPORTED, m}; };
     if (p->objective != MBH_OBJ_REGRESSION && p->objective != MBH_OBJ_BINARY &&
-        p->objective != MBH_OBJ_MULTICLASS)
+        p->objective != MBH_OBJ_MULTICLASS && p->objective != MBH_OBJ_LAMBDARANK)
         bad("unknown objective");
+    if (p->objective == MBH_OBJ_LAMBDARANK) {
+        // train_ranker's checks (ranking.mojo:205-232, :492-497, :713-737)
+        if (ds->qstart.empty()) bad("objective lambdarank needs query groups");
+        if (ds->grades.empty()) bad("relevance labels must be integers in [0, 30]");
+        if (p->lambdarank_truncation_level < 1) bad("lambdarank_truncation_level must be positive");
+        if (!(p->lambdarank_sigmoid > 0.0)) bad("sigmoid must be positive");
+        if (p->bagging_freq > 0 && p->bagging_fraction < 1.0)
+            unsup("query bagging for lambdarank is not built on the device path");
+        if (p->goss) unsup("GOSS with lambdarank is not built on the device path");
+    }
     if (p->objective == MBH_OBJ_MULTICLASS) {
         if (p->num_class < 2 || p->num_class > kMaxClass) bad("num_class must be in [2, 1024]");
         if (!ds->labels_integral || ds->label_min < 0.0 || ds->label_max >= (double)p->num_class)
@@ -317,6 +333,8 @@ double base_score_for(const mbh_dataset *ds, int objective) {
 // Per-class base scores. boosting.train_multiclass
 // (src/mojotrees/boosting.mojo:4167-4250): log of each class's clamped share.
 std::vector<double> base_scores_for(const mbh_dataset *ds, int objective, int K) {
+    // train_ranker boosts from 0 (ranking.mojo:700-712)
+    if (objective == MBH_OBJ_LAMBDARANK) return {0.0};
     if (objective != MBH_OBJ_MULTICLASS) return {base_score_for(ds, objective)};
     std::vector<double> b(K);
     for (int k = 0; k < K; ++k) {
@@ -411,6 +429,42 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.quant_seed = p->quant_seed;
     // boosting.round_has_constant_hessian: squared error without weights.
     hp.const_hessian = p->objective == MBH_OBJ_REGRESSION ? 1 : 0;
+    if (p->objective == MBH_OBJ_LAMBDARANK) {
+        // binary64 lambdas (the reference's ranker does not narrow them), the
+        // queries, 1 / maxDCG per query at the truncation level and the
+        // position discounts (ranking.mojo:240-245, :306-338), on the host
+        hp.grad64 = 1;
+        hp.rank_trunc = p->lambdarank_truncation_level;
+        hp.rank_norm = p->lambdarank_norm ? 1 : 0;
+        hp.rank_sigma = p->lambdarank_sigmoid;
+        s.grad64 = dalloc<double>(ds->n, run.owned);
+        s.hess64 = dalloc<double>(ds->n, run.owned);
+        s.stats64 = dalloc<unsigned long long>(4, run.owned);
+        HIPX(hipMemset(s.stats64, 0, 4 * sizeof(unsigned long long)));
+        const int64_t nq = (int64_t)ds->qstart.size() - 1;
+        std::vector<double> disc(ds->max_query), inv(nq);
+        for (int i = 0; i < ds->max_query; ++i) disc[i] = 1.0 / mb::ref_log2((double)i + 2.0);
+        for (int64_t q = 0; q < nq; ++q) {
+            const int64_t a = ds->qstart[q], c = ds->qstart[q + 1] - a;
+            std::vector<int> g(ds->grades.begin() + a, ds->grades.begin() + a + c);
+            std::sort(g.begin(), g.end(), [](int x, int y) { return x > y; });
+            const int64_t m = std::min<int64_t>(c, hp.rank_trunc);
+            double md = 0.0;
+            for (int64_t j = 0; j < m; ++j) md += mb::label_gain(g[j]) * disc[j];
+            inv[q] = md > 0.0 ? 1.0 / md : 0.0;
+        }
+        double *d_disc = dalloc<double>(std::max(1, ds->max_query), run.owned);
+        double *d_inv = dalloc<double>(nq, run.owned);
+        HIPX(hipMemcpy(d_disc, disc.data(), disc.size() * sizeof(double), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(d_inv, inv.data(), inv.size() * sizeof(double), hipMemcpyHostToDevice));
+        s.rank_disc = d_disc;
+        s.inv_max_dcg = d_inv;
+        s.qstart = ds->d_qstart;
+        s.n_queries = (int32_t)nq;
+        int pad = 1;
+        while (pad < ds->max_query) pad <<= 1;
+        s.rank_pad = pad;
+    }
     hp.quantized = p->use_quantized_grad ? 1 : 0;
     hp.goss = p->goss ? 1 : 0;
     // GossParams.warmup (goss.mojo:102-157): floor(1 / learning_rate) rounds
@@ -555,6 +609,10 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         ds->labels_integral = lo >= 0.0 && hi < (double)kMaxClass;
         for (int64_t r = 0; r < n && ds->labels_integral; ++r)
             if (labels[r] != std::floor(labels[r])) ds->labels_integral = false;
+        if (ds->labels_integral && hi <= 30.0) {
+            ds->grades.resize(n);
+            for (int64_t r = 0; r < n; ++r) ds->grades[r] = (int8_t)labels[r];
+        }
         if (ds->labels_integral) {
             ds->class_count.assign((size_t)hi + 1, 0.0);
             for (int64_t r = 0; r < n; ++r) ds->class_count[(size_t)labels[r]] += 1.0;
@@ -860,6 +918,62 @@ int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out
         HIPX(mb::launch_exp_sigmoid(dx, de, dsg, n, nullptr));
         HIPX(hipMemcpy(out_exp, de, n * sizeof(double), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(out_sig, dsg, n * sizeof(double), hipMemcpyDeviceToHost));
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_dataset_set_groups(mbh_dataset *ds, const int32_t *counts, int64_t nq, char *err, int32_t err_len) {
+    if (!ds || !counts || nq < 1) {
+        set_err(err, err_len, "group must contain at least one query");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        // groups_from_counts + check_groups (ranking.mojo:152-169, :205-218)
+        std::vector<int64_t> st(nq + 1, 0);
+        int max_q = 0;
+        for (int64_t q = 0; q < nq; ++q) {
+            if (counts[q] <= 0) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "group counts must be positive"};
+            st[q + 1] = st[q] + counts[q];
+            max_q = std::max(max_q, counts[q]);
+        }
+        if (st[nq] != ds->n) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "group counts must sum to n_rows"};
+        if (max_q > mb::kMaxQueryRows)
+            throw Error{MOJOTREES_ERROR_UNSUPPORTED, "a query holds more than 2048 rows (the device sorts a query in LDS)"};
+        int64_t *d = dalloc<int64_t>(nq + 1, ds->owned);
+        HIPX(hipMemcpy(d, st.data(), st.size() * sizeof(int64_t), hipMemcpyHostToDevice));
+        ds->qstart = std::move(st);
+        ds->d_qstart = d;
+        ds->max_query = max_q;
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_lambdarank(mbh_dataset *ds, const mbh_params *p, const double *raw, double *grad, double *hess,
+                       char *err, int32_t err_len) {
+    if (!ds || !p || !raw || !grad || !hess) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        mbh_params p1 = *p;
+        p1.objective = MBH_OBJ_LAMBDARANK;
+        p1.num_iterations = 1;
+        check_params(ds, &p1);
+        Run run;
+        TrainBuffers tb = setup_state(ds, &p1, run);
+        mb::DevState &s = tb.s;
+        HIPX(hipMemcpy(s.raw, raw, ds->n * sizeof(double), hipMemcpyHostToDevice));
+        HIPX(mb::prepare_kernels(s));
+        HIPX(mb::launch_objective(s, 8 * ds->n_cu, nullptr));
+        HIPX(hipDeviceSynchronize());
+        HIPX(hipMemcpy(grad, s.grad64, ds->n * sizeof(double), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(hess, s.hess64, ds->n * sizeof(double), hipMemcpyDeviceToHost));
     } catch (const Error &e) {
         set_err(err, err_len, e.msg);
         return e.code;

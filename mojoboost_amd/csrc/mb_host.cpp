@@ -300,7 +300,7 @@ Model Model::load(const std::string &path) {
     const std::string kind = next();
     if (kind == "objective") {
         m.objective = (int)geti();
-        if (m.objective != 0 && m.objective != 1)
+        if (m.objective != 0 && m.objective != 1 && m.objective != 7)
             throw std::runtime_error("objective " + std::to_string(m.objective) + " is not served by this library");
         expect("learning_rate");
         m.learning_rate = from_bits(next());

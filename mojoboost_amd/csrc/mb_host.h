@@ -33,7 +33,7 @@ BinMapper fit_bins(const double *x, int64_t n_rows, int n_features, int max_bins
                    int min_data_in_bin, bool use_missing, int64_t sample_cnt, int64_t seed);
 
 struct Model {
-    int objective = 0;  // 0 regression (squared error), 1 binary, -1 multiclass
+    int objective = 0;  // 0 regression (squared error), 1 binary, -1 multiclass, 7 lambdarank (raw scores)
     int num_class = 1;
     double learning_rate = 0.1;
     std::vector<double> base;  // num_class

@@ -20,6 +20,7 @@ size_t pb_lds_bytes(const DevState &s);
 size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized);
 size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
+size_t rank_lds_bytes(const DevState &s);
 hipError_t launch_hist(const DevState &s, hipStream_t st);
 hipError_t launch_part_hist(const DevState &s, hipStream_t st);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);

@@ -200,6 +200,171 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
     }
 }
 
+// --------------------------------------------------------------- lambdarank
+// LambdaRank gradients (ranking._fill_query_lambdas,
+// src/mojotrees/ranking.mojo:510-570, over every query, _fill_lambdas
+// :573-600), one block per query, in binary64 as the reference's ranker
+// keeps them. The query's documents are sorted by score in LDS (bitonic,
+// descending, ties by position: the reference's stable order). The pairs
+// (i, j), i below the truncation level, j > i, are then taken one rank i at
+// a time: the block evaluates row i's pairs in parallel, each rank j > i
+// adds its one contribution (it receives the pairs in i order, as in the
+// reference's loop), and two threads add row i's values in j order into the
+// running sum of |lambda| and into rank i's own gradient. Every sum thus has
+// the reference's order and the lambdas its bits. Query LDS: 49 bytes per
+// document of the largest query (rounded up to a power of two).
+__device__ __forceinline__ bool rank_before(double ka, int ia, double kb, int ib) {
+    return ka > kb || (ka == kb && ia < ib);
+}
+
+__global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
+    extern __shared__ unsigned char rank_lds[];
+    __shared__ double s_factor;
+    __shared__ double red_g[4], red_h[4];
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const HyperParams &hp = s.hp;
+    if (blockIdx.x == 0 && threadIdx.x == 0) s.cursor[0] = 0;  // root row count
+    const int P = s.rank_pad;
+    double *key = (double *)rank_lds;
+    double *G = key + P;
+    double *H = G + P;
+    double *PL = H + P;
+    double *PH = PL + P;
+    int32_t *idx = (int32_t *)(PH + P);
+    int32_t *lab = idx + P;
+    uint8_t *V = (uint8_t *)(lab + P);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const double sigma = hp.rank_sigma;
+    const bool norm = hp.rank_norm != 0;
+    double mg = 0.0, mh = 0.0;
+    for (int q = blockIdx.x; q < s.n_queries; q += gridDim.x) {
+        const int64_t a = s.qstart[q];
+        const int cnt = (int)(s.qstart[q + 1] - a);
+        int p2 = 1;
+        while (p2 < cnt) p2 <<= 1;
+        for (int i = tid; i < p2; i += nt) {
+            key[i] = i < cnt ? s.raw[a + i] : -INFINITY;
+            idx[i] = i;
+        }
+        __syncthreads();
+        for (int k = 2; k <= p2; k <<= 1)
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < p2; i += nt) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        const bool l_first = rank_before(key[l], idx[l], key[i], idx[i]);
+                        if ((i & k) == 0 ? l_first : !l_first) {
+                            const double tk = key[i];
+                            key[i] = key[l];
+                            key[l] = tk;
+                            const int ti = idx[i];
+                            idx[i] = idx[l];
+                            idx[l] = ti;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        for (int k = tid; k < cnt; k += nt) {
+            lab[k] = (int)s.labels[a + idx[k]];
+            G[k] = 0.0;
+            H[k] = 0.0;
+        }
+        __syncthreads();
+        const double best = key[0], worst = key[cnt - 1];
+        const double inv = s.inv_max_dcg[q];
+        const int top = cnt - 1 < hp.rank_trunc ? cnt - 1 : hp.rank_trunc;
+        double sum = 0.0;  // thread 0's running sum of |lambda| (ranking.mojo:565)
+        for (int i = 0; i < top; ++i) {
+            const int li = lab[i];
+            const double si = key[i];
+            for (int j = i + 1 + tid; j < cnt; j += nt) {
+                const int lj = lab[j];
+                double pl = 0.0, ph = 0.0;
+                uint8_t v = 0;
+                if (li != lj) {
+                    const bool ih = li > lj;  // rank i holds the more relevant document
+                    const int hr = ih ? i : j, lr = ih ? j : i;
+                    const double delta = ih ? si - key[j] : key[j] - si;
+                    const double gap = label_gain(ih ? li : lj) - label_gain(ih ? lj : li);
+                    const double paired = fabs(s.rank_disc[hr] - s.rank_disc[lr]);
+                    double dn = gap * paired * inv;
+                    if (norm && best != worst) dn /= 0.01 + fabs(delta);
+                    double p = pair_sigmoid(delta, sigma);
+                    double phh = p * (1.0 - p);
+                    p *= -sigma * dn;
+                    phh *= sigma * sigma * dn;
+                    pl = p;
+                    ph = phh;
+                    v = ih ? 3 : 1;
+                    G[j] = ih ? G[j] - p : G[j] + p;
+                    H[j] = H[j] + phh;
+                }
+                PL[j] = pl;
+                PH[j] = ph;
+                V[j] = v;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                for (int j = i + 1; j < cnt; ++j)
+                    if (V[j]) sum -= 2.0 * PL[j];
+            } else if (tid == 64) {
+                double g = G[i], h = H[i];
+                for (int j = i + 1; j < cnt; ++j) {
+                    const uint8_t v = V[j];
+                    if (!v) continue;
+                    g = (v & 2) ? g + PL[j] : g - PL[j];
+                    h = h + PH[j];
+                }
+                G[i] = g;
+                H[i] = h;
+            }
+            __syncthreads();
+        }
+        // the query's normalizer log2(1 + S) / S (ranking.mojo:567-570); 0
+        // marks "not applied"
+        if (tid == 0) s_factor = (norm && sum > 0.0) ? ref_log2(1.0 + sum) / sum : 0.0;
+        __syncthreads();
+        const double factor = s_factor;
+        for (int k = tid; k < cnt; k += nt) {
+            double g = G[k], h = H[k];
+            if (factor != 0.0) {
+                g *= factor;
+                h *= factor;
+            }
+            const int64_t r = a + idx[k];
+            s.grad64[r] = g;
+            s.hess64[r] = h;
+            if (isfinite(g) && isfinite(h)) {
+                mg = fmax(mg, fabs(g));
+                mh = fmax(mh, fabs(h));
+            }
+        }
+        __syncthreads();  // the LDS is the next query's
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        mg = fmax(mg, __shfl_xor(mg, d, 64));
+        mh = fmax(mh, __shfl_xor(mh, d, 64));
+    }
+    const int w = tid >> 6;
+    if (lane_id() == 0) {
+        red_g[w] = mg;
+        red_h[w] = mh;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < (nt >> 6); ++i) {
+            mg = fmax(mg, red_g[i]);
+            mh = fmax(mh, red_h[i]);
+        }
+        // non-negative doubles order like their bit patterns
+        atomicMax(&s.stats64[rd.parity * 2 + 0], (unsigned long long)__double_as_longlong(mg));
+        atomicMax(&s.stats64[rd.parity * 2 + 1], (unsigned long long)__double_as_longlong(mh));
+    }
+}
+
 // ----------------------------------------------------------------- softmax
 // boosting._softmax_rows (src/mojotrees/boosting.mojo:3529-3573): per row,
 // shift by the maximum, exponentiate with the reference's exp, sum in class
@@ -235,8 +400,10 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const Round rd = *s.round;
     if (rd.stopped) return;
     const HyperParams &hp = s.hp;
-    double max_g = (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
-    double max_h = (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
+    double max_g = hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 0])
+                             : (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
+    double max_h = hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 1])
+                             : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
     if (max_g < 1e-12) max_g = 1e-12;
     if (max_h < 1e-12) max_h = 1e-12;
     const int32_t gmax = hp.quant_bins / 2;
@@ -254,6 +421,10 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
         s.round->hess_units = hu;
         s.stats[(1 - rd.parity) * 2 + 0] = 0u;
         s.stats[(1 - rd.parity) * 2 + 1] = 0u;
+        if (hp.grad64) {
+            s.stats64[(1 - rd.parity) * 2 + 0] = 0ULL;
+            s.stats64[(1 - rd.parity) * 2 + 1] = 0ULL;
+        }
     }
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int rec = s.rec_bytes;
@@ -261,8 +432,10 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
         const int64_t r = r0 + threadIdx.x;
         const bool valid = r < s.n;
         if (valid && hp.quantized) {
-            int32_t qg = quantize_scalar((double)s.grad[r], gu, gmax, stoch, gs + (uint64_t)r);
-            int32_t qh = quantize_scalar((double)s.hess[r], hu, hmax, stoch, hs + (uint64_t)r);
+            const double gv = hp.grad64 ? s.grad64[r] : (double)s.grad[r];
+            const double hv = hp.grad64 ? s.hess64[r] : (double)s.hess[r];
+            int32_t qg = quantize_scalar(gv, gu, gmax, stoch, gs + (uint64_t)r);
+            int32_t qh = quantize_scalar(hv, hu, hmax, stoch, hs + (uint64_t)r);
             uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
             for (int t = 0; t < s.n_tiles; ++t)
                 *(uint16_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 2) = v;
@@ -792,7 +965,8 @@ struct FAcc {
         double *g = (double *)lds;
         double *h = g + (size_t)F * ls;
         uint32_t *c = (uint32_t *)(h + (size_t)F * ls);
-        double gv = (double)s.grad[row], hv = (double)s.hess[row];
+        double gv = s.hp.grad64 ? s.grad64[row] : (double)s.grad[row];
+        double hv = s.hp.grad64 ? s.hess64[row] : (double)s.hess[row];
         if (goss_mult != 1.0 && s.goss_other != nullptr && s.goss_other[row]) {
             gv *= goss_mult;
             hv *= goss_mult;
@@ -2300,8 +2474,14 @@ __global__ void k_exp_sigmoid(const double *x, double *e, double *sg, int64_t n)
 }
 
 // ------------------------------------------------------------------ launch
+size_t rank_lds_bytes(const DevState &s) { return (size_t)s.rank_pad * 49; }
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st) {
-    hipLaunchKernelGGL(k_objective, dim3(grid), dim3(256), 0, st, s);
+    if (s.hp.objective == kObjLambdarank) {
+        const int g = s.n_queries < 4 * grid ? s.n_queries : 4 * grid;
+        hipLaunchKernelGGL(k_lambdarank, dim3(g > 0 ? g : 1), dim3(256), rank_lds_bytes(s), st, s);
+    } else {
+        hipLaunchKernelGGL(k_objective, dim3(grid), dim3(256), 0, st, s);
+    }
     return hipGetLastError();
 }
 hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st) {
@@ -2370,6 +2550,7 @@ size_t plan_lds_bytes(const DevState &s) {
 
 hipError_t prepare_kernels(const DevState &s) {
     const size_t h = hist_lds_bytes(s), pb = pb_lds_bytes(s);
+    if (s.hp.objective == kObjLambdarank) MB_SET_LDS(k_lambdarank, rank_lds_bytes(s));
     if (s.hp.quantized) {
         MB_SET_LDS((k_hist<1, QAcc>), h);
         MB_SET_LDS((k_hist<2, QAcc>), h);

@@ -92,6 +92,43 @@ MB_HD double ref_log(double xv) {
     return fma((double)e, 0.69314718055994530942, y);
 }
 
+// The reference's log2 (ranking.mojo:240-244, :598): the same reduction and
+// polynomial as ref_log, taken in base 2 as y * log2(e) + e; exact at powers
+// of two.
+MB_HD double ref_log2(double xv) {
+    const double c[9] = {3.3333331174e-1, -2.4999993993e-1, 2.0000714765e-1,
+                         -1.6668057665e-1, 1.4249322787e-1, -1.2420140846e-1,
+                         1.1676998740e-1, -1.1514610310e-1, 7.0376836292e-2};
+    int e = 0;
+    double x1 = frexp(xv, &e);
+    if (x1 < 0.70710678118654752440) {
+        x1 = x1 * 2.0 - 1.0;
+        e -= 1;
+    } else {
+        x1 = x1 - 1.0;
+    }
+    double x2 = x1 * x1;
+    double y = c[8];
+    for (int i = 7; i >= 0; --i) y = fma(y, x1, c[i]);
+    y = x1 * x2 * y;
+    y = fma(-0.5, x2, y);
+    y = x1 + y;
+    return fma(y, 1.44269504088896340736, (double)e);
+}
+
+// LambdaRank pieces (ranking.mojo:235-237, :500-507): the label gain
+// 2^l - 1 and the pairwise logistic 1 / (1 + exp(sigma * delta)).
+MB_HD double label_gain(int l) { return (double)((1LL << l) - 1); }
+MB_HD double pair_sigmoid(double delta, double sigma) {
+    const double z = sigma * delta;
+    if (z >= 0.0) {
+        const double e = ref_exp(-z);
+        return e / (1.0 + e);
+    }
+    const double e = ref_exp(z);
+    return 1.0 / (1.0 + e);
+}
+
 // Logistic link in branch-on-sign form (boosting.mojo:261-266).
 MB_HD double sigmoid(double x) {
     if (x >= 0.0) {

@@ -15,6 +15,8 @@ namespace mb {
 constexpr int kObjL2 = 0;
 constexpr int kObjBinary = 1;
 constexpr int kObjMulticlass = 2;
+constexpr int kObjLambdarank = 3;
+constexpr int kMaxQueryRows = 2048;  // the largest query the LDS sort takes
 
 // Leaf-wise growth, batched. The reference grows a tree best-first: split the
 // frontier leaf of largest gain, score both children, repeat. A leaf's best
@@ -149,6 +151,11 @@ struct HyperParams {
     int32_t goss_seed;
     int32_t goss_exact;     // 1: always the full sequential count (no predicted band)
     double goss_band;       // band half-width in standard deviations of the count
+    int32_t grad64;         // 1: derivatives kept in binary64 (lambdarank), else narrowed to fp32
+    int32_t rank_trunc;     // lambdarank_truncation_level
+    int32_t rank_norm;      // lambdarank_norm
+    int32_t pad_rank_;
+    double rank_sigma;      // lambdarank sigmoid
     double top_rate, other_rate;
     int32_t bagging_freq;
     int32_t bagging_seed;
@@ -181,6 +188,14 @@ struct DevState {
     double *raw;           // n x num_class
     double *prob;          // n x num_class softmax of raw at the start of a round (multiclass)
     float *grad, *hess;    // n
+    double *grad64, *hess64;        // n, when hp.grad64
+    unsigned long long *stats64;    // [2 parities][2]: max |g|, |h| as double bits, when hp.grad64
+    // lambdarank: query q owns rows [qstart[q], qstart[q + 1])
+    const int64_t *qstart;
+    const double *inv_max_dcg;      // per query: 1 / maxDCG at the truncation level (0: none)
+    const double *rank_disc;        // 1 / log2(rank + 2) for ranks below the largest query
+    int32_t n_queries;
+    int32_t rank_pad;               // largest query rounded up to a power of two
     uint32_t *stats;       // [2 parities][2]: max |g|, max |h| as float bits
     Round *round;
     // rows and histograms

@@ -57,6 +57,22 @@ class Dataset:
         except Exception:
             pass
 
+    def set_groups(self, counts):
+        """Query groups for objective lambdarank: rows per query, in row order."""
+        c = np.ascontiguousarray(counts, np.int32)
+        err = C.create_string_buffer(512)
+        check(lib().mbh_dataset_set_groups(self.h, ptr(c), len(c), err, 512), err)
+
+    def lambdarank(self, raw, **params):
+        """LambdaRank gradients and hessians (binary64) of raw scores."""
+        p = _lib.mbh_params(**params)
+        raw = np.ascontiguousarray(raw, np.float64)
+        g = np.zeros(self.n_rows)
+        h = np.zeros(self.n_rows)
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_lambdarank(self.h, C.byref(p), ptr(raw), ptr(g), ptr(h), err, 1024), err)
+        return g, h
+
     def train(self, **params):
         p = _lib.mbh_params(**params)
         f = C.c_void_p()

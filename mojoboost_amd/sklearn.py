@@ -268,3 +268,60 @@ class MojoTreesClassifier(_Base):
         k = est.booster_.num_classes
         est.classes_ = np.arange(2 if k == 1 else k)
         return est
+
+
+class MojoTreesRanker(_Base):
+    """LambdaRank learning to rank (the reference's MojoTreesRanker,
+    python/mojotrees/sklearn.py:6951; objective lambdarank,
+    src/mojotrees/ranking.mojo). fit takes LightGBM's `group`: one row count
+    per query, in row order. Predictions are raw scores; only their order
+    within a query means anything."""
+    _objective = "lambdarank"
+
+    def __init__(self, n_estimators=100, learning_rate=0.1, num_leaves=31, max_depth=-1,
+                 min_child_samples=20, min_child_weight=1e-3, reg_alpha=0.0, reg_lambda=1.0,
+                 colsample_bytree=1.0, max_bin=255, random_state=None, device="gpu",
+                 use_quantized_grad=False, num_grad_quant_bins=4, stochastic_rounding=True,
+                 lambdarank_truncation_level=30, sigmoid=1.0, lambdarank_norm=True):
+        super().__init__(n_estimators=n_estimators, learning_rate=learning_rate,
+                         num_leaves=num_leaves, max_depth=max_depth,
+                         min_child_samples=min_child_samples, min_child_weight=min_child_weight,
+                         reg_alpha=reg_alpha, reg_lambda=reg_lambda,
+                         colsample_bytree=colsample_bytree, max_bin=max_bin,
+                         random_state=random_state, device=device,
+                         use_quantized_grad=use_quantized_grad,
+                         num_grad_quant_bins=num_grad_quant_bins,
+                         stochastic_rounding=stochastic_rounding)
+        self.lambdarank_truncation_level = lambdarank_truncation_level
+        self.sigmoid = sigmoid
+        self.lambdarank_norm = lambdarank_norm
+
+    def fit(self, X, y, group):
+        Xf, n, f = _colmajor(X)
+        y = np.ascontiguousarray(y, dtype=np.float64)
+        if y.shape[0] != n:
+            raise ValueError("y must have one entry per row of X")
+        g = np.ascontiguousarray(group, dtype=np.int32)
+        if g.ndim != 1 or g.size == 0:
+            raise ValueError("group must be a non-empty 1-d array of query sizes")
+        params = self._params(
+            f"lambdarank_truncation_level={self.lambdarank_truncation_level} "
+            f"sigmoid={self.sigmoid!r} "
+            f"lambdarank_norm={'true' if self.lambdarank_norm else 'false'}")
+        h = C.c_void_p()
+        e = _Error()
+        e.check(lib().mbh_train_ranker_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), ptr(g), g.size,
+                                             params.encode(), C.byref(h), e.h))
+        self.booster_ = _Booster(h)
+        return self
+
+    def predict(self, X, start_iteration=0, num_iteration=None, device=None):
+        self._check_fitted()
+        return self.booster_.predict(X, raw=True, start_iteration=start_iteration,
+                                     num_iteration=num_iteration, device=device)
+
+    @classmethod
+    def load(cls, path):
+        est = cls()
+        est.booster_ = _Booster.load(path)
+        return est

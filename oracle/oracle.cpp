@@ -112,6 +112,33 @@ double ref_log(double xv) {
     return std::fma((double)e, 0.69314718055994530942, y);
 }
 
+// Mojo stdlib `log2`, called for the LambdaRank position discounts and the
+// per-query normalizer (src/mojotrees/ranking.mojo:240-244, :598). Restated
+// as the same Cephes reduction and polynomial as ref_log with the result
+// taken in base 2, y * log2(e) + e. The reference's own tests pin log2 only
+// to 1e-8 (tests/test_ranking.mojo:5-8, :47-48), so its last bits are
+// parity unpinned; exact at powers of two.
+double ref_log2(double xv) {
+    static const double C[9] = {3.3333331174e-1, -2.4999993993e-1, 2.0000714765e-1,
+                                -1.6668057665e-1, 1.4249322787e-1, -1.2420140846e-1,
+                                1.1676998740e-1, -1.1514610310e-1, 7.0376836292e-2};
+    int e = 0;
+    double x1 = std::frexp(xv, &e);
+    if (x1 < 0.70710678118654752440) {
+        x1 = x1 * 2.0 - 1.0;
+        e -= 1;
+    } else {
+        x1 = x1 - 1.0;
+    }
+    double x2 = x1 * x1;
+    double y = C[8];
+    for (int i = 7; i >= 0; --i) y = std::fma(y, x1, C[i]);
+    y = x1 * x2 * y;
+    y = std::fma(-0.5, x2, y);
+    y = x1 + y;
+    return std::fma(y, 1.44269504088896340736, (double)e);
+}
+
 // src/mojotrees/boosting.mojo:261-266
 inline double sigmoid(double x) {
     if (x >= 0.0) {
@@ -999,6 +1026,128 @@ bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
     return true;
 }
 
+// ---------------------------------------------------------------- ranking
+// LambdaRank, LightGBM's LambdarankNDCG (src/mojotrees/ranking.mojo).
+struct RankSpec {
+    std::vector<int64_t> starts;  // n_queries + 1
+    int truncation = 30;
+    double sigmoid = 1.0;
+    bool norm = true;
+};
+
+// label_gain (ranking.mojo:235-237)
+inline double label_gain(int l) { return (double)((1LL << l) - 1); }
+
+// _discounts (ranking.mojo:240-245)
+std::vector<double> rank_discounts(int64_t n) {
+    std::vector<double> d((size_t)n);
+    for (int64_t i = 0; i < n; ++i) d[i] = 1.0 / ref_log2((double)i + 2.0);
+    return d;
+}
+
+// _argsort_desc_range (ranking.mojo:248-289): stable descending, ties in
+// input order.
+std::vector<int64_t> argsort_desc(const double *v, int64_t cnt) {
+    std::vector<int64_t> idx((size_t)cnt);
+    for (int64_t i = 0; i < cnt; ++i) idx[i] = i;
+    std::stable_sort(idx.begin(), idx.end(), [&](int64_t a, int64_t b) { return v[a] > v[b]; });
+    return idx;
+}
+
+// max_dcg (ranking.mojo:306-323) over the query's labels, cutoff k
+double max_dcg(const int *labels, int64_t cnt, int k) {
+    std::vector<int> sorted(labels, labels + cnt);
+    std::sort(sorted.begin(), sorted.end(), [](int a, int b) { return a > b; });
+    const int64_t m = k < cnt ? k : cnt;
+    std::vector<double> disc = rank_discounts(m);
+    double total = 0.0;
+    for (int64_t j = 0; j < m; ++j) total += label_gain(sorted[j]) * disc[j];
+    return total;
+}
+
+// _pair_sigmoid (ranking.mojo:500-507)
+inline double pair_sigmoid(double delta, double sigma) {
+    const double z = sigma * delta;
+    if (z >= 0.0) {
+        const double e = ref_exp(-z);
+        return e / (1.0 + e);
+    }
+    const double e = ref_exp(z);
+    return 1.0 / (1.0 + e);
+}
+
+// _fill_query_lambdas (ranking.mojo:510-570)
+void query_lambdas(const double *scores, const int *labels, int64_t cnt, double inv_max_dcg,
+                   const std::vector<double> &disc, const RankSpec &rs, double *grad, double *hess) {
+    for (int64_t i = 0; i < cnt; ++i) grad[i] = hess[i] = 0.0;
+    if (cnt < 2) return;
+    std::vector<int64_t> order = argsort_desc(scores, cnt);
+    const double best = scores[order[0]], worst = scores[order[cnt - 1]];
+    double sum_lambdas = 0.0;
+    int64_t top = cnt - 1;
+    if (rs.truncation < top) top = rs.truncation;
+    for (int64_t i = 0; i < top; ++i)
+        for (int64_t j = i + 1; j < cnt; ++j) {
+            if (labels[order[i]] == labels[order[j]]) continue;
+            int64_t hr, lr;
+            if (labels[order[i]] > labels[order[j]]) {
+                hr = i;
+                lr = j;
+            } else {
+                hr = j;
+                lr = i;
+            }
+            const int64_t high = order[hr], low = order[lr];
+            const double delta_score = scores[high] - scores[low];
+            const double dcg_gap = label_gain(labels[high]) - label_gain(labels[low]);
+            const double paired = std::fabs(disc[hr] - disc[lr]);
+            double delta_ndcg = dcg_gap * paired * inv_max_dcg;
+            if (rs.norm && best != worst) delta_ndcg /= 0.01 + std::fabs(delta_score);
+            double p_lambda = pair_sigmoid(delta_score, rs.sigmoid);
+            double p_hess = p_lambda * (1.0 - p_lambda);
+            p_lambda *= -rs.sigmoid * delta_ndcg;
+            p_hess *= rs.sigmoid * rs.sigmoid * delta_ndcg;
+            grad[low] -= p_lambda;
+            hess[low] += p_hess;
+            grad[high] += p_lambda;
+            hess[high] += p_hess;
+            sum_lambdas -= 2.0 * p_lambda;
+        }
+    if (rs.norm && sum_lambdas > 0.0) {
+        const double factor = ref_log2(1.0 + sum_lambdas) / sum_lambdas;
+        for (int64_t i = 0; i < cnt; ++i) {
+            grad[i] *= factor;
+            hess[i] *= factor;
+        }
+    }
+}
+
+// lambdarank_gradients / _fill_lambdas (ranking.mojo:573-654), unweighted:
+// every query's lambdas, in binary64 (the reference's ranker does not narrow).
+void fill_lambdas(const double *raw, const std::vector<int> &labels, const RankSpec &rs,
+                  const std::vector<double> &inv_max_dcg, const std::vector<double> &disc,
+                  double *grad, double *hess) {
+    const int64_t nq = (int64_t)rs.starts.size() - 1;
+    for (int64_t q = 0; q < nq; ++q) {
+        const int64_t a = rs.starts[q], c = rs.starts[q + 1] - a;
+        query_lambdas(raw + a, labels.data() + a, c, inv_max_dcg[q], disc, rs, grad + a, hess + a);
+    }
+}
+
+RankSpec rank_spec(const orc_params &p, int64_t n) {
+    RankSpec rs;
+    if (!p.query_starts || p.n_queries < 1) throw std::runtime_error("lambdarank needs query boundaries");
+    rs.starts.assign(p.query_starts, p.query_starts + p.n_queries + 1);
+    if (rs.starts[0] != 0 || rs.starts.back() != n) throw std::runtime_error("query boundaries must span the rows");
+    for (int64_t q = 0; q < p.n_queries; ++q)
+        if (rs.starts[q + 1] <= rs.starts[q]) throw std::runtime_error("query boundaries must increase");
+    rs.truncation = p.lambdarank_truncation_level;
+    rs.sigmoid = p.lambdarank_sigmoid;
+    rs.norm = p.lambdarank_norm != 0;
+    if (rs.truncation < 1 || !(rs.sigmoid > 0.0)) throw std::runtime_error("bad lambdarank parameters");
+    return rs;
+}
+
 }  // namespace
 
 // ================================================================ model
@@ -1350,6 +1499,40 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
 // One GOSS selection (goss_importance + goss_select + apply_goss_scaling,
 // goss.mojo:294-373) on caller arrays, warmup not applied. rows_out and
 // scale_out need n entries; grad/hess are scaled in place like the trainer's.
+int32_t orc_lambdarank(const double *scores, const double *labels, const int64_t *starts,
+                       int64_t n_queries, int32_t truncation, double sigma, int32_t norm,
+                       double *grad, double *hess) {
+    try {
+        orc_params p{};
+        p.query_starts = starts;
+        p.n_queries = n_queries;
+        p.lambdarank_truncation_level = truncation;
+        p.lambdarank_sigmoid = sigma;
+        p.lambdarank_norm = norm;
+        const int64_t n = starts[n_queries];
+        RankSpec rs = rank_spec(p, n);
+        std::vector<int> lab(n);
+        for (int64_t r = 0; r < n; ++r) {
+            if (!(labels[r] >= 0.0 && labels[r] <= 30.0)) return -1;
+            lab[r] = (int)labels[r];
+        }
+        std::vector<double> inv;
+        int64_t max_size = 0;
+        for (int64_t q = 0; q < n_queries; ++q) {
+            const int64_t a = starts[q], c = starts[q + 1] - a;
+            max_size = std::max(max_size, c);
+            const double md = max_dcg(lab.data() + a, c, truncation);
+            inv.push_back(md > 0.0 ? 1.0 / md : 0.0);
+        }
+        fill_lambdas(scores, lab, rs, inv, rank_discounts(max_size), grad, hess);
+        return 0;
+    } catch (const std::exception &) {
+        return -1;
+    }
+}
+
+double orc_log2(double x) { return ref_log2(x); }
+
 int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
                         double other_rate, int32_t seed, int64_t round_index,
                         int32_t *rows_out, double *scale_out, int64_t *n_out) {
@@ -1425,7 +1608,32 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
         // boosting.round_has_constant_hessian: L2, unweighted, no GOSS.
         P.const_hessian = (P.p.objective == ORC_OBJ_L2) && !P.p.goss;
         std::vector<double> raw((size_t)n * K);
-        if (K == 1) {
+        const bool rank = P.p.objective == ORC_OBJ_LAMBDARANK;
+        RankSpec rs;
+        std::vector<int> rank_labels;
+        std::vector<double> inv_max_dcg, rank_disc;
+        if (rank) {
+            // train_ranker (ranking.mojo:713-771): base score 0, labels in [0, 30]
+            rs = rank_spec(P.p, n);
+            rank_labels.resize(n);
+            for (int64_t r = 0; r < n; ++r) {
+                if (!(labels[r] >= 0.0 && labels[r] <= 30.0) || labels[r] != std::floor(labels[r]))
+                    throw std::runtime_error("relevance labels must be integers in [0, 30]");
+                rank_labels[r] = (int)labels[r];
+            }
+            int64_t max_size = 0;
+            for (int64_t q = 0; q + 1 < (int64_t)rs.starts.size(); ++q) {
+                const int64_t a = rs.starts[q], c = rs.starts[q + 1] - a;
+                max_size = std::max(max_size, c);
+                const double md = max_dcg(rank_labels.data() + a, c, rs.truncation);
+                inv_max_dcg.push_back(md > 0.0 ? 1.0 / md : 0.0);
+            }
+            rank_disc = rank_discounts(max_size);
+        }
+        if (K == 1 && rank) {
+            m->base.push_back(0.0);
+            std::fill(raw.begin(), raw.end(), 0.0);
+        } else if (K == 1) {
             // boosting._base_score (src/mojotrees/boosting.mojo:521-568)
             double mean = 0.0, tw = 0.0;
             for (int64_t r = 0; r < n; ++r) {
@@ -1462,7 +1670,10 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
             auto t0 = std::chrono::steady_clock::now();
             refresh_bag(bag, P.p, n, it);
             if (K == 1) {
-                fill_grad_hess(P.p.objective, raw.data(), labels, n, 1, 0, grad.data(), hess.data());
+                if (rank)
+                    fill_lambdas(raw.data(), rank_labels, rs, inv_max_dcg, rank_disc, grad.data(), hess.data());
+                else
+                    fill_grad_hess(P.p.objective, raw.data(), labels, n, 1, 0, grad.data(), hess.data());
                 goss_round(bag, grad, hess, P.p, it);
                 Tree t = grow_one(d, P, grad, hess, bag, it, 0, it, leaves, qg, qh, pool);
                 if (t.n_leaves == 1 && std::fabs(t.value[0]) < 1e-12) {

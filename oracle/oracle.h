@@ -22,6 +22,7 @@ extern "C" {
 #define ORC_OBJ_L2 0
 #define ORC_OBJ_BINARY 1
 #define ORC_OBJ_MULTICLASS 2
+#define ORC_OBJ_LAMBDARANK 3
 
 typedef struct {
     int32_t objective;          /* ORC_OBJ_* */
@@ -53,6 +54,12 @@ typedef struct {
     int32_t totals_tree_reduce; /* 1: SIMD totals reduced pairwise (Mojo reduce) */
     int32_t use_init_base;      /* 1: start every row at init_base (single output) */
     double init_base;
+    /* lambdarank: query q owns rows [query_starts[q], query_starts[q + 1]) */
+    const int64_t *query_starts;
+    int64_t n_queries;
+    int32_t lambdarank_truncation_level;
+    int32_t lambdarank_norm;
+    double lambdarank_sigmoid;
 } orc_params;
 
 /* A trained model in flat arrays. Trees are laid out one after another;
@@ -116,6 +123,14 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n_rows,
                        const int32_t *rows, int64_t n_sel,
                        int32_t row_blocks, double *out_gh,
                        int64_t *out_count);
+
+/* ---------------------------------------------------------------- ranking */
+/* LambdaRank gradients and hessians of every query (binary64), and the log2
+ * the discounts use. */
+int32_t orc_lambdarank(const double *scores, const double *labels, const int64_t *starts,
+                       int64_t n_queries, int32_t truncation, double sigma, int32_t norm,
+                       double *grad, double *hess);
+double orc_log2(double x);
 
 /* ------------------------------------------------------------------ GOSS */
 /* One GOSS selection of round `round_index` (no warmup): ascending kept rows,

@@ -12,7 +12,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent.parent
 LIB_PATH = ROOT / "oracle" / "_build" / "liboracle.so"
 
-OBJ_L2, OBJ_BINARY, OBJ_MULTICLASS = 0, 1, 2
+OBJ_L2, OBJ_BINARY, OBJ_MULTICLASS, OBJ_LAMBDARANK = 0, 1, 2, 3
 
 
 class Params(C.Structure):
@@ -46,6 +46,11 @@ class Params(C.Structure):
         ("totals_tree_reduce", C.c_int32),
         ("use_init_base", C.c_int32),
         ("init_base", C.c_double),
+        ("query_starts", C.c_void_p),
+        ("n_queries", C.c_int64),
+        ("lambdarank_truncation_level", C.c_int32),
+        ("lambdarank_norm", C.c_int32),
+        ("lambdarank_sigmoid", C.c_double),
     ]
 
 
@@ -59,6 +64,8 @@ def default_params(**kw) -> Params:
         stochastic_rounding=1, quant_seed=11, goss=0, top_rate=0.2,
         other_rate=0.1, goss_seed=3, n_threads=0, fused_score_update=1,
         fused_predict=1, totals_tree_reduce=1, use_init_base=0, init_base=0.0,
+        query_starts=None, n_queries=0, lambdarank_truncation_level=30, lambdarank_norm=1,
+        lambdarank_sigmoid=1.0,
     )
     for k, v in kw.items():
         setattr(p, k, v)
@@ -132,6 +139,11 @@ def lib():
                                           C.c_void_p, C.c_double, C.c_double, C.c_double,
                                           C.c_double, C.c_double, C.c_int32, C.c_void_p,
                                           C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_lambdarank.restype = C.c_int32
+        L.orc_lambdarank.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                     C.c_double, C.c_int32, C.c_void_p, C.c_void_p]
+        L.orc_log2.restype = C.c_double
+        L.orc_log2.argtypes = [C.c_double]
         L.orc_goss_select.restype = C.c_int32
         L.orc_goss_select.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_double, C.c_double,
                                       C.c_int32, C.c_int64, C.c_void_p, C.c_void_p,
@@ -287,3 +299,32 @@ def goss_select(grad, hess, top_rate=0.2, other_rate=0.1, seed=3, round_index=0)
                                _ptr(rows), _ptr(scale), C.byref(cnt))
     assert rc == 0, rc
     return rows[:cnt.value], scale[:cnt.value], g, h
+
+
+def query_starts(counts):
+    """Query boundaries (int64, n_queries + 1) from per-query row counts."""
+    return np.concatenate([[0], np.cumsum(np.asarray(counts, np.int64))]).astype(np.int64)
+
+
+def lambdarank(scores, labels, counts, truncation=30, sigma=1.0, norm=True):
+    """LambdaRank gradients and hessians of every query, binary64."""
+    sc = np.ascontiguousarray(scores, np.float64)
+    lab = np.ascontiguousarray(labels, np.float64)
+    st = query_starts(counts)
+    g = np.zeros(len(sc))
+    h = np.zeros(len(sc))
+    rc = lib().orc_lambdarank(_ptr(sc), _ptr(lab), _ptr(st), len(st) - 1, truncation, sigma,
+                              1 if norm else 0, _ptr(g), _ptr(h))
+    if rc != 0:
+        raise ValueError("invalid lambdarank input")
+    return g, h
+
+
+def rank_params(counts, **kw):
+    """default_params for objective lambdarank over the given query counts;
+    the returned starts array must outlive the params."""
+    st = query_starts(counts)
+    p = default_params(objective=OBJ_LAMBDARANK, **kw)
+    p.query_starts = st.ctypes.data
+    p.n_queries = len(st) - 1
+    return p, st

@@ -99,6 +99,9 @@ def test_train_argument_errors():
     ("boosting=goss top_rate=0 other_rate=0", _lib.ERROR_INVALID_ARGUMENT),
     ("boosting=goss bagging_seed=-1", _lib.ERROR_INVALID_ARGUMENT),
     ("boosting=goss top_rate=0.9 other_rate=0.2", _lib.ERROR_INVALID_ARGUMENT),
+    # lambdarank needs query groups, which only mbh_train_ranker_dense takes
+    ("objective=lambdarank", _lib.ERROR_INVALID_ARGUMENT),
+    ("sigmoid=abc", _lib.ERROR_INVALID_ARGUMENT),
     # _check_goss (boosting.mojo:346-355): GOSS and row bagging both own the row list
     ("boosting=goss bagging_fraction=0.5 bagging_freq=1", _lib.ERROR_INVALID_ARGUMENT),
 ])
@@ -144,7 +147,8 @@ def test_parameter_keys():
     L.mojotrees_string_free(out)
     L.mojotrees_error_free(e)
     for k in ("objective", "num_leaves", "learning_rate", "use_quantized_grad",
-              "num_grad_quant_bins", "device"):
+              "num_grad_quant_bins", "device", "lambdarank_truncation_level", "sigmoid",
+              "lambdarank_norm"):
         assert k in keys
 
 

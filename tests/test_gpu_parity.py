@@ -538,3 +538,89 @@ def test_device_predict_wide_multiclass_through_c_abi(dev):
             pb = est.predict_proba(X, start_iteration=s0, num_iteration=num, device="gpu")
             assert np.array_equal(bits(pa), bits(pb)), (n, f, s0, num)
         assert np.array_equal(est.predict(X, device="auto"), est.predict(X))
+
+
+# --------------------------------------------------------------- lambdarank
+def ranking_data(n_queries, f=10, seed=41, max_q=200, grades=4):
+    """Queries of 1..max_q documents; the relevance grade follows a noisy
+    linear score of the features."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(1, max_q + 1, size=n_queries)
+    n = int(counts.sum())
+    x = rng.normal(size=(f, n))
+    s = x[0] - 0.5 * x[1] + 0.3 * x[2] * x[3] + 0.5 * rng.normal(size=n)
+    y = np.clip(np.floor((s + 2.0) * grades / 4.0), 0, grades).astype(np.float64)
+    return x, y, counts.astype(np.int32), n
+
+
+@pytest.mark.parametrize("trunc,norm", [(30, True), (5, True), (30, False), (1, True)])
+def test_lambdarank_gradients_bit_exact(dev, trunc, norm):
+    """The device lambdas (ranking._fill_query_lambdas in binary64): every
+    gradient and hessian bit equal to the oracle's, over queries of 1 to
+    2048 documents with tied scores and grades up to 30."""
+    rng = np.random.default_rng(43 + trunc)
+    counts = np.array([1, 2, 3, 7, 64, 65, 300, 2048, 1, 129, 5], np.int32)
+    n = int(counts.sum())
+    y = rng.integers(0, 5, size=n).astype(np.float64)
+    y[:40] = rng.integers(0, 31, size=40)
+    raw = np.round(rng.normal(size=n), 1)             # many ties
+    raw[100:140] = 0.0
+    bins = rng.integers(0, 8, size=(2, n), dtype=np.uint8)
+    ds = dev.Dataset(bins, n, 2, 8, y)
+    ds.set_groups(counts)
+    g, h = ds.lambdarank(raw, lambdarank_truncation_level=trunc, lambdarank_norm=int(norm))
+    wg, wh = O.lambdarank(raw, y, counts, truncation=trunc, sigma=1.0, norm=norm)
+    assert np.array_equal(bits(g), bits(wg))
+    assert np.array_equal(bits(h), bits(wh))
+
+
+@pytest.mark.parametrize("quantized", [1, 0])
+def test_training_lambdarank(dev, quantized):
+    """A LambdaRank ensemble on the device against the oracle's restatement
+    of train_ranker (ranking.mojo:690-771): quantized gradients bit-exact;
+    fp32-path histograms (fp64 sums of the binary64 lambdas) within 1e-5."""
+    x, y, counts, n = ranking_data(300)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, 10, max_bins=63)
+    kw = dict(num_iterations=10, num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.1)
+    ds = dev.Dataset(bins, n, 10, 64, y, missing_bin=mb)
+    ds.set_groups(counts)
+    fit = ds.train(objective=3, use_quantized_grad=quantized, **kw)
+    p, st = O.rank_params(counts, use_quantized_grad=quantized, **kw)
+    ref = O.train(bins, n, 10, 64, y, p, missing_bin=mb)
+    assert fit.base[0] == 0.0 and fit.n_trees == ref.n_trees
+    if quantized:
+        _compare_fit(fit, ref, n)
+    else:
+        assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+        assert _tree_agreement(fit, ref) >= ref.n_trees - 1
+
+
+def test_ranker_estimator_through_c_abi(dev, tmp_path):
+    """MojoTreesRanker(device="gpu").fit(X, y, group) -> mbh_train_ranker_dense:
+    the model ranks better than chance, predicts the same bits on the host
+    and the device, and survives save/load (objective 7)."""
+    from mojoboost_amd.sklearn import MojoTreesRanker
+
+    x, y, counts, n = ranking_data(200, seed=47)
+    X = np.ascontiguousarray(x.T)
+    est = MojoTreesRanker(n_estimators=20, num_leaves=15, learning_rate=0.2, max_bin=63,
+                          min_child_samples=5).fit(X, y, group=counts)
+    s_cpu = est.predict(X)
+    s_gpu = est.predict(X, device="gpu")
+    assert np.array_equal(bits(s_cpu), bits(s_gpu))
+    # within every query the score order agrees with the grade more often than not
+    agree, total, a = 0, 0, 0
+    for c in counts:
+        ss, yy = s_cpu[a:a + c], y[a:a + c]
+        i, j = np.triu_indices(c, 1)
+        m = yy[i] != yy[j]
+        agree += int(np.sum(np.sign(ss[i] - ss[j])[m] == np.sign(yy[i] - yy[j])[m]))
+        total += int(m.sum())
+        a += c
+    assert agree > 0.75 * total
+    path = tmp_path / "ranker.txt"
+    est.save(str(path))
+    assert "objective 7" in path.read_text()
+    back = MojoTreesRanker.load(str(path))
+    assert np.array_equal(bits(back.predict(X)), bits(s_cpu))
