@@ -911,40 +911,103 @@ __device__ __forceinline__ int64_t root_rows(const DevState &s) {
 // count per cell, summing the fp32 gradient values exactly as the
 // reference's Float64 histograms do (histogram.mojo:1002); only the order of
 // the additions differs.
+// Bytes of a row's record in a tile of tf features: the tile's bins, zero
+// pad, the g/h pair in the last two bytes, rounded up to a power of two.
+__host__ __device__ constexpr int record_bytes_for(int tf) {
+    int r = 16;
+    while (r < tf + 2) r *= 2;
+    return r;
+}
+
 struct QAcc {
-    static constexpr int kUnroll = 4;  // partition tile: 4 x 1024 rows
-    static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 8; }
-    __device__ static void zero(unsigned char *lds, int F, int ls) {
-        unsigned long long *a = (unsigned long long *)lds;
-        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) a[i] = 0ULL;
+    static constexpr int kUnroll = 3;  // partition tile: 3 x 1024 rows
+    // LDS cells are bin-major: cell (byte position p of the record, bin) at
+    // bin * FS + p, FS = max(32, record bytes). A 64-bit cell's banks then
+    // depend on p alone, whatever the bin, and add() has the lanes of a wave
+    // take different byte positions at each step, so a step's 64 atomics
+    // meet no bank conflict (measured: random bins cost twice the LDS cycles
+    // of this layout). Every byte of the record is
+    // added, unconditionally: the pad and g/h positions land in bin-0 cells
+    // that the store never reads.
+    static __host__ __device__ constexpr int row_cells_for(int rec) { return rec < 32 ? 32 : rec; }
+    static __host__ __device__ size_t lds_bytes(int tf, int ls) {
+        return (size_t)row_cells_for(record_bytes_for(tf)) * ls * 8;
     }
-    // one record (this lane's 16-byte slice: features sub*16 ..)
-    __device__ static void add(unsigned char *lds, const DevState &, const uint4 &w, int sub, int F, int ls,
-                               int64_t, uint32_t gh_word, double) {
+    template <int LPR>
+    __device__ static void zero(unsigned char *lds, int, int ls) {
+        constexpr int FS = row_cells_for(LPR * 16);
         unsigned long long *a = (unsigned long long *)lds;
+        for (int i = threadIdx.x; i < FS * ls; i += blockDim.x) a[i] = 0ULL;
+    }
+    // one record slice (this lane's 16 bytes: positions sub*16 ..). The slice
+    // is rotated right by rot bytes, so step k adds position
+    // sub*16 + (k + rot) mod 16, with rot = (lane mod 16) xor (bit 4 of
+    // lane): the 16 lanes of a quarter-wave take 16 different positions
+    // mod 16 (no conflict when the LDS serves a 64-bit op 16 lanes at a time
+    // over 32 banks), and the 32 lanes of a half-wave 32 different positions
+    // mod 32 (none when it serves 32 lanes over 64 banks), for LPR >= 2.
+    template <int LPR>
+    __device__ static void add(unsigned char *lds, const DevState &, const uint4 &w, int sub, int, int, int64_t,
+                               uint32_t gh_word, double) {
+        constexpr int FS = row_cells_for(LPR * 16);
+        constexpr int kRowShift = FS == 32 ? 8 : FS == 64 ? 9 : 10;  // log2(FS * 8 bytes)
+        static_assert(FS * 8 == (1 << kRowShift), "row of a power-of-two size");
         const int g = (int)(int8_t)(gh_word >> 16);
         const int h = (int)(int8_t)(gh_word >> 24);
         const unsigned long long packed =
             (unsigned long long)(((long long)g << 42) + ((long long)h << 20) + 1LL);
-        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t rot = ((uint32_t)lane_id() & 15u) ^ (((uint32_t)lane_id() >> 4) & 1u);
+        // the g/h bytes are added as bin 0 (any bin id must be below the LDS
+        // rows, n_bins); pad bytes are zero
+        uint32_t d0 = w.x, d1 = w.y, d2 = w.z, d3 = sub == LPR - 1 ? w.w & 0xFFFFu : w.w;
+        if (rot & 4u) {  // one dword
+            const uint32_t t = d0;
+            d0 = d1;
+            d1 = d2;
+            d2 = d3;
+            d3 = t;
+        }
+        if (rot & 8u) {  // two dwords
+            uint32_t t = d0;
+            d0 = d2;
+            d2 = t;
+            t = d1;
+            d1 = d3;
+            d3 = t;
+        }
+        const uint32_t sh = rot & 3u;
+        const uint32_t r[4] = {__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                               __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d0, d3, sh)};
+        const uint32_t pb = (uint32_t)sub * 128u;  // byte offset of position sub*16
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int f = sub * 16 + q * 4 + j;
-                if (f < F) atomicAdd(&a[f * ls + ((d[q] >> (8 * j)) & 255u)], packed);
-            }
+        for (int k = 0; k < 16; ++k) {
+            const uint32_t p8 = pb | ((((uint32_t)k + rot) & 15u) << 3);
+            const uint32_t bin = (r[k >> 2] >> (8 * (k & 3))) & 255u;
+            atomicAdd((unsigned long long *)(lds + ((bin << kRowShift) | p8)), packed);
+        }
     }
-    // every cell of the block's histogram as its partial: features
-    // [f0, f0 + Ft) of partial blk
+    // every cell of the block's histogram as its partial (feature-major:
+    // features [f0, f0 + Ft) of partial blk). A lane reads four bins of one
+    // feature (the lanes of a wave spread over 32 positions, two per bank
+    // pair) and writes them as 32 contiguous bytes.
+    template <int LPR>
     __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
+        constexpr int FS = row_cells_for(LPR * 16);
         const unsigned long long *a = (const unsigned long long *)lds;
-        const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
+        const int F = s.n_features, nb = s.n_bins, ps = s.part_stride;
         unsigned long long *out = s.part + ((size_t)blk * F + f0) * ps;
-        for (int c = threadIdx.x; c < Ft * ps; c += blockDim.x) {
-            const int f = c / ps;
-            const int b = c - f * ps;
-            out[c] = b < nb ? a[f * ls + b] : 0ULL;
+        const int nq = (ps + 3) >> 2;
+        for (int u = threadIdx.x; u < FS * nq; u += blockDim.x) {
+            const int q = u / FS;
+            const int f = u - q * FS;
+            if (f >= Ft) continue;
+            const int b = 4 * q;
+            unsigned long long v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = b + i < nb ? a[(b + i) * FS + f] : 0ULL;
+            ulonglong2 *o = (ulonglong2 *)(out + (size_t)f * ps + b);  // ps is even: 16-byte aligned
+            o[0] = make_ulonglong2(v[0], v[1]);
+            if (b + 2 < ps) o[1] = make_ulonglong2(v[2], v[3]);
         }
     }
 };
@@ -952,6 +1015,7 @@ struct QAcc {
 struct FAcc {
     static constexpr int kUnroll = 2;  // partition tile: 2 x 1024 rows (LDS budget)
     static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 20; }
+    template <int LPR>
     __device__ static void zero(unsigned char *lds, int F, int ls) {
         double *g = (double *)lds;
         uint32_t *c = (uint32_t *)(g + 2 * (size_t)F * ls);
@@ -960,6 +1024,7 @@ struct FAcc {
     }
     // goss_mult: the GOSS weight of rows the sampling kept (1 outside GOSS
     // rounds); goss.apply_goss_scaling multiplies their g and h in fp64
+    template <int LPR>
     __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
                                int64_t row, uint32_t, double goss_mult) {
         double *g = (double *)lds;
@@ -985,6 +1050,7 @@ struct FAcc {
                 }
             }
     }
+    template <int LPR>
     __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
         const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
         const double *g = (const double *)lds;
@@ -1028,7 +1094,7 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     const int ls = s.lds_stride;
     const int f0 = (int)blockIdx.y * s.tile_f;
     const int Ft = min(s.tile_f, s.n_features - f0);
-    Acc::zero(lds, Ft, ls);
+    Acc::template zero<LPR>(lds, Ft, ls);
     __syncthreads();
     const int lane = lane_id();
     const int sub = threadIdx.x % LPR;
@@ -1036,10 +1102,13 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     const int rpp = blockDim.x / LPR;
     const int src_lane = (lane / LPR) * LPR + (LPR - 1);
     const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
-    for (int64_t i0 = c0; i0 < c1; i0 += (int64_t)kHistUnroll * rpp) {
-        uint4 w[kHistUnroll];
-        int64_t row[kHistUnroll];
-        bool ok[kHistUnroll];
+    // Two register sets: the loads of the next kHistUnroll x rpp rows are in
+    // flight while the current ones are added into LDS.
+    const int64_t step = (int64_t)kHistUnroll * rpp;
+    uint4 wa[kHistUnroll], wb[kHistUnroll];
+    int64_t ra[kHistUnroll], rb[kHistUnroll];
+    bool oa[kHistUnroll], ob[kHistUnroll];
+    auto fetch = [&](int64_t i0, uint4 *w, int64_t *row, bool *ok) {
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const int64_t i = i0 + (int64_t)u * rpp + rr;
@@ -1051,14 +1120,29 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
             }
             w[u] = ok[u] ? rec[row[u] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
         }
+    };
+    auto accumulate = [&](const uint4 *w, const int64_t *row, const bool *ok) {
 #pragma unroll
         for (int u = 0; u < kHistUnroll; ++u) {
             const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (ok[u]) Acc::add(lds, s, w[u], sub, Ft, ls, row[u], gh, goss_mult);
+            if (ok[u]) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, row[u], gh, goss_mult);
         }
+    };
+    int64_t i0 = c0;
+    fetch(i0, wa, ra, oa);
+    for (;;) {
+        const int64_t i1 = i0 + step;
+        if (i1 < c1) fetch(i1, wb, rb, ob);
+        accumulate(wa, ra, oa);
+        if (i1 >= c1) break;
+        const int64_t i2 = i1 + step;
+        if (i2 < c1) fetch(i2, wa, ra, oa);
+        accumulate(wb, rb, ob);
+        if (i2 >= c1) break;
+        i0 = i2;
     }
     __syncthreads();
-    Acc::store(s, lds, blockIdx.x, f0, Ft);
+    Acc::template store<LPR>(s, lds, blockIdx.x, f0, Ft);
 }
 
 // ------------------------------------------------- partition + histogram
@@ -1118,7 +1202,7 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
     // whole accumulation (zeroed LDS, stored partial)
     for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
         const PbDesc d = s.pb_desc[blk];
-        Acc::zero(lds, Ft, ls);
+        Acc::template zero<LPR>(lds, Ft, ls);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
@@ -1204,13 +1288,13 @@ __global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
 #pragma unroll
                 for (int u = 0; u < kHistUnroll; ++u) {
                     const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                    if (ok[u]) Acc::add(lds, s, v[u], sub, Ft, ls, row[u], gh, goss_mult);
+                    if (ok[u]) Acc::template add<LPR>(lds, s, v[u], sub, Ft, ls, row[u], gh, goss_mult);
                 }
             }
             __syncthreads();
         }
         __syncthreads();
-        Acc::store(s, lds, blk, f0, Ft);
+        Acc::template store<LPR>(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
     }
 }
