@@ -133,9 +133,12 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *   [10] expansion launches that did work   [11] leaves expanded (including
  *        speculative expansions the best-first replay discarded)
  *   [12] rows accumulated by expansions     [13] parent rows partitioned
- *   [14] expansion launches enqueued        [15] ms of those launches
+ *   [14] expansion iterations enqueued
+ *   [15] ms of their partition and accumulation launches
  *   [16] their algorithmic bytes: [13] * 9 (row id in, bin, row id out)
- *        + [12] * (n_features + gh) */
+ *        + [12] * (n_features + gh)
+ *   [17] ms of the partition launches   [18] ms of the accumulation launches
+ *   [19] the accumulations' algorithmic bytes: [12] * (n_features + gh) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
 /* Query groups of a resident dataset, for objective lambdarank: counts[q]

@@ -124,7 +124,7 @@ struct mbh_dataset {
     }
 };
 
-constexpr int kNumStats = 17;
+constexpr int kNumStats = 20;
 
 struct mbh_fit {
     int num_class = 1;
@@ -155,12 +155,12 @@ struct PinnedFlags {
     }
 };
 
-// Static LDS of the partition+histogram kernel (tile counters and offsets).
+// LDS a histogram block leaves free beside its histogram (scheduling slack).
 constexpr size_t kPbStaticLds = 2048;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
 // trees reaches the tree's depth in iterations with 32).
 constexpr int kMaxBatch = 32;
-// Expansion iterations ([partition + histogram, scan, plan]) per group of
+// Expansion iterations ([partition, accumulation, scan, plan]) per group of
 // launches between done-flag reads: the first group of a tree is as long as
 // the previous tree needed (kFirstGroup for the first tree), later ones
 // kNextGroup.
@@ -284,10 +284,12 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // Histogram launch geometry and the partial buffer. The root build of m rows
 // runs ceil(m / chunk) blocks with chunk = clamp(ceil(m / grid), chunk_min,
 // chunk_limit); the grid is widened when needed so grid * chunk_limit covers
-// every row. An expansion launch gives each leaf of m rows ceil(m / chunk)
-// blocks with chunk = clamp(ceil(m / 256), chunk_min, chunk_limit); the
-// leaves of a batch are disjoint, so n / chunk_min + (batch size) blocks
-// always suffice.
+// every row. An expansion's accumulation gives each accumulated child of m
+// rows ceil(m / chunk) tasks (block partials) with chunk = clamp(ceil(batch
+// rows / n_cu), chunk_min, chunk_limit); the leaves of a batch are disjoint,
+// so n / chunk_min + (batch size) tasks always suffice. Its partition tasks
+// take at most kPartChunk parent rows each, n / kPartChunk + (batch size) of
+// them at most.
 constexpr int64_t kHistChunkMin = 4096;
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantized, Run &run) {
@@ -301,8 +303,10 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantize
     s.hist_chunk_limit = limit;
     s.kmax = kMaxBatch;
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
+    s.part_grid = (int32_t)((ds->n + mb::kPartChunk - 1) / mb::kPartChunk + s.kmax);
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
-    s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);
+    s.pb_launch = std::min<int32_t>(s.pb_grid, ds->n_cu);
+    s.part_launch = std::min<int32_t>(s.part_grid, 4 * ds->n_cu);
     // a root build uses at most ceil(n / chunk_min) chunks
     const int64_t parts = std::max<int64_t>(std::min<int64_t>(grid, (ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min),
                                             s.pb_grid);
@@ -314,7 +318,8 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantize
         s.fpart_h = dalloc<double>(cells, run.owned);
         s.fpart_c = dalloc<uint32_t>(cells, run.owned);
     }
-    s.pb_desc = dalloc<mb::PbDesc>(s.pb_grid, run.owned);
+    s.pb_desc = dalloc<mb::PbDesc>(s.part_grid, run.owned);
+    s.ac_desc = dalloc<mb::AcDesc>(s.pb_grid, run.owned);
 }
 
 double base_score_for(const mbh_dataset *ds, int objective) {
@@ -507,14 +512,15 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     if (mb::plan_lds_bytes(s) > 160 * 1024)
         throw Error{MOJOTREES_ERROR_UNSUPPORTED,
                     "num_leaves * n_features too large for the planner's LDS (160 KiB)"};
-    if (mb::pb_lds_bytes(s) + kPbStaticLds > 160 * 1024)
+    if (mb::hist_lds_bytes(s) + kPbStaticLds > 160 * 1024)
         throw Error{MOJOTREES_ERROR_TRAINING, "internal: the feature tile exceeds one workgroup's LDS"};
     HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
     HIPX(hipMemset(s.batch, 0, sizeof(mb::Batch)));
     HIPX(hipMemset(s.grow, 0, sizeof(mb::Grow)));
-    HIPX(hipMemset(s.pb_desc, 0, (size_t)s.pb_grid * sizeof(mb::PbDesc)));
+    HIPX(hipMemset(s.pb_desc, 0, (size_t)s.part_grid * sizeof(mb::PbDesc)));
+    HIPX(hipMemset(s.ac_desc, 0, (size_t)s.pb_grid * sizeof(mb::AcDesc)));
     HIPX(hipMemset(s.cursor, 0, (2 + 2 * (size_t)s.kmax) * sizeof(int64_t)));
     HIPX(hipMemset(s.error, 0, sizeof(int32_t)));
     HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));
@@ -672,22 +678,27 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         PinnedFlags flags;
         HIPX(hipHostMalloc((void **)&flags.p, 2 * sizeof(mb::Batch), hipHostMallocDefault));
         // events: [0..1] flag markers of the two in-flight groups; when
-        // timed, [2..4] the root build and per group slot kMaxGroup x 3
-        // (before the expansion, after it, after scan + plan)
-        const int n_ev = 2 + (timed ? 3 + 2 * kMaxGroup * 3 : 0);
+        // timed, [2..4] the root build and per group slot kMaxGroup x 4
+        // (before the partition, after it, after the accumulation, after
+        // scan + plan)
+        const int n_ev = 2 + (timed ? 3 + 2 * kMaxGroup * 4 : 0);
         events.resize(n_ev);
         for (int i = 0; i < n_ev; ++i)
             HIPX(hipEventCreateWithFlags(&events[i], i < 2 ? hipEventDisableTiming : hipEventDefault));
-        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kMaxGroup + c) * 3 + k]; };
+        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kMaxGroup + c) * 4 + k]; };
         double t_acc = 0.0, t_root = 0.0, t_root_scan = 0.0, t_pb = 0.0, t_scan = 0.0;
+        double t_part = 0.0, t_accum = 0.0;
         double pb_launches = 0.0;
         auto add_group = [&](int slot, int n) {
             for (int c = 0; c < n; ++c) {
-                float a = 0.f, b = 0.f;
+                float a = 0.f, b = 0.f, d = 0.f;
                 HIPX(hipEventElapsedTime(&a, ev_group(slot, c, 0), ev_group(slot, c, 1)));
                 HIPX(hipEventElapsedTime(&b, ev_group(slot, c, 1), ev_group(slot, c, 2)));
-                t_pb += a;
-                t_scan += b;
+                HIPX(hipEventElapsedTime(&d, ev_group(slot, c, 2), ev_group(slot, c, 3)));
+                t_part += a;
+                t_accum += b;
+                t_pb += a + b;
+                t_scan += d;
             }
         };
         // expansion launches the previous tree needed: the first group of a
@@ -716,11 +727,13 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 group_size[slot] = n;
                 for (int c = 0; c < n; ++c) {
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 0), st));
-                    HIPX(mb::launch_part_hist(s, st));
+                    HIPX(mb::launch_partition(s, st));
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 1), st));
+                    HIPX(mb::launch_accum(s, st));
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 2), st));
                     HIPX(mb::launch_scan(s, 0, st));
                     HIPX(mb::launch_plan(s, 0, st));
-                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 2), st));
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 3), st));
                 }
                 pb_launches += n;
                 iters += n;
@@ -854,6 +867,9 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         o[14] = pb_launches;
         o[15] = t_pb;
         o[16] = rows_parted * 9.0 + rows_built * rb;
+        o[17] = t_part;
+        o[18] = t_accum;
+        o[19] = rows_built * rb;
         for (auto &e : events) (void)hipEventDestroy(e);
         events.clear();
     } catch (const Error &e) {

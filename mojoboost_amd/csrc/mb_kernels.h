@@ -15,14 +15,14 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 // Raises the dynamic LDS limits of the kernels that need more than 64 KB.
 hipError_t prepare_kernels(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
-size_t pb_lds_bytes(const DevState &s);
-// partition + histogram LDS of a tile of tile_f features
+// accumulation LDS of a tile of tile_f features
 size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized);
 size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
 size_t rank_lds_bytes(const DevState &s);
 hipError_t launch_hist(const DevState &s, hipStream_t st);
-hipError_t launch_part_hist(const DevState &s, hipStream_t st);
+hipError_t launch_partition(const DevState &s, hipStream_t st);
+hipError_t launch_accum(const DevState &s, hipStream_t st);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);

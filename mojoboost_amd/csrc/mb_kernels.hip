@@ -8,9 +8,10 @@
 //   k_hist        root histogram: LDS-privatized packed 64-bit counters
 //                 (grad | hess | count in one ds_add_u64) per block, stored
 //                 as block partials
-//   k_part_hist   expansion of a batch of leaves: row partition (wave ballot
-//                 ranks, one atomic reservation per tile and side) fused with
-//                 the smaller child's histogram accumulation
+//   k_partition   expansion of a batch of leaves, step 1: row partition (wave
+//                 ballot ranks, one atomic reservation per tile and side)
+//   k_accum       step 2: the smaller child's histogram from its now
+//                 contiguous rows (as k_hist), one block partial per task
 //   k_scan        partial merge + sibling subtraction + per-feature integer
 //                 prefix scan with fp64 gains + argmax, per (leaf, feature)
 //   k_plan        one block: folds features into each new leaf's best split,
@@ -1078,12 +1079,83 @@ struct FAcc {
 // records and stores that tile's features of its partial.
 constexpr int kHistUnroll = 4;
 
+// Accumulates the records of rows [lo, hi) of a row list (kList), or of the
+// rows lo .. hi - 1 themselves, into the block's LDS histogram:
+// LPR lanes per row, each loading 16 bytes of the record, the g/h pair
+// reaching the row's lanes by a shuffle. Loads are software-pipelined: while
+// the records of step i are added into LDS, the records of step i + 1 and
+// the row ids of step i + 2 are in flight. (The memory counter completes in
+// issue order, so a step's ids must be issued a step before its records or
+// waiting for them would also wait for every record load issued earlier.)
+template <int LPR, class Acc, bool kList>
+__device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char *lds, const int32_t *rows,
+                                                int64_t lo, int64_t hi, int Ft, const uint4 *rec,
+                                                double goss_mult) {
+    constexpr int U = kHistUnroll;
+    const int ls = s.lds_stride;
+    const int lane = lane_id();
+    const int sub = threadIdx.x % LPR;
+    const int rr = threadIdx.x / LPR;
+    const int rpp = blockDim.x / LPR;
+    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
+    const int64_t step = (int64_t)U * rpp;
+    const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
+    if (lo >= hi) return;
+    // Every load is unconditional (an entry past the range loads the last
+    // row again and is masked off when added): branches around loads would
+    // make the compiler wait for every load in flight at each of them.
+    auto load_ids = [&](int64_t i0, int32_t *id) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            int64_t i = i0 + (int64_t)u * rpp + rr;
+            i = i < hi ? i : hi - 1;
+            id[u] = kList ? rows[i] : (int32_t)i;
+        }
+    };
+    auto load_recs = [&](int64_t, const int32_t *id, uint4 *w) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t r = (uint32_t)id[u] < n32 ? (uint32_t)id[u] : 0u;  // ids come from the row lists
+            w[u] = rec[(size_t)r * LPR + sub];
+        }
+    };
+    auto accumulate = [&](int64_t i0, const int32_t *id, const uint4 *w) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * rpp + rr;
+            const uint32_t gh = __shfl(w[u].w, src_lane, 64);
+            if (i < hi) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, (int64_t)(uint32_t)id[u], gh, goss_mult);
+        }
+    };
+    int32_t id_cur[U], id_nxt[U], id_nn[U];
+    uint4 w_cur[U], w_nxt[U];
+    int64_t i0 = lo;
+    load_ids(i0, id_cur);
+    load_recs(i0, id_cur, w_cur);
+    load_ids(i0 + step, id_nxt);
+    for (;;) {
+        const bool more = i0 + step < hi;
+        if (more) {
+            load_recs(i0 + step, id_nxt, w_nxt);
+            load_ids(i0 + 2 * step, id_nn);
+        }
+        accumulate(i0, id_cur, w_cur);
+        if (!more) break;
+        i0 += step;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            id_cur[u] = id_nxt[u];
+            id_nxt[u] = id_nn[u];
+            w_cur[u] = w_nxt[u];
+        }
+    }
+}
+
 template <int LPR, class Acc>
 __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     extern __shared__ unsigned char lds[];
     if (s.round->stopped) return;
     const int64_t m = root_rows(s);
-    const int32_t *rows = s.rows0;
     const bool direct = !s.round->sampled;
     const double goss_mult = s.round->goss_mult;
     if (m <= 0) return;
@@ -1096,203 +1168,164 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     const int Ft = min(s.tile_f, s.n_features - f0);
     Acc::template zero<LPR>(lds, Ft, ls);
     __syncthreads();
-    const int lane = lane_id();
-    const int sub = threadIdx.x % LPR;
-    const int rr = threadIdx.x / LPR;
-    const int rpp = blockDim.x / LPR;
-    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
     const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
-    // Two register sets: the loads of the next kHistUnroll x rpp rows are in
-    // flight while the current ones are added into LDS.
-    const int64_t step = (int64_t)kHistUnroll * rpp;
-    uint4 wa[kHistUnroll], wb[kHistUnroll];
-    int64_t ra[kHistUnroll], rb[kHistUnroll];
-    bool oa[kHistUnroll], ob[kHistUnroll];
-    auto fetch = [&](int64_t i0, uint4 *w, int64_t *row, bool *ok) {
-#pragma unroll
-        for (int u = 0; u < kHistUnroll; ++u) {
-            const int64_t i = i0 + (int64_t)u * rpp + rr;
-            ok[u] = i < c1;
-            row[u] = 0;
-            if (ok[u]) {
-                row[u] = direct ? i : (int64_t)rows[i];
-                if ((uint64_t)row[u] >= (uint64_t)s.n) row[u] = 0;  // never taken: ids come from the row lists
-            }
-            w[u] = ok[u] ? rec[row[u] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
-        }
-    };
-    auto accumulate = [&](const uint4 *w, const int64_t *row, const bool *ok) {
-#pragma unroll
-        for (int u = 0; u < kHistUnroll; ++u) {
-            const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (ok[u]) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, row[u], gh, goss_mult);
-        }
-    };
-    int64_t i0 = c0;
-    fetch(i0, wa, ra, oa);
-    for (;;) {
-        const int64_t i1 = i0 + step;
-        if (i1 < c1) fetch(i1, wb, rb, ob);
-        accumulate(wa, ra, oa);
-        if (i1 >= c1) break;
-        const int64_t i2 = i1 + step;
-        if (i2 < c1) fetch(i2, wa, ra, oa);
-        accumulate(wb, rb, ob);
-        if (i2 >= c1) break;
-        i0 = i2;
-    }
+    if (direct) accumulate_rows<LPR, Acc, false>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
+    else accumulate_rows<LPR, Acc, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
     __syncthreads();
     Acc::template store<LPR>(s, lds, blockIdx.x, f0, Ft);
 }
 
-// ------------------------------------------------- partition + histogram
-// One launch expands every leaf of the batch: each block takes a chunk of
-// one leaf's rows (its descriptor, written by the planner), routes them to
-// the children (tree.partition_rows_into semantics: the missing bin follows
-// default_left, otherwise bin <= threshold goes left) in the other row
-// buffer -- left rows fill [begin, begin + n_left), right rows the rest --
-// and accumulates the rows of the smaller child into its LDS histogram,
-// stored as the block's partial.
-//
-// A tile is Acc::kUnroll x 1024 rows. Per tile: row ids and the split
-// feature's bins are loaded, wave ballots rank the rows, wave 0 scans the
-// per-wave counts and reserves the tile's output with one atomic per side,
-// rows are scattered, and the smaller child's rows are listed in LDS; then
-// the accumulation pass reads their records (LPR lanes per row). The order
-// of rows inside a child is not the reference's (tiles land in reservation
-// order); integer histograms are order-free, fp64 sums differ only in their
-// rounding.
-//
-// blockIdx.y is the feature tile. Every tile's block ranks the rows of its
-// descriptor the same way (ballots and a block-local scan are deterministic),
-// so each lists the same smaller-child rows; only tile 0's block reserves
-// output and scatters the rows, the others accumulate their tile's features
-// from the same list.
-constexpr int kPbThreads = 1024;
-constexpr int kPbMaxUnroll = 4;
-
-template <class Acc>
-__host__ __device__ size_t pb_lds_bytes_of(int F, int ls) {
-    return Acc::lds_bytes(F, ls) + (size_t)kPbThreads * Acc::kUnroll * 4;
+// A raw buffer resource over `bytes` bytes at p (gfx9 word 3): loads through
+// it take 32-bit offsets, and offsets at or past `bytes` read 0.
+// The arguments must be wave-uniform; they are moved to scalar registers so
+// the loads need no per-lane descriptor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    void *q = (void *)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
-template <int LPR, class Acc>
-__global__ __launch_bounds__(kPbThreads) void k_part_hist(DevState s) {
-    constexpr int U = Acc::kUnroll;
-    constexpr int kTile = kPbThreads * U;
-    extern __shared__ unsigned char lds[];
-    __shared__ int cnt_l[kPbMaxUnroll * 16], cnt_r[kPbMaxUnroll * 16];
-    __shared__ long long off_l[kPbMaxUnroll * 16], off_r[kPbMaxUnroll * 16], off_b[kPbMaxUnroll * 16];
-    __shared__ int s_nbuilt;
+// ------------------------------------------------------------- partition
+// One launch routes the rows of every leaf of the batch to the children
+// (tree.partition_rows_into semantics: the missing bin follows default_left,
+// otherwise bin <= threshold goes left) in the other row buffer -- left rows
+// fill [begin, begin + n_left), right rows the rest. Each task (descriptor,
+// written by the planner) is a chunk of at most kPartChunk rows of one leaf:
+// every thread keeps its kPartRows row ids and their sides in registers,
+// wave ballots count the rows of each (row group u, wave) entry, the block
+// scans the entries in row order and reserves the chunk's output with one
+// atomic per side, and the rows are written in their input order within each
+// side. One reservation per chunk of 8K rows keeps the same-address atomics
+// on a leaf's two cursors (the L2 serializes them, ~12 ns each on MI355X)
+// within the kernel's own duration even for the root split (1.3K chunks). The order of rows inside a child is not the
+// reference's (chunks land in reservation order); integer histograms are
+// order-free, fp64 sums differ only in their rounding.
+constexpr int kPartThreads = 256;
+constexpr int kPartRows = kPartChunk / kPartThreads;  // rows per thread of a task
+static_assert(kPartRows * kPartThreads == kPartChunk && kPartRows <= 32, "a task's rows fit the thread bit masks");
+
+__global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
+    constexpr int NW = kPartThreads / 64;  // waves
+    constexpr int E = kPartRows * NW;      // (row group, wave) entries of a task
+    constexpr int SW = E / 64;             // waves that scan one side's entries
+    static_assert(E % 64 == 0 && 2 * SW <= NW, "one wave scans 64 entries");
+    __shared__ int cnt_l[E], cnt_r[E];     // counts, then exclusive prefixes within a scan wave
+    __shared__ int wtot[2][SW];            // scan-wave totals, then their exclusive prefixes
+    __shared__ long long base[2];
     const int n_blocks = s.batch->n_blocks;
-    const double goss_mult = s.round->goss_mult;
-    const int ls = s.lds_stride, tf = s.tile_f;
-    const int f0 = (int)blockIdx.y * tf;
-    const int Ft = min(tf, s.n_features - f0);
-    const bool owner = blockIdx.y == 0;  // reserves output and scatters the rows
-    int32_t *list = (int32_t *)(lds + Acc::lds_bytes(tf, ls));
-    const int lane = lane_id(), w = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
     const unsigned long long below = (1ULL << lane) - 1ULL;
-    const int sub = threadIdx.x % LPR;
-    const int rr = threadIdx.x / LPR;
-    const int rpp = kPbThreads / LPR;
-    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
-    const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
-    // a block takes descriptors blockIdx.x, + gridDim.x, ...; each one is a
-    // whole accumulation (zeroed LDS, stored partial)
+    const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
     for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
         const PbDesc d = s.pb_desc[blk];
-        Acc::template zero<LPR>(lds, Ft, ls);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
-        const uint8_t *col = s.bins_cm + (size_t)d.feature * s.n;
         const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
-        const bool bl = d.builds_left != 0;
-        unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item];
-        for (int64_t t0 = d.c0; t0 < d.c1; t0 += kTile) {
-            int32_t r[U];
-            bool left[U], valid[U];
-            unsigned long long lm[U], rm[U];
+        // buffer loads: 32-bit offsets (one VGPR per gather instead of a
+        // 64-bit address), and any offset past the range reads 0
+        const __amdgpu_buffer_rsrc_t ids = buffer_rsrc(src + d.c0, (uint32_t)(d.c1 - d.c0) * 4u);
+        const __amdgpu_buffer_rsrc_t col = buffer_rsrc(s.bins_cm + (size_t)d.feature * s.n, (uint32_t)s.n);
+        int32_t r[kPartRows];
+        uint32_t vbits = 0, lbits = 0;
+        // every load unconditional (a row past the task reads id 0 and is
+        // masked off), so all of them are in flight together
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int64_t i = t0 + (int64_t)u * kPbThreads + threadIdx.x;
-                valid[u] = i < d.c1;
-                r[u] = valid[u] ? src[i] : 0;
-                if ((uint32_t)r[u] >= (uint64_t)s.n) r[u] = 0;  // never taken: ids come from the row lists
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int b = valid[u] ? (int)col[r[u]] : 0;
-                left[u] = (b == mb) ? (dl != 0) : (b <= thr);
-                lm[u] = __ballot(valid[u] && left[u]);
-                rm[u] = __ballot(valid[u] && !left[u]);
-                if (lane == 0) {
-                    cnt_l[u * 16 + w] = __popcll(lm[u]);
-                    cnt_r[u * 16 + w] = __popcll(rm[u]);
-                }
-            }
-            __syncthreads();
-            if (w == 0) {
-                // entry k = u * 16 + wave, in tile order (U * 16 <= 64 entries)
-                const long long vl = lane < U * 16 ? cnt_l[lane] : 0, vr = lane < U * 16 ? cnt_r[lane] : 0;
-                const long long il = wave_incl_scan(vl), ir = wave_incl_scan(vr);
-                const long long tl = __shfl(il, 63, 64), tr = __shfl(ir, 63, 64);
-                long long bl_base = 0, br_base = 0;
-                if (lane == 0 && owner) {
-                    bl_base = tl ? (long long)atomicAdd(&cur[0], (unsigned long long)tl) : 0;
-                    br_base = tr ? (long long)atomicAdd(&cur[1], (unsigned long long)tr) : 0;
-                }
-                bl_base = __shfl(bl_base, 0, 64);
-                br_base = __shfl(br_base, 0, 64);
-                off_l[lane] = bl_base + il - vl;
-                off_r[lane] = br_base + ir - vr;
-                off_b[lane] = bl ? il - vl : ir - vr;
-                if (lane == 0) s_nbuilt = (int)(bl ? tl : tr);
-            }
-            __syncthreads();
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (!valid[u]) continue;
-                const int k = u * 16 + w;
-                long long rank;
-                if (left[u]) {
-                    rank = __popcll(lm[u] & below);
-                    const long long p = off_l[k] + rank;
-                    if (owner) {
-                        if (p < d.n_left) dst[p] = r[u];
-                        else atomicOr(s.error, 1);
-                    }
-                } else {
-                    rank = __popcll(rm[u] & below);
-                    const long long p = d.n_left + off_r[k] + rank;
-                    if (owner) {
-                        if (p < d.m) dst[p] = r[u];
-                        else atomicOr(s.error, 1);
-                    }
-                }
-                if (left[u] == bl) list[off_b[k] + rank] = r[u];
-            }
-            __syncthreads();
-            const int nbt = s_nbuilt;
-            for (int k0 = 0; k0 < nbt; k0 += kHistUnroll * rpp) {
-                uint4 v[kHistUnroll];
-                int64_t row[kHistUnroll];
-                bool ok[kHistUnroll];
-#pragma unroll
-                for (int u = 0; u < kHistUnroll; ++u) {
-                    const int k = k0 + u * rpp + rr;
-                    ok[u] = k < nbt;
-                    row[u] = ok[u] ? (int64_t)list[k] : 0;
-                    v[u] = ok[u] ? rec[row[u] * LPR + sub] : make_uint4(0u, 0u, 0u, 0u);
-                }
-#pragma unroll
-                for (int u = 0; u < kHistUnroll; ++u) {
-                    const uint32_t gh = __shfl(v[u].w, src_lane, 64);
-                    if (ok[u]) Acc::template add<LPR>(lds, s, v[u], sub, Ft, ls, row[u], gh, goss_mult);
-                }
-            }
-            __syncthreads();
+        for (int u = 0; u < kPartRows; ++u) {
+            const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
+            vbits |= (i < d.c1 ? 1u : 0u) << u;
+            r[u] = __builtin_amdgcn_raw_buffer_load_b32(ids, (u * kPartThreads + tid) * 4, 0, 0);
+            if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the row lists
         }
+        uint32_t bin[kPartRows];
+#pragma unroll
+        for (int u = 0; u < kPartRows; ++u) bin[u] = __builtin_amdgcn_raw_buffer_load_b8(col, r[u], 0, 0);
+#pragma unroll
+        for (int u = 0; u < kPartRows; ++u) {
+            const bool valid = (vbits >> u) & 1u;
+            const int b = (int)bin[u];
+            const bool left = (b == mb) ? (dl != 0) : (b <= thr);
+            lbits |= (left ? 1u : 0u) << u;
+            const unsigned long long lm = __ballot(valid && left);
+            const unsigned long long rm = __ballot(valid && !left);
+            if (lane == 0) {
+                cnt_l[u * NW + w] = __popcll(lm);
+                cnt_r[u * NW + w] = __popcll(rm);
+            }
+        }
+        __syncthreads();
+        // entry k = u * NW + wave is in row order; waves 0 .. SW-1 scan the
+        // left counts, SW .. 2 SW - 1 the right ones
+        if (w < 2 * SW) {
+            int *c = w < SW ? cnt_l : cnt_r;
+            const int k = (w % SW) * 64 + lane;
+            const int v = c[k];
+            const int inc = (int)wave_incl_scan((long long)v);
+            c[k] = inc - v;
+            if (lane == 63) wtot[w / SW][w % SW] = inc;
+        }
+        __syncthreads();
+        if (tid < 2) {
+            int a = 0;
+            for (int j = 0; j < SW; ++j) {
+                const int t = wtot[tid][j];
+                wtot[tid][j] = a;
+                a += t;
+            }
+            unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * d.item + tid];
+            base[tid] = a ? (long long)atomicAdd(cur, (unsigned long long)a) : 0;
+        }
+        __syncthreads();
+        // positions relative to the leaf's begin (below m < 2^31); a store
+        // past the leaf's range is dropped by the buffer and flagged
+        const int bl = (int)base[0], br = (int)base[1];
+        const int nl = (int)d.n_left, m = (int)d.m;
+        const __amdgpu_buffer_rsrc_t out = buffer_rsrc(dst, (uint32_t)m * 4u);
+        bool overflow = false;
+        // opaque to the compiler, so the ballots below are not merged with
+        // the counting ones (which would keep 64 wave masks live across the
+        // barriers)
+        asm volatile("" : "+v"(lbits), "+v"(vbits));
+#pragma unroll
+        for (int u = 0; u < kPartRows; ++u) {
+            const bool valid = (vbits >> u) & 1u;
+            const bool left = (lbits >> u) & 1u;
+            const unsigned long long lm = __ballot(valid && left);
+            const unsigned long long rm = __ballot(valid && !left);
+            const int k = u * NW + w;
+            const int pl = bl + wtot[0][k >> 6] + cnt_l[k] + (int)__popcll(lm & below);
+            const int pr = nl + br + wtot[1][k >> 6] + cnt_r[k] + (int)__popcll(rm & below);
+            const int p = left ? pl : pr;
+            overflow |= valid && (left ? pl >= nl : pr >= m);
+            if (valid) __builtin_amdgcn_raw_buffer_store_b32(r[u], out, p * 4, 0, 0);
+        }
+        if (overflow) atomicOr(s.error, 1);
+        __syncthreads();  // counts and offsets are rewritten by the next task
+    }
+}
+
+// ---------------------------------------------------------- accumulation
+// One launch accumulates the smaller child of every leaf of the batch from
+// its rows, now contiguous in the partitioned row buffer. Each task
+// (descriptor, written by the planner) is a chunk of one child's rows and
+// yields one block partial; the scan kernel merges an item's partials.
+// blockIdx.y is the feature tile: the block reads that tile's records and
+// stores that tile's features of its partial.
+template <int LPR, class Acc>
+__global__ __launch_bounds__(1024) void k_accum(DevState s) {
+    extern __shared__ unsigned char lds[];
+    const int n_acc = s.batch->n_acc;
+    const double goss_mult = s.round->goss_mult;
+    const int ls = s.lds_stride;
+    const int f0 = (int)blockIdx.y * s.tile_f;
+    const int Ft = min(s.tile_f, s.n_features - f0);
+    const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
+    for (int blk = blockIdx.x; blk < n_acc; blk += gridDim.x) {
+        const AcDesc d = s.ac_desc[blk];
+        Acc::template zero<LPR>(lds, Ft, ls);
+        __syncthreads();
+        accumulate_rows<LPR, Acc, true>(s, lds, d.buf ? s.rows1 : s.rows0, d.lo, d.hi, Ft, rec, goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
@@ -1821,7 +1854,7 @@ constexpr int kPlanThreads = 1024;
 // LDS layout of the planner (byte offsets), shared by the host's size query
 // and the kernel.
 struct PlanLayout {
-    size_t wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, it;
+    size_t wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
     size_t total;
 };
 
@@ -1851,6 +1884,8 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
     p.sel_e = take((size_t)4 * K, 4);
     p.pcnt = take((size_t)4 * K, 4);
     p.poff = take((size_t)4 * (K + 1), 4);
+    p.qcnt = take((size_t)4 * K, 4);
+    p.qoff = take((size_t)4 * (K + 1), 4);
     p.it = take(sizeof(Item) * K, 16);
     p.total = o;
     return p;
@@ -1858,7 +1893,7 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
 
 struct PlanView {
     double *wg, *eg, *sg, *cb;
-    int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff;
+    int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff, *qcnt, *qoff;
     Item *it;
 };
 
@@ -1882,6 +1917,8 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.sel_e = (int32_t *)(smem + p.sel_e);
     v.pcnt = (int32_t *)(smem + p.pcnt);
     v.poff = (int32_t *)(smem + p.poff);
+    v.qcnt = (int32_t *)(smem + p.qcnt);
+    v.qoff = (int32_t *)(smem + p.qoff);
     v.it = (Item *)(smem + p.it);
     return v;
 }
@@ -1890,7 +1927,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
     __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x, s_vf;
-    __shared__ unsigned long long s_rows_built, s_rows_parted, s_rows_total;
+    __shared__ unsigned long long s_rows_built, s_rows_parted, s_rows_total, s_built_total;
+    __shared__ int s_total_p;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
     const int L = s.hp.num_leaves, F = s.n_features;
@@ -1909,6 +1947,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.n_blocks = 0;
             b.done = 1;
             b.iters = 0;
+            b.n_acc = 0;
+            b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
             *s.batch = b;
         }
         return;
@@ -2125,6 +2165,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.n_blocks = 0;
             b.done = 1;
             b.iters = g.iterations;
+            b.n_acc = 0;
+            b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
             *s.batch = b;
         }
     };
@@ -2234,38 +2276,52 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             return;
         }
     }
-    // Rows per block, one value for the whole batch: the batch's rows spread
-    // over about pb_launch blocks (one wave of resident blocks), at least
-    // hist_chunk_min rows each. Fewer blocks mean fewer partials to store and
-    // merge; a batch never needs more than n / hist_chunk_min + nsel blocks.
-    if (tid == 0) s_rows_total = 0;
-    __syncthreads();
-    for (int jj = tid; jj < nsel; jj += nthr) {
-        const ENode *e = &s.enodes[v.sel_e[jj]];
-        atomicAdd(&s_rows_total, (unsigned long long)(e->end - e->begin));
+    // Rows per task, one value per kind for the whole batch. Accumulation:
+    // the batch's accumulated rows spread over about pb_launch tasks (one
+    // per resident block), at least hist_chunk_min rows each (fewer tasks
+    // mean fewer partials to store and merge; a batch never needs more than
+    // n / hist_chunk_min + nsel of them). Partition: chunks of kPartChunk
+    // parent rows (one output reservation each).
+    if (tid == 0) {
+        s_rows_total = 0;
+        s_built_total = 0;
     }
     __syncthreads();
-    int64_t chunk = ((int64_t)s_rows_total + s.pb_launch - 1) / s.pb_launch;
-    if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
-    if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
     for (int jj = tid; jj < nsel; jj += nthr) {
         const ENode *e = &s.enodes[v.sel_e[jj]];
-        const int64_t m = e->end - e->begin;
-        v.pcnt[jj] = (int)((m + chunk - 1) / chunk);
+        const int64_t m = e->end - e->begin, nl = e->n_left;
+        atomicAdd(&s_rows_total, (unsigned long long)m);
+        atomicAdd(&s_built_total, (unsigned long long)(nl <= m - nl ? nl : m - nl));
+    }
+    __syncthreads();
+    int64_t chunk = ((int64_t)s_built_total + s.pb_launch - 1) / s.pb_launch;
+    if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+    if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
+    const int64_t chunk_p = kPartChunk;
+    for (int jj = tid; jj < nsel; jj += nthr) {
+        const ENode *e = &s.enodes[v.sel_e[jj]];
+        const int64_t m = e->end - e->begin, nl = e->n_left;
+        const int64_t mb = nl <= m - nl ? nl : m - nl;
+        v.pcnt[jj] = (int)((mb + chunk - 1) / chunk);
+        v.qcnt[jj] = (int)((m + chunk_p - 1) / chunk_p);
     }
     __syncthreads();
     if (tid == 0) {
-        int a = 0;
+        int a = 0, c = 0;
         for (int jj = 0; jj < nsel; ++jj) {
             v.poff[jj] = a;
             a += v.pcnt[jj];
+            v.qoff[jj] = c;
+            c += v.qcnt[jj];
         }
         v.poff[nsel] = a;
+        v.qoff[nsel] = c;
         s_total = a;
+        s_total_p = c;
     }
     __syncthreads();
-    const int total = s_total;
-    if (total > s.pb_grid) {  // the leaves of a batch are disjoint, so never
+    const int total = s_total, total_p = s_total_p;
+    if (total > s.pb_grid || total_p > s.part_grid) {  // the leaves of a batch are disjoint, so never
         finish(4);
         return;
     }
@@ -2330,12 +2386,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         atomicAdd(&s_rows_parted, (unsigned long long)m);
     }
     __syncthreads();
-    // block descriptors
-    for (int b = tid; b < total; b += nthr) {
-        int lo = 0, hi = nsel - 1;  // last item with poff <= b
+    // partition descriptors
+    for (int b = tid; b < total_p; b += nthr) {
+        int lo = 0, hi = nsel - 1;  // last item with qoff <= b
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (v.poff[mid] <= b) lo = mid;
+            if (v.qoff[mid] <= b) lo = mid;
             else hi = mid - 1;
         }
         const Item &it = v.it[lo];
@@ -2345,8 +2401,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         d.begin = it.begin;
         d.n_left = it.n_left;
         d.m = m;
-        d.c0 = (int64_t)(b - v.poff[lo]) * chunk;
-        d.c1 = d.c0 + chunk < m ? d.c0 + chunk : m;
+        d.c0 = (int64_t)(b - v.qoff[lo]) * chunk_p;
+        d.c1 = d.c0 + chunk_p < m ? d.c0 + chunk_p : m;
         d.item = lo;
         d.src_buf = it.src_buf;
         d.feature = pe.feature;
@@ -2356,6 +2412,25 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         d.builds_left = it.builds_left;
         d.pad_ = 0;
         s.pb_desc[b] = d;
+    }
+    // accumulation descriptors: chunks of the accumulated child's range in
+    // the other row buffer
+    for (int b = tid; b < total; b += nthr) {
+        int lo = 0, hi = nsel - 1;  // last item with poff <= b
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (v.poff[mid] <= b) lo = mid;
+            else hi = mid - 1;
+        }
+        const Item &it = v.it[lo];
+        const int64_t c_lo = it.builds_left ? it.begin : it.begin + it.n_left;
+        const int64_t c_hi = it.builds_left ? it.begin + it.n_left : it.end;
+        AcDesc d;
+        d.lo = c_lo + (int64_t)(b - v.poff[lo]) * chunk;
+        d.hi = d.lo + chunk < c_hi ? d.lo + chunk : c_hi;
+        d.item = lo;
+        d.buf = 1 - it.src_buf;
+        s.ac_desc[b] = d;
     }
     __syncthreads();
     if (tid == 0) {
@@ -2368,9 +2443,11 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         *s.grow = g;
         Batch b;
         b.n_items = nsel;
-        b.n_blocks = total;
+        b.n_blocks = total_p;
         b.done = 0;
         b.iters = g.iterations;
+        b.n_acc = total;
+        b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
         *s.batch = b;
     }
 }
@@ -2614,12 +2691,8 @@ size_t score_lds_bytes(const DevState &s) {
 size_t hist_lds_bytes(const DevState &s) {
     return s.hp.quantized ? QAcc::lds_bytes(s.tile_f, s.lds_stride) : FAcc::lds_bytes(s.tile_f, s.lds_stride);
 }
-size_t pb_lds_bytes(const DevState &s) {
-    return s.hp.quantized ? pb_lds_bytes_of<QAcc>(s.tile_f, s.lds_stride)
-                          : pb_lds_bytes_of<FAcc>(s.tile_f, s.lds_stride);
-}
 size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized) {
-    return quantized ? pb_lds_bytes_of<QAcc>(tile_f, lds_stride) : pb_lds_bytes_of<FAcc>(tile_f, lds_stride);
+    return quantized ? QAcc::lds_bytes(tile_f, lds_stride) : FAcc::lds_bytes(tile_f, lds_stride);
 }
 size_t plan_lds_bytes(const DevState &s) {
     return plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features).total;
@@ -2633,26 +2706,26 @@ size_t plan_lds_bytes(const DevState &s) {
     } while (0)
 
 hipError_t prepare_kernels(const DevState &s) {
-    const size_t h = hist_lds_bytes(s), pb = pb_lds_bytes(s);
+    const size_t h = hist_lds_bytes(s);
     if (s.hp.objective == kObjLambdarank) MB_SET_LDS(k_lambdarank, rank_lds_bytes(s));
     if (s.hp.quantized) {
         MB_SET_LDS((k_hist<1, QAcc>), h);
         MB_SET_LDS((k_hist<2, QAcc>), h);
         MB_SET_LDS((k_hist<4, QAcc>), h);
         MB_SET_LDS((k_hist<8, QAcc>), h);
-        MB_SET_LDS((k_part_hist<1, QAcc>), pb);
-        MB_SET_LDS((k_part_hist<2, QAcc>), pb);
-        MB_SET_LDS((k_part_hist<4, QAcc>), pb);
-        MB_SET_LDS((k_part_hist<8, QAcc>), pb);
+        MB_SET_LDS((k_accum<1, QAcc>), h);
+        MB_SET_LDS((k_accum<2, QAcc>), h);
+        MB_SET_LDS((k_accum<4, QAcc>), h);
+        MB_SET_LDS((k_accum<8, QAcc>), h);
     } else {
         MB_SET_LDS((k_hist<1, FAcc>), h);
         MB_SET_LDS((k_hist<2, FAcc>), h);
         MB_SET_LDS((k_hist<4, FAcc>), h);
         MB_SET_LDS((k_hist<8, FAcc>), h);
-        MB_SET_LDS((k_part_hist<1, FAcc>), pb);
-        MB_SET_LDS((k_part_hist<2, FAcc>), pb);
-        MB_SET_LDS((k_part_hist<4, FAcc>), pb);
-        MB_SET_LDS((k_part_hist<8, FAcc>), pb);
+        MB_SET_LDS((k_accum<1, FAcc>), h);
+        MB_SET_LDS((k_accum<2, FAcc>), h);
+        MB_SET_LDS((k_accum<4, FAcc>), h);
+        MB_SET_LDS((k_accum<8, FAcc>), h);
     }
     MB_SET_LDS(k_plan, plan_lds_bytes(s));
     MB_SET_LDS(k_goss_walk, (size_t)2 * kGossTile * sizeof(int32_t));
@@ -2675,21 +2748,25 @@ hipError_t launch_hist_t(const DevState &s, hipStream_t st) {
 hipError_t launch_hist(const DevState &s, hipStream_t st) {
     return s.hp.quantized ? launch_hist_t<QAcc>(s, st) : launch_hist_t<FAcc>(s, st);
 }
+hipError_t launch_partition(const DevState &s, hipStream_t st) {
+    hipLaunchKernelGGL(k_partition, dim3(s.part_launch), dim3(kPartThreads), 0, st, s);
+    return hipGetLastError();
+}
 template <class Acc>
-hipError_t launch_part_hist_t(const DevState &s, hipStream_t st) {
-    const size_t lds = pb_lds_bytes(s);
-    const dim3 grid(s.pb_launch, s.n_tiles), block(kPbThreads);
+hipError_t launch_accum_t(const DevState &s, hipStream_t st) {
+    const size_t lds = hist_lds_bytes(s);
+    const dim3 grid(s.pb_launch, s.n_tiles), block(1024);
     switch (s.rec_bytes / 16) {
-    case 1: hipLaunchKernelGGL((k_part_hist<1, Acc>), grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL((k_part_hist<2, Acc>), grid, block, lds, st, s); break;
-    case 4: hipLaunchKernelGGL((k_part_hist<4, Acc>), grid, block, lds, st, s); break;
-    case 8: hipLaunchKernelGGL((k_part_hist<8, Acc>), grid, block, lds, st, s); break;
+    case 1: hipLaunchKernelGGL((k_accum<1, Acc>), grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL((k_accum<2, Acc>), grid, block, lds, st, s); break;
+    case 4: hipLaunchKernelGGL((k_accum<4, Acc>), grid, block, lds, st, s); break;
+    case 8: hipLaunchKernelGGL((k_accum<8, Acc>), grid, block, lds, st, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
-hipError_t launch_part_hist(const DevState &s, hipStream_t st) {
-    return s.hp.quantized ? launch_part_hist_t<QAcc>(s, st) : launch_part_hist_t<FAcc>(s, st);
+hipError_t launch_accum(const DevState &s, hipStream_t st) {
+    return s.hp.quantized ? launch_accum_t<QAcc>(s, st) : launch_accum_t<FAcc>(s, st);
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     const int grid = root_mode ? s.n_features : s.scan_grid;

@@ -56,19 +56,28 @@ struct Item {
     int32_t pad_;
 };
 
-// Work of one partition+histogram block: a chunk [c0, c1) of an item's
-// parent range (offsets relative to begin).
+// Work of one partition task: a chunk [c0, c1) of an item's parent range
+// (offsets relative to begin).
 struct PbDesc {
     int64_t begin, n_left, m, c0, c1;
     int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left, pad_;
 };
 
+// Work of one accumulation task: rows [lo, hi) of row buffer `buf` (a chunk
+// of an item's accumulated child), summed into one block partial.
+struct AcDesc {
+    int64_t lo, hi;
+    int32_t item, buf;
+};
+
 // Written by the planner; the host reads it back between launch groups.
 struct Batch {
     int32_t n_items;   // 0: nothing to do this iteration
-    int32_t n_blocks;  // partition+histogram descriptors in use
+    int32_t n_blocks;  // partition descriptors in use
     int32_t done;      // the tree is complete
     int32_t iters;     // expansion iterations planned so far in this tree
+    int32_t n_acc;     // accumulation descriptors (block partials) in use
+    int32_t pad_[3];
 };
 
 // Replay state of the best-first order (touched by the planning block only).
@@ -110,6 +119,10 @@ struct Round {
     double grad_units, hess_units;
     double goss_mult;    // GOSS weight of the sampled small-gradient rows (1 when off)
 };
+
+// Parent rows of a partition task, at most (the planner's chunking; the host
+// sizes the descriptor buffer from it).
+constexpr int kPartChunk = 8192;
 
 // Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
 constexpr int kGossTileRows = 16384;
@@ -228,7 +241,8 @@ struct DevState {
     int32_t *e_left;       // e_cap: left child (right = left + 1), -1 while unexpanded
     int32_t *e_parent;     // e_cap: parent, -1 for the root
     Item *items;           // kmax
-    PbDesc *pb_desc;       // pb_grid
+    PbDesc *pb_desc;       // part_grid
+    AcDesc *ac_desc;       // pb_grid
     Batch *batch;
     Grow *grow;
     int32_t *slot_e;       // num_leaves: explored node of each frontier slot
@@ -239,9 +253,12 @@ struct DevState {
     int32_t kmax;          // most leaves expanded per launch
     int32_t max_exp;       // most expansions per tree (2 num_leaves - 1)
     int32_t e_cap;         // ENode capacity (1 + 2 max_exp)
-    int32_t pb_grid;       // most partition+histogram descriptors of a batch
+    int32_t pb_grid;       // most accumulation descriptors (block partials) of a batch
+    int32_t part_grid;     // most partition descriptors of a batch
     int32_t scan_grid;     // blocks of a scan launch
-    int32_t pb_launch;     // blocks of a partition+histogram launch (grid-strided)
+    int32_t pb_launch;     // blocks of an accumulation launch (grid-strided)
+    int32_t part_launch;   // blocks of a partition launch (grid-strided)
+    int32_t pad_grid_;
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;

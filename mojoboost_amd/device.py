@@ -150,7 +150,8 @@ class Fit:
         names = ("train_seconds", "hist_ms", "hist_bytes", "hist_rows_features",
                  "hist_builds", "root_bytes", "root_ms", "trees_grown", "growth_ms",
                  "root_growth_ms", "iterations", "expansions", "rows_built", "rows_parted",
-                 "expand_launches", "expand_ms", "expand_bytes")
+                 "expand_launches", "expand_ms", "expand_bytes", "partition_ms", "accum_ms",
+                 "accum_bytes")
         st = np.zeros(len(names))
         count = L.mbh_fit_stats(handle, ptr(st), len(names))
         assert count == len(names), count
