@@ -112,6 +112,33 @@ __device__ __forceinline__ unsigned wave_min_u32(unsigned x) {
 // so the maximum is found on the high word, then the low word among lanes
 // tied on it, then the smallest order among lanes holding the maximum.
 // Orders are non-negative.
+// The same argmax in one pass: every DPP step carries (gain bits, order)
+// and keeps the better pair (larger gain, then smaller order), so the
+// reduction is one chain of 6 steps instead of three.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void lex_step(unsigned &hi, unsigned &lo, unsigned &ord) {
+    const unsigned ohi = dpp_u32<CTRL, ROW_MASK>(hi), olo = dpp_u32<CTRL, ROW_MASK>(lo),
+                   oord = dpp_u32<CTRL, ROW_MASK>(ord);
+    const bool better = ohi > hi || (ohi == hi && (olo > lo || (olo == lo && oord < ord)));
+    hi = better ? ohi : hi;
+    lo = better ? olo : lo;
+    ord = better ? oord : ord;
+}
+__device__ __forceinline__ void wave_argmax_lex(double &gain, int &order) {
+    const unsigned long long bits = gain > 0.0 ? (unsigned long long)__double_as_longlong(gain) : 0ULL;
+    unsigned hi = (unsigned)(bits >> 32), lo = (unsigned)bits, ord = (unsigned)order;
+    lex_step<0xB1, 0xF>(hi, lo, ord);
+    lex_step<0x4E, 0xF>(hi, lo, ord);
+    lex_step<0x141, 0xF>(hi, lo, ord);
+    lex_step<0x140, 0xF>(hi, lo, ord);
+    lex_step<0x142, 0xA>(hi, lo, ord);
+    lex_step<0x143, 0xC>(hi, lo, ord);
+    hi = (unsigned)__builtin_amdgcn_readlane((int)hi, 63);
+    lo = (unsigned)__builtin_amdgcn_readlane((int)lo, 63);
+    order = __builtin_amdgcn_readlane((int)ord, 63);
+    gain = __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 __device__ __forceinline__ void wave_argmax(double &gain, int &order) {
     const unsigned long long bits = gain > 0.0 ? (unsigned long long)__double_as_longlong(gain) : 0ULL;
     const unsigned hi = (unsigned)(bits >> 32), lo = (unsigned)bits;
@@ -1854,7 +1881,7 @@ constexpr int kPlanThreads = 1024;
 // LDS layout of the planner (byte offsets), shared by the host's size query
 // and the kernel.
 struct PlanLayout {
-    size_t wg, eg, sg, cb, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
+    size_t wg, eg, sg, cb, kr, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
     size_t total;
 };
 
@@ -1870,12 +1897,13 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
     p.wg = take((size_t)8 * 2 * K, 8);       // pair's best gain
     p.eg = take((size_t)8 * E, 8);           // explored node's gain view
     p.sg = take((size_t)8 * L, 8);           // frontier slot's gain
-    p.cb = take((size_t)8 * E, 8);           // candidates' bottleneck values
+    p.cb = take((size_t)8 * E, 8);           // replay: left child's gain; selection: bottleneck values
+    p.kr = take((size_t)8 * E, 8);           // replay: right child's gain; selection: fr, ci
+    p.fr = p.kr;                             // in the committed frontier
+    p.ci = p.kr + (size_t)4 * E;             // jump pointers, then candidates' node ids
     p.wf = take((size_t)4 * 2 * K, 4);       // pair's best feature
     p.el = take((size_t)4 * E, 4);           // explored node's left child
     p.ep = take((size_t)4 * E, 4);           // explored node's parent
-    p.fr = take((size_t)4 * E, 4);           // in the committed frontier
-    p.ci = take((size_t)4 * E, 4);           // candidates' node ids
     p.sl_e = take((size_t)4 * L, 4);
     p.sl_fid = take((size_t)4 * L, 4);
     p.cm_e = take((size_t)4 * L, 4);
@@ -1892,7 +1920,7 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
 }
 
 struct PlanView {
-    double *wg, *eg, *sg, *cb;
+    double *wg, *eg, *sg, *cb, *gr;
     int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff, *qcnt, *qoff;
     Item *it;
 };
@@ -1904,6 +1932,7 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.eg = (double *)(smem + p.eg);
     v.sg = (double *)(smem + p.sg);
     v.cb = (double *)(smem + p.cb);
+    v.gr = (double *)(smem + p.kr);
     v.wf = (int32_t *)(smem + p.wf);
     v.el = (int32_t *)(smem + p.el);
     v.ep = (int32_t *)(smem + p.ep);
@@ -1921,6 +1950,106 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.qoff = (int32_t *)(smem + p.qoff);
     v.it = (Item *)(smem + p.it);
     return v;
+}
+
+// Best-first replay by one wave (tree.grow_tree_leaves_profiled with
+// growth_policy.GrowthSchedule.next_leaf: the frontier slot of largest gain
+// splits next, lowest slot on ties, gain > 0, until num_leaves). The frontier
+// lives in registers: lane l holds slots l, l + 64, ... (QS of them: gain,
+// explored node, node id) and its own best (gain, slot), so a pick is one
+// wave argmax, and a commit reads the picked node's children (one LDS round
+// trip) and updates the two slots it touches -- the left child keeps the
+// parent's slot, the right one takes slot n_leaves; node ids left = n_nodes,
+// right = n_nodes + 1. The replay stops at a pick whose leaf has not been
+// expanded yet (x) or when the tree is complete (done).
+template <int QS>
+__device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &done, int &x) {
+    const int lane = lane_id();
+    const int nl0 = nl;
+    double sg[QS];
+    int se[QS], sf[QS];
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+        const int slot = lane + 64 * q;
+        const bool in = slot < nl0;
+        sg[q] = in ? v.sg[slot] : 0.0;  // 0 is never picked (gain must be > 0)
+        se[q] = in ? v.sl_e[slot] : -1;
+        sf[q] = in ? v.sl_fid[slot] : -1;
+    }
+    double lbg;
+    int lbi;
+    auto local_best = [&]() {
+        lbg = 0.0;
+        lbi = 0x7FFFFFFF;
+#pragma unroll
+        for (int q = 0; q < QS; ++q)
+            if (sg[q] > lbg) {  // ascending slots: strict '>' keeps the lowest
+                lbg = sg[q];
+                lbi = lane + 64 * q;
+            }
+    };
+    local_best();
+    for (;;) {
+        if (nl >= L) {
+            done = 1;
+            break;
+        }
+        double bg = lbg;
+        int bi = lbi;
+        wave_argmax_lex(bg, bi);
+        if (bi == 0x7FFFFFFF) {
+            done = 1;
+            break;
+        }
+        const int q = bi >> 6, ol = bi & 63;
+        int xe = se[0], xf = sf[0];
+#pragma unroll
+        for (int qq = 1; qq < QS; ++qq)
+            if (qq == q) {
+                xe = se[qq];
+                xf = sf[qq];
+            }
+        const int X = __builtin_amdgcn_readlane(xe, ol);
+        const int fid = __builtin_amdgcn_readlane(xf, ol);
+        const int le = v.el[X];
+        const double gl = v.cb[X], gr = v.gr[X];
+        if (le < 0) {
+            x = X;
+            break;
+        }
+        if (lane == 0) {
+            v.cm_e[nc] = X;
+            v.cm_fid[nc] = fid;
+            v.cm_lf[nc] = nn;
+        }
+        const int q2 = nl >> 6, ol2 = nl & 63;
+#pragma unroll
+        for (int qq = 0; qq < QS; ++qq) {
+            if (lane == ol && qq == q) {
+                sg[qq] = gl;
+                se[qq] = le;
+                sf[qq] = nn;
+            }
+            if (lane == ol2 && qq == q2) {
+                sg[qq] = gr;
+                se[qq] = le + 1;
+                sf[qq] = nn + 1;
+            }
+        }
+        local_best();
+        ++nl;
+        nn += 2;
+        ++nc;
+    }
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+        const int slot = lane + 64 * q;
+        if (slot < nl) {
+            v.sg[slot] = sg[q];
+            v.sl_e[slot] = se[q];
+            v.sl_fid[slot] = sf[q];
+        }
+    }
 }
 
 __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode) {
@@ -1990,21 +2119,54 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             v.sl_e[i] = s.slot_e[i];
             v.sl_fid[i] = s.slot_fid[i];
         }
-    for (int pr = wv; pr < n_pairs; pr += nwaves) {
-        double bg = 0.0;
-        int bf = 0x7FFFFFFF;
-        for (int ff = lane; ff < F; ff += 64) {
-            const ScanResult &sr = s.scan[(size_t)pr * F + ff];
-            const double q = sr.found ? sr.gain : -1.0;
-            if (q > bg) {
-                bg = q;
-                bf = ff;
+    // every load unconditional (a branch between dependent loads would cost a
+    // memory round trip each): a wave takes kPW pairs at once when F <= 64,
+    // lane = feature; the argmax keeps the lowest feature on equal gains
+    constexpr int kPW = 4;
+    if (F <= 64) {
+        for (int pr0 = wv; pr0 < n_pairs; pr0 += nwaves * kPW) {
+            double gq[kPW];
+            int fq[kPW];
+#pragma unroll
+            for (int k = 0; k < kPW; ++k) {
+                int pr = pr0 + k * nwaves;
+                pr = pr < n_pairs ? pr : pr0;
+                const ScanResult &sr = s.scan[(size_t)pr * F + (lane < F ? lane : 0)];
+                gq[k] = sr.gain;
+                fq[k] = sr.found;
+            }
+#pragma unroll
+            for (int k = 0; k < kPW; ++k) {
+                const int pr = pr0 + k * nwaves;
+                double bg = (lane < F && fq[k]) ? gq[k] : 0.0;
+                int bf = (lane < F && fq[k] && gq[k] > 0.0) ? lane : 0x7FFFFFFF;
+                if (bf == 0x7FFFFFFF) bg = 0.0;
+                wave_argmax_lex(bg, bf);
+                if (lane == 0 && pr < n_pairs) {
+                    v.wg[pr] = bg;
+                    v.wf[pr] = bf;
+                }
             }
         }
-        wave_argmax(bg, bf);
-        if (lane == 0) {
-            v.wg[pr] = bg;
-            v.wf[pr] = bf;
+    } else {
+        for (int pr = wv; pr < n_pairs; pr += nwaves) {
+            double bg = 0.0;
+            int bf = 0x7FFFFFFF;
+            for (int ff = lane; ff < F; ff += 64) {
+                const ScanResult &sr = s.scan[(size_t)pr * F + ff];
+                const double gv = sr.gain;
+                const int fv = sr.found;
+                const double q = fv ? gv : -1.0;
+                if (q > bg) {
+                    bg = q;
+                    bf = ff;
+                }
+            }
+            wave_argmax_lex(bg, bf);
+            if (lane == 0) {
+                v.wg[pr] = bg;
+                v.wf[pr] = bf;
+            }
         }
     }
     __syncthreads();
@@ -2016,13 +2178,19 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             e_id = (built == (it.builds_left != 0)) ? it.left_e : it.left_e + 1;
         }
         const ScanResult *base = &s.scan[(size_t)pr * F];
+        const int bf = v.wf[pr];
+        const bool found = bf != 0x7FFFFFFF;
+        // the three results this pair needs, loaded together
         const long long G = base->tot_g, H = base->tot_h, C = base->tot_c;
+        const double fg = base[s_vf].fg, fh = base[s_vf].fh;
+        const ScanResult &qb = base[found ? bf : 0];
+        const int q_bin = qb.bin, q_dl = qb.default_left;
+        const long long q_nl = qb.n_left;
         // leaf value: integer sums are the same on every feature; the fp32
         // path sums the tree's first selected feature serially, as
         // tree._leaf_value does (value_feature = tree_features[0])
         const double value = hp.quantized ? qleaf(G, H, gu, hu, hp.lambda_l1, hp.lambda_l2)
-                                          : -soft_threshold_l1(base[s_vf].fg, hp.lambda_l1) /
-                                                (base[s_vf].fh + hp.lambda_l2);
+                                          : -soft_threshold_l1(fg, hp.lambda_l1) / (fh + hp.lambda_l2);
         ENode *e = &s.enodes[e_id];
         if (root_mode) {
             e->begin = 0;
@@ -2040,16 +2208,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         e->tot_h = H;
         e->tot_c = C;
         e->value = value;
-        const int bf = v.wf[pr];
-        const bool found = bf != 0x7FFFFFFF;
         e->found = found ? 1 : 0;
         if (found) {
-            const ScanResult &q = base[bf];
             e->gain = v.wg[pr];
             e->feature = bf;
-            e->bin = q.bin;
-            e->default_left = q.default_left;
-            e->n_left = q.n_left;
+            e->bin = q_bin;
+            e->default_left = q_dl;
+            e->n_left = q_nl;
         } else {
             e->gain = 0.0;
             e->feature = -1;
@@ -2074,58 +2239,20 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __syncthreads();
     for (int i = tid; i < nl0; i += nthr) v.sg[i] = v.eg[v.sl_e[i]];
     __syncthreads();
-    // ---- 2. replay (wave 0). The frontier lives in LDS; lane l owns slots
-    // l, l + 64, ... and keeps the best (gain, slot) of its own slots in
-    // registers, so a pick is one wave reduction. Every lane writes the same
-    // values to the shared arrays, so each lane reads back its own writes.
+    // ---- 2. replay (wave 0), see replay_wave. Each explored node's
+    // children gains sit beside it (cb = left, gr = right) so a commit costs
+    // one LDS round trip.
+    for (int i = tid; i < ne; i += nthr) {
+        const int le = v.el[i];
+        v.cb[i] = le >= 0 ? v.eg[le] : 0.0;
+        v.gr[i] = le >= 0 ? v.eg[le + 1] : 0.0;
+    }
+    __syncthreads();
     if (tid < 64) {
-        double lbg = 0.0;
-        int lbi = 0x7FFFFFFF;
-        auto own_best = [&](int nslots) {
-            lbg = 0.0;
-            lbi = 0x7FFFFFFF;
-            for (int i = lane; i < nslots; i += 64) {
-                const double gi = v.sg[i];
-                if (gi > lbg) {
-                    lbg = gi;
-                    lbi = i;
-                }
-            }
-        };
-        auto pick = [&](int &bi) {
-            double bg = lbg;
-            bi = lbi;
-            wave_argmax(bg, bi);
-            return bi != 0x7FFFFFFF;
-        };
         int nl = nl0, nn = g.n_nodes, nc = 0, done = 0, x = -1;
-        own_best(nl);
-        for (;;) {
-            int bi;
-            if (nl >= L || !pick(bi)) {
-                done = 1;
-                break;
-            }
-            const int X = v.sl_e[bi];
-            const int le = v.el[X];
-            if (le < 0) {
-                x = X;
-                break;
-            }
-            v.cm_e[nc] = X;
-            v.cm_fid[nc] = v.sl_fid[bi];
-            v.cm_lf[nc] = nn;
-            v.sl_e[bi] = le;
-            v.sl_fid[bi] = nn;
-            v.sg[bi] = v.eg[le];
-            v.sl_e[nl] = le + 1;
-            v.sl_fid[nl] = nn + 1;
-            v.sg[nl] = v.eg[le + 1];
-            if (lane == (bi & 63) || lane == (nl & 63)) own_best(nl + 1);
-            ++nl;
-            nn += 2;
-            ++nc;
-        }
+        if (L <= 256) replay_wave<4>(v, L, nl, nn, nc, done, x);
+        else if (L <= 512) replay_wave<8>(v, L, nl, nn, nc, done, x);
+        else replay_wave<16>(v, L, nl, nn, nc, done, x);
         if (lane == 0) {
             s_nc = nc;
             s_done = done;
@@ -2206,28 +2333,85 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __syncthreads();
     for (int i = tid; i < nl; i += nthr) v.fr[v.sl_e[i]] = 1;
     __syncthreads();
-    for (int i = tid; i < ne; i += nthr) {
-        double b = -1.0;  // outside the region below the frontier, or no split
-        if (v.eg[i] > 0.0) {
-            double m = v.eg[i];
-            int u = i;
-            bool inside = true;
-            while (!v.fr[u]) {
-                u = v.ep[u];
-                if (u < 0) {
-                    inside = false;  // a committed internal node
-                    break;
-                }
-                m = v.eg[u] < m ? v.eg[u] : m;
+    // b by pointer jumping: node i carries the smallest gain on its path up
+    // to (excluding) up[i]; up = -1 once a frontier node was passed
+    // (inside), -2 at the root without one (a committed internal node).
+    // Each round doubles the covered path, so a depth-D tree needs
+    // ceil(log2 D) rounds. Nodes per thread: ne <= e_cap <= 4 x 1024.
+    constexpr int kJ = 4;
+    double jv[kJ];
+    int ju[kJ];
+#pragma unroll
+    for (int k = 0; k < kJ; ++k) {
+        const int i = tid + k * nthr;
+        jv[k] = -1.0;
+        ju[k] = -2;
+        if (i < ne) {
+            jv[k] = v.eg[i];
+            ju[k] = v.fr[i] ? -1 : (v.ep[i] < 0 ? -2 : v.ep[i]);
+            v.cb[i] = jv[k];
+            v.ci[i] = ju[k];
+        }
+    }
+    for (;;) {
+        __syncthreads();
+        double nv[kJ];
+        int nu[kJ];
+        bool more = false;
+#pragma unroll
+        for (int k = 0; k < kJ; ++k) {
+            nv[k] = jv[k];
+            nu[k] = ju[k];
+            if (ju[k] >= 0) {
+                const double pv = v.cb[ju[k]];
+                nv[k] = pv < jv[k] ? pv : jv[k];
+                nu[k] = v.ci[ju[k]];
+                more |= nu[k] >= 0;
             }
-            if (inside) b = m;
         }
-        if (b > 0.0) {
-            // node id, with bit 31 set when the node is expanded
-            const int k = atomicAdd(&s_ncand, 1);
-            v.cb[k] = b;
-            v.ci[k] = i | (v.el[i] >= 0 ? (int)0x80000000 : 0);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kJ; ++k) {
+            const int i = tid + k * nthr;
+            if (ju[k] >= 0) {
+                jv[k] = nv[k];
+                ju[k] = nu[k];
+                v.cb[i] = nv[k];
+                v.ci[i] = nu[k];
+            }
         }
+        if (!__syncthreads_or(more)) break;
+    }
+    // candidates: b > 0 inside the region below the frontier; compacted by
+    // wave ballots (node id, with bit 31 set when the node is expanded)
+    __shared__ int s_wcnt[kPlanThreads / 64 * kJ];
+    int myb[kJ];
+#pragma unroll
+    for (int k = 0; k < kJ; ++k) {
+        const int i = tid + k * nthr;
+        const bool c = i < ne && ju[k] == -1 && v.eg[i] > 0.0 && jv[k] > 0.0;
+        const unsigned long long m = __ballot(c);
+        myb[k] = c ? (int)__popcll(m & ((1ULL << lane) - 1ULL)) : -1;
+        if (lane == 0) s_wcnt[k * nwaves + wv] = __popcll(m);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int a = 0;
+        for (int j = 0; j < kJ * nwaves; ++j) {
+            const int t = s_wcnt[j];
+            s_wcnt[j] = a;
+            a += t;
+        }
+        s_ncand = a;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kJ; ++k) {
+        if (myb[k] < 0) continue;
+        const int i = tid + k * nthr;
+        const int kk = s_wcnt[k * nwaves + wv] + myb[k];
+        v.cb[kk] = jv[k];
+        v.ci[kk] = i | (v.el[i] >= 0 ? (int)0x80000000 : 0);
     }
     __syncthreads();
     const int ncand = s_ncand;
