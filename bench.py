@@ -10,14 +10,17 @@ A "step" is one boosting iteration (one tree). The timed region trains
 --steps trees from scratch on the HBM-resident dataset, bracketed by device
 synchronization (the library syncs before returning). `value` is the
 histogram-build throughput of an instrumented run of the same training (HIP
-events around every growth kernel): the algorithmic bytes are those of the
-committed trees' builds -- the root and the smaller child of every split,
-m rows * (28 + 2) (uint8 bins + int8 g/h pair; row ids, LDS traffic and
-histogram writes not counted) -- and the time is that of every growth
-kernel: accumulation (with the fused row partition), partial merge, sibling
-subtraction, split scan and planning, including speculative expansions the
-best-first replay discarded. `roofline` prices the partition + accumulation
-kernel alone, whose average duration rocprofv3 reports too.
+events around every growth kernel, on the stream they run on): the
+algorithmic bytes of every histogram the run accumulated -- the root and each
+expansion's smaller child, speculative expansions included -- m rows *
+(F + gh) (uint8 bins + the g/h pair: 2 bytes int8, 8 bytes fp32; row ids,
+LDS traffic and partial writes not counted), over the time of the kernels
+that accumulate them (k_hist for the root, k_accum for the children).
+`roofline` prices k_accum alone, whose average duration rocprofv3 reports
+too; `traffic` is its HBM bytes per launch from rocprofv3 PMC counters.
+The conservative figure that charges every growth kernel (partition,
+accumulation, partial merge and scan, planning) against the committed
+trees' builds only is reported as `hist_gbs_committed_over_growth`.
 
 cpu_baseline: the CPU oracle (a C++ restatement of the reference's CPU
 trainer; the reference itself is Mojo and cannot run here) on the first
@@ -143,10 +146,10 @@ def workload_data(name, n_rows):
 
 
 def traffic_per_launch(workload):
-    """HBM bytes per k_part_hist launch measured by rocprofv3 (FETCH_SIZE and
+    """HBM bytes per k_accum launch measured by rocprofv3 (FETCH_SIZE and
     WRITE_SIZE passes over the same workload, calibrated against a plain
     device copy), as committed under profiles/; None when absent."""
-    p = ROOT / "profiles" / f"k_part_hist_{workload}_traffic.json"
+    p = ROOT / "profiles" / f"k_accum_{workload}_traffic.json"
     if not p.exists():
         return None
     return json.loads(p.read_text()).get("traffic_bytes_per_launch")
@@ -314,39 +317,43 @@ def main():
     root_gbs = algo_root / (root_mean_ms * 1e-3) / 1e9
     root_merged_gbs = algo_root / (root_merged_ms * 1e-3) / 1e9
     extra = {}
-    fst = fit.stats
-    if fst["expand_launches"] > 0:
-        extra["expand_bytes_per_launch"] = round(fst["expand_bytes"] / fst["expand_launches"], 1)
     if st:
-        # a histogram build = accumulation (root kernel, or the expansion
-        # kernel that also partitions) + the scan kernel that merges the
-        # block partials, subtracts the sibling, scans and plans; `value`
-        # charges all of it against the committed trees' algorithmic bytes
-        value = st["hist_bytes"] / (st["growth_ms"] * 1e-3) / 1e9
+        # the histograms accumulated (root + every expansion's smaller child)
+        # over the kernels that accumulate them
+        acc_bytes = st["root_bytes"] + st["accum_bytes"]
+        acc_ms = st["root_ms"] + st["accum_ms"]
+        value = acc_bytes / (acc_ms * 1e-3) / 1e9
         launches = max(1.0, st["expand_launches"])
-        kernel_gbs = st["expand_bytes"] / (st["expand_ms"] * 1e-3) / 1e9
-        kernel_avg_ms = st["expand_ms"] / launches
+        kernel_gbs = st["accum_bytes"] / (st["accum_ms"] * 1e-3) / 1e9
+        kernel_avg_ms = st["accum_ms"] / launches
+        part_bytes = st["rows_parted"] * 9.0
         per_tree = 1.0 / max(1, args.steps)
         extra = {
-            "hist_rows_features_per_s": round(st["hist_rows_features"] / (st["growth_ms"] * 1e-3), 1),
+            "hist_rows_features_per_s": round(acc_bytes / (F + GH) * F / (acc_ms * 1e-3), 1),
+            "hist_gbs_committed_over_growth": round(st["hist_bytes"] / (st["growth_ms"] * 1e-3) / 1e9, 2),
             "hist_builds_per_tree": round(st["hist_builds"] * per_tree, 2),
             "growth_ms_per_tree": round(st["growth_ms"] * per_tree, 4),
+            "accumulation_ms_per_tree": round(acc_ms * per_tree, 4),
+            "partition_ms_per_tree": round(st["partition_ms"] * per_tree, 4),
+            "partition_gbs": round(part_bytes / (st["partition_ms"] * 1e-3) / 1e9, 2),
+            "scan_plan_ms_per_tree": round((st["growth_ms"] - st["root_ms"] - st["partition_ms"]
+                                            - st["accum_ms"]) * per_tree, 4),
             "expansion_iterations_per_tree": round(st["iterations"] * per_tree, 2),
-            "expansion_launches_per_tree": round(st["expand_launches"] * per_tree, 2),
             "leaves_expanded_per_tree": round(st["expansions"] * per_tree, 2),
+            "rows_accumulated_per_tree": round(st["rows_built"] * per_tree, 1),
+            "rows_partitioned_per_tree": round(st["rows_parted"] * per_tree, 1),
             "speculative_row_overhead": round(
                 st["rows_built"] / max(1.0, st["hist_bytes"] / (F + GH) - st["root_bytes"] / (F + GH))
                 - 1.0, 4),
-            "expand_kernel_avg_ms": round(kernel_avg_ms, 5),
+            "accum_kernel_avg_ms": round(kernel_avg_ms, 5),
         }
-        note = (f"dominant kernel k_part_hist (partition + smaller-child accumulation), "
-                f"algorithmic bytes per launch = parent rows * 9 (row id in, split bin, row "
-                f"id out) + accumulated rows * (F + {GH}), over its average launch "
-                f"({kernel_avg_ms * 1e3:.1f} us, {int(st['expand_launches'])} launches incl. "
-                f"empty tail launches); root build alone {root_gbs:.0f} GB/s "
-                f"({root_gbs / HBM_PEAK_GBS:.1%})")
+        note = (f"dominant histogram kernel k_accum (smaller-child accumulation from the "
+                f"partitioned row list), algorithmic bytes per launch = accumulated rows * "
+                f"(F + {GH}), over its average launch ({kernel_avg_ms * 1e3:.1f} us, "
+                f"{int(st['expand_launches'])} launches incl. empty tail launches); root build "
+                f"k_hist alone {root_gbs:.0f} GB/s ({root_gbs / HBM_PEAK_GBS:.1%})")
     else:
-        value = root_merged_gbs
+        value = root_gbs
         kernel_gbs = root_gbs
         note = "root build only (instrumented run skipped)"
     out = {

@@ -205,6 +205,7 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     if (p->num_leaves < 1) bad("num_leaves must be positive");
     if (p->num_leaves > 1024)
         unsup("num_leaves above 1024: the planner keeps the explored tree in LDS");
+    if (ds->F >= 0xFFFF) unsup("65535 or more features: the score update packs a node's feature in 16 bits");
     if (p->min_data_in_leaf < 0) bad("min_data_in_leaf must be nonnegative");
     if (!(p->learning_rate > 0.0)) bad("learning_rate must be positive");
     if (!(p->lambda_l2 >= 0.0) || !(p->lambda_l1 >= 0.0)) bad("lambda_l1 and lambda_l2 must be nonnegative");
@@ -704,10 +705,14 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         // expansion launches the previous tree needed: the first group of a
         // tree is that long, later groups kNextGroup
         int est = kFirstGroup;
+        // single-output L2 / binary: the score update of tree t computes the
+        // objective of tree t + 1 in the same pass
+        const bool fuse_objective =
+            K == 1 && (p->objective == MBH_OBJ_BINARY || p->objective == MBH_OBJ_REGRESSION);
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
             if (K > 1 && t % K == 0) HIPX(mb::launch_softmax(s, grid_rows, st));
-            HIPX(mb::launch_objective(s, grid_rows, st));
+            if (!(fuse_objective && t > 0)) HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
             if (s.hp.goss) HIPX(mb::launch_goss(s, st));
             if (timed) HIPX(hipEventRecord(events[2], st));
@@ -762,7 +767,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 t_root += a;
                 t_root_scan += b;
             }
-            HIPX(mb::launch_score(s, grid_rows, st));
+            if (fuse_objective && t + 1 < T) HIPX(mb::launch_score_objective(s, grid_rows, st));
+            else HIPX(mb::launch_score(s, grid_rows, st));
             HIPX(mb::launch_round_end(s, st));
         }
         HIPX(hipStreamSynchronize(st));

@@ -26,6 +26,9 @@ hipError_t launch_accum(const DevState &s, hipStream_t st);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
+// The score update fused with the next round's objective (single-output L2
+// and binary): after it, the next tree skips launch_objective.
+hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_round_end(const DevState &s, hipStream_t st);
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
                                 int tile_f, int n_tiles, int grid, hipStream_t st);

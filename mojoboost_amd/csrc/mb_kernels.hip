@@ -2643,8 +2643,91 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
 // covered too (the traversal route, :1947). A single-leaf tree whose value is
 // below 1e-12 is the reference's stopping condition (:2898-2907) and adds
 // nothing.
+// The finished tree in LDS, one 64-bit word per node: feature (16 bits,
+// 0xFFFF for a leaf), threshold bin (8), missing bin + 1 (9), default_left
+// (1), left child (16); the right child is always left + 1 (node ids are
+// given in pairs). One LDS read per level of a walk.
+struct PackedTree {
+    const unsigned long long *node;
+    const double *value;
+};
+
+__device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsigned char *smem) {
+    unsigned long long *pn = (unsigned long long *)smem;
+    double *vals = (double *)(pn + s.max_nodes);
+    const int n_nodes = s.t_meta[0];
+    for (int i = threadIdx.x; i < n_nodes; i += blockDim.x) {
+        const int f = s.t_feature[i];
+        unsigned long long w;
+        if (f < 0) {
+            w = 0xFFFFULL;
+        } else {
+            w = (unsigned long long)(uint32_t)f | ((unsigned long long)(s.t_threshold[i] & 255) << 16) |
+                ((unsigned long long)((s.t_missing_bin[i] + 1) & 511) << 24) |
+                ((unsigned long long)(s.t_default_left[i] ? 1 : 0) << 33) |
+                ((unsigned long long)(s.t_left[i] & 0xFFFF) << 34);
+        }
+        pn[i] = w;
+        vals[i] = s.t_value[i];
+    }
+    __syncthreads();
+    return PackedTree{pn, vals};
+}
+
+// Leaf of a row: bin(f) gives the row's bin of feature f. The missing bin
+// follows default_left, otherwise bin <= threshold goes left
+// (tree.goes_left, src/mojotrees/tree.mojo:483-505). Children always have
+// larger ids than their parent, so a walk ends within n_nodes steps.
+template <class BinOf>
+__device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, BinOf bin) {
+    int node = 0;
+    for (int d = 0; d < n_nodes; ++d) {
+        const unsigned long long w = t.node[node];
+        const int f = (int)(w & 0xFFFFULL);
+        if (f == 0xFFFF) break;
+        const int b = bin(f);
+        const int thr = (int)((w >> 16) & 255ULL);
+        const int mbin = (int)((w >> 24) & 511ULL) - 1;
+        const bool dl = (w >> 33) & 1ULL;
+        const int left = (int)((w >> 34) & 0xFFFFULL);
+        const bool go_left = (b == mbin) ? dl : (b <= thr);
+        node = go_left ? left : left + 1;
+        if ((unsigned)node >= (unsigned)n_nodes) node = 0;
+    }
+    return node;
+}
+
+// Two independent walks advanced together, so each level's LDS round trips
+// of one row overlap the other's.
+template <class BinA, class BinB>
+__device__ __forceinline__ void walk_packed2(const PackedTree &t, int n_nodes, BinA bin_a, BinB bin_b, int &na,
+                                             int &nb) {
+    int a = 0, b = 0;
+    bool da = false, db = false;
+    for (int d = 0; d < n_nodes && !(da && db); ++d) {
+        const unsigned long long wa = t.node[a], wb = t.node[b];
+        const int fa = (int)(wa & 0xFFFFULL), fb = (int)(wb & 0xFFFFULL);
+        da |= fa == 0xFFFF;
+        db |= fb == 0xFFFF;
+        const int ba = da ? 0 : bin_a(fa), bb = db ? 0 : bin_b(fb);
+        auto next = [](unsigned long long w, int bin, int node, int n) {
+            const int thr = (int)((w >> 16) & 255ULL);
+            const int mbin = (int)((w >> 24) & 511ULL) - 1;
+            const bool dl = (w >> 33) & 1ULL;
+            const int left = (int)((w >> 34) & 0xFFFFULL);
+            const bool go_left = (bin == mbin) ? dl : (bin <= thr);
+            const int c = go_left ? left : left + 1;
+            return (unsigned)c < (unsigned)n ? c : 0;
+        };
+        if (!da) a = next(wa, ba, a, n_nodes);
+        if (!db) b = next(wb, bb, b, n_nodes);
+    }
+    na = a;
+    nb = b;
+}
+
 __global__ __launch_bounds__(256) void k_score(DevState s) {
-    extern __shared__ int32_t tnode[];  // 5 ints per node
+    extern __shared__ unsigned char score_smem[];
     const int n_nodes = s.t_meta[0];
     const int n_leaves = s.t_meta[1];
     if (s.round->stopped) return;
@@ -2652,45 +2735,156 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     // round adds every class tree and decides afterwards
     // (boosting.mojo:2898-2907, :3876-4165)
     if (s.hp.num_class == 1 && n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
-    double *vals = (double *)(tnode + 5 * s.max_nodes + (s.max_nodes & 1));
-    for (int i = threadIdx.x; i < n_nodes; i += blockDim.x) {
-        tnode[5 * i + 0] = s.t_feature[i];
-        tnode[5 * i + 1] = s.t_threshold[i];
-        tnode[5 * i + 2] = s.t_left[i];
-        tnode[5 * i + 3] = s.t_right[i];
-        tnode[5 * i + 4] = s.t_missing_bin[i] * 2 + (s.t_default_left[i] ? 1 : 0);
-        vals[i] = s.t_value[i];
-    }
-    __syncthreads();
+    const PackedTree tree = load_packed_tree(s, score_smem);
     const double lr = s.hp.learning_rate;
     const int K = s.hp.num_class;
     const int k = s.round->class_k;
     const int rec = s.rec_bytes, tf = s.tile_f;
-    const bool tiled = s.n_tiles > 1;
     const size_t tile_bytes = (size_t)s.n * rec;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
         const uint8_t *rb = s.records + r * rec;
-        int node = 0;
-        // children always have larger ids than their parent, so a walk ends
-        // within n_nodes steps
-        for (int d = 0; d < n_nodes && tnode[5 * node] >= 0; ++d) {
-            const int f = tnode[5 * node];
-            int b;
-            if (tiled) {
-                const int t = f / tf;
-                b = rb[(size_t)t * tile_bytes + (f - t * tf)];
-            } else {
-                b = rb[f];
-            }
-            const int md = tnode[5 * node + 4];
-            const int mbin = md >> 1;  // arithmetic shift keeps -1
-            const bool left = (b == mbin) ? (md & 1) : (b <= tnode[5 * node + 1]);
-            node = left ? tnode[5 * node + 2] : tnode[5 * node + 3];
-            if ((unsigned)node >= (unsigned)n_nodes) node = 0;
-        }
+        const int node = walk_packed(tree, n_nodes, [&](int f) {
+            const int t = f / tf;
+            return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
+        });
         double *slot = s.raw + r * K + k;
-        *slot = fma(lr, vals[node], *slot);
+        *slot = fma(lr, tree.value[node], *slot);
+    }
+}
+
+// Score update of the finished tree fused with the next round's objective,
+// for single-output L2 and binary objectives: per row, raw += lr x leaf
+// value (k_score) and then the next round's g, h from the updated raw score
+// and max |g|, |h| over the next round's bag (k_objective), so raw scores are
+// read once and written once per round. Training that stops at this tree
+// never reads these g, h. With one feature tile of at most 32 bytes the
+// row's record is loaded whole (one or two 16-byte loads) into the thread's
+// LDS slot and the walk reads its bins there.
+__global__ __launch_bounds__(256) void k_score_objective(DevState s) {
+    extern __shared__ unsigned char score_smem[];
+    __shared__ float red_g[4], red_h[4];
+    __shared__ uint4 srec[256 * 4];     // each thread's two records (at most 32 bytes each)
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const HyperParams &hp = s.hp;
+    const int n_nodes = s.t_meta[0];
+    const bool add = !(s.t_meta[1] == 1 && fabs(s.t_value[0]) < 1e-12);
+    const PackedTree tree = load_packed_tree(s, score_smem);
+    const double lr = hp.learning_rate;
+    const int rec = s.rec_bytes;
+    const bool in_regs = s.n_tiles == 1 && rec <= 32;
+    const int np = 1 - rd.parity;  // the next tree's magnitude-stats pair
+    const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round + 1) : 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) s.cursor[0] = 0;  // the next root row count
+    float mg = 0.0f, mh = 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    // the row's next-round objective and the bag's magnitude stats
+    auto objective = [&](int64_t r, double raw, double y) {
+        float g, h;
+        if (hp.objective == kObjBinary) {
+            const double p = sigmoid(raw);
+            g = (float)(p - y);
+            double hh = p * (1.0 - p);
+            if (hh < 1e-16) hh = 1e-16;
+            h = (float)hh;
+        } else {
+            g = (float)(raw - y);
+            h = 1.0f;
+        }
+        s.grad[r] = g;
+        s.hess[r] = h;
+        const float ag = fabsf(g), ah = fabsf(h);
+        const bool sel = !hp.bagging || in_bag(hp, bstream, r);
+        if (sel && isfinite(ag) && isfinite(ah)) {
+            mg = fmaxf(mg, ag);
+            mh = fmaxf(mh, ah);
+        }
+    };
+    const int64_t r0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (in_regs) {
+        // one feature tile of at most 32 bytes: the next row's record, raw
+        // score and label are loaded (unconditionally, the last row again
+        // past the end) while the current row walks the tree
+        const uint4 *R = (const uint4 *)s.records;
+        const int per = rec / 16;  // 1 or 2 uint4 per record
+        uint8_t *mine = (uint8_t *)&srec[threadIdx.x * 2];
+        auto fetch = [&](int64_t r, uint4 &a, uint4 &b, double &raw, double &y) {
+            const int64_t q = r < s.n ? r : s.n - 1;
+            a = R[q * per];
+            b = R[q * per + per - 1];
+            raw = s.raw[q];
+            y = s.labels[q];
+        };
+        // two rows per step (r and r + stride), walked together
+        uint8_t *mine2 = (uint8_t *)&srec[256 * 2 + threadIdx.x * 2];
+        uint4 ca, cb, ca2, cb2;
+        double craw, cy, craw2, cy2;
+        fetch(r0, ca, cb, craw, cy);
+        fetch(r0 + stride, ca2, cb2, craw2, cy2);
+        for (int64_t r = r0; r < s.n; r += 2 * stride) {
+            uint4 na, nb, na2, nb2;
+            double nraw, ny, nraw2, ny2;
+            fetch(r + 2 * stride, na, nb, nraw, ny);
+            fetch(r + 3 * stride, na2, nb2, nraw2, ny2);
+            const int64_t r2 = r + stride;
+            double raw = craw, raw2 = craw2;
+            if (add) {
+                srec[threadIdx.x * 2] = ca;
+                srec[threadIdx.x * 2 + 1] = cb;  // this thread's own slots: no barrier needed
+                srec[256 * 2 + threadIdx.x * 2] = ca2;
+                srec[256 * 2 + threadIdx.x * 2 + 1] = cb2;
+                int n1, n2;
+                walk_packed2(tree, n_nodes, [&](int f) { return (int)mine[f]; },
+                             [&](int f) { return (int)mine2[f]; }, n1, n2);
+                raw = fma(lr, tree.value[n1], raw);
+                s.raw[r] = raw;
+                raw2 = fma(lr, tree.value[n2], raw2);
+                if (r2 < s.n) s.raw[r2] = raw2;
+            }
+            objective(r, raw, cy);
+            if (r2 < s.n) objective(r2, raw2, cy2);
+            ca = na;
+            cb = nb;
+            craw = nraw;
+            cy = ny;
+            ca2 = na2;
+            cb2 = nb2;
+            craw2 = nraw2;
+            cy2 = ny2;
+        }
+    } else {
+        const int tf = s.tile_f;
+        const size_t tile_bytes = (size_t)s.n * rec;
+        for (int64_t r = r0; r < s.n; r += stride) {
+            double raw = s.raw[r];
+            if (add) {
+                const uint8_t *rb = s.records + r * rec;
+                const int node = walk_packed(tree, n_nodes, [&](int f) {
+                    const int t = f / tf;
+                    return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
+                });
+                raw = fma(lr, tree.value[node], raw);
+                s.raw[r] = raw;
+            }
+            objective(r, raw, s.labels[r]);
+        }
+    }
+    mg = wave_max(mg);
+    mh = wave_max(mh);
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 0) {
+        red_g[w] = mg;
+        red_h[w] = mh;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
+            mg = fmaxf(mg, red_g[i]);
+            mh = fmaxf(mh, red_h[i]);
+        }
+        atomicMax(&s.stats[np * 2 + 0], __float_as_uint(mg));
+        atomicMax(&s.stats[np * 2 + 1], __float_as_uint(mh));
     }
 }
 
@@ -2869,9 +3063,7 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
-size_t score_lds_bytes(const DevState &s) {
-    return (size_t)(5 * s.max_nodes + (s.max_nodes & 1)) * 4 + (size_t)s.max_nodes * 8;
-}
+size_t score_lds_bytes(const DevState &s) { return (size_t)s.max_nodes * 16; }
 size_t hist_lds_bytes(const DevState &s) {
     return s.hp.quantized ? QAcc::lds_bytes(s.tile_f, s.lds_stride) : FAcc::lds_bytes(s.tile_f, s.lds_stride);
 }
@@ -2914,6 +3106,7 @@ hipError_t prepare_kernels(const DevState &s) {
     MB_SET_LDS(k_plan, plan_lds_bytes(s));
     MB_SET_LDS(k_goss_walk, (size_t)2 * kGossTile * sizeof(int32_t));
     MB_SET_LDS(k_score, score_lds_bytes(s));
+    MB_SET_LDS(k_score_objective, score_lds_bytes(s));
     return hipSuccess;
 }
 template <class Acc>
@@ -2966,6 +3159,10 @@ hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st) {
 }
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_score, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
+    return hipGetLastError();
+}
+hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_score_objective, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
     return hipGetLastError();
 }
 hipError_t launch_round_end(const DevState &s, hipStream_t st) {
