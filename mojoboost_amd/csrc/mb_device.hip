@@ -390,7 +390,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.round = dalloc<mb::Round>(1, run.owned);
     s.rows0 = dalloc<int32_t>(ds->n, run.owned);
     s.rows1 = dalloc<int32_t>(ds->n, run.owned);
-    const int max_exp = 2 * L - 1;
+    const int max_exp = std::min(4 * L - 1, 2047);
     s.max_exp = max_exp;
     s.e_cap = 1 + 2 * max_exp;
     if (quantized) s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
