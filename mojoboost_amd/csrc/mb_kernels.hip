@@ -1880,7 +1880,14 @@ constexpr int kPlanThreads = 1024;
 
 // LDS layout of the planner (byte offsets), shared by the host's size query
 // and the kernel.
+// The fields of a selected leaf's explored node the batch setup needs.
+struct SelNode {
+    int64_t begin, end, n_left;
+    int32_t buf, hist, depth, feature, bin, default_left;
+};
+
 struct PlanLayout {
+    size_t sn, mbin;
     size_t wg, eg, sg, cb, kr, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
     size_t total;
 };
@@ -1915,11 +1922,15 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
     p.qcnt = take((size_t)4 * K, 4);
     p.qoff = take((size_t)4 * (K + 1), 4);
     p.it = take(sizeof(Item) * K, 16);
+    p.sn = take(sizeof(SelNode) * K, 16);    // the selected leaves' nodes
+    p.mbin = take((size_t)4 * F, 4);         // missing bin per feature
     p.total = o;
     return p;
 }
 
 struct PlanView {
+    SelNode *sn;
+    int32_t *mbin;
     double *wg, *eg, *sg, *cb, *gr;
     int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff, *qcnt, *qoff;
     Item *it;
@@ -1949,6 +1960,8 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.qcnt = (int32_t *)(smem + p.qcnt);
     v.qoff = (int32_t *)(smem + p.qoff);
     v.it = (Item *)(smem + p.it);
+    v.sn = (SelNode *)(smem + p.sn);
+    v.mbin = (int32_t *)(smem + p.mbin);
     return v;
 }
 
@@ -2056,7 +2069,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
     __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x, s_vf;
-    __shared__ unsigned long long s_rows_built, s_rows_parted, s_rows_total, s_built_total;
+    __shared__ unsigned long long s_rows_built, s_rows_parted;
+    __shared__ long long s_chunk;
     __shared__ int s_total_p;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
@@ -2107,6 +2121,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     const int n_pairs = root_mode ? 1 : 2 * n_items;
     if (!root_mode)
         for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
+    for (int f = tid; f < F; f += nthr) v.mbin[f] = s.missing_bin[f];
     __syncthreads();
     const int ne = g.n_explored, nl0 = g.n_leaves;
     for (int i = tid; i < ne; i += nthr) {
@@ -2274,7 +2289,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.t_left[fx] = lf;
         s.t_right[fx] = lf + 1;
         s.t_default_left[fx] = e->default_left;
-        s.t_missing_bin[fx] = s.missing_bin[feat];
+        s.t_missing_bin[fx] = v.mbin[feat];
         s.t_gain[fx] = e->gain;
         s.t_value[lf] = s.enodes[le].value;
         s.t_count[lf] = (double)s.enodes[le].tot_c;
@@ -2466,44 +2481,55 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // mean fewer partials to store and merge; a batch never needs more than
     // n / hist_chunk_min + nsel of them). Partition: chunks of kPartChunk
     // parent rows (one output reservation each).
-    if (tid == 0) {
-        s_rows_total = 0;
-        s_built_total = 0;
+    // the selected leaves' nodes, one memory round trip
+    if (tid < nsel) {
+        const ENode *e = &s.enodes[v.sel_e[tid]];
+        SelNode sn;
+        sn.begin = e->begin;
+        sn.end = e->end;
+        sn.n_left = e->n_left;
+        sn.buf = e->buf;
+        sn.hist = e->hist;
+        sn.depth = e->depth;
+        sn.feature = e->feature;
+        sn.bin = e->bin;
+        sn.default_left = e->default_left;
+        v.sn[tid] = sn;
     }
     __syncthreads();
-    for (int jj = tid; jj < nsel; jj += nthr) {
-        const ENode *e = &s.enodes[v.sel_e[jj]];
-        const int64_t m = e->end - e->begin, nl = e->n_left;
-        atomicAdd(&s_rows_total, (unsigned long long)m);
-        atomicAdd(&s_built_total, (unsigned long long)(nl <= m - nl ? nl : m - nl));
-    }
-    __syncthreads();
-    int64_t chunk = ((int64_t)s_built_total + s.pb_launch - 1) / s.pb_launch;
-    if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
-    if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
-    const int64_t chunk_p = kPartChunk;
-    for (int jj = tid; jj < nsel; jj += nthr) {
-        const ENode *e = &s.enodes[v.sel_e[jj]];
-        const int64_t m = e->end - e->begin, nl = e->n_left;
-        const int64_t mb = nl <= m - nl ? nl : m - nl;
-        v.pcnt[jj] = (int)((mb + chunk - 1) / chunk);
-        v.qcnt[jj] = (int)((m + chunk_p - 1) / chunk_p);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int a = 0, c = 0;
-        for (int jj = 0; jj < nsel; ++jj) {
-            v.poff[jj] = a;
-            a += v.pcnt[jj];
-            v.qoff[jj] = c;
-            c += v.qcnt[jj];
+    if (tid < 64) {  // wave 0: totals, chunks, task counts and their prefixes (nsel <= kmax <= 64)
+        long long m = 0, mb = 0;
+        if (lane < nsel) {
+            const SelNode &sn = v.sn[lane];
+            m = sn.end - sn.begin;
+            mb = sn.n_left <= m - sn.n_left ? sn.n_left : m - sn.n_left;
         }
-        v.poff[nsel] = a;
-        v.qoff[nsel] = c;
-        s_total = a;
-        s_total_p = c;
+        const long long rows_total = wave_sum_ll(m), built_total = wave_sum_ll(mb);
+        int64_t chunk = (built_total + s.pb_launch - 1) / s.pb_launch;
+        if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
+        if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
+        const long long pc = lane < nsel ? (mb + chunk - 1) / chunk : 0;
+        const long long qc = lane < nsel ? (m + kPartChunk - 1) / kPartChunk : 0;
+        const long long pi = wave_incl_scan(pc), qi = wave_incl_scan(qc);
+        if (lane < nsel) {
+            v.pcnt[lane] = (int)pc;
+            v.qcnt[lane] = (int)qc;
+            v.poff[lane] = (int)(pi - pc);
+            v.qoff[lane] = (int)(qi - qc);
+        }
+        if (lane == 63) {
+            v.poff[nsel] = (int)pi;
+            v.qoff[nsel] = (int)qi;
+            s_total = (int)pi;
+            s_total_p = (int)qi;
+            s_chunk = chunk;
+            s_rows_parted = (unsigned long long)rows_total;
+            s_rows_built = (unsigned long long)built_total;
+        }
     }
     __syncthreads();
+    const int64_t chunk = s_chunk;
+    const int64_t chunk_p = kPartChunk;
     const int total = s_total, total_p = s_total_p;
     if (total > s.pb_grid || total_p > s.part_grid) {  // the leaves of a batch are disjoint, so never
         finish(4);
@@ -2512,9 +2538,10 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     for (int jj = tid; jj < nsel; jj += nthr) {
         const int Xs = v.sel_e[jj];
         ENode *e = &s.enodes[Xs];
-        const int64_t b0 = e->begin, e0 = e->end, nlft = e->n_left;
+        const SelNode &sn = v.sn[jj];
+        const int64_t b0 = sn.begin, e0 = sn.end, nlft = sn.n_left;
         const int64_t m = e0 - b0;
-        const int ebuf = e->buf, ehist = e->hist, edep = e->depth;
+        const int ebuf = sn.buf, ehist = sn.hist, edep = sn.depth;
         const bool bl = nlft <= m - nlft;
         const int le = ne + 2 * jj, hb = g.n_hist + jj;
         Item it;
@@ -2566,8 +2593,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.e_left[Xs] = le;
         s.cursor[2 + 2 * jj] = 0;
         s.cursor[3 + 2 * jj] = 0;
-        atomicAdd(&s_rows_built, (unsigned long long)(bl ? nlft : m - nlft));
-        atomicAdd(&s_rows_parted, (unsigned long long)m);
     }
     __syncthreads();
     // partition descriptors
@@ -2579,7 +2604,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             else hi = mid - 1;
         }
         const Item &it = v.it[lo];
-        const ENode &pe = s.enodes[it.parent_e];
+        const SelNode &pe = v.sn[lo];  // the parent is the selected leaf itself
         const int64_t m = it.end - it.begin;
         PbDesc d;
         d.begin = it.begin;
@@ -2592,7 +2617,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         d.feature = pe.feature;
         d.bin = pe.bin;
         d.default_left = pe.default_left;
-        d.missing_bin = s.missing_bin[pe.feature];
+        d.missing_bin = v.mbin[pe.feature];
         d.builds_left = it.builds_left;
         d.pad_ = 0;
         s.pb_desc[b] = d;
