@@ -105,6 +105,23 @@ __device__ __forceinline__ unsigned wave_min_u32(unsigned x) {
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
+// Sum of a 32-bit value over the 64 lanes, the same DPP steps as
+// wave_max_u32 but with lanes a control does not cover reading 0 (the
+// identity of the sum), returned wave-uniform.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned dpp0_u32(unsigned x) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ unsigned wave_add_u32(unsigned x) {
+    x += dpp0_u32<0xB1, 0xF>(x);
+    x += dpp0_u32<0x4E, 0xF>(x);
+    x += dpp0_u32<0x141, 0xF>(x);
+    x += dpp0_u32<0x140, 0xF>(x);
+    x += dpp0_u32<0x142, 0xA>(x);
+    x += dpp0_u32<0x143, 0xC>(x);
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 // (gain, order) argmax across the wave, result on every lane: larger gain
 // wins, equal gains go to the smaller order, so the result is the first
 // maximum in scan order. Gains must be >= 0 (a lane with nothing to offer
@@ -1965,22 +1982,57 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     return v;
 }
 
+// Maximum of a 64-bit unsigned value over the 64 lanes (every lane active),
+// returned wave-uniform: the DPP steps of wave_max_u32 on both halves, one
+// 64-bit compare per step.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned long long dpp_max_u64_step(unsigned long long x) {
+    const unsigned long long o = ((unsigned long long)dpp_u32<CTRL, ROW_MASK>((unsigned)(x >> 32)) << 32) |
+                                 dpp_u32<CTRL, ROW_MASK>((unsigned)x);
+    return o > x ? o : x;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+    x = dpp_max_u64_step<0xB1, 0xF>(x);
+    x = dpp_max_u64_step<0x4E, 0xF>(x);
+    x = dpp_max_u64_step<0x141, 0xF>(x);
+    x = dpp_max_u64_step<0x140, 0xF>(x);
+    x = dpp_max_u64_step<0x142, 0xA>(x);
+    x = dpp_max_u64_step<0x143, 0xC>(x);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(x >> 32), 63);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 63);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ double readlane_f64(double d, int l) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(d);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // Best-first replay by one wave (tree.grow_tree_leaves_profiled with
 // growth_policy.GrowthSchedule.next_leaf: the frontier slot of largest gain
 // splits next, lowest slot on ties, gain > 0, until num_leaves). The frontier
 // lives in registers: lane l holds slots l, l + 64, ... (QS of them: gain,
-// explored node, node id) and its own best (gain, slot), so a pick is one
-// wave argmax, and a commit reads the picked node's children (one LDS round
-// trip) and updates the two slots it touches -- the left child keeps the
-// parent's slot, the right one takes slot n_leaves; node ids left = n_nodes,
-// right = n_nodes + 1. The replay stops at a pick whose leaf has not been
-// expanded yet (x) or when the tree is complete (done).
+// explored node, node id, and the node's children -- left child id and both
+// children's gains) and its own best (gain, slot). A pick is the wave
+// maximum of the lanes' best gains as 64-bit patterns (non-negative
+// binary64 values order like their bits); a ballot finds the lane holding
+// it, and only when several lanes hold exactly that gain does a wave
+// minimum pick the lowest slot among them. A commit updates the two slots
+// it touches -- the left child keeps the parent's slot, the right one takes
+// slot n_leaves; node ids left = n_nodes, right = n_nodes + 1 -- and the
+// LDS loads of the new slots' children complete behind the next pick. The
+// replay stops at a pick whose leaf has not been expanded yet (x) or when
+// the tree is complete (done).
 template <int QS>
 __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &done, int &x) {
+    constexpr bool kRegKids = QS <= 4;  // the children in registers fit the budget of a 1024-thread block
+    constexpr int QK = kRegKids ? QS : 1;
     const int lane = lane_id();
     const int nl0 = nl;
-    double sg[QS];
-    int se[QS], sf[QS];
+    double sg[QS], cl[QK], cr[QK];
+    int se[QS], sf[QS], sc[QK];
 #pragma unroll
     for (int q = 0; q < QS; ++q) {
         const int slot = lane + 64 * q;
@@ -1988,6 +2040,12 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
         sg[q] = in ? v.sg[slot] : 0.0;  // 0 is never picked (gain must be > 0)
         se[q] = in ? v.sl_e[slot] : -1;
         sf[q] = in ? v.sl_fid[slot] : -1;
+        if constexpr (kRegKids) {
+            const int e = in ? se[q] : 0;
+            sc[q] = in ? v.el[e] : -1;
+            cl[q] = v.cb[e];
+            cr[q] = v.gr[e];
+        }
     }
     double lbg;
     int lbi;
@@ -2002,33 +2060,75 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
             }
     };
     local_best();
+    // children of the two slots the last commit wrote, still to be placed
+    int pq0 = -1, pl0 = 0, pq1 = -1, pl1 = 0, pc0 = -1, pc1 = -1;
+    double pgl0 = 0.0, pgr0 = 0.0, pgl1 = 0.0, pgr1 = 0.0;
     for (;;) {
         if (nl >= L) {
             done = 1;
             break;
         }
-        double bg = lbg;
-        int bi = lbi;
-        wave_argmax_lex(bg, bi);
-        if (bi == 0x7FFFFFFF) {
+        const unsigned long long mine = (unsigned long long)__double_as_longlong(lbg);
+        const unsigned long long m = wave_max_u64(mine);
+#pragma unroll
+        for (int qq = 0; qq < QK; ++qq) {
+            if (lane == pl0 && qq == pq0) {
+                sc[qq] = pc0;
+                cl[qq] = pgl0;
+                cr[qq] = pgr0;
+            }
+            if (lane == pl1 && qq == pq1) {
+                sc[qq] = pc1;
+                cl[qq] = pgl1;
+                cr[qq] = pgr1;
+            }
+        }
+        if (m == 0ULL) {  // no slot with a positive gain
             done = 1;
             break;
         }
+        const unsigned long long tie = __ballot(mine == m);
+        int bi;
+        if ((tie & (tie - 1ULL)) == 0ULL) bi = __builtin_amdgcn_readlane(lbi, (int)__builtin_ctzll(tie));
+        else bi = (int)wave_min_u32(mine == m ? (unsigned)lbi : 0xFFFFFFFFu);
         const int q = bi >> 6, ol = bi & 63;
-        int xe = se[0], xf = sf[0];
+        int xe = se[0], xf = sf[0], xc = sc[0];
+        double xl = cl[0], xr = cr[0];
 #pragma unroll
         for (int qq = 1; qq < QS; ++qq)
             if (qq == q) {
                 xe = se[qq];
                 xf = sf[qq];
+                if constexpr (kRegKids) {
+                    xc = sc[qq];
+                    xl = cl[qq];
+                    xr = cr[qq];
+                }
             }
         const int X = __builtin_amdgcn_readlane(xe, ol);
         const int fid = __builtin_amdgcn_readlane(xf, ol);
-        const int le = v.el[X];
-        const double gl = v.cb[X], gr = v.gr[X];
+        int le;
+        double gl, gr;
+        if constexpr (kRegKids) {
+            le = __builtin_amdgcn_readlane(xc, ol);
+            gl = readlane_f64(xl, ol);
+            gr = readlane_f64(xr, ol);
+        } else {
+            le = v.el[X];
+            gl = v.cb[X];
+            gr = v.gr[X];
+        }
         if (le < 0) {
             x = X;
             break;
+        }
+        if constexpr (kRegKids) {  // the children's own children, for the two slots written below
+            pc0 = v.el[le];
+            pgl0 = v.cb[le];
+            pgr0 = v.gr[le];
+            pc1 = v.el[le + 1];
+            pgl1 = v.cb[le + 1];
+            pgr1 = v.gr[le + 1];
         }
         if (lane == 0) {
             v.cm_e[nc] = X;
@@ -2049,6 +2149,10 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
                 sf[qq] = nn + 1;
             }
         }
+        pq0 = q;
+        pl0 = ol;
+        pq1 = q2;
+        pl1 = ol2;
         local_best();
         ++nl;
         nn += 2;
@@ -2397,27 +2501,40 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
         if (!__syncthreads_or(more)) break;
     }
-    // candidates: b > 0 inside the region below the frontier; compacted by
-    // wave ballots (node id, with bit 31 set when the node is expanded)
-    __shared__ int s_wcnt[kPlanThreads / 64 * kJ];
-    int myb[kJ];
+    // candidates: b > 0 inside the region below the frontier, compacted by
+    // wave ballots into (cb, ci): b and the node id, bit 31 set when the
+    // node is expanded; the pending (unexpanded) ones are also listed, by
+    // their candidate index, in fr (free once the jump pointers are done).
+    // The kJ x nwaves ballot counts are scanned by wave 0 in one pass.
+    static_assert(kPlanThreads / 64 * kJ == 64, "one wave scans the ballot counts");
+    __shared__ int s_wcnt[64], s_pcnt[64];
+    __shared__ int s_npend;
+    int myb[kJ], myp[kJ];
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
         const int i = tid + k * nthr;
         const bool c = i < ne && ju[k] == -1 && v.eg[i] > 0.0 && jv[k] > 0.0;
-        const unsigned long long m = __ballot(c);
-        myb[k] = c ? (int)__popcll(m & ((1ULL << lane) - 1ULL)) : -1;
-        if (lane == 0) s_wcnt[k * nwaves + wv] = __popcll(m);
+        const bool pend = c && v.el[i] < 0;
+        const unsigned long long m = __ballot(c), mp = __ballot(pend);
+        const unsigned long long below = (1ULL << lane) - 1ULL;
+        myb[k] = c ? (int)__popcll(m & below) : -1;
+        myp[k] = pend ? (int)__popcll(mp & below) : -1;
+        if (lane == 0) {
+            s_wcnt[k * nwaves + wv] = __popcll(m);
+            s_pcnt[k * nwaves + wv] = __popcll(mp);
+        }
     }
     __syncthreads();
-    if (tid == 0) {
-        int a = 0;
-        for (int j = 0; j < kJ * nwaves; ++j) {
-            const int t = s_wcnt[j];
-            s_wcnt[j] = a;
-            a += t;
+    if (tid < 64) {
+        const int a = s_wcnt[lane], b = s_pcnt[lane];
+        const int ia = (int)wave_incl_scan((long long)a), ib = (int)wave_incl_scan((long long)b);
+        s_wcnt[lane] = ia - a;
+        s_pcnt[lane] = ib - b;
+        if (lane == 63) {
+            s_ncand = ia;
+            s_npend = ib;
+            s_nsel = 0;
         }
-        s_ncand = a;
     }
     __syncthreads();
 #pragma unroll
@@ -2426,42 +2543,73 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const int i = tid + k * nthr;
         const int kk = s_wcnt[k * nwaves + wv] + myb[k];
         v.cb[kk] = jv[k];
-        v.ci[kk] = i | (v.el[i] >= 0 ? (int)0x80000000 : 0);
+        v.ci[kk] = i | (myp[k] < 0 ? (int)0x80000000 : 0);
+        if (myp[k] >= 0) v.fr[s_pcnt[k * nwaves + wv] + myp[k]] = kk;
     }
     __syncthreads();
-    const int ncand = s_ncand;
-    if (tid == 0) s_nsel = 0;
-    __syncthreads();
-    for (int k = tid; k < ncand; k += nthr) {
-        const double bk = v.cb[k];
-        const int ck = v.ci[k];
-        if (ck < 0) continue;  // expanded: visited, not selected
-        int rank_all = 0, rank_pend = 0;
-#pragma unroll 8
-        for (int q = 0; q < ncand; ++q) {
-            const double bq = v.cb[q];
-            const int cq = v.ci[q];
-            const int iq = cq & 0x7FFFFFFF;
-            const int before = (bq > bk || (bq == bk && iq < ck)) ? 1 : 0;
-            rank_all += before;
-            rank_pend += before & (cq >= 0 ? 1 : 0);
+    const int ncand = s_ncand, npend = s_npend;
+    // A pending candidate joins the batch when fewer than r candidates and
+    // fewer than cap pending ones come before it in (b descending, node id
+    // ascending) order; its rank among the pending ones is its batch slot.
+    // One wave ranks two pending candidates at a time, its lanes striding
+    // over all candidates with four independent loads in flight.
+    auto before = [](double bq, int iq, double bk, int ik) -> unsigned {
+        return (bq > bk || (bq == bk && iq < ik)) ? 1u : 0u;
+    };
+    for (int p = 2 * wv; p < npend; p += 2 * nwaves) {
+        const bool two = p + 1 < npend;
+        const int ka = v.fr[p], kb = v.fr[two ? p + 1 : p];
+        const double ba = v.cb[ka], bb = v.cb[kb];
+        const int ca = v.ci[ka], cb = v.ci[kb];
+        unsigned raa = 0, rpa = 0, rab = 0, rpb = 0;
+        for (int q0 = lane; q0 < ncand; q0 += 256) {
+            double bq[4];
+            int cq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + 64 * u;
+                const int qq = q < ncand ? q : q0;
+                bq[u] = v.cb[qq];
+                cq[u] = v.ci[qq];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned in = q0 + 64 * u < ncand ? 1u : 0u;
+                const int iq = cq[u] & 0x7FFFFFFF;
+                const unsigned pq = cq[u] >= 0 ? 1u : 0u;
+                const unsigned xa = in & before(bq[u], iq, ba, ca);
+                const unsigned xb = in & before(bq[u], iq, bb, cb);
+                raa += xa;
+                rpa += xa & pq;
+                rab += xb;
+                rpb += xb & pq;
+            }
         }
-        if (rank_all < r && rank_pend < cap) {
-            v.sel_e[rank_pend] = ck;
-            atomicAdd(&s_nsel, 1);
+        raa = wave_add_u32(raa);
+        rpa = wave_add_u32(rpa);
+        rab = wave_add_u32(rab);
+        rpb = wave_add_u32(rpb);
+        if (lane == 0) {
+            if ((int)raa < r && (int)rpa < cap) {
+                v.sel_e[rpa] = ca;
+                atomicAdd(&s_nsel, 1);
+            }
+            if (two && (int)rab < r && (int)rpb < cap) {
+                v.sel_e[rpb] = cb;
+                atomicAdd(&s_nsel, 1);
+            }
         }
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
         // the leaf the replay waits for is always in the batch
         int n = s_nsel;
-        bool has = false;
-        for (int jj = 0; jj < n; ++jj) has |= v.sel_e[jj] == s_x;
+        const bool has = __ballot(lane < n && v.sel_e[lane] == s_x) != 0ULL;  // n <= cap <= kmax <= 64
         if (!has && cap > 0) {
             if (n < cap) ++n;
-            v.sel_e[n - 1] = s_x;
+            if (lane == 0) v.sel_e[n - 1] = s_x;
         }
-        s_nsel = n;
+        if (lane == 0) s_nsel = n;
     }
     __syncthreads();
     const int nsel = s_nsel;
