@@ -295,7 +295,7 @@ constexpr int64_t kHistChunkMin = 4096;
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantized, Run &run) {
     const int64_t limit = chunk_limit_for(B);
-    int64_t grid = (int64_t)ds->n_cu;  // one resident 1024-thread block per CU
+    int64_t grid = (int64_t)ds->n_cu * mb::kHistBlocksPerCU;  // resident root-build blocks
     const int64_t need = (ds->n + limit - 1) / limit;
     if (grid < need) grid = need;
     s.hist_grid = (int32_t)grid;

@@ -1121,7 +1121,30 @@ struct FAcc {
 // reaches the group by a lane shuffle. Each lane keeps kHistUnroll row loads
 // in flight. blockIdx.y is the feature tile: the block reads that tile's
 // records and stores that tile's features of its partial.
-constexpr int kHistUnroll = 4;
+#ifndef MB_HIST_UNROLL
+#define MB_HIST_UNROLL 4
+#endif
+constexpr int kHistUnroll = MB_HIST_UNROLL;
+
+// The value of the last lane of each LPR-lane group, on every lane of the
+// group, by DPP (a VALU operand modifier): unlike a crossbar shuffle it does
+// not go through the LDS queue, so reading it never waits for the LDS
+// atomics issued before it. LPR 2: quad_perm [1,1,3,3]; LPR 4: quad_perm
+// [3,3,3,3]; LPR 8: that, then row_shl:4 into lane banks 0 and 2 (lanes
+// 0-3 and 8-11 of each row take lanes 4-7 and 12-15).
+template <int LPR>
+__device__ __forceinline__ uint32_t group_last_lane(uint32_t x) {
+    if constexpr (LPR == 1) {
+        return x;
+    } else if constexpr (LPR == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0xF5, 0xF, 0xF, false);
+    } else {
+        static_assert(LPR == 4 || LPR == 8, "records of 16, 32, 64 or 128 bytes");
+        const int y = __builtin_amdgcn_update_dpp((int)x, (int)x, 0xFF, 0xF, 0xF, false);
+        if constexpr (LPR == 4) return (uint32_t)y;
+        else return (uint32_t)__builtin_amdgcn_update_dpp(y, y, 0x104, 0xF, 0x5, false);
+    }
+}
 
 // Accumulates the records of rows [lo, hi) of a row list (kList), or of the
 // rows lo .. hi - 1 themselves, into the block's LDS histogram:
@@ -1137,11 +1160,9 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                                                 double goss_mult) {
     constexpr int U = kHistUnroll;
     const int ls = s.lds_stride;
-    const int lane = lane_id();
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
     const int rpp = blockDim.x / LPR;
-    const int src_lane = (lane / LPR) * LPR + (LPR - 1);
     const int64_t step = (int64_t)U * rpp;
     const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
     if (lo >= hi) return;
@@ -1164,11 +1185,13 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
         }
     };
     auto accumulate = [&](int64_t i0, const int32_t *id, const uint4 *w) {
+        uint32_t gh[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) gh[u] = group_last_lane<LPR>(w[u].w);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + (int64_t)u * rpp + rr;
-            const uint32_t gh = __shfl(w[u].w, src_lane, 64);
-            if (i < hi) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, (int64_t)(uint32_t)id[u], gh, goss_mult);
+            if (i < hi) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, (int64_t)(uint32_t)id[u], gh[u], goss_mult);
         }
     };
     int32_t id_cur[U], id_nxt[U], id_nn[U];
@@ -1177,12 +1200,14 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     load_ids(i0, id_cur);
     load_recs(i0, id_cur, w_cur);
     load_ids(i0 + step, id_nxt);
+    // The next step's loads are issued unconditionally (past the range they
+    // re-read the last row): under a branch, the compiler's wait for the
+    // current records at the join would also wait for them, and loads would
+    // no longer overlap the LDS atomics.
     for (;;) {
         const bool more = i0 + step < hi;
-        if (more) {
-            load_recs(i0 + step, id_nxt, w_nxt);
-            load_ids(i0 + 2 * step, id_nn);
-        }
+        load_recs(i0 + step, id_nxt, w_nxt);
+        load_ids(i0 + 2 * step, id_nn);
         accumulate(i0, id_cur, w_cur);
         if (!more) break;
         i0 += step;
@@ -3285,7 +3310,7 @@ hipError_t prepare_kernels(const DevState &s) {
 template <class Acc>
 hipError_t launch_hist_t(const DevState &s, hipStream_t st) {
     const size_t lds = hist_lds_bytes(s);
-    const dim3 grid(s.hist_grid, s.n_tiles), block(1024);
+    const dim3 grid(s.hist_grid, s.n_tiles), block(kHistThreads);
     switch (s.rec_bytes / 16) {
     case 1: hipLaunchKernelGGL((k_hist<1, Acc>), grid, block, lds, st, s); break;
     case 2: hipLaunchKernelGGL((k_hist<2, Acc>), grid, block, lds, st, s); break;

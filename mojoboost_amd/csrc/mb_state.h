@@ -123,6 +123,16 @@ struct Round {
 // Parent rows of a partition task, at most (the planner's chunking; the host
 // sizes the descriptor buffer from it).
 constexpr int kPartChunk = 8192;
+// Root build launch: kHistThreads per block, kHistBlocksPerCU blocks per CU
+// (each with its own LDS histogram).
+#ifndef MB_HIST_THREADS
+#define MB_HIST_THREADS 1024
+#endif
+#ifndef MB_HIST_BPC
+#define MB_HIST_BPC 1
+#endif
+constexpr int kHistThreads = MB_HIST_THREADS;
+constexpr int kHistBlocksPerCU = MB_HIST_BPC;
 
 // Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
 constexpr int kGossTileRows = 16384;
