@@ -241,6 +241,8 @@ struct Data {
     int nb;
     std::vector<int> missing_bin;  // -1: none
     std::vector<int> widths;       // binning.histogram_widths
+    std::vector<int> ncat;         // categories of a categorical feature, 0 numerical
+    bool is_cat(int f) const { return !ncat.empty() && ncat[f] > 0; }
 };
 
 // src/mojotrees/binning.mojo:2303-2337
@@ -264,7 +266,13 @@ struct Split {
     double gain = 0.0;
     bool found = false;
     bool default_left = false;
+    bool cat = false;           // a category-set split: bins in `bits` go left
+    uint64_t bits[4] = {0, 0, 0, 0};
 };
+
+inline bool cat_contains(const uint64_t *bits, int bin) {
+    return (bits[bin >> 6] >> (bin & 63)) & 1ULL;
+}
 
 struct Params {
     orc_params p;
@@ -401,6 +409,143 @@ double reduce_lanes(const double *v, int w, bool tree) {
     return buf[0];
 }
 
+// ------------------------------------------------------------ categorical
+// categorical.find_best_categorical_split (src/mojotrees/categorical.mojo:
+// 684-782) with _onehot_search (:478-525) and _sorted_search (:527-623);
+// the arithmetic helpers cat_sort_key, cat_enters_search, cat_side_cap,
+// cat_partition_gain and cat_effective_l2 (tree_parameters_extra.mojo:
+// 981-1042). Written once over a sums type S so the Float64 histograms and
+// the integer (quantized) ones share it: Ops supplies a bin's sums, their
+// sum and difference, the leaf score at an L2, the sort key, the Hessian
+// guard and the count.
+struct CatCfg {
+    int max_cat_to_onehot, max_cat_threshold, min_data_per_group, one_hot_max_size;
+    double cat_smooth, cat_l2;
+};
+CatCfg cat_cfg(const orc_params &p) {
+    return CatCfg{p.max_cat_to_onehot, p.max_cat_threshold, p.min_data_per_group, p.one_hot_max_size,
+                  p.cat_smooth, p.cat_l2};
+}
+
+// metrics._argsort (src/mojotrees/metrics.mojo:514-556): stable bottom-up
+// merge sort, ascending, `<=` keeps the left run's element first.
+std::vector<int> argsort_stable(const std::vector<double> &v) {
+    const int n = (int)v.size();
+    std::vector<int> idx(n), buf(n);
+    for (int i = 0; i < n; ++i) idx[i] = i;
+    for (int width = 1; width < n; width *= 2) {
+        for (int lo = 0; lo < n; lo += 2 * width) {
+            int mid = std::min(lo + width, n), hi = std::min(lo + 2 * width, n);
+            int i = lo, j = mid, k = lo;
+            while (i < mid && j < hi) buf[k++] = v[idx[i]] <= v[idx[j]] ? idx[i++] : idx[j++];
+            while (i < mid) buf[k++] = idx[i++];
+            while (j < hi) buf[k++] = idx[j++];
+        }
+        idx = buf;
+    }
+    return idx;
+}
+
+struct CatResult {
+    double gain = 0.0;
+    bool found = false;
+    uint64_t bits[4] = {0, 0, 0, 0};
+};
+
+template <class Ops>
+CatResult cat_search(const Ops &o, int n_cat, const typename Ops::S &total, double l2,
+                     int64_t min_data_in_leaf, const CatCfg &c) {
+    using S = typename Ops::S;
+    CatResult best;
+    if (n_cat < 2) return best;
+    const double parent = o.score(total, l2);
+    const bool one_hot = c.one_hot_max_size >= 0 ? n_cat <= c.one_hot_max_size
+                                                   : n_cat + 1 <= c.max_cat_to_onehot;
+    if (one_hot) {
+        for (int t = 1; t <= n_cat; ++t) {
+            const S left = o.cell(t);
+            if (o.count(left) < min_data_in_leaf || o.low_hess(left)) continue;
+            const S right = o.sub(total, left);
+            if (o.count(right) < min_data_in_leaf) continue;
+            if (o.low_hess(right)) continue;
+            const double gain = o.score(left, l2) + o.score(right, l2) - parent;
+            if (gain > best.gain) {
+                best = CatResult();
+                best.gain = gain;
+                best.found = true;
+                best.bits[t >> 6] |= 1ULL << (t & 63);
+            }
+        }
+        return best;
+    }
+    std::vector<int> cand;
+    std::vector<double> keys;
+    for (int t = 1; t <= n_cat; ++t) {
+        const S s = o.cell(t);
+        if (!((double)o.count(s) >= c.cat_smooth)) continue;
+        cand.push_back(t);
+        keys.push_back(o.key(s, c.cat_smooth));
+    }
+    const int used = (int)cand.size();
+    if (used < 2) return best;
+    const std::vector<int> order = argsort_stable(keys);
+    std::vector<int> sorted(used);
+    for (int i = 0; i < used; ++i) sorted[i] = cand[order[i]];
+    int max_num_cat = c.max_cat_threshold;
+    if ((used + 1) / 2 < max_num_cat) max_num_cat = (used + 1) / 2;
+    if (max_num_cat < 0) max_num_cat = 0;
+    const double l2c = l2 + c.cat_l2;
+    for (int d = 0; d < 2; ++d) {
+        const int dir = d == 0 ? 1 : -1;
+        const int start = d == 0 ? 0 : used - 1;
+        int pos = start;
+        int64_t group = 0;
+        S left = o.zero();
+        const int steps = used < max_num_cat ? used : max_num_cat;
+        for (int i = 0; i < steps; ++i) {
+            const int t = sorted[pos];
+            pos += dir;
+            const S s = o.cell(t);
+            left = o.add(left, s);
+            group += o.count(s);
+            if (o.count(left) < min_data_in_leaf || o.low_hess(left)) continue;
+            const S right = o.sub(total, left);
+            if (o.count(right) < min_data_in_leaf || o.count(right) < c.min_data_per_group) break;
+            if (o.low_hess(right)) break;
+            if (group < c.min_data_per_group) continue;
+            group = 0;
+            const double gain = o.score(left, l2c) + o.score(right, l2c) - parent;
+            if (gain > best.gain) {
+                best = CatResult();
+                best.gain = gain;
+                best.found = true;
+                int q = start;
+                for (int k = 0; k <= i; ++k, q += dir) best.bits[sorted[q] >> 6] |= 1ULL << (sorted[q] & 63);
+            }
+        }
+    }
+    return best;
+}
+
+// Float64 sums (the reference's own histograms).
+struct FloatCatOps {
+    struct S {
+        double g, h;
+        int64_t c;
+    };
+    const double *gh;
+    const int64_t *cnt;
+    double l1, min_h;
+    S cell(int t) const { return S{gh[2 * t], gh[2 * t + 1], cnt[t]}; }
+    S zero() const { return S{0.0, 0.0, 0}; }
+    S add(const S &a, const S &b) const { return S{a.g + b.g, a.h + b.h, a.c + b.c}; }
+    S sub(const S &tot, const S &a) const { return S{tot.g - a.g, tot.h - a.h, tot.c - a.c}; }
+    double score(const S &s, double l2) const { return leaf_score(s.g, s.h, l1, l2); }
+    double key(const S &s, double smooth) const { return s.g / (s.h + smooth); }
+    bool low_hess(const S &s) const { return s.h < min_h; }
+    int64_t count(const S &s) const { return s.c; }
+};
+
 // split.find_best_split (src/mojotrees/split.mojo:601-1360), numerical
 // features, L2 score, no extra-tree controls.
 Split find_best_split_float(const FHist &hist, const Data &d,
@@ -411,6 +556,8 @@ Split find_best_split_float(const FHist &hist, const Data &d,
         int bin = -1;
         bool dl = false;
         bool found = false;
+        bool cat = false;
+        uint64_t bits[4] = {0, 0, 0, 0};
     };
     std::vector<Slot> slots(scan.size());
     const double l1 = P.p.lambda_l1, l2 = P.p.lambda_l2;
@@ -438,6 +585,21 @@ Split find_best_split_float(const FHist &hist, const Data &d,
             th += gh[2 * b + 1];
             tc += cc[b];
             ++b;
+        }
+        if (d.is_cat(f)) {
+            // a categorical feature is searched as category partitions
+            // (split.mojo:1022-1066); bin 0 joins no set
+            FloatCatOps ops{gh, cc, l1, min_h};
+            CatResult cr = cat_search(ops, d.ncat[f], FloatCatOps::S{tg, th, tc}, l2, min_c, cat_cfg(P.p));
+            Slot s;
+            if (cr.found) {
+                s.gain = cr.gain;
+                s.found = true;
+                s.cat = true;
+                std::memcpy(s.bits, cr.bits, sizeof s.bits);
+            }
+            slots[fi] = s;
+            continue;
         }
         int mb = d.missing_bin[f];
         double pg = soft_threshold_l1(tg, l1);
@@ -500,6 +662,8 @@ Split find_best_split_float(const FHist &hist, const Data &d,
             best.bin = slots[fi].bin;
             best.default_left = slots[fi].dl;
             best.found = true;
+            best.cat = slots[fi].cat;
+            std::memcpy(best.bits, slots[fi].bits, sizeof best.bits);
         }
     }
     return best;
@@ -626,6 +790,26 @@ inline double qleaf(int64_t g, int64_t h, const QScales &s, double l1, double l2
     return -soft_threshold_l1((double)g / s.gu, l1) / ((double)h / s.hu + l2);
 }
 
+// Integer sums on the (gu, hu) lattice: accumulated exactly, dequantized
+// (Float64(q) / units) for every score and sort key, the Hessian guard in
+// integer units (hessian_units_at_least), as the numerical quantized scan.
+struct QuantCatOps {
+    struct S {
+        int64_t g, h, c;
+    };
+    const int64_t *cell3;  // {grad, hess, count} per bin
+    double gu, hu, l1;
+    int64_t hmin;
+    S cell(int t) const { return S{cell3[3 * t], cell3[3 * t + 1], cell3[3 * t + 2]}; }
+    S zero() const { return S{0, 0, 0}; }
+    S add(const S &a, const S &b) const { return S{a.g + b.g, a.h + b.h, a.c + b.c}; }
+    S sub(const S &tot, const S &a) const { return S{tot.g - a.g, tot.h - a.h, tot.c - a.c}; }
+    double score(const S &s, double l2) const { return leaf_score((double)s.g / gu, (double)s.h / hu, l1, l2); }
+    double key(const S &s, double smooth) const { return ((double)s.g / gu) / ((double)s.h / hu + smooth); }
+    bool low_hess(const S &s) const { return s.h < hmin; }
+    int64_t count(const S &s) const { return s.c; }
+};
+
 // The integer form of find_best_split: the same candidate order, guards and
 // strict-greater fold as split.mojo:601-1360, with left/right/parent sums
 // kept as exact integers and each candidate scored by quantized_split_gain.
@@ -644,6 +828,19 @@ Split find_best_split_quant(const QHist &hist, const Data &d,
             tg += cell[3 * b];
             th += cell[3 * b + 1];
             tc += cell[3 * b + 2];
+        }
+        if (d.is_cat(f)) {
+            QuantCatOps ops{cell, s.gu, s.hu, l1, hmin};
+            CatResult cr = cat_search(ops, d.ncat[f], QuantCatOps::S{tg, th, tc}, l2, min_c, cat_cfg(P.p));
+            if (cr.found && cr.gain > best.gain) {
+                best = Split();
+                best.gain = cr.gain;
+                best.feature = f;
+                best.found = true;
+                best.cat = true;
+                std::memcpy(best.bits, cr.bits, sizeof best.bits);
+            }
+            continue;
         }
         double parent = qscore(tg, th, s, l1, l2);
         int mb = d.missing_bin[f];
@@ -693,6 +890,7 @@ Split find_best_split_quant(const QHist &hist, const Data &d,
             }
         }
         if (f_found && f_gain > best.gain) {
+            best = Split();
             best.gain = f_gain;
             best.feature = f;
             best.bin = f_bin;
@@ -707,9 +905,11 @@ Split find_best_split_quant(const QHist &hist, const Data &d,
 struct Tree {
     std::vector<int> feature, threshold, left, right, default_left, missing_bin;
     std::vector<double> value, gain, count;
+    std::vector<uint64_t> cat;  // 4 words per node: the left set of a categorical node
     int n_leaves = 0;
     int add_node(double v, double cnt) {
         int id = (int)feature.size();
+        cat.insert(cat.end(), 4, 0ULL);
         feature.push_back(-1);
         threshold.push_back(-1);
         left.push_back(-1);
@@ -721,8 +921,11 @@ struct Tree {
         count.push_back(cnt);
         return id;
     }
-    // tree.goes_left (src/mojotrees/tree.mojo:483-495)
+    bool is_cat(int node) const { return feature[node] >= 0 && threshold[node] < 0; }
+    // tree.goes_left (src/mojotrees/tree.mojo:483-495): a categorical node
+    // routes by set membership (bin 0 is never a member)
     bool goes_left(int node, int bin) const {
+        if (is_cat(node)) return cat_contains(&cat[4 * (size_t)node], bin);
         if (bin == missing_bin[node]) return default_left[node] != 0;
         return bin <= threshold[node];
     }
@@ -779,7 +982,7 @@ void partition_rows(const Data &d, const std::vector<int32_t> &rows,
     const uint8_t *col = d.bins + (int64_t)s.feature * d.n;
     for (int32_t r : rows) {
         int b = col[r];
-        bool gl = (b == missing_bin) ? s.default_left : (b <= s.bin);
+        bool gl = s.cat ? cat_contains(s.bits, b) : (b == missing_bin) ? s.default_left : (b <= s.bin);
         (gl ? left : right).push_back(r);
     }
 }
@@ -887,7 +1090,9 @@ Tree grow_tree(Policy &pol, const Data &d, const Params &P,
         if (best_i < 0) break;
         Leaf<H> &par = frontier[best_i];
         Split split = par.split;
-        int mbin = d.missing_bin[split.feature];
+        // tree._set_split (src/mojotrees/tree.mojo:462-481): a categorical
+        // node has no threshold and no missing bin
+        int mbin = split.cat ? -1 : d.missing_bin[split.feature];
         std::vector<int32_t> lrows, rrows;
         partition_rows(d, par.rows, split, mbin, lrows, rrows);
         H lh, rh;
@@ -908,9 +1113,10 @@ Tree grow_tree(Policy &pol, const Data &d, const Params &P,
         tree.right[pn] = rn;
         tree.feature[pn] = split.feature;
         tree.gain[pn] = split.gain;
-        tree.threshold[pn] = split.bin;
+        tree.threshold[pn] = split.cat ? -1 : split.bin;
         tree.default_left[pn] = split.default_left ? 1 : 0;
         tree.missing_bin[pn] = mbin;
+        if (split.cat) std::memcpy(&tree.cat[4 * (size_t)pn], split.bits, sizeof split.bits);
         int cd = par.depth + 1;
         Split ls = search(lh, (int64_t)lrows.size(), cd);
         Split rs = search(rh, (int64_t)rrows.size(), cd);
@@ -1470,7 +1676,7 @@ int32_t orc_quantize(const double *grad, const double *hess, int64_t n,
 int32_t orc_hist_quantized(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
                            const int8_t *qg, const int8_t *qh, const int32_t *rows,
                            int64_t n_sel, int64_t *out) {
-    Data d{bins, n, nf, nb, std::vector<int>(nf, -1), {}};
+    Data d{bins, n, nf, nb, std::vector<int>(nf, -1), {}, {}};
     std::vector<int> feats(nf);
     for (int f = 0; f < nf; ++f) feats[f] = f;
     QHist h;
@@ -1484,7 +1690,7 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
                        const double *grad, const double *hess, const int32_t *rows,
                        int64_t n_sel, int32_t row_blocks, double *out_gh,
                        int64_t *out_count) {
-    Data d{bins, n, nf, nb, std::vector<int>(nf, -1), {}};
+    Data d{bins, n, nf, nb, std::vector<int>(nf, -1), {}, {}};
     std::vector<int> feats(nf);
     for (int f = 0; f < nf; ++f) feats[f] = f;
     std::vector<double> g(grad, grad + n), h(hess, hess + n);
@@ -1562,7 +1768,7 @@ int32_t orc_split_quantized(const int64_t *hist, int32_t nf, int32_t nb,
                             double min_sum_hessian, int32_t min_data_in_leaf,
                             int32_t *of, int32_t *ob, int32_t *odl, double *og) {
     Data d{nullptr, 0, nf, nb, std::vector<int>(missing_bin, missing_bin + nf),
-           widths ? std::vector<int>(widths, widths + nf) : std::vector<int>()};
+           widths ? std::vector<int>(widths, widths + nf) : std::vector<int>(), {}};
     QHist h;
     h.v.assign(hist, hist + 3 * (int64_t)nf * nb);
     QScales s;
@@ -1593,7 +1799,12 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
         Data d{bins, n, nf, nb,
                missing_bin ? std::vector<int>(missing_bin, missing_bin + nf)
                            : std::vector<int>(nf, -1),
-               {}};
+               {}, {}};
+        if (P.p.n_categories) {
+            d.ncat.assign(P.p.n_categories, P.p.n_categories + nf);
+            for (int f = 0; f < nf; ++f)
+                if (d.ncat[f] >= nb) throw std::runtime_error("categorical feature has more categories than bins");
+        }
         d.widths = histogram_widths(d);
         int threads = P.p.n_threads > 0 ? P.p.n_threads
                                         : (int)std::max(1u, std::thread::hardware_concurrency());
@@ -1747,6 +1958,27 @@ void orc_model_arrays(const orc_model *m, double *base, int64_t *off, int32_t *f
     }
     off[m->trees.size()] = o;
 }
+void orc_model_cat_bits(const orc_model *m, uint64_t *out) {
+    size_t o = 0;
+    for (const Tree &tr : m->trees) {
+        std::memcpy(out + o, tr.cat.data(), tr.cat.size() * sizeof(uint64_t));
+        o += tr.cat.size();
+    }
+}
+int32_t orc_cat_split(const double *gh, const int64_t *count, int32_t n_categories, double total_g,
+                      double total_h, int64_t total_c, double lambda_l2, double lambda_l1,
+                      double min_child_hess, int32_t min_data_in_leaf, int32_t max_cat_to_onehot,
+                      int32_t max_cat_threshold, double cat_smooth, double cat_l2,
+                      int32_t min_data_per_group, int32_t one_hot_max_size, double *out_gain,
+                      uint64_t *out_bits) {
+    FloatCatOps ops{gh, count, lambda_l1, min_child_hess};
+    CatCfg c{max_cat_to_onehot, max_cat_threshold, min_data_per_group, one_hot_max_size, cat_smooth, cat_l2};
+    CatResult r = cat_search(ops, n_categories, FloatCatOps::S{total_g, total_h, total_c}, lambda_l2,
+                             min_data_in_leaf, c);
+    *out_gain = r.gain;
+    std::memcpy(out_bits, r.bits, sizeof r.bits);
+    return r.found ? 1 : 0;
+}
 void orc_model_train_raw(const orc_model *m, double *out) {
     std::memcpy(out, m->train_raw.data(), m->train_raw.size() * sizeof(double));
 }
@@ -1758,7 +1990,7 @@ void orc_model_round_seconds(const orc_model *m, double *out) {
 // and MulticlassBooster softmax.
 int32_t orc_predict_binned(const orc_model *m, const uint8_t *bins, int64_t n,
                            int32_t nf, double *raw, double *resp) {
-    Data d{bins, n, nf, 256, std::vector<int>(nf, -1), {}};
+    Data d{bins, n, nf, 256, std::vector<int>(nf, -1), {}, {}};
     int K = m->num_class;
     double lr = m->learning_rate;
     for (int64_t r = 0; r < n; ++r) {

@@ -60,6 +60,16 @@ typedef struct {
     int32_t lambdarank_truncation_level;
     int32_t lambdarank_norm;
     double lambdarank_sigmoid;
+    /* categorical features (categorical.mojo): n_categories[f] > 0 marks
+     * feature f categorical, its categories in bins 1..n_categories[f] and
+     * bin 0 holding missing, unseen and dropped codes; NULL: all numerical */
+    const int32_t *n_categories;
+    int32_t max_cat_to_onehot;  /* LightGBM default 4 */
+    int32_t max_cat_threshold;  /* 32 */
+    double cat_smooth;          /* 10 */
+    double cat_l2;              /* 10 */
+    int32_t min_data_per_group; /* 100 */
+    int32_t one_hot_max_size;   /* -1: off (CatBoost's one-hot rule when >= 0) */
 } orc_params;
 
 /* A trained model in flat arrays. Trees are laid out one after another;
@@ -152,6 +162,19 @@ int32_t orc_split_quantized(const int64_t *hist, int32_t n_features,
                             int32_t *out_bin, int32_t *out_default_left,
                             double *out_gain);
 
+/* Best category partition of one categorical feature from a Float64
+ * histogram plane (categorical.find_best_categorical_split): gh holds
+ * n_categories + 1 interleaved (grad, hess) cells (bin 0 first), count the
+ * matching counts. Returns found (0/1); out_bits is the 256-bit set of bins
+ * routed left. */
+int32_t orc_cat_split(const double *gh, const int64_t *count, int32_t n_categories,
+                      double total_g, double total_h, int64_t total_c,
+                      double lambda_l2, double lambda_l1, double min_child_hess,
+                      int32_t min_data_in_leaf, int32_t max_cat_to_onehot,
+                      int32_t max_cat_threshold, double cat_smooth, double cat_l2,
+                      int32_t min_data_per_group, int32_t one_hot_max_size,
+                      double *out_gain, uint64_t *out_bits);
+
 /* --------------------------------------------------------------- training */
 orc_model *orc_train(const uint8_t *bins, int64_t n_rows, int32_t n_features,
                      int32_t n_bins, const int32_t *missing_bin,
@@ -168,6 +191,9 @@ void orc_model_arrays(const orc_model *model, double *base,
                       double *value, int32_t *default_left,
                       int32_t *missing_bin, double *split_gain,
                       double *count);
+/* Category sets, 4 words per node (all zero on numerical nodes and leaves);
+ * a categorical node has threshold_bin -1 and a non-empty set. */
+void orc_model_cat_bits(const orc_model *model, uint64_t *out);
 /* Training-time raw scores after the last round, row-major n * num_class. */
 void orc_model_train_raw(const orc_model *model, double *out);
 /* Per-round wall seconds, num_iterations entries (0 for rounds not run). */

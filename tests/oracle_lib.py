@@ -51,6 +51,13 @@ class Params(C.Structure):
         ("lambdarank_truncation_level", C.c_int32),
         ("lambdarank_norm", C.c_int32),
         ("lambdarank_sigmoid", C.c_double),
+        ("n_categories", C.c_void_p),
+        ("max_cat_to_onehot", C.c_int32),
+        ("max_cat_threshold", C.c_int32),
+        ("cat_smooth", C.c_double),
+        ("cat_l2", C.c_double),
+        ("min_data_per_group", C.c_int32),
+        ("one_hot_max_size", C.c_int32),
     ]
 
 
@@ -65,7 +72,8 @@ def default_params(**kw) -> Params:
         other_rate=0.1, goss_seed=3, n_threads=0, fused_score_update=1,
         fused_predict=1, totals_tree_reduce=1, use_init_base=0, init_base=0.0,
         query_starts=None, n_queries=0, lambdarank_truncation_level=30, lambdarank_norm=1,
-        lambdarank_sigmoid=1.0,
+        lambdarank_sigmoid=1.0, n_categories=None, max_cat_to_onehot=4, max_cat_threshold=32,
+        cat_smooth=10.0, cat_l2=10.0, min_data_per_group=100, one_hot_max_size=-1,
     )
     for k, v in kw.items():
         setattr(p, k, v)
@@ -148,6 +156,12 @@ def lib():
         L.orc_goss_select.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_double, C.c_double,
                                       C.c_int32, C.c_int64, C.c_void_p, C.c_void_p,
                                       P(C.c_int64)]
+        L.orc_model_cat_bits.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_cat_split.restype = C.c_int32
+        L.orc_cat_split.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_double, C.c_double,
+                                    C.c_int64, C.c_double, C.c_double, C.c_double, C.c_int32,
+                                    C.c_int32, C.c_int32, C.c_double, C.c_double, C.c_int32,
+                                    C.c_int32, C.c_void_p, C.c_void_p]
         _lib = L
     return _lib
 
@@ -176,6 +190,8 @@ class Model:
                            _ptr(self.threshold), _ptr(self.left), _ptr(self.right),
                            _ptr(self.value), _ptr(self.default_left), _ptr(self.missing_bin),
                            _ptr(self.gain), _ptr(self.count))
+        self.cat_bits = np.zeros((nn, 4), np.uint64)
+        L.orc_model_cat_bits(handle, _ptr(self.cat_bits))
 
     def tree(self, t):
         a, b = self.off[t], self.off[t + 1]
@@ -328,3 +344,36 @@ def rank_params(counts, **kw):
     p.query_starts = st.ctypes.data
     p.n_queries = len(st) - 1
     return p, st
+
+
+def categorical_params(n_categories, **kw):
+    """default_params with feature f categorical when n_categories[f] > 0;
+    the returned array must outlive the params."""
+    nc = np.ascontiguousarray(n_categories, np.int32)
+    p = default_params(**kw)
+    p.n_categories = nc.ctypes.data
+    return p, nc
+
+
+def cat_split(gh, count, n_categories, total_g=None, total_h=None, total_c=None, lambda_l2=1.0,
+              lambda_l1=0.0, min_child_hess=1e-3, min_data_in_leaf=20, max_cat_to_onehot=4,
+              max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0, min_data_per_group=100,
+              one_hot_max_size=-1):
+    """categorical.find_best_categorical_split on one feature's Float64 plane:
+    (found, gain, sorted list of the bins routed left)."""
+    gh = np.ascontiguousarray(gh, np.float64).reshape(-1)
+    count = np.ascontiguousarray(count, np.int64)
+    if total_g is None:
+        total_g = float(gh[0::2].sum())
+    if total_h is None:
+        total_h = float(gh[1::2].sum())
+    if total_c is None:
+        total_c = int(count.sum())
+    g = C.c_double()
+    bits = np.zeros(4, np.uint64)
+    found = lib().orc_cat_split(_ptr(gh), _ptr(count), n_categories, total_g, total_h, total_c,
+                                lambda_l2, lambda_l1, min_child_hess, min_data_in_leaf,
+                                max_cat_to_onehot, max_cat_threshold, cat_smooth, cat_l2,
+                                min_data_per_group, one_hot_max_size, C.byref(g), _ptr(bits))
+    left = [b for b in range(256) if (int(bits[b >> 6]) >> (b & 63)) & 1]
+    return bool(found), g.value, left
