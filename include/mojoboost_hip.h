@@ -80,6 +80,16 @@ typedef struct {
     int32_t lambdarank_truncation_level;
     int32_t lambdarank_norm;
     double lambdarank_sigmoid;
+    /* categorical features (categorical.CategoricalParams,
+     * src/mojotrees/categorical.mojo:164-240, LightGBM names and defaults
+     * 4, 32, 10, 10, 100; one_hot_max_size -1 = off). Used only when the
+     * dataset marks features categorical (mbh_dataset_set_categorical). */
+    int32_t max_cat_to_onehot;
+    int32_t max_cat_threshold;
+    double cat_smooth;
+    double cat_l2;
+    int32_t min_data_per_group;
+    int32_t one_hot_max_size;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -91,6 +101,19 @@ int32_t mbh_bin_dense(const double *data, int64_t n_rows, int32_t n_features,
                       int32_t use_missing, int64_t sample_cnt, int64_t seed,
                       uint8_t *out_bins, int32_t *out_missing_bin, char *err,
                       int32_t err_len);
+/* The same with categorical features (categorical.fit_categorical_spec,
+ * src/mojotrees/categorical.mojo:419-464): the n_categorical features listed
+ * in `categorical` are fitted as category tables over all rows -- code c of
+ * the feature's kept codes (at most max_bins - 1, the most frequent) in bin
+ * 1 + its rank, missing (negative, NaN), unseen and dropped codes in bin 0 --
+ * and out_n_categories[f] receives each feature's category count (0 for a
+ * numerical feature). */
+int32_t mbh_bin_dense_cat(const double *data, int64_t n_rows, int32_t n_features,
+                          int32_t max_bins, int32_t min_data_in_bin,
+                          int32_t use_missing, int64_t sample_cnt, int64_t seed,
+                          const int32_t *categorical, int32_t n_categorical,
+                          uint8_t *out_bins, int32_t *out_missing_bin,
+                          int32_t *out_n_categories, char *err, int32_t err_len);
 
 /* Number of usable gfx950 devices (0 without a GPU or runtime). */
 int32_t mbh_device_count(void);
@@ -102,6 +125,15 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n_rows,
                            const int32_t *missing_bin, const double *labels,
                            mbh_dataset **out, char *err, int32_t err_len);
 void mbh_dataset_free(mbh_dataset *ds);
+/* Marks categorical features of a resident dataset: n_categories[f] > 0
+ * makes feature f categorical with its categories in bins 1..n_categories[f]
+ * (bin 0: missing, unseen, dropped); 0 keeps it numerical. Training then
+ * searches that feature as category sets (categorical.
+ * find_best_categorical_split, src/mojotrees/categorical.mojo:684-782) and a
+ * categorical node routes its set left and every other bin right. Served on
+ * the quantized-gradient path. */
+int32_t mbh_dataset_set_categorical(mbh_dataset *ds, const int32_t *n_categories,
+                                    char *err, int32_t err_len);
 
 /* Train on a resident dataset: quantized gradients with integer histograms,
  * or fp32 gradients with fp64 histogram sums (use_quantized_grad = 0). */
@@ -115,6 +147,9 @@ void mbh_fit_arrays(const mbh_fit *fit, double *base, int64_t *node_offset,
                     int32_t *feature, int32_t *threshold_bin, int32_t *left,
                     int32_t *right, double *value, int32_t *default_left,
                     int32_t *missing_bin, double *split_gain, double *count);
+/* Category sets, 4 words per node in mbh_fit_arrays' order: the bins a
+ * categorical node (threshold_bin -1) routes left; zero elsewhere. */
+void mbh_fit_cat_bits(const mbh_fit *fit, uint64_t *out);
 /* Final raw scores of the training rows, row-major n_rows * num_class. */
 int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
                           int32_t err_len);
@@ -178,14 +213,15 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
  * mbh_fit_arrays does (tree_begin a multiple of num_class). base: num_class
  * scores added first, or NULL for a range that starts after iteration 0. out:
  * row-major n_rows x num_class, bit-identical to the host predictor (fused
- * multiply-adds in ascending tree order). */
+ * multiply-adds in ascending tree order). cat_bits: 4 words per node, the
+ * left set of a categorical node (threshold -1), or NULL without any. */
 int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n_rows, int32_t n_features,
                            int32_t num_class, double learning_rate, const double *base,
                            const int64_t *node_offset, int64_t tree_begin, int64_t tree_end,
                            const int32_t *feature, const int32_t *threshold,
                            const int32_t *left, const int32_t *right, const double *value,
                            const int32_t *default_left, const int32_t *missing_bin,
-                           double *out, char *err, int32_t err_len);
+                           const uint64_t *cat_bits, double *out, char *err, int32_t err_len);
 
 /* ------------------------------------------- stage-level (parity, bench) */
 /* Device exp and sigmoid of x[0..n). */

@@ -36,6 +36,7 @@ MBH_SYMBOLS = [
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
+    "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits",
 ]
 
 
@@ -69,6 +70,12 @@ class MbhParams(C.Structure):
         ("lambdarank_truncation_level", C.c_int32),
         ("lambdarank_norm", C.c_int32),
         ("lambdarank_sigmoid", C.c_double),
+        ("max_cat_to_onehot", C.c_int32),
+        ("max_cat_threshold", C.c_int32),
+        ("cat_smooth", C.c_double),
+        ("cat_l2", C.c_double),
+        ("min_data_per_group", C.c_int32),
+        ("one_hot_max_size", C.c_int32),
     ]
 
 
@@ -80,7 +87,9 @@ def mbh_params(**kw) -> MbhParams:
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
                   quant_seed=11, time_histograms=0, use_quantized_grad=1, goss=0,
                   top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0,
-                  lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0)
+                  lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0,
+                  max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
+                  min_data_per_group=100, one_hot_max_size=-1)
     for k, v in kw.items():
         setattr(p, k, v)
     return p
@@ -147,7 +156,11 @@ def lib():
         "mbh_histogram_fp32": (I32, [V, V, V, V, I64, V, V, C.c_char_p, I32]),
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),
         "mbh_predict_binned": (I32, [V, I64, I32, I32, C.c_double, V, V, I64, I64, V, V, V, V, V, V, V,
-                                     V, C.c_char_p, I32]),
+                                     V, V, C.c_char_p, I32]),
+        "mbh_bin_dense_cat": (I32, [V, I64, I32, I32, I32, I32, I64, I64, V, I32, V, V, V,
+                                    C.c_char_p, I32]),
+        "mbh_dataset_set_categorical": (I32, [V, V, C.c_char_p, I32]),
+        "mbh_fit_cat_bits": (None, [V, V]),
         "mbh_dataset_set_groups": (I32, [V, V, I64, C.c_char_p, I32]),
         "mbh_lambdarank": (I32, [V, P(MbhParams), V, V, V, C.c_char_p, I32]),
         "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, I64, C.c_char_p, V, V]),

@@ -103,6 +103,18 @@ const std::map<std::string, std::string> &aliases() {
         {"lambdarank_truncation_level", "lambdarank_truncation_level"},
         {"sigmoid", "sigmoid"},
         {"lambdarank_norm", "lambdarank_norm"},
+        // categorical features (LightGBM names; categorical.mojo:164-240)
+        {"categorical_feature", "categorical_feature"},
+        {"categorical_features", "categorical_feature"},
+        {"cat_features", "categorical_feature"},
+        {"categorical_column", "categorical_feature"},
+        {"cat_feature", "categorical_feature"},
+        {"max_cat_to_onehot", "max_cat_to_onehot"},
+        {"max_cat_threshold", "max_cat_threshold"},
+        {"cat_smooth", "cat_smooth"},
+        {"cat_l2", "cat_l2"},
+        {"min_data_per_group", "min_data_per_group"},
+        {"one_hot_max_size", "one_hot_max_size"},
     };
     return a;
 }
@@ -113,7 +125,9 @@ const char *kPrimaryKeys =
     "feature_fraction_bynode,feature_fraction_seed,max_bin,alpha,device,use_missing,"
     "use_quantized_grad,num_grad_quant_bins,stochastic_rounding,bagging_fraction,"
     "bagging_freq,bagging_seed,boosting,top_rate,other_rate,min_data_in_bin,"
-    "bin_construct_sample_cnt,data_random_seed,lambdarank_truncation_level,sigmoid,lambdarank_norm";
+    "bin_construct_sample_cnt,data_random_seed,lambdarank_truncation_level,sigmoid,lambdarank_norm,"
+    "categorical_feature,max_cat_to_onehot,max_cat_threshold,cat_smooth,cat_l2,min_data_per_group,"
+    "one_hot_max_size";
 
 struct Config {
     mbh_params p{};
@@ -126,6 +140,7 @@ struct Config {
     bool quantized = false;  // LightGBM's default; the reference trains unquantized
     int num_class = 1;
     bool saw_num_class = false;
+    std::vector<int> categorical;  // categorical_feature: column indices
 };
 
 double to_double(const std::string &k, const std::string &v) {
@@ -182,6 +197,12 @@ Config parse(const char *spec) {
     p.lambdarank_truncation_level = 30;  // RankerParams.default (ranking.mojo:478-490)
     p.lambdarank_norm = 1;
     p.lambdarank_sigmoid = 1.0;
+    p.max_cat_to_onehot = 4;  // CategoricalParams.default (categorical.mojo:205-207)
+    p.max_cat_threshold = 32;
+    p.cat_smooth = 10.0;
+    p.cat_l2 = 10.0;
+    p.min_data_per_group = 100;
+    p.one_hot_max_size = -1;
     if (!spec) return c;
     std::istringstream in(spec);
     std::string item;
@@ -279,6 +300,28 @@ Config parse(const char *spec) {
             p.lambdarank_sigmoid = to_double(k, val);
         } else if (k == "lambdarank_norm") {
             p.lambdarank_norm = to_bool(k, val) ? 1 : 0;
+        } else if (k == "categorical_feature") {
+            // comma-separated column indices (LightGBM's form)
+            c.categorical.clear();
+            std::istringstream cs(val);
+            for (std::string tok; std::getline(cs, tok, ',');) {
+                if (tok.empty()) continue;
+                const int64_t f = to_int(k, tok);
+                if (f < 0) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "categorical_feature indices must be non-negative"};
+                c.categorical.push_back((int)f);
+            }
+        } else if (k == "max_cat_to_onehot") {
+            p.max_cat_to_onehot = (int)to_int(k, val);
+        } else if (k == "max_cat_threshold") {
+            p.max_cat_threshold = (int)to_int(k, val);
+        } else if (k == "cat_smooth") {
+            p.cat_smooth = to_double(k, val);
+        } else if (k == "cat_l2") {
+            p.cat_l2 = to_double(k, val);
+        } else if (k == "min_data_per_group") {
+            p.min_data_per_group = (int)to_int(k, val);
+        } else if (k == "one_hot_max_size") {
+            p.one_hot_max_size = (int)to_int(k, val);
         }
     }
     if (c.saw_num_class && p.objective != MBH_OBJ_MULTICLASS)
@@ -366,7 +409,8 @@ int32_t predict_common(const MojoTreesModel *model, const double *data, int64_t 
             const int32_t rc = mbh_predict_binned(
                 bins.data(), n_rows, (int32_t)n_features, (int32_t)k, m.learning_rate, s0 == 0 ? m.base.data() : nullptr,
                 m.offsets.data(), s0 * k, s1 * k, m.feature.data(), m.threshold.data(), m.left.data(), m.right.data(),
-                m.value.data(), m.default_left.data(), m.missing_bin.data(), tmp.data(), msg, sizeof(msg));
+                m.value.data(), m.default_left.data(), m.missing_bin.data(),
+                m.mapper.any_cat() ? m.cat_bits.data() : nullptr, tmp.data(), msg, sizeof(msg));
             if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
         } else {
             m.predict_raw(data, n_rows, s0, s1, tmp.data());
@@ -377,13 +421,28 @@ int32_t predict_common(const MojoTreesModel *model, const double *data, int64_t 
     });
 }
 
+// categorical_feature indices name columns of the matrix, each once
+// (fit_categorical_spec's checks, categorical.mojo:434-444)
+void check_categorical(const Config &c, int64_t n_features) {
+    std::vector<int> seen;
+    for (int f : c.categorical) {
+        if (f >= n_features)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
+                           "categorical_feature index " + std::to_string(f) + " is out of range"};
+        if (std::find(seen.begin(), seen.end(), f) != seen.end())
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "duplicate categorical feature index"};
+        seen.push_back(f);
+    }
+}
+
 // Host binning, the resident dataset, device training and the model: the
 // common body of the training entry points. groups: per-query row counts
 // (lambdarank), or null.
 MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_features, const double *labels,
                             const int32_t *groups, int64_t n_groups, Config &c) {
+    check_categorical(c, n_features);
     mb::BinMapper mapper = mb::fit_bins(data, n_rows, (int)n_features, c.max_bin, c.min_data_in_bin,
-                                        c.use_missing, c.bin_sample, c.data_seed);
+                                        c.use_missing, c.bin_sample, c.data_seed, c.categorical);
     std::vector<uint8_t> bins((size_t)n_rows * n_features);
     mapper.transform(data, n_rows, bins.data());
     char msg[512] = {0};
@@ -391,6 +450,15 @@ MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_featur
     int32_t rc = mbh_dataset_create(bins.data(), n_rows, (int32_t)n_features, c.max_bin,
                                     mapper.missing_bin.data(), labels, &ds, msg, sizeof(msg));
     if (rc != MOJOTREES_OK) throw ApiError{rc, msg};
+    if (mapper.any_cat()) {
+        std::vector<int32_t> ncat(n_features);
+        for (int f = 0; f < (int)n_features; ++f) ncat[f] = mapper.n_categories(f);
+        rc = mbh_dataset_set_categorical(ds, ncat.data(), msg, sizeof(msg));
+        if (rc != MOJOTREES_OK) {
+            mbh_dataset_free(ds);
+            throw ApiError{rc, msg};
+        }
+    }
     if (groups) {
         rc = mbh_dataset_set_groups(ds, groups, n_groups, msg, sizeof(msg));
         if (rc != MOJOTREES_OK) {
@@ -428,6 +496,10 @@ MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_featur
     mbh_fit_arrays(fit, m.base.data(), m.offsets.data(), m.feature.data(), m.threshold.data(), m.left.data(),
                    m.right.data(), m.value.data(), m.default_left.data(), m.missing_bin.data(), m.gain.data(),
                    m.count.data());
+    m.cat_bits.resize((size_t)nn * 4);
+    mbh_fit_cat_bits(fit, m.cat_bits.data());
+    m.is_cat_node.resize(nn);
+    for (int64_t i = 0; i < nn; ++i) m.is_cat_node[i] = (m.feature[i] >= 0 && m.threshold[i] < 0) ? 1 : 0;
     mbh_fit_free(fit);
     m.n_leaves.resize(nt);
     for (int t = 0; t < nt; ++t) {
@@ -465,6 +537,7 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
         if (n_rows <= 0 || n_features <= 0)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "n_rows and n_features must be positive"};
         Config c = parse(parameters);
+        check_categorical(c, n_features);
         if (c.p.objective == MBH_OBJ_LAMBDARANK)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
                            "objective=lambdarank needs query groups: train it with mbh_train_ranker_dense"};
@@ -624,6 +697,7 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
         if (n_rows <= 0 || n_features <= 0 || n_groups <= 0)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "n_rows, n_features and n_groups must be positive"};
         Config c = parse(parameters);
+        check_categorical(c, n_features);
         c.p.objective = MBH_OBJ_LAMBDARANK;
         if (c.device == MOJOTREES_DEVICE_CPU)
             throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,

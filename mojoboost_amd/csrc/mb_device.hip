@@ -108,6 +108,10 @@ struct mbh_dataset {
     double *d_labels = nullptr;
     int32_t *d_missing = nullptr, *d_widths = nullptr;
     std::vector<int32_t> missing, widths;
+    // categories per feature (0: numerical), set by mbh_dataset_set_categorical
+    std::vector<int32_t> ncat;
+    int32_t *d_ncat = nullptr;
+    bool any_cat = false;
     double label_sum = 0.0;  // sequential sum, for the base score
     std::vector<double> class_count;  // when labels are integers in [0, 1024)
     bool labels_integral = false;
@@ -135,6 +139,7 @@ struct mbh_fit {
     std::vector<int64_t> offsets{0};
     std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
     std::vector<double> value, gain, count;
+    std::vector<uint64_t> cat_bits;  // 4 words per node
     std::vector<double> train_raw;
     double stats[kNumStats] = {0};
 };
@@ -195,6 +200,19 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         if (p->bagging_freq > 0 && p->bagging_fraction < 1.0)
             unsup("query bagging for lambdarank is not built on the device path");
         if (p->goss) unsup("GOSS with lambdarank is not built on the device path");
+    }
+    if (ds->any_cat) {
+        // CategoricalParams.check_one_hot (categorical.mojo:216-240) and
+        // the search's own bounds
+        if (!p->use_quantized_grad)
+            unsup("categorical features are served on the quantized-gradient path (use_quantized_grad=true)");
+        if (!(p->cat_smooth > 0.0)) bad("cat_smooth must be positive");
+        if (!(p->cat_l2 >= 0.0)) bad("cat_l2 must be non-negative");
+        if (p->max_cat_threshold < 1) bad("max_cat_threshold must be positive");
+        if (p->min_data_per_group < 1) bad("min_data_per_group must be positive");
+        if (p->max_cat_to_onehot < 1) bad("max_cat_to_onehot must be positive");
+        if (p->one_hot_max_size < -1 || p->one_hot_max_size > 256)
+            bad("one_hot_max_size must be -1 (off) or in [0, 256]");
     }
     if (p->objective == MBH_OBJ_MULTICLASS) {
         if (p->num_class < 2 || p->num_class > kMaxClass) bad("num_class must be in [2, 1024]");
@@ -375,6 +393,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.labels = ds->d_labels;
     s.missing_bin = ds->d_missing;
     s.widths = ds->d_widths;
+    s.ncat = ds->any_cat ? ds->d_ncat : nullptr;
     s.n = ds->n;
     s.n_features = F;
     s.n_bins = ds->nb;
@@ -421,6 +440,14 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.arc_int = dalloc<int32_t>((size_t)T * (6 * max_nodes + 2), run.owned);
     s.arc_dbl = dalloc<double>((size_t)T * 3 * max_nodes, run.owned);
     s.arc_aux = dalloc<int64_t>((size_t)T * 4, run.owned);
+    if (ds->any_cat) {
+        s.scan_cat = dalloc<unsigned long long>((size_t)s.kmax * 2 * F * 4, run.owned);
+        s.e_cat = dalloc<unsigned long long>((size_t)s.e_cap * 4, run.owned);
+        s.t_cat = dalloc<unsigned long long>((size_t)max_nodes * 4, run.owned);
+        s.arc_cat = dalloc<unsigned long long>((size_t)T * max_nodes * 4, run.owned);
+        HIPX(hipMemset(s.t_cat, 0, (size_t)max_nodes * 4 * sizeof(unsigned long long)));
+        HIPX(hipMemset(s.arc_cat, 0, (size_t)T * max_nodes * 4 * sizeof(unsigned long long)));
+    }
     s.max_nodes = max_nodes;
     uint8_t *fmask = dalloc<uint8_t>((size_t)T * F, run.owned);
     s.feature_mask = fmask;
@@ -509,6 +536,12 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.lambda_l1 = p->lambda_l1;
     hp.lambda_l2 = p->lambda_l2;
     hp.min_sum_hessian = p->min_sum_hessian;
+    hp.max_cat_to_onehot = p->max_cat_to_onehot;
+    hp.max_cat_threshold = p->max_cat_threshold;
+    hp.min_data_per_group = p->min_data_per_group;
+    hp.one_hot_max_size = p->one_hot_max_size;
+    hp.cat_smooth = p->cat_smooth;
+    hp.cat_l2 = p->cat_l2;
 
     if (mb::plan_lds_bytes(s) > 160 * 1024)
         throw Error{MOJOTREES_ERROR_UNSUPPORTED,
@@ -561,6 +594,55 @@ int32_t mbh_bin_dense(const double *data, int64_t n, int32_t F, int32_t max_bins
     } catch (const std::exception &e) {
         set_err(err, err_len, e.what());
         return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_bin_dense_cat(const double *data, int64_t n, int32_t F, int32_t max_bins, int32_t min_data_in_bin,
+                          int32_t use_missing, int64_t sample_cnt, int64_t seed, const int32_t *categorical,
+                          int32_t n_categorical, uint8_t *out_bins, int32_t *out_missing, int32_t *out_ncat,
+                          char *err, int32_t err_len) {
+    if (!data || !out_bins || !out_missing || !out_ncat || n <= 0 || F <= 0 || n_categorical < 0 ||
+        (n_categorical > 0 && !categorical)) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        const std::vector<int> cats(categorical, categorical + n_categorical);
+        mb::BinMapper m = mb::fit_bins(data, n, F, max_bins, min_data_in_bin, use_missing != 0, sample_cnt, seed, cats);
+        m.transform(data, n, out_bins);
+        for (int f = 0; f < F; ++f) {
+            out_missing[f] = m.missing_bin[f];
+            out_ncat[f] = m.n_categories(f);
+        }
+    } catch (const std::exception &e) {
+        set_err(err, err_len, e.what());
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_dataset_set_categorical(mbh_dataset *ds, const int32_t *ncat, char *err, int32_t err_len) {
+    if (!ds || !ncat) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        for (int f = 0; f < ds->F; ++f) {
+            if (ncat[f] < 0) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "n_categories must be non-negative"};
+            // a split search past the histogram's bins would read another
+            // feature's cells (split.mojo:1028-1033)
+            if (ncat[f] >= ds->nb)
+                throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "categorical feature has more categories than bins"};
+        }
+        ds->ncat.assign(ncat, ncat + ds->F);
+        ds->any_cat = false;
+        for (int f = 0; f < ds->F; ++f) ds->any_cat = ds->any_cat || ncat[f] > 0;
+        if (!ds->d_ncat) ds->d_ncat = dalloc<int32_t>(ds->F, ds->owned);
+        HIPX(hipMemcpy(ds->d_ncat, ds->ncat.data(), ds->F * sizeof(int32_t), hipMemcpyHostToDevice));
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
     }
     return MOJOTREES_OK;
 }
@@ -787,6 +869,11 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         HIPX(hipMemcpy(ai.data(), s.arc_int, ai.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(ad.data(), s.arc_dbl, ad.size() * sizeof(double), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(ax.data(), s.arc_aux, ax.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
+        std::vector<unsigned long long> acat;
+        if (s.arc_cat) {
+            acat.resize((size_t)tb.T * mn * 4);
+            HIPX(hipMemcpy(acat.data(), s.arc_cat, acat.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+        }
         fit->train_raw.resize((size_t)ds->n * K);
         HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
                        hipMemcpyDeviceToHost));
@@ -850,6 +937,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                     fit->value.push_back(td[3 * i + 0]);
                     fit->gain.push_back(td[3 * i + 1]);
                     fit->count.push_back(td[3 * i + 2]);
+                    for (int w = 0; w < 4; ++w)
+                        fit->cat_bits.push_back(acat.empty() ? 0ULL : acat[((size_t)t * mn + i) * 4 + w]);
                 }
                 fit->offsets.push_back((int64_t)fit->feature.size());
                 ++grown;
@@ -907,6 +996,9 @@ void mbh_fit_arrays(const mbh_fit *fit, double *base, int64_t *off, int32_t *fea
     std::memcpy(mb_, fit->missing_bin.data(), nn * sizeof(int32_t));
     std::memcpy(gain, fit->gain.data(), nn * sizeof(double));
     std::memcpy(count, fit->count.data(), nn * sizeof(double));
+}
+void mbh_fit_cat_bits(const mbh_fit *fit, uint64_t *out) {
+    if (fit && out) std::memcpy(out, fit->cat_bits.data(), fit->cat_bits.size() * sizeof(uint64_t));
 }
 int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err, int32_t err_len) {
     if (!fit || !out) {
@@ -1008,7 +1100,7 @@ int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
                            int64_t tree_begin, int64_t tree_end, const int32_t *feature,
                            const int32_t *threshold, const int32_t *left, const int32_t *right,
                            const double *value, const int32_t *default_left, const int32_t *missing_bin,
-                           double *out, char *err, int32_t err_len) {
+                           const uint64_t *cat_bits, double *out, char *err, int32_t err_len) {
     if (!bins_cm || !node_offset || !feature || !threshold || !left || !right || !value || !default_left ||
         !missing_bin || !out || n <= 0 || F <= 0 || num_class <= 0 || tree_begin < 0 || tree_end < tree_begin ||
         tree_begin % num_class != 0) {
@@ -1046,6 +1138,9 @@ int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
                 if (feature[i] >= 0 && (feature[i] >= F || left[i] <= loc || right[i] <= loc ||
                                         left[i] >= b - a || right[i] >= b - a))
                     throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "malformed tree: a child index must exceed its parent's"};
+                // a node without a threshold is categorical and routes by its set
+                if (feature[i] >= 0 && threshold[i] < 0 && !cat_bits)
+                    throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "a categorical node needs its category set (cat_bits)"};
                 nodes[i - o0] = v;
                 md[i - o0] = missing_bin[i] * 2 + (default_left[i] ? 1 : 0);
             }
@@ -1061,6 +1156,12 @@ int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         int32_t *d_root = dalloc<int32_t>(root.size(), run.owned);
         double *d_val = dalloc<double>(vals.size(), run.owned);
         double *d_base = base ? dalloc<double>(K, run.owned) : nullptr;
+        unsigned long long *d_cat = nullptr;
+        if (cat_bits) {
+            d_cat = dalloc<unsigned long long>((size_t)std::max<int64_t>(nn, 1) * 4, run.owned);
+            HIPX(hipMemcpy(d_cat, cat_bits + (size_t)o0 * 4, (size_t)std::max<int64_t>(nn, 0) * 4 * sizeof(uint64_t),
+                           hipMemcpyHostToDevice));
+        }
         HIPX(hipMemcpy(d_nodes, nodes.data(), nodes.size() * sizeof(int4), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(d_md, md.data(), md.size() * sizeof(int32_t), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(d_root, root.data(), root.size() * sizeof(int32_t), hipMemcpyHostToDevice));
@@ -1094,6 +1195,7 @@ int32_t mbh_predict_binned(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
             a.num_class = K;
             a.nodes = d_nodes;
             a.md = d_md;
+            a.cat = d_cat;
             a.value = d_val;
             a.root = d_root;
             a.max_steps = max_steps;

@@ -47,7 +47,26 @@ double from_bits(const std::string &tok) {
 
 }  // namespace
 
+bool BinMapper::any_cat() const {
+    for (uint8_t c : is_cat)
+        if (c) return true;
+    return false;
+}
+
+int BinMapper::n_categories(int f) const {
+    return cat_offsets.empty() ? 0 : (int)(cat_offsets[f + 1] - cat_offsets[f]);
+}
+
 int BinMapper::bin_of(int f, double v) const {
+    if (!is_cat.empty() && is_cat[f]) {
+        // CategoricalSpec.bin_of (categorical.mojo:296-322): missing, codes
+        // out of range and unseen codes take bin 0; a fraction truncates
+        if (!(v >= 0.0) || v >= 2147483648.0) return 0;
+        const int64_t code = (int64_t)v;
+        const int64_t *a = cat_codes.data() + cat_offsets[f], *b = cat_codes.data() + cat_offsets[f + 1];
+        const int64_t *it = std::lower_bound(a, b, code);
+        return (it != b && *it == code) ? (int)(it - a) + 1 : 0;
+    }
     if (v != v) {
         if (missing_bin[f] >= 0) return missing_bin[f];
         v = 0.0;
@@ -73,10 +92,48 @@ void BinMapper::transform(const double *x, int64_t n, uint8_t *out) const {
     });
 }
 
+// fit_categorical_spec's per-column table (categorical.mojo:325-464): the
+// distinct non-negative codes, the keep most frequent (ties toward the smaller
+// code), returned ascending.
+static std::vector<int64_t> fit_category_codes(const double *col, int64_t n, int keep) {
+    std::vector<int64_t> present;
+    present.reserve(n);
+    for (int64_t r = 0; r < n; ++r) {
+        const double v = col[r];
+        if (!(v >= 0.0)) continue;
+        if (v >= 2147483648.0)
+            throw std::invalid_argument("categorical feature values must be below 2^31; use smaller integer codes");
+        present.push_back((int64_t)v);
+    }
+    std::sort(present.begin(), present.end());
+    std::vector<int64_t> codes, counts;
+    for (size_t i = 0; i < present.size();) {
+        size_t j = i;
+        while (j < present.size() && present[j] == present[i]) ++j;
+        codes.push_back(present[i]);
+        counts.push_back((int64_t)(j - i));
+        i = j;
+    }
+    if ((int)codes.size() <= keep) return codes;
+    std::vector<int> order(codes.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return counts[a] > counts[b]; });
+    std::vector<int64_t> kept;
+    for (int i = 0; i < keep; ++i) kept.push_back(codes[order[i]]);
+    std::sort(kept.begin(), kept.end());
+    return kept;
+}
+
 BinMapper fit_bins(const double *x, int64_t n, int nf, int max_bins, int min_data_in_bin,
-                   bool use_missing, int64_t sample_cnt, int64_t seed) {
+                   bool use_missing, int64_t sample_cnt, int64_t seed, const std::vector<int> &categorical) {
     if (max_bins < 2 || max_bins > 256) throw std::invalid_argument("max_bin must be in [2, 256]");
     if (min_data_in_bin < 1) throw std::invalid_argument("min_data_in_bin must be positive");
+    std::vector<uint8_t> is_cat(nf, 0);
+    for (int f : categorical) {
+        if (f < 0 || f >= nf) throw std::invalid_argument("categorical feature index out of range");
+        if (is_cat[f]) throw std::invalid_argument("duplicate categorical feature index");
+        is_cat[f] = 1;
+    }
     // bin_construct_sample_rows (binning.mojo:1745): sequential selection
     // sampling keyed by the data seed.
     std::vector<int64_t> sample;
@@ -95,9 +152,14 @@ BinMapper fit_bins(const double *x, int64_t n, int nf, int max_bins, int min_dat
     const int64_t n_sample = sampled ? (int64_t)sample.size() : n;
     std::vector<std::vector<double>> per(nf);
     std::vector<int32_t> missing(nf, -1);
+    std::vector<std::vector<int64_t>> codes(nf);
     parallel_for(nf, [&](int64_t fi) {
         const int f = (int)fi;
         const double *colp = x + (size_t)f * n;
+        if (is_cat[f]) {  // categorical columns never enter quantile binning
+            codes[f] = fit_category_codes(colp, n, max_bins - 1);
+            return;
+        }
         std::vector<double> col;
         col.reserve(n_sample);
         for (int64_t i = 0; i < n_sample; ++i) {
@@ -171,6 +233,14 @@ BinMapper fit_bins(const double *x, int64_t n, int nf, int max_bins, int min_dat
         m.edges.insert(m.edges.end(), per[f].begin(), per[f].end());
         m.edge_offsets.push_back((int64_t)m.edges.size());
     }
+    if (!categorical.empty()) {
+        m.is_cat = is_cat;
+        m.cat_offsets.assign(1, 0);
+        for (int f = 0; f < nf; ++f) {
+            m.cat_codes.insert(m.cat_codes.end(), codes[f].begin(), codes[f].end());
+            m.cat_offsets.push_back((int64_t)m.cat_codes.size());
+        }
+    }
     return m;
 }
 
@@ -188,9 +258,7 @@ void Model::predict_raw(const double *x, int64_t n, int64_t it0, int64_t it1, do
                 while (feature[o + node] >= 0) {
                     const int f = feature[o + node];
                     const int bn = mapper.bin_of(f, x[(size_t)f * n + r]);
-                    bool go_left = (bn == missing_bin[o + node]) ? default_left[o + node] != 0
-                                                                 : bn <= threshold[o + node];
-                    node = go_left ? left[o + node] : right[o + node];
+                    node = goes_left(o + node, bn) ? left[o + node] : right[o + node];
                 }
                 double &s = out[r * K + (int)(t % K)];
                 s = fma(learning_rate, value[o + node], s);  // predict_raw_row, fused
@@ -243,6 +311,15 @@ void Model::save(const std::string &path) const {
     o << "\n";
     for (int32_t v : mapper.missing_bin) o << v << " ";
     o << "\n";
+    if (mapper.any_cat()) {  // _write_categorical (serialize.mojo:545-566)
+        o << "categorical " << mapper.n_features << " " << mapper.cat_codes.size() << "\n";
+        for (int f = 0; f < mapper.n_features; ++f) o << (mapper.is_cat[f] ? 1 : 0) << " ";
+        o << "\n";
+        for (int64_t c : mapper.cat_codes) o << c << " ";
+        o << "\n";
+        for (int64_t c : mapper.cat_offsets) o << c << " ";
+        o << "\n";
+    }
     o << "trees " << num_trees() << "\n";
     for (int64_t t = 0; t < num_trees(); ++t) {
         const int64_t a = offsets[t], b = offsets[t + 1];
@@ -271,6 +348,23 @@ void Model::save(const std::string &path) const {
         if (covers) dbls(count);
         o << "gains " << (gains ? 1 : 0) << "\n";
         if (gains) dbls(gain);
+        // category sets, only for a tree with a categorical node
+        // (serialize.mojo:533-543): offsets into the tree's pool, -1 numerical
+        int64_t n_cat = 0;
+        for (int64_t i = a; i < b; ++i) n_cat += is_cat_node[i] ? 1 : 0;
+        if (n_cat > 0) {
+            o << "cat " << 4 * n_cat << "\n";
+            int64_t off = 0;
+            for (int64_t i = a; i < b; ++i) {
+                o << (is_cat_node[i] ? off : -1) << " ";
+                if (is_cat_node[i]) off += 4;
+            }
+            o << "\n";
+            for (int64_t i = a; i < b; ++i)
+                if (is_cat_node[i])
+                    for (int w = 0; w < 4; ++w) o << cat_bits[4 * (size_t)i + w] << " ";
+            o << "\n";
+        }
     }
     std::ofstream f(path);
     if (!f) throw std::runtime_error("cannot open '" + path + "' for writing");
@@ -326,6 +420,24 @@ Model Model::load(const std::string &path) {
     for (int k = 0; k <= m.mapper.n_features; ++k) m.mapper.edge_offsets.push_back(geti());
     for (int k = 0; k < m.mapper.n_features; ++k) m.mapper.missing_bin.push_back((int32_t)geti());
     if (m.mapper.edge_offsets.back() != ne) throw std::runtime_error("mapper offsets disagree with edges");
+    if (i < tok.size() && tok[i] == "categorical") {  // _read_categorical (serialize.mojo:1196-1232)
+        next();
+        const int64_t nfl = geti(), ncodes = geti();
+        if (nfl != m.mapper.n_features || ncodes < 0) throw std::runtime_error("corrupt categorical header");
+        for (int f = 0; f < m.mapper.n_features; ++f) m.mapper.is_cat.push_back(geti() != 0 ? 1 : 0);
+        for (int64_t k = 0; k < ncodes; ++k) m.mapper.cat_codes.push_back(geti());
+        for (int f = 0; f <= m.mapper.n_features; ++f) m.mapper.cat_offsets.push_back(geti());
+        if (m.mapper.cat_offsets[0] != 0 || m.mapper.cat_offsets.back() != ncodes)
+            throw std::runtime_error("corrupt categorical offsets");
+        for (int f = 0; f < m.mapper.n_features; ++f) {
+            const int64_t c0 = m.mapper.cat_offsets[f], c1 = m.mapper.cat_offsets[f + 1];
+            if (c1 < c0 || c1 - c0 >= m.mapper.n_bins) throw std::runtime_error("corrupt categorical offsets");
+            if (c1 > c0 && !m.mapper.is_cat[f]) throw std::runtime_error("corrupt categorical: table on a numerical feature");
+            for (int64_t k = c0 + 1; k < c1; ++k)
+                if (m.mapper.cat_codes[k] <= m.mapper.cat_codes[k - 1])
+                    throw std::runtime_error("corrupt categorical: codes are not ascending");
+        }
+    }
     const std::string tr = next();
     if (tr != "trees") throw std::runtime_error("section '" + tr + "' is not served by this library");
     const int64_t nt = geti();
@@ -352,6 +464,24 @@ Model Model::load(const std::string &path) {
         expect("gains");
         if (geti()) dbls(m.gain);
         else m.gain.insert(m.gain.end(), (size_t)nn, 0.0);
+        const size_t base_node = m.is_cat_node.size();
+        m.is_cat_node.insert(m.is_cat_node.end(), (size_t)nn, 0);
+        m.cat_bits.insert(m.cat_bits.end(), 4 * (size_t)nn, 0ULL);
+        if (i < tok.size() && tok[i] == "cat") {
+            next();
+            const int64_t pool = geti();
+            if (pool < 0 || pool % 4) throw std::runtime_error("corrupt cat section");
+            std::vector<int64_t> off(nn);
+            for (int64_t k = 0; k < nn; ++k) off[k] = geti();
+            std::vector<uint64_t> words(pool);
+            for (int64_t k = 0; k < pool; ++k) words[k] = std::stoull(next());
+            for (int64_t k = 0; k < nn; ++k) {
+                if (off[k] < 0) continue;
+                if (off[k] + 4 > pool) throw std::runtime_error("corrupt cat section: offset out of range");
+                m.is_cat_node[base_node + k] = 1;
+                for (int w = 0; w < 4; ++w) m.cat_bits[4 * (base_node + k) + w] = words[off[k] + w];
+            }
+        }
         m.offsets.push_back((int64_t)m.feature.size());
         for (int64_t k = m.offsets[t]; k < m.offsets[t + 1]; ++k) {
             const int fe = m.feature[k];
@@ -398,7 +528,19 @@ std::string Model::dump_json() const {
                 const int64_t eo = mapper.edge_offsets[f];
                 const int64_t ne = mapper.edge_offsets[f + 1] - eo;
                 o << ",\"split_feature\":" << f << ",\"threshold_bin\":" << bn;
-                if (bn < ne) o << ",\"threshold\":" << mapper.edges[eo + bn];
+                if (is_cat_node[k]) {
+                    // the raw category codes routed left
+                    o << ",\"categories_left\":[";
+                    bool first = true;
+                    for (int b = 1; b < 256; ++b)
+                        if ((cat_bits[4 * (size_t)k + (b >> 6)] >> (b & 63)) & 1ULL) {
+                            const int64_t c = mapper.cat_offsets.empty() || b > mapper.n_categories(f)
+                                                  ? -1 : mapper.cat_codes[mapper.cat_offsets[f] + b - 1];
+                            o << (first ? "" : ",") << c;
+                            first = false;
+                        }
+                    o << "]";
+                } else if (bn < ne) o << ",\"threshold\":" << mapper.edges[eo + bn];
                 else o << ",\"threshold\":1e300";
                 o << ",\"default_left\":" << (default_left[k] ? "true" : "false")
                   << ",\"left\":" << left[k] << ",\"right\":" << right[k] << ",\"split_gain\":" << gain[k];

@@ -21,7 +21,17 @@ struct BinMapper {
     std::vector<double> edges;         // concatenated
     std::vector<int64_t> edge_offsets; // n_features + 1
     std::vector<int32_t> missing_bin;  // -1: none
+    // categorical.CategoricalSpec (src/mojotrees/categorical.mojo:242-323):
+    // feature f's kept category codes are cat_codes[cat_offsets[f],
+    // cat_offsets[f + 1]), ascending, the i-th in bin i + 1; bin 0 holds
+    // missing (negative or NaN), unseen and dropped codes. Empty when no
+    // feature is categorical.
+    std::vector<uint8_t> is_cat;
+    std::vector<int64_t> cat_codes;
+    std::vector<int64_t> cat_offsets;
 
+    bool any_cat() const;
+    int n_categories(int f) const;
     int bin_of(int f, double v) const;
     // Column-major doubles -> column-major uint8 bins (threads over columns).
     void transform(const double *x, int64_t n_rows, uint8_t *out) const;
@@ -29,8 +39,12 @@ struct BinMapper {
 
 // binning.fit_bins with the quantile border type
 // (src/mojotrees/binning.mojo:3565-4047).
+// `categorical` lists the features fitted as category tables
+// (fit_categorical_spec, categorical.mojo:419-464, over all rows): no edges,
+// no missing bin, the max_bins - 1 most frequent codes kept.
 BinMapper fit_bins(const double *x, int64_t n_rows, int n_features, int max_bins,
-                   int min_data_in_bin, bool use_missing, int64_t sample_cnt, int64_t seed);
+                   int min_data_in_bin, bool use_missing, int64_t sample_cnt, int64_t seed,
+                   const std::vector<int> &categorical = {});
 
 struct Model {
     int objective = 0;  // 0 regression (squared error), 1 binary, -1 multiclass, 7 lambdarank (raw scores)
@@ -43,11 +57,21 @@ struct Model {
     std::vector<int32_t> n_leaves;
     std::vector<int32_t> feature, threshold, left, right, default_left, missing_bin;
     std::vector<double> value, gain, count;
+    // 4 words per node: the bins a categorical node routes left (tree.mojo:
+    // 300-306); is_cat_node marks those nodes (threshold -1, no missing bin)
+    std::vector<uint64_t> cat_bits;
+    std::vector<uint8_t> is_cat_node;
 
     int64_t num_trees() const { return (int64_t)offsets.size() - 1; }
     int64_t num_iterations() const { return num_trees() / num_class; }
     // raw scores for rows of a column-major matrix, iterations [it0, it1)
     void predict_raw(const double *x, int64_t n_rows, int64_t it0, int64_t it1, double *out) const;
+    // tree.goes_left (src/mojotrees/tree.mojo:483-495) for node k (model-wide index)
+    bool goes_left(int64_t k, int bin) const {
+        if (is_cat_node[k]) return (cat_bits[4 * (size_t)k + (bin >> 6)] >> (bin & 63)) & 1ULL;
+        if (bin == missing_bin[k]) return default_left[k] != 0;
+        return bin <= threshold[k];
+    }
     void response(double *raw, int64_t n_rows) const;
 
     void save(const std::string &path) const;  // throws std::runtime_error

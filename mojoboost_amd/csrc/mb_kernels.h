@@ -44,6 +44,7 @@ struct PredictArgs {
     int32_t rec_bytes, tile_f, n_tiles, num_class;
     const int4 *nodes;        // {feature (-1: leaf), threshold bin, left, right}
     const int32_t *md;        // missing_bin * 2 + default_left
+    const unsigned long long *cat;  // 4 words per node, the left set of a categorical node (threshold -1)
     const double *value;      // per node
     const int32_t *root;      // per tree: index of its root node
     int32_t max_steps;        // nodes of the largest tree: no walk is longer

@@ -1292,6 +1292,12 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
+        // a categorical split routes by its set (tree.goes_left): bins in it go left
+        unsigned long long cset[4] = {0ULL, 0ULL, 0ULL, 0ULL};
+        const bool is_cat = d.cat_e >= 0;
+        if (is_cat)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) cset[w] = s.e_cat[(size_t)d.cat_e * 4 + w];
         // buffer loads: 32-bit offsets (one VGPR per gather instead of a
         // 64-bit address), and any offset past the range reads 0
         const __amdgpu_buffer_rsrc_t ids = buffer_rsrc(src + d.c0, (uint32_t)(d.c1 - d.c0) * 4u);
@@ -1314,7 +1320,8 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         for (int u = 0; u < kPartRows; ++u) {
             const bool valid = (vbits >> u) & 1u;
             const int b = (int)bin[u];
-            const bool left = (b == mb) ? (dl != 0) : (b <= thr);
+            const unsigned long long cw = b < 64 ? cset[0] : b < 128 ? cset[1] : b < 192 ? cset[2] : cset[3];
+            const bool left = is_cat ? ((cw >> (b & 63)) & 1ULL) != 0 : (b == mb) ? (dl != 0) : (b <= thr);
             lbits |= (left ? 1u : 0u) << u;
             const unsigned long long lm = __ballot(valid && left);
             const unsigned long long rm = __ballot(valid && !left);
@@ -1433,6 +1440,14 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
     __shared__ double wgain[8];
     __shared__ int word[8];
     __shared__ long long wleft[8];
+    // categorical search (per child): sort keys, the sorted candidates, their
+    // count, and each walk direction's best (gain, step, left rows)
+    __shared__ double ckey[2][256];
+    __shared__ int csort[2][256];
+    __shared__ int cwcnt[8];
+    __shared__ double cdg[2][2];
+    __shared__ int cdi[2][2];
+    __shared__ long long cdl[2][2];
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const HyperParams &hp = s.hp;
     const int F = s.n_features, nb = s.n_bins;
@@ -1569,7 +1584,92 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
         double best_gain = 0.0;
         int best_order = 0x7FFFFFFF;
         int best_left = 0;
-        if (!gated) {
+        // a categorical feature is searched as category partitions
+        // (categorical.find_best_categorical_split, categorical.mojo:684-782)
+        const int ncf = s.ncat ? s.ncat[f] : 0;  // block-uniform
+        const bool cat_onehot = ncf > 0 && (hp.one_hot_max_size >= 0 ? ncf <= hp.one_hot_max_size
+                                                                      : ncf + 1 <= hp.max_cat_to_onehot);
+        bool cat_sorted = false;
+        if (ncf > 0) {
+            const double parent = qscore(TG, TH, gu, hu, l1, l2);
+            const long long min_c = hp.min_data_in_leaf;
+            if (cat_onehot) {
+                // _onehot_search (:478-525): each category alone goes left;
+                // the argmax below keeps the lowest bin on equal gains
+                if (!gated && ncf >= 2 && bin >= 1 && bin <= ncf && !(vc < min_c || vh < hmin) &&
+                    !(TC - vc < min_c) && !(TH - vh < hmin)) {
+                    const double gain = qscore(vg, vh, gu, hu, l1, l2) + qscore(TG - vg, TH - vh, gu, hu, l1, l2) - parent;
+                    if (gain > best_gain) {
+                        best_gain = gain;
+                        best_order = bin;
+                        best_left = vc;
+                    }
+                }
+            } else {
+                // _sorted_search (:527-623): categories holding at least
+                // cat_smooth rows, ordered by G / (H + cat_smooth) (stable:
+                // equal keys keep bin order, as metrics._argsort), prefixes
+                // walked from both ends
+                cat_sorted = true;
+                const bool cand = !gated && ncf >= 2 && bin >= 1 && bin <= ncf && (double)vc >= hp.cat_smooth;
+                const double key = ((double)vg / gu) / ((double)vh / hu + hp.cat_smooth);
+                ckey[child][bin] = cand ? key : 0.0;
+                const unsigned long long cm = __ballot(cand);
+                if (lane == 0) cwcnt[wv] = __popcll(cm);
+                csort[child][bin] = cand ? 1 : 0;  // candidate flags until ranked
+                __syncthreads();
+                int rank = 0;
+                if (cand)
+                    for (int u = 1; u <= ncf; ++u) {
+                        const double ku = ckey[child][u];
+                        rank += (csort[child][u] != 0 && (ku < key || (ku == key && u < bin))) ? 1 : 0;
+                    }
+                const int used = cwcnt[child << 2] + cwcnt[(child << 2) + 1] + cwcnt[(child << 2) + 2] +
+                                 cwcnt[(child << 2) + 3];
+                __syncthreads();
+                if (cand) csort[child][rank] = bin;
+                __syncthreads();
+                const int dthr = (tid & 255) >> 6;  // waves 0 and 1 of the half walk directions 0 and 1
+                if (lane == 0 && dthr < 2) {
+                    const int d = dthr;
+                    double dg = 0.0;
+                    int di = -1;
+                    long long dl_ = 0;
+                    if (used >= 2) {
+                        int max_num_cat = hp.max_cat_threshold;
+                        if ((used + 1) / 2 < max_num_cat) max_num_cat = (used + 1) / 2;
+                        if (max_num_cat < 0) max_num_cat = 0;
+                        const int steps = used < max_num_cat ? used : max_num_cat;
+                        const double l2c = l2 + hp.cat_l2;
+                        long long agg = 0, ag = 0, ah = 0, ac = 0;
+                        for (int i = 0; i < steps; ++i) {
+                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
+                            const int c_ = cc[child][tb];
+                            ag += cg[child][tb];
+                            ah += ch[child][tb];
+                            ac += c_;
+                            agg += c_;
+                            if (ac < min_c || ah < hmin) continue;
+                            const long long rc = TC - ac;
+                            if (rc < min_c || rc < hp.min_data_per_group) break;
+                            if (TH - ah < hmin) break;
+                            if (agg < hp.min_data_per_group) continue;
+                            agg = 0;
+                            const double gain = qscore(ag, ah, gu, hu, l1, l2c) + qscore(TG - ag, TH - ah, gu, hu, l1, l2c) - parent;
+                            if (gain > dg) {
+                                dg = gain;
+                                di = i;
+                                dl_ = ac;
+                            }
+                        }
+                    }
+                    cdg[child][d] = dg;
+                    cdi[child][d] = di;
+                    cdl[child][d] = dl_;
+                }
+                __syncthreads();
+            }
+        } else if (!gated) {
             const int mg = mbf >= 0 ? cg[child][mbf] : 0, mh = mbf >= 0 ? ch[child][mbf] : 0,
                       mc = mbf >= 0 ? cc[child][mbf] : 0;
             const long long min_c = hp.min_data_in_leaf;
@@ -1620,7 +1720,61 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
             wleft[wv] = best_left;
         }
         __syncthreads();
-        if ((tid & 255) == 0 && !(root_mode && child == 1)) {
+        if (ncf > 0) {
+            if ((tid & 255) == 0 && !(root_mode && child == 1)) {
+                ScanResult rs;
+                unsigned long long bits[4] = {0ULL, 0ULL, 0ULL, 0ULL};
+                rs.gain = 0.0;
+                rs.found = 0;
+                rs.n_left = 0;
+                if (cat_sorted) {
+                    // direction 0 first, then direction 1 on a strictly larger gain
+                    int d = -1;
+                    if (cdi[child][0] >= 0) d = 0;
+                    if (cdi[child][1] >= 0 && (d < 0 || cdg[child][1] > cdg[child][0])) d = 1;
+                    if (d >= 0) {
+                        int used = 0;
+                        for (int k = 0; k < 4; ++k) used += cwcnt[(child << 2) + k];
+                        for (int i = 0; i <= cdi[child][d]; ++i) {
+                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
+                            bits[tb >> 6] |= 1ULL << (tb & 63);
+                        }
+                        rs.gain = cdg[child][d];
+                        rs.found = 1;
+                        rs.n_left = cdl[child][d];
+                    }
+                } else {
+                    double bgn = wgain[child << 2];
+                    int bo = word[child << 2];
+                    long long bleft = wleft[child << 2];
+                    for (int k = 1; k < 4; ++k) {
+                        const double og = wgain[(child << 2) + k];
+                        const int oo = word[(child << 2) + k];
+                        if (og > bgn || (og == bgn && oo < bo)) {
+                            bgn = og;
+                            bo = oo;
+                            bleft = wleft[(child << 2) + k];
+                        }
+                    }
+                    if (bo != 0x7FFFFFFF) {
+                        bits[bo >> 6] |= 1ULL << (bo & 63);
+                        rs.gain = bgn;
+                        rs.found = 1;
+                        rs.n_left = bleft;
+                    }
+                }
+                rs.bin = -1;
+                rs.default_left = 0;
+                rs.cat = rs.found;
+                rs.tot_g = TG;
+                rs.tot_h = TH;
+                rs.tot_c = TC;
+                const size_t ri = (size_t)(j * 2 + child) * F + f;
+                s.scan[ri] = rs;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) s.scan_cat[ri * 4 + w] = bits[w];
+            }
+        } else if ((tid & 255) == 0 && !(root_mode && child == 1)) {
             double bgn = wgain[child << 2];
             int bo = word[child << 2];
             long long bleft = wleft[child << 2];
@@ -1638,7 +1792,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
             rs.found = bo != 0x7FFFFFFF;
             rs.bin = rs.found ? bo >> 1 : -1;
             rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
-            rs.pad_ = 0;
+            rs.cat = 0;
             rs.tot_g = TG;
             rs.tot_h = TH;
             rs.tot_c = TC;
@@ -1882,7 +2036,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
             rs.found = bo != 0x7FFFFFFF;
             rs.bin = rs.found ? bo >> 1 : -1;
             rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
-            rs.pad_ = 0;
+            rs.cat = 0;
             rs.tot_g = 0;
             rs.tot_h = 0;
             rs.tot_c = TC;
@@ -1925,7 +2079,7 @@ constexpr int kPlanThreads = 1024;
 // The fields of a selected leaf's explored node the batch setup needs.
 struct SelNode {
     int64_t begin, end, n_left;
-    int32_t buf, hist, depth, feature, bin, default_left;
+    int32_t buf, hist, depth, feature, bin, default_left, cat, pad_;
 };
 
 struct PlanLayout {
@@ -2328,7 +2482,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const long long G = base->tot_g, H = base->tot_h, C = base->tot_c;
         const double fg = base[s_vf].fg, fh = base[s_vf].fh;
         const ScanResult &qb = base[found ? bf : 0];
-        const int q_bin = qb.bin, q_dl = qb.default_left;
+        const int q_bin = qb.bin, q_dl = qb.default_left, q_cat = qb.cat;
         const long long q_nl = qb.n_left;
         // leaf value: integer sums are the same on every feature; the fp32
         // path sums the tree's first selected feature serially, as
@@ -2344,7 +2498,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             e->depth = 0;
             e->left_e = -1;
             e->right_e = -1;
-            e->pad_ = 0;
             s.t_value[0] = value;
             s.t_count[0] = (double)C;
         }
@@ -2353,6 +2506,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         e->tot_c = C;
         e->value = value;
         e->found = found ? 1 : 0;
+        e->cat = found && q_cat ? 1 : 0;
+        if (found && q_cat) {
+            const unsigned long long *sb = s.scan_cat + ((size_t)pr * F + bf) * 4;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) s.e_cat[(size_t)e_id * 4 + w] = sb[w];
+        }
         if (found) {
             e->gain = v.wg[pr];
             e->feature = bf;
@@ -2414,11 +2573,18 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const int feat = e->feature;
         const int le = v.el[v.cm_e[c]];
         s.t_feature[fx] = feat;
-        s.t_threshold[fx] = e->bin;
+        s.t_threshold[fx] = e->cat ? -1 : e->bin;
         s.t_left[fx] = lf;
         s.t_right[fx] = lf + 1;
-        s.t_default_left[fx] = e->default_left;
-        s.t_missing_bin[fx] = v.mbin[feat];
+        s.t_default_left[fx] = e->cat ? 0 : e->default_left;
+        // tree._set_split (tree.mojo:462-481): a categorical node has no
+        // threshold and no missing bin, only its set
+        s.t_missing_bin[fx] = e->cat ? -1 : v.mbin[feat];
+        if (s.t_cat) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                s.t_cat[(size_t)fx * 4 + w] = e->cat ? s.e_cat[(size_t)v.cm_e[c] * 4 + w] : 0ULL;
+        }
         s.t_gain[fx] = e->gain;
         s.t_value[lf] = s.enodes[le].value;
         s.t_count[lf] = (double)s.enodes[le].tot_c;
@@ -2451,6 +2617,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             s.t_default_left[fid] = 0;
             s.t_missing_bin[fid] = -1;
             s.t_gain[fid] = 0.0;
+            if (s.t_cat)
+                for (int w = 0; w < 4; ++w) s.t_cat[(size_t)fid * 4 + w] = 0ULL;
         }
         finish(0);
         return;
@@ -2667,6 +2835,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         sn.feature = e->feature;
         sn.bin = e->bin;
         sn.default_left = e->default_left;
+        sn.cat = e->cat;
+        sn.pad_ = 0;
         v.sn[tid] = sn;
     }
     __syncthreads();
@@ -2746,7 +2916,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         c.default_left = 0;
         c.left_e = -1;
         c.right_e = -1;
-        c.pad_ = 0;
+        c.cat = 0;
         c.begin = b0;
         c.end = b0 + nlft;
         c.hist = bl ? hb : ehist;
@@ -2792,7 +2962,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         d.default_left = pe.default_left;
         d.missing_bin = v.mbin[pe.feature];
         d.builds_left = it.builds_left;
-        d.pad_ = 0;
+        d.cat_e = pe.cat ? it.parent_e : -1;
         s.pb_desc[b] = d;
     }
     // accumulation descriptors: chunks of the accumulated child's range in
@@ -2848,11 +3018,24 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
 struct PackedTree {
     const unsigned long long *node;
     const double *value;
+    const unsigned long long *cat;  // 4 words per node: a categorical node's left set
 };
+
+// tree.goes_left for a packed node: bit 50 marks a categorical node, routed
+// by its set (bin 0, missing or unseen, is in no set); otherwise the missing
+// bin follows default_left and bin <= threshold goes left.
+__device__ __forceinline__ bool packed_goes_left(const PackedTree &t, unsigned long long w, int node, int b) {
+    if ((w >> 50) & 1ULL) return (t.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1ULL;
+    const int thr = (int)((w >> 16) & 255ULL);
+    const int mbin = (int)((w >> 24) & 511ULL) - 1;
+    const bool dl = (w >> 33) & 1ULL;
+    return (b == mbin) ? dl : (b <= thr);
+}
 
 __device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsigned char *smem) {
     unsigned long long *pn = (unsigned long long *)smem;
     double *vals = (double *)(pn + s.max_nodes);
+    unsigned long long *cats = (unsigned long long *)(vals + s.max_nodes);  // when s.t_cat
     const int n_nodes = s.t_meta[0];
     for (int i = threadIdx.x; i < n_nodes; i += blockDim.x) {
         const int f = s.t_feature[i];
@@ -2860,16 +3043,19 @@ __device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsign
         if (f < 0) {
             w = 0xFFFFULL;
         } else {
+            const bool cat = s.t_threshold[i] < 0;  // a categorical node has no threshold
             w = (unsigned long long)(uint32_t)f | ((unsigned long long)(s.t_threshold[i] & 255) << 16) |
                 ((unsigned long long)((s.t_missing_bin[i] + 1) & 511) << 24) |
                 ((unsigned long long)(s.t_default_left[i] ? 1 : 0) << 33) |
-                ((unsigned long long)(s.t_left[i] & 0xFFFF) << 34);
+                ((unsigned long long)(s.t_left[i] & 0xFFFF) << 34) | ((unsigned long long)(cat ? 1 : 0) << 50);
+            if (cat)
+                for (int k = 0; k < 4; ++k) cats[(size_t)i * 4 + k] = s.t_cat[(size_t)i * 4 + k];
         }
         pn[i] = w;
         vals[i] = s.t_value[i];
     }
     __syncthreads();
-    return PackedTree{pn, vals};
+    return PackedTree{pn, vals, cats};
 }
 
 // Leaf of a row: bin(f) gives the row's bin of feature f. The missing bin
@@ -2884,12 +3070,8 @@ __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, Bin
         const int f = (int)(w & 0xFFFFULL);
         if (f == 0xFFFF) break;
         const int b = bin(f);
-        const int thr = (int)((w >> 16) & 255ULL);
-        const int mbin = (int)((w >> 24) & 511ULL) - 1;
-        const bool dl = (w >> 33) & 1ULL;
         const int left = (int)((w >> 34) & 0xFFFFULL);
-        const bool go_left = (b == mbin) ? dl : (b <= thr);
-        node = go_left ? left : left + 1;
+        node = packed_goes_left(t, w, node, b) ? left : left + 1;
         if ((unsigned)node >= (unsigned)n_nodes) node = 0;
     }
     return node;
@@ -2908,13 +3090,9 @@ __device__ __forceinline__ void walk_packed2(const PackedTree &t, int n_nodes, B
         da |= fa == 0xFFFF;
         db |= fb == 0xFFFF;
         const int ba = da ? 0 : bin_a(fa), bb = db ? 0 : bin_b(fb);
-        auto next = [](unsigned long long w, int bin, int node, int n) {
-            const int thr = (int)((w >> 16) & 255ULL);
-            const int mbin = (int)((w >> 24) & 511ULL) - 1;
-            const bool dl = (w >> 33) & 1ULL;
+        auto next = [&t](unsigned long long w, int bin, int node, int n) {
             const int left = (int)((w >> 34) & 0xFFFFULL);
-            const bool go_left = (bin == mbin) ? dl : (bin <= thr);
-            const int c = go_left ? left : left + 1;
+            const int c = packed_goes_left(t, w, node, bin) ? left : left + 1;
             return (unsigned)c < (unsigned)n ? c : 0;
         };
         if (!da) a = next(wa, ba, a, n_nodes);
@@ -3103,6 +3281,9 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
         ad[3 * i + 0] = s.t_value[i];
         ad[3 * i + 1] = s.t_gain[i];
         ad[3 * i + 2] = s.t_count[i];
+        if (s.arc_cat)
+            for (int w = 0; w < 4; ++w)
+                s.arc_cat[((size_t)rd.tree_index * mn + i) * 4 + w] = s.t_cat[(size_t)i * 4 + w];
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -3186,7 +3367,8 @@ __global__ __launch_bounds__(256) void k_predict(PredictArgs a) {
                     b = rb[nd.x];
                 }
                 const int md = a.md[node];
-                const bool left = (b == (md >> 1)) ? (md & 1) : (b <= nd.y);
+                const bool left = nd.y < 0 ? ((a.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1ULL) != 0
+                                           : (b == (md >> 1)) ? (md & 1) : (b <= nd.y);
                 node = left ? nd.z : nd.w;
                 nd = a.nodes[node];
             }
@@ -3261,7 +3443,7 @@ hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
-size_t score_lds_bytes(const DevState &s) { return (size_t)s.max_nodes * 16; }
+size_t score_lds_bytes(const DevState &s) { return (size_t)s.max_nodes * (s.t_cat ? 48 : 16); }
 size_t hist_lds_bytes(const DevState &s) {
     return s.hp.quantized ? QAcc::lds_bytes(s.tile_f, s.lds_stride) : FAcc::lds_bytes(s.tile_f, s.lds_stride);
 }

@@ -39,7 +39,7 @@ struct ENode {
     int32_t buf, hist, depth;
     int32_t found, feature, bin, default_left;
     int32_t left_e, right_e;     // explored children, -1 until expanded
-    int32_t pad_;
+    int32_t cat;                 // 1: the best split is a category set (e_cat holds it)
 };
 
 // One leaf expanded by a launch of the partition+histogram and scan kernels.
@@ -60,7 +60,8 @@ struct Item {
 // (offsets relative to begin).
 struct PbDesc {
     int64_t begin, n_left, m, c0, c1;
-    int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left, pad_;
+    int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left;
+    int32_t cat_e;  // categorical split: the explored node whose e_cat set routes left; -1 numerical
 };
 
 // Work of one accumulation task: rows [lo, hi) of row buffer `buf` (a chunk
@@ -94,7 +95,8 @@ struct Grow {
 // Best candidate of one (child, feature) scan.
 struct ScanResult {
     double gain;
-    int32_t bin, default_left, found, pad_;
+    int32_t bin, default_left, found;
+    int32_t cat;  // 1: a category set (scan_cat holds it), bin -1
     int64_t tot_g, tot_h, tot_c;  // integer sums (quantized path; tot_c on both)
     int64_t n_left;  // rows left of the candidate
     double fg, fh;   // fp64 serial sums over the feature's bins (fp32 path's leaf value)
@@ -185,6 +187,9 @@ struct HyperParams {
     double bagging_fraction;
     double learning_rate;
     double lambda_l1, lambda_l2, min_sum_hessian;
+    // categorical splits (categorical.CategoricalParams, LightGBM names)
+    int32_t max_cat_to_onehot, max_cat_threshold, min_data_per_group, one_hot_max_size;
+    double cat_smooth, cat_l2;
 };
 
 // Everything the kernels touch, passed by value.
@@ -198,6 +203,7 @@ struct DevState {
     const double *labels;    // n
     const int32_t *missing_bin;  // F
     const int32_t *widths;       // F: realized bin count bound
+    const int32_t *ncat;         // F: categories of a categorical feature (bins 1..ncat), 0 numerical; null: none
     const uint8_t *feature_mask; // num_trees x F (1: the tree may split it)
     uint8_t *records_w;          // same buffer as records, writable view
     int64_t n;
@@ -258,6 +264,8 @@ struct DevState {
     int32_t *slot_e;       // num_leaves: explored node of each frontier slot
     int32_t *slot_fid;     // num_leaves: its node id in the committed tree
     ScanResult *scan;      // kmax x 2 x F
+    unsigned long long *scan_cat;  // kmax x 2 x F x 4: a categorical result's left set
+    unsigned long long *e_cat;     // e_cap x 4: an explored node's categorical left set
     int64_t *cursor;       // [0] root bag size; [2 + 2j], [3 + 2j]: item j's output cursors
     int32_t *error;        // sticky error flag (partition overflow)
     int32_t kmax;          // most leaves expanded per launch
@@ -272,11 +280,13 @@ struct DevState {
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;
+    unsigned long long *t_cat;  // max_nodes x 4: left set of a categorical node, zero elsewhere
     int32_t *t_meta;       // [0] n_nodes, [1] n_leaves
     // archive of finished trees (downloaded at the end)
     int32_t *arc_int;      // per tree: max_nodes x 6 ints + 2 meta
     double *arc_dbl;       // per tree: max_nodes x 3 doubles
     int64_t *arc_aux;      // per tree: rows accumulated, iterations, expansions, 0
+    unsigned long long *arc_cat;  // per tree: max_nodes x 4 (when a feature is categorical)
     int32_t max_nodes;
     HyperParams hp;
 };

@@ -16,13 +16,22 @@ def device_count() -> int:
 
 
 def bin_dense(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_missing=True,
-              sample_cnt=200_000, seed=1):
+              sample_cnt=200_000, seed=1, categorical=None):
     """Quantile-bin a column-major float64 matrix on the host (the library's
-    binning, not the oracle's). Returns (bins_cm uint8, missing_bin int32)."""
+    binning, not the oracle's). Returns (bins_cm uint8, missing_bin int32), or
+    with `categorical` (column indices fitted as category tables)
+    (bins_cm, missing_bin, n_categories int32)."""
     x_cm = np.ascontiguousarray(x_cm, np.float64).ravel()
     bins = np.zeros(n_rows * n_features, np.uint8)
     mb = np.zeros(n_features, np.int32)
     err = C.create_string_buffer(512)
+    if categorical is not None:
+        cats = np.ascontiguousarray(categorical, np.int32)
+        nc = np.zeros(n_features, np.int32)
+        check(lib().mbh_bin_dense_cat(ptr(x_cm), n_rows, n_features, max_bins, min_data_in_bin,
+                                      1 if use_missing else 0, sample_cnt, seed, ptr(cats), len(cats),
+                                      ptr(bins), ptr(mb), ptr(nc), err, 512), err)
+        return bins, mb, nc
     check(lib().mbh_bin_dense(ptr(x_cm), n_rows, n_features, max_bins, min_data_in_bin,
                               1 if use_missing else 0, sample_cnt, seed, ptr(bins), ptr(mb),
                               err, 512), err)
@@ -32,7 +41,8 @@ def bin_dense(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_mis
 class Dataset:
     """A column-major uint8 binned matrix and its labels, uploaded once."""
 
-    def __init__(self, bins_cm, n_rows, n_features, n_bins, labels, missing_bin=None):
+    def __init__(self, bins_cm, n_rows, n_features, n_bins, labels, missing_bin=None,
+                 n_categories=None):
         L = lib()
         self.n_rows, self.n_features, self.n_bins = int(n_rows), int(n_features), int(n_bins)
         bins_cm = np.ascontiguousarray(bins_cm, dtype=np.uint8).ravel()
@@ -45,6 +55,15 @@ class Dataset:
         check(L.mbh_dataset_create(ptr(bins_cm), self.n_rows, self.n_features, self.n_bins,
                                    ptr(mb), ptr(labels), C.byref(h), err, 1024), err)
         self.h = h
+        if n_categories is not None:
+            self.set_categorical(n_categories)
+
+    def set_categorical(self, n_categories):
+        """n_categories[f] > 0 marks feature f categorical (bins 1..n, bin 0
+        missing/unseen)."""
+        nc = np.ascontiguousarray(n_categories, np.int32)
+        err = C.create_string_buffer(512)
+        check(lib().mbh_dataset_set_categorical(self.h, ptr(nc), err, 512), err)
 
     def free(self):
         if getattr(self, "h", None):
@@ -147,6 +166,8 @@ class Fit:
                          ptr(self.threshold), ptr(self.left), ptr(self.right), ptr(self.value),
                          ptr(self.default_left), ptr(self.missing_bin), ptr(self.gain),
                          ptr(self.count))
+        self.cat_bits = np.zeros((nn, 4), np.uint64)
+        L.mbh_fit_cat_bits(handle, ptr(self.cat_bits))
         names = ("train_seconds", "hist_ms", "hist_bytes", "hist_rows_features",
                  "hist_builds", "root_bytes", "root_ms", "trees_grown", "growth_ms",
                  "root_growth_ms", "iterations", "expansions", "rows_built", "rows_parted",
@@ -175,7 +196,8 @@ class Fit:
             ptr(bins_cm), n_rows, n_features, self.num_class, self.learning_rate,
             ptr(self.base) if tree_begin == 0 else None, ptr(self.off), tree_begin, tree_end,
             ptr(self.feature), ptr(self.threshold), ptr(self.left), ptr(self.right),
-            ptr(self.value), ptr(self.default_left), ptr(self.missing_bin), ptr(out), err, 512), err)
+            ptr(self.value), ptr(self.default_left), ptr(self.missing_bin),
+            ptr(self.cat_bits) if self.cat_bits.any() else None, ptr(out), err, 512), err)
         return out
 
     def train_raw(self):

@@ -144,7 +144,9 @@ class _Base:
                  min_child_samples=20, min_child_weight=1e-3, reg_alpha=0.0, reg_lambda=1.0,
                  colsample_bytree=1.0, subsample=1.0, subsample_freq=0, max_bin=255,
                  random_state=None, device="gpu", use_quantized_grad=False,
-                 num_grad_quant_bins=4, stochastic_rounding=True):
+                 num_grad_quant_bins=4, stochastic_rounding=True, categorical_feature=None,
+                 max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
+                 min_data_per_group=100):
         self.n_estimators = n_estimators
         self.learning_rate = learning_rate
         self.num_leaves = num_leaves
@@ -162,6 +164,15 @@ class _Base:
         self.use_quantized_grad = use_quantized_grad
         self.num_grad_quant_bins = num_grad_quant_bins
         self.stochastic_rounding = stochastic_rounding
+        # categorical_feature: column indices split by category set
+        # (LightGBM's parameter; the reference's estimators,
+        # python/mojotrees/sklearn.py:929-951), with LightGBM's defaults
+        self.categorical_feature = categorical_feature
+        self.max_cat_to_onehot = max_cat_to_onehot
+        self.max_cat_threshold = max_cat_threshold
+        self.cat_smooth = cat_smooth
+        self.cat_l2 = cat_l2
+        self.min_data_per_group = min_data_per_group
         self.booster_ = None
 
     def _params(self, extra=""):
@@ -181,6 +192,23 @@ class _Base:
         if self.random_state is not None:
             p += [f"feature_fraction_seed={int(self.random_state)}",
                   f"bagging_seed={int(self.random_state)}"]
+        cats = self.categorical_feature
+        if cats is not None and not (isinstance(cats, str) and cats == "auto"):
+            if isinstance(cats, (str, bytes)):
+                raise ValueError("categorical_feature must be None, 'auto' or a sequence of column indices")
+            idx = []
+            for c in cats:
+                if isinstance(c, bool) or int(c) != c or int(c) < 0:
+                    raise ValueError(f"categorical_feature entry {c!r} is not a column index")
+                if int(c) in idx:
+                    raise ValueError(f"categorical_feature lists feature {int(c)} twice")
+                idx.append(int(c))
+            if idx:
+                p += ["categorical_feature=" + ",".join(str(i) for i in sorted(idx)),
+                      f"max_cat_to_onehot={self.max_cat_to_onehot}",
+                      f"max_cat_threshold={self.max_cat_threshold}",
+                      f"cat_smooth={self.cat_smooth!r}", f"cat_l2={self.cat_l2!r}",
+                      f"min_data_per_group={self.min_data_per_group}"]
         return " ".join(p) + (" " + extra if extra else "")
 
     def save(self, path):

@@ -1,0 +1,150 @@
+"""GPU parity for categorical set splits (categorical.find_best_categorical_
+split, src/mojotrees/categorical.mojo): device training against the CPU
+oracle on the same bins -- trees, category sets, values and raw scores
+bit-exact on the quantized path -- and the public surface end to end
+(estimator with categorical_feature -> C ABI -> model with category tables ->
+save/load -> host and device prediction).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from mojoboost_amd import device
+
+    if device.device_count() < 1:
+        pytest.fail("no gfx950 device visible to the HIP library")
+    return device
+
+
+def bits(a):
+    return np.asarray(a, np.float64).view(np.uint64)
+
+
+def cat_data(n, seed, cards=(3, 9, 40, 200), n_num=4):
+    """n_num N(0,1) columns then one integer column per cardinality; the
+    label mixes a numeric term with a random effect per category value, so
+    both kinds of split win nodes."""
+    rng = np.random.default_rng(seed)
+    num = rng.normal(size=(n_num, n))
+    cats = [rng.integers(0, c, size=n).astype(np.float64) for c in cards]
+    z = num[0] - 0.5 * num[min(1, n_num - 1)] * num[n_num - 1]
+    for j, c in enumerate(cards):
+        eff = rng.normal(size=c) * (1.5 if j % 2 else 0.8)
+        z = z + eff[cats[j].astype(int)]
+    x = np.vstack([num] + cats)
+    cat_idx = list(range(n_num, n_num + len(cards)))
+    return x, z, cat_idx
+
+
+def compare(fit, ref, n):
+    assert fit.n_trees == ref.n_trees, (fit.n_trees, ref.n_trees)
+    assert np.array_equal(fit.off, ref.off)
+    for k in ("feature", "threshold", "left", "right", "default_left", "missing_bin"):
+        assert np.array_equal(getattr(fit, k), getattr(ref, k)), k
+    assert np.array_equal(fit.cat_bits, ref.cat_bits)
+    for k in ("value", "gain", "count"):
+        assert np.array_equal(bits(getattr(fit, k)), bits(getattr(ref, k))), k
+    assert np.array_equal(bits(fit.train_raw()), bits(ref.train_raw(n)))
+
+
+CAT = dict(max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
+           min_data_per_group=100)
+
+
+@pytest.mark.parametrize("objective,leaves,trees", [(0, 31, 10), (1, 63, 8)])
+def test_training_categorical_bit_exact(dev, objective, leaves, trees):
+    n = 120_000
+    x, z, cat_idx = cat_data(n, seed=3 + objective)
+    rng = np.random.default_rng(7)
+    y = z + 0.1 * rng.normal(size=n) if objective == 0 else \
+        (rng.uniform(size=n) < 1 / (1 + np.exp(-z))).astype(np.float64)
+    f = x.shape[0]
+    bins, mb, nc = dev.bin_dense(x.ravel(), n, f, max_bins=255, categorical=cat_idx)
+    assert nc.tolist() == [0, 0, 0, 0, 3, 9, 40, 200]
+    kw = dict(objective=objective, num_iterations=trees, num_leaves=leaves, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    fit = dev.Dataset(bins, n, f, 255, y, missing_bin=mb, n_categories=nc).train(**kw, **CAT)
+    p, keep = O.categorical_params(nc, **kw, **CAT, use_quantized_grad=1)
+    ref = O.train(bins, n, f, 255, y, p, missing_bin=mb)
+    cat_nodes = (fit.feature >= 0) & (fit.threshold < 0)
+    assert cat_nodes.sum() > 0 and ((fit.feature >= 0) & (fit.threshold >= 0)).sum() > 0
+    compare(fit, ref, n)
+    # the device predictor routes the sets as the host one does
+    raw, _ = ref.predict_binned(bins, n, f)
+    assert np.array_equal(bits(fit.predict_binned(bins, n, f)), bits(raw))
+
+
+def test_training_categorical_onehot_and_small_groups(dev):
+    """One-vs-rest (3 categories <= max_cat_to_onehot - 1), a CatBoost
+    one_hot_max_size override, and small min_data_per_group / cat_smooth so
+    the sorted walk's guards and caps engage."""
+    n = 40_000
+    x, z, cat_idx = cat_data(n, seed=11, cards=(3, 6, 17), n_num=2)
+    y = z + 0.2 * np.random.default_rng(1).normal(size=n)
+    f = x.shape[0]
+    bins, mb, nc = dev.bin_dense(x.ravel(), n, f, max_bins=63, categorical=cat_idx)
+    for extra in (dict(max_cat_to_onehot=4, max_cat_threshold=3, cat_smooth=2.0, cat_l2=1.0,
+                       min_data_per_group=5, one_hot_max_size=-1),
+                  dict(max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
+                       min_data_per_group=50, one_hot_max_size=6)):
+        kw = dict(objective=0, num_iterations=6, num_leaves=15, min_data_in_leaf=5, lambda_l2=1.0,
+                  learning_rate=0.2)
+        fit = dev.Dataset(bins, n, f, 63, y, missing_bin=mb, n_categories=nc).train(**kw, **extra)
+        p, keep = O.categorical_params(nc, **kw, **extra, use_quantized_grad=1)
+        ref = O.train(bins, n, f, 63, y, p, missing_bin=mb)
+        compare(fit, ref, n)
+
+
+def test_categorical_needs_the_quantized_path(dev):
+    n = 5_000
+    x, z, cat_idx = cat_data(n, seed=2, cards=(5,), n_num=1)
+    bins, mb, nc = dev.bin_dense(x.ravel(), n, 2, max_bins=32, categorical=cat_idx)
+    ds = dev.Dataset(bins, n, 2, 32, z, missing_bin=mb, n_categories=nc)
+    from mojoboost_amd._lib import MojoTreesError
+
+    with pytest.raises(MojoTreesError, match="quantized"):
+        ds.train(objective=0, num_iterations=1, use_quantized_grad=0)
+
+
+def test_estimator_categorical_through_c_abi(dev, tmp_path):
+    from mojoboost_amd.sklearn import MojoTreesRegressor
+
+    n = 60_000
+    x, z, cat_idx = cat_data(n, seed=5, cards=(7, 30))
+    X = np.ascontiguousarray(x.T)
+    X[np.random.default_rng(4).uniform(size=n) < 0.03, cat_idx[0]] = np.nan  # missing codes
+    y = z + 0.1 * np.random.default_rng(9).normal(size=n)
+    est = MojoTreesRegressor(n_estimators=8, num_leaves=31, max_bin=63, device="gpu",
+                             use_quantized_grad=True, categorical_feature=cat_idx, min_data_per_group=50)
+    est.fit(X, y)
+    pred = est.predict(X)
+    # the oracle on the library's own bins of the same matrix
+    f = x.shape[0]
+    bins, mb, nc = dev.bin_dense(np.ascontiguousarray(X.T).ravel(), n, f, max_bins=63, categorical=cat_idx)
+    p, keep = O.categorical_params(nc, objective=0, num_iterations=8, num_leaves=31, learning_rate=0.1,
+                                   min_data_in_leaf=20, lambda_l2=1.0, min_sum_hessian=1e-3,
+                                   use_quantized_grad=1, max_cat_to_onehot=4, max_cat_threshold=32,
+                                   cat_smooth=10.0, cat_l2=10.0, min_data_per_group=50)
+    ref = O.train(bins, n, f, 63, y, p, missing_bin=mb)
+    want, _ = ref.predict_binned(bins, n, f)
+    assert np.array_equal(bits(pred), bits(want))
+    # unseen codes predict like missing ones: right at every categorical node
+    Xu = X[:100].copy()
+    Xm = X[:100].copy()
+    Xu[:, cat_idx[1]] = 1000.0
+    Xm[:, cat_idx[1]] = np.nan
+    assert np.array_equal(bits(est.predict(Xu)), bits(est.predict(Xm)))
+    # the file keeps the category tables and sets; device prediction agrees
+    path = tmp_path / "cat.txt"
+    est.save(str(path))
+    text = path.read_text()
+    assert "\ncategorical 6 " in text and "\ncat " in text
+    back = MojoTreesRegressor.load(str(path))
+    assert np.array_equal(bits(back.predict(X)), bits(pred))
+    assert np.array_equal(bits(back.predict(X, device="gpu")), bits(pred))
