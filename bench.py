@@ -130,9 +130,10 @@ WORKLOADS = {
                dtype="int8 g/h, int32 cells"),
     "c5": dict(rows=2_000_000, features=50, max_bin=255, leaves=63, trees=100, classes=10,
                gh_bytes=2, params=dict(objective=2, num_class=10, use_quantized_grad=1),
-               cpu_sample=2, desc="C5: 2M x 50 (10 integer columns split as ordered bins) softmax, 10 classes, "
-                    "max_bin 255, num_leaves 63, quantized gradients per class; a step is "
-                    "one round of 10 trees",
+               cpu_sample=2, categorical=list(range(40, 50)),
+               desc="C5: 2M x 50 (40 continuous, 10 integer columns of cardinality 4-64 split as "
+                    "category sets) softmax, 10 classes, max_bin 255, num_leaves 63, quantized "
+                    "gradients per class; a step is one round of 10 trees",
                dtype="int8 g/h, int32 cells"),
 }
 
@@ -247,12 +248,17 @@ def main():
         args.cpu_trees = wl["cpu_sample"]
     t0 = time.perf_counter()
     x, y = workload_data(args.workload, args.rows)
-    bins, missing = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB)
+    cats = wl.get("categorical")
+    n_cat = None
+    if cats:
+        bins, missing, n_cat = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB, categorical=cats)
+    else:
+        bins, missing = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB)
     del x
     t_data = time.perf_counter() - t0
     print(f"[bench] {args.workload}: data {args.rows}x{F} generated+binned in {t_data:.1f}s, "
           f"label mean {y.mean():.3f}", file=sys.stderr, flush=True)
-    ds = device.Dataset(bins, args.rows, F, NB, y, missing_bin=missing)
+    ds = device.Dataset(bins, args.rows, F, NB, y, missing_bin=missing, n_categories=n_cat)
     kw = dict(num_leaves=L, min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1,
               num_grad_quant_bins=4, stochastic_rounding=1, **wl["params"])
     if args.warmup > 0:
@@ -287,6 +293,8 @@ def main():
         oparams = {k: v for k, v in kw.items() if k not in ("num_grad_quant_bins", "stochastic_rounding")}
         p = O.default_params(num_iterations=args.cpu_trees, num_grad_quant_bins=4, n_threads=cores,
                              **oparams)
+        if n_cat is not None:
+            p.n_categories = n_cat.ctypes.data  # n_cat outlives the oracle call
         tc = time.perf_counter()
         ref = O.train(bins, args.rows, F, NB, y, p, missing_bin=missing)
         cpu_s = time.perf_counter() - tc
@@ -294,7 +302,7 @@ def main():
         a, b = ref.off[k], fit.off[k]
         same_shape = bool(a == b and all(
             np.array_equal(getattr(ref, f)[:a], getattr(fit, f)[:b])
-            for f in ("feature", "threshold", "left", "right", "default_left")))
+            for f in ("feature", "threshold", "left", "right", "default_left", "cat_bits")))
         if wl["params"].get("use_quantized_grad"):
             parity = same_shape and bool(np.array_equal(ref.value[:a].view(np.uint64),
                                                         fit.value[:b].view(np.uint64)))
