@@ -164,7 +164,11 @@ struct PinnedFlags {
 constexpr size_t kPbStaticLds = 2048;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
 // trees reaches the tree's depth in iterations with 32).
-constexpr int kMaxBatch = 32;
+#ifndef MB_MAX_BATCH
+#define MB_MAX_BATCH 32
+#endif
+constexpr int kMaxBatch = MB_MAX_BATCH;  // at most 64 (the planner's one-wave batch steps)
+static_assert(kMaxBatch >= 1 && kMaxBatch <= 64, "batch of 1..64 leaves");
 // Expansion iterations ([partition, accumulation, scan, plan]) per group of
 // launches between done-flag reads: the first group of a tree is as long as
 // the previous tree needed (kFirstGroup for the first tree), later ones
@@ -204,8 +208,6 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     if (ds->any_cat) {
         // CategoricalParams.check_one_hot (categorical.mojo:216-240) and
         // the search's own bounds
-        if (!p->use_quantized_grad)
-            unsup("categorical features are served on the quantized-gradient path (use_quantized_grad=true)");
         if (!(p->cat_smooth > 0.0)) bad("cat_smooth must be positive");
         if (!(p->cat_l2 >= 0.0)) bad("cat_l2 must be non-negative");
         if (p->max_cat_threshold < 1) bad("max_cat_threshold must be positive");

@@ -1820,6 +1820,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
     __shared__ double pg_[2][256], ph_[2][256];
     __shared__ int pc_[2][256];
     __shared__ double accg[256], acch[256];
+    __shared__ double ckey[2][256];
+    __shared__ int csort[2][256];
+    __shared__ int cwcnt[8];
+    __shared__ double cdg[2][2];
+    __shared__ int cdi[2][2];
+    __shared__ long long cdl[2][2];
     __shared__ int accc[256];
     __shared__ double s_tg[2], s_th[2], s_sg[2], s_sh[2];
     __shared__ long long s_tc[2];
@@ -1966,7 +1972,94 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
         double best_gain = 0.0;
         int best_order = 0x7FFFFFFF;
         long long best_left = 0;
-        if (!gated) {
+        // a categorical feature: category sets over the Float64 cells, the
+        // oracle's arithmetic (categorical.find_best_categorical_split,
+        // categorical.mojo:684-782) with the totals above; the walk adds the
+        // sorted categories' sums in order, one thread per direction
+        const int ncf = s.ncat ? s.ncat[f] : 0;  // block-uniform
+        const bool cat_onehot = ncf > 0 && (hp.one_hot_max_size >= 0 ? ncf <= hp.one_hot_max_size
+                                                                      : ncf + 1 <= hp.max_cat_to_onehot);
+        bool cat_sorted = false;
+        auto leaf = [&](double g, double h, double l2x) {
+            const double tl = soft_threshold_l1(g, l1);
+            return tl * tl / (h + l2x);
+        };
+        if (ncf > 0) {
+            const double parent = leaf(TG, TH, l2);
+            const double vg = cg[child][bin], vh = ch[child][bin];
+            const long long vc = cc[child][bin];
+            if (cat_onehot) {
+                if (!gated && ncf >= 2 && bin >= 1 && bin <= ncf && !(vc < min_c || vh < min_h) &&
+                    !(TC - vc < min_c) && !(TH - vh < min_h)) {
+                    const double gain = leaf(vg, vh, l2) + leaf(TG - vg, TH - vh, l2) - parent;
+                    if (gain > best_gain) {
+                        best_gain = gain;
+                        best_order = bin;
+                        best_left = vc;
+                    }
+                }
+            } else {
+                cat_sorted = true;
+                const bool cand = !gated && ncf >= 2 && bin >= 1 && bin <= ncf && (double)vc >= hp.cat_smooth;
+                const double key = vg / (vh + hp.cat_smooth);
+                ckey[child][bin] = cand ? key : 0.0;
+                const unsigned long long cm = __ballot(cand);
+                if (lane == 0) cwcnt[wv] = __popcll(cm);
+                csort[child][bin] = cand ? 1 : 0;
+                __syncthreads();
+                int rank = 0;
+                if (cand)
+                    for (int u = 1; u <= ncf; ++u) {
+                        const double ku = ckey[child][u];
+                        rank += (csort[child][u] != 0 && (ku < key || (ku == key && u < bin))) ? 1 : 0;
+                    }
+                const int used = cwcnt[child << 2] + cwcnt[(child << 2) + 1] + cwcnt[(child << 2) + 2] +
+                                 cwcnt[(child << 2) + 3];
+                __syncthreads();
+                if (cand) csort[child][rank] = bin;
+                __syncthreads();
+                const int dthr = (tid & 255) >> 6;
+                if (lane == 0 && dthr < 2) {
+                    const int d = dthr;
+                    double dg = 0.0;
+                    int di = -1;
+                    long long dl_ = 0;
+                    if (used >= 2) {
+                        int max_num_cat = hp.max_cat_threshold;
+                        if ((used + 1) / 2 < max_num_cat) max_num_cat = (used + 1) / 2;
+                        if (max_num_cat < 0) max_num_cat = 0;
+                        const int steps = used < max_num_cat ? used : max_num_cat;
+                        const double l2c = l2 + hp.cat_l2;
+                        double ag = 0.0, ah = 0.0;
+                        long long ac = 0, agg = 0;
+                        for (int i = 0; i < steps; ++i) {
+                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
+                            const long long c_ = cc[child][tb];
+                            ag = ag + cg[child][tb];
+                            ah = ah + ch[child][tb];
+                            ac += c_;
+                            agg += c_;
+                            if (ac < min_c || ah < min_h) continue;
+                            const long long rc = TC - ac;
+                            if (rc < min_c || rc < hp.min_data_per_group) break;
+                            if (TH - ah < min_h) break;
+                            if (agg < hp.min_data_per_group) continue;
+                            agg = 0;
+                            const double gain = leaf(ag, ah, l2c) + leaf(TG - ag, TH - ah, l2c) - parent;
+                            if (gain > dg) {
+                                dg = gain;
+                                di = i;
+                                dl_ = ac;
+                            }
+                        }
+                    }
+                    cdg[child][d] = dg;
+                    cdi[child][d] = di;
+                    cdl[child][d] = dl_;
+                }
+                __syncthreads();
+            }
+        } else if (!gated) {
             const double mg = mbf >= 0 ? cg[child][mbf] : 0.0, mh = mbf >= 0 ? ch[child][mbf] : 0.0;
             const long long mc = mbf >= 0 ? cc[child][mbf] : 0;
             const int n_scan = mbf >= 0 ? mbf : nb;
@@ -2032,18 +2125,52 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
                 }
             }
             ScanResult rs;
-            rs.gain = bgn;
-            rs.found = bo != 0x7FFFFFFF;
-            rs.bin = rs.found ? bo >> 1 : -1;
-            rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
-            rs.cat = 0;
+            unsigned long long cbits[4] = {0ULL, 0ULL, 0ULL, 0ULL};
+            if (ncf > 0) {
+                rs.gain = 0.0;
+                rs.found = 0;
+                rs.n_left = 0;
+                if (cat_sorted) {
+                    int d = -1;
+                    if (cdi[child][0] >= 0) d = 0;
+                    if (cdi[child][1] >= 0 && (d < 0 || cdg[child][1] > cdg[child][0])) d = 1;
+                    if (d >= 0) {
+                        int used = 0;
+                        for (int k = 0; k < 4; ++k) used += cwcnt[(child << 2) + k];
+                        for (int i = 0; i <= cdi[child][d]; ++i) {
+                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
+                            cbits[tb >> 6] |= 1ULL << (tb & 63);
+                        }
+                        rs.gain = cdg[child][d];
+                        rs.found = 1;
+                        rs.n_left = cdl[child][d];
+                    }
+                } else if (bo != 0x7FFFFFFF) {
+                    cbits[bo >> 6] |= 1ULL << (bo & 63);
+                    rs.gain = bgn;
+                    rs.found = 1;
+                    rs.n_left = bleft;
+                }
+                rs.bin = -1;
+                rs.default_left = 0;
+                rs.cat = rs.found;
+            } else {
+                rs.gain = bgn;
+                rs.found = bo != 0x7FFFFFFF;
+                rs.bin = rs.found ? bo >> 1 : -1;
+                rs.default_left = rs.found ? ((bo & 1) == 0) : 0;
+                rs.cat = 0;
+                rs.n_left = rs.found ? bleft : 0;
+            }
             rs.tot_g = 0;
             rs.tot_h = 0;
             rs.tot_c = TC;
-            rs.n_left = rs.found ? bleft : 0;
             rs.fg = s_sg[child];
             rs.fh = s_sh[child];
-            s.scan[(size_t)(j * 2 + child) * F + f] = rs;
+            const size_t ri = (size_t)(j * 2 + child) * F + f;
+            s.scan[ri] = rs;
+            if (ncf > 0)
+                for (int w = 0; w < 4; ++w) s.scan_cat[ri * 4 + w] = cbits[w];
         }
         __syncthreads();
     }

@@ -101,15 +101,29 @@ def test_training_categorical_onehot_and_small_groups(dev):
         compare(fit, ref, n)
 
 
-def test_categorical_needs_the_quantized_path(dev):
-    n = 5_000
-    x, z, cat_idx = cat_data(n, seed=2, cards=(5,), n_num=1)
-    bins, mb, nc = dev.bin_dense(x.ravel(), n, 2, max_bins=32, categorical=cat_idx)
-    ds = dev.Dataset(bins, n, 2, 32, z, missing_bin=mb, n_categories=nc)
-    from mojoboost_amd._lib import MojoTreesError
-
-    with pytest.raises(MojoTreesError, match="quantized"):
-        ds.train(objective=0, num_iterations=1, use_quantized_grad=0)
+def test_training_categorical_fp32(dev):
+    """fp32 gradients with fp64 histogram sums (the reference's own path):
+    the sums differ from the oracle's only in rounding order, so the bar is
+    the fp32 one -- the same splits and category sets, values within 1e-5
+    relative, raw scores within 1e-5."""
+    n = 80_000
+    x, z, cat_idx = cat_data(n, seed=13, cards=(3, 12, 50))
+    y = z + 0.1 * np.random.default_rng(3).normal(size=n)
+    f = x.shape[0]
+    bins, mb, nc = dev.bin_dense(x.ravel(), n, f, max_bins=255, categorical=cat_idx)
+    kw = dict(objective=0, num_iterations=6, num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.1)
+    fit = dev.Dataset(bins, n, f, 255, y, missing_bin=mb, n_categories=nc).train(
+        **kw, **CAT, use_quantized_grad=0)
+    p, keep = O.categorical_params(nc, **kw, **CAT, use_quantized_grad=0)
+    ref = O.train(bins, n, f, 255, y, p, missing_bin=mb)
+    assert fit.n_trees == ref.n_trees
+    for k in ("feature", "threshold", "left", "right", "default_left"):
+        assert np.array_equal(getattr(fit, k), getattr(ref, k)), k
+    assert np.array_equal(fit.cat_bits, ref.cat_bits)
+    assert ((fit.feature >= 0) & (fit.threshold < 0)).sum() > 0
+    assert np.allclose(fit.value, ref.value, rtol=1e-5, atol=1e-12)
+    assert np.allclose(fit.train_raw(), ref.train_raw(n), rtol=1e-5, atol=1e-9)
 
 
 def test_estimator_categorical_through_c_abi(dev, tmp_path):
