@@ -105,6 +105,14 @@ __device__ __forceinline__ unsigned wave_min_u32(unsigned x) {
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
+// Lane l's binary64 value on every lane (l wave-uniform).
+__device__ __forceinline__ double rl_f64(double d, int l) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(d);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // Sum of a 32-bit value over the 64 lanes, the same DPP steps as
 // wave_max_u32 but with lanes a control does not cover reading 0 (the
 // identity of the sum), returned wave-uniform.
@@ -1629,8 +1637,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
                 __syncthreads();
                 if (cand) csort[child][rank] = bin;
                 __syncthreads();
-                const int dthr = (tid & 255) >> 6;  // waves 0 and 1 of the half walk directions 0 and 1
-                if (lane == 0 && dthr < 2) {
+                // each direction's wave: its lanes load the steps' cells, a
+                // uniform pass adds them in the walk's order and takes the
+                // walk's decisions (continue / break / min_data_per_group
+                // groups), then the evaluated steps are scored in parallel;
+                // the first maximum wins (strict '>' along the walk)
+                const int dthr = (tid & 255) >> 6;  // waves 0 and 1 of the half: directions 0 and 1
+                if (dthr < 2) {
                     const int d = dthr;
                     double dg = 0.0;
                     int di = -1;
@@ -1641,31 +1654,68 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
                         if (max_num_cat < 0) max_num_cat = 0;
                         const int steps = used < max_num_cat ? used : max_num_cat;
                         const double l2c = l2 + hp.cat_l2;
-                        long long agg = 0, ag = 0, ah = 0, ac = 0;
-                        for (int i = 0; i < steps; ++i) {
-                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
-                            const int c_ = cc[child][tb];
-                            ag += cg[child][tb];
-                            ah += ch[child][tb];
-                            ac += c_;
-                            agg += c_;
-                            if (ac < min_c || ah < hmin) continue;
-                            const long long rc = TC - ac;
-                            if (rc < min_c || rc < hp.min_data_per_group) break;
-                            if (TH - ah < hmin) break;
-                            if (agg < hp.min_data_per_group) continue;
-                            agg = 0;
-                            const double gain = qscore(ag, ah, gu, hu, l1, l2c) + qscore(TG - ag, TH - ah, gu, hu, l1, l2c) - parent;
-                            if (gain > dg) {
-                                dg = gain;
-                                di = i;
-                                dl_ = ac;
+                        long long ag = 0, ah = 0;
+                        long long ac = 0, agg = 0;
+                        bool stop = false;
+                        for (int c0 = 0; c0 < steps && !stop; c0 += 64) {
+                            const int i = c0 + lane;
+                            const bool in = i < steps;
+                            const int tb = in ? csort[child][d == 0 ? i : used - 1 - i] : 0;
+                            const int xg = in ? cg[child][tb] : 0, xh = in ? ch[child][tb] : 0;
+                            const int xc = in ? cc[child][tb] : 0;
+                            long long mg = 0, mh = 0;
+                            long long mc = 0;
+                            bool mev = false;
+                            const int n_here = steps - c0 < 64 ? steps - c0 : 64;
+                            for (int k = 0; k < n_here; ++k) {
+                                ag += __builtin_amdgcn_readlane(xg, k);
+                                ah += __builtin_amdgcn_readlane(xh, k);
+                                const long long kc = __builtin_amdgcn_readlane(xc, k);
+                                ac += kc;
+                                agg += kc;
+                                bool ev = false;
+                                if (!(ac < min_c || ah < hmin)) {
+                                    const long long rc = TC - ac;
+                                    if (rc < min_c || rc < hp.min_data_per_group || TH - ah < hmin) {
+                                        stop = true;
+                                        break;
+                                    }
+                                    if (agg >= hp.min_data_per_group) {
+                                        ev = true;
+                                        agg = 0;
+                                    }
+                                }
+                                if (lane == k) {
+                                    mg = ag;
+                                    mh = ah;
+                                    mc = ac;
+                                    mev = ev;
+                                }
+                            }
+                            double bg = 0.0;
+                            int bo = 0x7FFFFFFF;
+                            if (mev) {
+                                const double g_ = qscore(mg, mh, gu, hu, l1, l2c) + qscore(TG - mg, TH - mh, gu, hu, l1, l2c) - parent;
+                                if (g_ > 0.0) {
+                                    bg = g_;
+                                    bo = i;
+                                }
+                            }
+                            const int mine = bo;
+                            wave_argmax(bg, bo);
+                            if (bo != 0x7FFFFFFF && bg > dg) {
+                                const unsigned long long wl = __ballot(mine == bo);
+                                dg = bg;
+                                di = bo;
+                                dl_ = __builtin_amdgcn_readlane((int)mc, (int)__builtin_ctzll(wl));
                             }
                         }
                     }
-                    cdg[child][d] = dg;
-                    cdi[child][d] = di;
-                    cdl[child][d] = dl_;
+                    if (lane == 0) {
+                        cdg[child][d] = dg;
+                        cdi[child][d] = di;
+                        cdl[child][d] = dl_;
+                    }
                 }
                 __syncthreads();
             }
@@ -2018,8 +2068,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
                 __syncthreads();
                 if (cand) csort[child][rank] = bin;
                 __syncthreads();
-                const int dthr = (tid & 255) >> 6;
-                if (lane == 0 && dthr < 2) {
+                // each direction's wave: its lanes load the steps' cells, a
+                // uniform pass adds them in the walk's order and takes the
+                // walk's decisions (continue / break / min_data_per_group
+                // groups), then the evaluated steps are scored in parallel;
+                // the first maximum wins (strict '>' along the walk)
+                const int dthr = (tid & 255) >> 6;  // waves 0 and 1 of the half: directions 0 and 1
+                if (dthr < 2) {
                     const int d = dthr;
                     double dg = 0.0;
                     int di = -1;
@@ -2032,30 +2087,66 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
                         const double l2c = l2 + hp.cat_l2;
                         double ag = 0.0, ah = 0.0;
                         long long ac = 0, agg = 0;
-                        for (int i = 0; i < steps; ++i) {
-                            const int tb = csort[child][d == 0 ? i : used - 1 - i];
-                            const long long c_ = cc[child][tb];
-                            ag = ag + cg[child][tb];
-                            ah = ah + ch[child][tb];
-                            ac += c_;
-                            agg += c_;
-                            if (ac < min_c || ah < min_h) continue;
-                            const long long rc = TC - ac;
-                            if (rc < min_c || rc < hp.min_data_per_group) break;
-                            if (TH - ah < min_h) break;
-                            if (agg < hp.min_data_per_group) continue;
-                            agg = 0;
-                            const double gain = leaf(ag, ah, l2c) + leaf(TG - ag, TH - ah, l2c) - parent;
-                            if (gain > dg) {
-                                dg = gain;
-                                di = i;
-                                dl_ = ac;
+                        bool stop = false;
+                        for (int c0 = 0; c0 < steps && !stop; c0 += 64) {
+                            const int i = c0 + lane;
+                            const bool in = i < steps;
+                            const int tb = in ? csort[child][d == 0 ? i : used - 1 - i] : 0;
+                            const double xg = in ? cg[child][tb] : 0.0, xh = in ? ch[child][tb] : 0.0;
+                            const int xc = in ? (int)cc[child][tb] : 0;
+                            double mg = 0.0, mh = 0.0;
+                            long long mc = 0;
+                            bool mev = false;
+                            const int n_here = steps - c0 < 64 ? steps - c0 : 64;
+                            for (int k = 0; k < n_here; ++k) {
+                                ag = ag + rl_f64(xg, k);
+                                ah = ah + rl_f64(xh, k);
+                                const long long kc = __builtin_amdgcn_readlane(xc, k);
+                                ac += kc;
+                                agg += kc;
+                                bool ev = false;
+                                if (!(ac < min_c || ah < min_h)) {
+                                    const long long rc = TC - ac;
+                                    if (rc < min_c || rc < hp.min_data_per_group || TH - ah < min_h) {
+                                        stop = true;
+                                        break;
+                                    }
+                                    if (agg >= hp.min_data_per_group) {
+                                        ev = true;
+                                        agg = 0;
+                                    }
+                                }
+                                if (lane == k) {
+                                    mg = ag;
+                                    mh = ah;
+                                    mc = ac;
+                                    mev = ev;
+                                }
+                            }
+                            double bg = 0.0;
+                            int bo = 0x7FFFFFFF;
+                            if (mev) {
+                                const double g_ = leaf(mg, mh, l2c) + leaf(TG - mg, TH - mh, l2c) - parent;
+                                if (g_ > 0.0) {
+                                    bg = g_;
+                                    bo = i;
+                                }
+                            }
+                            const int mine = bo;
+                            wave_argmax(bg, bo);
+                            if (bo != 0x7FFFFFFF && bg > dg) {
+                                const unsigned long long wl = __ballot(mine == bo);
+                                dg = bg;
+                                di = bo;
+                                dl_ = __builtin_amdgcn_readlane((int)mc, (int)__builtin_ctzll(wl));
                             }
                         }
                     }
-                    cdg[child][d] = dg;
-                    cdi[child][d] = di;
-                    cdl[child][d] = dl_;
+                    if (lane == 0) {
+                        cdg[child][d] = dg;
+                        cdi[child][d] = di;
+                        cdl[child][d] = dl_;
+                    }
                 }
                 __syncthreads();
             }
