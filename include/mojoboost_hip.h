@@ -183,6 +183,17 @@ int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 int32_t mbh_dataset_set_groups(mbh_dataset *ds, const int32_t *counts, int64_t n_queries,
                                char *err, int32_t err_len);
 
+/* Per-row sample weights of a resident dataset (the `sample_weight` of
+ * mojotrees_train_dense, include/capi/mojotrees.h; checked as
+ * boosting._check_sample_weight, src/mojotrees/boosting.mojo:334-343: one
+ * finite, nonnegative weight per row, positive sum). Every later mbh_train
+ * scales each row's gradient and hessian by its weight after the hessian
+ * floor (boosting._fill_grad_hess_into, boosting.mojo:676-811) and boosts
+ * from the weighted mean or weighted class shares. weights == NULL clears
+ * them. Not served with objective lambdarank (MOJOTREES_ERROR_UNSUPPORTED). */
+int32_t mbh_dataset_set_weights(mbh_dataset *ds, const double *weights, int64_t n_weights,
+                                char *err, int32_t err_len);
+
 /* LambdaRank gradients and hessians (binary64) of one set of raw scores on
  * the device (ranking.lambdarank_gradients, src/mojotrees/ranking.mojo:
  * 603-654, unweighted), with the dataset's labels and groups. */

@@ -36,7 +36,7 @@ MBH_SYMBOLS = [
     "mbh_fit_arrays", "mbh_fit_train_raw", "mbh_fit_stats", "mbh_exp_sigmoid",
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
-    "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits",
+    "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
 ]
 
 
@@ -162,6 +162,7 @@ def lib():
         "mbh_dataset_set_categorical": (I32, [V, V, C.c_char_p, I32]),
         "mbh_fit_cat_bits": (None, [V, V]),
         "mbh_dataset_set_groups": (I32, [V, V, I64, C.c_char_p, I32]),
+        "mbh_dataset_set_weights": (I32, [V, V, I64, C.c_char_p, I32]),
         "mbh_lambdarank": (I32, [V, P(MbhParams), V, V, V, C.c_char_p, I32]),
         "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, I64, C.c_char_p, V, V]),
     }

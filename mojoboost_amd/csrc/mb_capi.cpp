@@ -439,7 +439,7 @@ void check_categorical(const Config &c, int64_t n_features) {
 // common body of the training entry points. groups: per-query row counts
 // (lambdarank), or null.
 MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_features, const double *labels,
-                            const int32_t *groups, int64_t n_groups, Config &c) {
+                            const double *weights, const int32_t *groups, int64_t n_groups, Config &c) {
     check_categorical(c, n_features);
     mb::BinMapper mapper = mb::fit_bins(data, n_rows, (int)n_features, c.max_bin, c.min_data_in_bin,
                                         c.use_missing, c.bin_sample, c.data_seed, c.categorical);
@@ -454,6 +454,13 @@ MojoTreesModel *train_model(const double *data, int64_t n_rows, int64_t n_featur
         std::vector<int32_t> ncat(n_features);
         for (int f = 0; f < (int)n_features; ++f) ncat[f] = mapper.n_categories(f);
         rc = mbh_dataset_set_categorical(ds, ncat.data(), msg, sizeof(msg));
+        if (rc != MOJOTREES_OK) {
+            mbh_dataset_free(ds);
+            throw ApiError{rc, msg};
+        }
+    }
+    if (weights) {
+        rc = mbh_dataset_set_weights(ds, weights, n_rows, msg, sizeof(msg));
         if (rc != MOJOTREES_OK) {
             mbh_dataset_free(ds);
             throw ApiError{rc, msg};
@@ -541,8 +548,17 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
         if (c.p.objective == MBH_OBJ_LAMBDARANK)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
                            "objective=lambdarank needs query groups: train it with mbh_train_ranker_dense"};
-        if (weights)
-            throw ApiError{MOJOTREES_ERROR_UNSUPPORTED, "sample weights are not served by the device training path"};
+        if (weights) {
+            // boosting._check_sample_weight (boosting.mojo:334-343), before
+            // any device work so a bad vector is named on any host
+            double total = 0.0;
+            for (int64_t r = 0; r < n_rows; ++r) {
+                if (!std::isfinite(weights[r]) || weights[r] < 0.0)
+                    throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must be finite and nonnegative"};
+                total += weights[r];
+            }
+            if (!(total > 0.0)) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must have a positive sum"};
+        }
         if (c.device == MOJOTREES_DEVICE_CPU)
             throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
                            "device=cpu: this library is the MI355X training path and has no CPU trainer"};
@@ -553,7 +569,7 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
             for (int64_t r = 0; r < n_rows; ++r)
                 if (labels[r] != 0.0 && labels[r] != 1.0)
                     throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "binary labels must be 0 or 1"};
-        MojoTreesModel *model = train_model(data, n_rows, n_features, labels, nullptr, 0, c);
+        MojoTreesModel *model = train_model(data, n_rows, n_features, labels, weights, nullptr, 0, c);
         *out_model = model;
         return MOJOTREES_OK;
     });
@@ -709,7 +725,7 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
         for (int64_t r = 0; r < n_rows; ++r)
             if (!(labels[r] >= 0.0 && labels[r] <= 30.0) || labels[r] != std::floor(labels[r]))
                 throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "relevance labels must be integers in [0, 30]"};
-        *out_model = train_model(data, n_rows, n_features, labels, group_counts, n_groups, c);
+        *out_model = train_model(data, n_rows, n_features, labels, nullptr, group_counts, n_groups, c);
         return MOJOTREES_OK;
     });
 }

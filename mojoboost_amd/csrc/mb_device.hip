@@ -114,6 +114,12 @@ struct mbh_dataset {
     bool any_cat = false;
     double label_sum = 0.0;  // sequential sum, for the base score
     std::vector<double> class_count;  // when labels are integers in [0, 1024)
+    // sample weights (mbh_dataset_set_weights): the weighted label sum, the
+    // weight total and per-class weight, each a sequential sum in row order
+    std::vector<double> weights;
+    double *d_weights = nullptr, *d_weights_buf = nullptr;
+    double wlabel_sum = 0.0, weight_sum = 0.0;
+    std::vector<double> class_weight;
     bool labels_integral = false;
     double label_min = 0.0, label_max = 0.0;
     // lambdarank: labels as relevance grades (when integers in [0, 30]) and
@@ -204,6 +210,7 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         if (p->bagging_freq > 0 && p->bagging_fraction < 1.0)
             unsup("query bagging for lambdarank is not built on the device path");
         if (p->goss) unsup("GOSS with lambdarank is not built on the device path");
+        if (ds->d_weights) unsup("sample weights with lambdarank are not built on the device path");
     }
     if (ds->any_cat) {
         // CategoricalParams.check_one_hot (categorical.mojo:216-240) and
@@ -346,7 +353,7 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantize
 double base_score_for(const mbh_dataset *ds, int objective) {
     // boosting._base_score (src/mojotrees/boosting.mojo:521-568): the
     // sequential label mean; binary takes the clamped log-odds.
-    double mean = ds->label_sum / (double)ds->n;
+    double mean = ds->d_weights ? ds->wlabel_sum / ds->weight_sum : ds->label_sum / (double)ds->n;
     if (objective == MBH_OBJ_BINARY) {
         double p = mean;
         if (p < 1e-15) p = 1e-15;
@@ -364,8 +371,9 @@ std::vector<double> base_scores_for(const mbh_dataset *ds, int objective, int K)
     if (objective != MBH_OBJ_MULTICLASS) return {base_score_for(ds, objective)};
     std::vector<double> b(K);
     for (int k = 0; k < K; ++k) {
-        const double cnt = (size_t)k < ds->class_count.size() ? ds->class_count[k] : 0.0;
-        double p = cnt / (double)ds->n;
+        const std::vector<double> &cc = ds->d_weights ? ds->class_weight : ds->class_count;
+        const double cnt = (size_t)k < cc.size() ? cc[k] : 0.0;
+        double p = cnt / (ds->d_weights ? ds->weight_sum : (double)ds->n);
         if (p < 1e-15) p = 1e-15;
         if (p > 1.0 - 1e-15) p = 1.0 - 1e-15;
         b[k] = mb::ref_log(p);
@@ -393,6 +401,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     s.records_w = ds->d_records;
     s.bins_cm = ds->d_bins_cm;
     s.labels = ds->d_labels;
+    s.weights = ds->d_weights;
     s.missing_bin = ds->d_missing;
     s.widths = ds->d_widths;
     s.ncat = ds->any_cat ? ds->d_ncat : nullptr;
@@ -463,7 +472,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.stochastic = p->stochastic_rounding;
     hp.quant_seed = p->quant_seed;
     // boosting.round_has_constant_hessian: squared error without weights.
-    hp.const_hessian = p->objective == MBH_OBJ_REGRESSION ? 1 : 0;
+    hp.const_hessian = p->objective == MBH_OBJ_REGRESSION && !ds->d_weights ? 1 : 0;
     if (p->objective == MBH_OBJ_LAMBDARANK) {
         // binary64 lambdas (the reference's ranker does not narrow them), the
         // queries, 1 / maxDCG per query at the truncation level and the
@@ -1034,6 +1043,52 @@ int32_t mbh_exp_sigmoid(const double *x, int64_t n, double *out_exp, double *out
         HIPX(mb::launch_exp_sigmoid(dx, de, dsg, n, nullptr));
         HIPX(hipMemcpy(out_exp, de, n * sizeof(double), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(out_sig, dsg, n * sizeof(double), hipMemcpyDeviceToHost));
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_dataset_set_weights(mbh_dataset *ds, const double *weights, int64_t n_weights, char *err,
+                                int32_t err_len) {
+    // boosting._check_sample_weight (src/mojotrees/boosting.mojo:334-343):
+    // one finite, nonnegative weight per row with a positive sum; null clears
+    if (!ds) {
+        set_err(err, err_len, "null dataset");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        if (!weights) {
+            ds->weights.clear();
+            ds->class_weight.clear();
+            ds->d_weights = nullptr;  // the buffer stays owned until the dataset is freed
+            return MOJOTREES_OK;
+        }
+        if (n_weights != ds->n) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight length must equal n_rows"};
+        double total = 0.0, wy = 0.0;
+        for (int64_t r = 0; r < ds->n; ++r) {
+            const double w = weights[r];
+            if (!std::isfinite(w) || w < 0.0)
+                throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must be finite and nonnegative"};
+            total += w;
+        }
+        if (!(total > 0.0)) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must have a positive sum"};
+        // the labels are on the device only; the base score needs Σ w·y
+        std::vector<double> y((size_t)ds->n);
+        HIPX(hipMemcpy(y.data(), ds->d_labels, (size_t)ds->n * sizeof(double), hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < ds->n; ++r) wy += weights[r] * y[r];
+        ds->class_weight.clear();
+        if (ds->labels_integral) {
+            ds->class_weight.assign(ds->class_count.size(), 0.0);
+            for (int64_t r = 0; r < ds->n; ++r) ds->class_weight[(size_t)y[r]] += weights[r];
+        }
+        ds->weights.assign(weights, weights + ds->n);
+        if (!ds->d_weights_buf) ds->d_weights_buf = dalloc<double>(ds->n, ds->owned);
+        HIPX(hipMemcpy(ds->d_weights_buf, weights, (size_t)ds->n * sizeof(double), hipMemcpyHostToDevice));
+        ds->d_weights = ds->d_weights_buf;
+        ds->weight_sum = total;
+        ds->wlabel_sum = wy;
     } catch (const Error &e) {
         set_err(err, err_len, e.msg);
         return e.code;

@@ -207,24 +207,27 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
         float g, h;
+        // boosting._fill_grad_hess_into (boosting.mojo:676-811): the weight
+        // scales both, after the hessian floor
+        const double w = s.weights ? s.weights[r] : 1.0;
         if (hp.objective == kObjMulticlass) {
             // _fill_softmax_grad_hess_at (boosting.mojo:3621-3678) on the
             // probabilities of the round's start
             const double p = s.prob[r * K + ck];
             const double y = ((int)s.labels[r] == ck) ? 1.0 : 0.0;
-            g = (float)(p - y);
+            g = (float)(w * (p - y));
             double hh = factor * p * (1.0 - p);
             if (hh < 1e-16) hh = 1e-16;
-            h = (float)hh;
+            h = (float)(w * hh);
         } else if (hp.objective == kObjBinary) {
             double p = sigmoid(s.raw[r]);
-            g = (float)(p - s.labels[r]);
+            g = (float)(w * (p - s.labels[r]));
             double hh = p * (1.0 - p);
             if (hh < 1e-16) hh = 1e-16;
-            h = (float)hh;
+            h = (float)(w * hh);
         } else {
-            g = (float)(s.raw[r] - s.labels[r]);
-            h = 1.0f;
+            g = (float)(w * (s.raw[r] - s.labels[r]));
+            h = (float)(w * 1.0);
         }
         s.grad[r] = g;
         s.hess[r] = h;
@@ -3377,14 +3380,16 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
     auto objective = [&](int64_t r, double raw, double y) {
         float g, h;
         if (hp.objective == kObjBinary) {
+            const double w = s.weights ? s.weights[r] : 1.0;
             const double p = sigmoid(raw);
-            g = (float)(p - y);
+            g = (float)(w * (p - y));
             double hh = p * (1.0 - p);
             if (hh < 1e-16) hh = 1e-16;
-            h = (float)hh;
+            h = (float)(w * hh);
         } else {
-            g = (float)(raw - y);
-            h = 1.0f;
+            const double w = s.weights ? s.weights[r] : 1.0;
+            g = (float)(w * (raw - y));
+            h = (float)(w * 1.0);
         }
         s.grad[r] = g;
         s.hess[r] = h;

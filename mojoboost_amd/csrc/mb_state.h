@@ -201,6 +201,7 @@ struct DevState {
     const uint8_t *records;
     const uint8_t *bins_cm;  // F x n, column-major (partition, score update)
     const double *labels;    // n
+    const double *weights;   // n sample weights, or null (unweighted)
     const int32_t *missing_bin;  // F
     const int32_t *widths;       // F: realized bin count bound
     const int32_t *ncat;         // F: categories of a categorical feature (bins 1..ncat), 0 numerical; null: none

@@ -42,7 +42,7 @@ class Dataset:
     """A column-major uint8 binned matrix and its labels, uploaded once."""
 
     def __init__(self, bins_cm, n_rows, n_features, n_bins, labels, missing_bin=None,
-                 n_categories=None):
+                 n_categories=None, weights=None):
         L = lib()
         self.n_rows, self.n_features, self.n_bins = int(n_rows), int(n_features), int(n_bins)
         bins_cm = np.ascontiguousarray(bins_cm, dtype=np.uint8).ravel()
@@ -57,6 +57,8 @@ class Dataset:
         self.h = h
         if n_categories is not None:
             self.set_categorical(n_categories)
+        if weights is not None:
+            self.set_weights(weights)
 
     def set_categorical(self, n_categories):
         """n_categories[f] > 0 marks feature f categorical (bins 1..n, bin 0
@@ -75,6 +77,15 @@ class Dataset:
             self.free()
         except Exception:
             pass
+
+    def set_weights(self, weights):
+        """Per-row sample weights for later trainings (None clears them)."""
+        err = C.create_string_buffer(512)
+        if weights is None:
+            check(lib().mbh_dataset_set_weights(self.h, None, 0, err, 512), err)
+            return
+        w = np.ascontiguousarray(weights, np.float64)
+        check(lib().mbh_dataset_set_weights(self.h, ptr(w), w.size, err, 512), err)
 
     def set_groups(self, counts):
         """Query groups for objective lambdarank: rows per query, in row order."""

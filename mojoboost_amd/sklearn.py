@@ -125,14 +125,19 @@ class _Booster:
         return out
 
 
-def _train(X, y, params: str):
+def _train(X, y, params: str, sample_weight=None):
     Xf, n, f = _colmajor(X)
     y = np.ascontiguousarray(y, dtype=np.float64)
     if y.shape[0] != n:
         raise ValueError("y must have one entry per row of X")
+    w = None
+    if sample_weight is not None:
+        w = np.ascontiguousarray(sample_weight, dtype=np.float64)
+        if w.shape != (n,):
+            raise ValueError("sample_weight length must equal n_rows")
     h = C.c_void_p()
     e = _Error()
-    e.check(lib().mojotrees_train_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), None,
+    e.check(lib().mojotrees_train_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), ptr(w),
                                         params.encode(), C.byref(h), e.h))
     return _Booster(h)
 
@@ -232,8 +237,8 @@ class _Base:
 class MojoTreesRegressor(_Base):
     _objective = "regression"
 
-    def fit(self, X, y):
-        self.booster_ = _train(X, y, self._params())
+    def fit(self, X, y, sample_weight=None):
+        self.booster_ = _train(X, y, self._params(), sample_weight)
         return self
 
     def predict(self, X, raw_score=False, start_iteration=0, num_iteration=None, device=None):
@@ -257,17 +262,17 @@ class MojoTreesClassifier(_Base):
     classifier does (python/mojotrees/sklearn.py:6412)."""
     _objective = "binary"
 
-    def fit(self, X, y):
+    def fit(self, X, y, sample_weight=None):
         y = np.asarray(y)
         self.classes_, yi = np.unique(y, return_inverse=True)
         k = len(self.classes_)
         if k < 2:
             raise ValueError("y needs at least two classes")
         if k == 2:
-            self.booster_ = _train(X, yi.astype(np.float64), self._params())
+            self.booster_ = _train(X, yi.astype(np.float64), self._params(), sample_weight)
         else:
             params = self._params().replace("objective=binary", "objective=multiclass")
-            self.booster_ = _train(X, yi.astype(np.float64), params + f" num_class={k}")
+            self.booster_ = _train(X, yi.astype(np.float64), params + f" num_class={k}", sample_weight)
         return self
 
     def predict_proba(self, X, start_iteration=0, num_iteration=None, device=None):

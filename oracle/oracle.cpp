@@ -1371,16 +1371,18 @@ struct orc_model {
 namespace {
 
 void fill_grad_hess(int objective, const double *raw, const double *labels,
-                    int64_t n, int k, int kk, double *grad, double *hess) {
+                    int64_t n, int k, int kk, double *grad, double *hess, const double *weights = nullptr) {
     // boosting._fill_grad_hess_into (src/mojotrees/boosting.mojo:676-811)
-    // and _fill_softmax_grad_hess_at (:3621-3678); unweighted, narrowed.
+    // and _fill_softmax_grad_hess_at (:3621-3678), narrowed; w = 1.0 when
+    // unweighted (the reference multiplies by it either way).
     if (objective == ORC_OBJ_BINARY) {
         for (int64_t r = 0; r < n; ++r) {
             double p = sigmoid(raw[r]);
-            grad[r] = narrow(1.0 * (p - labels[r]));
+            const double w = weights ? weights[r] : 1.0;
+            grad[r] = narrow(w * (p - labels[r]));
             double h = p * (1.0 - p);
             if (h < 1e-16) h = 1e-16;
-            hess[r] = narrow(1.0 * h);
+            hess[r] = narrow(w * h);
         }
     } else if (objective == ORC_OBJ_MULTICLASS) {
         double factor = (double)k / (double)(k - 1);
@@ -1388,15 +1390,17 @@ void fill_grad_hess(int objective, const double *raw, const double *labels,
             // raw holds probabilities here (softmax already applied).
             double p = raw[r * k + kk];
             double y = ((int)labels[r] == kk) ? 1.0 : 0.0;
-            grad[r] = narrow(1.0 * (p - y));
+            const double w = weights ? weights[r] : 1.0;
+            grad[r] = narrow(w * (p - y));
             double h = factor * p * (1.0 - p);
             if (h < 1e-16) h = 1e-16;
-            hess[r] = narrow(1.0 * h);
+            hess[r] = narrow(w * h);
         }
     } else {
         for (int64_t r = 0; r < n; ++r) {
-            grad[r] = narrow(1.0 * (raw[r] - labels[r]));
-            hess[r] = narrow(1.0);
+            const double w = weights ? weights[r] : 1.0;
+            grad[r] = narrow(w * (raw[r] - labels[r]));
+            hess[r] = narrow(w * 1.0);
         }
     }
 }
@@ -1655,6 +1659,11 @@ int32_t orc_grad_hess(int32_t objective, const double *raw, const double *labels
     fill_grad_hess(objective, raw, labels, n, num_class, class_k, grad, hess);
     return 0;
 }
+int32_t orc_grad_hess_w(int32_t objective, const double *raw, const double *labels, const double *weights,
+                        int64_t n, int32_t num_class, int32_t class_k, double *grad, double *hess) {
+    fill_grad_hess(objective, raw, labels, n, num_class, class_k, grad, hess, weights);
+    return 0;
+}
 
 int32_t orc_quantize(const double *grad, const double *hess, int64_t n,
                      const int32_t *rows, int64_t n_sel, int32_t quant_bins,
@@ -1817,7 +1826,7 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
         m->num_class = K;
         m->round_seconds.assign(P.p.num_iterations, 0.0);
         // boosting.round_has_constant_hessian: L2, unweighted, no GOSS.
-        P.const_hessian = (P.p.objective == ORC_OBJ_L2) && !P.p.goss;
+        P.const_hessian = (P.p.objective == ORC_OBJ_L2) && !P.p.goss && !P.p.weights;
         std::vector<double> raw((size_t)n * K);
         const bool rank = P.p.objective == ORC_OBJ_LAMBDARANK;
         RankSpec rs;
@@ -1848,8 +1857,9 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
             // boosting._base_score (src/mojotrees/boosting.mojo:521-568)
             double mean = 0.0, tw = 0.0;
             for (int64_t r = 0; r < n; ++r) {
-                mean += 1.0 * labels[r];
-                tw += 1.0;
+                const double w = P.p.weights ? P.p.weights[r] : 1.0;
+                mean += w * labels[r];
+                tw += w;
             }
             mean /= tw;
             double base = mean;
@@ -1865,8 +1875,9 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
             std::vector<double> cw(K, 0.0);
             double tw = 0.0;
             for (int64_t r = 0; r < n; ++r) {
-                cw[(int)labels[r]] += 1.0;
-                tw += 1.0;
+                const double w = P.p.weights ? P.p.weights[r] : 1.0;
+                cw[(int)labels[r]] += w;
+                tw += w;
             }
             for (int k = 0; k < K; ++k) m->base.push_back(ref_log(clamp_prob(cw[k] / tw)));
             for (int64_t r = 0; r < n; ++r)
@@ -1884,7 +1895,7 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
                 if (rank)
                     fill_lambdas(raw.data(), rank_labels, rs, inv_max_dcg, rank_disc, grad.data(), hess.data());
                 else
-                    fill_grad_hess(P.p.objective, raw.data(), labels, n, 1, 0, grad.data(), hess.data());
+                    fill_grad_hess(P.p.objective, raw.data(), labels, n, 1, 0, grad.data(), hess.data(), P.p.weights);
                 goss_round(bag, grad, hess, P.p, it);
                 Tree t = grow_one(d, P, grad, hess, bag, it, 0, it, leaves, qg, qh, pool);
                 if (t.n_leaves == 1 && std::fabs(t.value[0]) < 1e-12) {
@@ -1902,7 +1913,7 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
                 std::vector<Tree> round_trees;
                 for (int k = 0; k < K; ++k) {
                     fill_grad_hess(ORC_OBJ_MULTICLASS, prob.data(), labels, n, K, k,
-                                   grad.data(), hess.data());
+                                   grad.data(), hess.data(), P.p.weights);
                     Tree t = grow_one(d, P, grad, hess, bag, it, k, (int64_t)it * K + k,
                                       leaves, qg, qh, pool);
                     if (t.n_leaves > 1 || std::fabs(t.value[0]) >= 1e-12) progress = true;

@@ -70,6 +70,10 @@ typedef struct {
     double cat_l2;              /* 10 */
     int32_t min_data_per_group; /* 100 */
     int32_t one_hot_max_size;   /* -1: off (CatBoost's one-hot rule when >= 0) */
+    /* per-row sample weights (n_rows), or NULL for unweighted: they scale
+     * each row's gradient and hessian and weight the base score / class
+     * priors (boosting._fill_grad_hess_into, _base_score, train_multiclass) */
+    const double *weights;
 } orc_params;
 
 /* A trained model in flat arrays. Trees are laid out one after another;
@@ -107,6 +111,11 @@ int32_t orc_grad_hess(int32_t objective, const double *raw,
                       const double *labels, int64_t n_rows,
                       int32_t num_class, int32_t class_k, double *grad,
                       double *hess);
+/* The same with per-row weights (NULL: unweighted). */
+int32_t orc_grad_hess_w(int32_t objective, const double *raw,
+                        const double *labels, const double *weights,
+                        int64_t n_rows, int32_t num_class, int32_t class_k,
+                        double *grad, double *hess);
 
 /* ----------------------------------------------------------- quantization */
 /* gradient_stats + derive_scales (max-abs rule) + per-row rounding.

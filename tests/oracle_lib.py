@@ -58,6 +58,7 @@ class Params(C.Structure):
         ("cat_l2", C.c_double),
         ("min_data_per_group", C.c_int32),
         ("one_hot_max_size", C.c_int32),
+        ("weights", C.c_void_p),
     ]
 
 
@@ -73,7 +74,7 @@ def default_params(**kw) -> Params:
         fused_predict=1, totals_tree_reduce=1, use_init_base=0, init_base=0.0,
         query_starts=None, n_queries=0, lambdarank_truncation_level=30, lambdarank_norm=1,
         lambdarank_sigmoid=1.0, n_categories=None, max_cat_to_onehot=4, max_cat_threshold=32,
-        cat_smooth=10.0, cat_l2=10.0, min_data_per_group=100, one_hot_max_size=-1,
+        cat_smooth=10.0, cat_l2=10.0, min_data_per_group=100, one_hot_max_size=-1, weights=None,
     )
     for k, v in kw.items():
         setattr(p, k, v)
@@ -157,6 +158,9 @@ def lib():
                                       C.c_int32, C.c_int64, C.c_void_p, C.c_void_p,
                                       P(C.c_int64)]
         L.orc_model_cat_bits.argtypes = [C.c_void_p, C.c_void_p]
+        L.orc_grad_hess_w.restype = C.c_int32
+        L.orc_grad_hess_w.argtypes = [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                      C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]
         L.orc_cat_split.restype = C.c_int32
         L.orc_cat_split.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_double, C.c_double,
                                     C.c_int64, C.c_double, C.c_double, C.c_double, C.c_int32,
@@ -266,6 +270,17 @@ def grad_hess(objective, raw, labels, num_class=1, class_k=0):
     return g, h
 
 
+def grad_hess_w(objective, raw, labels, weights, num_class=1, class_k=0):
+    n = len(labels)
+    g = np.zeros(n)
+    h = np.zeros(n)
+    lib().orc_grad_hess_w(objective, _ptr(np.ascontiguousarray(raw, np.float64)),
+                          _ptr(np.ascontiguousarray(labels, np.float64)),
+                          _ptr(np.ascontiguousarray(weights, np.float64)), n, num_class, class_k,
+                          _ptr(g), _ptr(h))
+    return g, h
+
+
 def quantize(grad, hess, rows=None, quant_bins=4, stochastic=1, seed=11, round_index=0,
              class_index=0, const_hessian=0):
     n = len(grad)
@@ -353,6 +368,15 @@ def categorical_params(n_categories, **kw):
     p = default_params(**kw)
     p.n_categories = nc.ctypes.data
     return p, nc
+
+
+def weighted_params(weights, **kw):
+    """default_params with per-row sample weights; the returned array must
+    outlive the params."""
+    w = np.ascontiguousarray(weights, np.float64)
+    p = default_params(**kw)
+    p.weights = w.ctypes.data
+    return p, w
 
 
 def cat_split(gh, count, n_categories, total_g=None, total_h=None, total_c=None, lambda_l2=1.0,
