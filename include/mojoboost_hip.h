@@ -208,11 +208,16 @@ int32_t mbh_lambdarank(mbh_dataset *ds, const mbh_params *params, const double *
  * reference serves its ranker only from Python (MojoTreesRanker,
  * python/mojotrees/sklearn.py:6951); this entry is what an estimator or a C
  * caller uses here. Parameters as for mojotrees_train_dense plus
- * lambdarank_truncation_level, sigmoid, lambdarank_norm. */
+ * lambdarank_truncation_level, sigmoid, lambdarank_norm. weights: per-row
+ * sample weights scaling each finished lambda and hessian (train_ranker's
+ * sample_weight, ranking.mojo:613-616), or NULL. bagging_fraction /
+ * bagging_freq bag whole queries (ranking._refresh_query_bag,
+ * ranking.mojo:667-686). */
 struct MojoTreesModel;
 struct MojoTreesError;
 int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_features,
-                               const double *labels, const int32_t *group_counts,
+                               const double *labels, const double *weights,
+                               const int32_t *group_counts,
                                int64_t n_groups, const char *parameters,
                                struct MojoTreesModel **out_model, struct MojoTreesError *error);
 

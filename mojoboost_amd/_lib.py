@@ -164,7 +164,7 @@ def lib():
         "mbh_dataset_set_groups": (I32, [V, V, I64, C.c_char_p, I32]),
         "mbh_dataset_set_weights": (I32, [V, V, I64, C.c_char_p, I32]),
         "mbh_lambdarank": (I32, [V, P(MbhParams), V, V, V, C.c_char_p, I32]),
-        "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, I64, C.c_char_p, V, V]),
+        "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, V, I64, C.c_char_p, V, V]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

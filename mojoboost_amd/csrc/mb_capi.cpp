@@ -435,6 +435,19 @@ void check_categorical(const Config &c, int64_t n_features) {
     }
 }
 
+// boosting._check_sample_weight (boosting.mojo:334-343), before any device
+// work so a bad vector is named on any host; null means unweighted
+void check_weights(const double *weights, int64_t n_rows) {
+    if (!weights) return;
+    double total = 0.0;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        if (!std::isfinite(weights[r]) || weights[r] < 0.0)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must be finite and nonnegative"};
+        total += weights[r];
+    }
+    if (!(total > 0.0)) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must have a positive sum"};
+}
+
 // Host binning, the resident dataset, device training and the model: the
 // common body of the training entry points. groups: per-query row counts
 // (lambdarank), or null.
@@ -548,17 +561,7 @@ int32_t mojotrees_train_dense(const double *data, int64_t n_rows, int64_t n_feat
         if (c.p.objective == MBH_OBJ_LAMBDARANK)
             throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
                            "objective=lambdarank needs query groups: train it with mbh_train_ranker_dense"};
-        if (weights) {
-            // boosting._check_sample_weight (boosting.mojo:334-343), before
-            // any device work so a bad vector is named on any host
-            double total = 0.0;
-            for (int64_t r = 0; r < n_rows; ++r) {
-                if (!std::isfinite(weights[r]) || weights[r] < 0.0)
-                    throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must be finite and nonnegative"};
-                total += weights[r];
-            }
-            if (!(total > 0.0)) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "sample_weight must have a positive sum"};
-        }
+        check_weights(weights, n_rows);
         if (c.device == MOJOTREES_DEVICE_CPU)
             throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
                            "device=cpu: this library is the MI355X training path and has no CPU trainer"};
@@ -705,7 +708,7 @@ void mojotrees_string_free(char *text) { std::free(text); }
 void mojotrees_model_free(MojoTreesModel *model) { delete model; }
 
 int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_features, const double *labels,
-                               const int32_t *group_counts, int64_t n_groups, const char *parameters,
+                               const double *weights, const int32_t *group_counts, int64_t n_groups, const char *parameters,
                                MojoTreesModel **out_model, MojoTreesError *error) {
     return guarded(error, [&]() -> int32_t {
         if (!data || !labels || !group_counts || !out_model)
@@ -715,6 +718,7 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
         Config c = parse(parameters);
         check_categorical(c, n_features);
         c.p.objective = MBH_OBJ_LAMBDARANK;
+        check_weights(weights, n_rows);
         if (c.device == MOJOTREES_DEVICE_CPU)
             throw ApiError{MOJOTREES_ERROR_UNSUPPORTED,
                            "device=cpu: this library is the MI355X training path and has no CPU trainer"};
@@ -725,7 +729,7 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
         for (int64_t r = 0; r < n_rows; ++r)
             if (!(labels[r] >= 0.0 && labels[r] <= 30.0) || labels[r] != std::floor(labels[r]))
                 throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "relevance labels must be integers in [0, 30]"};
-        *out_model = train_model(data, n_rows, n_features, labels, nullptr, group_counts, n_groups, c);
+        *out_model = train_model(data, n_rows, n_features, labels, weights, group_counts, n_groups, c);
         return MOJOTREES_OK;
     });
 }

@@ -207,10 +207,7 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
         if (ds->grades.empty()) bad("relevance labels must be integers in [0, 30]");
         if (p->lambdarank_truncation_level < 1) bad("lambdarank_truncation_level must be positive");
         if (!(p->lambdarank_sigmoid > 0.0)) bad("sigmoid must be positive");
-        if (p->bagging_freq > 0 && p->bagging_fraction < 1.0)
-            unsup("query bagging for lambdarank is not built on the device path");
         if (p->goss) unsup("GOSS with lambdarank is not built on the device path");
-        if (ds->d_weights) unsup("sample weights with lambdarank are not built on the device path");
     }
     if (ds->any_cat) {
         // CategoricalParams.check_one_hot (categorical.mojo:216-240) and
@@ -543,6 +540,46 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
     hp.bagging_freq = p->bagging_freq;
     hp.bagging_seed = p->bagging_seed;
     hp.bagging_fraction = p->bagging_fraction;
+    if (hp.bagging) {
+        // bagging.sample_rows (bagging.mojo:101-129) never returns an empty
+        // bag: it then takes the unit of the least draw. Per bag index (the
+        // score kernel draws the next round's bag, so one past the last
+        // round), -1, or that unit when no unit is drawn; the scan stops at
+        // the first drawn unit, after ~1 / fraction draws.
+        const bool by_query = p->objective == MBH_OBJ_LAMBDARANK;
+        const int64_t units = by_query ? (int64_t)ds->qstart.size() - 1 : ds->n;
+        const int64_t n_bags = (int64_t)p->num_iterations / p->bagging_freq + 2;
+        std::vector<int64_t> fb((size_t)n_bags, -1);
+        for (int64_t b = 0; b < n_bags; ++b) {
+            const uint64_t stream = mb::splitmix64((uint64_t)(p->bagging_seed & 0x7FFFFFFFFFFFFFFFLL) ^
+                                                   ((uint64_t)b * mb::kGolden));
+            double min_draw = 2.0;
+            int64_t min_unit = 0;
+            bool any = false;
+            for (int64_t u = 0; u < units && !any; ++u) {
+                const double d = mb::uniform53(stream + (uint64_t)u);
+                any = d < p->bagging_fraction;
+                if (d < min_draw) {
+                    min_draw = d;
+                    min_unit = u;
+                }
+            }
+            if (!any) fb[(size_t)b] = min_unit;
+        }
+        int64_t *d_fb = dalloc<int64_t>(n_bags, run.owned);
+        HIPX(hipMemcpy(d_fb, fb.data(), n_bags * sizeof(int64_t), hipMemcpyHostToDevice));
+        s.bag_fallback = d_fb;
+        if (by_query) {
+            // ranking._refresh_query_bag (ranking.mojo:667-686): the draw is
+            // per query, so each row carries its query's index
+            std::vector<int32_t> qid((size_t)ds->n);
+            for (size_t q = 0; q + 1 < ds->qstart.size(); ++q)
+                for (int64_t r = ds->qstart[q]; r < ds->qstart[q + 1]; ++r) qid[(size_t)r] = (int32_t)q;
+            int32_t *d_qid = dalloc<int32_t>(ds->n, run.owned);
+            HIPX(hipMemcpy(d_qid, qid.data(), (size_t)ds->n * sizeof(int32_t), hipMemcpyHostToDevice));
+            s.qid = d_qid;
+        }
+    }
     hp.learning_rate = p->learning_rate;
     hp.lambda_l1 = p->lambda_l1;
     hp.lambda_l2 = p->lambda_l2;

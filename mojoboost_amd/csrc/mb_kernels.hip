@@ -175,15 +175,28 @@ __device__ __forceinline__ void wave_argmax(double &gain, int &order) {
     order = (int)mord;
 }
 
-__device__ __forceinline__ bool in_bag(const HyperParams &hp, uint64_t bag_stream, int64_t r) {
-    return uniform53(bag_stream + (uint64_t)r) < hp.bagging_fraction;
+// bagging.sample_rows (src/mojotrees/bagging.mojo:101-129): unit u is in
+// the bag when uniform(stream + u) < fraction, and an empty bag takes the
+// unit of the least draw (`fallback`, found on the host per bag; -1 when the
+// bag is not empty). The unit is the row, or under lambdarank the row's query
+// (ranking._refresh_query_bag, ranking.mojo:667-686: whole queries).
+__device__ __forceinline__ bool in_bag(const DevState &s, uint64_t bag_stream, int64_t fallback, int64_t r) {
+    const int64_t u = s.qid ? (int64_t)s.qid[r] : r;
+    return uniform53(bag_stream + (uint64_t)u) < s.hp.bagging_fraction || u == fallback;
+}
+
+__device__ __forceinline__ int64_t bag_index_of(const HyperParams &hp, int64_t round) {
+    return hp.bagging_freq > 0 ? round / hp.bagging_freq : 0;
 }
 
 // bagging.sample_rows stream of one bag (src/mojotrees/bagging.mojo).
 __device__ __forceinline__ uint64_t bag_stream_of(const HyperParams &hp, int64_t round) {
-    int64_t bag_index = hp.bagging_freq > 0 ? round / hp.bagging_freq : 0;
     return splitmix64((uint64_t)(hp.bagging_seed & 0x7FFFFFFFFFFFFFFFLL) ^
-                      ((uint64_t)bag_index * kGolden));
+                      ((uint64_t)bag_index_of(hp, round) * kGolden));
+}
+
+__device__ __forceinline__ int64_t bag_fallback_of(const DevState &s, int64_t round) {
+    return s.bag_fallback ? (int64_t)s.bag_fallback[bag_index_of(s.hp, round)] : -1;
 }
 
 }  // namespace
@@ -201,6 +214,7 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
     const HyperParams &hp = s.hp;
     if (blockIdx.x == 0 && threadIdx.x == 0) s.cursor[0] = 0;  // root row count
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
     const int K = hp.num_class, ck = rd.class_k;
     const double factor = K > 1 ? (double)K / (double)(K - 1) : 0.0;
     float mg = 0.0f, mh = 0.0f;
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
         s.grad[r] = g;
         s.hess[r] = h;
         float ag = fabsf(g), ah = fabsf(h);
-        bool sel = !hp.bagging || in_bag(hp, bstream, r);
+        bool sel = !hp.bagging || in_bag(s, bstream, bfall, r);
         if (sel && isfinite(ag) && isfinite(ah)) {
             mg = fmaxf(mg, ag);
             mh = fmaxf(mh, ah);
@@ -293,6 +307,8 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
     const int tid = threadIdx.x, nt = blockDim.x;
     const double sigma = hp.rank_sigma;
     const bool norm = hp.rank_norm != 0;
+    const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
     double mg = 0.0, mh = 0.0;
     for (int q = blockIdx.x; q < s.n_queries; q += gridDim.x) {
         const int64_t a = s.qstart[q];
@@ -383,6 +399,8 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
         if (tid == 0) s_factor = (norm && sum > 0.0) ? ref_log2(1.0 + sum) / sum : 0.0;
         __syncthreads();
         const double factor = s_factor;
+        // the magnitude stats are the bag's (whole queries)
+        const bool sel = !hp.bagging || in_bag(s, bstream, bfall, a);
         for (int k = tid; k < cnt; k += nt) {
             double g = G[k], h = H[k];
             if (factor != 0.0) {
@@ -390,9 +408,15 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
                 h *= factor;
             }
             const int64_t r = a + idx[k];
+            // lambdarank_gradients (ranking.mojo:613-616): sample weights
+            // scale the finished lambda and hessian
+            if (s.weights) {
+                g *= s.weights[r];
+                h *= s.weights[r];
+            }
             s.grad64[r] = g;
             s.hess64[r] = h;
-            if (isfinite(g) && isfinite(h)) {
+            if (sel && isfinite(g) && isfinite(h)) {
                 mg = fmax(mg, fabs(g));
                 mh = fmax(mh, fabs(h));
             }
@@ -470,6 +494,7 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const uint64_t hs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 1);
     const bool stoch = hp.stochastic != 0;
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         s.round->sampled = hp.bagging;
         s.round->goss_mult = 1.0;
@@ -501,7 +526,7 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
         } else {
             // Sampled rows appended with one atomic per wave; their order in
             // the root range does not matter (integer histograms).
-            bool take = valid && in_bag(hp, bstream, r);
+            bool take = valid && in_bag(s, bstream, bfall, r);
             unsigned long long m = __ballot(take);
             int cnt = __popcll(m);
             long long base = 0;
@@ -3373,6 +3398,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
     const bool in_regs = s.n_tiles == 1 && rec <= 32;
     const int np = 1 - rd.parity;  // the next tree's magnitude-stats pair
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round + 1) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round + 1) : -1;
     if (blockIdx.x == 0 && threadIdx.x == 0) s.cursor[0] = 0;  // the next root row count
     float mg = 0.0f, mh = 0.0f;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -3394,7 +3420,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
         s.grad[r] = g;
         s.hess[r] = h;
         const float ag = fabsf(g), ah = fabsf(h);
-        const bool sel = !hp.bagging || in_bag(hp, bstream, r);
+        const bool sel = !hp.bagging || in_bag(s, bstream, bfall, r);
         if (sel && isfinite(ag) && isfinite(ah)) {
             mg = fmaxf(mg, ag);
             mh = fmaxf(mh, ah);

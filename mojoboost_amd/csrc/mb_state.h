@@ -202,6 +202,8 @@ struct DevState {
     const uint8_t *bins_cm;  // F x n, column-major (partition, score update)
     const double *labels;    // n
     const double *weights;   // n sample weights, or null (unweighted)
+    const int32_t *qid;      // n: each row's query when lambdarank bags by query, else null
+    const int64_t *bag_fallback;  // per bag index: the unit an empty bag takes, or -1 (null: none)
     const int32_t *missing_bin;  // F
     const int32_t *widths;       // F: realized bin count bound
     const int32_t *ncat;         // F: categories of a categorical feature (bins 1..ncat), 0 numerical; null: none

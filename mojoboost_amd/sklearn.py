@@ -313,14 +313,16 @@ class MojoTreesRanker(_Base):
 
     def __init__(self, n_estimators=100, learning_rate=0.1, num_leaves=31, max_depth=-1,
                  min_child_samples=20, min_child_weight=1e-3, reg_alpha=0.0, reg_lambda=1.0,
-                 colsample_bytree=1.0, max_bin=255, random_state=None, device="gpu",
+                 colsample_bytree=1.0, subsample=1.0, subsample_freq=0, max_bin=255,
+                 random_state=None, device="gpu",
                  use_quantized_grad=False, num_grad_quant_bins=4, stochastic_rounding=True,
                  lambdarank_truncation_level=30, sigmoid=1.0, lambdarank_norm=True):
         super().__init__(n_estimators=n_estimators, learning_rate=learning_rate,
                          num_leaves=num_leaves, max_depth=max_depth,
                          min_child_samples=min_child_samples, min_child_weight=min_child_weight,
                          reg_alpha=reg_alpha, reg_lambda=reg_lambda,
-                         colsample_bytree=colsample_bytree, max_bin=max_bin,
+                         colsample_bytree=colsample_bytree, subsample=subsample,
+                         subsample_freq=subsample_freq, max_bin=max_bin,
                          random_state=random_state, device=device,
                          use_quantized_grad=use_quantized_grad,
                          num_grad_quant_bins=num_grad_quant_bins,
@@ -329,11 +331,19 @@ class MojoTreesRanker(_Base):
         self.sigmoid = sigmoid
         self.lambdarank_norm = lambdarank_norm
 
-    def fit(self, X, y, group):
+    def fit(self, X, y, group, sample_weight=None):
+        """subsample / subsample_freq bag whole queries
+        (ranking._refresh_query_bag, src/mojotrees/ranking.mojo:667-686);
+        sample_weight scales each row's lambda and hessian."""
         Xf, n, f = _colmajor(X)
         y = np.ascontiguousarray(y, dtype=np.float64)
         if y.shape[0] != n:
             raise ValueError("y must have one entry per row of X")
+        w = None
+        if sample_weight is not None:
+            w = np.ascontiguousarray(sample_weight, dtype=np.float64)
+            if w.shape != (n,):
+                raise ValueError("sample_weight length must equal n_rows")
         g = np.ascontiguousarray(group, dtype=np.int32)
         if g.ndim != 1 or g.size == 0:
             raise ValueError("group must be a non-empty 1-d array of query sizes")
@@ -343,7 +353,7 @@ class MojoTreesRanker(_Base):
             f"lambdarank_norm={'true' if self.lambdarank_norm else 'false'}")
         h = C.c_void_p()
         e = _Error()
-        e.check(lib().mbh_train_ranker_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), ptr(g), g.size,
+        e.check(lib().mbh_train_ranker_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), ptr(w), ptr(g), g.size,
                                              params.encode(), C.byref(h), e.h))
         self.booster_ = _Booster(h)
         return self

@@ -1156,6 +1156,20 @@ void refresh_bag(std::vector<int32_t> &bag, const orc_params &p, int64_t n,
     if (bag.empty()) bag.push_back((int32_t)min_row);
 }
 
+// ranking._refresh_query_bag / _expand_queries (src/mojotrees/ranking.mojo:
+// 655-686): the same draw over query indices, then the rows of the drawn
+// queries, ascending
+void refresh_query_bag(std::vector<int32_t> &bag, const orc_params &p, const std::vector<int64_t> &starts,
+                       int64_t iteration) {
+    if (!(p.bagging_freq > 0 && p.bagging_fraction < 1.0)) return;
+    if (iteration % p.bagging_freq != 0) return;
+    std::vector<int32_t> qbag;
+    refresh_bag(qbag, p, (int64_t)starts.size() - 1, iteration);
+    bag.clear();
+    for (int32_t q : qbag)
+        for (int64_t r = starts[q]; r < starts[q + 1]; ++r) bag.push_back((int32_t)r);
+}
+
 // goss.mojo:240-396
 double select_kth_desc(std::vector<double> &v, int64_t k) {
     auto median3 = [](double a, double b, double c) {
@@ -1890,11 +1904,21 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
         bool bagging = P.p.bagging_freq > 0 && P.p.bagging_fraction < 1.0;
         for (int it = 0; it < P.p.num_iterations; ++it) {
             auto t0 = std::chrono::steady_clock::now();
-            refresh_bag(bag, P.p, n, it);
+            if (rank)
+                refresh_query_bag(bag, P.p, rs.starts, it);
+            else
+                refresh_bag(bag, P.p, n, it);
             if (K == 1) {
-                if (rank)
+                if (rank) {
                     fill_lambdas(raw.data(), rank_labels, rs, inv_max_dcg, rank_disc, grad.data(), hess.data());
-                else
+                    // lambdarank_gradients (ranking.mojo:613-616): weights
+                    // scale the finished lambdas and hessians
+                    if (P.p.weights)
+                        for (int64_t r = 0; r < n; ++r) {
+                            grad[r] *= P.p.weights[r];
+                            hess[r] *= P.p.weights[r];
+                        }
+                } else
                     fill_grad_hess(P.p.objective, raw.data(), labels, n, 1, 0, grad.data(), hess.data(), P.p.weights);
                 goss_round(bag, grad, hess, P.p, it);
                 Tree t = grow_one(d, P, grad, hess, bag, it, 0, it, leaves, qg, qh, pool);

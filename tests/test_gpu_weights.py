@@ -111,3 +111,42 @@ def test_estimators_sample_weight_through_c_abi(dev):
         ref = O.train(bins, n, f, 63, y, p, missing_bin=mb)
         want, _ = ref.predict_binned(bins, n, f)
         assert np.array_equal(bits(raw), bits(want))
+
+
+def ranking_data(n_queries, f=8, seed=61, max_q=120):
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(1, max_q + 1, size=n_queries)
+    n = int(counts.sum())
+    x = rng.normal(size=(f, n))
+    s = x[0] - 0.5 * x[1] + 0.3 * x[2] * x[3] + 0.5 * rng.normal(size=n)
+    y = np.clip(np.floor((s + 2.0)), 0, 4).astype(np.float64)
+    return x, y, counts.astype(np.int32), n
+
+
+@pytest.mark.parametrize("n_queries,fraction,freq,weighted", [(300, 0.6, 2, True), (300, 0.5, 1, False),
+                                                               (3, 0.05, 1, True)])
+def test_lambdarank_query_bagging_and_weights_bit_exact(dev, n_queries, fraction, freq, weighted):
+    """train_ranker with bagging and sample_weight (ranking.mojo:690-771):
+    whole queries bagged, weights scaling the lambdas; quantized training
+    bit-exact to the oracle. Three queries at fraction 0.05 draw empty bags,
+    which take the query of the least draw (bagging.sample_rows)."""
+    x, y, counts, n = ranking_data(n_queries)
+    f = x.shape[0]
+    bins, mb = dev.bin_dense(x.ravel(), n, f, max_bins=63)
+    w = np.random.default_rng(5).uniform(0.2, 2.0, size=n) if weighted else None
+    kw = dict(num_iterations=8, num_leaves=15, min_data_in_leaf=5, lambda_l2=1.0, learning_rate=0.1,
+              bagging_fraction=fraction, bagging_freq=freq, bagging_seed=9)
+    ds = dev.Dataset(bins, n, f, 63, y, missing_bin=mb, weights=w)
+    ds.set_groups(counts)
+    fit = ds.train(objective=3, use_quantized_grad=1, **kw)
+    p, st = O.rank_params(counts, use_quantized_grad=1, **kw)
+    if weighted:
+        wk = np.ascontiguousarray(w)
+        p.weights = wk.ctypes.data
+    ref = O.train(bins, n, f, 63, y, p, missing_bin=mb)
+    assert fit.n_trees == ref.n_trees > 0
+    for k in ("feature", "threshold", "left", "right", "default_left"):
+        assert np.array_equal(getattr(fit, k), getattr(ref, k)), k
+    for k in ("value", "gain", "count"):
+        assert np.array_equal(bits(getattr(fit, k)), bits(getattr(ref, k))), k
+    assert np.array_equal(bits(fit.train_raw()), bits(ref.train_raw(n)))

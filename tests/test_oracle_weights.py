@@ -93,3 +93,27 @@ def test_integer_weights_act_as_repeated_rows_in_the_base_score():
     bm = O.train(bins, n, 1, nb, yc, pm).base
     for k in range(3):
         assert bm[k] == O.lib().orc_log(np.sum(reps * (yc == k)) / reps.sum())
+
+
+def test_ranker_unit_weights_and_query_bags():
+    """train_ranker (ranking.mojo:690-771): unit weights change nothing; a
+    query bag holds whole queries, so a fit whose bag draws every query
+    (fraction just under 1) equals the unbagged fit tree for tree."""
+    rng = np.random.default_rng(3)
+    counts = rng.integers(1, 40, size=60).astype(np.int32)
+    n = int(counts.sum())
+    bins = rng.integers(0, 16, size=(3, n)).astype(np.uint8)
+    y = rng.integers(0, 4, size=n).astype(float)
+    kw = dict(num_iterations=4, num_leaves=7, min_data_in_leaf=3, use_quantized_grad=0)
+    p0, s0 = O.rank_params(counts, **kw)
+    plain = O.train(bins.ravel(), n, 3, 16, y, p0)
+    p1, s1 = O.rank_params(counts, **kw)
+    w = np.ones(n)
+    p1.weights = w.ctypes.data
+    unit = O.train(bins.ravel(), n, 3, 16, y, p1)
+    assert np.array_equal(plain.value.view(np.uint64), unit.value.view(np.uint64))
+    # every draw falls below 1 - 2^-40 (240 draws; any above it has odds ~2e-10)
+    p2, s2 = O.rank_params(counts, bagging_fraction=1.0 - 2.0 ** -40, bagging_freq=1, **kw)
+    bagged = O.train(bins.ravel(), n, 3, 16, y, p2)
+    assert np.array_equal(plain.feature, bagged.feature)
+    assert np.array_equal(plain.value.view(np.uint64), bagged.value.view(np.uint64))
