@@ -196,7 +196,8 @@ int32_t mbh_dataset_set_weights(mbh_dataset *ds, const double *weights, int64_t 
 
 /* LambdaRank gradients and hessians (binary64) of one set of raw scores on
  * the device (ranking.lambdarank_gradients, src/mojotrees/ranking.mojo:
- * 603-654, unweighted), with the dataset's labels and groups. */
+ * 603-654), with the dataset's labels and groups, scaled by its sample
+ * weights when mbh_dataset_set_weights gave it some. */
 int32_t mbh_lambdarank(mbh_dataset *ds, const mbh_params *params, const double *raw,
                        double *grad, double *hess, char *err, int32_t err_len);
 

@@ -384,7 +384,7 @@ struct TrainBuffers {
     int T = 0, L = 0, max_nodes = 0;
 };
 
-TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
+TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t last_round = 0) {
     TrainBuffers tb;
     const int K = p->objective == MBH_OBJ_MULTICLASS ? p->num_class : 1;
     const int L = p->num_leaves;
@@ -548,7 +548,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
         // the first drawn unit, after ~1 / fraction draws.
         const bool by_query = p->objective == MBH_OBJ_LAMBDARANK;
         const int64_t units = by_query ? (int64_t)ds->qstart.size() - 1 : ds->n;
-        const int64_t n_bags = (int64_t)p->num_iterations / p->bagging_freq + 2;
+        const int64_t n_bags = std::max<int64_t>(p->num_iterations, last_round + 1) / p->bagging_freq + 2;
         std::vector<int64_t> fb((size_t)n_bags, -1);
         for (int64_t b = 0; b < n_bags; ++b) {
             const uint64_t stream = mb::splitmix64((uint64_t)(p->bagging_seed & 0x7FFFFFFFFFFFFFFFLL) ^
@@ -569,6 +569,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run) {
         int64_t *d_fb = dalloc<int64_t>(n_bags, run.owned);
         HIPX(hipMemcpy(d_fb, fb.data(), n_bags * sizeof(int64_t), hipMemcpyHostToDevice));
         s.bag_fallback = d_fb;
+        s.n_bags = n_bags;
         if (by_query) {
             // ranking._refresh_query_bag (ranking.mojo:667-686): the draw is
             // per query, so each row carries its query's index
@@ -1321,7 +1322,8 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const doubl
         Run run;
         mbh_params p1 = *p;
         p1.num_iterations = 1;
-        TrainBuffers tb = setup_state(ds, &p1, run);
+        if (round_index < 0) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "round_index must be nonnegative"};
+        TrainBuffers tb = setup_state(ds, &p1, run, round_index);
         mb::DevState &s = tb.s;
         mb::Round r0 = mb::initial_round();
         r0.round = round_index;

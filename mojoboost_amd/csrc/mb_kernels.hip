@@ -196,7 +196,8 @@ __device__ __forceinline__ uint64_t bag_stream_of(const HyperParams &hp, int64_t
 }
 
 __device__ __forceinline__ int64_t bag_fallback_of(const DevState &s, int64_t round) {
-    return s.bag_fallback ? (int64_t)s.bag_fallback[bag_index_of(s.hp, round)] : -1;
+    const int64_t b = bag_index_of(s.hp, round);
+    return s.bag_fallback && b < s.n_bags ? s.bag_fallback[b] : -1;
 }
 
 }  // namespace

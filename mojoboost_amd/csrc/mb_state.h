@@ -204,6 +204,7 @@ struct DevState {
     const double *weights;   // n sample weights, or null (unweighted)
     const int32_t *qid;      // n: each row's query when lambdarank bags by query, else null
     const int64_t *bag_fallback;  // per bag index: the unit an empty bag takes, or -1 (null: none)
+    int64_t n_bags;               // entries of bag_fallback
     const int32_t *missing_bin;  // F
     const int32_t *widths;       // F: realized bin count bound
     const int32_t *ncat;         // F: categories of a categorical feature (bins 1..ncat), 0 numerical; null: none
