@@ -224,7 +224,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU row sharding is a "
-                          "design only (see DESIGN.md), --gpus must be 1"}))
+                          "design only (rows sharded per GPU, histograms all-reduced), "
+                          "--gpus must be 1"}))
         return 2
 
     if args.rocprof_summary:
