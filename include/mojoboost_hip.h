@@ -262,6 +262,29 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad,
                       int64_t n_sel, int32_t num_grad_quant_bins,
                       int32_t *out, char *err, int32_t err_len);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the histogram of mbh_histogram, computed from the
+ * caller's DEVICE buffers without any allocation. bins_cm: n_rows x
+ * n_features column-major uint8 bins (< n_bins); q_grad, q_hess: n_rows
+ * int8 each (|q_grad| <= B/2 + 1, 0 <= q_hess <= B + 1, B =
+ * num_grad_quant_bins); rows: n_sel row ids, or NULL for every row; out:
+ * n_features * n_bins * 3 int32 {grad, hess, count}, fully written; status:
+ * NULL or one int32 set to 0, then to 1 when an entry was out of range (a
+ * row id, a quantized pair, a bin id), which is then left out. Enqueued on
+ * `stream` (a hipStream_t, NULL for the default stream); returns without
+ * waiting. Block partials live in a static device array of
+ * MBH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends: one
+ * partial of n_features * n_bins * 8 bytes must fit it, and sizes beyond it
+ * are refused (MOJOTREES_ERROR_INVALID_ARGUMENT). Calls that overlap on one
+ * GPU share that array and race. */
+#define MBH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int32_t mbh_histogram_noalloc(const uint8_t *bins_cm, int64_t n_rows, int32_t n_features,
+                              int32_t n_bins, const int8_t *q_grad, const int8_t *q_hess,
+                              const int32_t *rows, int64_t n_sel, int32_t num_grad_quant_bins,
+                              int32_t *out, int32_t *status, void *stream, char *err,
+                              int32_t err_len);
+
 /* fp32-gradient histogram of the rows `rows[0..n_sel)` (all rows when rows
  * is NULL) with the given fp32 grad/hess (n_rows each), summed in fp64 on the
  * device: out_gh is n_features * n_bins * 2 doubles {grad, hess} per cell,

@@ -37,6 +37,7 @@ MBH_SYMBOLS = [
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
     "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
+    "mbh_histogram_noalloc",
 ]
 
 
@@ -154,6 +155,7 @@ def lib():
         "mbh_objective_quantize": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),
         "mbh_histogram_fp32": (I32, [V, V, V, V, I64, V, V, C.c_char_p, I32]),
+        "mbh_histogram_noalloc": (I32, [V, I64, I32, I32, V, V, V, I64, I32, V, V, V, C.c_char_p, I32]),
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),
         "mbh_predict_binned": (I32, [V, I64, I32, I32, C.c_double, V, V, I64, I64, V, V, V, V, V, V, V,
                                      V, V, C.c_char_p, I32]),
