@@ -1366,7 +1366,7 @@ int32_t mbh_histogram(mbh_dataset *ds, const int8_t *q_grad, const int8_t *q_hes
                 if (rows[i] < 0 || rows[i] >= ds->n)
                     throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "row id out of range"};
         for (int64_t r = 0; r < ds->n; ++r)
-            if (q_grad[r] < -(B / 2 + 1) || q_grad[r] > B / 2 + 1 || q_hess[r] < -(B + 1) || q_hess[r] > B + 1)
+            if (q_grad[r] < -(B / 2 + 1) || q_grad[r] > B / 2 + 1 || q_hess[r] < 0 || q_hess[r] > B + 1)
                 throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "quantized value outside the lattice"};
         Run run;
         mbh_params p{};
