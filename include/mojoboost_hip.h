@@ -222,6 +222,23 @@ int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_fea
                                int64_t n_groups, const char *parameters,
                                struct MojoTreesModel **out_model, struct MojoTreesError *error);
 
+/* Save with feature names, as the reference's estimators do
+ * (bindings/_mojotrees.mojo:4931 `save(model, path, names, n)` over
+ * serialize.save_model(model, path, feature_names),
+ * src/mojotrees/serialize.mojo:999-1030): the v4 file gains the optional
+ * `feature_names` section. n_names 0 writes none; otherwise it must equal the
+ * model's feature count. Names may hold any bytes but other control bytes
+ * than tab, newline and carriage return (MOJOTREES_ERROR_IO). */
+int32_t mbh_save_model_named(const struct MojoTreesModel *model, const char *path,
+                             const char *const *names, int64_t n_names,
+                             struct MojoTreesError *error);
+/* The feature names a model file carries (serialize.load_feature_names,
+ * src/mojotrees/serialize.mojo:1448-1460; bindings/_mojotrees.mojo:4968):
+ * *out_count names, back to back as NUL-terminated strings in *out_names
+ * (free with mojotrees_string_free); 0 and NULL when the file has none. */
+int32_t mbh_model_feature_names(const char *path, char **out_names, int64_t *out_count,
+                                struct MojoTreesError *error);
+
 /* Raw scores on the device (Booster.predict_raw_row,
  * src/mojotrees/boosting.mojo:1722-1760; the reference's device counterpart is
  * _predict_kernel, src/mojotrees/gpu_predict.mojo:206, in Float32). bins_cm is

@@ -72,10 +72,11 @@ void mojotrees_error_free(MojoTreesError *error);
 const char *mojotrees_error_message(const MojoTreesError *error);
 
 /* reference capi/mojotrees.h:180-184. Column-major doubles
- * data[f * n_rows + r], NaN = missing; labels n_rows doubles; weights must be
- * NULL (sample weights are not part of the device path); `parameters` is a
- * whitespace-separated LightGBM key=value string. `out_model` is written only
- * on success. */
+ * data[f * n_rows + r], NaN = missing; labels n_rows doubles; weights NULL
+ * (unweighted) or n_rows finite, nonnegative doubles with a positive sum,
+ * which scale each row's gradient and hessian and weight the base score and
+ * class priors; `parameters` is a whitespace-separated LightGBM key=value
+ * string. `out_model` is written only on success. */
 int32_t mojotrees_train_dense(const double *data, int64_t n_rows,
                               int64_t n_features, const double *labels,
                               const double *weights, const char *parameters,

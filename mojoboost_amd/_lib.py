@@ -37,7 +37,7 @@ MBH_SYMBOLS = [
     "mbh_objective_quantize", "mbh_histogram", "mbh_histogram_fp32", "mbh_bench_root_histogram",
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
     "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
-    "mbh_histogram_noalloc",
+    "mbh_histogram_noalloc", "mbh_save_model_named", "mbh_model_feature_names",
 ]
 
 
@@ -167,6 +167,8 @@ def lib():
         "mbh_dataset_set_weights": (I32, [V, V, I64, C.c_char_p, I32]),
         "mbh_lambdarank": (I32, [V, P(MbhParams), V, V, V, C.c_char_p, I32]),
         "mbh_train_ranker_dense": (I32, [V, I64, I64, V, V, V, I64, C.c_char_p, V, V]),
+        "mbh_save_model_named": (I32, [V, C.c_char_p, V, I64, V]),
+        "mbh_model_feature_names": (I32, [C.c_char_p, V, V, V]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -619,6 +619,10 @@ int32_t mojotrees_load_model(const char *path, MojoTreesModel **out_model, MojoT
         } catch (const std::exception &e) {
             throw ApiError{MOJOTREES_ERROR_IO, e.what()};
         }
+        // serialize.load_model checks a names section and leaves the names
+        // out of the model (serialize.mojo:1463-1475): a C ABI model carries
+        // none, and mbh_model_feature_names reads them from the file
+        m.feature_names.clear();
         auto *model = new MojoTreesModel();
         model->m = std::move(m);
         *out_model = model;
@@ -705,6 +709,59 @@ int32_t mojotrees_parameter_keys(char **out_text, MojoTreesError *error) {
 }
 
 void mojotrees_string_free(char *text) { std::free(text); }
+
+int32_t mbh_save_model_named(const MojoTreesModel *model, const char *path, const char *const *names,
+                             int64_t n_names, MojoTreesError *error) {
+    return guarded(error, [&]() -> int32_t {
+        check_model(model);
+        if (!path) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "path is NULL"};
+        if (n_names < 0 || (n_names > 0 && !names))
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "names must hold n_names strings"};
+        if (n_names > 0 && n_names != model->m.mapper.n_features)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT,
+                           "feature_names has " + std::to_string(n_names) + " entries for " +
+                               std::to_string(model->m.mapper.n_features) + " features"};
+        mb::Model m = model->m;
+        m.feature_names.clear();
+        for (int64_t f = 0; f < n_names; ++f) {
+            if (!names[f]) throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "a feature name is NULL"};
+            m.feature_names.emplace_back(names[f]);
+        }
+        try {
+            m.save(path);
+        } catch (const std::runtime_error &e) {
+            throw ApiError{MOJOTREES_ERROR_IO, e.what()};
+        }
+        return MOJOTREES_OK;
+    });
+}
+
+int32_t mbh_model_feature_names(const char *path, char **out_names, int64_t *out_count, MojoTreesError *error) {
+    return guarded(error, [&]() -> int32_t {
+        if (!path || !out_names || !out_count)
+            throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "path, out_names and out_count must not be NULL"};
+        std::vector<std::string> names;
+        try {
+            names = mb::Model::load_feature_names(path);
+        } catch (const std::exception &e) {
+            throw ApiError{MOJOTREES_ERROR_IO, e.what()};
+        }
+        *out_names = nullptr;
+        *out_count = (int64_t)names.size();
+        if (names.empty()) return MOJOTREES_OK;
+        size_t total = 0;
+        for (const std::string &nm : names) total += nm.size() + 1;
+        char *buf = (char *)std::malloc(total);
+        if (!buf) throw std::bad_alloc();
+        size_t at = 0;
+        for (const std::string &nm : names) {
+            std::memcpy(buf + at, nm.c_str(), nm.size() + 1);
+            at += nm.size() + 1;
+        }
+        *out_names = buf;
+        return MOJOTREES_OK;
+    });
+}
 void mojotrees_model_free(MojoTreesModel *model) { delete model; }
 
 int32_t mbh_train_ranker_dense(const double *data, int64_t n_rows, int64_t n_features, const double *labels,

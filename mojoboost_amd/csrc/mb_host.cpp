@@ -45,6 +45,91 @@ double from_bits(const std::string &tok) {
     return d;
 }
 
+// A feature name as one whitespace-free token of the model file
+// (serialize._escape_name, src/mojotrees/serialize.mojo:276-319): space, tab,
+// newline, carriage return and the backslash become two-character escapes,
+// other control bytes are refused, every other byte (UTF-8 included) is
+// copied; an empty name travels as the token "\e".
+std::string escape_name(const std::string &name) {
+    if (name.empty()) return "\\e";
+    std::string out;
+    for (unsigned char b : name) {
+        switch (b) {
+            case ' ': out += "\\s"; break;
+            case '\t': out += "\\t"; break;
+            case '\n': out += "\\n"; break;
+            case '\r': out += "\\r"; break;
+            case '\\': out += "\\\\"; break;
+            default:
+                if (b < 32 || b == 127)
+                    throw std::runtime_error("feature name contains control byte " + std::to_string((int)b) +
+                                             ", which the model file format cannot carry");
+                out += (char)b;
+        }
+    }
+    return out;
+}
+
+// The exact inverse (serialize._unescape_name, serialize.mojo:321-355).
+std::string unescape_name(const std::string &tok) {
+    if (tok == "\\e") return "";
+    std::string out;
+    for (size_t i = 0; i < tok.size(); ++i) {
+        if (tok[i] != '\\') {
+            out += tok[i];
+            continue;
+        }
+        if (i + 1 >= tok.size()) throw std::runtime_error("corrupt feature name: token ends in an escape");
+        const char c = tok[++i];
+        if (c == 's') out += ' ';
+        else if (c == 't') out += '\t';
+        else if (c == 'n') out += '\n';
+        else if (c == 'r') out += '\r';
+        else if (c == '\\') out += '\\';
+        else throw std::runtime_error("corrupt feature name: unknown escape");
+    }
+    return out;
+}
+
+// Whitespace tokens of a model file.
+std::vector<std::string> file_tokens(const std::string &path) {
+    std::ifstream f(path);
+    if (!f) throw std::runtime_error("cannot open '" + path + "'");
+    std::vector<std::string> tok;
+    for (std::string s; f >> s;) tok.push_back(s);
+    return tok;
+}
+
+// serialize._read_version (serialize.mojo:1372-1398): the magic, then v1..v4.
+// v5 (linear leaves, CTR tables) is outside this library's models.
+int read_version(const std::vector<std::string> &tok, size_t &i) {
+    if (i >= tok.size() || tok[i] != "mojotrees") throw std::runtime_error("not a mojotrees model file");
+    ++i;
+    if (i >= tok.size()) throw std::runtime_error("truncated model file");
+    const std::string &v = tok[i++];
+    if (v == "v1") return 1;
+    if (v == "v2") return 2;
+    if (v == "v3") return 3;
+    if (v == "v4") return 4;
+    if (v == "v5")
+        throw std::runtime_error("model file version 'v5' (linear leaves or CTR tables) is not served by this library");
+    throw std::runtime_error("unsupported model file version '" + v + "'");
+}
+
+// serialize._read_feature_names (serialize.mojo:401-415): the optional
+// section right after the version.
+std::vector<std::string> read_feature_names(const std::vector<std::string> &tok, size_t &i) {
+    std::vector<std::string> names;
+    if (i >= tok.size() || tok[i] != "feature_names") return names;
+    ++i;
+    if (i >= tok.size()) throw std::runtime_error("truncated model file");
+    const long long n = std::stoll(tok[i++]);
+    if (n < 1) throw std::runtime_error("corrupt feature_names section: nonpositive count");
+    if ((size_t)n > tok.size() - i) throw std::runtime_error("truncated model file");
+    for (long long k = 0; k < n; ++k) names.push_back(unescape_name(tok[i++]));
+    return names;
+}
+
 }  // namespace
 
 bool BinMapper::any_cat() const {
@@ -293,6 +378,14 @@ void Model::response(double *raw, int64_t n) const {
 void Model::save(const std::string &path) const {
     std::ostringstream o;
     o << "mojotrees v4\n";
+    if (!feature_names.empty()) {  // _write_feature_names (serialize.mojo:389-398)
+        if ((int)feature_names.size() != mapper.n_features)
+            throw std::runtime_error("feature_names has " + std::to_string(feature_names.size()) + " entries for " +
+                                     std::to_string(mapper.n_features) + " features");
+        o << "feature_names " << feature_names.size() << "\n";
+        for (const std::string &nm : feature_names) o << escape_name(nm) << " ";
+        o << "\n";
+    }
     if (num_class == 1) {
         o << "objective " << objective << "\n";
         o << "learning_rate " << bits(learning_rate) << "\n";
@@ -318,6 +411,11 @@ void Model::save(const std::string &path) const {
         for (int64_t c : mapper.cat_codes) o << c << " ";
         o << "\n";
         for (int64_t c : mapper.cat_offsets) o << c << " ";
+        o << "\n";
+    }
+    if (!monotone.empty()) {  // _write_monotone (serialize.mojo:964-973)
+        o << "monotone " << monotone.size();
+        for (int32_t v : monotone) o << " " << v;
         o << "\n";
     }
     o << "trees " << num_trees() << "\n";
@@ -372,25 +470,27 @@ void Model::save(const std::string &path) const {
     if (!f) throw std::runtime_error("cannot write '" + path + "'");
 }
 
+// serialize.load_model / load_multiclass_model (serialize.mojo:1463-1560)
+// over the reader functions of that file: _read_version, _read_feature_names,
+// _read_kind, _read_mapper (:1121-1165; v1 reserves no missing bins),
+// _read_categorical (:1168-1232), _read_monotone (:976-995) and _read_trees
+// (:1235-1369: v1 nodes carry no missing routing, v3 covers have no presence
+// flag, v4 flags covers and gains, category sets from v2 on).
 Model Model::load(const std::string &path) {
-    std::ifstream f(path);
-    if (!f) throw std::runtime_error("cannot open '" + path + "'");
-    std::vector<std::string> tok;
-    for (std::string s; f >> s;) tok.push_back(s);
+    const std::vector<std::string> tok = file_tokens(path);
     size_t i = 0;
     auto next = [&]() -> const std::string & {
         if (i >= tok.size()) throw std::runtime_error("truncated model file");
         return tok[i++];
     };
+    auto peek_is = [&](const char *w) { return i < tok.size() && tok[i] == w; };
     auto expect = [&](const char *w) {
         if (next() != w) throw std::runtime_error(std::string("malformed model file: expected '") + w + "'");
     };
     auto geti = [&]() { return std::stoll(next()); };
     Model m;
-    expect("mojotrees");
-    const std::string ver = next();
-    if (ver != "v4" && ver != "v3" && ver != "v2")
-        throw std::runtime_error("unsupported model file version '" + ver + "'");
+    const int version = read_version(tok, i);
+    m.feature_names = read_feature_names(tok, i);
     const std::string kind = next();
     if (kind == "objective") {
         m.objective = (int)geti();
@@ -409,18 +509,35 @@ Model Model::load(const std::string &path) {
         expect("base_scores");
         for (int k = 0; k < m.num_class; ++k) m.base.push_back(from_bits(next()));
     } else {
-        throw std::runtime_error("unsupported model section '" + kind + "'");
+        throw std::runtime_error("corrupt model file: unknown model kind '" + kind + "'");
     }
     expect("mapper");
     m.mapper.n_features = (int)geti();
     m.mapper.n_bins = (int)geti();
     const int64_t ne = geti();
+    if (m.mapper.n_features < 1 || ne < 0) throw std::runtime_error("corrupt mapper header");
+    if (m.mapper.n_bins < 1 || m.mapper.n_bins > 256)
+        throw std::runtime_error("corrupt mapper: n_bins must be in [1, 256]");
+    if ((size_t)ne > tok.size() - i) throw std::runtime_error("truncated model file");
     for (int64_t k = 0; k < ne; ++k) m.mapper.edges.push_back(from_bits(next()));
     m.mapper.edge_offsets.clear();
     for (int k = 0; k <= m.mapper.n_features; ++k) m.mapper.edge_offsets.push_back(geti());
-    for (int k = 0; k < m.mapper.n_features; ++k) m.mapper.missing_bin.push_back((int32_t)geti());
-    if (m.mapper.edge_offsets.back() != ne) throw std::runtime_error("mapper offsets disagree with edges");
-    if (i < tok.size() && tok[i] == "categorical") {  // _read_categorical (serialize.mojo:1196-1232)
+    if (m.mapper.edge_offsets[0] != 0 || m.mapper.edge_offsets.back() != ne)
+        throw std::runtime_error("corrupt mapper offsets");
+    for (int f = 0; f < m.mapper.n_features; ++f) {
+        const int64_t w = m.mapper.edge_offsets[f + 1] - m.mapper.edge_offsets[f];
+        if (w < 0) throw std::runtime_error("corrupt mapper offsets");
+        if (w > m.mapper.n_bins - 1) throw std::runtime_error("corrupt mapper: more edges than bins allow");
+    }
+    for (int f = 0; f < m.mapper.n_features; ++f) {
+        int32_t mb = -1;
+        if (version >= 2) {
+            mb = (int32_t)geti();
+            if (mb < -1 || mb >= m.mapper.n_bins) throw std::runtime_error("corrupt mapper: missing bin out of range");
+        }
+        m.mapper.missing_bin.push_back(mb);
+    }
+    if (peek_is("categorical")) {
         next();
         const int64_t nfl = geti(), ncodes = geti();
         if (nfl != m.mapper.n_features || ncodes < 0) throw std::runtime_error("corrupt categorical header");
@@ -438,13 +555,34 @@ Model Model::load(const std::string &path) {
                     throw std::runtime_error("corrupt categorical: codes are not ascending");
         }
     }
+    // _check_feature_names (serialize.mojo:417-430)
+    if (!m.feature_names.empty() && (int)m.feature_names.size() != m.mapper.n_features)
+        throw std::runtime_error("corrupt model file: feature_names has " + std::to_string(m.feature_names.size()) +
+                                 " entries for " + std::to_string(m.mapper.n_features) + " features");
+    if (peek_is("monotone")) {
+        next();
+        const int64_t n = geti();
+        if (n != m.mapper.n_features)
+            throw std::runtime_error("corrupt model file: monotone section has " + std::to_string(n) + " entries for " +
+                                     std::to_string(m.mapper.n_features) + " features");
+        for (int64_t k = 0; k < n; ++k) {
+            const int64_t v = geti();
+            if (v < -1 || v > 1) throw std::runtime_error("corrupt model file: monotone sign out of range");
+            m.monotone.push_back((int32_t)v);
+        }
+    }
     const std::string tr = next();
     if (tr != "trees") throw std::runtime_error("section '" + tr + "' is not served by this library");
     const int64_t nt = geti();
+    if (nt < 0) throw std::runtime_error("corrupt model file: negative tree count");
     for (int64_t t = 0; t < nt; ++t) {
         expect("tree");
         const int64_t nn = geti();
-        m.n_leaves.push_back((int32_t)geti());
+        const int64_t nl = geti();
+        // validation.check_tree_header (src/mojotrees/validation.mojo:1253-1290)
+        if (nn < 1 || nl < 1 || nl > nn || nn > 2 * nl - 1 || (size_t)nn > tok.size() - i)
+            throw std::runtime_error("corrupt tree header");
+        m.n_leaves.push_back((int32_t)nl);
         auto ints = [&](std::vector<int32_t> &v) {
             for (int64_t k = 0; k < nn; ++k) v.push_back((int32_t)geti());
         };
@@ -456,18 +594,51 @@ Model Model::load(const std::string &path) {
         ints(m.left);
         ints(m.right);
         dbls(m.value);
-        ints(m.default_left);
-        ints(m.missing_bin);
-        expect("counts");
-        if (geti()) dbls(m.count);
-        else m.count.insert(m.count.end(), (size_t)nn, 0.0);
-        expect("gains");
-        if (geti()) dbls(m.gain);
-        else m.gain.insert(m.gain.end(), (size_t)nn, 0.0);
+        if (version >= 2) {
+            ints(m.default_left);
+            const size_t mb0 = m.missing_bin.size();
+            ints(m.missing_bin);
+            for (size_t k = mb0; k < m.missing_bin.size(); ++k)
+                if (m.missing_bin[k] < -1 || m.missing_bin[k] >= m.mapper.n_bins)
+                    throw std::runtime_error("corrupt tree: missing bin out of range");
+        } else {
+            m.default_left.insert(m.default_left.end(), (size_t)nn, 0);
+            m.missing_bin.insert(m.missing_bin.end(), (size_t)nn, -1);
+        }
+        bool has_counts = version == 3;
+        if (version >= 4) {
+            expect("counts");
+            has_counts = geti() != 0;
+        }
+        if (has_counts) {
+            const size_t c0 = m.count.size();
+            dbls(m.count);
+            int64_t zeros = 0;
+            for (size_t k = c0; k < m.count.size(); ++k) {
+                if (m.count[k] == 0.0) ++zeros;
+                else if (!(m.count[k] > 0.0)) throw std::runtime_error("corrupt tree: node cover must be positive");
+            }
+            if (zeros > 0 && zeros != nn) throw std::runtime_error("corrupt tree: node cover must be positive");
+        } else {
+            m.count.insert(m.count.end(), (size_t)nn, 0.0);
+        }
+        bool has_gains = false;
+        if (version >= 4) {
+            expect("gains");
+            has_gains = geti() != 0;
+        }
+        if (has_gains) {
+            const size_t g0 = m.gain.size();
+            dbls(m.gain);
+            for (size_t k = g0; k < m.gain.size(); ++k)
+                if (m.gain[k] != m.gain[k]) throw std::runtime_error("corrupt tree: split gain is NaN");
+        } else {
+            m.gain.insert(m.gain.end(), (size_t)nn, 0.0);
+        }
         const size_t base_node = m.is_cat_node.size();
         m.is_cat_node.insert(m.is_cat_node.end(), (size_t)nn, 0);
         m.cat_bits.insert(m.cat_bits.end(), 4 * (size_t)nn, 0ULL);
-        if (i < tok.size() && tok[i] == "cat") {
+        if (version >= 2 && peek_is("cat")) {
             next();
             const int64_t pool = geti();
             if (pool < 0 || pool % 4) throw std::runtime_error("corrupt cat section");
@@ -477,7 +648,7 @@ Model Model::load(const std::string &path) {
             for (int64_t k = 0; k < pool; ++k) words[k] = std::stoull(next());
             for (int64_t k = 0; k < nn; ++k) {
                 if (off[k] < 0) continue;
-                if (off[k] + 4 > pool) throw std::runtime_error("corrupt cat section: offset out of range");
+                if (off[k] % 4 || off[k] + 4 > pool) throw std::runtime_error("corrupt cat section: offset out of range");
                 m.is_cat_node[base_node + k] = 1;
                 for (int w = 0; w < 4; ++w) m.cat_bits[4 * (base_node + k) + w] = words[off[k] + w];
             }
@@ -493,6 +664,13 @@ Model Model::load(const std::string &path) {
     if (i != tok.size()) throw std::runtime_error("unexpected trailing section in model file");
     if (m.num_trees() % m.num_class != 0) throw std::runtime_error("tree count is not a multiple of the class count");
     return m;
+}
+
+std::vector<std::string> Model::load_feature_names(const std::string &path) {
+    const std::vector<std::string> tok = file_tokens(path);
+    size_t i = 0;
+    read_version(tok, i);
+    return read_feature_names(tok, i);
 }
 
 std::string Model::dump_json() const {

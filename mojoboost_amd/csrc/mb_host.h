@@ -61,6 +61,11 @@ struct Model {
     // 300-306); is_cat_node marks those nodes (threshold -1, no missing bin)
     std::vector<uint64_t> cat_bits;
     std::vector<uint8_t> is_cat_node;
+    // optional file sections carried through load and save: the v4
+    // `feature_names` section (serialize.mojo:389-430) and the `monotone`
+    // constraint vector (serialize.mojo:964-995); empty when absent
+    std::vector<std::string> feature_names;
+    std::vector<int32_t> monotone;
 
     int64_t num_trees() const { return (int64_t)offsets.size() - 1; }
     int64_t num_iterations() const { return num_trees() / num_class; }
@@ -74,8 +79,13 @@ struct Model {
     }
     void response(double *raw, int64_t n_rows) const;
 
-    void save(const std::string &path) const;  // throws std::runtime_error
+    // v4 text file; feature_names (when not empty) and monotone are written
+    // as their optional sections. Throws std::runtime_error.
+    void save(const std::string &path) const;
+    // v1..v4 files (serialize.mojo:1372-1500); throws std::runtime_error
     static Model load(const std::string &path);
+    // the feature_names section of a model file, empty when it has none
+    static std::vector<std::string> load_feature_names(const std::string &path);
     std::string dump_json() const;
 };
 

@@ -34,6 +34,27 @@ class _Error:
             pass
 
 
+def _feature_names(X):
+    """Column names of a DataFrame-like X when every one is a string (the
+    estimators' feature_names_in_, python/mojotrees/sklearn.py:4776-4830),
+    else None."""
+    cols = getattr(X, "columns", None)
+    if cols is None:
+        return None
+    names = list(cols)
+    if not names or not all(isinstance(c, str) for c in names):
+        return None
+    return np.asarray(names, dtype=object)
+
+
+def _set_feature_names(est, X):
+    names = _feature_names(X)
+    if names is None:
+        est.__dict__.pop("feature_names_in_", None)
+    else:
+        est.feature_names_in_ = names
+
+
 def _colmajor(X):
     X = np.asarray(X, dtype=np.float64)
     if X.ndim != 2:
@@ -97,9 +118,18 @@ class _Booster:
                                            _predict_device(device), ptr(out), out.size, e.h))
         return out.reshape(n, k) if k > 1 else out
 
-    def save(self, path):
+    def save(self, path, feature_names=None):
+        """The v4 model file; with feature_names, its optional
+        feature_names section (serialize.save_model,
+        src/mojotrees/serialize.mojo:999-1030)."""
         e = _Error()
-        e.check(lib().mojotrees_save_model(self.h, str(path).encode(), e.h))
+        if feature_names is None or len(feature_names) == 0:
+            e.check(lib().mojotrees_save_model(self.h, str(path).encode(), e.h))
+            return
+        enc = [str(nm).encode() for nm in feature_names]
+        arr = (C.c_char_p * len(enc))(*enc)
+        e.check(lib().mbh_save_model_named(self.h, str(path).encode(), C.cast(arr, C.c_void_p),
+                                           len(enc), e.h))
 
     @staticmethod
     def load(path):
@@ -107,6 +137,26 @@ class _Booster:
         e = _Error()
         e.check(lib().mojotrees_load_model(str(path).encode(), C.byref(h), e.h))
         return _Booster(h)
+
+    @staticmethod
+    def feature_names(path):
+        """The names a model file carries (serialize.load_feature_names),
+        [] when it has none."""
+        out = C.c_void_p()
+        cnt = C.c_int64()
+        e = _Error()
+        e.check(lib().mbh_model_feature_names(str(path).encode(), C.byref(out), C.byref(cnt), e.h))
+        if not out.value:
+            return []
+        try:
+            names, at = [], out.value
+            for _ in range(cnt.value):
+                raw = C.string_at(at)
+                names.append(raw.decode())
+                at += len(raw) + 1
+            return names
+        finally:
+            lib().mojotrees_string_free(C.cast(out, C.c_char_p))
 
     def dump_json(self):
         out = C.c_char_p()
@@ -217,8 +267,17 @@ class _Base:
         return " ".join(p) + (" " + extra if extra else "")
 
     def save(self, path):
+        """v4 model file, with feature_names_in_ as its feature_names section
+        when the estimator was fitted on named columns (the reference's
+        estimators, python/mojotrees/sklearn.py:6140-6148)."""
         self._check_fitted()
-        self.booster_.save(path)
+        self.booster_.save(path, getattr(self, "feature_names_in_", None))
+
+    def _restore(self, path):
+        self.booster_ = _Booster.load(path)
+        names = _Booster.feature_names(path)
+        if names:
+            self.feature_names_in_ = np.asarray(names, dtype=object)
 
     def _check_fitted(self):
         if self.booster_ is None:
@@ -239,6 +298,7 @@ class MojoTreesRegressor(_Base):
 
     def fit(self, X, y, sample_weight=None):
         self.booster_ = _train(X, y, self._params(), sample_weight)
+        _set_feature_names(self, X)
         return self
 
     def predict(self, X, raw_score=False, start_iteration=0, num_iteration=None, device=None):
@@ -252,7 +312,7 @@ class MojoTreesRegressor(_Base):
     @classmethod
     def load(cls, path):
         est = cls()
-        est.booster_ = _Booster.load(path)
+        est._restore(path)
         return est
 
 
@@ -273,6 +333,7 @@ class MojoTreesClassifier(_Base):
         else:
             params = self._params().replace("objective=binary", "objective=multiclass")
             self.booster_ = _train(X, yi.astype(np.float64), params + f" num_class={k}", sample_weight)
+        _set_feature_names(self, X)
         return self
 
     def predict_proba(self, X, start_iteration=0, num_iteration=None, device=None):
@@ -297,7 +358,7 @@ class MojoTreesClassifier(_Base):
     @classmethod
     def load(cls, path):
         est = cls()
-        est.booster_ = _Booster.load(path)
+        est._restore(path)
         k = est.booster_.num_classes
         est.classes_ = np.arange(2 if k == 1 else k)
         return est
@@ -356,6 +417,7 @@ class MojoTreesRanker(_Base):
         e.check(lib().mbh_train_ranker_dense(ptr(Xf.ravel(order="K")), n, f, ptr(y), ptr(w), ptr(g), g.size,
                                              params.encode(), C.byref(h), e.h))
         self.booster_ = _Booster(h)
+        _set_feature_names(self, X)
         return self
 
     def predict(self, X, start_iteration=0, num_iteration=None, device=None):
@@ -366,5 +428,5 @@ class MojoTreesRanker(_Base):
     @classmethod
     def load(cls, path):
         est = cls()
-        est.booster_ = _Booster.load(path)
+        est._restore(path)
         return est

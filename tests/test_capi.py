@@ -257,3 +257,24 @@ def test_load_errors(tmp_path):
     write_model(trunc)
     trunc.write_text(trunc.read_text()[:-40])
     assert _load(trunc)[0] == _lib.ERROR_IO
+
+
+def test_c_program_against_the_header(tmp_path):
+    """tests/c/capi_program.c, compiled as C99 with -Werror against
+    include/mojotrees.h and linked to the shared library, calls all 21
+    functions on the CPU (the reference's capi/test_capi.c calls)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    exe = tmp_path / "capi_program"
+    libdir = ROOT / "mojoboost_amd"
+    subprocess.run([cc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic",
+                    "-I", str(ROOT / "include"), str(ROOT / "tests" / "c" / "capi_program.c"),
+                    "-o", str(exe), "-L", str(libdir), "-lmojoboost_hip",
+                    "-Wl,-rpath," + str(libdir), "-lm"], check=True)
+    r = subprocess.run([str(exe), str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip() == "ok"
