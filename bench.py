@@ -6,26 +6,33 @@ binary label ~ Bernoulli(sigmoid(sum of 8 random pairwise terms)), logistic
 objective, max_bin 255, num_leaves 255, quantized gradients (int8 g/h,
 int32 histogram cells). Synthetic and seeded; generated here.
 
-A "step" is one boosting iteration (one tree). The timed region trains
---steps trees from scratch on the HBM-resident dataset, bracketed by device
-synchronization (the library syncs before returning). `value` is the
-histogram-build throughput of an instrumented run of the same training (HIP
-events around every growth kernel, on the stream they run on): the
-algorithmic bytes of every histogram the run accumulated -- the root and each
-expansion's smaller child, speculative expansions included -- m rows *
-(F + gh) (uint8 bins + the g/h pair: 2 bytes int8, 8 bytes fp32; row ids,
-LDS traffic and partial writes not counted), over the time of the kernels
-that accumulate them (k_hist for the root, k_accum for the children).
-`roofline` prices k_accum alone, whose average duration rocprofv3 reports
-too; `traffic` is its HBM bytes per launch from rocprofv3 PMC counters.
-The conservative figure that charges every growth kernel (partition,
-accumulation, partial merge and scan, planning) against the committed
-trees' builds only is reported as `hist_gbs_committed_over_growth`.
+A "step" is one boosting iteration (one tree; one round of K trees for
+multiclass). The timed region trains --steps trees from scratch on the
+HBM-resident dataset, bracketed by device synchronization (the library syncs
+before returning): `ms_per_step`. Whatever --steps says, every run also
+trains the workload's full tree count (500 for C2) from scratch and times it:
+`train_sec_per_<full>_trees` is that measured time, never an extrapolation.
+
+`value` is the histogram-build throughput of an instrumented run of the full
+training: the algorithmic bytes of every histogram the run accumulated -- the
+root and each expansion's smaller child, speculative expansions included --
+m rows * (F + gh) (uint8 bins + the g/h pair: 2 bytes int8, 8 bytes fp32; row
+ids, LDS traffic and partial writes not counted), over the durations of the
+kernels that accumulate them (k_hist for the root, k_accum for the children).
+The durations come from HIP events that the runtime records at each kernel's
+own start and end (hipExtLaunchKernel), on the stream the kernel runs on, so
+they are the kernel times rocprofv3's kernel trace reports. `roofline` prices
+k_accum alone; `traffic` is its HBM bytes per launch from rocprofv3 PMC
+counters. The conservative figure that charges every growth kernel
+(partition, accumulation, partial merge and scan, planning) against the
+committed trees' builds only is reported as `hist_gbs_committed_over_growth`.
 
 cpu_baseline: the CPU oracle (a C++ restatement of the reference's CPU
 trainer; the reference itself is Mojo and cannot run here) on the first
---cpu-trees trees of the same workload on all rows, whose trees are also
-compared bit for bit with the GPU's.
+--cpu-trees trees of the same workload on all rows (a bounded sample of
+10-20 s), whose trees are also compared bit for bit with the GPU's, on the
+host cores this process may use, at most 16 (a GPU box's CPU share for one
+GPU); the CPU model is reported beside it.
 """
 import argparse
 import json
@@ -41,6 +48,13 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "hist-build GB/s (% HBM peak) + train sec/500 trees, 10.5M×28 logistic, 1 GPU"
+# the same metric on the other BASELINE configurations
+METRICS = {
+    "c2": METRIC,
+    "c3": "hist-build GB/s (% HBM peak) + train sec/500 trees, 10.5M×28 logistic, fp32 g/h + GOSS, 1 GPU",
+    "c4": "hist-build GB/s (% HBM peak) + train sec/200 trees, 400k×2000 logistic, 63 bins, 1 GPU",
+    "c5": "hist-build GB/s (% HBM peak) + train sec/100 rounds, 2M×50 softmax 10 classes, 1 GPU",
+}
 
 
 def c2_data(n_rows, seed=0x5EED0002):
@@ -114,23 +128,23 @@ def c5_data(n_rows, n_classes=10, seed=0x5EED0005):
 WORKLOADS = {
     "c2": dict(rows=10_500_000, features=28, max_bin=255, leaves=255, trees=500, classes=1,
                gh_bytes=2, params=dict(objective=1, use_quantized_grad=1),
-               cpu_sample=6, desc="C2: 10.5M x 28 binary logistic, max_bin 255, num_leaves 255, "
+               cpu_sample=16, desc="C2: 10.5M x 28 binary logistic, max_bin 255, num_leaves 255, "
                     "quantized gradients (int8 g/h, int32 histogram bins)",
                dtype="int8 g/h, int32 cells"),
     "c3": dict(rows=10_500_000, features=28, max_bin=255, leaves=255, trees=500, classes=1,
                gh_bytes=8, params=dict(objective=1, use_quantized_grad=0, goss=1, top_rate=0.2,
                                        other_rate=0.1),
-               cpu_sample=6, desc="C3: the C2 workload with fp32 gradients (fp64 histogram sums) and GOSS "
+               cpu_sample=14, desc="C3: the C2 workload with fp32 gradients (fp64 histogram sums) and GOSS "
                     "(top_rate 0.2, other_rate 0.1, warmup 10 rounds)",
                dtype="fp32 g/h, fp64 sums"),
     "c4": dict(rows=400_000, features=2000, max_bin=63, leaves=127, trees=200, classes=1,
                gh_bytes=2, params=dict(objective=1, use_quantized_grad=1),
-               cpu_sample=4, desc="C4: 400k x 2000 binary logistic (sparse linear label), max_bin 63, "
+               cpu_sample=10, desc="C4: 400k x 2000 binary logistic (sparse linear label), max_bin 63, "
                     "num_leaves 127, quantized gradients; 16 feature tiles",
                dtype="int8 g/h, int32 cells"),
     "c5": dict(rows=2_000_000, features=50, max_bin=255, leaves=63, trees=100, classes=10,
                gh_bytes=2, params=dict(objective=2, num_class=10, use_quantized_grad=1),
-               cpu_sample=2, categorical=list(range(40, 50)),
+               cpu_sample=6, categorical=list(range(40, 50)),
                desc="C5: 2M x 50 (40 continuous, 10 integer columns of cardinality 4-64 split as "
                     "category sets) softmax, 10 classes, max_bin 255, num_leaves 63, quantized "
                     "gradients per class; a step is one round of 10 trees",
@@ -144,6 +158,27 @@ def workload_data(name, n_rows):
     if name == "c4":
         return c4_data(n_rows)
     return c5_data(n_rows)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def host_cores():
+    """(cores used, cores visible): the CPUs this process may run on, at most
+    16, a GPU box's CPU share for one GPU."""
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except AttributeError:
+        visible = os.cpu_count() or 1
+    return min(16, visible), visible
 
 
 def traffic_per_launch(workload):
@@ -272,14 +307,25 @@ def main():
     trees = fit.n_trees
     print(f"[bench] timed: {args.steps} steps in {wall:.3f}s ({trees} trees kept)",
           file=sys.stderr, flush=True)
+    # the workload's full training, measured whatever --steps is
+    full = wl["trees"]
+    if args.steps == full:
+        full_fit, full_wall = fit, wall
+    else:
+        t2 = time.perf_counter()
+        full_fit = ds.train(num_iterations=full, **kw)
+        full_wall = time.perf_counter() - t2
+    print(f"[bench] full training: {full} steps in {full_wall:.3f}s ({full_fit.n_trees} trees kept)",
+          file=sys.stderr, flush=True)
 
     st = None
+    stat_steps = full
     if not args.no_instrumented:
-        ifit = ds.train(num_iterations=args.steps, time_histograms=1, **kw)
+        ifit = ds.train(num_iterations=full, time_histograms=1, **kw)
         st = ifit.stats
-        same = np.array_equal(ifit.threshold, fit.threshold) and np.array_equal(
-            ifit.value.view(np.uint64), fit.value.view(np.uint64))
-        print(f"[bench] instrumented run done (trees identical to timed run: {same})",
+        same = np.array_equal(ifit.threshold, full_fit.threshold) and np.array_equal(
+            ifit.value.view(np.uint64), full_fit.value.view(np.uint64))
+        print(f"[bench] instrumented full run done (trees identical to the timed run: {same})",
               file=sys.stderr, flush=True)
     root_mean_ms, root_min_ms, root_merged_ms = ds.bench_root_histogram(reps=20)
 
@@ -290,7 +336,7 @@ def main():
         sys.path.insert(0, str(ROOT / "tests"))
         import oracle_lib as O
 
-        cores = min(16, os.cpu_count() or 1)
+        cores, visible = host_cores()
         oparams = {k: v for k, v in kw.items() if k not in ("num_grad_quant_bins", "stochastic_rounding")}
         p = O.default_params(num_iterations=args.cpu_trees, num_grad_quant_bins=4, n_threads=cores,
                              **oparams)
@@ -299,26 +345,26 @@ def main():
         tc = time.perf_counter()
         ref = O.train(bins, args.rows, F, NB, y, p, missing_bin=missing)
         cpu_s = time.perf_counter() - tc
-        k = min(ref.n_trees, fit.n_trees)
-        a, b = ref.off[k], fit.off[k]
+        k = min(ref.n_trees, full_fit.n_trees)
+        a, b = ref.off[k], full_fit.off[k]
         same_shape = bool(a == b and all(
-            np.array_equal(getattr(ref, f)[:a], getattr(fit, f)[:b])
+            np.array_equal(getattr(ref, f)[:a], getattr(full_fit, f)[:b])
             for f in ("feature", "threshold", "left", "right", "default_left", "cat_bits")))
         if wl["params"].get("use_quantized_grad"):
             parity = same_shape and bool(np.array_equal(ref.value[:a].view(np.uint64),
-                                                        fit.value[:b].view(np.uint64)))
+                                                        full_fit.value[:b].view(np.uint64)))
             how = "bit-identical"
         else:
-            parity = same_shape and bool(np.allclose(ref.value[:a], fit.value[:b], rtol=1e-5, atol=0))
+            parity = same_shape and bool(np.allclose(ref.value[:a], full_fit.value[:b], rtol=1e-5, atol=0))
             how = "same splits, values within 1e-5"
         per_step = cpu_s / max(1, args.cpu_trees)
-        full = wl["trees"]
         unit_steps = "rounds" if K > 1 else "trees"
         cpu = {"value": round(per_step * full, 2), "unit": f"s/{full} {unit_steps}", "cores": cores,
-               "kind": "port",
+               "kind": "port", "cpu_model": cpu_model(), "cpus_visible": visible,
                "sample": f"first {args.cpu_trees} {unit_steps} of the {args.workload.upper()} workload "
                          f"on all {args.rows} rows ({cpu_s:.1f}s, {per_step:.2f}s each, "
-                         f"extrapolated x{full}); trees {how} to GPU: {parity}"}
+                         f"scaled x{full / args.cpu_trees:.1f} to {full} {unit_steps}) on {cores} "
+                         f"threads; trees {how} to GPU: {parity}"}
         print(f"[bench] cpu oracle {args.cpu_trees} {unit_steps} in {cpu_s:.1f}s", file=sys.stderr,
               flush=True)
 
@@ -336,7 +382,7 @@ def main():
         kernel_gbs = st["accum_bytes"] / (st["accum_ms"] * 1e-3) / 1e9
         kernel_avg_ms = st["accum_ms"] / launches
         part_bytes = st["rows_parted"] * 9.0
-        per_tree = 1.0 / max(1, args.steps)
+        per_tree = 1.0 / max(1, stat_steps)
         extra = {
             "hist_rows_features_per_s": round(acc_bytes / (F + GH) * F / (acc_ms * 1e-3), 1),
             "hist_gbs_committed_over_growth": round(st["hist_bytes"] / (st["growth_ms"] * 1e-3) / 1e9, 2),
@@ -357,16 +403,18 @@ def main():
             "accum_kernel_avg_ms": round(kernel_avg_ms, 5),
         }
         note = (f"dominant histogram kernel k_accum (smaller-child accumulation from the "
-                f"partitioned row list), algorithmic bytes per launch = accumulated rows * "
-                f"(F + {GH}), over its average launch ({kernel_avg_ms * 1e3:.1f} us, "
-                f"{int(st['expand_launches'])} launches incl. empty tail launches); root build "
-                f"k_hist alone {root_gbs:.0f} GB/s ({root_gbs / HBM_PEAK_GBS:.1%})")
+                f"partitioned row list) over the instrumented {stat_steps}-step training, "
+                f"algorithmic bytes per launch = accumulated rows * (F + {GH}) "
+                f"({st['accum_bytes'] / launches / 1e6:.2f} MB), over its average kernel duration "
+                f"({kernel_avg_ms * 1e3:.1f} us, {int(st['expand_launches'])} launches incl. empty "
+                f"tail launches); root build k_hist alone {root_gbs:.0f} GB/s "
+                f"({root_gbs / HBM_PEAK_GBS:.1%})")
     else:
         value = root_gbs
         kernel_gbs = root_gbs
         note = "root build only (instrumented run skipped)"
     out = {
-        "metric": METRIC,
+        "metric": METRICS[args.workload],
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -381,8 +429,8 @@ def main():
         "config": {"workload": wl["desc"], "rows": args.rows, "features": F, "max_bin": NB,
                    "num_leaves": L, "steps": args.steps, "trees_per_step": K},
         "train_seconds": round(wall, 3),
-        f"train_sec_per_{wl['trees']}_{'rounds' if K > 1 else 'trees'}":
-            round(wall * wl["trees"] / max(1, args.steps), 3),
+        f"train_sec_per_{full}_{'rounds' if K > 1 else 'trees'}": round(full_wall, 3),
+        "full_training_trees_kept": full_fit.n_trees,
         "hist_frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         **extra,
         "root_hist_gbs": round(root_gbs, 1),

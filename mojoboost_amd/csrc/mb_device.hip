@@ -810,14 +810,19 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         PinnedFlags flags;
         HIPX(hipHostMalloc((void **)&flags.p, 2 * sizeof(mb::Batch), hipHostMallocDefault));
         // events: [0..1] flag markers of the two in-flight groups; when
-        // timed, [2..4] the root build and per group slot kMaxGroup x 4
-        // (before the partition, after it, after the accumulation, after
-        // scan + plan)
-        const int n_ev = 2 + (timed ? 3 + 2 * kMaxGroup * 4 : 0);
+        // timed, [2..4] the root build (kernel start, kernel end, after its
+        // scan + plan) and per group slot kMaxGroup x 6: the partition and
+        // the accumulation kernels' own start and end (recorded by the
+        // launch itself, so no queue gap is counted) and stream events
+        // around scan + plan
+        constexpr int kEvPer = 6;
+        const int n_ev = 2 + (timed ? 3 + 2 * kMaxGroup * kEvPer : 0);
         events.resize(n_ev);
         for (int i = 0; i < n_ev; ++i)
             HIPX(hipEventCreateWithFlags(&events[i], i < 2 ? hipEventDisableTiming : hipEventDefault));
-        auto ev_group = [&](int slot, int c, int k) { return events[5 + (slot * kMaxGroup + c) * 4 + k]; };
+        auto ev_group = [&](int slot, int c, int k) {
+            return events[5 + (slot * kMaxGroup + c) * kEvPer + k];
+        };
         double t_acc = 0.0, t_root = 0.0, t_root_scan = 0.0, t_pb = 0.0, t_scan = 0.0;
         double t_part = 0.0, t_accum = 0.0;
         double pb_launches = 0.0;
@@ -825,8 +830,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             for (int c = 0; c < n; ++c) {
                 float a = 0.f, b = 0.f, d = 0.f;
                 HIPX(hipEventElapsedTime(&a, ev_group(slot, c, 0), ev_group(slot, c, 1)));
-                HIPX(hipEventElapsedTime(&b, ev_group(slot, c, 1), ev_group(slot, c, 2)));
-                HIPX(hipEventElapsedTime(&d, ev_group(slot, c, 2), ev_group(slot, c, 3)));
+                HIPX(hipEventElapsedTime(&b, ev_group(slot, c, 2), ev_group(slot, c, 3)));
+                HIPX(hipEventElapsedTime(&d, ev_group(slot, c, 4), ev_group(slot, c, 5)));
                 t_part += a;
                 t_accum += b;
                 t_pb += a + b;
@@ -846,9 +851,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             if (!(fuse_objective && t > 0)) HIPX(mb::launch_objective(s, grid_rows, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
             if (s.hp.goss) HIPX(mb::launch_goss(s, st));
-            if (timed) HIPX(hipEventRecord(events[2], st));
-            HIPX(mb::launch_hist(s, st));
-            if (timed) HIPX(hipEventRecord(events[3], st));
+            if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3]));
+            else HIPX(mb::launch_hist(s, st));
             HIPX(mb::launch_scan(s, 1, st));
             HIPX(mb::launch_plan(s, 1, st));
             if (timed) HIPX(hipEventRecord(events[4], st));
@@ -862,14 +866,17 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 const int n = k == 0 ? std::max(1, std::min(est - 2, kMaxGroup)) : kNextGroup;
                 group_size[slot] = n;
                 for (int c = 0; c < n; ++c) {
-                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 0), st));
-                    HIPX(mb::launch_partition(s, st));
-                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 1), st));
-                    HIPX(mb::launch_accum(s, st));
-                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 2), st));
+                    if (timed) {
+                        HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1)));
+                        HIPX(mb::launch_accum(s, st, ev_group(slot, c, 2), ev_group(slot, c, 3)));
+                        HIPX(hipEventRecord(ev_group(slot, c, 4), st));
+                    } else {
+                        HIPX(mb::launch_partition(s, st));
+                        HIPX(mb::launch_accum(s, st));
+                    }
                     HIPX(mb::launch_scan(s, 0, st));
                     HIPX(mb::launch_plan(s, 0, st));
-                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 3), st));
+                    if (timed) HIPX(hipEventRecord(ev_group(slot, c, 5), st));
                 }
                 pb_launches += n;
                 iters += n;
@@ -1494,9 +1501,8 @@ int32_t mbh_bench_root_histogram(mbh_dataset *ds, int32_t reps, double *out_ms, 
         HIPX(mb::prepare_kernels(s));
         for (auto &e : ev) HIPX(hipEventCreate(&e));
         for (int i = 0; i < reps; ++i) {
-            HIPX(hipEventRecord(ev[3 * i], nullptr));
-            HIPX(mb::launch_hist(s, nullptr));
-            HIPX(hipEventRecord(ev[3 * i + 1], nullptr));
+            // the kernel's own start and end (no queue gap), then its merge
+            HIPX(mb::launch_hist(s, nullptr, ev[3 * i], ev[3 * i + 1]));
             HIPX(mb::launch_scan(s, 1, nullptr));
             HIPX(mb::launch_plan(s, 1, nullptr));
             HIPX(hipEventRecord(ev[3 * i + 2], nullptr));

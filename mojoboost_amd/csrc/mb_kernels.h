@@ -20,9 +20,11 @@ size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized);
 size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
 size_t rank_lds_bytes(const DevState &s);
-hipError_t launch_hist(const DevState &s, hipStream_t st);
-hipError_t launch_partition(const DevState &s, hipStream_t st);
-hipError_t launch_accum(const DevState &s, hipStream_t st);
+// With both events given, the runtime records them at the kernel's own start
+// and end (for timing without queue gaps).
+hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);

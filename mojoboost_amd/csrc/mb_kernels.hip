@@ -27,6 +27,7 @@
 // quantized_split_gain, tree.grow_tree_leaves_profiled and
 // growth_policy.GrowthSchedule.next_leaf (leaf choice), and
 // boosting._add_by_leaf (score update).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "mb_kernels.h"
@@ -3739,41 +3740,49 @@ hipError_t prepare_kernels(const DevState &s) {
     MB_SET_LDS(k_score_objective, score_lds_bytes(s));
     return hipSuccess;
 }
+// A launch of kernel k with DevState s; with both events given, the runtime
+// records them at the kernel's own start and end (hipExtLaunchKernel), so
+// their elapsed time is the kernel's duration without the queue gaps that
+// stream events around the launch would add.
+template <class K>
+hipError_t launch_timed(K k, dim3 grid, dim3 block, size_t lds, hipStream_t st, const DevState &s,
+                        hipEvent_t ev0, hipEvent_t ev1) {
+    if (ev0 && ev1) hipExtLaunchKernelGGL(k, grid, block, (uint32_t)lds, st, ev0, ev1, 0u, s);
+    else hipLaunchKernelGGL(k, grid, block, lds, st, s);
+    return hipGetLastError();
+}
 template <class Acc>
-hipError_t launch_hist_t(const DevState &s, hipStream_t st) {
+hipError_t launch_hist_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const size_t lds = hist_lds_bytes(s);
     const dim3 grid(s.hist_grid, s.n_tiles), block(kHistThreads);
     switch (s.rec_bytes / 16) {
-    case 1: hipLaunchKernelGGL((k_hist<1, Acc>), grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL((k_hist<2, Acc>), grid, block, lds, st, s); break;
-    case 4: hipLaunchKernelGGL((k_hist<4, Acc>), grid, block, lds, st, s); break;
-    case 8: hipLaunchKernelGGL((k_hist<8, Acc>), grid, block, lds, st, s); break;
+    case 1: return launch_timed(k_hist<1, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 2: return launch_timed(k_hist<2, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 4: return launch_timed(k_hist<4, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 8: return launch_timed(k_hist<8, Acc>, grid, block, lds, st, s, ev0, ev1);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
-hipError_t launch_hist(const DevState &s, hipStream_t st) {
-    return s.hp.quantized ? launch_hist_t<QAcc>(s, st) : launch_hist_t<FAcc>(s, st);
+hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    return s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1) : launch_hist_t<FAcc>(s, st, ev0, ev1);
 }
-hipError_t launch_partition(const DevState &s, hipStream_t st) {
-    hipLaunchKernelGGL(k_partition, dim3(s.part_launch), dim3(kPartThreads), 0, st, s);
-    return hipGetLastError();
+hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    return launch_timed(k_partition, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
 }
 template <class Acc>
-hipError_t launch_accum_t(const DevState &s, hipStream_t st) {
+hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const size_t lds = hist_lds_bytes(s);
     const dim3 grid(s.pb_launch, s.n_tiles), block(1024);
     switch (s.rec_bytes / 16) {
-    case 1: hipLaunchKernelGGL((k_accum<1, Acc>), grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL((k_accum<2, Acc>), grid, block, lds, st, s); break;
-    case 4: hipLaunchKernelGGL((k_accum<4, Acc>), grid, block, lds, st, s); break;
-    case 8: hipLaunchKernelGGL((k_accum<8, Acc>), grid, block, lds, st, s); break;
+    case 1: return launch_timed(k_accum<1, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 2: return launch_timed(k_accum<2, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 4: return launch_timed(k_accum<4, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 8: return launch_timed(k_accum<8, Acc>, grid, block, lds, st, s, ev0, ev1);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
-hipError_t launch_accum(const DevState &s, hipStream_t st) {
-    return s.hp.quantized ? launch_accum_t<QAcc>(s, st) : launch_accum_t<FAcc>(s, st);
+hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    return s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1) : launch_accum_t<FAcc>(s, st, ev0, ev1);
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     const int grid = root_mode ? s.n_features : s.scan_grid;
