@@ -90,6 +90,15 @@ typedef struct {
     double cat_l2;
     int32_t min_data_per_group;
     int32_t one_hot_max_size;
+    /* quantized-gradient lattice (derive_scales,
+     * src/mojotrees/quantized_gradient.mojo:1343-1453): 0 LightGBM's
+     * max-abs rule, num_grad_quant_bins units, int8 pairs (default); 1 the
+     * reference's magnitude-sum power-of-two rule (the lattice its GPU
+     * histogram ships and its CPU quantized path defaults to): scales
+     * 2^k <= 2^30 / sum|g| (sum|h|), int32 pairs, int32 histogram sums;
+     * num_grad_quant_bins is then unused. n_rows < 2^30; not with
+     * lambdarank. */
+    int32_t quant_scale_rule;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -270,6 +279,23 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *params,
                                float *grad, float *hess, int8_t *q_grad,
                                int8_t *q_hess, double *scales, char *err,
                                int32_t err_len);
+
+/* The same for either lattice with int32 outputs: with quant_scale_rule 1
+ * (the magnitude-sum lattice) q_grad/q_hess receive the 2^30-lattice values
+ * and scales[2..3] the device magnitude sums (sum |g|, sum |h|) the scales
+ * came from; scales holds 4 doubles. */
+int32_t mbh_objective_quantize32(mbh_dataset *ds, const mbh_params *params,
+                                 const double *raw, int64_t round_index, float *grad,
+                                 float *hess, int32_t *q_grad, int32_t *q_hess,
+                                 double *scales, char *err, int32_t err_len);
+
+/* Histogram of the magnitude-sum lattice (int32 values per row, hessians
+ * nonnegative, the selection's sums of |q| below 2^31) over `rows[0..n_sel)`
+ * (all rows when rows is NULL): out is n_features * n_bins * 3 int32
+ * {grad, hess, count}. */
+int32_t mbh_histogram32(mbh_dataset *ds, const int32_t *q_grad, const int32_t *q_hess,
+                        const int32_t *rows, int64_t n_sel, int32_t *out, char *err,
+                        int32_t err_len);
 
 /* Histogram of the rows `rows[0..n_sel)` (all rows when rows is NULL) with the
  * given int8 q_grad/q_hess: out is n_features * n_bins * 3 int32

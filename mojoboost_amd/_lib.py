@@ -38,6 +38,7 @@ MBH_SYMBOLS = [
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
     "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
     "mbh_histogram_noalloc", "mbh_save_model_named", "mbh_model_feature_names",
+    "mbh_objective_quantize32", "mbh_histogram32",
 ]
 
 
@@ -77,6 +78,7 @@ class MbhParams(C.Structure):
         ("cat_l2", C.c_double),
         ("min_data_per_group", C.c_int32),
         ("one_hot_max_size", C.c_int32),
+        ("quant_scale_rule", C.c_int32),
     ]
 
 
@@ -90,7 +92,7 @@ def mbh_params(**kw) -> MbhParams:
                   top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0,
                   lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0,
                   max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
-                  min_data_per_group=100, one_hot_max_size=-1)
+                  min_data_per_group=100, one_hot_max_size=-1, quant_scale_rule=0)
     for k, v in kw.items():
         setattr(p, k, v)
     return p
@@ -154,6 +156,8 @@ def lib():
         "mbh_exp_sigmoid": (I32, [V, I64, V, V, C.c_char_p, I32]),
         "mbh_objective_quantize": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),
+        "mbh_objective_quantize32": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
+        "mbh_histogram32": (I32, [V, V, V, V, I64, V, C.c_char_p, I32]),
         "mbh_histogram_fp32": (I32, [V, V, V, V, I64, V, V, C.c_char_p, I32]),
         "mbh_histogram_noalloc": (I32, [V, I64, I32, I32, V, V, V, I64, I32, V, V, V, C.c_char_p, I32]),
         "mbh_bench_root_histogram": (I32, [V, I32, V, C.c_char_p, I32]),

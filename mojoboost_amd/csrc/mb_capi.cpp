@@ -88,6 +88,7 @@ const std::map<std::string, std::string> &aliases() {
         {"use_quantized_grad", "use_quantized_grad"},
         {"num_grad_quant_bins", "num_grad_quant_bins"},
         {"stochastic_rounding", "stochastic_rounding"},
+        {"quant_scale_rule", "quant_scale_rule"},
         {"bagging_fraction", "bagging_fraction"},
         {"subsample", "bagging_fraction"},
         {"bagging_freq", "bagging_freq"},
@@ -127,7 +128,7 @@ const char *kPrimaryKeys =
     "bagging_freq,bagging_seed,boosting,top_rate,other_rate,min_data_in_bin,"
     "bin_construct_sample_cnt,data_random_seed,lambdarank_truncation_level,sigmoid,lambdarank_norm,"
     "categorical_feature,max_cat_to_onehot,max_cat_threshold,cat_smooth,cat_l2,min_data_per_group,"
-    "one_hot_max_size";
+    "one_hot_max_size,quant_scale_rule";
 
 struct Config {
     mbh_params p{};
@@ -273,6 +274,13 @@ Config parse(const char *spec) {
             p.num_grad_quant_bins = (int)to_int(k, val);
         } else if (k == "stochastic_rounding") {
             p.stochastic_rounding = to_bool(k, val) ? 1 : 0;
+        } else if (k == "quant_scale_rule") {
+            // derive_scales' two rules (quantized_gradient.mojo:1343-1453):
+            // LightGBM's max-abs lattice, or the reference's magnitude-sum
+            // power-of-two lattice (its MOJOTREES_CPU_QUANT_SCALE switch)
+            if (val == "max_abs" || val == "0") p.quant_scale_rule = 0;
+            else if (val == "magnitude_sum" || val == "1") p.quant_scale_rule = 1;
+            else throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "quant_scale_rule must be max_abs or magnitude_sum"};
         } else if (k == "bagging_fraction") {
             p.bagging_fraction = to_double(k, val);
         } else if (k == "bagging_freq") {

@@ -238,7 +238,17 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     if (!(p->bagging_fraction > 0.0 && p->bagging_fraction <= 1.0)) bad("bagging_fraction must be in (0, 1]");
     if (p->bagging_freq < 0) bad("bagging_freq must be nonnegative");
     const int B = p->num_grad_quant_bins;
-    if (p->use_quantized_grad) {
+    if (p->quant_scale_rule != 0 && p->quant_scale_rule != 1)
+        bad("quant_scale_rule must be 0 (max_abs) or 1 (magnitude_sum)");
+    if (p->use_quantized_grad && p->quant_scale_rule == 1) {
+        // the headroom argument of fixed_point_scale_pow2
+        // (quantized_gradient.mojo:908-1117): a node's int32 sum stays
+        // within 2^30 + n_rows
+        if (ds->n >= ((int64_t)1 << 30))
+            unsup("quant_scale_rule=magnitude_sum needs n_rows below 2^30 (int32 histogram sums)");
+        if (p->objective == MBH_OBJ_LAMBDARANK)
+            unsup("quant_scale_rule=magnitude_sum with lambdarank is not built on the device path");
+    } else if (p->use_quantized_grad) {
         if (B < 2 || B > 126 || B % 2 != 0)
             unsup("num_grad_quant_bins must be even and in [2, 126] (int8 gradient storage)");
         if ((double)ds->n * (double)(B + 1) >= 2147483647.0)
@@ -269,9 +279,9 @@ struct RecLayout {
     int rec = 0, tile_f = 0, n_tiles = 0;
 };
 
-RecLayout record_layout(int F, int lds_stride, bool quantized) {
+RecLayout record_layout(int F, int lds_stride, int kind) {
     int ft_max = 126;
-    while (ft_max > 0 && mb::pb_lds_bytes_for(ft_max, lds_stride, quantized) + kPbStaticLds > 160 * 1024)
+    while (ft_max > 0 && mb::pb_lds_bytes_for(ft_max, lds_stride, kind) + kPbStaticLds > 160 * 1024)
         --ft_max;
     if (ft_max < 1)
         throw Error{MOJOTREES_ERROR_UNSUPPORTED, "one feature's histogram exceeds a workgroup's LDS"};
@@ -317,8 +327,11 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // them at most.
 constexpr int64_t kHistChunkMin = 4096;
 
-void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantized, Run &run) {
-    const int64_t limit = chunk_limit_for(B);
+void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run &run) {
+    const bool quantized = kind != mb::kAccFloat;
+    // the packed int8-lattice counters bound a block's rows; the other
+    // accumulators hold whole-round sums in every field
+    const int64_t limit = kind == mb::kAccQuant ? chunk_limit_for(B) : (int64_t)1 << 30;
     int64_t grid = (int64_t)ds->n_cu * mb::kHistBlocksPerCU;  // resident root-build blocks
     const int64_t need = (ds->n + limit - 1) / limit;
     if (grid < need) grid = need;
@@ -338,6 +351,7 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, bool quantize
     const size_t cells = (size_t)parts * ds->F * s.part_stride;
     if (quantized) {
         s.part = dalloc<unsigned long long>(cells, run.owned);
+        if (kind == mb::kAccWide) s.part_c = dalloc<uint32_t>(cells, run.owned);
     } else {
         s.fpart_g = dalloc<double>(cells, run.owned);
         s.fpart_h = dalloc<double>(cells, run.owned);
@@ -393,7 +407,9 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     const int F = ds->F;
     mb::DevState &s = tb.s;
     const bool quantized = p->use_quantized_grad != 0;
-    ensure_records(ds, record_layout(F, ds->lds_stride, quantized));
+    const bool wide = quantized && p->quant_scale_rule == 1;
+    const int kind = wide ? mb::kAccWide : quantized ? mb::kAccQuant : mb::kAccFloat;
+    ensure_records(ds, record_layout(F, ds->lds_stride, kind));
     s.records = ds->d_records;
     s.records_w = ds->d_records;
     s.bins_cm = ds->d_bins_cm;
@@ -422,7 +438,11 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.e_cap = 1 + 2 * max_exp;
     if (quantized) s.hist = dalloc<int32_t>((size_t)(1 + max_exp) * F * ds->nb * 3, run.owned);
     else s.histf = dalloc<mb::HistF>((size_t)(1 + max_exp) * F * ds->nb, run.owned);
-    configure_hist(s, ds, quantized ? p->num_grad_quant_bins : 4, quantized, run);
+    configure_hist(s, ds, quantized ? p->num_grad_quant_bins : 4, kind, run);
+    if (wide) {
+        s.gq = dalloc<int32_t>(2 * (size_t)ds->n, run.owned);
+        s.magpart = dalloc<float>(2 * 256, run.owned);
+    }
     s.enodes = dalloc<mb::ENode>(s.e_cap, run.owned);
     s.items = dalloc<mb::Item>(s.kmax, run.owned);
     s.batch = dalloc<mb::Batch>(1, run.owned);
@@ -507,6 +527,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
         s.rank_pad = pad;
     }
     hp.quantized = p->use_quantized_grad ? 1 : 0;
+    hp.wide = wide ? 1 : 0;
     hp.goss = p->goss ? 1 : 0;
     // GossParams.warmup (goss.mojo:102-157): floor(1 / learning_rate) rounds
     hp.goss_warm = p->learning_rate > 0.0 ? (int32_t)(1.0 / p->learning_rate) : 0;
@@ -849,6 +870,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         for (int t = 0; t < T; ++t) {
             if (K > 1 && t % K == 0) HIPX(mb::launch_softmax(s, grid_rows, st));
             if (!(fuse_objective && t > 0)) HIPX(mb::launch_objective(s, grid_rows, st));
+            if (s.hp.wide) HIPX(mb::launch_magnitude(s, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
             if (s.hp.goss) HIPX(mb::launch_goss(s, st));
             if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3]));
@@ -914,6 +936,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         t_acc = t_root + t_pb;
         int32_t h_error = 0;
         HIPX(hipMemcpy(&h_error, s.error, sizeof(int32_t), hipMemcpyDeviceToHost));
+        if (h_error & 4)
+            throw Error{MOJOTREES_ERROR_TRAINING,
+                        "gradient/hessian magnitudes are out of range for the fixed-point histogram "
+                        "(quant_scale_rule=magnitude_sum)"};
         if (h_error)
             throw Error{MOJOTREES_ERROR_TRAINING,
                         std::string("device growth check failed (internal error, code ") +
@@ -936,7 +962,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         const bool bagging = s.hp.bagging != 0 || s.hp.goss != 0;  // sampled rounds are skipped, not stops
         // algorithmic bytes per accumulated row: its bins plus its g/h pair
         // (int8 x 2 quantized, fp32 x 2 otherwise)
-        const double rb = ds->F + (s.hp.quantized ? 2 : 8);
+        const double rb = ds->F + (s.hp.wide ? 8 : s.hp.quantized ? 2 : 8);
         double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
         double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
         int grown = 0;
@@ -1353,6 +1379,137 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const doubl
         HIPX(hipMemcpy(&rr, s.round, sizeof(rr), hipMemcpyDeviceToHost));
         scales[0] = rr.grad_units;
         scales[1] = rr.hess_units;
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_objective_quantize32(mbh_dataset *ds, const mbh_params *p, const double *raw, int64_t round_index,
+                                 float *grad, float *hess, int32_t *q_grad, int32_t *q_hess, double *scales,
+                                 char *err, int32_t err_len) {
+    if (!ds || !p || !raw || !grad || !hess || !q_grad || !q_hess || !scales) {
+        set_err(err, err_len, "null argument");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        if (!p->use_quantized_grad) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "use_quantized_grad must be 1"};
+        check_params(ds, p);
+        Run run;
+        mbh_params p1 = *p;
+        p1.num_iterations = 1;
+        if (round_index < 0) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "round_index must be nonnegative"};
+        TrainBuffers tb = setup_state(ds, &p1, run, round_index);
+        mb::DevState &s = tb.s;
+        mb::Round r0 = mb::initial_round();
+        r0.round = round_index;
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
+        HIPX(hipMemcpy(s.raw, raw, ds->n * sizeof(double), hipMemcpyHostToDevice));
+        const int grid = 8 * ds->n_cu;
+        HIPX(mb::launch_objective(s, grid, nullptr));
+        if (s.hp.wide) HIPX(mb::launch_magnitude(s, nullptr));
+        HIPX(mb::launch_quantize(s, grid, nullptr));
+        HIPX(hipDeviceSynchronize());
+        int32_t h_error = 0;
+        HIPX(hipMemcpy(&h_error, s.error, sizeof(int32_t), hipMemcpyDeviceToHost));
+        if (h_error & 4)
+            throw Error{MOJOTREES_ERROR_TRAINING, "gradient/hessian magnitudes are out of range for the fixed-point histogram"};
+        HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        if (s.hp.wide) {
+            std::vector<int32_t> q(2 * (size_t)ds->n);
+            HIPX(hipMemcpy(q.data(), s.gq, q.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+            for (int64_t r = 0; r < ds->n; ++r) {
+                q_grad[r] = q[2 * (size_t)r];
+                q_hess[r] = q[2 * (size_t)r + 1];
+            }
+            float part[512];
+            HIPX(hipMemcpy(part, s.magpart, sizeof(part), hipMemcpyDeviceToHost));
+            double tg = 0.0, th = 0.0;
+            for (int b = 0; b < 256; ++b) {
+                tg += (double)part[b];
+                th += (double)part[256 + b];
+            }
+            scales[2] = tg;
+            scales[3] = th;
+        } else {
+            std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
+            HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
+            for (int64_t r = 0; r < ds->n; ++r) {
+                q_grad[r] = (int8_t)rec[(size_t)r * ds->rec + ds->rec - 2];
+                q_hess[r] = (int8_t)rec[(size_t)r * ds->rec + ds->rec - 1];
+            }
+            scales[2] = 0.0;
+            scales[3] = 0.0;
+        }
+        mb::Round rr;
+        HIPX(hipMemcpy(&rr, s.round, sizeof(rr), hipMemcpyDeviceToHost));
+        scales[0] = rr.grad_units;
+        scales[1] = rr.hess_units;
+    } catch (const Error &e) {
+        set_err(err, err_len, e.msg);
+        return e.code;
+    }
+    return MOJOTREES_OK;
+}
+
+int32_t mbh_histogram32(mbh_dataset *ds, const int32_t *q_grad, const int32_t *q_hess, const int32_t *rows,
+                        int64_t n_sel, int32_t *out, char *err, int32_t err_len) {
+    if (!ds || !q_grad || !q_hess || !out || (rows && n_sel <= 0)) {
+        set_err(err, err_len, "invalid arguments");
+        return MOJOTREES_ERROR_INVALID_ARGUMENT;
+    }
+    try {
+        if (ds->n >= ((int64_t)1 << 30)) throw Error{MOJOTREES_ERROR_UNSUPPORTED, "n_rows must be below 2^30"};
+        // every subset of the selection must sum within int32: the lattice's
+        // headroom (|q| <= 2^30, sums of |q| below 2^31), checked here
+        const int64_t m = rows ? n_sel : ds->n;
+        int64_t sg = 0, sh = 0;
+        for (int64_t i = 0; i < m; ++i) {
+            const int64_t r = rows ? rows[i] : i;
+            if (r < 0 || r >= ds->n) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "row id out of range"};
+            if (q_hess[r] < 0) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "quantized hessians must be nonnegative"};
+            sg += q_grad[r] < 0 ? -(int64_t)q_grad[r] : (int64_t)q_grad[r];
+            sh += q_hess[r];
+        }
+        if (sg >= ((int64_t)1 << 31) || sh >= ((int64_t)1 << 31))
+            throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "the selection's quantized magnitudes exceed int32 cells"};
+        Run run;
+        mbh_params p{};
+        p.objective = MBH_OBJ_BINARY;
+        p.num_iterations = 1;
+        p.num_leaves = 2;
+        p.learning_rate = 0.1;
+        p.feature_fraction = 1.0;
+        p.bagging_fraction = 1.0;
+        p.num_grad_quant_bins = 4;
+        p.use_quantized_grad = 1;
+        p.quant_scale_rule = 1;
+        TrainBuffers tb = setup_state(ds, &p, run);
+        mb::DevState &s = tb.s;
+        std::vector<int32_t> q(2 * (size_t)ds->n);
+        for (int64_t r = 0; r < ds->n; ++r) {
+            q[2 * (size_t)r] = q_grad[r];
+            q[2 * (size_t)r + 1] = q_hess[r];
+        }
+        HIPX(hipMemcpy(s.gq, q.data(), q.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        const size_t cells = (size_t)ds->F * ds->nb * 3;
+        mb::Round r0 = mb::initial_round();
+        r0.grad_units = 1.0;
+        r0.hess_units = 1.0;
+        r0.sampled = rows ? 1 : 0;
+        HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
+        if (rows) {
+            HIPX(hipMemcpy(s.rows0, rows, n_sel * sizeof(int32_t), hipMemcpyHostToDevice));
+            int64_t c[2] = {n_sel, 0};
+            HIPX(hipMemcpy(s.cursor, c, sizeof(c), hipMemcpyHostToDevice));
+        }
+        HIPX(mb::prepare_kernels(s));
+        HIPX(mb::launch_hist(s, nullptr));
+        HIPX(mb::launch_scan(s, 1, nullptr));
+        HIPX(hipDeviceSynchronize());
+        HIPX(hipMemcpy(out, s.hist, cells * sizeof(int32_t), hipMemcpyDeviceToHost));
     } catch (const Error &e) {
         set_err(err, err_len, e.msg);
         return e.code;

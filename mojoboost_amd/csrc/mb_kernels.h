@@ -11,12 +11,18 @@ hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st);
 // The GOSS selection of the round (no-ops before the warmup ends).
 hipError_t launch_goss(const DevState &s, hipStream_t st);
+// The magnitude-sum lattice's reduction and scales (before launch_quantize).
+hipError_t launch_magnitude(const DevState &s, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
 // Raises the dynamic LDS limits of the kernels that need more than 64 KB.
 hipError_t prepare_kernels(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
+// histogram accumulators: packed int8-lattice counters, fp64 sums of fp32
+// gradients, int32 sums of the magnitude-sum lattice
+enum AccKind { kAccQuant = 0, kAccFloat = 1, kAccWide = 2 };
+inline int acc_kind(const HyperParams &hp) { return hp.wide ? kAccWide : hp.quantized ? kAccQuant : kAccFloat; }
 // accumulation LDS of a tile of tile_f features
-size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized);
+size_t pb_lds_bytes_for(int tile_f, int lds_stride, int kind);
 size_t plan_lds_bytes(const DevState &s);
 size_t score_lds_bytes(const DevState &s);
 size_t rank_lds_bytes(const DevState &s);

@@ -488,10 +488,13 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
                              : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
     if (max_g < 1e-12) max_g = 1e-12;
     if (max_h < 1e-12) max_h = 1e-12;
-    const int32_t gmax = hp.quant_bins / 2;
-    const int32_t hmax = hp.const_hessian ? 1 : hp.quant_bins;
-    const double gu = (double)gmax / max_g;
-    const double hu = hp.const_hessian ? 1.0 / max_h : (double)hmax / max_h;
+    // max-abs: (B / 2) / max|g| and B / max|h| with clamps B / 2, B; the
+    // magnitude-sum lattice: the round's power-of-two scales (k_magfold)
+    // with clamps 2^30; a constant hessian takes one unit over max|h| on both
+    const int32_t gmax = hp.wide ? (int32_t)kFixedOne : hp.quant_bins / 2;
+    const int32_t hmax = hp.const_hessian ? 1 : hp.wide ? (int32_t)kFixedOne : hp.quant_bins;
+    const double gu = hp.wide ? rd.grad_units : (double)gmax / max_g;
+    const double hu = hp.wide ? rd.hess_units : hp.const_hessian ? 1.0 / max_h : (double)hmax / max_h;
     const uint64_t gs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 0);
     const uint64_t hs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 1);
     const bool stoch = hp.stochastic != 0;
@@ -500,8 +503,10 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         s.round->sampled = hp.bagging;
         s.round->goss_mult = 1.0;
-        s.round->grad_units = gu;
-        s.round->hess_units = hu;
+        if (!hp.wide) {
+            s.round->grad_units = gu;
+            s.round->hess_units = hu;
+        }
         s.stats[(1 - rd.parity) * 2 + 0] = 0u;
         s.stats[(1 - rd.parity) * 2 + 1] = 0u;
         if (hp.grad64) {
@@ -519,9 +524,13 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
             const double hv = hp.grad64 ? s.hess64[r] : (double)s.hess[r];
             int32_t qg = quantize_scalar(gv, gu, gmax, stoch, gs + (uint64_t)r);
             int32_t qh = quantize_scalar(hv, hu, hmax, stoch, hs + (uint64_t)r);
-            uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
-            for (int t = 0; t < s.n_tiles; ++t)
-                *(uint16_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 2) = v;
+            if (hp.wide) {
+                *(int2 *)(s.gq + 2 * r) = make_int2(qg, qh);
+            } else {
+                uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
+                for (int t = 0; t < s.n_tiles; ++t)
+                    *(uint16_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 2) = v;
+            }
         }
         if (!hp.bagging) {
             if (valid) s.rows0[r] = (int32_t)r;
@@ -540,6 +549,78 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
             }
         }
     }
+}
+
+// ------------------------------------------------ magnitude-sum lattice
+// The magnitude reduction of the reference's device histogram, in its fixed
+// order (gpu_objectives_native._abs_sum_kernel :982-1040): 256 workgroups of
+// 256 threads; thread t of workgroup b adds |g| and |h| in binary32 for rows
+// b * 256 + t + k * 65536 of the round's sample (gradient_stats' subset,
+// quantized_gradient.mojo:762-810: rows outside it, and rows whose gradient
+// or hessian is not finite, add nothing); each workgroup then halves its 256
+// sums in LDS. The sums are the same bits on every run and every GPU.
+constexpr int kMagBlocks = 256, kMagThreads = 256;
+
+__global__ __launch_bounds__(kMagThreads) void k_magsum(DevState s) {
+    __shared__ float sg[kMagThreads], sh[kMagThreads];
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const HyperParams &hp = s.hp;
+    const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
+    const int t = threadIdx.x;
+    float ag = 0.0f, ah = 0.0f;
+    for (int64_t r = (int64_t)blockIdx.x * kMagThreads + t; r < s.n; r += (int64_t)kMagBlocks * kMagThreads) {
+        if (hp.bagging && !in_bag(s, bstream, bfall, r)) continue;
+        const float g = fabsf(s.grad[r]), h = fabsf(s.hess[r]);
+        if (!(isfinite(g) && isfinite(h))) continue;
+        ag += g;
+        ah += h;
+    }
+    sg[t] = ag;
+    sh[t] = ah;
+    __syncthreads();
+    for (int a = kMagThreads / 2; a > 0; a >>= 1) {
+        if (t < a) {
+            sg[t] = sg[t] + sg[t + a];
+            sh[t] = sh[t] + sh[t + a];
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        s.magpart[blockIdx.x] = sg[0];
+        s.magpart[kMagBlocks + blockIdx.x] = sh[0];
+    }
+}
+
+// sum_abs_partials (gpu_objectives_native.mojo:1100-1125): the workgroup sums
+// added in binary64 in ascending order, then derive_scales' magnitude-sum
+// rule (quantized_gradient.mojo:1343-1420): the power-of-two scales
+// fixed_point_scale_pow2(sum |g|) and (sum |h|), or one unit over max|h| for
+// a constant hessian. A total out of the fixed-point range flags the sticky
+// error (code 4) and leaves a unit scale.
+__global__ void k_magfold(DevState s) {
+    if (threadIdx.x != 0) return;
+    Round *rp = s.round;
+    if (rp->stopped) return;
+    double tg = 0.0, th = 0.0;
+    for (int b = 0; b < kMagBlocks; ++b) {
+        tg += (double)s.magpart[b];
+        th += (double)s.magpart[kMagBlocks + b];
+    }
+    bool okg = false, okh = true;
+    const double gu = fixed_point_scale_pow2(tg, okg);
+    double hu;
+    if (s.hp.const_hessian) {
+        double mh = (double)__uint_as_float(s.stats[rp->parity * 2 + 1]);
+        if (mh < 1e-12) mh = 1e-12;
+        hu = 1.0 / mh;
+    } else {
+        hu = fixed_point_scale_pow2(th, okh);
+    }
+    if (!okg || !okh) atomicOr(s.error, 4);
+    rp->grad_units = gu;
+    rp->hess_units = hu;
 }
 
 // -------------------------------------------------------------------- GOSS
@@ -1003,7 +1084,6 @@ __host__ __device__ constexpr int record_bytes_for(int tf) {
 }
 
 struct QAcc {
-    static constexpr int kUnroll = 3;  // partition tile: 3 x 1024 rows
     // LDS cells are bin-major: cell (byte position p of the record, bin) at
     // bin * FS + p, FS = max(32, record bytes). A 64-bit cell's banks then
     // depend on p alone, whatever the bin, and add() has the lanes of a wave
@@ -1096,7 +1176,6 @@ struct QAcc {
 };
 
 struct FAcc {
-    static constexpr int kUnroll = 2;  // partition tile: 2 x 1024 rows (LDS budget)
     static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 20; }
     template <int LPR>
     __device__ static void zero(unsigned char *lds, int F, int ls) {
@@ -1147,6 +1226,60 @@ struct FAcc {
             s.fpart_g[base + i] = in ? g[f * ls + b] : 0.0;
             s.fpart_h[base + i] = in ? h[f * ls + b] : 0.0;
             s.fpart_c[base + i] = in ? c[f * ls + b] : 0u;
+        }
+    }
+};
+
+// WAcc (the magnitude-sum lattice): each row's int32 (grad, hess) pair from
+// `gq`, gathered by row id; per cell one 64-bit LDS add of the packed pair --
+// hess in the low 32 bits (nonnegative, a cell's sum below 2^32), signed grad
+// in the high 32 -- and one 32-bit count. Any subset of a round's rows sums
+// to at most 2^30 + n in magnitude on this lattice (quantized_gradient.mojo:
+// 908-1117, the headroom argument), so neither field overflows and no carry
+// crosses from hess into grad, whatever the block's row count.
+struct WAcc {
+    static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 12; }
+    template <int LPR>
+    __device__ static void zero(unsigned char *lds, int F, int ls) {
+        unsigned long long *gh = (unsigned long long *)lds;
+        uint32_t *c = (uint32_t *)(gh + (size_t)F * ls);
+        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) {
+            gh[i] = 0ULL;
+            c[i] = 0u;
+        }
+    }
+    template <int LPR>
+    __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
+                               int64_t row, uint32_t, double) {
+        unsigned long long *gh = (unsigned long long *)lds;
+        uint32_t *c = (uint32_t *)(gh + (size_t)F * ls);
+        const int2 q = *(const int2 *)(s.gq + 2 * row);
+        const unsigned long long packed = ((unsigned long long)(uint32_t)q.x << 32) | (uint32_t)q.y;
+        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = sub * 16 + k * 4 + j;
+                if (f < F) {
+                    const int cell = f * ls + (int)((d[k] >> (8 * j)) & 255u);
+                    atomicAdd(&gh[cell], packed);
+                    atomicAdd(&c[cell], 1u);
+                }
+            }
+    }
+    template <int LPR>
+    __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
+        const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
+        const unsigned long long *gh = (const unsigned long long *)lds;
+        const uint32_t *c = (const uint32_t *)(gh + (size_t)Ft * ls);
+        const size_t base = ((size_t)blk * F + f0) * ps;
+        for (int i = threadIdx.x; i < Ft * ps; i += blockDim.x) {
+            const int f = i / ps;
+            const int b = i - f * ps;
+            const bool in = b < nb;
+            s.part[base + i] = in ? gh[f * ls + b] : 0ULL;
+            s.part_c[base + i] = in ? c[f * ls + b] : 0u;
         }
     }
 };
@@ -1534,22 +1667,40 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
                     s.part + (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
                 const int np = it.part_cnt;
                 int b = half;
-                for (; b + 14 < np; b += 16) {
-                    unsigned long long vv[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) vv[u] = p[(size_t)(b + 2 * u) * pstride];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        c += (int)(vv[u] & 0xFFFFFULL);
-                        h += (int)((vv[u] >> 20) & 0x3FFFFFULL);
-                        g += (int)((long long)vv[u] >> 42);
+                if (hp.wide) {
+                    // grad | hess halves and a separate count per partial
+                    // (WAcc); the sums wrap as unsigned words, and every
+                    // subset of the round's rows fits int32
+                    const uint32_t *pc =
+                        s.part_c + (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
+                    uint32_t ug = 0u, uh = 0u, uc = 0u;
+                    for (; b < np; b += 2) {
+                        const unsigned long long vv = p[(size_t)b * pstride];
+                        ug += (uint32_t)(vv >> 32);
+                        uh += (uint32_t)vv;
+                        uc += pc[(size_t)b * pstride];
                     }
-                }
-                for (; b < np; b += 2) {
-                    const unsigned long long vv = p[(size_t)b * pstride];
-                    c += (int)(vv & 0xFFFFFULL);
-                    h += (int)((vv >> 20) & 0x3FFFFFULL);
-                    g += (int)((long long)vv >> 42);
+                    g = (int)ug;
+                    h = (int)uh;
+                    c = (int)uc;
+                } else {
+                    for (; b + 14 < np; b += 16) {
+                        unsigned long long vv[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) vv[u] = p[(size_t)(b + 2 * u) * pstride];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            c += (int)(vv[u] & 0xFFFFFULL);
+                            h += (int)((vv[u] >> 20) & 0x3FFFFFULL);
+                            g += (int)((long long)vv[u] >> 42);
+                        }
+                    }
+                    for (; b < np; b += 2) {
+                        const unsigned long long vv = p[(size_t)b * pstride];
+                        c += (int)(vv & 0xFFFFFULL);
+                        h += (int)((vv >> 20) & 0x3FFFFFULL);
+                        g += (int)((long long)vv >> 42);
+                    }
                 }
             }
             if (half == 1) {
@@ -3690,17 +3841,24 @@ hipError_t launch_goss(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(1024), 0, st, s);
     return hipGetLastError();
 }
+hipError_t launch_magnitude(const DevState &s, hipStream_t st) {
+    hipLaunchKernelGGL(k_magsum, dim3(kMagBlocks), dim3(kMagThreads), 0, st, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_magfold, dim3(1), dim3(64), 0, st, s);
+    return hipGetLastError();
+}
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
 size_t score_lds_bytes(const DevState &s) { return (size_t)s.max_nodes * (s.t_cat ? 48 : 16); }
-size_t hist_lds_bytes(const DevState &s) {
-    return s.hp.quantized ? QAcc::lds_bytes(s.tile_f, s.lds_stride) : FAcc::lds_bytes(s.tile_f, s.lds_stride);
+size_t pb_lds_bytes_for(int tile_f, int lds_stride, int kind) {
+    return kind == kAccQuant  ? QAcc::lds_bytes(tile_f, lds_stride)
+           : kind == kAccWide ? WAcc::lds_bytes(tile_f, lds_stride)
+                              : FAcc::lds_bytes(tile_f, lds_stride);
 }
-size_t pb_lds_bytes_for(int tile_f, int lds_stride, bool quantized) {
-    return quantized ? QAcc::lds_bytes(tile_f, lds_stride) : FAcc::lds_bytes(tile_f, lds_stride);
-}
+size_t hist_lds_bytes(const DevState &s) { return pb_lds_bytes_for(s.tile_f, s.lds_stride, acc_kind(s.hp)); }
 size_t plan_lds_bytes(const DevState &s) {
     return plan_layout(s.hp.num_leaves, s.e_cap, s.kmax, s.n_features).total;
 }
@@ -3715,7 +3873,16 @@ size_t plan_lds_bytes(const DevState &s) {
 hipError_t prepare_kernels(const DevState &s) {
     const size_t h = hist_lds_bytes(s);
     if (s.hp.objective == kObjLambdarank) MB_SET_LDS(k_lambdarank, rank_lds_bytes(s));
-    if (s.hp.quantized) {
+    if (s.hp.wide) {
+        MB_SET_LDS((k_hist<1, WAcc>), h);
+        MB_SET_LDS((k_hist<2, WAcc>), h);
+        MB_SET_LDS((k_hist<4, WAcc>), h);
+        MB_SET_LDS((k_hist<8, WAcc>), h);
+        MB_SET_LDS((k_accum<1, WAcc>), h);
+        MB_SET_LDS((k_accum<2, WAcc>), h);
+        MB_SET_LDS((k_accum<4, WAcc>), h);
+        MB_SET_LDS((k_accum<8, WAcc>), h);
+    } else if (s.hp.quantized) {
         MB_SET_LDS((k_hist<1, QAcc>), h);
         MB_SET_LDS((k_hist<2, QAcc>), h);
         MB_SET_LDS((k_hist<4, QAcc>), h);
@@ -3764,7 +3931,9 @@ hipError_t launch_hist_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipE
     }
 }
 hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    return s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1) : launch_hist_t<FAcc>(s, st, ev0, ev1);
+    return s.hp.wide        ? launch_hist_t<WAcc>(s, st, ev0, ev1)
+           : s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1)
+                            : launch_hist_t<FAcc>(s, st, ev0, ev1);
 }
 hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     return launch_timed(k_partition, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
@@ -3782,7 +3951,9 @@ hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hip
     }
 }
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    return s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1) : launch_accum_t<FAcc>(s, st, ev0, ev1);
+    return s.hp.wide        ? launch_accum_t<WAcc>(s, st, ev0, ev1)
+           : s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1)
+                            : launch_accum_t<FAcc>(s, st, ev0, ev1);
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     const int grid = root_mode ? s.n_features : s.scan_grid;

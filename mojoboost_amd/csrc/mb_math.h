@@ -175,4 +175,29 @@ MB_HD int32_t quantize_scalar(double value, double units, int32_t max_unit, bool
     return (int32_t)round(y);
 }
 
+// The magnitude-sum lattice (quantized_gradient.mojo:856-1117): the scale is
+// the power of two 2^k <= fl(2^30 / max(total, 1e-12)), found by clearing
+// the mantissa bits of the quotient (largest_power_of_two_at_most), and must
+// be a binary32 value exactly (the reference multiplies in binary32). ok is
+// false for a non-finite total, a subnormal quotient or a power below 2^-149.
+constexpr double kFixedOne = 1073741824.0;  // FIXED_ONE = 2^30
+MB_HD double fixed_point_scale_pow2(double total, bool &ok) {
+    ok = false;
+    if (!(total == total) || total > 1.7976931348623157e308) return 1.0;
+    const double t = total < 1e-12 ? 1e-12 : total;
+    const double q = kFixedOne / t;
+    if (!(q > 0.0) || q > 1.7976931348623157e308) return 1.0;
+    unsigned long long b;
+    __builtin_memcpy(&b, &q, 8);
+    const unsigned long long biased = (b >> 52) & 0x7FFULL;
+    if (biased == 0) return 1.0;
+    const unsigned long long pb = biased << 52;
+    double p;
+    __builtin_memcpy(&p, &pb, 8);
+    const float f = (float)p;
+    if (!(f > 0.0f) || (double)f != p) return 1.0;
+    ok = true;
+    return p;
+}
+
 }  // namespace mb

@@ -170,7 +170,14 @@ struct HyperParams {
     int32_t quant_seed;
     int32_t const_hessian;
     int32_t bagging;        // 1: rows sampled per bag
-    int32_t quantized;      // 1: int8 gradients, integer histograms; 0: fp32 gradients, fp64 sums
+    int32_t quantized;      // 1: quantized gradients, integer histograms; 0: fp32 gradients, fp64 sums
+    // quantized lattice: 0 LightGBM's max-abs rule (int8 pair in each record,
+    // packed 64-bit LDS counters), 1 the reference's magnitude-sum
+    // power-of-two rule (int32 pair per row in `gq`, 2^30 lattice, int32 LDS
+    // sums: derive_scales with SCALE_MAGNITUDE_SUM, quantized_gradient.mojo:
+    // 1343-1453, and _quantize_grad_hess_kernel, gpu_active_rows.mojo:
+    // 2211-2255)
+    int32_t wide;
     int32_t goss;           // 1: GOSS from round goss_warm on
     int32_t goss_warm;
     int32_t goss_seed;
@@ -230,11 +237,17 @@ struct DevState {
     int32_t n_queries;
     int32_t rank_pad;               // largest query rounded up to a power of two
     uint32_t *stats;       // [2 parities][2]: max |g|, max |h| as float bits
+    // magnitude-sum lattice (hp.wide): each row's quantized (grad, hess)
+    // interleaved, and the magnitude reduction's 256 + 256 binary32
+    // workgroup sums (|g| then |h|)
+    int32_t *gq;
+    float *magpart;
     Round *round;
     // rows and histograms
     int32_t *rows0, *rows1;
     int32_t *hist;         // (1 + max_exp) x F x n_bins x 3 (grad, hess, count)
     unsigned long long *part;  // max(hist_grid, pb_grid) x F x part_stride packed partials
+    uint32_t *part_c;          // magnitude-sum lattice: the partials' counts (part holds grad | hess)
     HistF *histf;              // fp32 path: (1 + max_exp) x F x n_bins cells
     double *fpart_g, *fpart_h; // fp32 path partials, same shape as part
     uint32_t *fpart_c;

@@ -124,6 +124,33 @@ class Dataset:
                                            ptr(h), ptr(qg), ptr(qh), ptr(sc), err, 1024), err)
         return g, h, qg, qh, sc
 
+    def objective_quantize32(self, raw, round_index=0, **params):
+        """Either lattice with int32 values: (grad, hess, q_grad, q_hess,
+        [grad units, hess units, sum|g|, sum|h|]) -- the sums are the device
+        magnitude reduction's under quant_scale_rule=1, else 0."""
+        n = self.n_rows
+        p = _lib.mbh_params(**params)
+        g = np.zeros(n, np.float32)
+        h = np.zeros(n, np.float32)
+        qg = np.zeros(n, np.int32)
+        qh = np.zeros(n, np.int32)
+        sc = np.zeros(4)
+        err = C.create_string_buffer(1024)
+        raw = np.ascontiguousarray(raw, np.float64)
+        check(lib().mbh_objective_quantize32(self.h, C.byref(p), ptr(raw), round_index, ptr(g),
+                                             ptr(h), ptr(qg), ptr(qh), ptr(sc), err, 1024), err)
+        return g, h, qg, qh, sc
+
+    def histogram32(self, q_grad, q_hess, rows=None):
+        """Histogram of int32 quantized values (the magnitude-sum lattice)."""
+        out = np.zeros(self.n_features * self.n_bins * 3, np.int32)
+        r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+        err = C.create_string_buffer(1024)
+        check(lib().mbh_histogram32(self.h, ptr(np.ascontiguousarray(q_grad, np.int32)),
+                                    ptr(np.ascontiguousarray(q_hess, np.int32)), ptr(r),
+                                    0 if r is None else len(r), ptr(out), err, 1024), err)
+        return out.reshape(self.n_features, self.n_bins, 3)
+
     def histogram(self, q_grad, q_hess, rows=None, quant_bins=4):
         out = np.zeros(self.n_features * self.n_bins * 3, np.int32)
         r = None if rows is None else np.ascontiguousarray(rows, np.int32)

@@ -18,6 +18,13 @@
 //   fit_bins/transform .............. golden "large" fixture + closed forms
 //   quantizer (max-abs, stochastic) ... closed forms and the reference's
 //        worked example y=-1.3,u=0.9 -> -2 (quantized_gradient.mojo:1502-1505)
+//   magnitude-sum lattice: largest_power_of_two_at_most and
+//        fixed_point_scale_pow2 .... closed forms (exact powers, binade
+//        interiors, refusals) and the reference's assertions
+//        (tests/test_cpu_quantized_grad.mojo:429-460: the factor is its own
+//        power-of-two floor and <= 2^30 / sum|g|); magnitude_sums' fixed
+//        reduction order ... a hand-derived binary32 total that any other
+//        order, or a binary64 sum, misses (tests/test_oracle_magnitude.py)
 //   integer histogram ................ brute force + float/int agreement
 //   quantized split search ........... brute-force enumeration on tiny nodes
 //   GOSS ........... the reference's GOSS properties (tests/test_goss.mojo:
@@ -699,13 +706,102 @@ struct QScales {
     int64_t gmax = 0, hmax = 0;
 };
 
-// gradient_stats + derive_scales (max-abs) + quantize_round_cpu
+// The scale rules of derive_scales (quantized_gradient.mojo:1343-1453):
+// LightGBM's max-abs lattice, or the reference's magnitude-sum power-of-two
+// lattice (SCALE_MAGNITUDE_SUM at SCALE_SHAPE_POW2, the rule its GPU
+// histogram ships and its CPU quantized path defaults to).
+constexpr int kRuleMaxAbs = 0;
+constexpr int kRuleMagnitudeSum = 1;
+constexpr double kFixedOne = 1073741824.0;  // FIXED_ONE = 2^30 (quantized_gradient.mojo:418)
+constexpr double kMagnitudeFloor = 1e-12;   // MAGNITUDE_FLOOR (quantized_gradient.mojo:428)
+
+// largest_power_of_two_at_most (quantized_gradient.mojo:856-888): 2^floor(
+// log2 x) for a positive normal x, by clearing the mantissa bits; zero,
+// subnormal and non-finite inputs are refused.
+double largest_power_of_two_at_most(double x) {
+    if (!std::isfinite(x) || x <= 0.0) throw std::runtime_error("a power-of-two floor needs a positive finite value");
+    uint64_t b;
+    std::memcpy(&b, &x, 8);
+    const uint64_t biased = (b >> 52) & 0x7FF;
+    if (biased == 0) throw std::runtime_error("a power-of-two floor needs a normal value");
+    const uint64_t out = biased << 52;
+    double p;
+    std::memcpy(&p, &out, 8);
+    return p;
+}
+
+// fixed_point_scale_pow2 (quantized_gradient.mojo:908-1117): the power of two
+// 2^k <= fl(2^30 / max(total, 1e-12)), which must be a binary32 value exactly
+// (the width the device multiplies by).
+double fixed_point_scale_pow2(double total) {
+    if (!std::isfinite(total)) throw std::runtime_error("gradients and hessians must be finite");
+    const double t = total < kMagnitudeFloor ? kMagnitudeFloor : total;
+    const double q = kFixedOne / t;
+    if (!std::isfinite(q) || q <= 0.0)
+        throw std::runtime_error("gradient/hessian magnitudes are out of range for the fixed-point histogram");
+    const double p = largest_power_of_two_at_most(q);
+    const float f = (float)p;
+    if (!std::isfinite(f) || f <= 0.0f || (double)f != p)
+        throw std::runtime_error("gradient/hessian magnitudes are out of range for the fixed-point histogram");
+    return p;
+}
+
+// The device magnitude reduction in its fixed order
+// (gpu_objectives_native._abs_sum_kernel :982-1040 and sum_abs_partials
+// :1100-1125): 256 workgroups of 256 threads; thread t of workgroup b adds
+// |x| in binary32 for rows b * 256 + t, stepping by 65536; each workgroup
+// halves its 256 sums in binary32 (s[t] += s[t + a] for a = 128, 64, .., 1);
+// the 256 workgroup sums are added in binary64 in ascending order. Rows
+// outside the round's sample (in_sample[r] == 0) add nothing, and rows whose
+// gradient or hessian is not finite are left out, as gradient_stats
+// (:762-810) leaves them out.
+void magnitude_sums(const std::vector<double> &grad, const std::vector<double> &hess,
+                    const std::vector<uint8_t> &in_sample, double &sum_g, double &sum_h) {
+    constexpr int kBlocks = 256, kThreads = 256;
+    const int64_t n = (int64_t)grad.size();
+    std::vector<float> pg(kBlocks), ph(kBlocks);
+    float sg[kThreads], sh[kThreads];
+    for (int b = 0; b < kBlocks; ++b) {
+        for (int t = 0; t < kThreads; ++t) {
+            float ag = 0.0f, ah = 0.0f;
+            for (int64_t r = (int64_t)b * kThreads + t; r < n; r += (int64_t)kBlocks * kThreads) {
+                if (!in_sample.empty() && !in_sample[r]) continue;
+                const float g = std::fabs((float)grad[r]), h = std::fabs((float)hess[r]);
+                if (!(std::isfinite(g) && std::isfinite(h))) continue;
+                ag += g;
+                ah += h;
+            }
+            sg[t] = ag;
+            sh[t] = ah;
+        }
+        for (int a = kThreads / 2; a > 0; a /= 2)
+            for (int t = 0; t < a; ++t) {
+                sg[t] = sg[t] + sg[t + a];
+                sh[t] = sh[t] + sh[t + a];
+            }
+        pg[b] = sg[0];
+        ph[b] = sh[0];
+    }
+    sum_g = 0.0;
+    sum_h = 0.0;
+    for (int b = 0; b < kBlocks; ++b) {
+        sum_g += (double)pg[b];
+        sum_h += (double)ph[b];
+    }
+}
+
+// gradient_stats + derive_scales + quantize_round_cpu
 // (src/mojotrees/quantized_gradient.mojo:762-810, :1343-1453, :2487-2565).
+// Max-abs: units = (B / 2) / max|g| and B / max|h| (one unit over max|h|
+// under a constant hessian), clamps B / 2 and B. Magnitude sum: units =
+// fixed_point_scale_pow2(sum |g|) and (sum |h|) -- again 1 / max|h| with a
+// one-unit clamp under a constant hessian -- and clamps 2^30. Every row is
+// quantized; the sample decides the magnitudes.
 QScales quantize_round(const std::vector<double> &grad,
                        const std::vector<double> &hess, const int32_t *rows,
                        int64_t n_sel, int quant_bins, bool stochastic,
                        int64_t seed, int64_t round_index, int64_t class_index,
-                       bool const_hessian, int8_t *qg, int8_t *qh, Pool &pool) {
+                       bool const_hessian, int rule, int32_t *qg, int32_t *qh, Pool &pool) {
     int64_t n = (int64_t)grad.size();
     double max_g = 0.0, max_h = 0.0;
     int64_t count = rows ? n_sel : n;
@@ -716,18 +812,36 @@ QScales quantize_round(const std::vector<double> &grad,
         if (g > max_g) max_g = g;
         if (h > max_h) max_h = h;
     }
-    const double floor_mag = 1e-12;
     QScales s;
-    if (max_g < floor_mag) max_g = floor_mag;
-    if (max_h < floor_mag) max_h = floor_mag;
-    s.gmax = quant_bins / 2;
-    s.gu = (double)s.gmax / max_g;
-    if (const_hessian) {
-        s.hmax = 1;
-        s.hu = 1.0 / max_h;
+    if (max_g < kMagnitudeFloor) max_g = kMagnitudeFloor;
+    if (max_h < kMagnitudeFloor) max_h = kMagnitudeFloor;
+    if (rule == kRuleMagnitudeSum) {
+        std::vector<uint8_t> in_sample;
+        if (rows) {
+            in_sample.assign((size_t)n, 0);
+            for (int64_t i = 0; i < n_sel; ++i) in_sample[(size_t)rows[i]] = 1;
+        }
+        double sum_g = 0.0, sum_h = 0.0;
+        magnitude_sums(grad, hess, in_sample, sum_g, sum_h);
+        s.gu = fixed_point_scale_pow2(sum_g);
+        s.gmax = (int64_t)kFixedOne;
+        if (const_hessian) {
+            s.hu = 1.0 / max_h;
+            s.hmax = 1;
+        } else {
+            s.hu = fixed_point_scale_pow2(sum_h);
+            s.hmax = (int64_t)kFixedOne;
+        }
     } else {
-        s.hmax = quant_bins;
-        s.hu = (double)s.hmax / max_h;
+        s.gmax = quant_bins / 2;
+        s.gu = (double)s.gmax / max_g;
+        if (const_hessian) {
+            s.hmax = 1;
+            s.hu = 1.0 / max_h;
+        } else {
+            s.hmax = quant_bins;
+            s.hu = (double)s.hmax / max_h;
+        }
     }
     uint64_t gs = quant_stream(seed, round_index, class_index, 0);
     uint64_t hs = quant_stream(seed, round_index, class_index, 1);
@@ -735,8 +849,8 @@ QScales quantize_round(const std::vector<double> &grad,
     pool.run(blocks, [&](int64_t b) {
         int64_t lo = b * 65536, hi = std::min(n, lo + 65536);
         for (int64_t r = lo; r < hi; ++r) {
-            qg[r] = (int8_t)quantize_scalar(grad[r], s.gu, s.gmax, stochastic, gs + (uint64_t)r);
-            qh[r] = (int8_t)quantize_scalar(hess[r], s.hu, s.hmax, stochastic, hs + (uint64_t)r);
+            qg[r] = (int32_t)quantize_scalar(grad[r], s.gu, s.gmax, stochastic, gs + (uint64_t)r);
+            qh[r] = (int32_t)quantize_scalar(hess[r], s.hu, s.hmax, stochastic, hs + (uint64_t)r);
         }
     });
     return s;
@@ -748,7 +862,7 @@ struct QHist {
 };
 
 // Integer accumulation: order-free (quantized_gradient.mojo:2688-2945).
-void build_quant(QHist &out, const Data &d, const int8_t *qg, const int8_t *qh,
+void build_quant(QHist &out, const Data &d, const int32_t *qg, const int32_t *qh,
                  const int32_t *rows, int64_t m, const std::vector<int> &features,
                  Pool &pool) {
     out.reset(d.nf * d.nb);
@@ -1015,7 +1129,7 @@ struct FloatPolicy {
 
 struct QuantPolicy {
     const Data &d;
-    const int8_t *qg, *qh;
+    const int32_t *qg, *qh;
     const QScales &s;
     const Params &P;
     Pool &pool;
@@ -1445,7 +1559,7 @@ Tree grow_one(const Data &d, const Params &P, std::vector<double> &grad,
               std::vector<double> &hess, const std::vector<int32_t> &bag,
               int64_t round, int64_t class_index, int64_t tree_index,
               std::vector<std::pair<int, std::vector<int32_t>>> &leaves,
-              std::vector<int8_t> &qg, std::vector<int8_t> &qh, Pool &pool) {
+              std::vector<int32_t> &qg, std::vector<int32_t> &qh, Pool &pool) {
     const std::vector<int32_t> *bagp = bag.empty() ? nullptr : &bag;
     std::vector<int> tf = select_tree_features(d.nf, P.p.feature_fraction,
                                                P.p.feature_fraction_seed, tree_index);
@@ -1455,7 +1569,8 @@ Tree grow_one(const Data &d, const Params &P, std::vector<double> &grad,
         QScales s = quantize_round(grad, hess, bag.empty() ? nullptr : bag.data(),
                                    (int64_t)bag.size(), P.p.num_grad_quant_bins,
                                    P.p.stochastic_rounding != 0, P.p.quant_seed, round,
-                                   class_index, P.const_hessian, qg.data(), qh.data(), pool);
+                                   class_index, P.const_hessian, P.p.quant_scale_rule, qg.data(),
+                                   qh.data(), pool);
         QuantPolicy pol{d, qg.data(), qh.data(), s, P, pool, tf[0]};
         return grow_tree(pol, d, P, bagp, tree_index, &leaves);
     }
@@ -1679,26 +1794,71 @@ int32_t orc_grad_hess_w(int32_t objective, const double *raw, const double *labe
     return 0;
 }
 
+int32_t orc_quantize_rule(const double *grad, const double *hess, int64_t n,
+                          const int32_t *rows, int64_t n_sel, int32_t quant_bins,
+                          int32_t stochastic, int64_t seed, int64_t round_index,
+                          int64_t class_index, int32_t const_hessian, int32_t rule,
+                          int32_t *q_grad, int32_t *q_hess, double *out_scales) {
+    std::vector<double> g(grad, grad + n), h(hess, hess + n);
+    Pool pool(1);
+    try {
+        QScales s = quantize_round(g, h, rows, n_sel, quant_bins, stochastic != 0, seed,
+                                   round_index, class_index, const_hessian != 0, rule, q_grad,
+                                   q_hess, pool);
+        out_scales[0] = s.gu;
+        out_scales[1] = s.hu;
+        out_scales[2] = (double)s.gmax;
+        out_scales[3] = (double)s.hmax;
+    } catch (const std::exception &) {
+        return -1;
+    }
+    return 0;
+}
+
 int32_t orc_quantize(const double *grad, const double *hess, int64_t n,
                      const int32_t *rows, int64_t n_sel, int32_t quant_bins,
                      int32_t stochastic, int64_t seed, int64_t round_index,
                      int64_t class_index, int32_t const_hessian, int8_t *q_grad,
                      int8_t *q_hess, double *out_scales) {
+    std::vector<int32_t> qg((size_t)n), qh((size_t)n);
+    const int32_t rc = orc_quantize_rule(grad, hess, n, rows, n_sel, quant_bins, stochastic, seed,
+                                         round_index, class_index, const_hessian, kRuleMaxAbs,
+                                         qg.data(), qh.data(), out_scales);
+    for (int64_t r = 0; r < n; ++r) {
+        q_grad[r] = (int8_t)qg[(size_t)r];
+        q_hess[r] = (int8_t)qh[(size_t)r];
+    }
+    return rc;
+}
+
+int32_t orc_magnitude_sums(const double *grad, const double *hess, int64_t n,
+                           const uint8_t *in_sample, double *out_sums) {
     std::vector<double> g(grad, grad + n), h(hess, hess + n);
-    Pool pool(1);
-    QScales s = quantize_round(g, h, rows, n_sel, quant_bins, stochastic != 0, seed,
-                               round_index, class_index, const_hessian != 0, q_grad,
-                               q_hess, pool);
-    out_scales[0] = s.gu;
-    out_scales[1] = s.hu;
-    out_scales[2] = (double)s.gmax;
-    out_scales[3] = (double)s.hmax;
+    std::vector<uint8_t> m;
+    if (in_sample) m.assign(in_sample, in_sample + n);
+    magnitude_sums(g, h, m, out_sums[0], out_sums[1]);
     return 0;
 }
 
-int32_t orc_hist_quantized(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
-                           const int8_t *qg, const int8_t *qh, const int32_t *rows,
-                           int64_t n_sel, int64_t *out) {
+double orc_largest_power_of_two_at_most(double x) {
+    try {
+        return largest_power_of_two_at_most(x);
+    } catch (const std::exception &) {
+        return -1.0;
+    }
+}
+
+double orc_fixed_point_scale_pow2(double total) {
+    try {
+        return fixed_point_scale_pow2(total);
+    } catch (const std::exception &) {
+        return -1.0;
+    }
+}
+
+int32_t orc_hist_quantized32(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
+                             const int32_t *qg, const int32_t *qh, const int32_t *rows,
+                             int64_t n_sel, int64_t *out) {
     Data d{bins, n, nf, nb, std::vector<int>(nf, -1), {}, {}};
     std::vector<int> feats(nf);
     for (int f = 0; f < nf; ++f) feats[f] = f;
@@ -1707,6 +1867,13 @@ int32_t orc_hist_quantized(const uint8_t *bins, int64_t n, int32_t nf, int32_t n
     build_quant(h, d, qg, qh, rows, rows ? n_sel : n, feats, pool);
     std::memcpy(out, h.v.data(), h.v.size() * sizeof(int64_t));
     return 0;
+}
+
+int32_t orc_hist_quantized(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
+                           const int8_t *qg, const int8_t *qh, const int32_t *rows,
+                           int64_t n_sel, int64_t *out) {
+    std::vector<int32_t> g(qg, qg + n), h(qh, qh + n);
+    return orc_hist_quantized32(bins, n, nf, nb, g.data(), h.data(), rows, n_sel, out);
 }
 
 int32_t orc_hist_float(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
@@ -1899,7 +2066,7 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
         }
         std::vector<double> grad(n), hess(n), prob;
         std::vector<int32_t> bag;
-        std::vector<int8_t> qg, qh;
+        std::vector<int32_t> qg, qh;
         std::vector<std::pair<int, std::vector<int32_t>>> leaves;
         bool bagging = P.p.bagging_freq > 0 && P.p.bagging_fraction < 1.0;
         for (int it = 0; it < P.p.num_iterations; ++it) {

@@ -74,6 +74,10 @@ typedef struct {
      * each row's gradient and hessian and weight the base score / class
      * priors (boosting._fill_grad_hess_into, _base_score, train_multiclass) */
     const double *weights;
+    /* quantized-gradient lattice (derive_scales, quantized_gradient.mojo:
+     * 1343-1453): 0 LightGBM's max-abs rule (num_grad_quant_bins units), 1
+     * the reference's magnitude-sum power-of-two rule (2^30 lattice) */
+    int32_t quant_scale_rule;
 } orc_params;
 
 /* A trained model in flat arrays. Trees are laid out one after another;
@@ -127,7 +131,25 @@ int32_t orc_quantize(const double *grad, const double *hess, int64_t n_rows,
                      int64_t class_index, int32_t const_hessian,
                      int8_t *q_grad, int8_t *q_hess, double *out_scales);
 
+/* The same for either lattice (rule 0 max-abs, 1 magnitude sum), with
+ * int32 outputs; returns -1 when the magnitudes are out of range. */
+int32_t orc_quantize_rule(const double *grad, const double *hess, int64_t n_rows,
+                          const int32_t *rows, int64_t n_sel, int32_t quant_bins,
+                          int32_t stochastic, int64_t seed, int64_t round_index,
+                          int64_t class_index, int32_t const_hessian, int32_t rule,
+                          int32_t *q_grad, int32_t *q_hess, double *out_scales);
+/* The device magnitude reduction's sums (sum |g|, sum |h|) in its fixed
+ * order; in_sample NULL or n_rows flags (0: the row adds nothing). */
+int32_t orc_magnitude_sums(const double *grad, const double *hess, int64_t n_rows,
+                           const uint8_t *in_sample, double *out_sums);
+/* largest_power_of_two_at_most / fixed_point_scale_pow2; -1 when refused. */
+double orc_largest_power_of_two_at_most(double x);
+double orc_fixed_point_scale_pow2(double total);
+
 /* ------------------------------------------------------------ histograms */
+int32_t orc_hist_quantized32(const uint8_t *bins, int64_t n_rows, int32_t n_features,
+                             int32_t n_bins, const int32_t *q_grad, const int32_t *q_hess,
+                             const int32_t *rows, int64_t n_sel, int64_t *out);
 /* Integer histogram over `rows` (or all rows when rows == NULL):
  * out is n_features * n_bins cells of int64 {grad, hess, count}. */
 int32_t orc_hist_quantized(const uint8_t *bins, int64_t n_rows,

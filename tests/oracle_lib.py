@@ -59,6 +59,7 @@ class Params(C.Structure):
         ("min_data_per_group", C.c_int32),
         ("one_hot_max_size", C.c_int32),
         ("weights", C.c_void_p),
+        ("quant_scale_rule", C.c_int32),
     ]
 
 
@@ -75,6 +76,7 @@ def default_params(**kw) -> Params:
         query_starts=None, n_queries=0, lambdarank_truncation_level=30, lambdarank_norm=1,
         lambdarank_sigmoid=1.0, n_categories=None, max_cat_to_onehot=4, max_cat_threshold=32,
         cat_smooth=10.0, cat_l2=10.0, min_data_per_group=100, one_hot_max_size=-1, weights=None,
+        quant_scale_rule=0,
     )
     for k, v in kw.items():
         setattr(p, k, v)
@@ -135,6 +137,21 @@ def lib():
         L.orc_quantize.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
                                    C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64,
                                    C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_quantize_rule.restype = C.c_int32
+        L.orc_quantize_rule.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                        C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64,
+                                        C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_magnitude_sums.restype = C.c_int32
+        L.orc_magnitude_sums.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
+                                         C.c_void_p]
+        L.orc_largest_power_of_two_at_most.restype = C.c_double
+        L.orc_largest_power_of_two_at_most.argtypes = [C.c_double]
+        L.orc_fixed_point_scale_pow2.restype = C.c_double
+        L.orc_fixed_point_scale_pow2.argtypes = [C.c_double]
+        L.orc_hist_quantized32.restype = C.c_int32
+        L.orc_hist_quantized32.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
+                                           C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                           C.c_void_p]
         L.orc_hist_quantized.restype = C.c_int32
         L.orc_hist_quantized.argtypes = [C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
                                          C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
@@ -293,6 +310,55 @@ def quantize(grad, hess, rows=None, quant_bins=4, stochastic=1, seed=11, round_i
                        0 if r is None else len(r), quant_bins, stochastic, seed, round_index,
                        class_index, const_hessian, _ptr(qg), _ptr(qh), _ptr(sc))
     return qg, qh, sc
+
+
+RULE_MAX_ABS, RULE_MAGNITUDE_SUM = 0, 1
+
+
+def quantize_rule(grad, hess, rule, rows=None, quant_bins=4, stochastic=1, seed=11,
+                  round_index=0, class_index=0, const_hessian=0):
+    """Either lattice, int32 values: (qg, qh, [gu, hu, gmax, hmax]); raises
+    when the magnitudes are out of the fixed-point range."""
+    n = len(grad)
+    qg = np.zeros(n, np.int32)
+    qh = np.zeros(n, np.int32)
+    sc = np.zeros(4)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    rc = lib().orc_quantize_rule(_ptr(np.ascontiguousarray(grad, np.float64)),
+                                 _ptr(np.ascontiguousarray(hess, np.float64)), n, _ptr(r),
+                                 0 if r is None else len(r), quant_bins, stochastic, seed,
+                                 round_index, class_index, const_hessian, rule, _ptr(qg), _ptr(qh),
+                                 _ptr(sc))
+    if rc != 0:
+        raise ValueError("magnitudes out of range for the fixed-point lattice")
+    return qg, qh, sc
+
+
+def magnitude_sums(grad, hess, in_sample=None):
+    out = np.zeros(2)
+    m = None if in_sample is None else np.ascontiguousarray(in_sample, np.uint8)
+    lib().orc_magnitude_sums(_ptr(np.ascontiguousarray(grad, np.float64)),
+                             _ptr(np.ascontiguousarray(hess, np.float64)), len(grad), _ptr(m),
+                             _ptr(out))
+    return float(out[0]), float(out[1])
+
+
+def largest_power_of_two_at_most(x):
+    return float(lib().orc_largest_power_of_two_at_most(x))
+
+
+def fixed_point_scale_pow2(total):
+    return float(lib().orc_fixed_point_scale_pow2(total))
+
+
+def hist_quantized32(bins_cm, n_rows, n_features, n_bins, qg, qh, rows=None):
+    out = np.zeros(n_features * n_bins * 3, np.int64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    lib().orc_hist_quantized32(_ptr(np.ascontiguousarray(bins_cm, np.uint8)), n_rows,
+                               n_features, n_bins, _ptr(np.ascontiguousarray(qg, np.int32)),
+                               _ptr(np.ascontiguousarray(qh, np.int32)), _ptr(r),
+                               0 if r is None else len(r), _ptr(out))
+    return out.reshape(n_features, n_bins, 3)
 
 
 def hist_quantized(bins_cm, n_rows, n_features, n_bins, qg, qh, rows=None):
