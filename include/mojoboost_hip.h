@@ -99,6 +99,13 @@ typedef struct {
      * num_grad_quant_bins is then unused. n_rows < 2^30; not with
      * lambdarank. */
     int32_t quant_scale_rule;
+    /* magnitude-sum lattice staging (GpuActiveRows.set_packed_gradients,
+     * src/mojotrees/gpu_active_rows.mojo:2257-2395): 0 int32 pairs (the
+     * reference's default), 1 the packed int16 arm -- each row's pair
+     * narrowed to int16 in its record, exact while every value fits; a fit
+     * in which any value does not is refused (MOJOTREES_ERROR_TRAINING,
+     * naming the count per plane). */
+    int32_t quant_staging;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -282,8 +289,10 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *params,
 
 /* The same for either lattice with int32 outputs: with quant_scale_rule 1
  * (the magnitude-sum lattice) q_grad/q_hess receive the 2^30-lattice values
- * and scales[2..3] the device magnitude sums (sum |g|, sum |h|) the scales
- * came from; scales holds 4 doubles. */
+ * (with quant_staging 1, the staged int16 values) and scales[2..3] the
+ * device magnitude sums (sum |g|, sum |h|) the scales came from, and with
+ * quant_staging 1 scales[4..5] the counts of grad and hess values that did
+ * not fit int16; scales holds 6 doubles. */
 int32_t mbh_objective_quantize32(mbh_dataset *ds, const mbh_params *params,
                                  const double *raw, int64_t round_index, float *grad,
                                  float *hess, int32_t *q_grad, int32_t *q_hess,

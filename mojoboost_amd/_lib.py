@@ -79,6 +79,7 @@ class MbhParams(C.Structure):
         ("min_data_per_group", C.c_int32),
         ("one_hot_max_size", C.c_int32),
         ("quant_scale_rule", C.c_int32),
+        ("quant_staging", C.c_int32),
     ]
 
 
@@ -92,7 +93,8 @@ def mbh_params(**kw) -> MbhParams:
                   top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0,
                   lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0,
                   max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
-                  min_data_per_group=100, one_hot_max_size=-1, quant_scale_rule=0)
+                  min_data_per_group=100, one_hot_max_size=-1, quant_scale_rule=0,
+                  quant_staging=0)
     for k, v in kw.items():
         setattr(p, k, v)
     return p

@@ -89,6 +89,7 @@ const std::map<std::string, std::string> &aliases() {
         {"num_grad_quant_bins", "num_grad_quant_bins"},
         {"stochastic_rounding", "stochastic_rounding"},
         {"quant_scale_rule", "quant_scale_rule"},
+        {"quant_staging", "quant_staging"},
         {"bagging_fraction", "bagging_fraction"},
         {"subsample", "bagging_fraction"},
         {"bagging_freq", "bagging_freq"},
@@ -128,7 +129,7 @@ const char *kPrimaryKeys =
     "bagging_freq,bagging_seed,boosting,top_rate,other_rate,min_data_in_bin,"
     "bin_construct_sample_cnt,data_random_seed,lambdarank_truncation_level,sigmoid,lambdarank_norm,"
     "categorical_feature,max_cat_to_onehot,max_cat_threshold,cat_smooth,cat_l2,min_data_per_group,"
-    "one_hot_max_size,quant_scale_rule";
+    "one_hot_max_size,quant_scale_rule,quant_staging";
 
 struct Config {
     mbh_params p{};
@@ -281,6 +282,12 @@ Config parse(const char *spec) {
             if (val == "max_abs" || val == "0") p.quant_scale_rule = 0;
             else if (val == "magnitude_sum" || val == "1") p.quant_scale_rule = 1;
             else throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "quant_scale_rule must be max_abs or magnitude_sum"};
+        } else if (k == "quant_staging") {
+            // the magnitude-sum lattice's staged pair width
+            // (GpuActiveRows.set_packed_gradients, gpu_active_rows.mojo:2257-2395)
+            if (val == "int32" || val == "0") p.quant_staging = 0;
+            else if (val == "int16" || val == "1") p.quant_staging = 1;
+            else throw ApiError{MOJOTREES_ERROR_INVALID_ARGUMENT, "quant_staging must be int32 or int16"};
         } else if (k == "bagging_fraction") {
             p.bagging_fraction = to_double(k, val);
         } else if (k == "bagging_freq") {

@@ -240,6 +240,9 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
     const int B = p->num_grad_quant_bins;
     if (p->quant_scale_rule != 0 && p->quant_scale_rule != 1)
         bad("quant_scale_rule must be 0 (max_abs) or 1 (magnitude_sum)");
+    if (p->quant_staging != 0 && p->quant_staging != 1) bad("quant_staging must be 0 (int32) or 1 (int16)");
+    if (p->quant_staging == 1 && !(p->use_quantized_grad && p->quant_scale_rule == 1))
+        bad("quant_staging=int16 stages the magnitude-sum lattice (quant_scale_rule=magnitude_sum)");
     if (p->use_quantized_grad && p->quant_scale_rule == 1) {
         // the headroom argument of fixed_point_scale_pow2
         // (quantized_gradient.mojo:908-1117): a node's int32 sum stays
@@ -279,7 +282,9 @@ struct RecLayout {
     int rec = 0, tile_f = 0, n_tiles = 0;
 };
 
-RecLayout record_layout(int F, int lds_stride, int kind) {
+// pair_bytes: the g/h pair at the end of each record (2: an int8 pair, 4: the
+// int16 staging pair).
+RecLayout record_layout(int F, int lds_stride, int kind, int pair_bytes = 2) {
     int ft_max = 126;
     while (ft_max > 0 && mb::pb_lds_bytes_for(ft_max, lds_stride, kind) + kPbStaticLds > 160 * 1024)
         --ft_max;
@@ -289,7 +294,7 @@ RecLayout record_layout(int F, int lds_stride, int kind) {
     l.n_tiles = (F + ft_max - 1) / ft_max;
     l.tile_f = (F + l.n_tiles - 1) / l.n_tiles;
     l.rec = 16;
-    while (l.rec < l.tile_f + 2) l.rec *= 2;
+    while (l.rec < l.tile_f + pair_bytes) l.rec *= 2;
     return l;
 }
 
@@ -408,8 +413,9 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     mb::DevState &s = tb.s;
     const bool quantized = p->use_quantized_grad != 0;
     const bool wide = quantized && p->quant_scale_rule == 1;
+    const bool stage16 = wide && p->quant_staging == 1;
     const int kind = wide ? mb::kAccWide : quantized ? mb::kAccQuant : mb::kAccFloat;
-    ensure_records(ds, record_layout(F, ds->lds_stride, kind));
+    ensure_records(ds, record_layout(F, ds->lds_stride, kind, stage16 ? 4 : 2));
     s.records = ds->d_records;
     s.records_w = ds->d_records;
     s.bins_cm = ds->d_bins_cm;
@@ -440,8 +446,10 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     else s.histf = dalloc<mb::HistF>((size_t)(1 + max_exp) * F * ds->nb, run.owned);
     configure_hist(s, ds, quantized ? p->num_grad_quant_bins : 4, kind, run);
     if (wide) {
-        s.gq = dalloc<int32_t>(2 * (size_t)ds->n, run.owned);
+        if (!stage16) s.gq = dalloc<int32_t>(2 * (size_t)ds->n, run.owned);
         s.magpart = dalloc<float>(2 * 256, run.owned);
+        s.stage16_over = dalloc<unsigned long long>(2, run.owned);
+        HIPX(hipMemset(s.stage16_over, 0, 2 * sizeof(unsigned long long)));
     }
     s.enodes = dalloc<mb::ENode>(s.e_cap, run.owned);
     s.items = dalloc<mb::Item>(s.kmax, run.owned);
@@ -528,6 +536,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     }
     hp.quantized = p->use_quantized_grad ? 1 : 0;
     hp.wide = wide ? 1 : 0;
+    hp.stage16 = stage16 ? 1 : 0;
     hp.goss = p->goss ? 1 : 0;
     // GossParams.warmup (goss.mojo:102-157): floor(1 / learning_rate) rounds
     hp.goss_warm = p->learning_rate > 0.0 ? (int32_t)(1.0 / p->learning_rate) : 0;
@@ -642,6 +651,25 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     tb.L = L;
     tb.max_nodes = max_nodes;
     return tb;
+}
+
+// The packed int16 arm's refusal (gpu_active_rows._raise_stage16): values
+// that did not fit a signed 16-bit word were counted per plane by the
+// quantizer; any such value (the hessian plane only when it is read, not
+// under a constant hessian) refuses the fit and names the counts. The
+// remedy is the int32 staging, not a smaller scale.
+void check_stage16(const mb::DevState &s, int64_t n) {
+    if (!s.hp.stage16) return;
+    unsigned long long over[2] = {0ULL, 0ULL};
+    HIPX(hipMemcpy(over, s.stage16_over, sizeof(over), hipMemcpyDeviceToHost));
+    if (s.hp.const_hessian) over[1] = 0ULL;
+    if (over[0] || over[1])
+        throw Error{MOJOTREES_ERROR_TRAINING,
+                    "the packed int16 gradient staging lost " + std::to_string(over[0]) + " gradient and " +
+                        std::to_string(over[1]) + " hessian values (over all rounds, " + std::to_string(n) +
+                        " rows each) that do not fit a signed 16-bit word at the round's scale; this bound is "
+                        "per row and tightens as the row count falls, so the remedy is the int32 staging "
+                        "(quant_staging=0, the default), not a smaller scale"};
 }
 
 }  // namespace
@@ -944,6 +972,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             throw Error{MOJOTREES_ERROR_TRAINING,
                         std::string("device growth check failed (internal error, code ") +
                             std::to_string(h_error) + ")"};
+        check_stage16(s, ds->n);
         const int mn = tb.max_nodes;
         std::vector<int32_t> ai((size_t)tb.T * (6 * mn + 2));
         std::vector<double> ad((size_t)tb.T * 3 * mn);
@@ -1417,7 +1446,23 @@ int32_t mbh_objective_quantize32(mbh_dataset *ds, const mbh_params *p, const dou
             throw Error{MOJOTREES_ERROR_TRAINING, "gradient/hessian magnitudes are out of range for the fixed-point histogram"};
         HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
-        if (s.hp.wide) {
+        scales[4] = 0.0;
+        scales[5] = 0.0;
+        if (s.hp.stage16) {
+            std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
+            HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
+            for (int64_t r = 0; r < ds->n; ++r) {
+                int16_t g16, h16;
+                std::memcpy(&g16, rec.data() + (size_t)r * ds->rec + ds->rec - 4, 2);
+                std::memcpy(&h16, rec.data() + (size_t)r * ds->rec + ds->rec - 2, 2);
+                q_grad[r] = g16;
+                q_hess[r] = h16;
+            }
+            unsigned long long over[2];
+            HIPX(hipMemcpy(over, s.stage16_over, sizeof(over), hipMemcpyDeviceToHost));
+            scales[4] = (double)over[0];
+            scales[5] = (double)over[1];
+        } else if (s.hp.wide) {
             std::vector<int32_t> q(2 * (size_t)ds->n);
             HIPX(hipMemcpy(q.data(), s.gq, q.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
             for (int64_t r = 0; r < ds->n; ++r) {

@@ -524,7 +524,16 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
             const double hv = hp.grad64 ? s.hess64[r] : (double)s.hess[r];
             int32_t qg = quantize_scalar(gv, gu, gmax, stoch, gs + (uint64_t)r);
             int32_t qh = quantize_scalar(hv, hu, hmax, stoch, hs + (uint64_t)r);
-            if (hp.wide) {
+            if (hp.stage16) {
+                // _quantize_grad_hess_i16_kernel: the same integers narrowed,
+                // each plane's misfits counted (a constant hessian's plane is
+                // never read, and its values are 1)
+                if (qg > 32767 || qg < -32768) atomicAdd(&s.stage16_over[0], 1ULL);
+                if (qh > 32767 || qh < -32768) atomicAdd(&s.stage16_over[1], 1ULL);
+                const uint32_t v = (uint32_t)(uint16_t)(int16_t)qg | ((uint32_t)(uint16_t)(int16_t)qh << 16);
+                for (int t = 0; t < s.n_tiles; ++t)
+                    *(uint32_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 4) = v;
+            } else if (hp.wide) {
                 *(int2 *)(s.gq + 2 * r) = make_int2(qg, qh);
             } else {
                 uint16_t v = (uint16_t)(uint8_t)(int8_t)qg | (uint16_t)((uint16_t)(uint8_t)(int8_t)qh << 8);
@@ -1231,13 +1240,16 @@ struct FAcc {
 };
 
 // WAcc (the magnitude-sum lattice): each row's int32 (grad, hess) pair from
-// `gq`, gathered by row id; per cell one 64-bit LDS add of the packed pair --
+// `gq`, gathered by row id -- or, with int16 staging (K16), the int16 pair in
+// the record's last four bytes, which the row's lanes already hold; per cell
+// one 64-bit LDS add of the packed pair --
 // hess in the low 32 bits (nonnegative, a cell's sum below 2^32), signed grad
 // in the high 32 -- and one 32-bit count. Any subset of a round's rows sums
 // to at most 2^30 + n in magnitude on this lattice (quantized_gradient.mojo:
 // 908-1117, the headroom argument), so neither field overflows and no carry
 // crosses from hess into grad, whatever the block's row count.
-struct WAcc {
+template <bool K16>
+struct WAccT {
     static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 12; }
     template <int LPR>
     __device__ static void zero(unsigned char *lds, int F, int ls) {
@@ -1250,10 +1262,12 @@ struct WAcc {
     }
     template <int LPR>
     __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
-                               int64_t row, uint32_t, double) {
+                               int64_t row, uint32_t gh_word, double) {
         unsigned long long *gh = (unsigned long long *)lds;
         uint32_t *c = (uint32_t *)(gh + (size_t)F * ls);
-        const int2 q = *(const int2 *)(s.gq + 2 * row);
+        int2 q;
+        if constexpr (K16) q = make_int2((int)(int16_t)(gh_word & 0xFFFFu), (int)(int16_t)(gh_word >> 16));
+        else q = *(const int2 *)(s.gq + 2 * row);
         const unsigned long long packed = ((unsigned long long)(uint32_t)q.x << 32) | (uint32_t)q.y;
         const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -1283,6 +1297,9 @@ struct WAcc {
         }
     }
 };
+
+using WAcc = WAccT<false>;
+using WAcc16 = WAccT<true>;
 
 // Root histogram, accumulation pass. Rows are split into contiguous chunks,
 // one per block; a block accumulates its rows into its LDS histogram and
@@ -3873,7 +3890,16 @@ size_t plan_lds_bytes(const DevState &s) {
 hipError_t prepare_kernels(const DevState &s) {
     const size_t h = hist_lds_bytes(s);
     if (s.hp.objective == kObjLambdarank) MB_SET_LDS(k_lambdarank, rank_lds_bytes(s));
-    if (s.hp.wide) {
+    if (s.hp.stage16) {
+        MB_SET_LDS((k_hist<1, WAcc16>), h);
+        MB_SET_LDS((k_hist<2, WAcc16>), h);
+        MB_SET_LDS((k_hist<4, WAcc16>), h);
+        MB_SET_LDS((k_hist<8, WAcc16>), h);
+        MB_SET_LDS((k_accum<1, WAcc16>), h);
+        MB_SET_LDS((k_accum<2, WAcc16>), h);
+        MB_SET_LDS((k_accum<4, WAcc16>), h);
+        MB_SET_LDS((k_accum<8, WAcc16>), h);
+    } else if (s.hp.wide) {
         MB_SET_LDS((k_hist<1, WAcc>), h);
         MB_SET_LDS((k_hist<2, WAcc>), h);
         MB_SET_LDS((k_hist<4, WAcc>), h);
@@ -3931,7 +3957,8 @@ hipError_t launch_hist_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipE
     }
 }
 hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    return s.hp.wide        ? launch_hist_t<WAcc>(s, st, ev0, ev1)
+    return s.hp.stage16     ? launch_hist_t<WAcc16>(s, st, ev0, ev1)
+           : s.hp.wide      ? launch_hist_t<WAcc>(s, st, ev0, ev1)
            : s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1)
                             : launch_hist_t<FAcc>(s, st, ev0, ev1);
 }
@@ -3951,7 +3978,8 @@ hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hip
     }
 }
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    return s.hp.wide        ? launch_accum_t<WAcc>(s, st, ev0, ev1)
+    return s.hp.stage16     ? launch_accum_t<WAcc16>(s, st, ev0, ev1)
+           : s.hp.wide      ? launch_accum_t<WAcc>(s, st, ev0, ev1)
            : s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1)
                             : launch_accum_t<FAcc>(s, st, ev0, ev1);
 }

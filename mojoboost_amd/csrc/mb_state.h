@@ -178,6 +178,11 @@ struct HyperParams {
     // 1343-1453, and _quantize_grad_hess_kernel, gpu_active_rows.mojo:
     // 2211-2255)
     int32_t wide;
+    // magnitude-sum lattice, the reference's packed Int16 staging arm
+    // (QUANT_SOURCE_PACKED16, gpu_active_rows.mojo:2257-2395): each row's
+    // pair narrowed to int16 in its record's last four bytes, with per-plane
+    // counts of the values that did not fit
+    int32_t stage16;
     int32_t goss;           // 1: GOSS from round goss_warm on
     int32_t goss_warm;
     int32_t goss_seed;
@@ -242,6 +247,7 @@ struct DevState {
     // workgroup sums (|g| then |h|)
     int32_t *gq;
     float *magpart;
+    unsigned long long *stage16_over;  // [2]: grad and hess values outside int16 (stage16)
     Round *round;
     // rows and histograms
     int32_t *rows0, *rows1;

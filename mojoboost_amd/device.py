@@ -126,15 +126,17 @@ class Dataset:
 
     def objective_quantize32(self, raw, round_index=0, **params):
         """Either lattice with int32 values: (grad, hess, q_grad, q_hess,
-        [grad units, hess units, sum|g|, sum|h|]) -- the sums are the device
-        magnitude reduction's under quant_scale_rule=1, else 0."""
+        [grad units, hess units, sum|g|, sum|h|, int16 misfits of grad,
+        of hess]) -- the sums are the device magnitude reduction's under
+        quant_scale_rule=1, the misfit counts the int16 staging's
+        (quant_staging=1), else 0."""
         n = self.n_rows
         p = _lib.mbh_params(**params)
         g = np.zeros(n, np.float32)
         h = np.zeros(n, np.float32)
         qg = np.zeros(n, np.int32)
         qh = np.zeros(n, np.int32)
-        sc = np.zeros(4)
+        sc = np.zeros(6)
         err = C.create_string_buffer(1024)
         raw = np.ascontiguousarray(raw, np.float64)
         check(lib().mbh_objective_quantize32(self.h, C.byref(p), ptr(raw), round_index, ptr(g),

@@ -171,3 +171,59 @@ def test_magnitude_lattice_through_the_c_abi(dev):
     ref = O.train(bins, n, f, 64, y, p, missing_bin=mb)
     want, _ = ref.predict_binned(bins, n, f)
     assert np.array_equal(bits(raw), bits(want))
+
+
+@pytest.mark.parametrize("n", [300_000, 6_000])
+def test_int16_staging_values_and_misfit_counts(dev, n):
+    """The packed int16 arm (_quantize_grad_hess_i16_kernel,
+    gpu_active_rows.mojo:2298-2352): the staged values are the int32
+    lattice's integers narrowed to 16 bits, and the per-plane counters count
+    exactly the values outside [-32768, 32767]. At 300k logistic rows every
+    value fits (max|g| / sum|g| is near 1 / n); at 6k rows many do not."""
+    f = 4
+    rng = np.random.default_rng(n)
+    bins = rng.integers(0, 16, size=(f, n), dtype=np.uint8)
+    y = (rng.uniform(size=n) < 0.4).astype(np.float64)
+    raw = rng.normal(0, 2, size=n)
+    ds = dev.Dataset(bins, n, f, 16, y)
+    g, h, qg, qh, sc = ds.objective_quantize32(raw, objective=1, quant_scale_rule=1, quant_staging=1)
+    og, oh = O.grad_hess(1, raw, y)
+    oqg, oqh, _ = O.quantize_rule(og, oh, O.RULE_MAGNITUDE_SUM, stochastic=1, seed=11)
+    misfit_g = int(np.sum((oqg > 32767) | (oqg < -32768)))
+    misfit_h = int(np.sum((oqh > 32767) | (oqh < -32768)))
+    assert (sc[4], sc[5]) == (misfit_g, misfit_h)
+    assert np.array_equal(qg, oqg.astype(np.int16).astype(np.int32))
+    assert np.array_equal(qh, oqh.astype(np.int16).astype(np.int32))
+    if n == 300_000:
+        assert misfit_g == misfit_h == 0
+    else:
+        assert misfit_g > 0
+
+
+def test_training_int16_staging_equals_int32_staging(dev):
+    n = 300_000
+    bins, y, mb, nb = c2_like(n, seed=9)
+    kw = dict(objective=1, num_iterations=8, num_leaves=255, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.1, quant_scale_rule=1)
+    ds = dev.Dataset(bins, n, 28, nb, y, missing_bin=mb)
+    a = ds.train(quant_staging=1, **kw)
+    b = ds.train(quant_staging=0, **kw)
+    ref = O.train(bins, n, 28, nb, y, O.default_params(**{k: v for k, v in kw.items()},
+                                                       use_quantized_grad=1), missing_bin=mb)
+    _compare_fit(a, ref, n)
+    _compare_fit(b, ref, n)
+
+
+def test_int16_staging_refuses_a_misfit(dev):
+    from mojoboost_amd._lib import ERROR_TRAINING, MojoTreesError
+
+    n, f = 3_000, 4
+    rng = np.random.default_rng(2)
+    bins = rng.integers(0, 16, size=(f, n), dtype=np.uint8)
+    y = (rng.uniform(size=n) < 0.5).astype(np.float64)
+    ds = dev.Dataset(bins, n, f, 16, y)
+    with pytest.raises(MojoTreesError) as e:
+        ds.train(objective=1, num_iterations=2, num_leaves=7, quant_scale_rule=1, quant_staging=1)
+    assert e.value.code == ERROR_TRAINING and "int16" in e.value.message
+    # the same fit on the int32 staging trains
+    assert ds.train(objective=1, num_iterations=2, num_leaves=7, quant_scale_rule=1).n_trees == 2
