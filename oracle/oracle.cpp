@@ -1643,6 +1643,43 @@ int32_t orc_bin_equal_width(const double *x, int64_t n, int32_t nf, int32_t nb,
     return 0;
 }
 
+}  // extern "C"
+
+namespace {
+// bin_construct_sample_rows (src/mojotrees/binning.mojo:1745-1785): Knuth's
+// selection sampling, row r of the `left` still to consider taken when
+// uniform(seed * GOLDEN + r) * left < need, every remaining row once need >=
+// left; empty (every row) for sample_cnt <= 0 or >= n.
+std::vector<int64_t> bin_sample_rows(int64_t n, int64_t sample_cnt, int64_t seed) {
+    std::vector<int64_t> sample;
+    if (n < 1 || sample_cnt <= 0 || sample_cnt >= n) return sample;
+    sample.reserve((size_t)sample_cnt);
+    const uint64_t base = (uint64_t)seed * GOLDEN;
+    int64_t need = sample_cnt;
+    for (int64_t r = 0; r < n && need > 0; ++r) {
+        const int64_t left = n - r;
+        if (need >= left) {
+            sample.push_back(r);
+            --need;
+            continue;
+        }
+        if (uniform(base + (uint64_t)r) * (double)left < (double)need) {
+            sample.push_back(r);
+            --need;
+        }
+    }
+    return sample;
+}
+}  // namespace
+
+extern "C" {
+
+int64_t orc_bin_sample_rows(int64_t n, int64_t sample_cnt, int64_t seed, int64_t *out) {
+    const std::vector<int64_t> s = bin_sample_rows(n, sample_cnt, seed);
+    if (out) std::memcpy(out, s.data(), s.size() * sizeof(int64_t));
+    return (int64_t)s.size();
+}
+
 // binning.fit_bins, quantile border type, numerical features
 // (src/mojotrees/binning.mojo:3565-4047; quantile_boundary_indices :558,
 // emit_quantile_edges :583, bin_construct_sample_rows :1745). The
@@ -1653,23 +1690,7 @@ int32_t orc_fit_bins(const double *x, int64_t n, int32_t nf, int32_t max_bins,
                      int64_t seed, double *out_edges, int32_t *out_n_edges,
                      int32_t *out_missing_bin) {
     if (max_bins < 2 || max_bins > 256 || n < 1 || min_data_in_bin < 1) return -1;
-    std::vector<int64_t> sample;
-    if (!(sample_cnt <= 0 || sample_cnt >= n)) {
-        uint64_t base = (uint64_t)seed * GOLDEN;
-        int64_t need = sample_cnt;
-        for (int64_t r = 0; r < n && need > 0; ++r) {
-            int64_t left = n - r;
-            if (need >= left) {
-                sample.push_back(r);
-                --need;
-                continue;
-            }
-            if (uniform(base + (uint64_t)r) * (double)left < (double)need) {
-                sample.push_back(r);
-                --need;
-            }
-        }
-    }
+    const std::vector<int64_t> sample = bin_sample_rows(n, sample_cnt, seed);
     bool sampled = !sample.empty();
     int64_t n_sample = sampled ? (int64_t)sample.size() : n;
     int max_edges = max_bins - 1;

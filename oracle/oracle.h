@@ -104,6 +104,9 @@ int32_t orc_fit_bins(const double *x, int64_t n_rows, int32_t n_features,
                      int32_t use_missing, int64_t sample_cnt, int64_t seed,
                      double *out_edges, int32_t *out_n_edges,
                      int32_t *out_missing_bin);
+/* bin_construct_sample_rows: the ascending rows a sampled fit reads
+ * (written to out when not NULL); returns their count, 0 meaning every row. */
+int64_t orc_bin_sample_rows(int64_t n_rows, int64_t sample_cnt, int64_t seed, int64_t *out);
 int32_t orc_transform(const double *x, int64_t n_rows, int32_t n_features,
                       int32_t max_bins, const double *edges,
                       const int32_t *n_edges, const int32_t *missing_bin,

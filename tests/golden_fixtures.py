@@ -114,6 +114,29 @@ def fixture(name: str):
         return x, n, f, regression_target(x, n), ("fit", 255), dict(
             objective=0, num_iterations=8, learning_rate=0.3, num_leaves=31,
             min_data_in_leaf=20, lambda_l2=1.0, min_sum_hessian=1e-3)
+    if name == "misscat":
+        # _fixture_misscat (tests/test_golden_bits.mojo:8072-8113): feature 1
+        # missing on every seventh row, feature 2 an integer code in [0, 6)
+        # fitted as a categorical, the target additive in both. 2 * x0 is
+        # exact, so no contraction choice moves the target's bits.
+        n, f = 200, 5
+        x = features(n, f, 40_000)
+        r = np.arange(n)
+        x[1 * n:2 * n][r % 7 == 0] = np.nan
+        x[2 * n:3 * n] = np.floor(x[2 * n:3 * n] * 6.0)
+        weight = np.array([0.0, 1.5, -1.0, 0.7, -2.0, 2.5])
+        y = np.empty(n)
+        for i in range(n):
+            x1 = float(x[n + i])
+            v = 2.0 * float(x[i])
+            v += 0.5 if np.isnan(x1) else x1
+            v += float(weight[int(x[2 * n + i])])
+            y[i] = v
+        return x, n, f, y, ("fit_cat", 32, [2]), dict(
+            objective=0, num_iterations=8, learning_rate=0.3, num_leaves=8,
+            min_data_in_leaf=5, lambda_l2=1.0, min_sum_hessian=1e-3, lambda_l1=0.0,
+            max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=2.0, cat_l2=10.0,
+            min_data_per_group=5)
     raise KeyError(name)
 
 

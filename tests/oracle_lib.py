@@ -63,6 +63,15 @@ class Params(C.Structure):
     ]
 
 
+def _threads():
+    """Oracle worker threads: the CPUs this process may use, at most 16 (a
+    GPU box's CPU share for one GPU, whatever the host reports)."""
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except AttributeError:
+        return max(1, min(16, os.cpu_count() or 1))
+
+
 def default_params(**kw) -> Params:
     p = Params(
         objective=OBJ_L2, num_class=1, num_iterations=100, learning_rate=0.1,
@@ -71,7 +80,7 @@ def default_params(**kw) -> Params:
         feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
         bagging_seed=3, use_quantized_grad=0, num_grad_quant_bins=4,
         stochastic_rounding=1, quant_seed=11, goss=0, top_rate=0.2,
-        other_rate=0.1, goss_seed=3, n_threads=0, fused_score_update=1,
+        other_rate=0.1, goss_seed=3, n_threads=_threads(), fused_score_update=1,
         fused_predict=1, totals_tree_reduce=1, use_init_base=0, init_base=0.0,
         query_starts=None, n_queries=0, lambdarank_truncation_level=30, lambdarank_norm=1,
         lambdarank_sigmoid=1.0, n_categories=None, max_cat_to_onehot=4, max_cat_threshold=32,
