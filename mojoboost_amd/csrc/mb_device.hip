@@ -328,9 +328,10 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // rows ceil(m / chunk) tasks (block partials) with chunk = clamp(ceil(batch
 // rows / n_cu), chunk_min, chunk_limit); the leaves of a batch are disjoint,
 // so n / chunk_min + (batch size) tasks always suffice. Its partition tasks
-// take at most kPartChunk parent rows each, n / kPartChunk + (batch size) of
-// them at most.
-constexpr int64_t kHistChunkMin = 4096;
+// take at least kPartChunkMin parent rows each (but the last of a leaf),
+// n / kPartChunkMin + (batch size) of them at most, spread over about two
+// tasks per CU.
+constexpr int64_t kHistChunkMin = 2048;
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run &run) {
     const bool quantized = kind != mb::kAccFloat;
@@ -346,10 +347,11 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     s.hist_chunk_limit = limit;
     s.kmax = kMaxBatch;
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
-    s.part_grid = (int32_t)((ds->n + mb::kPartChunk - 1) / mb::kPartChunk + s.kmax);
+    s.part_grid = (int32_t)((ds->n + mb::kPartChunkMin - 1) / mb::kPartChunkMin + s.kmax);
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     s.pb_launch = std::min<int32_t>(s.pb_grid, ds->n_cu);
-    s.part_launch = std::min<int32_t>(s.part_grid, 4 * ds->n_cu);
+    s.part_launch = std::min<int32_t>(s.part_grid, 8 * ds->n_cu);
+    s.part_target = 2 * ds->n_cu;
     // a root build uses at most ceil(n / chunk_min) chunks
     const int64_t parts = std::max<int64_t>(std::min<int64_t>(grid, (ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min),
                                             s.pb_grid);

@@ -1449,16 +1449,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uin
 // (tree.partition_rows_into semantics: the missing bin follows default_left,
 // otherwise bin <= threshold goes left) in the other row buffer -- left rows
 // fill [begin, begin + n_left), right rows the rest. Each task (descriptor,
-// written by the planner) is a chunk of at most kPartChunk rows of one leaf:
-// every thread keeps its kPartRows row ids and their sides in registers,
-// wave ballots count the rows of each (row group u, wave) entry, the block
-// scans the entries in row order and reserves the chunk's output with one
-// atomic per side, and the rows are written in their input order within each
-// side. One reservation per chunk of 8K rows keeps the same-address atomics
-// on a leaf's two cursors (the L2 serializes them, ~12 ns each on MI355X)
-// within the kernel's own duration even for the root split (1.3K chunks). The order of rows inside a child is not the
-// reference's (chunks land in reservation order); integer histograms are
-// order-free, fp64 sums differ only in their rounding.
+// written by the planner) is a chunk of 1K-8K rows of one leaf: every
+// thread keeps its kPartRows row ids and their sides in registers (slots past
+// the chunk read nothing: buffer loads out of range return 0), wave ballots
+// count the rows of each (row group u, wave) entry, the block scans the
+// entries in row order and reserves the chunk's output with one atomic per
+// side, and the rows are written in their input order within each side.
+// Chunks of 8K rows at the top levels keep the same-address atomics on a
+// leaf's two cursors (the L2 serializes them, ~12 ns each on MI355X) within
+// the kernel's own duration even for the root split (1.3K chunks); smaller
+// batches take smaller chunks so that their gathers spread over every CU.
+// The order of rows inside a child is not the reference's (chunks land in
+// reservation order); integer histograms are order-free, fp64 sums differ
+// only in their rounding.
 constexpr int kPartThreads = 256;
 constexpr int kPartRows = kPartChunk / kPartThreads;  // rows per thread of a task
 static_assert(kPartRows * kPartThreads == kPartChunk && kPartRows <= 32, "a task's rows fit the thread bit masks");
@@ -2609,128 +2612,90 @@ __device__ __forceinline__ double readlane_f64(double d, int l) {
 // growth_policy.GrowthSchedule.next_leaf: the frontier slot of largest gain
 // splits next, lowest slot on ties, gain > 0, until num_leaves). The frontier
 // lives in registers: lane l holds slots l, l + 64, ... (QS of them: gain,
-// explored node, node id, and the node's children -- left child id and both
-// children's gains) and its own best (gain, slot). A pick is the wave
-// maximum of the lanes' best gains as 64-bit patterns (non-negative
-// binary64 values order like their bits); a ballot finds the lane holding
-// it, and only when several lanes hold exactly that gain does a wave
-// minimum pick the lowest slot among them. A commit updates the two slots
-// it touches -- the left child keeps the parent's slot, the right one takes
-// slot n_leaves; node ids left = n_nodes, right = n_nodes + 1 -- and the
-// LDS loads of the new slots' children complete behind the next pick. The
-// replay stops at a pick whose leaf has not been expanded yet (x) or when
-// the tree is complete (done).
+// explored node, node id) and its own best slot with that slot's children
+// (left child's explored id and both children's gains, loaded from LDS each
+// time the lane's best changes, behind the next pick). A pick is the wave
+// maximum of the lanes' best gains (non-negative binary64 values order like
+// their bits): a 32-bit maximum of the high words and a ballot find the lane
+// that holds it; only when several lanes share that high word does a 64-bit
+// maximum decide, and only when several hold exactly the same gain does a
+// wave minimum pick the lowest slot. A commit rewrites two slots -- the left
+// child keeps the parent's slot, the right one takes slot n_leaves; node ids
+// left = n_nodes, right = n_nodes + 1 -- and the two lanes holding them
+// recompute their best. The replay stops at a pick whose leaf has not been
+// expanded yet (x) or when the tree is complete (done).
 template <int QS>
 __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &done, int &x) {
-    constexpr bool kRegKids = QS <= 4;  // the children in registers fit the budget of a 1024-thread block
-    constexpr int QK = kRegKids ? QS : 1;
     const int lane = lane_id();
-    const int nl0 = nl;
-    double sg[QS], cl[QK], cr[QK];
-    int se[QS], sf[QS], sc[QK];
+    double sg[QS];
+    int se[QS], sf[QS];
 #pragma unroll
     for (int q = 0; q < QS; ++q) {
         const int slot = lane + 64 * q;
-        const bool in = slot < nl0;
+        const bool in = slot < nl;
         sg[q] = in ? v.sg[slot] : 0.0;  // 0 is never picked (gain must be > 0)
-        se[q] = in ? v.sl_e[slot] : -1;
+        se[q] = in ? v.sl_e[slot] : 0;
         sf[q] = in ? v.sl_fid[slot] : -1;
-        if constexpr (kRegKids) {
-            const int e = in ? se[q] : 0;
-            sc[q] = in ? v.el[e] : -1;
-            cl[q] = v.cb[e];
-            cr[q] = v.gr[e];
-        }
     }
-    double lbg;
-    int lbi;
+    double lbg, kgl, kgr;
+    int lbi, lbe, lbf, kle;
     auto local_best = [&]() {
         lbg = 0.0;
         lbi = 0x7FFFFFFF;
+        lbe = 0;
+        lbf = -1;
 #pragma unroll
         for (int q = 0; q < QS; ++q)
             if (sg[q] > lbg) {  // ascending slots: strict '>' keeps the lowest
                 lbg = sg[q];
                 lbi = lane + 64 * q;
+                lbe = se[q];
+                lbf = sf[q];
             }
+        kle = v.el[lbe];
+        kgl = v.cb[lbe];
+        kgr = v.gr[lbe];
     };
     local_best();
-    // children of the two slots the last commit wrote, still to be placed
-    int pq0 = -1, pl0 = 0, pq1 = -1, pl1 = 0, pc0 = -1, pc1 = -1;
-    double pgl0 = 0.0, pgr0 = 0.0, pgl1 = 0.0, pgr1 = 0.0;
     for (;;) {
         if (nl >= L) {
             done = 1;
             break;
         }
         const unsigned long long mine = (unsigned long long)__double_as_longlong(lbg);
-        const unsigned long long m = wave_max_u64(mine);
-#pragma unroll
-        for (int qq = 0; qq < QK; ++qq) {
-            if (lane == pl0 && qq == pq0) {
-                sc[qq] = pc0;
-                cl[qq] = pgl0;
-                cr[qq] = pgr0;
-            }
-            if (lane == pl1 && qq == pq1) {
-                sc[qq] = pc1;
-                cl[qq] = pgl1;
-                cr[qq] = pgr1;
-            }
-        }
-        if (m == 0ULL) {  // no slot with a positive gain
-            done = 1;
-            break;
-        }
-        const unsigned long long tie = __ballot(mine == m);
-        int bi;
-        if ((tie & (tie - 1ULL)) == 0ULL) bi = __builtin_amdgcn_readlane(lbi, (int)__builtin_ctzll(tie));
-        else bi = (int)wave_min_u32(mine == m ? (unsigned)lbi : 0xFFFFFFFFu);
-        const int q = bi >> 6, ol = bi & 63;
-        int xe = se[0], xf = sf[0], xc = sc[0];
-        double xl = cl[0], xr = cr[0];
-#pragma unroll
-        for (int qq = 1; qq < QS; ++qq)
-            if (qq == q) {
-                xe = se[qq];
-                xf = sf[qq];
-                if constexpr (kRegKids) {
-                    xc = sc[qq];
-                    xl = cl[qq];
-                    xr = cr[qq];
-                }
-            }
-        const int X = __builtin_amdgcn_readlane(xe, ol);
-        const int fid = __builtin_amdgcn_readlane(xf, ol);
-        int le;
-        double gl, gr;
-        if constexpr (kRegKids) {
-            le = __builtin_amdgcn_readlane(xc, ol);
-            gl = readlane_f64(xl, ol);
-            gr = readlane_f64(xr, ol);
+        const unsigned hi = (unsigned)(mine >> 32);
+        const unsigned mh = wave_max_u32(hi);
+        int ol;
+        const unsigned long long t1 = __ballot(hi == mh);
+        if (mh != 0u && (t1 & (t1 - 1ULL)) == 0ULL) {
+            ol = (int)__builtin_ctzll(t1);
         } else {
-            le = v.el[X];
-            gl = v.cb[X];
-            gr = v.gr[X];
+            // several lanes share the high word (or every best is below
+            // 2^-1022): the full 64-bit maximum among them
+            const unsigned long long m = wave_max_u64(hi == mh ? mine : 0ULL);
+            if (m == 0ULL) {  // no slot with a positive gain
+                done = 1;
+                break;
+            }
+            const unsigned long long t2 = __ballot(mine == m);
+            if ((t2 & (t2 - 1ULL)) == 0ULL) ol = (int)__builtin_ctzll(t2);
+            else ol = (int)(wave_min_u32(mine == m ? (unsigned)lbi : 0xFFFFFFFFu) & 63u);
         }
+        const int bi = __builtin_amdgcn_readlane(lbi, ol);
+        const int X = __builtin_amdgcn_readlane(lbe, ol);
+        const int fid = __builtin_amdgcn_readlane(lbf, ol);
+        const int le = __builtin_amdgcn_readlane(kle, ol);
         if (le < 0) {
             x = X;
             break;
         }
-        if constexpr (kRegKids) {  // the children's own children, for the two slots written below
-            pc0 = v.el[le];
-            pgl0 = v.cb[le];
-            pgr0 = v.gr[le];
-            pc1 = v.el[le + 1];
-            pgl1 = v.cb[le + 1];
-            pgr1 = v.gr[le + 1];
-        }
+        const double gl = readlane_f64(kgl, ol), gr = readlane_f64(kgr, ol);
         if (lane == 0) {
             v.cm_e[nc] = X;
             v.cm_fid[nc] = fid;
             v.cm_lf[nc] = nn;
         }
-        const int q2 = nl >> 6, ol2 = nl & 63;
+        const int q = bi >> 6, q2 = nl >> 6, ol2 = nl & 63;
 #pragma unroll
         for (int qq = 0; qq < QS; ++qq) {
             if (lane == ol && qq == q) {
@@ -2744,11 +2709,7 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
                 sf[qq] = nn + 1;
             }
         }
-        pq0 = q;
-        pl0 = ol;
-        pq1 = q2;
-        pl1 = ol2;
-        local_best();
+        if (lane == ol || lane == ol2) local_best();
         ++nl;
         nn += 2;
         ++nc;
@@ -2769,7 +2730,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __shared__ Grow g;
     __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x, s_vf;
     __shared__ unsigned long long s_rows_built, s_rows_parted;
-    __shared__ long long s_chunk;
+    __shared__ long long s_chunk, s_chunk_p;
     __shared__ int s_total_p;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
@@ -3236,8 +3197,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // the batch's accumulated rows spread over about pb_launch tasks (one
     // per resident block), at least hist_chunk_min rows each (fewer tasks
     // mean fewer partials to store and merge; a batch never needs more than
-    // n / hist_chunk_min + nsel of them). Partition: chunks of kPartChunk
-    // parent rows (one output reservation each).
+    // n / hist_chunk_min + nsel of them). Partition: the batch's parent rows
+    // spread over about part_target tasks (one output reservation each),
+    // kPartChunkMin to kPartChunk rows each.
     // the selected leaves' nodes, one memory round trip
     if (tid < nsel) {
         const ENode *e = &s.enodes[v.sel_e[tid]];
@@ -3268,7 +3230,10 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
         if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
         const long long pc = lane < nsel ? (mb + chunk - 1) / chunk : 0;
-        const long long qc = lane < nsel ? (m + kPartChunk - 1) / kPartChunk : 0;
+        long long chunk_p = (rows_total + s.part_target - 1) / s.part_target;
+        chunk_p = (chunk_p + kPartChunkStep - 1) / kPartChunkStep * kPartChunkStep;
+        chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > kPartChunk ? kPartChunk : chunk_p;
+        const long long qc = lane < nsel ? (m + chunk_p - 1) / chunk_p : 0;
         const long long pi = wave_incl_scan(pc), qi = wave_incl_scan(qc);
         if (lane < nsel) {
             v.pcnt[lane] = (int)pc;
@@ -3282,13 +3247,14 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             s_total = (int)pi;
             s_total_p = (int)qi;
             s_chunk = chunk;
+            s_chunk_p = chunk_p;
             s_rows_parted = (unsigned long long)rows_total;
             s_rows_built = (unsigned long long)built_total;
         }
     }
     __syncthreads();
     const int64_t chunk = s_chunk;
-    const int64_t chunk_p = kPartChunk;
+    const int64_t chunk_p = s_chunk_p;
     const int total = s_total, total_p = s_total_p;
     if (total > s.pb_grid || total_p > s.part_grid) {  // the leaves of a batch are disjoint, so never
         finish(4);

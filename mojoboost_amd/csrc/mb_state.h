@@ -122,9 +122,13 @@ struct Round {
     double goss_mult;    // GOSS weight of the sampled small-gradient rows (1 when off)
 };
 
-// Parent rows of a partition task, at most (the planner's chunking; the host
-// sizes the descriptor buffer from it).
+// Parent rows of a partition task: at most kPartChunk (one task per block
+// pass), at least kPartChunkMin (the host sizes the descriptor buffer from
+// it). The planner spreads a batch over about part_target tasks in between,
+// in multiples of kPartChunkStep rows.
 constexpr int kPartChunk = 8192;
+constexpr int kPartChunkMin = 1024;
+constexpr int kPartChunkStep = 256;
 // Root build launch: kHistThreads per block, kHistBlocksPerCU blocks per CU
 // (each with its own LDS histogram).
 #ifndef MB_HIST_THREADS
@@ -299,7 +303,7 @@ struct DevState {
     int32_t scan_grid;     // blocks of a scan launch
     int32_t pb_launch;     // blocks of an accumulation launch (grid-strided)
     int32_t part_launch;   // blocks of a partition launch (grid-strided)
-    int32_t pad_grid_;
+    int32_t part_target;   // partition tasks a batch is spread over
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;
