@@ -286,11 +286,32 @@ def main():
     x, y = workload_data(args.workload, args.rows)
     cats = wl.get("categorical")
     n_cat = None
+    # binning, reported apart from training: the host path (fit + transform
+    # on the host's threads) and the device path (the same fit on the host,
+    # the per-value transform as one kernel); both must give the same bytes
+    tb = time.perf_counter()
     if cats:
         bins, missing, n_cat = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB, categorical=cats)
     else:
         bins, missing = device.bin_dense(x.ravel(), args.rows, F, max_bins=NB)
-    del x
+    host_bin_s = time.perf_counter() - tb
+    tb = time.perf_counter()
+    dbins, dmissing, dn_cat, btimes = device.bin_dense_device(x.ravel(), args.rows, F, max_bins=NB,
+                                                              categorical=cats)
+    dev_bin_s = time.perf_counter() - tb
+    cells = args.rows * F
+    binning = {
+        "host_fit_and_transform_s": round(host_bin_s, 4),
+        "device_path_s": round(dev_bin_s, 4),
+        "device_fit_ms_host": round(btimes["fit_ms"], 2),
+        "device_h2d_ms": round(btimes["h2d_ms"], 2),
+        "device_transform_kernel_ms": round(btimes["transform_ms"], 4),
+        "device_d2h_ms": round(btimes["d2h_ms"], 2),
+        "transform_kernel_gbs": round(cells * 9 / (btimes["transform_ms"] * 1e-3) / 1e9, 1),
+        "transform_bytes_per_value": 9,
+        "bins_identical": bool(np.array_equal(bins, dbins) and np.array_equal(missing, dmissing)),
+    }
+    del x, dbins
     t_data = time.perf_counter() - t0
     print(f"[bench] {args.workload}: data {args.rows}x{F} generated+binned in {t_data:.1f}s, "
           f"label mean {y.mean():.3f}", file=sys.stderr, flush=True)
@@ -442,6 +463,7 @@ def main():
                      "traffic": traffic_per_launch(args.workload), "note": note},
         "cpu_baseline": cpu,
         "parity_first_trees_bit_exact": parity,
+        "binning": binning,
     }
     print(json.dumps(out))
     return 0

@@ -131,6 +131,23 @@ int32_t mbh_bin_dense_cat(const double *data, int64_t n_rows, int32_t n_features
                           uint8_t *out_bins, int32_t *out_missing_bin,
                           int32_t *out_n_categories, char *err, int32_t err_len);
 
+/* mbh_bin_dense_cat with the per-value transform on the GPU: the fit runs
+ * on the host as above, the column-major doubles are copied to the device and
+ * mapped there (BinMapper.transform, src/mojotrees/binning.mojo:3264-3330,
+ * bin_value :3242-3262; categorical codes by CategoricalSpec.bin_of,
+ * src/mojotrees/categorical.mojo:296-322), and the bins copied back; the
+ * result is byte-identical to mbh_bin_dense_cat's. n_categorical may be 0
+ * (categorical NULL); out_n_categories may be NULL. out_times_ms, when not
+ * NULL, receives 4 values: the host fit, the host-to-device copy, the
+ * transform kernel and the device-to-host copy, in milliseconds. */
+int32_t mbh_bin_dense_device(const double *data, int64_t n_rows, int32_t n_features,
+                             int32_t max_bins, int32_t min_data_in_bin,
+                             int32_t use_missing, int64_t sample_cnt, int64_t seed,
+                             const int32_t *categorical, int32_t n_categorical,
+                             uint8_t *out_bins, int32_t *out_missing_bin,
+                             int32_t *out_n_categories, double *out_times_ms,
+                             char *err, int32_t err_len);
+
 /* Number of usable gfx950 devices (0 without a GPU or runtime). */
 int32_t mbh_device_count(void);
 

@@ -38,7 +38,7 @@ MBH_SYMBOLS = [
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
     "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
     "mbh_histogram_noalloc", "mbh_save_model_named", "mbh_model_feature_names",
-    "mbh_objective_quantize32", "mbh_histogram32",
+    "mbh_objective_quantize32", "mbh_histogram32", "mbh_bin_dense_device",
 ]
 
 
@@ -167,6 +167,8 @@ def lib():
                                      V, V, C.c_char_p, I32]),
         "mbh_bin_dense_cat": (I32, [V, I64, I32, I32, I32, I32, I64, I64, V, I32, V, V, V,
                                     C.c_char_p, I32]),
+        "mbh_bin_dense_device": (I32, [V, I64, I32, I32, I32, I32, I64, I64, V, I32, V, V, V, V,
+                                       C.c_char_p, I32]),
         "mbh_dataset_set_categorical": (I32, [V, V, C.c_char_p, I32]),
         "mbh_fit_cat_bits": (None, [V, V]),
         "mbh_dataset_set_groups": (I32, [V, V, I64, C.c_char_p, I32]),

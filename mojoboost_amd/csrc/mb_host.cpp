@@ -5,7 +5,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
+#include <mutex>
 #include <sstream>
 #include <stdexcept>
 #include <thread>
@@ -16,6 +18,9 @@ namespace mb {
 
 namespace {
 
+// Runs fn(0 .. n_tasks - 1) on up to 16 threads. An exception thrown by a
+// task stops that thread's remaining tasks and the first one is rethrown on
+// the calling thread after every thread has joined.
 template <class Fn>
 void parallel_for(int64_t n_tasks, Fn fn) {
     int hw = (int)std::max(1u, std::thread::hardware_concurrency());
@@ -24,12 +29,20 @@ void parallel_for(int64_t n_tasks, Fn fn) {
         for (int64_t i = 0; i < n_tasks; ++i) fn(i);
         return;
     }
+    std::mutex mu;
+    std::exception_ptr first;
     std::vector<std::thread> th;
     for (int t = 0; t < nt; ++t)
         th.emplace_back([&, t] {
-            for (int64_t i = t; i < n_tasks; i += nt) fn(i);
+            try {
+                for (int64_t i = t; i < n_tasks; i += nt) fn(i);
+            } catch (...) {
+                std::lock_guard<std::mutex> lock(mu);
+                if (!first) first = std::current_exception();
+            }
         });
     for (auto &x : th) x.join();
+    if (first) std::rethrow_exception(first);
 }
 
 std::string bits(double x) {

@@ -38,6 +38,27 @@ def bin_dense(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_mis
     return bins, mb
 
 
+def bin_dense_device(x_cm, n_rows, n_features, max_bins=255, min_data_in_bin=3, use_missing=True,
+                     sample_cnt=200_000, seed=1, categorical=None):
+    """bin_dense with the per-value transform on the GPU (the fit stays on
+    the host). Returns (bins_cm uint8, missing_bin int32, n_categories int32,
+    times) with times = {fit_ms (host), h2d_ms, transform_ms (the kernel),
+    d2h_ms}."""
+    x_cm = np.ascontiguousarray(x_cm, np.float64).ravel()
+    bins = np.zeros(n_rows * n_features, np.uint8)
+    mb = np.zeros(n_features, np.int32)
+    nc = np.zeros(n_features, np.int32)
+    cats = np.ascontiguousarray(categorical if categorical is not None else [], np.int32)
+    t = np.zeros(4, np.float64)
+    err = C.create_string_buffer(512)
+    check(lib().mbh_bin_dense_device(ptr(x_cm), n_rows, n_features, max_bins, min_data_in_bin,
+                                     1 if use_missing else 0, sample_cnt, seed,
+                                     ptr(cats) if len(cats) else None, len(cats), ptr(bins), ptr(mb),
+                                     ptr(nc), ptr(t), err, 512), err)
+    times = dict(fit_ms=float(t[0]), h2d_ms=float(t[1]), transform_ms=float(t[2]), d2h_ms=float(t[3]))
+    return bins, mb, nc, times
+
+
 class Dataset:
     """A column-major uint8 binned matrix and its labels, uploaded once."""
 

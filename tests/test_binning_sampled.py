@@ -151,3 +151,17 @@ def test_product_category_bins_on_the_golden_misscat_input():
         assert np.array_equal(got[j], want[j])
         assert gmb[j] == wmb[j]
     assert gmb[1] >= 0          # feature 1 holds NaNs: a missing bin is reserved
+
+
+@pytest.mark.parametrize("n_features", [1, 6])
+def test_refused_categorical_code_is_an_error_not_an_abort(n_features):
+    """The fit refuses a category code of 2^31 or more (the reference's
+    categorical table is int32). The refusal is thrown on one of the host's
+    fitting threads and must come back as the entry point's error."""
+    n = 5000
+    x = np.zeros((n_features, n))
+    x[-1] = np.arange(n) % 7
+    x[-1, 123] = 2.0 ** 31
+    with pytest.raises(Exception, match="below 2\\^31"):
+        device.bin_dense(x.ravel(), n, n_features, max_bins=16,
+                         categorical=np.array([n_features - 1], np.int32))
