@@ -258,9 +258,9 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
             unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
     }
     if (p->goss) {
-        if (p->use_quantized_grad)
-            unsup("GOSS with quantized gradients is not built on the device path yet (use_quantized_grad=false)");
-        if (p->objective == MBH_OBJ_MULTICLASS) unsup("GOSS with multiclass is not built on the device path yet");
+        if (p->use_quantized_grad && p->quant_scale_rule == 1)
+            unsup("GOSS with the magnitude-sum lattice (quant_scale_rule=magnitude_sum) is not built on the "
+                  "device path; GOSS with quantized gradients takes the max-abs lattice");
         // GossParams.validate (goss.mojo:129-145), _check_goss (boosting.mojo:346-355)
         if (p->bagging_freq > 0 && p->bagging_fraction < 1.0) bad("goss and bagging cannot both be enabled");
         if (!(p->top_rate >= 0.0 && p->top_rate <= 1.0) || !(p->other_rate >= 0.0 && p->other_rate <= 1.0) ||
@@ -499,7 +499,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     hp.stochastic = p->stochastic_rounding;
     hp.quant_seed = p->quant_seed;
     // boosting.round_has_constant_hessian: squared error without weights.
-    hp.const_hessian = p->objective == MBH_OBJ_REGRESSION && !ds->d_weights ? 1 : 0;
+    // a GOSS round weights some rows' hessians: not constant
+    hp.const_hessian = p->objective == MBH_OBJ_REGRESSION && !ds->d_weights && !p->goss ? 1 : 0;
     if (p->objective == MBH_OBJ_LAMBDARANK) {
         // binary64 lambdas (the reference's ranker does not narrow them), the
         // queries, 1 / maxDCG per query at the truncation level and the
@@ -567,6 +568,10 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
         s.goss_umask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
         s.goss_other = dalloc<uint8_t>(ds->n, run.owned);
         HIPX(hipMemset(s.goss_other, 0, ds->n));
+        s.goss_rows = dalloc<int32_t>(ds->n, run.owned);
+        s.goss_max = dalloc<unsigned long long>(4, run.owned);
+        HIPX(hipMemset(s.goss_max, 0, 4 * sizeof(unsigned long long)));
+        if (p->objective == MBH_OBJ_MULTICLASS) s.goss_imp = dalloc<double>(ds->n, run.owned);
     }
     hp.bagging = (p->bagging_freq > 0 && p->bagging_fraction < 1.0) ? 1 : 0;
     hp.bagging_freq = p->bagging_freq;
@@ -898,11 +903,20 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             K == 1 && (p->objective == MBH_OBJ_BINARY || p->objective == MBH_OBJ_REGRESSION);
         auto t0 = std::chrono::steady_clock::now();
         for (int t = 0; t < T; ++t) {
-            if (K > 1 && t % K == 0) HIPX(mb::launch_softmax(s, grid_rows, st));
+            // GOSS draws its sample after the derivatives it ranks rows by
+            // and before the quantizer, which sees the weighted derivatives
+            // (goss_round, then the grower's quantizer): per tree for a
+            // single output, once per round from the softmax probabilities
+            // for multiclass (every class tree of the round on that sample)
+            if (K > 1 && t % K == 0) {
+                HIPX(mb::launch_softmax(s, grid_rows, st));
+                if (s.hp.goss) HIPX(mb::launch_goss(s, grid_rows, st));
+            }
             if (!(fuse_objective && t > 0)) HIPX(mb::launch_objective(s, grid_rows, st));
+            if (s.hp.goss && K == 1) HIPX(mb::launch_goss(s, grid_rows, st));
+            if (s.hp.goss && s.hp.quantized) HIPX(mb::launch_goss_stats(s, grid_rows, st));
             if (s.hp.wide) HIPX(mb::launch_magnitude(s, st));
             HIPX(mb::launch_quantize(s, grid_rows, st));
-            if (s.hp.goss) HIPX(mb::launch_goss(s, st));
             if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3]));
             else HIPX(mb::launch_hist(s, st));
             HIPX(mb::launch_scan(s, 1, st));

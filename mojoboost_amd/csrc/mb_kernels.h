@@ -10,7 +10,10 @@ namespace mb {
 hipError_t launch_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st);
 // The GOSS selection of the round (no-ops before the warmup ends).
-hipError_t launch_goss(const DevState &s, hipStream_t st);
+hipError_t launch_goss(const DevState &s, int grid, hipStream_t st);
+// max |g|, |h| of the round's weighted GOSS sample (quantized gradients,
+// between launch_goss and launch_quantize).
+hipError_t launch_goss_stats(const DevState &s, int grid, hipStream_t st);
 // The magnitude-sum lattice's reduction and scales (before launch_quantize).
 hipError_t launch_magnitude(const DevState &s, hipStream_t st);
 hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);

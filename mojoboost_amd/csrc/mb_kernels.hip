@@ -472,6 +472,18 @@ __global__ __launch_bounds__(256) void k_softmax(DevState s) {
     }
 }
 
+// GOSS is on for this tree: enabled and past its warmup rounds
+// (GossParams.active, goss.mojo:102-157).
+__device__ __forceinline__ bool goss_on(const DevState &s) {
+    const Round &rd = *s.round;
+    return s.hp.goss && !rd.stopped && rd.round >= s.hp.goss_warm;
+}
+
+// The GOSS weight of the round's sampled small-importance rows.
+__device__ __forceinline__ double goss_weight(const GossState &g, int64_t n) {
+    return g.other_k > 0 ? (double)(n - g.top_k) / (double)g.other_k : 1.0;
+}
+
 // ---------------------------------------------------------------- quantize
 // derive_scales (max-abs rule, quantized_gradient.mojo:1343-1453) and
 // quantize_scalar per row (:1479-1545). Every row is quantized, sampled or
@@ -482,10 +494,18 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const Round rd = *s.round;
     if (rd.stopped) return;
     const HyperParams &hp = s.hp;
-    double max_g = hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 0])
-                             : (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
-    double max_h = hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 1])
-                             : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
+    // a GOSS round: the root list is the round's sample and the quantizer
+    // sees the weighted derivatives (goss_round before the grower)
+    const bool gs_on = goss_on(s);
+    GossState gst{};
+    if (gs_on) gst = *s.gst;
+    const double gmult = gs_on ? goss_weight(gst, s.n) : 1.0;
+    double max_g = gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 0])
+                   : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 0])
+                               : (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
+    double max_h = gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 1])
+                   : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 1])
+                               : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
     if (max_g < 1e-12) max_g = 1e-12;
     if (max_h < 1e-12) max_h = 1e-12;
     // max-abs: (B / 2) / max|g| and B / max|h| with clamps B / 2, B; the
@@ -501,8 +521,13 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
     const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
-        s.round->sampled = hp.bagging;
-        s.round->goss_mult = 1.0;
+        s.round->sampled = hp.bagging || gs_on;
+        s.round->goss_mult = gmult;
+        if (gs_on) s.cursor[0] = gst.bag_n;
+        if (hp.goss) {
+            s.goss_max[(1 - rd.parity) * 2 + 0] = 0ULL;
+            s.goss_max[(1 - rd.parity) * 2 + 1] = 0ULL;
+        }
         if (!hp.wide) {
             s.round->grad_units = gu;
             s.round->hess_units = hu;
@@ -520,8 +545,9 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
         const int64_t r = r0 + threadIdx.x;
         const bool valid = r < s.n;
         if (valid && hp.quantized) {
-            const double gv = hp.grad64 ? s.grad64[r] : (double)s.grad[r];
-            const double hv = hp.grad64 ? s.hess64[r] : (double)s.hess[r];
+            const double gw = gs_on && s.goss_other[r] ? gmult : 1.0;
+            const double gv = (hp.grad64 ? s.grad64[r] : (double)s.grad[r]) * gw;
+            const double hv = (hp.grad64 ? s.hess64[r] : (double)s.hess[r]) * gw;
             int32_t qg = quantize_scalar(gv, gu, gmax, stoch, gs + (uint64_t)r);
             int32_t qh = quantize_scalar(hv, hu, hmax, stoch, hs + (uint64_t)r);
             if (hp.stage16) {
@@ -541,7 +567,9 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
                     *(uint16_t *)(s.records_w + ((size_t)t * s.n + r) * rec + rec - 2) = v;
             }
         }
-        if (!hp.bagging) {
+        if (gs_on) {
+            if (r < gst.bag_n) s.rows0[r] = s.goss_rows[r];
+        } else if (!hp.bagging) {
             if (valid) s.rows0[r] = (int32_t)r;
         } else {
             // Sampled rows appended with one atomic per wave; their order in
@@ -650,14 +678,39 @@ __global__ void k_magfold(DevState s) {
 // 64 or more is kept whatever the rows before it do, so a step costs a
 // ballot and a popcount; only steps with a kappa inside that window take the
 // 64 rows one by one.
-__device__ __forceinline__ bool goss_on(const DevState &s) {
-    const Round &rd = *s.round;
-    return s.hp.goss && !rd.stopped && rd.round >= s.hp.goss_warm;
+
+// A row's sampling importance: goss_importance's |g h| (goss.mojo:294-305)
+// of a single-output round, the class sum of a multiclass round (goss_imp).
+__device__ __forceinline__ unsigned long long goss_key(const DevState &s, int64_t r) {
+    const double imp = s.hp.num_class > 1 ? s.goss_imp[r] : fabs((double)s.grad[r] * (double)s.hess[r]);
+    return (unsigned long long)__double_as_longlong(imp);  // non-negative: ordered like its bits
 }
 
-__device__ __forceinline__ unsigned long long goss_key(const DevState &s, int64_t r) {
-    const double imp = fabs((double)s.grad[r] * (double)s.hess[r]);
-    return (unsigned long long)__double_as_longlong(imp);  // non-negative: ordered like its bits
+
+// _multiclass_goss_select's importance (boosting.mojo:3680-3710): per row,
+// the sum in class order of |g_k h_k| over every class k, each class's
+// derivatives exactly as k_objective writes them for that class's tree
+// (narrowed to binary32, weight applied), the products and the sum in
+// binary64.
+__global__ __launch_bounds__(256) void k_goss_importance(DevState s) {
+    if (!goss_on(s)) return;
+    const int K = s.hp.num_class;
+    const double factor = (double)K / (double)(K - 1);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
+        const double w = s.weights ? s.weights[r] : 1.0;
+        const int y = (int)s.labels[r];
+        double imp = 0.0;
+        for (int k = 0; k < K; ++k) {
+            const double p = s.prob[r * K + k];
+            const float g = (float)(w * (p - (y == k ? 1.0 : 0.0)));
+            double hh = factor * p * (1.0 - p);
+            if (hh < 1e-16) hh = 1e-16;
+            const float h = (float)(w * hh);
+            imp += fabs((double)g * (double)h);
+        }
+        s.goss_imp[r] = imp;
+    }
 }
 
 __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
@@ -1045,14 +1098,53 @@ __global__ __launch_bounds__(1024) void k_goss_scatter(DevState s) {
     }
     const int pre = block_excl_prefix(top || other, wsum);
     if (r < n) {
-        if (top || other) s.rows0[(int64_t)s.goss_blk[blockIdx.x] + pre] = (int32_t)r;
+        if (top || other) s.goss_rows[(int64_t)s.goss_blk[blockIdx.x] + pre] = (int32_t)r;
         s.goss_other[r] = other ? 1 : 0;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        const GossState g = *s.gst;
-        s.cursor[0] = g.bag_n;
-        s.round->sampled = 1;
-        s.round->goss_mult = g.other_k > 0 ? (double)(n - g.top_k) / (double)g.other_k : 1.0;
+}
+
+// max |g w| and |h w| over the round's sample, w the row's GOSS weight
+// (goss_weight for a sampled small-importance row, else 1), in binary64 as
+// apply_goss_scaling leaves the derivatives (goss.mojo:360-373); rows whose
+// weighted derivatives are not finite add nothing (gradient_stats,
+// quantized_gradient.mojo:762-810). Accumulated into goss_max[parity]; the
+// quantizer reads it and clears the other pair for the next tree.
+__global__ __launch_bounds__(256) void k_goss_stats(DevState s) {
+    __shared__ double red_g[4], red_h[4];
+    if (!goss_on(s) || !s.hp.quantized) return;
+    const GossState g = *s.gst;
+    const double mult = goss_weight(g, s.n);
+    const int parity = s.round->parity;
+    double mg = 0.0, mh = 0.0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < g.bag_n; j += stride) {
+        const int32_t r = s.goss_rows[j];
+        const double m = s.goss_other[r] ? mult : 1.0;
+        const double ag = fabs((double)s.grad[r] * m), ah = fabs((double)s.hess[r] * m);
+        if (isfinite(ag) && isfinite(ah)) {
+            mg = fmax(mg, ag);
+            mh = fmax(mh, ah);
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        mg = fmax(mg, __shfl_xor(mg, d, 64));
+        mh = fmax(mh, __shfl_xor(mh, d, 64));
+    }
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 0) {
+        red_g[w] = mg;
+        red_h[w] = mh;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) {
+            mg = fmax(mg, red_g[i]);
+            mh = fmax(mh, red_h[i]);
+        }
+        // non-negative doubles order like their bit patterns
+        atomicMax(&s.goss_max[parity * 2 + 0], (unsigned long long)__double_as_longlong(mg));
+        atomicMax(&s.goss_max[parity * 2 + 1], (unsigned long long)__double_as_longlong(mh));
     }
 }
 
@@ -3792,7 +3884,8 @@ hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st) {
     hipLaunchKernelGGL(k_softmax, dim3(grid), dim3(256), 0, st, s);
     return hipGetLastError();
 }
-hipError_t launch_goss(const DevState &s, hipStream_t st) {
+hipError_t launch_goss(const DevState &s, int grid_rows, hipStream_t st) {
+    if (s.hp.num_class > 1) hipLaunchKernelGGL(k_goss_importance, dim3(grid_rows), dim3(256), 0, st, s);
     hipLaunchKernelGGL(k_goss_setup, dim3(1), dim3(256), 0, st, s);
     const int grid = 1024;
     for (int pass = 0; pass < 8; ++pass) {
@@ -3822,6 +3915,10 @@ hipError_t launch_goss(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 1);
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, bag_n);
     hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(1024), 0, st, s);
+    return hipGetLastError();
+}
+hipError_t launch_goss_stats(const DevState &s, int grid_rows, hipStream_t st) {
+    hipLaunchKernelGGL(k_goss_stats, dim3(grid_rows), dim3(256), 0, st, s);
     return hipGetLastError();
 }
 hipError_t launch_magnitude(const DevState &s, hipStream_t st) {

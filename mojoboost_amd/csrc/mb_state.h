@@ -276,6 +276,9 @@ struct DevState {
     int32_t *goss_urow;         // their row ids
     unsigned long long *goss_umask; // the open rows' decisions, one bit per list position
     uint8_t *goss_other;        // n: 1 when the row was kept by the sampling (weighted)
+    int32_t *goss_rows;         // n: the round's sample, ascending (copied to the root list per tree)
+    double *goss_imp;           // n (multiclass): the round's importance, summed over the classes
+    unsigned long long *goss_max;  // 2 x 2: max |g|, |h| of the weighted sample (binary64 bits), by parity
     int32_t goss_nblk;
     int32_t pad_goss_;
     // growth

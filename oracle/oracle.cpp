@@ -1315,15 +1315,13 @@ double select_kth_desc(std::vector<double> &v, int64_t k) {
     return v[lo];
 }
 
-bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
-                std::vector<double> &hess, const orc_params &p, int64_t round,
-                std::vector<double> *scale = nullptr) {
-    if (!p.goss) return false;
-    int64_t warm = p.learning_rate <= 0.0 ? 0 : (int64_t)(1.0 / p.learning_rate);
-    if (round < warm) return false;
-    int64_t n = (int64_t)grad.size();
-    std::vector<double> imp(n);
-    for (int64_t r = 0; r < n; ++r) imp[r] = std::fabs(grad[r] * hess[r]);
+// goss_select (goss.mojo:308-357) over per-row importance: the sample in
+// ascending row order into bag, other[r] = 1 for a sampled small-importance
+// row (0 for every other row); returns the weight of those rows,
+// (n - top_k) / other_k (1 when other_k is 0).
+double goss_select(const std::vector<double> &imp, const orc_params &p, int64_t round,
+                   std::vector<int32_t> &bag, std::vector<uint8_t> &other) {
+    const int64_t n = (int64_t)imp.size();
     int64_t top_k = (int64_t)((double)n * p.top_rate);
     if (top_k < 1) top_k = 1;
     if (top_k > n) top_k = n;
@@ -1336,12 +1334,11 @@ bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
     uint64_t stream = splitmix64((uint64_t)(p.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
                                  ((uint64_t)round * GOLDEN));
     bag.clear();
-    if (scale) scale->clear();
+    other.assign((size_t)n, 0);
     int64_t n_top = 0, n_other = 0;
     for (int64_t r = 0; r < n; ++r) {
         if (imp[r] >= threshold) {
             bag.push_back((int32_t)r);
-            if (scale) scale->push_back(1.0);
             ++n_top;
         } else {
             int64_t rest_need = other_k - n_other;
@@ -1350,15 +1347,60 @@ bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
                                         : (double)rest_need / (double)rest_all;
             if (uniform(stream + (uint64_t)r) < prob) {
                 bag.push_back((int32_t)r);
-                if (scale) scale->push_back(mult);
-                grad[r] *= mult;
-                hess[r] *= mult;
+                other[(size_t)r] = 1;
                 ++n_other;
             }
         }
     }
+    return mult;
+}
+
+// GossParams.active (goss.mojo:102-157): on, and past floor(1 / learning_rate)
+// warmup rounds
+bool goss_active(const orc_params &p, int64_t round) {
+    if (!p.goss) return false;
+    int64_t warm = p.learning_rate <= 0.0 ? 0 : (int64_t)(1.0 / p.learning_rate);
+    return round >= warm;
+}
+
+// apply_goss_scaling (goss.mojo:360-373): the sampled small-importance rows'
+// derivatives times the weight, in binary64
+void goss_scale(const std::vector<uint8_t> &other, double mult, std::vector<double> &grad,
+                std::vector<double> &hess, const std::vector<int32_t> &bag) {
+    for (int32_t r : bag)
+        if (other[(size_t)r]) {
+            grad[r] *= mult;
+            hess[r] *= mult;
+        }
+}
+
+// goss_round (goss.mojo:376-396): a single-output round's sample from
+// goss_importance = |grad * hess| (:294-305), its rows scaled in place.
+// scale, when given, receives each sampled row's multiplier (1 for a top row).
+bool goss_round(std::vector<int32_t> &bag, std::vector<double> &grad,
+                std::vector<double> &hess, const orc_params &p, int64_t round,
+                std::vector<double> *scale = nullptr) {
+    if (!goss_active(p, round)) return false;
+    const int64_t n = (int64_t)grad.size();
+    std::vector<double> imp(n);
+    for (int64_t r = 0; r < n; ++r) imp[r] = std::fabs(grad[r] * hess[r]);
+    std::vector<uint8_t> other;
+    const double mult = goss_select(imp, p, round, bag, other);
+    goss_scale(other, mult, grad, hess, bag);
+    if (scale) {
+        scale->clear();
+        for (int32_t r : bag) scale->push_back(other[(size_t)r] ? mult : 1.0);
+    }
     return true;
 }
+
+// boosting._multiclass_goss_select (boosting.mojo:3680-3710): one sample for
+// a whole multiclass round from each row's sum over the classes, in class
+// order, of |grad_k * hess_k| with the derivatives at the round's precision
+// (_fill_softmax_grad_hess, as the class trees will use them).
+double goss_select_multiclass(const std::vector<double> &prob, const double *labels, int64_t n, int K,
+                              const double *weights, const orc_params &p, int64_t round,
+                              std::vector<int32_t> &bag, std::vector<uint8_t> &other);
 
 // ---------------------------------------------------------------- ranking
 // LambdaRank, LightGBM's LambdarankNDCG (src/mojotrees/ranking.mojo).
@@ -1552,6 +1594,17 @@ void softmax_rows(const std::vector<double> &raw, std::vector<double> &prob,
         }
         for (int i = 0; i < k; ++i) p[i] = p[i] / total;
     }
+}
+
+double goss_select_multiclass(const std::vector<double> &prob, const double *labels, int64_t n, int K,
+                              const double *weights, const orc_params &p, int64_t round,
+                              std::vector<int32_t> &bag, std::vector<uint8_t> &other) {
+    std::vector<double> imp((size_t)n, 0.0), g((size_t)n), h((size_t)n);
+    for (int k = 0; k < K; ++k) {
+        fill_grad_hess(ORC_OBJ_MULTICLASS, prob.data(), labels, n, K, k, g.data(), h.data(), weights);
+        for (int64_t r = 0; r < n; ++r) imp[r] += std::fabs(g[r] * h[r]);
+    }
+    return goss_select(imp, p, round, bag, other);
 }
 
 // One tree of a round: quantized or float, returns the tree and leaf rows.
@@ -1913,9 +1966,6 @@ int32_t orc_hist_float(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
     return 0;
 }
 
-// One GOSS selection (goss_importance + goss_select + apply_goss_scaling,
-// goss.mojo:294-373) on caller arrays, warmup not applied. rows_out and
-// scale_out need n entries; grad/hess are scaled in place like the trainer's.
 int32_t orc_lambdarank(const double *scores, const double *labels, const int64_t *starts,
                        int64_t n_queries, int32_t truncation, double sigma, int32_t norm,
                        double *grad, double *hess) {
@@ -1950,6 +2000,9 @@ int32_t orc_lambdarank(const double *scores, const double *labels, const int64_t
 
 double orc_log2(double x) { return ref_log2(x); }
 
+// One GOSS selection (goss_importance + goss_select + apply_goss_scaling,
+// goss.mojo:294-373) on caller arrays, warmup not applied. rows_out and
+// scale_out need n entries; grad/hess are scaled in place like the trainer's.
 int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
                         double other_rate, int32_t seed, int64_t round_index,
                         int32_t *rows_out, double *scale_out, int64_t *n_out) {
@@ -1969,6 +2022,32 @@ int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
     }
     std::memcpy(grad, g.data(), n * sizeof(double));
     std::memcpy(hess, h.data(), n * sizeof(double));
+    *n_out = (int64_t)bag.size();
+    return 0;
+}
+
+// One multiclass round's GOSS sample (_multiclass_goss_select,
+// boosting.mojo:3680-3710) from the round's class probabilities (row-major,
+// prob[r * K + k]), warmup not applied: rows_out (n entries) receives the
+// sample ascending, other_out[r] (n entries) 1 for a sampled small-importance
+// row, *mult_out their weight.
+int32_t orc_goss_select_multiclass(const double *prob, const double *labels, int64_t n, int32_t K,
+                                   const double *weights, double top_rate, double other_rate,
+                                   int32_t seed, int64_t round_index, int32_t *rows_out,
+                                   uint8_t *other_out, double *mult_out, int64_t *n_out) {
+    if (n <= 0 || K < 2 || !prob || !labels || !rows_out || !other_out || !mult_out || !n_out) return -1;
+    orc_params p{};
+    p.goss = 1;
+    p.learning_rate = 0.0;
+    p.top_rate = top_rate;
+    p.other_rate = other_rate;
+    p.goss_seed = seed;
+    std::vector<double> pr(prob, prob + n * K);
+    std::vector<int32_t> bag;
+    std::vector<uint8_t> other;
+    *mult_out = goss_select_multiclass(pr, labels, n, K, weights, p, round_index, bag, other);
+    for (size_t i = 0; i < bag.size(); ++i) rows_out[i] = bag[i];
+    std::memcpy(other_out, other.data(), (size_t)n);
     *n_out = (int64_t)bag.size();
     return 0;
 }
@@ -2121,11 +2200,18 @@ orc_model *orc_train(const uint8_t *bins, int64_t n, int32_t nf, int32_t nb,
             } else {
                 // boosting._boost_rounds_multiclass (boosting.mojo:3876-4165)
                 softmax_rows(raw, prob, n, K);
+                // one GOSS sample for the whole round, drawn before any class's
+                // tree (:4041-4053); each class's derivatives scaled by it
+                std::vector<uint8_t> gother;
+                double gmult = 1.0;
+                const bool gactive = goss_active(P.p, it);
+                if (gactive) gmult = goss_select_multiclass(prob, labels, n, K, P.p.weights, P.p, it, bag, gother);
                 bool progress = false;
                 std::vector<Tree> round_trees;
                 for (int k = 0; k < K; ++k) {
                     fill_grad_hess(ORC_OBJ_MULTICLASS, prob.data(), labels, n, K, k,
                                    grad.data(), hess.data(), P.p.weights);
+                    if (gactive) goss_scale(gother, gmult, grad, hess, bag);
                     Tree t = grow_one(d, P, grad, hess, bag, it, k, (int64_t)it * K + k,
                                       leaves, qg, qh, pool);
                     if (t.n_leaves > 1 || std::fabs(t.value[0]) >= 1e-12) progress = true;

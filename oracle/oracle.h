@@ -183,6 +183,12 @@ double orc_log2(double x);
 int32_t orc_goss_select(double *grad, double *hess, int64_t n, double top_rate,
                         double other_rate, int32_t seed, int64_t round_index,
                         int32_t *rows_out, double *scale_out, int64_t *n_out);
+/* One multiclass round's GOSS sample (boosting._multiclass_goss_select):
+ * prob row-major n x K, weights may be NULL; see oracle.cpp. */
+int32_t orc_goss_select_multiclass(const double *prob, const double *labels, int64_t n, int32_t K,
+                                   const double *weights, double top_rate, double other_rate,
+                                   int32_t seed, int64_t round_index, int32_t *rows_out,
+                                   uint8_t *other_out, double *mult_out, int64_t *n_out);
 
 /* ----------------------------------------------------------- split search */
 /* Best split of one node from an integer histogram. Returns found (0/1);

@@ -407,6 +407,30 @@ def goss_select(grad, hess, top_rate=0.2, other_rate=0.1, seed=3, round_index=0)
     return rows[:cnt.value], scale[:cnt.value], g, h
 
 
+def goss_select_multiclass(prob, labels, K, top_rate=0.2, other_rate=0.1, seed=3, round_index=0,
+                           weights=None):
+    """One multiclass round's GOSS sample (no warmup) from row-major class
+    probabilities: (rows, other flags per row, multiplier)."""
+    L = lib()
+    L.orc_goss_select_multiclass.restype = C.c_int32
+    L.orc_goss_select_multiclass.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_void_p,
+                                             C.c_double, C.c_double, C.c_int32, C.c_int64, C.c_void_p,
+                                             C.c_void_p, C.c_void_p, C.c_void_p]
+    pr = np.ascontiguousarray(prob, np.float64).ravel()
+    y = np.ascontiguousarray(labels, np.float64)
+    n = len(y)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float64)
+    rows = np.zeros(n, np.int32)
+    other = np.zeros(n, np.uint8)
+    mult = C.c_double(0.0)
+    cnt = C.c_int64(0)
+    rc = L.orc_goss_select_multiclass(_ptr(pr), _ptr(y), n, K, _ptr(w) if w is not None else None, top_rate,
+                                      other_rate, seed, round_index, _ptr(rows), _ptr(other),
+                                      C.byref(mult), C.byref(cnt))
+    assert rc == 0, rc
+    return rows[:cnt.value], other, mult.value
+
+
 def query_starts(counts):
     """Query boundaries (int64, n_queries + 1) from per-query row counts."""
     return np.concatenate([[0], np.cumsum(np.asarray(counts, np.int64))]).astype(np.int64)

@@ -148,3 +148,95 @@ def test_leaf_row_counts_come_from_the_sample():
         assert len(m.tree(t)["value"]) > 1
     for t in range(2, 4):
         assert len(m.tree(t)["value"]) == 1
+
+
+# ---- multiclass GOSS (boosting._multiclass_goss_select, boosting.mojo:3680-3710,
+# used once per round at :4041-4053)
+
+def _probs(n, K, seed):
+    rng = np.random.default_rng(seed)
+    p = rng.dirichlet(np.ones(K) * 0.7, size=n)
+    y = rng.integers(0, K, size=n).astype(np.float64)
+    return p, y
+
+
+def test_multiclass_sample_is_the_single_output_sample_of_the_class_sum():
+    """The round's importance is the class sum, in class order, of
+    |grad_k * hess_k| with each class's derivatives as its tree uses them
+    (pinned: the golden softmax fits). The multiclass selection must then be
+    goss_select over that importance: the single-output selection with
+    grad = importance and hess = 1 (|importance * 1| is the importance
+    itself), same rows, same weighted rows, same multiplier."""
+    for K, seed in ((3, 1), (5, 2), (2, 3)):
+        p, y = _probs(4000, K, seed)
+        w = np.random.default_rng(seed).uniform(0.5, 2.0, size=len(y)) if K == 5 else None
+        imp = np.zeros(len(y))
+        for k in range(K):
+            if w is None:
+                g, h = O.grad_hess(O.OBJ_MULTICLASS, p.ravel(), y, num_class=K, class_k=k)
+            else:
+                g, h = O.grad_hess_w(O.OBJ_MULTICLASS, p.ravel(), y, w, num_class=K, class_k=k)
+            imp += np.abs(g * h)
+        rows, other, mult = O.goss_select_multiclass(p, y, K, 0.25, 0.15, seed=7, round_index=4, weights=w)
+        srows, sscale, _, _ = O.goss_select(imp, np.ones(len(y)), 0.25, 0.15, 7, 4)
+        assert np.array_equal(rows, srows)
+        assert np.array_equal(np.flatnonzero(other), srows[sscale != 1.0])
+        assert np.all(sscale[sscale != 1.0] == mult)
+
+
+def test_multiclass_importance_counts_every_class():
+    """A row whose true class is badly predicted in one class only must
+    outrank rows that every class predicts well: dropping a class from the
+    sum (or taking one class's term) changes which rows are on top."""
+    n, K = 1000, 4
+    p = np.full((n, K), 0.25)
+    y = np.zeros(n)
+    # rows 0..99: class 3 confidently wrong (label 3, p_3 small)
+    p[:100] = [0.7, 0.1, 0.1, 0.1]
+    y[:100] = 3
+    # rows 100..: well predicted (label 0, p_0 large)
+    p[100:] = [0.97, 0.01, 0.01, 0.01]
+    rows, other, _ = O.goss_select_multiclass(p, y, K, 0.1, 0.0, seed=1, round_index=0)
+    assert np.array_equal(rows, np.arange(100))
+    assert not other.any()
+
+
+def test_multiclass_goss_with_every_row_on_top_trains_like_no_goss():
+    """top_rate = 1 puts every row on top with weight 1: past the warmup the
+    rounds train on every row, so the fit equals a fit without GOSS, tree for
+    tree (quantized and fp32)."""
+    n, f, K = 3000, 4, 3
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(f, n))
+    y = np.argmax(x[:K] + 0.3 * rng.normal(size=(K, n)), axis=0).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=32)
+    for quantized in (1, 0):
+        kw = dict(objective=O.OBJ_MULTICLASS, num_class=K, num_iterations=6, num_leaves=15,
+                  learning_rate=0.5, use_quantized_grad=quantized)
+        plain = O.train(bins, n, f, 32, y, O.default_params(**kw), missing_bin=mb)
+        goss = O.train(bins, n, f, 32, y, O.default_params(**kw, goss=1, top_rate=1.0, other_rate=0.0),
+                       missing_bin=mb)
+        assert plain.n_trees == goss.n_trees == 6 * K
+        for t in range(plain.n_trees):
+            a, b = plain.tree(t), goss.tree(t)
+            assert np.array_equal(a["feature"], b["feature"]) and np.array_equal(a["threshold"], b["threshold"])
+            assert np.array_equal(a["value"].view(np.uint64), b["value"].view(np.uint64))
+
+
+def test_multiclass_goss_samples_after_warmup():
+    n, f, K = 4000, 4, 3
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(f, n))
+    y = np.argmax(x[:K] + 0.3 * rng.normal(size=(K, n)), axis=0).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, f, max_bins=32)
+    kw = dict(objective=O.OBJ_MULTICLASS, num_class=K, num_iterations=5, num_leaves=7,
+              learning_rate=0.5, use_quantized_grad=1, min_data_in_leaf=5)
+    m = O.train(bins, n, f, 32, y, O.default_params(**kw, goss=1, top_rate=0.2, other_rate=0.1), missing_bin=mb)
+    # warmup floor(1 / 0.5) = 2 rounds on every row, then one sample per
+    # round of at least 0.2 n + 0.1 n rows (rows tied with the top_k-th
+    # importance all stay on top): every class tree of a round has it as
+    # its root count
+    roots = np.array([m.tree(t)["count"][0] for t in range(m.n_trees)]).reshape(-1, K)
+    assert np.all(roots[:2] == n)
+    assert np.all(roots[2:] >= 0.3 * n) and np.all(roots[2:] < n)
+    assert np.all(roots[2:] == roots[2:, :1])
