@@ -1716,7 +1716,11 @@ __device__ __forceinline__ int wave_incl_scan_i(int v) {
     return v;
 }
 
-__global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode) {
+// kCat: the dataset has categorical features (the category-set search is
+// compiled in). At most 128 VGPRs (4 waves per SIMD): two 512-thread blocks
+// per CU, so a batch's (leaf, feature) tasks need half the block rounds.
+template <bool kCat>
+__global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_mode) {
     __shared__ int cg[2][256], ch[2][256], cc[2][256];
     __shared__ int acc[3][256];
     __shared__ int wtot[8][3];
@@ -1887,7 +1891,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
         int best_left = 0;
         // a categorical feature is searched as category partitions
         // (categorical.find_best_categorical_split, categorical.mojo:684-782)
-        const int ncf = s.ncat ? s.ncat[f] : 0;  // block-uniform
+        const int ncf = kCat && s.ncat ? s.ncat[f] : 0;  // block-uniform
         const bool cat_onehot = ncf > 0 && (hp.one_hot_max_size >= 0 ? ncf <= hp.one_hot_max_size
                                                                       : ncf + 1 <= hp.max_cat_to_onehot);
         bool cat_sorted = false;
@@ -2157,7 +2161,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(DevState s, int root_mode
 // expression. Given identical histograms the gains are identical; the
 // histograms themselves differ from the reference's only in the rounding of
 // their fp64 sums.
-__global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mode) {
+// kCat as in k_scan; without categorical features at most 128 VGPRs (two
+// blocks per CU), with them uncapped (the category search would spill).
+template <bool kCat>
+__global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState s, int root_mode) {
     __shared__ double cg[2][256], ch[2][256];
     __shared__ int cc[2][256];
     __shared__ double pg_[2][256], ph_[2][256];
@@ -2319,7 +2326,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_f(DevState s, int root_mo
         // oracle's arithmetic (categorical.find_best_categorical_split,
         // categorical.mojo:684-782) with the totals above; the walk adds the
         // sorted categories' sums in order, one thread per direction
-        const int ncf = s.ncat ? s.ncat[f] : 0;  // block-uniform
+        const int ncf = kCat && s.ncat ? s.ncat[f] : 0;  // block-uniform
         const bool cat_onehot = ncf > 0 && (hp.one_hot_max_size >= 0 ? ncf <= hp.one_hot_max_size
                                                                       : ncf + 1 <= hp.max_cat_to_onehot);
         bool cat_sorted = false;
@@ -4048,10 +4055,14 @@ hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEv
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     const int grid = root_mode ? s.n_features : s.scan_grid;
-    if (s.hp.quantized)
-        hipLaunchKernelGGL(k_scan, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    if (s.hp.quantized && s.ncat)
+        hipLaunchKernelGGL(k_scan<true>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    else if (s.hp.quantized)
+        hipLaunchKernelGGL(k_scan<false>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+    else if (s.ncat)
+        hipLaunchKernelGGL(k_scan_f<true>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
     else
-        hipLaunchKernelGGL(k_scan_f, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+        hipLaunchKernelGGL(k_scan_f<false>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
     return hipGetLastError();
 }
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st) {
