@@ -916,9 +916,12 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             if (s.hp.goss && K == 1) HIPX(mb::launch_goss(s, grid_rows, st));
             if (s.hp.goss && s.hp.quantized) HIPX(mb::launch_goss_stats(s, grid_rows, st));
             if (s.hp.wide) HIPX(mb::launch_magnitude(s, st));
-            HIPX(mb::launch_quantize(s, grid_rows, st));
-            if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3]));
-            else HIPX(mb::launch_hist(s, st));
+            // the max-abs lattice quantizes in the root build, which reads
+            // every record of the round's rows anyway
+            const bool fuse_q = mb::acc_kind(s.hp) == mb::kAccQuant && !s.hp.grad64;
+            HIPX(mb::launch_quantize(s, grid_rows, st, !fuse_q));
+            if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3], fuse_q));
+            else HIPX(mb::launch_hist(s, st, nullptr, nullptr, fuse_q));
             HIPX(mb::launch_scan(s, 1, st));
             HIPX(mb::launch_plan(s, 1, st));
             if (timed) HIPX(hipEventRecord(events[4], st));
@@ -1008,6 +1011,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         // algorithmic bytes per accumulated row: its bins plus its g/h pair
         // (int8 x 2 quantized, fp32 x 2 otherwise)
         const double rb = ds->F + (s.hp.wide ? 8 : s.hp.quantized ? 2 : 8);
+        // a root build that quantizes (max-abs lattice) also reads each root
+        // row's binary32 g, h and writes its int8 pair: the quantizer's
+        // algorithmic bytes are the root kernel's too
+        const double rq = mb::acc_kind(s.hp) == mb::kAccQuant && !s.hp.grad64 ? 10.0 : 0.0;
         double useful_rows = 0.0, builds = 0.0, root_rows = 0.0;
         double iters_total = 0.0, exps = 0.0, rows_built = 0.0, rows_parted = 0.0;
         int grown = 0;
@@ -1074,10 +1081,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         double *o = fit->stats;
         o[0] = std::chrono::duration<double>(t1 - t0).count();
         o[1] = t_acc;
-        o[2] = useful_rows * rb;
+        o[2] = useful_rows * rb + root_rows * rq;
         o[3] = useful_rows * ds->F;
         o[4] = builds;
-        o[5] = root_rows * rb;
+        o[5] = root_rows * (rb + rq);
         o[6] = t_root;
         o[7] = grown;
         o[8] = t_root + t_root_scan + t_pb + t_scan;

@@ -16,7 +16,8 @@ hipError_t launch_goss(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_goss_stats(const DevState &s, int grid, hipStream_t st);
 // The magnitude-sum lattice's reduction and scales (before launch_quantize).
 hipError_t launch_magnitude(const DevState &s, hipStream_t st);
-hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st);
+// write_pairs = false leaves the max-abs int8 pairs to launch_hist(quantize).
+hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st, bool write_pairs = true);
 // Raises the dynamic LDS limits of the kernels that need more than 64 KB.
 hipError_t prepare_kernels(const DevState &s);
 size_t hist_lds_bytes(const DevState &s);
@@ -31,7 +32,10 @@ size_t score_lds_bytes(const DevState &s);
 size_t rank_lds_bytes(const DevState &s);
 // With both events given, the runtime records them at the kernel's own start
 // and end (for timing without queue gaps).
-hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+// quantize: the root build quantizes the rows it reads and writes their
+// pairs into the records (max-abs lattice only; other kinds ignore it).
+hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr,
+                       bool quantize = false);
 hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);

@@ -490,20 +490,25 @@ __device__ __forceinline__ double goss_weight(const GossState &g, int64_t n) {
 // not, with the row id as the stream counter. The int8 pair lands in the
 // last two bytes of the row's record, next to its bins. The root row list
 // (the bag) is gathered here; without bagging the root reads rows directly.
-__global__ __launch_bounds__(256) void k_quantize(DevState s) {
-    const Round rd = *s.round;
-    if (rd.stopped) return;
+// The quantizer of one tree: its scales, lattice bounds and streams, and
+// the tree's GOSS weight (rounds where GOSS samples: the quantizer sees the
+// weighted derivatives, goss_round before the grower).
+struct QCtx {
+    double gu, hu, gmult;
+    int32_t gmax, hmax;
+    uint64_t gs, hs;
+    bool stoch, gs_on;
+};
+
+__device__ __forceinline__ QCtx quant_ctx(const DevState &s, const Round &rd) {
     const HyperParams &hp = s.hp;
-    // a GOSS round: the root list is the round's sample and the quantizer
-    // sees the weighted derivatives (goss_round before the grower)
-    const bool gs_on = goss_on(s);
-    GossState gst{};
-    if (gs_on) gst = *s.gst;
-    const double gmult = gs_on ? goss_weight(gst, s.n) : 1.0;
-    double max_g = gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 0])
+    QCtx c;
+    c.gs_on = goss_on(s);
+    c.gmult = c.gs_on ? goss_weight(*s.gst, s.n) : 1.0;
+    double max_g = c.gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 0])
                    : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 0])
                                : (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
-    double max_h = gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 1])
+    double max_h = c.gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 1])
                    : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 1])
                                : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
     if (max_g < 1e-12) max_g = 1e-12;
@@ -511,13 +516,48 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     // max-abs: (B / 2) / max|g| and B / max|h| with clamps B / 2, B; the
     // magnitude-sum lattice: the round's power-of-two scales (k_magfold)
     // with clamps 2^30; a constant hessian takes one unit over max|h| on both
-    const int32_t gmax = hp.wide ? (int32_t)kFixedOne : hp.quant_bins / 2;
-    const int32_t hmax = hp.const_hessian ? 1 : hp.wide ? (int32_t)kFixedOne : hp.quant_bins;
-    const double gu = hp.wide ? rd.grad_units : (double)gmax / max_g;
-    const double hu = hp.wide ? rd.hess_units : hp.const_hessian ? 1.0 / max_h : (double)hmax / max_h;
-    const uint64_t gs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 0);
-    const uint64_t hs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 1);
-    const bool stoch = hp.stochastic != 0;
+    c.gmax = hp.wide ? (int32_t)kFixedOne : hp.quant_bins / 2;
+    c.hmax = hp.const_hessian ? 1 : hp.wide ? (int32_t)kFixedOne : hp.quant_bins;
+    c.gu = hp.wide ? rd.grad_units : (double)c.gmax / max_g;
+    c.hu = hp.wide ? rd.hess_units : hp.const_hessian ? 1.0 / max_h : (double)c.hmax / max_h;
+    c.gs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 0);
+    c.hs = quant_stream(hp.quant_seed, rd.round, rd.class_k, 1);
+    c.stoch = hp.stochastic != 0;
+    return c;
+}
+
+// Row r's quantized pair (quantize_scalar with the row id as the stream
+// counter), weighted by the GOSS weight when the row was sampled with it.
+__device__ __forceinline__ void quant_row(const DevState &s, const QCtx &c, int64_t r, int32_t &qg, int32_t &qh) {
+    const double gw = c.gs_on && s.goss_other[r] ? c.gmult : 1.0;
+    const double gv = (s.hp.grad64 ? s.grad64[r] : (double)s.grad[r]) * gw;
+    const double hv = (s.hp.grad64 ? s.hess64[r] : (double)s.hess[r]) * gw;
+    qg = quantize_scalar(gv, c.gu, c.gmax, c.stoch, c.gs + (uint64_t)r);
+    qh = quantize_scalar(hv, c.hu, c.hmax, c.stoch, c.hs + (uint64_t)r);
+}
+
+// One of row r's two binary32 values, its gradient (isg) or hessian, with
+// its GOSS weight applied in binary64 (w: the row was sampled with the
+// weight), quantized as quant_row does: the loads (binary32 derivatives
+// only) can be issued ahead of their use.
+__device__ __forceinline__ int32_t quant_value(const QCtx &c, float v, bool w, int64_t r, bool isg) {
+    return quantize_scalar((double)v * (w ? c.gmult : 1.0), isg ? c.gu : c.hu, isg ? c.gmax : c.hmax, c.stoch,
+                           (isg ? c.gs : c.hs) + (uint64_t)r);
+}
+
+// write_pairs = 0: the max-abs int8 pairs are left to the root build
+// (k_hist quantizes the rows it reads, k_hist<.., kQuant>); the scales and
+// the root row list are still published here.
+__global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const HyperParams &hp = s.hp;
+    const QCtx c = quant_ctx(s, rd);
+    const bool gs_on = c.gs_on;
+    GossState gst{};
+    if (gs_on) gst = *s.gst;
+    const double gmult = c.gmult;
+    const double gu = c.gu, hu = c.hu;
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
     const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -544,12 +584,9 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s) {
     for (int64_t r0 = (int64_t)blockIdx.x * blockDim.x; r0 < s.n; r0 += stride) {
         const int64_t r = r0 + threadIdx.x;
         const bool valid = r < s.n;
-        if (valid && hp.quantized) {
-            const double gw = gs_on && s.goss_other[r] ? gmult : 1.0;
-            const double gv = (hp.grad64 ? s.grad64[r] : (double)s.grad[r]) * gw;
-            const double hv = (hp.grad64 ? s.hess64[r] : (double)s.hess[r]) * gw;
-            int32_t qg = quantize_scalar(gv, gu, gmax, stoch, gs + (uint64_t)r);
-            int32_t qh = quantize_scalar(hv, hu, hmax, stoch, hs + (uint64_t)r);
+        if (valid && hp.quantized && write_pairs) {
+            int32_t qg, qh;
+            quant_row(s, c, r, qg, qh);
             if (hp.stage16) {
                 // _quantize_grad_hess_i16_kernel: the same integers narrowed,
                 // each plane's misfits counted (a constant hessian's plane is
@@ -1434,11 +1471,16 @@ __device__ __forceinline__ uint32_t group_last_lane(uint32_t x) {
 // the row ids of step i + 2 are in flight. (The memory counter completes in
 // issue order, so a step's ids must be issued a step before its records or
 // waiting for them would also wait for every record load issued earlier.)
-template <int LPR, class Acc, bool kList>
+// kQ (the root build of the max-abs lattice): each row's int8 pair is
+// quantized here from its derivatives (quant_row, the quantizer k_quantize
+// would apply) instead of read from the record, and the row's record is
+// written back with the pair in place, for the expansions' accumulations;
+// rec_w is the record tile being read.
+template <int LPR, class Acc, bool kList, bool kQ = false>
 __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char *lds, const int32_t *rows,
                                                 int64_t lo, int64_t hi, int Ft, const uint4 *rec,
-                                                double goss_mult) {
-    constexpr int U = kHistUnroll;
+                                                double goss_mult, const QCtx *qc = nullptr, uint4 *rec_w = nullptr) {
+    constexpr int U = kQ ? 3 : kHistUnroll;  // rows per lane and step (fewer while quantizing: registers)
     const int ls = s.lds_stride;
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
@@ -1457,17 +1499,58 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
             id[u] = kList ? rows[i] : (int32_t)i;
         }
     };
-    auto load_recs = [&](int64_t, const int32_t *id, uint4 *w) {
+    // kQ: the value this lane quantizes (lane 0 of a row its gradient, lane 1
+    // its hessian; one lane per row takes both) and the rows' GOSS weight
+    // bits, loaded with the records
+    float qv[U], qv2[U], qv_nxt[U], qv2_nxt[U];
+    uint32_t qw = 0u, qw_nxt = 0u;
+    const bool q_goss = kQ && qc->gs_on;
+    auto load_recs = [&](int64_t, const int32_t *id, uint4 *w, float *v, float *v2, uint32_t &wb) {
+        wb = 0u;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t r = (uint32_t)id[u] < n32 ? (uint32_t)id[u] : 0u;  // ids come from the row lists
             w[u] = rec[(size_t)r * LPR + sub];
+            if constexpr (kQ) {
+                v[u] = (LPR == 1 || (sub & 1) == 0) ? s.grad[r] : s.hess[r];
+                if constexpr (LPR == 1) v2[u] = s.hess[r];
+                if (q_goss) wb |= (s.goss_other[r] ? 1u : 0u) << u;
+            }
         }
     };
-    auto accumulate = [&](int64_t i0, const int32_t *id, const uint4 *w) {
+    auto accumulate = [&](int64_t i0, const int32_t *id, const uint4 *w, const float *v, const float *v2,
+                          uint32_t wb) {
         uint32_t gh[U];
+        if constexpr (kQ) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) gh[u] = group_last_lane<LPR>(w[u].w);
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = i0 + (int64_t)u * rpp + rr;
+                const uint32_t r = (uint32_t)id[u] < n32 ? (uint32_t)id[u] : 0u;
+                int32_t qg, qh;
+                const bool wt = (wb >> u) & 1u;
+                if constexpr (LPR == 1) {
+                    qg = quant_value(*qc, v[u], wt, (int64_t)r, true);
+                    qh = quant_value(*qc, v2[u], wt, (int64_t)r, false);
+                } else {
+                    // the row's lane 0 quantizes g, lane 1 h, then both are
+                    // read across the row's lanes
+                    const int q = quant_value(*qc, v[u], wt, (int64_t)r, (sub & 1) == 0);
+                    const int base = (int)lane_id() & ~(LPR - 1);
+                    qg = __shfl(q, base, 64);
+                    qh = __shfl(q, base + 1, 64);
+                }
+                const uint32_t pair = (uint32_t)(uint8_t)(int8_t)qg | ((uint32_t)(uint8_t)(int8_t)qh << 8);
+                uint4 v = w[u];
+                if (sub == LPR - 1) v.w = (v.w & 0xFFFFu) | (pair << 16);
+                // every lane writes its 16 bytes back, so consecutive rows
+                // rewrite whole 128-byte lines (no partial-line update)
+                if (i < hi) rec_w[(size_t)r * LPR + sub] = v;
+                gh[u] = group_last_lane<LPR>(v.w);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) gh[u] = group_last_lane<LPR>(w[u].w);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + (int64_t)u * rpp + rr;
@@ -1478,7 +1561,7 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     uint4 w_cur[U], w_nxt[U];
     int64_t i0 = lo;
     load_ids(i0, id_cur);
-    load_recs(i0, id_cur, w_cur);
+    load_recs(i0, id_cur, w_cur, qv, qv2, qw);
     load_ids(i0 + step, id_nxt);
     // The next step's loads are issued unconditionally (past the range they
     // re-read the last row): under a branch, the compiler's wait for the
@@ -1486,9 +1569,9 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     // no longer overlap the LDS atomics.
     for (;;) {
         const bool more = i0 + step < hi;
-        load_recs(i0 + step, id_nxt, w_nxt);
+        load_recs(i0 + step, id_nxt, w_nxt, qv_nxt, qv2_nxt, qw_nxt);
         load_ids(i0 + 2 * step, id_nn);
-        accumulate(i0, id_cur, w_cur);
+        accumulate(i0, id_cur, w_cur, qv, qv2, qw);
         if (!more) break;
         i0 += step;
 #pragma unroll
@@ -1496,11 +1579,16 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
             id_cur[u] = id_nxt[u];
             id_nxt[u] = id_nn[u];
             w_cur[u] = w_nxt[u];
+            if constexpr (kQ) {
+                qv[u] = qv_nxt[u];
+                if constexpr (LPR == 1) qv2[u] = qv2_nxt[u];
+            }
         }
+        qw = qw_nxt;
     }
 }
 
-template <int LPR, class Acc>
+template <int LPR, class Acc, bool kQ = false>
 __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     extern __shared__ unsigned char lds[];
     if (s.round->stopped) return;
@@ -1518,8 +1606,15 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     Acc::template zero<LPR>(lds, Ft, ls);
     __syncthreads();
     const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
-    if (direct) accumulate_rows<LPR, Acc, false>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
-    else accumulate_rows<LPR, Acc, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
+    if constexpr (kQ) {
+        const QCtx qc = quant_ctx(s, *s.round);
+        uint4 *rec_w = (uint4 *)(s.records_w + (size_t)blockIdx.y * s.n * s.rec_bytes);
+        if (direct) accumulate_rows<LPR, Acc, false, true>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
+        else accumulate_rows<LPR, Acc, true, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
+    } else {
+        if (direct) accumulate_rows<LPR, Acc, false>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
+        else accumulate_rows<LPR, Acc, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
+    }
     __syncthreads();
     Acc::template store<LPR>(s, lds, blockIdx.x, f0, Ft);
 }
@@ -3935,8 +4030,8 @@ hipError_t launch_magnitude(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_magfold, dim3(1), dim3(64), 0, st, s);
     return hipGetLastError();
 }
-hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st) {
-    hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s);
+hipError_t launch_quantize(const DevState &s, int grid, hipStream_t st, bool write_pairs) {
+    hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(256), 0, st, s, write_pairs ? 1 : 0);
     return hipGetLastError();
 }
 size_t score_lds_bytes(const DevState &s) { return (size_t)s.max_nodes * (s.t_cat ? 48 : 16); }
@@ -4014,19 +4109,21 @@ hipError_t launch_timed(K k, dim3 grid, dim3 block, size_t lds, hipStream_t st, 
     else hipLaunchKernelGGL(k, grid, block, lds, st, s);
     return hipGetLastError();
 }
-template <class Acc>
+template <class Acc, bool kQ = false>
 hipError_t launch_hist_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const size_t lds = hist_lds_bytes(s);
     const dim3 grid(s.hist_grid, s.n_tiles), block(kHistThreads);
     switch (s.rec_bytes / 16) {
-    case 1: return launch_timed(k_hist<1, Acc>, grid, block, lds, st, s, ev0, ev1);
-    case 2: return launch_timed(k_hist<2, Acc>, grid, block, lds, st, s, ev0, ev1);
-    case 4: return launch_timed(k_hist<4, Acc>, grid, block, lds, st, s, ev0, ev1);
-    case 8: return launch_timed(k_hist<8, Acc>, grid, block, lds, st, s, ev0, ev1);
+    case 1: return launch_timed(k_hist<1, Acc, kQ>, grid, block, lds, st, s, ev0, ev1);
+    case 2: return launch_timed(k_hist<2, Acc, kQ>, grid, block, lds, st, s, ev0, ev1);
+    case 4: return launch_timed(k_hist<4, Acc, kQ>, grid, block, lds, st, s, ev0, ev1);
+    case 8: return launch_timed(k_hist<8, Acc, kQ>, grid, block, lds, st, s, ev0, ev1);
     default: return hipErrorInvalidValue;
     }
 }
-hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, bool quantize) {
+    if (quantize && s.hp.quantized && !s.hp.wide && !s.hp.stage16 && !s.hp.grad64)
+        return launch_hist_t<QAcc, true>(s, st, ev0, ev1);
     return s.hp.stage16     ? launch_hist_t<WAcc16>(s, st, ev0, ev1)
            : s.hp.wide      ? launch_hist_t<WAcc>(s, st, ev0, ev1)
            : s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1)
