@@ -3273,6 +3273,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     static_assert(kPlanThreads / 64 * kJ == 64, "one wave scans the ballot counts");
     __shared__ int s_wcnt[64], s_pcnt[64];
     __shared__ int s_npend;
+    __shared__ unsigned long long s_keys[kPlanThreads];  // the sort's keys (up to kPlanThreads candidates)
     int myb[kJ], myp[kJ];
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
@@ -3301,17 +3302,78 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
     }
     __syncthreads();
+    // up to kPlanThreads candidates are ranked by a sort of 64-bit keys:
+    // b's bits (a positive double orders like its bits) with the low 13
+    // cleared for 0x1FFF - node id, so that a descending sort puts larger b
+    // first and, among equal truncated b, the lower node id (ne <= 4096)
+    const bool by_sort = s_ncand <= kPlanThreads;
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
         if (myb[k] < 0) continue;
         const int i = tid + k * nthr;
         const int kk = s_wcnt[k * nwaves + wv] + myb[k];
-        v.cb[kk] = jv[k];
-        v.ci[kk] = i | (myp[k] < 0 ? (int)0x80000000 : 0);
-        if (myp[k] >= 0) v.fr[s_pcnt[k * nwaves + wv] + myp[k]] = kk;
+        if (by_sort) {
+            s_keys[kk] = ((unsigned long long)__double_as_longlong(jv[k]) & ~0x1FFFULL) |
+                         (unsigned long long)(0x1FFF - i);
+        } else {
+            v.cb[kk] = jv[k];
+            v.ci[kk] = i | (myp[k] < 0 ? (int)0x80000000 : 0);
+            if (myp[k] >= 0) v.fr[s_pcnt[k * nwaves + wv] + myp[k]] = kk;
+        }
     }
     __syncthreads();
     const int ncand = s_ncand, npend = s_npend;
+    if (by_sort) {
+        // Bitonic sort, descending, one key per thread (tid = position):
+        // partners within a wave by lane shuffles, farther ones through LDS.
+        // A candidate's position is the number of candidates before it; the
+        // pending ones before it, an exclusive count over positions, is its
+        // batch slot. Pending candidates at positions below r with a slot
+        // below cap join the batch.
+        int N = 1;
+        while (N < ncand) N <<= 1;
+        unsigned long long x = tid < ncand ? s_keys[tid] : 0ULL;
+        for (int k = 2; k <= N; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                unsigned long long y;
+                if (j >= 64) {
+                    __syncthreads();  // the previous stage's reads are done
+                    s_keys[tid] = x;
+                    __syncthreads();
+                    y = s_keys[tid ^ j];
+                } else {
+                    const unsigned hi = (unsigned)__shfl_xor((int)(unsigned)(x >> 32), j, 64);
+                    const unsigned lo = (unsigned)__shfl_xor((int)(unsigned)x, j, 64);
+                    y = ((unsigned long long)hi << 32) | lo;
+                }
+                const bool desc = (tid & k) == 0, lower = (tid & j) == 0;
+                x = (lower == desc) ? (x > y ? x : y) : (x < y ? x : y);
+            }
+        }
+        const bool isc = tid < ncand;
+        const int id = isc ? (int)(0x1FFF - (int)(x & 0x1FFFULL)) : 0;
+        const bool pend = isc && v.el[id] < 0;
+        const bool in_r = pend && tid < r;
+        const unsigned long long pm = __ballot(pend), rm = __ballot(in_r);
+        if (lane == 0) {
+            s_wcnt[wv] = __popcll(pm);
+            s_pcnt[wv] = __popcll(rm);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int a = 0, t = 0;
+            for (int w = 0; w < nwaves; ++w) {
+                const int c = s_wcnt[w];
+                s_wcnt[w] = a;
+                a += c;
+                t += s_pcnt[w];
+            }
+            s_nsel = t < cap ? t : cap;  // pending candidates before position r, at most cap
+        }
+        __syncthreads();
+        const int slot = s_wcnt[wv] + (int)__popcll(pm & ((1ULL << lane) - 1ULL));
+        if (in_r && slot < cap) v.sel_e[slot] = id;
+    }
     // A pending candidate joins the batch when fewer than r candidates and
     // fewer than cap pending ones come before it in (b descending, node id
     // ascending) order; its rank among the pending ones is its batch slot.
@@ -3320,7 +3382,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     auto before = [](double bq, int iq, double bk, int ik) -> unsigned {
         return (bq > bk || (bq == bk && iq < ik)) ? 1u : 0u;
     };
-    for (int p = 2 * wv; p < npend; p += 2 * nwaves) {
+    // (more candidates than threads: the same rule by counting, pending
+    // candidate against every candidate)
+    for (int p = 2 * wv; !by_sort && p < npend; p += 2 * nwaves) {
         const bool two = p + 1 < npend;
         const int ka = v.fr[p], kb = v.fr[two ? p + 1 : p];
         const double ba = v.cb[ka], bb = v.cb[kb];
