@@ -86,13 +86,20 @@ __device__ __forceinline__ unsigned dpp_u32(unsigned x) {
 // Max / min of a 32-bit value over the 64 lanes (every lane active),
 // returned wave-uniform: quad swaps, half-row and row mirrors fold each row
 // of 16 lanes, then row broadcasts 15 and 31 fold the rows into lane 63.
+// (The moved value of a lane a control leaves out is 0, the identity of an
+// unsigned maximum, so each step compiles to one v_max_u32 with a DPP
+// source.)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned dpp_max0(unsigned x) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
 __device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
-    x = max(x, dpp_u32<0xB1, 0xF>(x));   // quad_perm [1,0,3,2]
-    x = max(x, dpp_u32<0x4E, 0xF>(x));   // quad_perm [2,3,0,1]
-    x = max(x, dpp_u32<0x141, 0xF>(x));  // row_half_mirror
-    x = max(x, dpp_u32<0x140, 0xF>(x));  // row_mirror
-    x = max(x, dpp_u32<0x142, 0xA>(x));  // row_bcast:15 into rows 1, 3
-    x = max(x, dpp_u32<0x143, 0xC>(x));  // row_bcast:31 into rows 2, 3
+    x = max(x, dpp_max0<0xB1, 0xF>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp_max0<0x4E, 0xF>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp_max0<0x141, 0xF>(x));  // row_half_mirror
+    x = max(x, dpp_max0<0x140, 0xF>(x));  // row_mirror
+    x = max(x, dpp_max0<0x142, 0xA>(x));  // row_bcast:15 into rows 1, 3
+    x = max(x, dpp_max0<0x143, 0xC>(x));  // row_bcast:31 into rows 2, 3
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
@@ -2839,13 +2846,13 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
         lbe = 0;
         lbf = -1;
 #pragma unroll
-        for (int q = 0; q < QS; ++q)
-            if (sg[q] > lbg) {  // ascending slots: strict '>' keeps the lowest
-                lbg = sg[q];
-                lbi = lane + 64 * q;
-                lbe = se[q];
-                lbf = sf[q];
-            }
+        for (int q = 0; q < QS; ++q) {
+            const bool t = sg[q] > lbg;  // ascending slots: strict '>' keeps the lowest
+            lbg = t ? sg[q] : lbg;
+            lbi = t ? lane + 64 * q : lbi;
+            lbe = t ? se[q] : lbe;
+            lbf = t ? sf[q] : lbf;
+        }
         kle = v.el[lbe];
         kgl = v.cb[lbe];
         kgr = v.gr[lbe];
