@@ -462,6 +462,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.scan = dalloc<mb::ScanResult>((size_t)s.kmax * 2 * F, run.owned);
     s.e_gain = dalloc<double>(s.e_cap, run.owned);
     s.e_left = dalloc<int32_t>(s.e_cap, run.owned);
+    s.e_rows = dalloc<int32_t>(s.e_cap, run.owned);
     s.e_parent = dalloc<int32_t>(s.e_cap, run.owned);
     s.cursor = dalloc<int64_t>(2 + 2 * (size_t)s.kmax, run.owned);
     s.error = dalloc<int32_t>(1, run.owned);

@@ -2704,7 +2704,7 @@ struct SelNode {
 
 struct PlanLayout {
     size_t sn, mbin;
-    size_t wg, eg, sg, cb, kr, wf, el, ep, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
+    size_t wg, eg, sg, cb, kr, wf, el, ep, rw, fr, ci, sl_e, sl_fid, cm_e, cm_fid, cm_lf, sel_e, pcnt, poff, qcnt, qoff, it;
     size_t total;
 };
 
@@ -2727,6 +2727,7 @@ __host__ __device__ inline PlanLayout plan_layout(int L, int E, int K, int F) {
     p.wf = take((size_t)4 * 2 * K, 4);       // pair's best feature
     p.el = take((size_t)4 * E, 4);           // explored node's left child
     p.ep = take((size_t)4 * E, 4);           // explored node's parent
+    p.rw = take((size_t)4 * E, 4);           // explored node's rows
     p.sl_e = take((size_t)4 * L, 4);
     p.sl_fid = take((size_t)4 * L, 4);
     p.cm_e = take((size_t)4 * L, 4);
@@ -2748,7 +2749,7 @@ struct PlanView {
     SelNode *sn;
     int32_t *mbin;
     double *wg, *eg, *sg, *cb, *gr;
-    int32_t *wf, *el, *ep, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff, *qcnt, *qoff;
+    int32_t *wf, *el, *ep, *rw, *fr, *ci, *sl_e, *sl_fid, *cm_e, *cm_fid, *cm_lf, *sel_e, *pcnt, *poff, *qcnt, *qoff;
     Item *it;
 };
 
@@ -2763,6 +2764,7 @@ __device__ PlanView plan_view(const DevState &s, unsigned char *smem) {
     v.wf = (int32_t *)(smem + p.wf);
     v.el = (int32_t *)(smem + p.el);
     v.ep = (int32_t *)(smem + p.ep);
+    v.rw = (int32_t *)(smem + p.rw);
     v.fr = (int32_t *)(smem + p.fr);
     v.ci = (int32_t *)(smem + p.ci);
     v.sl_e = (int32_t *)(smem + p.sl_e);
@@ -2989,6 +2991,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         v.eg[i] = s.e_gain[i];
         v.el[i] = s.e_left[i];
         v.ep[i] = s.e_parent[i];
+        v.rw[i] = s.e_rows[i];
     }
     if (!root_mode)
         for (int i = tid; i < nl0; i += nthr) {
@@ -3109,8 +3112,10 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         if (root_mode) {
             v.el[0] = -1;
             v.ep[0] = -1;
+            v.rw[0] = (int32_t)C;
             s.e_left[0] = -1;
             s.e_parent[0] = -1;
+            s.e_rows[0] = (int32_t)C;
         }
     }
     if (root_mode && tid == 0) {
@@ -3219,6 +3224,16 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     int cap = r < s.kmax ? r : s.kmax;
     const int room = (s.max_exp - g.expansions) - (r - 1);
     if (room < cap) cap = room;
+    // A speculative leaf (any but the one the replay waits for) joins the
+    // batch only when its partition and accumulation cost little against
+    // the waited-for leaf's: at most max(n / 2, 2 x its rows) rows. Late in
+    // training a root split often peels off a small high-gain region that
+    // takes every split while its large sibling never splits; expanding that
+    // sibling's subtree ahead doubled the rows a tree partitions and
+    // accumulated. Deferred leaves are expanded when the replay reaches them
+    // (measured on C2: 45M instead of 76M rows partitioned per tree, 22.1
+    // instead of 20.0 iterations, 6 % less time).
+    const int64_t spec_rows = s_x >= 0 ? max((int64_t)(s.n / 2), (int64_t)2 * v.rw[s_x]) : (int64_t)s.n;
     for (int i = tid; i < ne; i += nthr) v.fr[i] = 0;
     __syncthreads();
     for (int i = tid; i < nl; i += nthr) v.fr[v.sl_e[i]] = 1;
@@ -3286,7 +3301,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     for (int k = 0; k < kJ; ++k) {
         const int i = tid + k * nthr;
         const bool c = i < ne && ju[k] == -1 && v.eg[i] > 0.0 && jv[k] > 0.0;
-        const bool pend = c && v.el[i] < 0;
+        const bool pend = c && v.el[i] < 0 && (i == s_x || v.rw[i] <= spec_rows);
         const unsigned long long m = __ballot(c), mp = __ballot(pend);
         const unsigned long long below = (1ULL << lane) - 1ULL;
         myb[k] = c ? (int)__popcll(m & below) : -1;
@@ -3359,7 +3374,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
         const bool isc = tid < ncand;
         const int id = isc ? (int)(0x1FFF - (int)(x & 0x1FFFULL)) : 0;
-        const bool pend = isc && v.el[id] < 0;
+        const bool pend = isc && v.el[id] < 0 && (id == s_x || v.rw[id] <= spec_rows);
         const bool in_r = pend && tid < r;
         const unsigned long long pm = __ballot(pend), rm = __ballot(in_r);
         if (lane == 0) {
@@ -3578,6 +3593,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.e_left[le + 1] = -1;
         s.e_parent[le] = Xs;
         s.e_parent[le + 1] = Xs;
+        s.e_rows[le] = (int32_t)nlft;
+        s.e_rows[le + 1] = (int32_t)(m - nlft);
         e->left_e = le;
         e->right_e = le + 1;
         s.e_left[Xs] = le;

@@ -286,6 +286,7 @@ struct DevState {
     double *e_gain;        // e_cap: best gain when > 0 and found, else -1 (planner's view)
     int32_t *e_left;       // e_cap: left child (right = left + 1), -1 while unexpanded
     int32_t *e_parent;     // e_cap: parent, -1 for the root
+    int32_t *e_rows;       // e_cap: rows of the node (n < 2^31)
     Item *items;           // kmax
     PbDesc *pb_desc;       // part_grid
     AcDesc *ac_desc;       // pb_grid
