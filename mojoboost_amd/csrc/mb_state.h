@@ -126,8 +126,14 @@ struct Round {
 // pass), at least kPartChunkMin (the host sizes the descriptor buffer from
 // it). The planner spreads a batch over about part_target tasks in between,
 // in multiples of kPartChunkStep rows.
-constexpr int kPartChunk = 8192;
-constexpr int kPartChunkMin = 1024;
+#ifndef MB_PART_CHUNK
+#define MB_PART_CHUNK 4096
+#endif
+constexpr int kPartChunk = MB_PART_CHUNK;
+#ifndef MB_PART_CHUNK_MIN
+#define MB_PART_CHUNK_MIN 512
+#endif
+constexpr int kPartChunkMin = MB_PART_CHUNK_MIN;
 constexpr int kPartChunkStep = 256;
 // Root build launch: kHistThreads per block, kHistBlocksPerCU blocks per CU
 // (each with its own LDS histogram).
