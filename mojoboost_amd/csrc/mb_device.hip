@@ -326,7 +326,7 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // chunk_limit); the grid is widened when needed so grid * chunk_limit covers
 // every row. An expansion's accumulation gives each accumulated child of m
 // rows ceil(m / chunk) tasks (block partials) with chunk = clamp(ceil(batch
-// rows / n_cu), chunk_min, chunk_limit); the leaves of a batch are disjoint,
+// rows / (2 n_cu)), chunk_min, chunk_limit); the leaves of a batch are disjoint,
 // so n / chunk_min + (batch size) tasks always suffice. Its partition tasks
 // take at least kPartChunkMin parent rows each (but the last of a leaf),
 // n / kPartChunkMin + (batch size) of them at most, spread over about two
@@ -349,7 +349,7 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
     s.part_grid = (int32_t)((ds->n + mb::kPartChunkMin - 1) / mb::kPartChunkMin + s.kmax);
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
-    s.pb_launch = std::min<int32_t>(s.pb_grid, ds->n_cu);
+    s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);  // two resident accumulation blocks per CU
     s.part_launch = std::min<int32_t>(s.part_grid, 8 * ds->n_cu);
     s.part_target = 2 * ds->n_cu;
     // a root build uses at most ceil(n / chunk_min) chunks

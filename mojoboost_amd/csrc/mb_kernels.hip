@@ -1442,11 +1442,15 @@ using WAcc16 = WAccT<true>;
 // stores it as its partial; the scan kernel merges the partials. A row's
 // record is LPR x 16 bytes: each of the LPR lanes of a row group loads 16
 // bytes (16 features) and the int8 g/h pair (the record's last two bytes)
-// reaches the group by a lane shuffle. Each lane keeps kHistUnroll row loads
-// in flight. blockIdx.y is the feature tile: the block reads that tile's
-// records and stores that tile's features of its partial.
+// reaches the group by a lane shuffle. Each lane takes kHistUnroll rows per
+// step, and with the software pipelining of accumulate_rows (ids two steps
+// ahead, records one step ahead) one row per step already keeps three loads
+// per lane in flight at 50 VGPRs: two 16-wave blocks per CU. (Four rows per
+// step took 92 VGPRs, one block per CU, and accumulated 13 % slower.)
+// blockIdx.y is the feature tile: the block reads that tile's records and
+// stores that tile's features of its partial.
 #ifndef MB_HIST_UNROLL
-#define MB_HIST_UNROLL 4
+#define MB_HIST_UNROLL 1
 #endif
 constexpr int kHistUnroll = MB_HIST_UNROLL;
 
@@ -1777,8 +1781,9 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
 // yields one block partial; the scan kernel merges an item's partials.
 // blockIdx.y is the feature tile: the block reads that tile's records and
 // stores that tile's features of its partial.
+constexpr int kAccThreads = 1024;  // two blocks per CU resident (launch grid 2 x CUs)
 template <int LPR, class Acc>
-__global__ __launch_bounds__(1024) void k_accum(DevState s) {
+__global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
     extern __shared__ unsigned char lds[];
     const int n_acc = s.batch->n_acc;
     const double goss_mult = s.round->goss_mult;
@@ -4227,7 +4232,7 @@ hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, h
 template <class Acc>
 hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const size_t lds = hist_lds_bytes(s);
-    const dim3 grid(s.pb_launch, s.n_tiles), block(1024);
+    const dim3 grid(s.pb_launch, s.n_tiles), block(kAccThreads);
     switch (s.rec_bytes / 16) {
     case 1: return launch_timed(k_accum<1, Acc>, grid, block, lds, st, s, ev0, ev1);
     case 2: return launch_timed(k_accum<2, Acc>, grid, block, lds, st, s, ev0, ev1);
