@@ -1491,7 +1491,7 @@ template <int LPR, class Acc, bool kList, bool kQ = false>
 __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char *lds, const int32_t *rows,
                                                 int64_t lo, int64_t hi, int Ft, const uint4 *rec,
                                                 double goss_mult, const QCtx *qc = nullptr, uint4 *rec_w = nullptr) {
-    constexpr int U = kQ ? 3 : kHistUnroll;  // rows per lane and step (fewer while quantizing: registers)
+    constexpr int U = kQ ? 3 : kHistUnroll;  // rows per lane and step (more while quantizing: its loads)
     const int ls = s.lds_stride;
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
@@ -2813,6 +2813,53 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x)
     return ((unsigned long long)hi << 32) | lo;
 }
 
+// Bitonic sort of 2^LOGN 32-bit keys, descending, one key per thread of a
+// kPlanThreads block (thread = position; threads past 2^LOGN pass through).
+// Fully unrolled, so every exchange distance j is a constant: quad
+// permutations (DPP) for j = 1, 2; a row shift each way and a select for
+// j = 4, 8 (row_shl:j reads lane + j, row_shr:j lane - j, both inside the
+// lane's row of 16); a swizzle within 32 lanes for 16; a crossbar shuffle
+// for 32; through LDS for 64 and more, alternating between two buffers so
+// that each such step takes one barrier (a buffer is rewritten two steps
+// later, after every thread has passed the barrier between).
+template <int LOGN>
+__device__ __forceinline__ unsigned bitonic_desc(unsigned x, unsigned (*keys)[kPlanThreads]) {
+    const int tid = threadIdx.x, lane = lane_id();
+    int buf = 1;
+#pragma unroll
+    for (int lk = 1; lk <= LOGN; ++lk) {
+        const int k = 1 << lk;
+#pragma unroll
+        for (int lj = lk - 1; lj >= 0; --lj) {
+            const int j = 1 << lj;
+            unsigned y;
+            if (j >= 64) {
+                keys[buf][tid] = x;
+                __syncthreads();
+                y = keys[buf][tid ^ j];
+                buf ^= 1;
+            } else if (j == 1) {
+                y = dpp_u32<0xB1, 0xF>(x);  // quad_perm [1,0,3,2]
+            } else if (j == 2) {
+                y = dpp_u32<0x4E, 0xF>(x);  // quad_perm [2,3,0,1]
+            } else if (j == 4) {
+                const unsigned up = dpp_u32<0x104, 0xF>(x), dn = dpp_u32<0x114, 0xF>(x);
+                y = (lane & 4) ? dn : up;
+            } else if (j == 8) {
+                const unsigned up = dpp_u32<0x108, 0xF>(x), dn = dpp_u32<0x118, 0xF>(x);
+                y = (lane & 8) ? dn : up;
+            } else if (j == 16) {
+                y = (unsigned)__builtin_amdgcn_ds_swizzle((int)x, 0x401F);  // and 0x1F, xor 0x10
+            } else {
+                y = (unsigned)__shfl_xor((int)x, 32, 64);
+            }
+            const bool desc = (tid & k) == 0, lower = (tid & j) == 0;
+            x = (lower == desc) ? max(x, y) : min(x, y);
+        }
+    }
+    return x;
+}
+
 __device__ __forceinline__ double readlane_f64(double d, int l) {
     const unsigned long long b = (unsigned long long)__double_as_longlong(d);
     const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
@@ -3159,30 +3206,36 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __syncthreads();
     const int nc = s_nc, nl = g.n_leaves, nn = g.n_nodes;
     // committed splits -> tree arrays
-    for (int c = tid; c < nc; c += nthr) {
-        const ENode *e = &s.enodes[v.cm_e[c]];
-        const int fx = v.cm_fid[c], lf = v.cm_lf[c];
-        const int feat = e->feature;
-        const int le = v.el[v.cm_e[c]];
-        s.t_feature[fx] = feat;
-        s.t_threshold[fx] = e->cat ? -1 : e->bin;
-        s.t_left[fx] = lf;
-        s.t_right[fx] = lf + 1;
-        s.t_default_left[fx] = e->cat ? 0 : e->default_left;
-        // tree._set_split (tree.mojo:462-481): a categorical node has no
-        // threshold and no missing bin, only its set
-        s.t_missing_bin[fx] = e->cat ? -1 : v.mbin[feat];
-        if (s.t_cat) {
+    auto write_commits = [&]() {
+        for (int c = tid; c < nc; c += nthr) {
+            const ENode *e = &s.enodes[v.cm_e[c]];
+            const int fx = v.cm_fid[c], lf = v.cm_lf[c];
+            const int le = v.el[v.cm_e[c]];
+            // every load first, then the stores
+            const int feat = e->feature, ecat = e->cat, ebin = e->bin, edl = e->default_left;
+            const double egain = e->gain;
+            const double v0 = s.enodes[le].value, v1 = s.enodes[le + 1].value;
+            const int64_t c0 = s.enodes[le].tot_c, c1 = s.enodes[le + 1].tot_c;
+            s.t_feature[fx] = feat;
+            s.t_threshold[fx] = ecat ? -1 : ebin;
+            s.t_left[fx] = lf;
+            s.t_right[fx] = lf + 1;
+            s.t_default_left[fx] = ecat ? 0 : edl;
+            // tree._set_split (tree.mojo:462-481): a categorical node has no
+            // threshold and no missing bin, only its set
+            s.t_missing_bin[fx] = ecat ? -1 : v.mbin[feat];
+            if (s.t_cat) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
-                s.t_cat[(size_t)fx * 4 + w] = e->cat ? s.e_cat[(size_t)v.cm_e[c] * 4 + w] : 0ULL;
+                for (int w = 0; w < 4; ++w)
+                    s.t_cat[(size_t)fx * 4 + w] = ecat ? s.e_cat[(size_t)v.cm_e[c] * 4 + w] : 0ULL;
+            }
+            s.t_gain[fx] = egain;
+            s.t_value[lf] = v0;
+            s.t_count[lf] = (double)c0;
+            s.t_value[lf + 1] = v1;
+            s.t_count[lf + 1] = (double)c1;
         }
-        s.t_gain[fx] = e->gain;
-        s.t_value[lf] = s.enodes[le].value;
-        s.t_count[lf] = (double)s.enodes[le].tot_c;
-        s.t_value[lf + 1] = s.enodes[le + 1].value;
-        s.t_count[lf + 1] = (double)s.enodes[le + 1].tot_c;
-    }
+    };
     auto finish = [&](int err_code) {
         if (tid == 0) {
             if (err_code) atomicOr(s.error, err_code);
@@ -3200,6 +3253,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
     };
     if (s_done) {
+        write_commits();
         for (int i = tid; i < nl; i += nthr) {
             const int fid = v.sl_fid[i];
             s.t_feature[fid] = -1;
@@ -3304,7 +3358,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     static_assert(kPlanThreads / 64 * kJ == 64, "one wave scans the ballot counts");
     __shared__ int s_wcnt[64], s_pcnt[64];
     __shared__ int s_npend;
-    __shared__ unsigned long long s_keys[kPlanThreads];  // the sort's keys (up to kPlanThreads candidates)
+    __shared__ unsigned s_keys[2][kPlanThreads];  // the sort's keys (up to kPlanThreads candidates), two buffers
     int myb[kJ], myp[kJ];
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
@@ -3333,10 +3387,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
     }
     __syncthreads();
-    // up to kPlanThreads candidates are ranked by a sort of 64-bit keys:
-    // b's bits (a positive double orders like its bits) with the low 13
-    // cleared for 0x1FFF - node id, so that a descending sort puts larger b
-    // first and, among equal truncated b, the lower node id (ne <= 4096)
+    // up to kPlanThreads candidates are ranked by a sort of 32-bit keys:
+    // b rounded to binary32 (a positive float orders like its bits; the
+    // rounding is monotone) with the low 12 bits replaced by 0xFFF - node id
+    // (ne <= 4096), so that a descending sort puts larger b first and, among
+    // b equal to 11 mantissa bits, the lower node id. Keys are at least
+    // 0x1000, above the padding 0. The order only steers which leaves are
+    // expanded ahead, never the tree.
     const bool by_sort = s_ncand <= kPlanThreads;
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
@@ -3344,8 +3401,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const int i = tid + k * nthr;
         const int kk = s_wcnt[k * nwaves + wv] + myb[k];
         if (by_sort) {
-            s_keys[kk] = ((unsigned long long)__double_as_longlong(jv[k]) & ~0x1FFFULL) |
-                         (unsigned long long)(0x1FFF - i);
+            const unsigned fb = __float_as_uint((float)jv[k]) & ~0xFFFu;
+            s_keys[0][kk] = (fb > 0x1000u ? fb : 0x1000u) | (unsigned)(0xFFF - i);
         } else {
             v.cb[kk] = jv[k];
             v.ci[kk] = i | (myp[k] < 0 ? (int)0x80000000 : 0);
@@ -3361,28 +3418,25 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         // pending ones before it, an exclusive count over positions, is its
         // batch slot. Pending candidates at positions below r with a slot
         // below cap join the batch.
-        int N = 1;
-        while (N < ncand) N <<= 1;
-        unsigned long long x = tid < ncand ? s_keys[tid] : 0ULL;
-        for (int k = 2; k <= N; k <<= 1) {
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                unsigned long long y;
-                if (j >= 64) {
-                    __syncthreads();  // the previous stage's reads are done
-                    s_keys[tid] = x;
-                    __syncthreads();
-                    y = s_keys[tid ^ j];
-                } else {
-                    const unsigned hi = (unsigned)__shfl_xor((int)(unsigned)(x >> 32), j, 64);
-                    const unsigned lo = (unsigned)__shfl_xor((int)(unsigned)x, j, 64);
-                    y = ((unsigned long long)hi << 32) | lo;
-                }
-                const bool desc = (tid & k) == 0, lower = (tid & j) == 0;
-                x = (lower == desc) ? (x > y ? x : y) : (x < y ? x : y);
-            }
+        int lg = 0;
+        while ((1 << lg) < ncand) ++lg;
+        unsigned x = tid < ncand ? s_keys[0][tid] : 0u;
+        static_assert(kPlanThreads == 1024, "sorts of up to 2^10 keys");
+        switch (lg) {  // block-uniform
+        case 1: x = bitonic_desc<1>(x, s_keys); break;
+        case 2: x = bitonic_desc<2>(x, s_keys); break;
+        case 3: x = bitonic_desc<3>(x, s_keys); break;
+        case 4: x = bitonic_desc<4>(x, s_keys); break;
+        case 5: x = bitonic_desc<5>(x, s_keys); break;
+        case 6: x = bitonic_desc<6>(x, s_keys); break;
+        case 7: x = bitonic_desc<7>(x, s_keys); break;
+        case 8: x = bitonic_desc<8>(x, s_keys); break;
+        case 9: x = bitonic_desc<9>(x, s_keys); break;
+        case 10: x = bitonic_desc<10>(x, s_keys); break;
+        default: break;  // one candidate
         }
         const bool isc = tid < ncand;
-        const int id = isc ? (int)(0x1FFF - (int)(x & 0x1FFFULL)) : 0;
+        const int id = isc ? (int)(0xFFF - (int)(x & 0xFFFu)) : 0;
         const bool pend = isc && v.el[id] < 0 && (id == s_x || v.rw[id] <= spec_rows);
         const bool in_r = pend && tid < r;
         const unsigned long long pm = __ballot(pend), rm = __ballot(in_r);
@@ -3489,22 +3543,26 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // n / hist_chunk_min + nsel of them). Partition: the batch's parent rows
     // spread over about part_target tasks (one output reservation each),
     // kPartChunkMin to kPartChunk rows each.
-    // the selected leaves' nodes, one memory round trip
-    if (tid < nsel) {
-        const ENode *e = &s.enodes[v.sel_e[tid]];
+    // the selected leaves' nodes and the committed splits' tree entries, one
+    // memory round trip for both
+    {
         SelNode sn;
-        sn.begin = e->begin;
-        sn.end = e->end;
-        sn.n_left = e->n_left;
-        sn.buf = e->buf;
-        sn.hist = e->hist;
-        sn.depth = e->depth;
-        sn.feature = e->feature;
-        sn.bin = e->bin;
-        sn.default_left = e->default_left;
-        sn.cat = e->cat;
-        sn.pad_ = 0;
-        v.sn[tid] = sn;
+        if (tid < nsel) {
+            const ENode *e = &s.enodes[v.sel_e[tid]];
+            sn.begin = e->begin;
+            sn.end = e->end;
+            sn.n_left = e->n_left;
+            sn.buf = e->buf;
+            sn.hist = e->hist;
+            sn.depth = e->depth;
+            sn.feature = e->feature;
+            sn.bin = e->bin;
+            sn.default_left = e->default_left;
+            sn.cat = e->cat;
+            sn.pad_ = 0;
+        }
+        write_commits();
+        if (tid < nsel) v.sn[tid] = sn;
     }
     __syncthreads();
     if (tid < 64) {  // wave 0: totals, chunks, task counts and their prefixes (nsel <= kmax <= 64)
