@@ -2229,6 +2229,7 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                 rs.tot_c = TC;
                 const size_t ri = (size_t)(j * 2 + child) * F + f;
                 s.scan[ri] = rs;
+                s.scan_gain[ri] = rs.found ? rs.gain : -1.0;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) s.scan_cat[ri * 4 + w] = bits[w];
             }
@@ -2256,6 +2257,7 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
             rs.tot_c = TC;
             rs.n_left = rs.found ? bleft : 0;
             s.scan[(size_t)(j * 2 + child) * F + f] = rs;
+            s.scan_gain[(size_t)(j * 2 + child) * F + f] = rs.found ? rs.gain : -1.0;
         }
         __syncthreads();
     }
@@ -2671,6 +2673,7 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
             rs.fh = s_sh[child];
             const size_t ri = (size_t)(j * 2 + child) * F + f;
             s.scan[ri] = rs;
+            s.scan_gain[ri] = rs.found ? rs.gain : -1.0;
             if (ncf > 0)
                 for (int w = 0; w < 4; ++w) s.scan_cat[ri * 4 + w] = cbits[w];
         }
@@ -2995,10 +2998,14 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
     const int L = s.hp.num_leaves, F = s.n_features;
     const HyperParams &hp = s.hp;
+    // the batch size, the round and the growth counters in one memory round
+    // trip (every thread reads the counters itself, a broadcast load, instead
+    // of waiting at a barrier for one thread's copy)
     const int n_items = root_mode ? 1 : s.batch->n_items;
+    const Round rd = *s.round;
+    const int ne = root_mode ? 1 : s.grow->n_explored, nl0 = root_mode ? 1 : s.grow->n_leaves;
     if (n_items <= 0) return;  // the tree is complete
     PlanView v = plan_view(s, plan_smem);
-    const Round rd = *s.round;
     if (rd.stopped) {
         // training has stopped: an empty tree, nothing to expand
         if (tid == 0) {
@@ -3032,17 +3039,31 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s_rows_built = 0;
         s_rows_parted = 0;
         s_ncand = 0;
-        int vf = 0;
-        while (vf < F - 1 && !s.feature_mask[(size_t)rd.tree_index * F + vf]) ++vf;
-        s_vf = vf;
     }
-    // ---- 1. fold (one wave per pair over the pair's per-feature results)
+    // ---- 1. fold (one wave per pair over the pair's per-feature results).
+    // The fold's gains, the items, the explored nodes and the frontier are
+    // all loaded in one memory round trip, the gains first.
     const int n_pairs = root_mode ? 1 : 2 * n_items;
+    // The fold reads the dense gains (scan_gain: the gain of a found split,
+    // else -1), 8 bytes per (pair, feature): the planner's one CU moves a
+    // few lines per wave load instead of a line per lane. Every load
+    // unconditional (a branch between dependent loads would cost a memory
+    // round trip each): when F <= 64 wave w takes pairs w + 16 k, k < kPW,
+    // lane = feature; the argmax keeps the lowest feature on equal gains.
+    constexpr int kPW = 8;
+    static_assert(kPlanThreads / 64 * kPW >= 2 * 64, "every pair of a batch in one pass");
+    double gq[kPW];
+    if (F <= 64) {
+#pragma unroll
+        for (int k = 0; k < kPW; ++k) {
+            int pr = wv + k * nwaves;
+            pr = pr < n_pairs ? pr : 0;
+            gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+        }
+    }
     if (!root_mode)
         for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
     for (int f = tid; f < F; f += nthr) v.mbin[f] = s.missing_bin[f];
-    __syncthreads();
-    const int ne = g.n_explored, nl0 = g.n_leaves;
     for (int i = tid; i < ne; i += nthr) {
         v.eg[i] = s.e_gain[i];
         v.el[i] = s.e_left[i];
@@ -3054,33 +3075,31 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             v.sl_e[i] = s.slot_e[i];
             v.sl_fid[i] = s.slot_fid[i];
         }
-    // every load unconditional (a branch between dependent loads would cost a
-    // memory round trip each): a wave takes kPW pairs at once when F <= 64,
-    // lane = feature; the argmax keeps the lowest feature on equal gains
-    constexpr int kPW = 4;
-    if (F <= 64) {
-        for (int pr0 = wv; pr0 < n_pairs; pr0 += nwaves * kPW) {
-            double gq[kPW];
-            int fq[kPW];
-#pragma unroll
-            for (int k = 0; k < kPW; ++k) {
-                int pr = pr0 + k * nwaves;
-                pr = pr < n_pairs ? pr : pr0;
-                const ScanResult &sr = s.scan[(size_t)pr * F + (lane < F ? lane : 0)];
-                gq[k] = sr.gain;
-                fq[k] = sr.found;
+    if (tid < 64) {
+        // the tree's first selected feature (the fp32 path's leaf value sums)
+        int vf = F - 1;
+        for (int f0 = 0; f0 < F; f0 += 64) {
+            const unsigned long long m =
+                __ballot(f0 + lane < F && s.feature_mask[(size_t)rd.tree_index * F + f0 + lane]);
+            if (m) {
+                vf = f0 + (int)__builtin_ctzll(m);
+                break;
             }
+        }
+        if (lane == 0) s_vf = vf;
+    }
+    if (F <= 64) {
 #pragma unroll
-            for (int k = 0; k < kPW; ++k) {
-                const int pr = pr0 + k * nwaves;
-                double bg = (lane < F && fq[k]) ? gq[k] : 0.0;
-                int bf = (lane < F && fq[k] && gq[k] > 0.0) ? lane : 0x7FFFFFFF;
-                if (bf == 0x7FFFFFFF) bg = 0.0;
-                wave_argmax_lex(bg, bf);
-                if (lane == 0 && pr < n_pairs) {
-                    v.wg[pr] = bg;
-                    v.wf[pr] = bf;
-                }
+        for (int k = 0; k < kPW; ++k) {
+            const int pr = wv + k * nwaves;
+            if (pr >= n_pairs) break;  // wave-uniform
+            const bool ok = lane < F && gq[k] > 0.0;
+            double bg = ok ? gq[k] : 0.0;
+            int bf = ok ? lane : 0x7FFFFFFF;
+            wave_argmax_lex(bg, bf);
+            if (lane == 0) {
+                v.wg[pr] = bg;
+                v.wf[pr] = bf;
             }
         }
     } else {
@@ -3088,10 +3107,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             double bg = 0.0;
             int bf = 0x7FFFFFFF;
             for (int ff = lane; ff < F; ff += 64) {
-                const ScanResult &sr = s.scan[(size_t)pr * F + ff];
-                const double gv = sr.gain;
-                const int fv = sr.found;
-                const double q = fv ? gv : -1.0;
+                const double q = s.scan_gain[(size_t)pr * F + ff];
                 if (q > bg) {
                     bg = q;
                     bf = ff;

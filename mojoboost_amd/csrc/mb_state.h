@@ -301,6 +301,7 @@ struct DevState {
     int32_t *slot_e;       // num_leaves: explored node of each frontier slot
     int32_t *slot_fid;     // num_leaves: its node id in the committed tree
     ScanResult *scan;      // kmax x 2 x F
+    double *scan_gain;     // kmax x 2 x F: a result's gain when found, else -1 (all the planner's fold reads)
     unsigned long long *scan_cat;  // kmax x 2 x F x 4: a categorical result's left set
     unsigned long long *e_cat;     // e_cap x 4: an explored node's categorical left set
     int64_t *cursor;       // [0] root bag size; [2 + 2j], [3 + 2j]: item j's output cursors
