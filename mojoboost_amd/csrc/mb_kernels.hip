@@ -1442,17 +1442,17 @@ using WAcc16 = WAccT<true>;
 // stores it as its partial; the scan kernel merges the partials. A row's
 // record is LPR x 16 bytes: each of the LPR lanes of a row group loads 16
 // bytes (16 features) and the int8 g/h pair (the record's last two bytes)
-// reaches the group by a lane shuffle. Each lane takes kHistUnroll rows per
-// step, and with the software pipelining of accumulate_rows (ids two steps
-// ahead, records one step ahead) one row per step already keeps three loads
-// per lane in flight at 50 VGPRs: two 16-wave blocks per CU. (Four rows per
-// step took 92 VGPRs, one block per CU, and accumulated 13 % slower.)
-// blockIdx.y is the feature tile: the block reads that tile's records and
-// stores that tile's features of its partial.
-#ifndef MB_HIST_UNROLL
-#define MB_HIST_UNROLL 1
-#endif
-constexpr int kHistUnroll = MB_HIST_UNROLL;
+// reaches the group by a lane shuffle. Each lane takes U rows per step.
+// The root build (one pass over every row, 1024-thread blocks, one per CU)
+// keeps 4 rows per step in flight (3 while it also quantizes: its extra
+// loads). An expansion's accumulation takes 1: with the software pipelining
+// of accumulate_rows (ids two steps ahead, records one step ahead) that is
+// three loads per lane in flight at 50 VGPRs, so two 16-wave blocks fit a CU
+// (4 rows per step took 92 VGPRs, one block per CU, and accumulated 13 %
+// slower on C2). blockIdx.y is the feature tile: the block reads that
+// tile's records and stores that tile's features of its partial.
+constexpr int kRootUnroll = 4;
+constexpr int kAccUnroll = 1;
 
 // The value of the last lane of each LPR-lane group, on every lane of the
 // group, by DPP (a VALU operand modifier): unlike a crossbar shuffle it does
@@ -1487,11 +1487,10 @@ __device__ __forceinline__ uint32_t group_last_lane(uint32_t x) {
 // would apply) instead of read from the record, and the row's record is
 // written back with the pair in place, for the expansions' accumulations;
 // rec_w is the record tile being read.
-template <int LPR, class Acc, bool kList, bool kQ = false>
+template <int LPR, class Acc, bool kList, bool kQ, int U>
 __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char *lds, const int32_t *rows,
                                                 int64_t lo, int64_t hi, int Ft, const uint4 *rec,
                                                 double goss_mult, const QCtx *qc = nullptr, uint4 *rec_w = nullptr) {
-    constexpr int U = kQ ? 3 : kHistUnroll;  // rows per lane and step (more while quantizing: its loads)
     const int ls = s.lds_stride;
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
@@ -1620,11 +1619,11 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
     if constexpr (kQ) {
         const QCtx qc = quant_ctx(s, *s.round);
         uint4 *rec_w = (uint4 *)(s.records_w + (size_t)blockIdx.y * s.n * s.rec_bytes);
-        if (direct) accumulate_rows<LPR, Acc, false, true>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
-        else accumulate_rows<LPR, Acc, true, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
+        if (direct) accumulate_rows<LPR, Acc, false, true, 3>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
+        else accumulate_rows<LPR, Acc, true, true, 3>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
     } else {
-        if (direct) accumulate_rows<LPR, Acc, false>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
-        else accumulate_rows<LPR, Acc, true>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
+        if (direct) accumulate_rows<LPR, Acc, false, false, kRootUnroll>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
+        else accumulate_rows<LPR, Acc, true, false, kRootUnroll>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
     }
     __syncthreads();
     Acc::template store<LPR>(s, lds, blockIdx.x, f0, Ft);
@@ -1795,7 +1794,8 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
         const AcDesc d = s.ac_desc[blk];
         Acc::template zero<LPR>(lds, Ft, ls);
         __syncthreads();
-        accumulate_rows<LPR, Acc, true>(s, lds, d.buf ? s.rows1 : s.rows0, d.lo, d.hi, Ft, rec, goss_mult);
+        accumulate_rows<LPR, Acc, true, false, kAccUnroll>(s, lds, d.buf ? s.rows1 : s.rows0, d.lo, d.hi, Ft, rec,
+                                                           goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
