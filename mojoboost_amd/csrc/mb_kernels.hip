@@ -2276,6 +2276,211 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
 // their fp64 sums.
 // kCat as in k_scan; without categorical features at most 128 VGPRs (two
 // blocks per CU), with them uncapped (the category search would spill).
+// k_scan for narrow histograms (at most 64 bins per feature) without
+// categorical features: a block takes kNarrowFeat features of one leaf, so
+// that every thread has a bin. The merge maps thread -> (feature, half,
+// bin); the scan gives one wave to each (feature, child), lane = bin, so a
+// child's prefix sums are one wave scan and its best split one wave argmax,
+// with no block barrier. Candidates, guards and tie rules are k_scan's.
+constexpr int kNarrowFeat = kScanThreads / 128;
+__global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int root_mode) {
+    __shared__ int acc[kNarrowFeat][3][64];
+    __shared__ int cv[kNarrowFeat][2][3][64];  // (g, h, c) of the accumulated child (0) and the sibling (1)
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
+    const HyperParams &hp = s.hp;
+    const int F = s.n_features, nb = s.n_bins;
+    const size_t hsz = (size_t)F * nb * 3;
+    const int n_items = root_mode ? 1 : s.batch->n_items;
+    const int n_groups = (F + kNarrowFeat - 1) / kNarrowFeat;
+    const int n_tasks = n_items * n_groups;
+    if ((int)blockIdx.x >= n_tasks) return;
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const double gu = rd.grad_units, hu = rd.hess_units;
+    const double l1 = hp.lambda_l1, l2 = hp.lambda_l2;
+    long long hmin = 0;  // hessian_units_at_least: min_sum_hessian in lattice units, rounded up
+    if (hp.min_sum_hessian > 0.0) {
+        const double u = hp.min_sum_hessian * hu;
+        double fl = floor(u);
+        if (fl < u) fl += 1.0;
+        hmin = (long long)fl;
+    }
+    for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
+        const int j = task / n_groups;
+        const int f0 = (task - j * n_groups) * kNarrowFeat;
+        Item it;
+        int64_t m_built, m_sib;
+        if (root_mode) {
+            m_built = root_rows(s);
+            m_sib = 0;
+            it.part_off = 0;
+            const int64_t chk = hist_chunk(s, m_built);
+            it.part_cnt = m_built > 0 ? (int)((m_built + chk - 1) / chk) : 0;
+            it.hist_built = 0;
+            it.hist_sib = 0;
+            it.depth_child = 0;
+        } else {
+            it = s.items[j];
+            const int64_t m = it.end - it.begin;
+            m_built = it.builds_left ? it.n_left : m - it.n_left;
+            m_sib = m - m_built;
+        }
+        // ---- merge the accumulated child's partials: thread -> (feature, half, bin)
+        {
+            const int q = tid >> 7, half = (tid >> 6) & 1, bin = lane;
+            const int f = f0 + q;
+            int g = 0, h = 0, c = 0;
+            if (f < F && bin < nb) {
+                const size_t pstride = (size_t)F * s.part_stride;
+                const unsigned long long *p =
+                    s.part + (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
+                const int np = it.part_cnt;
+                int b = half;
+                if (hp.wide) {
+                    const uint32_t *pc =
+                        s.part_c + (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
+                    uint32_t ug = 0u, uh = 0u, uc = 0u;
+                    for (; b < np; b += 2) {
+                        const unsigned long long vv = p[(size_t)b * pstride];
+                        ug += (uint32_t)(vv >> 32);
+                        uh += (uint32_t)vv;
+                        uc += pc[(size_t)b * pstride];
+                    }
+                    g = (int)ug;
+                    h = (int)uh;
+                    c = (int)uc;
+                } else {
+                    for (; b + 14 < np; b += 16) {
+                        unsigned long long vv[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) vv[u] = p[(size_t)(b + 2 * u) * pstride];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            c += (int)(vv[u] & 0xFFFFFULL);
+                            h += (int)((vv[u] >> 20) & 0x3FFFFFULL);
+                            g += (int)((long long)vv[u] >> 42);
+                        }
+                    }
+                    for (; b < np; b += 2) {
+                        const unsigned long long vv = p[(size_t)b * pstride];
+                        c += (int)(vv & 0xFFFFFULL);
+                        h += (int)((vv >> 20) & 0x3FFFFFULL);
+                        g += (int)((long long)vv >> 42);
+                    }
+                }
+            }
+            if (half == 1) {
+                acc[q][0][bin] = g;
+                acc[q][1][bin] = h;
+                acc[q][2][bin] = c;
+            }
+            __syncthreads();
+            if (half == 0) {
+                g += acc[q][0][bin];
+                h += acc[q][1][bin];
+                c += acc[q][2][bin];
+                cv[q][0][0][bin] = g;
+                cv[q][0][1][bin] = h;
+                cv[q][0][2][bin] = c;
+                int sgv = 0, shv = 0, scv = 0;
+                if (f < F && bin < nb) {
+                    int32_t *ob = s.hist + (size_t)it.hist_built * hsz + ((size_t)f * nb + bin) * 3;
+                    ob[0] = g;
+                    ob[1] = h;
+                    ob[2] = c;
+                    if (!root_mode) {
+                        int32_t *pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
+                        sgv = pp[0] - g;
+                        shv = pp[1] - h;
+                        scv = pp[2] - c;
+                        pp[0] = sgv;
+                        pp[1] = shv;
+                        pp[2] = scv;
+                    }
+                }
+                cv[q][1][0][bin] = sgv;
+                cv[q][1][1][bin] = shv;
+                cv[q][1][2][bin] = scv;
+            }
+            __syncthreads();
+        }
+        // ---- scan: wave -> (feature, child), lane = bin
+        const int q = wv >> 1, child = wv & 1, bin = lane;
+        const int f = f0 + q;
+        if (f < F && !(root_mode && child == 1)) {  // wave-uniform
+            const int vg = cv[q][child][0][bin], vh = cv[q][child][1][bin], vc = cv[q][child][2][bin];
+            const int lg = wave_incl_scan_i(vg), lh = wave_incl_scan_i(vh), lc = wave_incl_scan_i(vc);
+            const int TG = __builtin_amdgcn_readlane(lg, 63), TH = __builtin_amdgcn_readlane(lh, 63),
+                      TC = __builtin_amdgcn_readlane(lc, 63);
+            const int64_t n_child = child == 0 ? m_built : m_sib;
+            const int mbf = s.missing_bin[f];
+            const bool gated = (hp.max_depth > 0 && it.depth_child >= hp.max_depth) ||
+                               n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
+                               !s.feature_mask[(size_t)rd.tree_index * F + f];
+            double best_gain = 0.0;
+            int best_order = 0x7FFFFFFF;
+            int best_left = 0;
+            if (!gated) {
+                const int mg = mbf >= 0 ? cv[q][child][0][mbf] : 0, mh = mbf >= 0 ? cv[q][child][1][mbf] : 0,
+                          mc = mbf >= 0 ? cv[q][child][2][mbf] : 0;
+                const long long min_c = hp.min_data_in_leaf;
+                const int n_scan = mbf >= 0 ? mbf : nb;
+                int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
+                if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
+                if (bin < lim) {
+                    const double parent = qscore(TG, TH, gu, hu, l1, l2);
+                    if (mbf >= 0) {
+                        const int ag = lg + mg, ah = lh + mh, ac = lc + mc;
+                        const int rg = TG - ag, rh = TH - ah, rc = TC - ac;
+                        if (!(ah < hmin || rh < hmin || ac < min_c || rc < min_c)) {
+                            const double gain =
+                                qscore(ag, ah, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                            if (gain > best_gain) {
+                                best_gain = gain;
+                                best_order = 2 * bin;
+                                best_left = ac;
+                            }
+                        }
+                    }
+                    if (mbf < 0 || mc > 0) {
+                        const int rg = TG - lg, rh = TH - lh, rc = TC - lc;
+                        if (!(lh < hmin || rh < hmin || lc < min_c || rc < min_c)) {
+                            const double gain =
+                                qscore(lg, lh, gu, hu, l1, l2) + qscore(rg, rh, gu, hu, l1, l2) - parent;
+                            if (gain > best_gain) {
+                                best_gain = gain;
+                                best_order = 2 * bin + 1;
+                                best_left = lc;
+                            }
+                        }
+                    }
+                }
+            }
+            const int mine = best_order;
+            wave_argmax(best_gain, best_order);
+            const unsigned long long wins = __ballot(mine == best_order && best_order != 0x7FFFFFFF);
+            const int srcl = wins ? (int)__ffsll((long long)wins) - 1 : 0;
+            best_left = __shfl(best_left, srcl, 64);
+            if (lane == 0) {
+                ScanResult rs;
+                rs.gain = best_gain;
+                rs.found = best_order != 0x7FFFFFFF;
+                rs.bin = rs.found ? best_order >> 1 : -1;
+                rs.default_left = rs.found ? ((best_order & 1) == 0) : 0;
+                rs.cat = 0;
+                rs.tot_g = TG;
+                rs.tot_h = TH;
+                rs.tot_c = TC;
+                rs.n_left = rs.found ? best_left : 0;
+                const size_t ri = (size_t)(j * 2 + child) * F + f;
+                s.scan[ri] = rs;
+                s.scan_gain[ri] = rs.found ? rs.gain : -1.0;
+            }
+        }
+        __syncthreads();  // the LDS tiles are rewritten by the next task
+    }
+}
+
 template <bool kCat>
 __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState s, int root_mode) {
     __shared__ double cg[2][256], ch[2][256];
@@ -4322,6 +4527,12 @@ hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEv
                             : launch_accum_t<FAcc>(s, st, ev0, ev1);
 }
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
+    if (s.hp.quantized && !s.ncat && s.n_bins <= 64) {
+        const int groups = (s.n_features + kNarrowFeat - 1) / kNarrowFeat;
+        const int grid = root_mode ? groups : std::min(s.scan_grid, s.kmax * groups);
+        hipLaunchKernelGGL(k_scan_narrow, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
+        return hipGetLastError();
+    }
     const int grid = root_mode ? s.n_features : s.scan_grid;
     if (s.hp.quantized && s.ncat)
         hipLaunchKernelGGL(k_scan<true>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
