@@ -1817,14 +1817,24 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
 // ScanResult per child; the planner folds them.
 constexpr int kScanThreads = 512;
 
+// Inclusive prefix sum of a 32-bit value across the 64 lanes, by DPP
+// (GPUOpen's cross-lane scan): row shifts 1, 2, 3 sum each lane's four-lane
+// window, shifts 4 and 8 (lanes of the upper banks only) complete each row
+// of 16, and row broadcasts 15 and 31 carry the rows' totals upward. A lane
+// a control leaves out adds 0. No LDS crossbar round trip.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ int dpp_add0(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, BANK_MASK, true);
+}
 __device__ __forceinline__ int wave_incl_scan_i(int v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(v, d, 64);
-        if (lane >= d) v += t;
-    }
-    return v;
+    int t = v + dpp_add0<0x111, 0xF, 0xF>(v);  // row_shr:1
+    t += dpp_add0<0x112, 0xF, 0xF>(v);         // row_shr:2
+    t += dpp_add0<0x113, 0xF, 0xF>(v);         // row_shr:3
+    t += dpp_add0<0x114, 0xF, 0xE>(t);         // row_shr:4, lanes 4-15 of each row
+    t += dpp_add0<0x118, 0xF, 0xC>(t);         // row_shr:8, lanes 8-15 of each row
+    t += dpp_add0<0x142, 0xA, 0xF>(t);         // row_bcast:15 into rows 1 and 3
+    t += dpp_add0<0x143, 0xC, 0xF>(t);         // row_bcast:31 into rows 2 and 3
+    return t;
 }
 
 // kCat: the dataset has categorical features (the category-set search is
