@@ -57,12 +57,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ long long wave_sum_ll(long long v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
-
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ __forceinline__ long long wave_incl_scan(long long v) {
     const int lane = lane_id();
@@ -136,6 +130,26 @@ __device__ __forceinline__ unsigned wave_add_u32(unsigned x) {
     x += dpp0_u32<0x142, 0xA>(x);
     x += dpp0_u32<0x143, 0xC>(x);
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// Inclusive prefix sum of a 32-bit value across the 64 lanes, by DPP
+// (GPUOpen's cross-lane scan): row shifts 1, 2, 3 sum each lane's four-lane
+// window, shifts 4 and 8 (lanes of the upper banks only) complete each row
+// of 16, and row broadcasts 15 and 31 carry the rows' totals upward. A lane
+// a control leaves out adds 0. No LDS crossbar round trip.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ int dpp_add0(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, BANK_MASK, true);
+}
+__device__ __forceinline__ int wave_incl_scan_i(int v) {
+    int t = v + dpp_add0<0x111, 0xF, 0xF>(v);  // row_shr:1
+    t += dpp_add0<0x112, 0xF, 0xF>(v);         // row_shr:2
+    t += dpp_add0<0x113, 0xF, 0xF>(v);         // row_shr:3
+    t += dpp_add0<0x114, 0xF, 0xE>(t);         // row_shr:4, lanes 4-15 of each row
+    t += dpp_add0<0x118, 0xF, 0xC>(t);         // row_shr:8, lanes 8-15 of each row
+    t += dpp_add0<0x142, 0xA, 0xF>(t);         // row_bcast:15 into rows 1 and 3
+    t += dpp_add0<0x143, 0xC, 0xF>(t);         // row_bcast:31 into rows 2 and 3
+    return t;
 }
 
 // (gain, order) argmax across the wave, result on every lane: larger gain
@@ -1729,7 +1743,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
             int *c = w < SW ? cnt_l : cnt_r;
             const int k = (w % SW) * 64 + lane;
             const int v = k < E ? c[k] : 0;
-            const int inc = (int)wave_incl_scan((long long)v);
+            const int inc = wave_incl_scan_i(v);
             if (k < E) c[k] = inc - v;
             if (lane == 63) wtot[w / SW][w % SW] = inc;
         }
@@ -1817,25 +1831,6 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
 // ScanResult per child; the planner folds them.
 constexpr int kScanThreads = 512;
 
-// Inclusive prefix sum of a 32-bit value across the 64 lanes, by DPP
-// (GPUOpen's cross-lane scan): row shifts 1, 2, 3 sum each lane's four-lane
-// window, shifts 4 and 8 (lanes of the upper banks only) complete each row
-// of 16, and row broadcasts 15 and 31 carry the rows' totals upward. A lane
-// a control leaves out adds 0. No LDS crossbar round trip.
-template <int CTRL, int ROW_MASK, int BANK_MASK>
-__device__ __forceinline__ int dpp_add0(int x) {
-    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, BANK_MASK, true);
-}
-__device__ __forceinline__ int wave_incl_scan_i(int v) {
-    int t = v + dpp_add0<0x111, 0xF, 0xF>(v);  // row_shr:1
-    t += dpp_add0<0x112, 0xF, 0xF>(v);         // row_shr:2
-    t += dpp_add0<0x113, 0xF, 0xF>(v);         // row_shr:3
-    t += dpp_add0<0x114, 0xF, 0xE>(t);         // row_shr:4, lanes 4-15 of each row
-    t += dpp_add0<0x118, 0xF, 0xC>(t);         // row_shr:8, lanes 8-15 of each row
-    t += dpp_add0<0x142, 0xA, 0xF>(t);         // row_bcast:15 into rows 1 and 3
-    t += dpp_add0<0x143, 0xC, 0xF>(t);         // row_bcast:31 into rows 2 and 3
-    return t;
-}
 
 // kCat: the dataset has categorical features (the category-set search is
 // compiled in). At most 128 VGPRs (4 waves per SIMD): two 512-thread blocks
@@ -3608,7 +3603,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __syncthreads();
     if (tid < 64) {
         const int a = s_wcnt[lane], b = s_pcnt[lane];
-        const int ia = (int)wave_incl_scan((long long)a), ib = (int)wave_incl_scan((long long)b);
+        const int ia = wave_incl_scan_i(a), ib = wave_incl_scan_i(b);
         s_wcnt[lane] = ia - a;
         s_pcnt[lane] = ib - b;
         if (lane == 63) {
@@ -3797,22 +3792,23 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     }
     __syncthreads();
     if (tid < 64) {  // wave 0: totals, chunks, task counts and their prefixes (nsel <= kmax <= 64)
+        // (row counts below n < 2^31 and task counts: 32-bit DPP sums and scans)
         long long m = 0, mb = 0;
         if (lane < nsel) {
             const SelNode &sn = v.sn[lane];
             m = sn.end - sn.begin;
             mb = sn.n_left <= m - sn.n_left ? sn.n_left : m - sn.n_left;
         }
-        const long long rows_total = wave_sum_ll(m), built_total = wave_sum_ll(mb);
+        const long long rows_total = wave_add_u32((unsigned)m), built_total = wave_add_u32((unsigned)mb);
         int64_t chunk = (built_total + s.pb_launch - 1) / s.pb_launch;
         if (chunk < s.hist_chunk_min) chunk = s.hist_chunk_min;
         if (chunk > s.hist_chunk_limit) chunk = s.hist_chunk_limit;
-        const long long pc = lane < nsel ? (mb + chunk - 1) / chunk : 0;
+        const int pc = lane < nsel ? (int)((mb + chunk - 1) / chunk) : 0;
         long long chunk_p = (rows_total + s.part_target - 1) / s.part_target;
         chunk_p = (chunk_p + kPartChunkStep - 1) / kPartChunkStep * kPartChunkStep;
         chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > kPartChunk ? kPartChunk : chunk_p;
-        const long long qc = lane < nsel ? (m + chunk_p - 1) / chunk_p : 0;
-        const long long pi = wave_incl_scan(pc), qi = wave_incl_scan(qc);
+        const int qc = lane < nsel ? (int)((m + chunk_p - 1) / chunk_p) : 0;
+        const int pi = wave_incl_scan_i(pc), qi = wave_incl_scan_i(qc);
         if (lane < nsel) {
             v.pcnt[lane] = (int)pc;
             v.qcnt[lane] = (int)qc;
