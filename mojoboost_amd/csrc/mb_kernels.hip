@@ -1559,9 +1559,17 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                     // the row's lane 0 quantizes g, lane 1 h, then both are
                     // read across the row's lanes
                     const int q = quant_value(*qc, v[u], wt, (int64_t)r, (sub & 1) == 0);
-                    const int base = (int)lane_id() & ~(LPR - 1);
-                    qg = __shfl(q, base, 64);
-                    qh = __shfl(q, base + 1, 64);
+                    if constexpr (LPR == 2) {  // DPP, off the LDS queue the histogram atomics use
+                        qg = __builtin_amdgcn_update_dpp(q, q, 0xA0, 0xF, 0xF, false);  // quad_perm [0,0,2,2]
+                        qh = __builtin_amdgcn_update_dpp(q, q, 0xF5, 0xF, 0xF, false);  // quad_perm [1,1,3,3]
+                    } else if constexpr (LPR == 4) {
+                        qg = __builtin_amdgcn_update_dpp(q, q, 0x00, 0xF, 0xF, false);  // quad_perm [0,0,0,0]
+                        qh = __builtin_amdgcn_update_dpp(q, q, 0x55, 0xF, 0xF, false);  // quad_perm [1,1,1,1]
+                    } else {
+                        const int base = (int)lane_id() & ~(LPR - 1);
+                        qg = __shfl(q, base, 64);
+                        qh = __shfl(q, base + 1, 64);
+                    }
                 }
                 const uint32_t pair = (uint32_t)(uint8_t)(int8_t)qg | ((uint32_t)(uint8_t)(int8_t)qh << 8);
                 uint4 v = w[u];
