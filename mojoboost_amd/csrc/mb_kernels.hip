@@ -3436,6 +3436,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             g.n_leaves = nl;
             g.n_nodes = nn;
         }
+        // the committed frontier's marks for the selection (fr reuses the
+        // replay's right-child gains, free now); one wave's LDS writes land
+        // in order
+        for (int i = lane; i < ne; i += 64) v.fr[i] = 0;
+        __asm__ volatile("" ::: "memory");
+        for (int i = lane; i < nl; i += 64) v.fr[v.sl_e[i]] = 1;
     }
     __syncthreads();
     const int nc = s_nc, nl = g.n_leaves, nn = g.n_nodes;
@@ -3503,12 +3509,11 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         finish(0);
         return;
     }
-    // the committed frontier is kept before the speculative pass reuses it
+    // the committed frontier is kept for the next launch
     for (int i = tid; i < nl; i += nthr) {
         s.slot_e[i] = v.sl_e[i];
         s.slot_fid[i] = v.sl_fid[i];
     }
-    __syncthreads();
     // ---- 3. selection. Best-first over a tree pops nodes in non-increasing
     // order of their bottleneck value b(v) = the smallest gain on the path
     // from the committed frontier down to v; continuing the replay as if
@@ -3531,58 +3536,46 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // (measured on C2: 45M instead of 76M rows partitioned per tree, 22.1
     // instead of 20.0 iterations, 6 % less time).
     const int64_t spec_rows = s_x >= 0 ? max((int64_t)(s.n / 2), (int64_t)2 * v.rw[s_x]) : (int64_t)s.n;
-    for (int i = tid; i < ne; i += nthr) v.fr[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < nl; i += nthr) v.fr[v.sl_e[i]] = 1;
-    __syncthreads();
-    // b by pointer jumping: node i carries the smallest gain on its path up
+    // b by pointer chasing: node i carries the smallest gain on its path up
     // to (excluding) up[i]; up = -1 once a frontier node was passed
     // (inside), -2 at the root without one (a committed internal node).
-    // Each round doubles the covered path, so a depth-D tree needs
-    // ceil(log2 D) rounds. Nodes per thread: ne <= e_cap <= 4 x 1024.
+    // Each node's (b, up) is one 64-bit LDS word (b rounded to binary32:
+    // the rounding is monotone and b only orders the selection), read and
+    // written whole, so a node that follows an ancestor's word always reads
+    // a consistent pair -- the ancestor's start or any later step of its own
+    // chase -- and takes the min and the pointer from it. Every thread
+    // follows its nodes' chains to the end with no barrier between steps
+    // (chains are at most the tree's depth and shortened by ancestors that
+    // have progressed). Nodes per thread: ne <= e_cap <= 4 x 1024.
     constexpr int kJ = 4;
-    double jv[kJ];
+    unsigned long long *bw = (unsigned long long *)v.cb;
+    auto pack_b = [](float b, int up) {
+        return ((unsigned long long)__float_as_uint(b) << 32) | (unsigned long long)(uint32_t)up;
+    };
+    float jv[kJ];
     int ju[kJ];
 #pragma unroll
     for (int k = 0; k < kJ; ++k) {
         const int i = tid + k * nthr;
-        jv[k] = -1.0;
+        jv[k] = -1.0f;
         ju[k] = -2;
         if (i < ne) {
-            jv[k] = v.eg[i];
+            jv[k] = (float)v.eg[i];
             ju[k] = v.fr[i] ? -1 : (v.ep[i] < 0 ? -2 : v.ep[i]);
-            v.cb[i] = jv[k];
-            v.ci[i] = ju[k];
+            __hip_atomic_store(&bw[i], pack_b(jv[k], ju[k]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
-    for (;;) {
-        __syncthreads();
-        double nv[kJ];
-        int nu[kJ];
-        bool more = false;
+    __syncthreads();  // every node's starting word is in place
 #pragma unroll
-        for (int k = 0; k < kJ; ++k) {
-            nv[k] = jv[k];
-            nu[k] = ju[k];
-            if (ju[k] >= 0) {
-                const double pv = v.cb[ju[k]];
-                nv[k] = pv < jv[k] ? pv : jv[k];
-                nu[k] = v.ci[ju[k]];
-                more |= nu[k] >= 0;
-            }
+    for (int k = 0; k < kJ; ++k) {
+        const int i = tid + k * nthr;
+        while (ju[k] >= 0) {
+            const unsigned long long w = __hip_atomic_load(&bw[ju[k]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const float pv = __uint_as_float((unsigned)(w >> 32));
+            jv[k] = pv < jv[k] ? pv : jv[k];
+            ju[k] = (int)(uint32_t)w;
+            __hip_atomic_store(&bw[i], pack_b(jv[k], ju[k]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < kJ; ++k) {
-            const int i = tid + k * nthr;
-            if (ju[k] >= 0) {
-                jv[k] = nv[k];
-                ju[k] = nu[k];
-                v.cb[i] = nv[k];
-                v.ci[i] = nu[k];
-            }
-        }
-        if (!__syncthreads_or(more)) break;
     }
     // candidates: b > 0 inside the region below the frontier, compacted by
     // wave ballots into (cb, ci): b and the node id, bit 31 set when the
@@ -3635,7 +3628,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const int i = tid + k * nthr;
         const int kk = s_wcnt[k * nwaves + wv] + myb[k];
         if (by_sort) {
-            const unsigned fb = __float_as_uint((float)jv[k]) & ~0xFFFu;
+            const unsigned fb = __float_as_uint(jv[k]) & ~0xFFFu;
             s_keys[0][kk] = (fb > 0x1000u ? fb : 0x1000u) | (unsigned)(0xFFF - i);
         } else {
             v.cb[kk] = jv[k];
