@@ -1901,6 +1901,16 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
         {
             const int bin = tid & 255, half = tid >> 8;
             int g = 0, h = 0, c = 0;
+            // the parent's cells (the sibling is parent - accumulated) are
+            // loaded with the partials, one memory round trip for both
+            int32_t *pp = nullptr;
+            int pg0 = 0, ph0 = 0, pc0 = 0;
+            if (half == 0 && !root_mode && bin < nb) {
+                pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
+                pg0 = pp[0];
+                ph0 = pp[1];
+                pc0 = pp[2];
+            }
             if (bin < nb) {
                 const size_t pstride = (size_t)F * s.part_stride;
                 const unsigned long long *p =
@@ -1963,10 +1973,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                     ob[1] = h;
                     ob[2] = c;
                     if (!root_mode) {
-                        int32_t *pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
-                        sgv = pp[0] - g;
-                        shv = pp[1] - h;
-                        scv = pp[2] - c;
+                        sgv = pg0 - g;
+                        shv = ph0 - h;
+                        scv = pc0 - c;
                         pp[0] = sgv;
                         pp[1] = shv;
                         pp[2] = scv;
@@ -2343,6 +2352,16 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
             const int q = tid >> 7, half = (tid >> 6) & 1, bin = lane;
             const int f = f0 + q;
             int g = 0, h = 0, c = 0;
+            // the parent's cells (the sibling is parent - accumulated) are
+            // loaded with the partials, one memory round trip for both
+            int32_t *pp = nullptr;
+            int pg0 = 0, ph0 = 0, pc0 = 0;
+            if (half == 0 && !root_mode && f < F && bin < nb) {
+                pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
+                pg0 = pp[0];
+                ph0 = pp[1];
+                pc0 = pp[2];
+            }
             if (f < F && bin < nb) {
                 const size_t pstride = (size_t)F * s.part_stride;
                 const unsigned long long *p =
@@ -2402,10 +2421,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
                     ob[1] = h;
                     ob[2] = c;
                     if (!root_mode) {
-                        int32_t *pp = s.hist + (size_t)it.hist_sib * hsz + ((size_t)f * nb + bin) * 3;
-                        sgv = pp[0] - g;
-                        shv = pp[1] - h;
-                        scv = pp[2] - c;
+                        sgv = pg0 - g;
+                        shv = ph0 - h;
+                        scv = pc0 - c;
                         pp[0] = sgv;
                         pp[1] = shv;
                         pp[2] = scv;
@@ -2549,6 +2567,14 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
             const int bin = tid & 255, half = tid >> 8;
             double g = 0.0, h = 0.0;
             int c = 0;
+            // the parent's cell (the sibling is parent - accumulated) is
+            // loaded with the partials, one memory round trip for both
+            HistF *pp = nullptr;
+            HistF pv{};
+            if (half == 0 && !root_mode && bin < nb) {
+                pp = s.histf + (size_t)it.hist_sib * hsz + (size_t)f * nb + bin;
+                pv = *pp;
+            }
             if (bin < nb) {
                 const size_t pstride = (size_t)F * s.part_stride;
                 const size_t base = (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
@@ -2580,10 +2606,9 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
                     ob->h = h;
                     ob->c = c;
                     if (!root_mode) {
-                        HistF *pp = s.histf + (size_t)it.hist_sib * hsz + (size_t)f * nb + bin;
-                        sgv = pp->g - g;
-                        shv = pp->h - h;
-                        scv = (int)(pp->c - c);
+                        sgv = pv.g - g;
+                        shv = pv.h - h;
+                        scv = (int)(pv.c - c);
                         pp->g = sgv;
                         pp->h = shv;
                         pp->c = scv;
