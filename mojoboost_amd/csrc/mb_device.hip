@@ -364,8 +364,8 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
         s.fpart_h = dalloc<double>(cells, run.owned);
         s.fpart_c = dalloc<uint32_t>(cells, run.owned);
     }
-    s.pb_desc = dalloc<mb::PbDesc>(s.part_grid, run.owned);
-    s.ac_desc = dalloc<mb::AcDesc>(s.pb_grid, run.owned);
+    s.part_items = dalloc<mb::PartItem>(s.kmax, run.owned);
+    s.acc_items = dalloc<mb::AccItem>(s.kmax, run.owned);
 }
 
 double base_score_for(const mbh_dataset *ds, int objective) {
@@ -641,8 +641,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
     HIPX(hipMemset(s.batch, 0, sizeof(mb::Batch)));
     HIPX(hipMemset(s.grow, 0, sizeof(mb::Grow)));
-    HIPX(hipMemset(s.pb_desc, 0, (size_t)s.part_grid * sizeof(mb::PbDesc)));
-    HIPX(hipMemset(s.ac_desc, 0, (size_t)s.pb_grid * sizeof(mb::AcDesc)));
+    HIPX(hipMemset(s.part_items, 0, (size_t)s.kmax * sizeof(mb::PartItem)));
+    HIPX(hipMemset(s.acc_items, 0, (size_t)s.kmax * sizeof(mb::AccItem)));
     HIPX(hipMemset(s.cursor, 0, (2 + 2 * (size_t)s.kmax) * sizeof(int64_t)));
     HIPX(hipMemset(s.error, 0, sizeof(int32_t)));
     HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));

@@ -72,6 +72,13 @@ __device__ __forceinline__ long long wave_incl_scan(long long v) {
 // modifier, so a reduction step costs a few cycles instead of an LDS
 // crossbar round trip. Lanes a control does not cover keep their own value,
 // which every reduction below treats as its identity.
+// Lane l's 64-bit value on every lane (l wave-uniform).
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(uint64_t)v, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ unsigned dpp_u32(unsigned x) {
     return (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROW_MASK, 0xF, false);
@@ -1697,12 +1704,35 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
     __shared__ int cnt_l[E], cnt_r[E];     // counts, then exclusive prefixes within a scan wave
     __shared__ int wtot[2][SW];            // scan-wave totals, then their exclusive prefixes
     __shared__ long long base[2];
-    const int n_blocks = s.batch->n_blocks;
+    const Batch bh = *s.batch;
+    const int n_blocks = bh.n_blocks;
+    if ((int)blockIdx.x >= n_blocks) return;
     const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
     const unsigned long long below = (1ULL << lane) - 1ULL;
     const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
+    // every wave holds the batch's items, lane i item i (n_items <= 64); a
+    // task finds its item by a ballot over the items' first tasks
+    PartItem pit{};
+    if (lane < bh.n_items) pit = s.part_items[lane];
     for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
-        const PbDesc d = s.pb_desc[blk];
+        const unsigned long long own = __ballot(lane < bh.n_items && pit.qoff <= blk);  // item 0 starts at 0
+        const int q = 63 - (int)__builtin_clzll(own);
+        struct {
+            int64_t begin, n_left, m, c0, c1;
+            int item, src_buf, feature, bin, default_left, missing_bin, cat_e;
+        } d;
+        d.begin = readlane_i64(pit.begin, q);
+        d.n_left = readlane_i64(pit.n_left, q);
+        d.m = readlane_i64(pit.m, q);
+        d.c0 = (int64_t)(blk - __builtin_amdgcn_readlane(pit.qoff, q)) * bh.chunk_p;
+        d.c1 = d.c0 + bh.chunk_p < d.m ? d.c0 + bh.chunk_p : d.m;
+        d.item = q;
+        d.src_buf = __builtin_amdgcn_readlane(pit.src_buf, q);
+        d.feature = __builtin_amdgcn_readlane(pit.feature, q);
+        d.bin = __builtin_amdgcn_readlane(pit.bin, q);
+        d.default_left = __builtin_amdgcn_readlane(pit.default_left, q);
+        d.missing_bin = __builtin_amdgcn_readlane(pit.missing_bin, q);
+        d.cat_e = __builtin_amdgcn_readlane(pit.cat_e, q);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
@@ -1806,17 +1836,29 @@ constexpr int kAccThreads = 1024;  // two blocks per CU resident (launch grid 2 
 template <int LPR, class Acc>
 __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
     extern __shared__ unsigned char lds[];
-    const int n_acc = s.batch->n_acc;
+    const Batch bh = *s.batch;
+    const int n_acc = bh.n_acc;
+    if ((int)blockIdx.x >= n_acc) return;
     const double goss_mult = s.round->goss_mult;
     const int ls = s.lds_stride;
     const int f0 = (int)blockIdx.y * s.tile_f;
     const int Ft = min(s.tile_f, s.n_features - f0);
     const uint4 *rec = (const uint4 *)(s.records + (size_t)blockIdx.y * s.n * s.rec_bytes);
+    const int lane = lane_id();
+    // every wave holds the batch's items, lane i item i (n_items <= 64); a
+    // task finds its item by a ballot over the items' first tasks
+    AccItem ait{};
+    if (lane < bh.n_items) ait = s.acc_items[lane];
     for (int blk = blockIdx.x; blk < n_acc; blk += gridDim.x) {
-        const AcDesc d = s.ac_desc[blk];
+        const unsigned long long own = __ballot(lane < bh.n_items && ait.poff <= blk);  // item 0 starts at 0
+        const int q = 63 - (int)__builtin_clzll(own);
+        const int64_t lo = readlane_i64(ait.lo, q) + (int64_t)(blk - __builtin_amdgcn_readlane(ait.poff, q)) * bh.chunk_a;
+        const int64_t hi_item = readlane_i64(ait.hi, q);
+        const int64_t hi = lo + bh.chunk_a < hi_item ? lo + bh.chunk_a : hi_item;
+        const int buf = __builtin_amdgcn_readlane(ait.buf, q);
         Acc::template zero<LPR>(lds, Ft, ls);
         __syncthreads();
-        accumulate_rows<LPR, Acc, true, false, kAccUnroll>(s, lds, d.buf ? s.rows1 : s.rows0, d.lo, d.hi, Ft, rec,
+        accumulate_rows<LPR, Acc, true, false, kAccUnroll>(s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec,
                                                            goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
@@ -3260,7 +3302,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.done = 1;
             b.iters = 0;
             b.n_acc = 0;
-            b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
+            b.chunk_p = b.chunk_a = b.pad_ = 0;
             *s.batch = b;
         }
         return;
@@ -3513,7 +3555,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.done = 1;
             b.iters = g.iterations;
             b.n_acc = 0;
-            b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
+            b.chunk_p = b.chunk_a = b.pad_ = 0;
             *s.batch = b;
         }
     };
@@ -3920,54 +3962,29 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         s.e_left[Xs] = le;
         s.cursor[2 + 2 * jj] = 0;
         s.cursor[3 + 2 * jj] = 0;
+        // the item's partition and accumulation work; each task of the
+        // launches finds its item from these (no per-task descriptors)
+        PartItem pi;
+        pi.begin = b0;
+        pi.n_left = nlft;
+        pi.m = m;
+        pi.qoff = v.qoff[jj];
+        pi.src_buf = ebuf;
+        pi.feature = sn.feature;
+        pi.bin = sn.bin;
+        pi.default_left = sn.default_left;
+        pi.missing_bin = v.mbin[sn.feature];
+        pi.cat_e = sn.cat ? Xs : -1;
+        pi.pad_ = 0;
+        s.part_items[jj] = pi;
+        AccItem ai;
+        ai.lo = bl ? b0 : b0 + nlft;
+        ai.hi = bl ? b0 + nlft : e0;
+        ai.poff = v.poff[jj];
+        ai.buf = 1 - ebuf;
+        s.acc_items[jj] = ai;
     }
     __syncthreads();
-    // partition descriptors
-    for (int b = tid; b < total_p; b += nthr) {
-        int lo = 0, hi = nsel - 1;  // last item with qoff <= b
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (v.qoff[mid] <= b) lo = mid;
-            else hi = mid - 1;
-        }
-        const Item &it = v.it[lo];
-        const SelNode &pe = v.sn[lo];  // the parent is the selected leaf itself
-        const int64_t m = it.end - it.begin;
-        PbDesc d;
-        d.begin = it.begin;
-        d.n_left = it.n_left;
-        d.m = m;
-        d.c0 = (int64_t)(b - v.qoff[lo]) * chunk_p;
-        d.c1 = d.c0 + chunk_p < m ? d.c0 + chunk_p : m;
-        d.item = lo;
-        d.src_buf = it.src_buf;
-        d.feature = pe.feature;
-        d.bin = pe.bin;
-        d.default_left = pe.default_left;
-        d.missing_bin = v.mbin[pe.feature];
-        d.builds_left = it.builds_left;
-        d.cat_e = pe.cat ? it.parent_e : -1;
-        s.pb_desc[b] = d;
-    }
-    // accumulation descriptors: chunks of the accumulated child's range in
-    // the other row buffer
-    for (int b = tid; b < total; b += nthr) {
-        int lo = 0, hi = nsel - 1;  // last item with poff <= b
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (v.poff[mid] <= b) lo = mid;
-            else hi = mid - 1;
-        }
-        const Item &it = v.it[lo];
-        const int64_t c_lo = it.builds_left ? it.begin : it.begin + it.n_left;
-        const int64_t c_hi = it.builds_left ? it.begin + it.n_left : it.end;
-        AcDesc d;
-        d.lo = c_lo + (int64_t)(b - v.poff[lo]) * chunk;
-        d.hi = d.lo + chunk < c_hi ? d.lo + chunk : c_hi;
-        d.item = lo;
-        d.buf = 1 - it.src_buf;
-        s.ac_desc[b] = d;
-    }
     __syncthreads();
     if (tid == 0) {
         g.n_explored = ne + 2 * nsel;
@@ -3983,7 +4000,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         b.done = 0;
         b.iters = g.iterations;
         b.n_acc = total;
-        b.pad_[0] = b.pad_[1] = b.pad_[2] = 0;
+        b.chunk_p = (int32_t)chunk_p;
+        b.chunk_a = (int32_t)chunk;
+        b.pad_ = 0;
         *s.batch = b;
     }
 }

@@ -56,29 +56,34 @@ struct Item {
     int32_t pad_;
 };
 
-// Work of one partition task: a chunk [c0, c1) of an item's parent range
-// (offsets relative to begin).
-struct PbDesc {
-    int64_t begin, n_left, m, c0, c1;
-    int32_t item, src_buf, feature, bin, default_left, missing_bin, builds_left;
+// A batch item's partition work: its parent range [begin, begin + m) of
+// row buffer src_buf, split into tasks of the batch's chunk_p rows numbered
+// from qoff (task t of the batch belongs to the last item with qoff <= t).
+struct PartItem {
+    int64_t begin, n_left, m;
+    int32_t qoff, src_buf, feature, bin, default_left, missing_bin;
     int32_t cat_e;  // categorical split: the explored node whose e_cat set routes left; -1 numerical
+    int32_t pad_;
 };
 
-// Work of one accumulation task: rows [lo, hi) of row buffer `buf` (a chunk
-// of an item's accumulated child), summed into one block partial.
-struct AcDesc {
+// A batch item's accumulation work: its accumulated child, rows [lo, hi) of
+// row buffer `buf`, in tasks of the batch's chunk_a rows numbered from poff
+// (one block partial each).
+struct AccItem {
     int64_t lo, hi;
-    int32_t item, buf;
+    int32_t poff, buf;
 };
 
 // Written by the planner; the host reads it back between launch groups.
 struct Batch {
     int32_t n_items;   // 0: nothing to do this iteration
-    int32_t n_blocks;  // partition descriptors in use
+    int32_t n_blocks;  // partition tasks in use
     int32_t done;      // the tree is complete
     int32_t iters;     // expansion iterations planned so far in this tree
-    int32_t n_acc;     // accumulation descriptors (block partials) in use
-    int32_t pad_[3];
+    int32_t n_acc;     // accumulation tasks (block partials) in use
+    int32_t chunk_p;   // parent rows per partition task
+    int32_t chunk_a;   // accumulated rows per accumulation task
+    int32_t pad_;
 };
 
 // Replay state of the best-first order (touched by the planning block only).
@@ -294,8 +299,8 @@ struct DevState {
     int32_t *e_parent;     // e_cap: parent, -1 for the root
     int32_t *e_rows;       // e_cap: rows of the node (n < 2^31)
     Item *items;           // kmax
-    PbDesc *pb_desc;       // part_grid
-    AcDesc *ac_desc;       // pb_grid
+    PartItem *part_items;  // kmax: the batch's partition work per item
+    AccItem *acc_items;    // kmax: the batch's accumulation work per item
     Batch *batch;
     Grow *grow;
     int32_t *slot_e;       // num_leaves: explored node of each frontier slot
