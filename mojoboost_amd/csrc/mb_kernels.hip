@@ -3283,6 +3283,44 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     const int nthr = blockDim.x, nwaves = blockDim.x >> 6;
     const int L = s.hp.num_leaves, F = s.n_features;
     const HyperParams &hp = s.hp;
+    // When the explored nodes, the frontier, the features and the items fit
+    // one per thread, every array the set-up needs is read up to its
+    // capacity first, with the batch header below in flight at the same
+    // time: one memory round trip instead of two (entries past the header's
+    // counts are allocated, read and never used).
+    constexpr int kPW = 8;  // fold: pairs per wave (16 waves x 8 >= 2 x 64)
+    static_assert(kPlanThreads / 64 * kPW >= 2 * 64, "every pair of a batch in one pass");
+    const bool pre = s.e_cap <= kPlanThreads && L <= kPlanThreads && F <= 64;  // launch-uniform
+    double p_eg = 0.0, gq[kPW];
+    int p_el = 0, p_ep = 0, p_rw = 0, p_se = 0, p_sf = 0, p_mb = 0;
+    static_assert(sizeof(Item) == 64, "an item is four 16-byte words");
+    uint4 p_i0 = make_uint4(0, 0, 0, 0), p_i1 = p_i0, p_i2 = p_i0, p_i3 = p_i0;
+    if (pre) {
+        if (tid < s.e_cap) {
+            p_eg = s.e_gain[tid];
+            p_el = s.e_left[tid];
+            p_ep = s.e_parent[tid];
+            p_rw = s.e_rows[tid];
+        }
+        if (tid < L) {
+            p_se = s.slot_e[tid];
+            p_sf = s.slot_fid[tid];
+        }
+        if (tid < F) p_mb = s.missing_bin[tid];
+        if (tid < s.kmax) {
+            const uint4 *q = (const uint4 *)&s.items[tid];
+            p_i0 = q[0];
+            p_i1 = q[1];
+            p_i2 = q[2];
+            p_i3 = q[3];
+        }
+#pragma unroll
+        for (int k = 0; k < kPW; ++k) {
+            int pr = wv + k * nwaves;
+            pr = pr < 2 * s.kmax ? pr : 0;
+            gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+        }
+    }
     // the batch size, the round and the growth counters in one memory round
     // trip (every thread reads the counters itself, a broadcast load, instead
     // of waiting at a barrier for one thread's copy)
@@ -3335,32 +3373,52 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // unconditional (a branch between dependent loads would cost a memory
     // round trip each): when F <= 64 wave w takes pairs w + 16 k, k < kPW,
     // lane = feature; the argmax keeps the lowest feature on equal gains.
-    constexpr int kPW = 8;
-    static_assert(kPlanThreads / 64 * kPW >= 2 * 64, "every pair of a batch in one pass");
-    double gq[kPW];
-    if (F <= 64) {
+    if (pre) {
+        if (!root_mode && tid < n_items) {
+            uint4 *q = (uint4 *)&v.it[tid];
+            q[0] = p_i0;
+            q[1] = p_i1;
+            q[2] = p_i2;
+            q[3] = p_i3;
+        }
+        if (tid < F) v.mbin[tid] = p_mb;
+        if (tid < ne) {
+            v.eg[tid] = p_eg;
+            v.el[tid] = p_el;
+            v.ep[tid] = p_ep;
+            v.rw[tid] = p_rw;
+        }
+        if (!root_mode && tid < nl0) {
+            v.sl_e[tid] = p_se;
+            v.sl_fid[tid] = p_sf;
+        }
+    } else {
+        if (F <= 64) {
 #pragma unroll
-        for (int k = 0; k < kPW; ++k) {
-            int pr = wv + k * nwaves;
-            pr = pr < n_pairs ? pr : 0;
-            gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+            for (int k = 0; k < kPW; ++k) {
+                int pr = wv + k * nwaves;
+                pr = pr < n_pairs ? pr : 0;
+                gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+            }
         }
-    }
-    if (!root_mode)
-        for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
-    for (int f = tid; f < F; f += nthr) v.mbin[f] = s.missing_bin[f];
-    for (int i = tid; i < ne; i += nthr) {
-        v.eg[i] = s.e_gain[i];
-        v.el[i] = s.e_left[i];
-        v.ep[i] = s.e_parent[i];
-        v.rw[i] = s.e_rows[i];
-    }
-    if (!root_mode)
-        for (int i = tid; i < nl0; i += nthr) {
-            v.sl_e[i] = s.slot_e[i];
-            v.sl_fid[i] = s.slot_fid[i];
+        if (!root_mode)
+            for (int jj = tid; jj < n_items; jj += nthr) v.it[jj] = s.items[jj];
+        for (int f = tid; f < F; f += nthr) v.mbin[f] = s.missing_bin[f];
+        for (int i = tid; i < ne; i += nthr) {
+            v.eg[i] = s.e_gain[i];
+            v.el[i] = s.e_left[i];
+            v.ep[i] = s.e_parent[i];
+            v.rw[i] = s.e_rows[i];
         }
-    if (tid < 64) {
+        if (!root_mode)
+            for (int i = tid; i < nl0; i += nthr) {
+                v.sl_e[i] = s.slot_e[i];
+                v.sl_fid[i] = s.slot_fid[i];
+            }
+    }
+    if (hp.quantized) {
+        if (tid == 0) s_vf = 0;  // unused: integer sums give the leaf values
+    } else if (tid < 64) {
         // the tree's first selected feature (the fp32 path's leaf value sums)
         int vf = F - 1;
         for (int f0 = 0; f0 < F; f0 += 64) {
