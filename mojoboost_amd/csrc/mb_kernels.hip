@@ -1674,8 +1674,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uin
 // One launch routes the rows of every leaf of the batch to the children
 // (tree.partition_rows_into semantics: the missing bin follows default_left,
 // otherwise bin <= threshold goes left) in the other row buffer -- left rows
-// fill [begin, begin + n_left), right rows the rest. Each task (descriptor,
-// written by the planner) is a chunk of 512-4K rows of one leaf: each of
+// fill [begin, begin + n_left), right rows the rest. Each task is a chunk
+// of 512-4K rows of one leaf (the item whose first task number, in the
+// planner's per-item table, is the last at or below the task's): each of
 // the block's 1024 threads keeps its kPartRows (4) row ids and their sides in
 // registers (slots past the chunk read nothing: buffer loads out of range
 // return 0), wave ballots count the rows of each (row group u, wave) entry,
@@ -1827,9 +1828,10 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
 
 // ---------------------------------------------------------- accumulation
 // One launch accumulates the smaller child of every leaf of the batch from
-// its rows, now contiguous in the partitioned row buffer. Each task
-// (descriptor, written by the planner) is a chunk of one child's rows and
-// yields one block partial; the scan kernel merges an item's partials.
+// its rows, now contiguous in the partitioned row buffer. Each task (found
+// from the planner's per-item table as in the partition) is a chunk of one
+// child's rows and yields one block partial; the scan kernel merges an
+// item's partials.
 // blockIdx.y is the feature tile: the block reads that tile's records and
 // stores that tile's features of its partial.
 constexpr int kAccThreads = 1024;  // two blocks per CU resident (launch grid 2 x CUs)
@@ -1862,7 +1864,7 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
                                                            goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
-        __syncthreads();  // the LDS histogram is zeroed again for the next descriptor
+        __syncthreads();  // the LDS histogram is zeroed again for the next task
     }
 }
 

@@ -1,8 +1,8 @@
 // Device-resident state of one training run on one GPU.
 //
 // The tree grows entirely on the device: every kernel reads what it needs
-// (the leaves to expand, their row ranges and splits) from descriptors that
-// the previous scan kernel's planning block wrote, so the host enqueues a
+// (the leaves to expand, their row ranges and splits) from the per-item
+// tables the planning kernel wrote, so the host enqueues a
 // tree without reading anything back except a done flag between groups of
 // launches. The host downloads the finished trees once, at the end of
 // training.
@@ -128,7 +128,7 @@ struct Round {
 };
 
 // Parent rows of a partition task: at most kPartChunk (one task per block
-// pass), at least kPartChunkMin (the host sizes the descriptor buffer from
+// pass), at least kPartChunkMin (the host bounds a batch's task count by
 // it). The planner spreads a batch over about part_target tasks in between,
 // in multiples of kPartChunkStep rows.
 #ifndef MB_PART_CHUNK
@@ -314,8 +314,8 @@ struct DevState {
     int32_t kmax;          // most leaves expanded per launch
     int32_t max_exp;       // most expansions per tree (2 num_leaves - 1)
     int32_t e_cap;         // ENode capacity (1 + 2 max_exp)
-    int32_t pb_grid;       // most accumulation descriptors (block partials) of a batch
-    int32_t part_grid;     // most partition descriptors of a batch
+    int32_t pb_grid;       // most accumulation tasks (block partials) of a batch
+    int32_t part_grid;     // most partition tasks of a batch
     int32_t scan_grid;     // blocks of a scan launch
     int32_t pb_launch;     // blocks of an accumulation launch (grid-strided)
     int32_t part_launch;   // blocks of a partition launch (grid-strided)
