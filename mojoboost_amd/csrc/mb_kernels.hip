@@ -2622,11 +2622,33 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
             if (bin < nb) {
                 const size_t pstride = (size_t)F * s.part_stride;
                 const size_t base = (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
-                for (int b = half; b < it.part_cnt; b += 2) {
-                    const size_t at = base + (size_t)b * pstride;
-                    g += s.fpart_g[at];
-                    h += s.fpart_h[at];
-                    c += (int)s.fpart_c[at];
+                const double *qg = s.fpart_g + base, *qh = s.fpart_h + base;
+                const uint32_t *qc = s.fpart_c + base;
+                const int np = it.part_cnt;
+                int b = half;
+                // four partials' loads in flight, added in partial order
+                for (; b + 6 < np; b += 8) {
+                    double vg[4], vh[4];
+                    uint32_t vc[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const size_t at = (size_t)(b + 2 * u) * pstride;
+                        vg[u] = qg[at];
+                        vh[u] = qh[at];
+                        vc[u] = qc[at];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        g += vg[u];
+                        h += vh[u];
+                        c += (int)vc[u];
+                    }
+                }
+                for (; b < np; b += 2) {
+                    const size_t at = (size_t)b * pstride;
+                    g += qg[at];
+                    h += qh[at];
+                    c += (int)qc[at];
                 }
             }
             if (half == 1) {
@@ -2666,49 +2688,85 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
         }
         const int child = tid >> 8;
         const int bin = tid & 255;
-        // ---- the reference's sequential sums, one thread per child
-        if ((tid & 255) == 0) {
+        // ---- the reference's sequential sums per child: lane 0 of the
+        // child's first wave sums the grad cells, lane 1 the hess cells, both
+        // the counts (the last count prefix is the total); the next four
+        // cells are requested before the current four are added
+        if ((tid & 255) < 2) {
             constexpr int W = 8;
-            double lg[W], lh[W];
-            for (int k = 0; k < W; ++k) lg[k] = lh[k] = 0.0;
-            long long tc = 0;
-            int b = 0;
-            while (b + W <= nb) {
-                for (int k = 0; k < W; ++k) {
-                    lg[k] += cg[child][b + k];
-                    lh[k] += ch[child][b + k];
-                    tc += cc[child][b + k];
-                }
-                b += W;
-            }
-            for (int w2 = W / 2; w2 >= 1; w2 >>= 1)
-                for (int k = 0; k < w2; ++k) {
-                    lg[k] = lg[k] + lg[k + w2];
-                    lh[k] = lh[k] + lh[k + w2];
-                }
-            double tg = lg[0], th = lh[0];
-            for (; b < nb; ++b) {
-                tg += cg[child][b];
-                th += ch[child][b];
-                tc += cc[child][b];
-            }
-            double rg = 0.0, rh = 0.0, sg = 0.0, sh = 0.0;
+            const int q = tid & 1;
+            const double *src = q ? ch[child] : cg[child];
+            double *dst = q ? ph_[child] : pg_[child];
+            const int *csrc = cc[child];
+            int *cdst = pc_[child];
+            double lw[W];
+#pragma unroll
+            for (int k = 0; k < W; ++k) lw[k] = 0.0;
+            double r = 0.0;
             int rc = 0;
-            for (int k = 0; k < nb; ++k) {
-                rg += cg[child][k];
-                rh += ch[child][k];
-                rc += cc[child][k];
-                pg_[child][k] = rg;
-                ph_[child][k] = rh;
-                pc_[child][k] = rc;
-                sg += cg[child][k];
-                sh += ch[child][k];
+            int b = 0;
+            if (nb >= W) {
+                // four cells per register block, the next four in flight
+                constexpr int H = W / 2;
+                double x[H];
+                int y[H];
+#pragma unroll
+                for (int u = 0; u < H; ++u) {
+                    x[u] = src[u];
+                    y[u] = csrc[u];
+                }
+                auto step = [&](int at, int lo) {
+                    // the next block's cells (clamped in bounds of the
+                    // 256-cell rows; past the last full block unused)
+                    const int nx = at + H <= 256 - H ? at + H : 256 - H;
+                    double xn[H];
+                    int yn[H];
+#pragma unroll
+                    for (int u = 0; u < H; ++u) {
+                        xn[u] = src[nx + u];
+                        yn[u] = csrc[nx + u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < H; ++u) {
+                        lw[lo + u] += x[u];
+                        r += x[u];
+                        rc += y[u];
+                        dst[at + u] = r;
+                        cdst[at + u] = rc;  // both lanes, the same value
+                    }
+#pragma unroll
+                    for (int u = 0; u < H; ++u) {
+                        x[u] = xn[u];
+                        y[u] = yn[u];
+                    }
+                };
+                for (; b + W <= nb; b += W) {
+                    step(b, 0);
+                    step(b + H, H);
+                }
             }
-            s_tg[child] = tg;
-            s_th[child] = th;
-            s_tc[child] = tc;
-            s_sg[child] = sg;
-            s_sh[child] = sh;
+#pragma unroll
+            for (int w2 = W / 2; w2 >= 1; w2 >>= 1)
+#pragma unroll
+                for (int k = 0; k < w2; ++k) lw[k] = lw[k] + lw[k + w2];
+            double t = lw[0];
+            for (; b < nb; ++b) {
+                const double xv = src[b];
+                const int yv = csrc[b];
+                t += xv;
+                r += xv;
+                rc += yv;
+                dst[b] = r;
+                cdst[b] = rc;
+            }
+            if (q == 0) {
+                s_tg[child] = t;
+                s_tc[child] = rc;  // the count total is the last prefix
+                s_sg[child] = r;
+            } else {
+                s_th[child] = t;
+                s_sh[child] = r;
+            }
         }
         __syncthreads();
         const double TG = s_tg[child], TH = s_th[child];
