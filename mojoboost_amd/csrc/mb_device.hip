@@ -349,7 +349,12 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
     s.part_grid = (int32_t)((ds->n + mb::kPartChunkMin - 1) / mb::kPartChunkMin + s.kmax);
     s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
-    s.pb_launch = std::min<int32_t>(s.pb_grid, 2 * ds->n_cu);  // two resident accumulation blocks per CU
+    // one accumulation task per resident block: two per CU where two LDS
+    // histograms fit (quantized), one for the fp32 and wide kinds (fewer
+    // tasks, fewer partials to store and merge)
+    const size_t acc_lds = mb::pb_lds_bytes_for(s.tile_f, s.lds_stride, kind) + kPbStaticLds;
+    const int acc_res = std::max(1, std::min(2, (int)((160 * 1024) / acc_lds)));
+    s.pb_launch = std::min<int32_t>(s.pb_grid, acc_res * ds->n_cu);
     s.part_launch = std::min<int32_t>(s.part_grid, 8 * ds->n_cu);
     s.part_target = 2 * ds->n_cu;
     // a root build uses at most ceil(n / chunk_min) chunks
@@ -554,6 +559,9 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
         s.goss_nblk = (int32_t)((ds->n + 1023) / 1024);
         s.gst = dalloc<mb::GossState>(1, run.owned);
         s.goss_hist = dalloc<uint32_t>(8 * 256, run.owned);
+        s.goss_sel = dalloc<unsigned long long>(16, run.owned);
+        s.goss_cand = dalloc<unsigned long long>(ds->n, run.owned);
+        s.goss_ccnt = dalloc<int32_t>(mb::kGossDigitBlocks, run.owned);
         // padded to whole count tiles; the pad holds INT_MIN (never kept) and
         // no kernel writes it
         const int64_t padded = (ds->n + mb::kGossTileRows - 1) / mb::kGossTileRows * mb::kGossTileRows;

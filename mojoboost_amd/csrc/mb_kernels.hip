@@ -791,6 +791,8 @@ __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
         if (other_k > n - top_k) other_k = n - top_k;
         g.prefix = 0ULL;
         g.rank = top_k - 1;
+        s.goss_sel[0] = 0ULL;
+        s.goss_sel[1] = (unsigned long long)(top_k - 1);
         g.top_k = top_k;
         g.other_k = other_k;
         g.threshold = 0.0;
@@ -804,67 +806,218 @@ __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
 }
 
 // Radix select of the top_k-th largest key, 8 bits per pass from the top.
+// The digit of the rank-th largest key (0-based, descending) in a 256-bin
+// digit histogram, by one wave: the highest digit whose count from the top
+// passes rank (digit 0 when none does); rank becomes the rank inside that
+// digit. Lane l holds digits 4l .. 4l + 3; counts are below n < 2^31.
+__device__ __forceinline__ int goss_pick_wave(const uint32_t *h, long long &rank) {
+    const int lane = lane_id();
+    const uint4 c = ((const uint4 *)h)[lane];
+    const int t = (int)(c.x + c.y + c.z + c.w);
+    const int incl = wave_incl_scan_i(t);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    const int cc[4] = {(int)c.x, (int)c.y, (int)c.z, (int)c.w};
+    int above = total - incl;  // the keys of the digits above this lane's four
+    int hit = -1, hit_above = 0;
+#pragma unroll
+    for (int b = 3; b >= 0; --b) {
+        if (hit < 0 && rank >= above && rank < (long long)above + cc[b]) {
+            hit = b;
+            hit_above = above;
+        }
+        above += cc[b];
+    }
+    const unsigned long long m = __ballot(hit >= 0);
+    if (m) {
+        const int l = __builtin_ctzll(m);
+        rank -= __builtin_amdgcn_readlane(hit_above, l);
+        return 4 * l + __builtin_amdgcn_readlane(hit, l);
+    }
+    rank -= total - __builtin_amdgcn_readlane(cc[0], 0);
+    return 0;
+}
+
+// Radix select of the top_k-th largest key, 8 bits per pass from the top.
+// The state after p picks (the prefix of the high 8p bits and the rank inside
+// it) is goss_sel[2p], goss_sel[2p + 1]; pass p's kernel takes pick p - 1
+// from pass p - 1's histogram in every block (block 0 stores it), so no
+// launch runs between passes. Each of kGossDigitBlocks blocks owns a
+// contiguous range of rows. Passes 0 to 2 read every row's key; pass 2 also
+// lists, in the block's own segment of goss_cand, the keys that match the
+// 16-bit prefix (they are the only keys later passes count), and passes 3 to
+// 7 read those lists.
 __global__ __launch_bounds__(256) void k_goss_digits(DevState s, int pass) {
     __shared__ uint32_t hist[256];
+    __shared__ unsigned long long s_prefix;
+    __shared__ long long s_rank;
+    __shared__ int s_nc;
     if (!goss_on(s)) return;
     hist[threadIdx.x] = 0u;
+    if (threadIdx.x == 0) s_nc = 0;
+    if (threadIdx.x < 64) {
+        unsigned long long prefix = 0ULL;
+        long long rank;
+        if (pass == 0) {
+            rank = (long long)s.goss_sel[1];
+        } else {
+            prefix = s.goss_sel[2 * (pass - 1)];
+            rank = (long long)s.goss_sel[2 * (pass - 1) + 1];
+            const int d = goss_pick_wave(s.goss_hist + (pass - 1) * 256, rank);
+            prefix |= (unsigned long long)d << (56 - 8 * (pass - 1));
+        }
+        if (threadIdx.x == 0) {
+            s_prefix = prefix;
+            s_rank = rank;
+            if (blockIdx.x == 0 && pass > 0) {
+                s.goss_sel[2 * pass] = prefix;
+                s.goss_sel[2 * pass + 1] = (unsigned long long)rank;
+            }
+        }
+    }
     __syncthreads();
-    const unsigned long long prefix = s.gst->prefix;
+    const unsigned long long prefix = s_prefix;
     const int shift = 56 - 8 * pass;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
-        const unsigned long long key = goss_key(s, r);
-        if (pass == 0 || (key >> (shift + 8)) == (prefix >> (shift + 8)))
-            atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    const int64_t n = s.n;
+    const int64_t seg = (n + kGossDigitBlocks - 1) / kGossDigitBlocks;
+    const int64_t lo = (int64_t)blockIdx.x * seg;
+    if (pass < 3) {
+        const int64_t hi = lo + seg < n ? lo + seg : n;
+        unsigned long long *cand = s.goss_cand + lo;
+        // four keys per thread in flight; the trip count is block-uniform
+        // (the candidate list's ballots need every lane)
+        for (int64_t b0 = lo; b0 < hi; b0 += 4 * 256) {
+            const int64_t r0 = b0 + threadIdx.x;
+            unsigned long long key[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t r = r0 + u * 256;
+                key[u] = r < hi ? goss_key(s, r) : 0ULL;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool in = r0 + u * 256 < hi && (pass == 0 || (key[u] >> (shift + 8)) == (prefix >> (shift + 8)));
+                if (in) atomicAdd(&hist[(key[u] >> shift) & 255u], 1u);
+                if (pass == 2) {
+                    const unsigned long long m = __ballot(in);
+                    int at = 0;
+                    if (lane_id() == 0 && m) at = atomicAdd(&s_nc, __popcll(m));
+                    at = __shfl(at, 0, 64);
+                    if (in) cand[at + __popcll(m & ((1ULL << lane_id()) - 1ULL))] = key[u];
+                }
+            }
+        }
+    } else {
+        const int nc = s.goss_ccnt[blockIdx.x];
+        const unsigned long long *cand = s.goss_cand + lo;
+        for (int j0 = threadIdx.x; j0 < nc; j0 += 4 * 256) {
+            unsigned long long key[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) key[u] = j0 + u * 256 < nc ? cand[j0 + u * 256] : 0ULL;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (j0 + u * 256 < nc && (key[u] >> (shift + 8)) == (prefix >> (shift + 8)))
+                    atomicAdd(&hist[(key[u] >> shift) & 255u], 1u);
+        }
     }
     __syncthreads();
     const uint32_t v = hist[threadIdx.x];
     if (v) atomicAdd(&s.goss_hist[pass * 256 + threadIdx.x], v);
+    if (pass == 2 && threadIdx.x == 0) s.goss_ccnt[blockIdx.x] = s_nc;
 }
 
-__global__ void k_goss_pick(DevState s, int pass) {
-    if (!goss_on(s) || threadIdx.x != 0) return;
-    GossState g = *s.gst;
-    const uint32_t *h = s.goss_hist + pass * 256;
-    int64_t above = 0;
-    int d = 255;
-    for (; d > 0; --d) {
-        if (g.rank < above + (int64_t)h[d]) break;
-        above += h[d];
+// The last pick: the threshold's low byte from pass 7's histogram.
+__global__ void k_goss_pick(DevState s) {
+    if (!goss_on(s) || threadIdx.x >= 64) return;
+    unsigned long long prefix = s.goss_sel[14];
+    long long rank = (long long)s.goss_sel[15];
+    const int d = goss_pick_wave(s.goss_hist + 7 * 256, rank);
+    prefix |= (unsigned long long)d;
+    if (threadIdx.x == 0) {
+        GossState g = *s.gst;
+        g.prefix = prefix;
+        g.rank = rank;
+        g.threshold = __longlong_as_double((long long)prefix);
+        *s.gst = g;
     }
-    g.rank -= above;
-    g.prefix |= (unsigned long long)d << (56 - 8 * pass);
-    if (pass == 7) g.threshold = __longlong_as_double((long long)g.prefix);
-    *s.gst = g;
 }
 
-// Blocks of 1024 rows: count of top rows (mode 0), of rows in the sample
-// (mode 1) or of rows kept by the sampling (mode 2) per block.
+// Rows of the GOSS kernels below come in blocks of 1024: a workgroup of 256
+// threads takes one, thread t the rows t, t + 256, t + 512 and t + 768 (each
+// load instruction reads consecutive rows; four rows per thread in flight).
+// Row j * 256 + w * 64 + lane of the block is slot j of lane `lane` of wave w.
+constexpr int kGossRowThreads = 256;
+
 __device__ __forceinline__ bool goss_top(const DevState &s, int64_t r, unsigned long long thr_bits) {
     return goss_key(s, r) >= thr_bits;
 }
 
-__global__ __launch_bounds__(1024) void k_goss_count(DevState s, int mode) {
-    __shared__ int wsum[16];
+// The sampling's kept bit of row r (the 64-row word is the same for the
+// whole wave: one broadcast load).
+__device__ __forceinline__ bool goss_kept_bit(const DevState &s, int64_t r) {
+    return (s.goss_mask[r >> 6] >> (r & 63)) & 1ULL;
+}
+
+// In-block exclusive prefix, in row order, of four flags per thread; returns
+// the block's total. wc: 4 x 4 ints of LDS.
+__device__ __forceinline__ int goss_block_prefix(const bool (&f)[4], int (&pre)[4], int (*wc)[4]) {
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    unsigned long long b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = __ballot(f[j]);
+    if (lane == 0)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wc[j][w] = __popcll(b[j]);
+    __syncthreads();
+    const unsigned long long lt = (1ULL << lane) - 1ULL;
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int tj = 0, bw = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = wc[j][i];
+            tj += c;
+            bw += i < w ? c : 0;
+        }
+        pre[j] = base + bw + __popcll(b[j] & lt);
+        base += tj;
+    }
+    return base;
+}
+
+// The block's count of four flags per thread (thread 0 gets it).
+__device__ __forceinline__ int goss_block_count(const bool (&f)[4], int *wc) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c += __popcll(__ballot(f[j]));
+    if (lane_id() == 0) wc[threadIdx.x >> 6] = c;
+    __syncthreads();
+    return wc[0] + wc[1] + wc[2] + wc[3];
+}
+
+// Per block of 1024 rows: count of top rows (mode 0), of rows in the sample
+// (mode 1) or of rows kept by the sampling (mode 2).
+__global__ __launch_bounds__(kGossRowThreads) void k_goss_count(DevState s, int mode) {
+    __shared__ int wc[4];
     if (!goss_on(s)) return;
-    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    bool in = false;
-    if (r < s.n) {
-        if (mode == 0) {
-            in = goss_top(s, r, (unsigned long long)__double_as_longlong(s.gst->threshold));
-        } else {
-            const bool other = (s.goss_mask[r >> 6] >> (r & 63)) & 1ULL;
-            in = mode == 2 ? other : (s.goss_kappa[r] == INT_MIN || other);
+    const int64_t n = s.n, r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const unsigned long long thr = mode == 0 ? (unsigned long long)__double_as_longlong(s.gst->threshold) : 0ULL;
+    bool in[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        in[j] = false;
+        if (r < n) {
+            if (mode == 0) {
+                in[j] = goss_top(s, r, thr);
+            } else {
+                const bool other = goss_kept_bit(s, r);
+                in[j] = mode == 2 ? other : (s.goss_kappa[r] == INT_MIN || other);
+            }
         }
     }
-    const unsigned long long b = __ballot(in);
-    if (lane_id() == 0) wsum[threadIdx.x >> 6] = __popcll(b);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int t = 0;
-        for (int i = 0; i < 16; ++i) t += wsum[i];
-        s.goss_blk[blockIdx.x] = t;
-    }
+    const int t = goss_block_count(in, wc);
+    if (threadIdx.x == 0) s.goss_blk[blockIdx.x] = t;
 }
 
 // Exclusive prefix of per-block counts, in place (one block); the total
@@ -893,17 +1046,6 @@ __global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, in
     }
 }
 
-// In-block exclusive prefix of a flag (1024 threads, one row each).
-__device__ __forceinline__ int block_excl_prefix(bool flag, int *wsum) {
-    const int lane = lane_id(), w = threadIdx.x >> 6;
-    const unsigned long long b = __ballot(flag);
-    if (lane == 0) wsum[w] = __popcll(b);
-    __syncthreads();
-    int before = 0;
-    for (int i = 0; i < w; ++i) before += wsum[i];
-    return before + __popcll(b & ((1ULL << lane) - 1ULL));
-}
-
 // kappa of every row, then its class against a predicted band of the count:
 // before row r the count is expected at K (1 - rest_r / N) (selection
 // sampling takes a uniform K-subset of the N = n - top_k other rows) with a
@@ -913,84 +1055,104 @@ __device__ __forceinline__ int block_excl_prefix(bool flag, int *wsum) {
 // count verifies; the rows in between are left to the sequential count.
 // Class (in goss_other): 0 dropped, 1 kept, 2 open. Kept rows' bits go to
 // goss_mask; per block the kept (goss_blk) and open (goss_blk_u) counts.
-__global__ __launch_bounds__(1024) void k_goss_kappa(DevState s) {
-    __shared__ int wsum[16], wk[16], wu[16];
+__global__ __launch_bounds__(kGossRowThreads) void k_goss_kappa(DevState s) {
+    __shared__ int wc[4][4], wk[4], wu[4];
     if (!goss_on(s)) return;
     const GossState g = *s.gst;
     const int64_t n = s.n;
-    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const int64_t top_before_blk = s.goss_blk[blockIdx.x];
     const unsigned long long thr = (unsigned long long)__double_as_longlong(g.threshold);
-    const bool top = r < n && goss_top(s, r, thr);
-    const int pre = block_excl_prefix(top, wsum);
-    int cls = 0;
-    if (r < n && !top) {
-        const int64_t n_top = top_before_blk + pre;
-        const int64_t rest = (n - r) - (g.top_k - n_top);
-        const int64_t K = g.other_k;
-        int64_t kappa;
-        if (rest <= 0) {
-            kappa = K;  // the reference keeps the row iff rows are still needed
-        } else {
-            const uint64_t stream = splitmix64((uint64_t)(s.hp.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
-                                               ((uint64_t)s.round->round * kGolden));
-            const double u = uniform53(stream + (uint64_t)r);
-            auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
-            int64_t c = (int64_t)floor((double)K - u * (double)rest);
-            if (c < 0) c = 0;
-            if (c > K) c = K;
-            while (c > 0 && !keep(c - 1)) --c;
-            while (c < K && keep(c)) ++c;
-            kappa = c;
-        }
-        s.goss_kappa[r] = (int32_t)kappa;
-        const double N = (double)(n - g.top_k);
-        double f = N > 0.0 ? 1.0 - (double)(rest > 0 ? rest : 0) / N : 1.0;
-        f = f < 0.0 ? 0.0 : (f > 1.0 ? 1.0 : f);
-        const double expect = (double)K * f;
-        const double var = N > 1.0 ? (double)K * f * (1.0 - f) * (N - (double)K) / (N - 1.0) : 0.0;
-        const double d = s.hp.goss_band * sqrt(var > 0.0 ? var : 0.0) + 64.0;
-        cls = (double)kappa > expect + d ? 1 : ((double)kappa <= expect - d ? 0 : 2);
-    } else if (r < n) {
-        s.goss_kappa[r] = INT_MIN;
+    bool top[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        top[j] = r < n && goss_top(s, r, thr);
     }
-    if (r < n) s.goss_other[r] = (uint8_t)cls;
-    const unsigned long long km = __ballot(cls == 1), um = __ballot(cls == 2);
-    const int64_t r0 = (int64_t)blockIdx.x * 1024 + w * 64;
+    int pre[4];
+    goss_block_prefix(top, pre, wc);
+    const uint64_t stream = splitmix64((uint64_t)(s.hp.goss_seed & 0x7FFFFFFFFFFFFFFFLL) ^
+                                       ((uint64_t)s.round->round * kGolden));
+    const int64_t K = g.other_k;
+    const double N = (double)(n - g.top_k);
+    int nk = 0, nu = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        int cls = 0;
+        if (r < n && !top[j]) {
+            const int64_t n_top = top_before_blk + pre[j];
+            const int64_t rest = (n - r) - (g.top_k - n_top);
+            int64_t kappa;
+            if (rest <= 0) {
+                kappa = K;  // the reference keeps the row iff rows are still needed
+            } else {
+                const double u = uniform53(stream + (uint64_t)r);
+                auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
+                int64_t c = (int64_t)floor((double)K - u * (double)rest);
+                if (c < 0) c = 0;
+                if (c > K) c = K;
+                while (c > 0 && !keep(c - 1)) --c;
+                while (c < K && keep(c)) ++c;
+                kappa = c;
+            }
+            s.goss_kappa[r] = (int32_t)kappa;
+            double f = N > 0.0 ? 1.0 - (double)(rest > 0 ? rest : 0) / N : 1.0;
+            f = f < 0.0 ? 0.0 : (f > 1.0 ? 1.0 : f);
+            const double expect = (double)K * f;
+            const double var = N > 1.0 ? (double)K * f * (1.0 - f) * (N - (double)K) / (N - 1.0) : 0.0;
+            const double d = s.hp.goss_band * sqrt(var > 0.0 ? var : 0.0) + 64.0;
+            cls = (double)kappa > expect + d ? 1 : ((double)kappa <= expect - d ? 0 : 2);
+        } else if (r < n) {
+            s.goss_kappa[r] = INT_MIN;
+        }
+        if (r < n) s.goss_other[r] = (uint8_t)cls;
+        const unsigned long long km = __ballot(cls == 1), um = __ballot(cls == 2);
+        const int64_t rw = (int64_t)blockIdx.x * 1024 + j * 256 + w * 64;
+        if (lane == 0 && rw < n) s.goss_mask[rw >> 6] = km;
+        nk += __popcll(km);
+        nu += __popcll(um);
+    }
     if (lane == 0) {
-        if (r0 < n) s.goss_mask[r0 >> 6] = km;
-        wk[w] = __popcll(km);
-        wu[w] = __popcll(um);
+        wk[w] = nk;
+        wu[w] = nu;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int tk = 0, tu = 0;
-        for (int i = 0; i < 16; ++i) {
-            tk += wk[i];
-            tu += wu[i];
-        }
-        s.goss_blk[blockIdx.x] = tk;
-        s.goss_blk_u[blockIdx.x] = tu;
+        s.goss_blk[blockIdx.x] = wk[0] + wk[1] + wk[2] + wk[3];
+        s.goss_blk_u[blockIdx.x] = wu[0] + wu[1] + wu[2] + wu[3];
     }
 }
 
 // The open rows in row order, each with its kappa less the kept rows before
 // it, which turns their decisions into the same sequential count.
-__global__ __launch_bounds__(1024) void k_goss_compact(DevState s) {
-    __shared__ int wk[16], wu[16];
+__global__ __launch_bounds__(kGossRowThreads) void k_goss_compact(DevState s) {
+    __shared__ int wk[4][4], wu[4][4];
     if (!goss_on(s)) return;
     const int64_t n = s.n;
-    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    const int cls = r < n ? (int)s.goss_other[r] : 0;
-    const int pk = block_excl_prefix(cls == 1, wk);
-    const int pu = block_excl_prefix(cls == 2, wu);
-    if (cls == 2) {
-        const int64_t pos = (int64_t)s.goss_blk_u[blockIdx.x] + pu;
-        const int64_t kept_before = (int64_t)s.goss_blk[blockIdx.x] + pk;
-        s.goss_ukappa[pos] = (int32_t)((int64_t)s.goss_kappa[r] - kept_before);
-        s.goss_urow[pos] = (int32_t)r;
+    const int64_t r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    int cls[4];
+    bool fk[4], fu[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        cls[j] = r < n ? (int)s.goss_other[r] : 0;
+        fk[j] = cls[j] == 1;
+        fu[j] = cls[j] == 2;
     }
+    int pk[4], pu[4];
+    goss_block_prefix(fk, pk, wk);
+    goss_block_prefix(fu, pu, wu);
+    const int64_t kb = s.goss_blk[blockIdx.x], ub = s.goss_blk_u[blockIdx.x];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (fu[j]) {
+            const int64_t r = r0 + j * 256;
+            const int64_t pos = ub + pu[j];
+            s.goss_ukappa[pos] = (int32_t)((int64_t)s.goss_kappa[r] - (kb + pk[j]));
+            s.goss_urow[pos] = (int32_t)r;
+        }
 }
 
 // Decisions of the open rows into goss_mask.
@@ -1008,18 +1170,27 @@ __global__ __launch_bounds__(256) void k_goss_apply(DevState s) {
 // The check: the sequential count keeps row r iff the rows it kept before r
 // number less than kappa_r, so kept flags that satisfy this at every row are
 // its result. goss_blk holds the exclusive prefix of kept rows per block.
-__global__ __launch_bounds__(1024) void k_goss_verify(DevState s) {
-    __shared__ int wsum[16];
+__global__ __launch_bounds__(kGossRowThreads) void k_goss_verify(DevState s) {
+    __shared__ int wc[4][4];
     if (!goss_on(s)) return;
     const int64_t n = s.n;
-    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    const bool kept = r < n && ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
-    const int pre = block_excl_prefix(kept, wsum);
-    if (r < n) {
-        const int64_t before = (int64_t)s.goss_blk[blockIdx.x] + pre;
-        const int32_t k = s.goss_kappa[r];
-        if ((before < (int64_t)k) != kept) atomicOr(&s.gst->fallback, 1);
+    const int64_t r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    bool kept[4];
+    int32_t k[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        kept[j] = r < n && goss_kept_bit(s, r);
+        k[j] = r < n ? s.goss_kappa[r] : 0;
     }
+    int pre[4];
+    goss_block_prefix(kept, pre, wc);
+    const int64_t kb = s.goss_blk[blockIdx.x];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (r0 + j * 256 < n) bad |= (kb + pre[j] < (int64_t)k[j]) != kept[j];
+    if (__ballot(bad) && lane_id() == 0) atomicOr(&s.gst->fallback, 1);
 }
 
 // One 64-row slice of the count: rows whose kappa exceeds the count by 64 or
@@ -1151,20 +1322,33 @@ __global__ __launch_bounds__(1024) void k_goss_walk(DevState s, int list) {
 }
 #undef MB_GOSS_LOAD
 
-__global__ __launch_bounds__(1024) void k_goss_scatter(DevState s) {
-    __shared__ int wsum[16];
+__global__ __launch_bounds__(kGossRowThreads) void k_goss_scatter(DevState s) {
+    __shared__ int wc[4][4];
     if (!goss_on(s)) return;
     const int64_t n = s.n;
-    const int64_t r = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    bool top = false, other = false;
-    if (r < n) {
-        top = s.goss_kappa[r] == INT_MIN;
-        other = !top && ((s.goss_mask[r >> 6] >> (r & 63)) & 1ULL);
+    const int64_t r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    bool in[4], other[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        bool top = false;
+        other[j] = false;
+        if (r < n) {
+            top = s.goss_kappa[r] == INT_MIN;
+            other[j] = !top && goss_kept_bit(s, r);
+        }
+        in[j] = top || other[j];
     }
-    const int pre = block_excl_prefix(top || other, wsum);
-    if (r < n) {
-        if (top || other) s.goss_rows[(int64_t)s.goss_blk[blockIdx.x] + pre] = (int32_t)r;
-        s.goss_other[r] = other ? 1 : 0;
+    int pre[4];
+    goss_block_prefix(in, pre, wc);
+    const int64_t base = s.goss_blk[blockIdx.x];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = r0 + j * 256;
+        if (r < n) {
+            if (in[j]) s.goss_rows[base + pre[j]] = (int32_t)r;
+            s.goss_other[r] = other[j] ? 1 : 0;
+        }
     }
 }
 
@@ -1474,6 +1658,10 @@ using WAcc16 = WAccT<true>;
 // tile's records and stores that tile's features of its partial.
 constexpr int kRootUnroll = 4;
 constexpr int kAccUnroll = 1;
+#ifndef MB_ACC_UNROLL_F
+#define MB_ACC_UNROLL_F 1
+#endif
+constexpr int kAccUnrollF = MB_ACC_UNROLL_F;
 
 // The value of the last lane of each LPR-lane group, on every lane of the
 // group, by DPP (a VALU operand modifier): unlike a crossbar shuffle it does
@@ -1860,8 +2048,8 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
         const int buf = __builtin_amdgcn_readlane(ait.buf, q);
         Acc::template zero<LPR>(lds, Ft, ls);
         __syncthreads();
-        accumulate_rows<LPR, Acc, true, false, kAccUnroll>(s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec,
-                                                           goss_mult);
+        accumulate_rows<LPR, Acc, true, false, std::is_same<Acc, FAcc>::value ? kAccUnrollF : kAccUnroll>(
+            s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec, goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next task
@@ -4534,34 +4722,32 @@ hipError_t launch_softmax(const DevState &s, int grid, hipStream_t st) {
 hipError_t launch_goss(const DevState &s, int grid_rows, hipStream_t st) {
     if (s.hp.num_class > 1) hipLaunchKernelGGL(k_goss_importance, dim3(grid_rows), dim3(256), 0, st, s);
     hipLaunchKernelGGL(k_goss_setup, dim3(1), dim3(256), 0, st, s);
-    const int grid = 1024;
-    for (int pass = 0; pass < 8; ++pass) {
-        hipLaunchKernelGGL(k_goss_digits, dim3(grid), dim3(256), 0, st, s, pass);
-        hipLaunchKernelGGL(k_goss_pick, dim3(1), dim3(64), 0, st, s, pass);
-    }
+    for (int pass = 0; pass < 8; ++pass)
+        hipLaunchKernelGGL(k_goss_digits, dim3(kGossDigitBlocks), dim3(256), 0, st, s, pass);
+    hipLaunchKernelGGL(k_goss_pick, dim3(1), dim3(64), 0, st, s);
     const dim3 blocks(s.goss_nblk);
     const size_t walk_lds = (size_t)2 * kGossTile * sizeof(int32_t);
     int64_t *n_unc = &s.gst->n_uncertain;
     int64_t *bag_n = &s.gst->bag_n;
     // top rows: counts, prefix; kappa and the band's classes
-    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 0);
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 0);
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
-    hipLaunchKernelGGL(k_goss_kappa, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_kappa, blocks, dim3(kGossRowThreads), 0, st, s);
     // the open rows: list, sequential count, decisions
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk_u, n_unc);
-    hipLaunchKernelGGL(k_goss_compact, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_compact, blocks, dim3(kGossRowThreads), 0, st, s);
     hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 1);
     hipLaunchKernelGGL(k_goss_apply, dim3(256), dim3(256), 0, st, s);
     // the check, and the full count when it fails
-    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 2);
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 2);
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
-    hipLaunchKernelGGL(k_goss_verify, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_verify, blocks, dim3(kGossRowThreads), 0, st, s);
     hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 0);
     // the sample: top rows and kept rows, ascending
-    hipLaunchKernelGGL(k_goss_count, blocks, dim3(1024), 0, st, s, 1);
+    hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 1);
     hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, bag_n);
-    hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(1024), 0, st, s);
+    hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(kGossRowThreads), 0, st, s);
     return hipGetLastError();
 }
 hipError_t launch_goss_stats(const DevState &s, int grid_rows, hipStream_t st) {

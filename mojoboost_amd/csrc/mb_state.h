@@ -153,6 +153,7 @@ constexpr int kHistBlocksPerCU = MB_HIST_BPC;
 
 // Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
 constexpr int kGossTileRows = 16384;
+constexpr int kGossDigitBlocks = 1024;  // blocks of a radix-select pass, each a contiguous row range
 
 // The state of a run before its first tree: no sampling, unit GOSS weight.
 inline Round initial_round() {
@@ -279,6 +280,9 @@ struct DevState {
     // GOSS (fp32 path)
     GossState *gst;
     uint32_t *goss_hist;        // 8 passes x 256 digit counts
+    unsigned long long *goss_sel;   // 8 x (prefix, rank): the radix select's state after each pick
+    unsigned long long *goss_cand;  // n: per select block, the keys that match the 16-bit prefix
+    int32_t *goss_ccnt;         // kGossDigitBlocks: their counts
     int32_t *goss_kappa;        // n: top row -> INT_MIN, else the count bound of the sampling
     unsigned long long *goss_mask;  // ceil(n / 64): rows kept by the sampling
     int32_t *goss_blk;          // per 1024-row block counts, then their exclusive prefix
