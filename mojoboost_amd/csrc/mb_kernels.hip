@@ -1046,6 +1046,17 @@ __global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, in
     }
 }
 
+// u < a / rest in binary64 (a = K - count and rest exact integers), as the
+// reference compares the draw with the keep probability: the sign of
+// u rest - a is exact from one fma (u rest - a is a multiple of 2^-53), so
+// the rounded quotient is computed only when u lies within a few of its ulps.
+__device__ __forceinline__ bool goss_keep(double u, double a, double rest) {
+    const double e = fma(u, rest, -a);
+    if (e >= 0.0) return false;        // u >= a / rest: the rounded quotient is at most u
+    if (e < -a * 0x1p-50) return true;  // below the quotient by more than its rounding
+    return u < a / rest;
+}
+
 // kappa of every row, then its class against a predicted band of the count:
 // before row r the count is expected at K (1 - rest_r / N) (selection
 // sampling takes a uniform K-subset of the N = n - top_k other rows) with a
@@ -1076,6 +1087,8 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_kappa(DevState s) {
                                        ((uint64_t)s.round->round * kGolden));
     const int64_t K = g.other_k;
     const double N = (double)(n - g.top_k);
+    const double inv_n = N > 0.0 ? 1.0 / N : 0.0;
+    const double cvar = N > 1.0 ? (double)K * (N - (double)K) / (N - 1.0) : 0.0;
     int nk = 0, nu = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1089,7 +1102,8 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_kappa(DevState s) {
                 kappa = K;  // the reference keeps the row iff rows are still needed
             } else {
                 const double u = uniform53(stream + (uint64_t)r);
-                auto keep = [&](int64_t cnt) { return u < (double)(K - cnt) / (double)rest; };
+                const double drest = (double)rest;
+                auto keep = [&](int64_t cnt) { return goss_keep(u, (double)(K - cnt), drest); };
                 int64_t c = (int64_t)floor((double)K - u * (double)rest);
                 if (c < 0) c = 0;
                 if (c > K) c = K;
@@ -1098,11 +1112,12 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_kappa(DevState s) {
                 kappa = c;
             }
             s.goss_kappa[r] = (int32_t)kappa;
-            double f = N > 0.0 ? 1.0 - (double)(rest > 0 ? rest : 0) / N : 1.0;
+            // the band needs no exact rounding (the check decides)
+            double f = N > 0.0 ? 1.0 - (double)(rest > 0 ? rest : 0) * inv_n : 1.0;
             f = f < 0.0 ? 0.0 : (f > 1.0 ? 1.0 : f);
             const double expect = (double)K * f;
-            const double var = N > 1.0 ? (double)K * f * (1.0 - f) * (N - (double)K) / (N - 1.0) : 0.0;
-            const double d = s.hp.goss_band * sqrt(var > 0.0 ? var : 0.0) + 64.0;
+            const double var = cvar * f * (1.0 - f);
+            const double d = s.hp.goss_band * (double)sqrtf((float)(var > 0.0 ? var : 0.0)) + 64.0;
             cls = (double)kappa > expect + d ? 1 : ((double)kappa <= expect - d ? 0 : 2);
         } else if (r < n) {
             s.goss_kappa[r] = INT_MIN;
