@@ -1549,20 +1549,13 @@ struct FAcc {
         for (int i = threadIdx.x; i < 2 * F * ls; i += blockDim.x) g[i] = 0.0;
         for (int i = threadIdx.x; i < F * ls; i += blockDim.x) c[i] = 0u;
     }
-    // goss_mult: the GOSS weight of rows the sampling kept (1 outside GOSS
-    // rounds); goss.apply_goss_scaling multiplies their g and h in fp64
+    // gv, hv: the row's derivatives in binary64 with its GOSS weight applied
+    // (accumulate_rows loads them with the record)
     template <int LPR>
-    __device__ static void add(unsigned char *lds, const DevState &s, const uint4 &w, int sub, int F, int ls,
-                               int64_t row, uint32_t, double goss_mult) {
+    __device__ static void add(unsigned char *lds, const uint4 &w, int sub, int F, int ls, double gv, double hv) {
         double *g = (double *)lds;
         double *h = g + (size_t)F * ls;
         uint32_t *c = (uint32_t *)(h + (size_t)F * ls);
-        double gv = s.hp.grad64 ? s.grad64[row] : (double)s.grad[row];
-        double hv = s.hp.grad64 ? s.hess64[row] : (double)s.hess[row];
-        if (goss_mult != 1.0 && s.goss_other != nullptr && s.goss_other[row]) {
-            gv *= goss_mult;
-            hv *= goss_mult;
-        }
         const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -1739,8 +1732,17 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     float qv[U], qv2[U], qv_nxt[U], qv2_nxt[U];
     uint32_t qw = 0u, qw_nxt = 0u;
     const bool q_goss = kQ && qc->gs_on;
-    auto load_recs = [&](int64_t, const int32_t *id, uint4 *w, float *v, float *v2, uint32_t &wb) {
+    // fp32 cells (FAcc): each row's derivatives (binary32 bits, or binary64
+    // with grad64) and GOSS weight bit, loaded with the record a step ahead
+    constexpr bool kF = std::is_same<Acc, FAcc>::value;
+    const bool f64 = kF && s.hp.grad64;
+    const bool f_goss = kF && goss_mult != 1.0 && s.goss_other != nullptr;
+    unsigned long long fg[U], fh[U], fg_nxt[U], fh_nxt[U];
+    uint32_t fw = 0u, fw_nxt = 0u;
+    auto load_recs = [&](int64_t, const int32_t *id, uint4 *w, float *v, float *v2, uint32_t &wb,
+                         unsigned long long *xg, unsigned long long *xh, uint32_t &xw) {
         wb = 0u;
+        xw = 0u;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t r = (uint32_t)id[u] < n32 ? (uint32_t)id[u] : 0u;  // ids come from the row lists
@@ -1750,10 +1752,20 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                 if constexpr (LPR == 1) v2[u] = s.hess[r];
                 if (q_goss) wb |= (s.goss_other[r] ? 1u : 0u) << u;
             }
+            if constexpr (kF) {
+                if (f64) {
+                    xg[u] = ((const unsigned long long *)s.grad64)[r];
+                    xh[u] = ((const unsigned long long *)s.hess64)[r];
+                } else {
+                    xg[u] = ((const uint32_t *)s.grad)[r];
+                    xh[u] = ((const uint32_t *)s.hess)[r];
+                }
+                if (f_goss) xw |= (s.goss_other[r] ? 1u : 0u) << u;
+            }
         }
     };
     auto accumulate = [&](int64_t i0, const int32_t *id, const uint4 *w, const float *v, const float *v2,
-                          uint32_t wb) {
+                          uint32_t wb, const unsigned long long *xg, const unsigned long long *xh, uint32_t xw) {
         uint32_t gh[U];
         if constexpr (kQ) {
 #pragma unroll
@@ -1796,14 +1808,27 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + (int64_t)u * rpp + rr;
-            if (i < hi) Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, (int64_t)(uint32_t)id[u], gh[u], goss_mult);
+            if constexpr (kF) {
+                // goss.apply_goss_scaling: the sampled small-gradient rows'
+                // g and h times the GOSS weight, in binary64
+                double gv = f64 ? __longlong_as_double((long long)xg[u]) : (double)__uint_as_float((uint32_t)xg[u]);
+                double hv = f64 ? __longlong_as_double((long long)xh[u]) : (double)__uint_as_float((uint32_t)xh[u]);
+                if ((xw >> u) & 1u) {
+                    gv *= goss_mult;
+                    hv *= goss_mult;
+                }
+                if (i < hi) FAcc::template add<LPR>(lds, w[u], sub, Ft, ls, gv, hv);
+            } else {
+                if (i < hi)
+                    Acc::template add<LPR>(lds, s, w[u], sub, Ft, ls, (int64_t)(uint32_t)id[u], gh[u], goss_mult);
+            }
         }
     };
     int32_t id_cur[U], id_nxt[U], id_nn[U];
     uint4 w_cur[U], w_nxt[U];
     int64_t i0 = lo;
     load_ids(i0, id_cur);
-    load_recs(i0, id_cur, w_cur, qv, qv2, qw);
+    load_recs(i0, id_cur, w_cur, qv, qv2, qw, fg, fh, fw);
     load_ids(i0 + step, id_nxt);
     // The next step's loads are issued unconditionally (past the range they
     // re-read the last row): under a branch, the compiler's wait for the
@@ -1811,9 +1836,9 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     // no longer overlap the LDS atomics.
     for (;;) {
         const bool more = i0 + step < hi;
-        load_recs(i0 + step, id_nxt, w_nxt, qv_nxt, qv2_nxt, qw_nxt);
+        load_recs(i0 + step, id_nxt, w_nxt, qv_nxt, qv2_nxt, qw_nxt, fg_nxt, fh_nxt, fw_nxt);
         load_ids(i0 + 2 * step, id_nn);
-        accumulate(i0, id_cur, w_cur, qv, qv2, qw);
+        accumulate(i0, id_cur, w_cur, qv, qv2, qw, fg, fh, fw);
         if (!more) break;
         i0 += step;
 #pragma unroll
@@ -1825,8 +1850,13 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                 qv[u] = qv_nxt[u];
                 if constexpr (LPR == 1) qv2[u] = qv2_nxt[u];
             }
+            if constexpr (kF) {
+                fg[u] = fg_nxt[u];
+                fh[u] = fh_nxt[u];
+            }
         }
         qw = qw_nxt;
+        fw = fw_nxt;
     }
 }
 
