@@ -953,12 +953,13 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                         HIPX(mb::launch_accum(s, st));
                     }
                     HIPX(mb::launch_scan(s, 0, st));
-                    HIPX(mb::launch_plan(s, 0, st));
+                    // the group's last planning launch also writes the header
+                    // into the pinned slot the host reads after the event
+                    HIPX(mb::launch_plan(s, 0, st, c == n - 1 ? &flags.p[slot] : nullptr));
                     if (timed) HIPX(hipEventRecord(ev_group(slot, c, 5), st));
                 }
                 pb_launches += n;
                 iters += n;
-                HIPX(hipMemcpyAsync(&flags.p[slot], s.batch, sizeof(mb::Batch), hipMemcpyDeviceToHost, st));
                 HIPX(hipEventRecord(events[slot], st));
                 if (k == 0) continue;
                 HIPX(hipEventSynchronize(events[1 - slot]));

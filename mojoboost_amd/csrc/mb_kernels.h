@@ -39,7 +39,7 @@ hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullp
 hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
-hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st);
+hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st, Batch *host = nullptr);
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
 // The score update fused with the next round's objective (single-output L2
 // and binary): after it, the next tree skips launch_objective.

@@ -3565,7 +3565,21 @@ __device__ void replay_wave(PlanView &v, int L, int &nl, int &nn, int &nc, int &
     }
 }
 
-__global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode) {
+// The batch header into pinned host memory by system-scope stores (they
+// reach host memory whatever the allocation's caching; the host reads them
+// after the launch's completion event).
+__device__ __forceinline__ void publish_header(Batch *host, const Batch &b) {
+    const int32_t *src = (const int32_t *)&b;
+    int32_t *dst = (int32_t *)host;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(Batch) / sizeof(int32_t)); ++i)
+        __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// host: when not null (the last planning launch of a group), the batch
+// header is also written there, to pinned host memory the host reads after
+// the group's event instead of copying the header with a launch of its own.
+__global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode, Batch *host) {
     extern __shared__ unsigned char plan_smem[];
     __shared__ Grow g;
     __shared__ int s_nc, s_done, s_ncand, s_nsel, s_total, s_x, s_vf;
@@ -3620,7 +3634,10 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     const int n_items = root_mode ? 1 : s.batch->n_items;
     const Round rd = *s.round;
     const int ne = root_mode ? 1 : s.grow->n_explored, nl0 = root_mode ? 1 : s.grow->n_leaves;
-    if (n_items <= 0) return;  // the tree is complete
+    if (n_items <= 0) {  // the tree is complete
+        if (host != nullptr && tid == 0) publish_header(host, *s.batch);
+        return;
+    }
     PlanView v = plan_view(s, plan_smem);
     if (rd.stopped) {
         // training has stopped: an empty tree, nothing to expand
@@ -3635,6 +3652,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.n_acc = 0;
             b.chunk_p = b.chunk_a = b.pad_ = 0;
             *s.batch = b;
+            if (host != nullptr) publish_header(host, b);
         }
         return;
     }
@@ -3908,6 +3926,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             b.n_acc = 0;
             b.chunk_p = b.chunk_a = b.pad_ = 0;
             *s.batch = b;
+            if (host != nullptr) publish_header(host, b);
         }
     };
     if (s_done) {
@@ -4355,6 +4374,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         b.chunk_a = (int32_t)chunk;
         b.pad_ = 0;
         *s.batch = b;
+        if (host != nullptr) publish_header(host, b);
     }
 }
 
@@ -4944,8 +4964,8 @@ hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
         hipLaunchKernelGGL(k_scan_f<false>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
     return hipGetLastError();
 }
-hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st) {
-    hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanThreads), plan_lds_bytes(s), st, s, root_mode);
+hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st, Batch *host) {
+    hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanThreads), plan_lds_bytes(s), st, s, root_mode, host);
     return hipGetLastError();
 }
 hipError_t launch_score(const DevState &s, int grid, hipStream_t st) {
