@@ -106,6 +106,7 @@ struct mbh_dataset {
     int n_cu = 0;
     uint8_t *d_records = nullptr, *d_bins_cm = nullptr;
     double *d_labels = nullptr;
+    uint8_t *d_labels8 = nullptr;  // the labels as bytes, when integers in [0, 255]
     int32_t *d_missing = nullptr, *d_widths = nullptr;
     std::vector<int32_t> missing, widths;
     // categories per feature (0: numerical), set by mbh_dataset_set_categorical
@@ -426,6 +427,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.records_w = ds->d_records;
     s.bins_cm = ds->d_bins_cm;
     s.labels = ds->d_labels;
+    s.labels8 = ds->d_labels8;
     s.weights = ds->d_weights;
     s.missing_bin = ds->d_missing;
     s.widths = ds->d_widths;
@@ -830,6 +832,12 @@ int32_t mbh_dataset_create(const uint8_t *bins_cm, int64_t n, int32_t F, int32_t
         ds->d_widths = dalloc<int32_t>(F, ds->owned);
         HIPX(hipMemcpy(ds->d_bins_cm, bins_cm, (size_t)F * n, hipMemcpyHostToDevice));
         HIPX(hipMemcpy(ds->d_labels, labels, (size_t)n * sizeof(double), hipMemcpyHostToDevice));
+        if (ds->labels_integral && hi <= 255.0) {
+            std::vector<uint8_t> l8((size_t)n);
+            for (int64_t r = 0; r < n; ++r) l8[(size_t)r] = (uint8_t)labels[r];
+            ds->d_labels8 = dalloc<uint8_t>(n, ds->owned);
+            HIPX(hipMemcpy(ds->d_labels8, l8.data(), (size_t)n, hipMemcpyHostToDevice));
+        }
         HIPX(hipMemcpy(ds->d_missing, ds->missing.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
         HIPX(hipMemcpy(ds->d_widths, ds->widths.data(), F * sizeof(int32_t), hipMemcpyHostToDevice));
         HIPX(hipDeviceSynchronize());

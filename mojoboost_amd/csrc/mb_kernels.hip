@@ -4511,6 +4511,9 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
 // never reads these g, h. With one feature tile of at most 32 bytes the
 // row's record is loaded whole (one or two 16-byte loads) into the thread's
 // LDS slot and the walk reads its bins there.
+// kL8: the labels as bytes (labels8, every label an integer in [0, 255]):
+// a row's label costs 1 byte of HBM instead of 8.
+template <bool kL8>
 __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
     extern __shared__ unsigned char score_smem[];
     __shared__ float red_g[4], red_h[4];
@@ -4567,7 +4570,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
             a = R[q * per];
             b = R[q * per + per - 1];
             raw = s.raw[q];
-            y = s.labels[q];
+            y = kL8 ? (double)s.labels8[q] : s.labels[q];
         };
         // two rows per step (r and r + stride), walked together
         uint8_t *mine2 = (uint8_t *)&srec[256 * 2 + threadIdx.x * 2];
@@ -4620,7 +4623,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
                 raw = fma(lr, tree.value[node], raw);
                 s.raw[r] = raw;
             }
-            objective(r, raw, s.labels[r]);
+            objective(r, raw, kL8 ? (double)s.labels8[r] : s.labels[r]);
         }
     }
     mg = wave_max(mg);
@@ -4891,7 +4894,8 @@ hipError_t prepare_kernels(const DevState &s) {
     MB_SET_LDS(k_plan, plan_lds_bytes(s));
     MB_SET_LDS(k_goss_walk, (size_t)2 * kGossTile * sizeof(int32_t));
     MB_SET_LDS(k_score, score_lds_bytes(s));
-    MB_SET_LDS(k_score_objective, score_lds_bytes(s));
+    MB_SET_LDS(k_score_objective<false>, score_lds_bytes(s));
+    MB_SET_LDS(k_score_objective<true>, score_lds_bytes(s));
     return hipSuccess;
 }
 // A launch of kernel k with DevState s; with both events given, the runtime
@@ -4973,7 +4977,10 @@ hipError_t launch_score(const DevState &s, int grid, hipStream_t st) {
     return hipGetLastError();
 }
 hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st) {
-    hipLaunchKernelGGL(k_score_objective, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
+    if (s.labels8 != nullptr)
+        hipLaunchKernelGGL(k_score_objective<true>, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
+    else
+        hipLaunchKernelGGL(k_score_objective<false>, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
     return hipGetLastError();
 }
 hipError_t launch_round_end(const DevState &s, hipStream_t st) {

@@ -229,6 +229,7 @@ struct DevState {
     const uint8_t *records;
     const uint8_t *bins_cm;  // F x n, column-major (partition, score update)
     const double *labels;    // n
+    const uint8_t *labels8;  // n, when every label is an integer in [0, 255] (else null)
     const double *weights;   // n sample weights, or null (unweighted)
     const int32_t *qid;      // n: each row's query when lambdarank bags by query, else null
     const int64_t *bag_fallback;  // per bag index: the unit an empty bag takes, or -1 (null: none)
