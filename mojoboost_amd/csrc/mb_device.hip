@@ -112,6 +112,9 @@ struct mbh_dataset {
     // categories per feature (0: numerical), set by mbh_dataset_set_categorical
     std::vector<int32_t> ncat;
     int32_t *d_ncat = nullptr;
+    // the scan's feature order when some feature is categorical: the
+    // category-set features first (their tasks run longest), then the others
+    int32_t *d_scan_order = nullptr;
     bool any_cat = false;
     double label_sum = 0.0;  // sequential sum, for the base score
     std::vector<double> class_count;  // when labels are integers in [0, 1024)
@@ -432,6 +435,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.missing_bin = ds->d_missing;
     s.widths = ds->d_widths;
     s.ncat = ds->any_cat ? ds->d_ncat : nullptr;
+    s.scan_order = ds->any_cat ? ds->d_scan_order : nullptr;
     s.n = ds->n;
     s.n_features = F;
     s.n_bins = ds->nb;
@@ -756,6 +760,13 @@ int32_t mbh_dataset_set_categorical(mbh_dataset *ds, const int32_t *ncat, char *
         for (int f = 0; f < ds->F; ++f) ds->any_cat = ds->any_cat || ncat[f] > 0;
         if (!ds->d_ncat) ds->d_ncat = dalloc<int32_t>(ds->F, ds->owned);
         HIPX(hipMemcpy(ds->d_ncat, ds->ncat.data(), ds->F * sizeof(int32_t), hipMemcpyHostToDevice));
+        std::vector<int32_t> order;
+        for (int f = 0; f < ds->F; ++f)
+            if (ncat[f] > 0) order.push_back(f);
+        for (int f = 0; f < ds->F; ++f)
+            if (ncat[f] <= 0) order.push_back(f);
+        if (!ds->d_scan_order) ds->d_scan_order = dalloc<int32_t>(ds->F, ds->owned);
+        HIPX(hipMemcpy(ds->d_scan_order, order.data(), ds->F * sizeof(int32_t), hipMemcpyHostToDevice));
     } catch (const Error &e) {
         set_err(err, err_len, e.msg);
         return e.code;

@@ -2155,8 +2155,18 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
         hmin = (long long)fl;
     }
     for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
-        const int j = task / F;
-        const int f = task - j * F;
+        // with category-set features, tasks go feature-major in scan_order
+        // (those features first: their searches run longest, so the
+        // shorter numerical tasks fill in behind them)
+        int j, f;
+        if (kCat && s.scan_order != nullptr) {
+            const int pos = task / n_items;
+            j = task - pos * n_items;
+            f = s.scan_order[pos];
+        } else {
+            j = task / F;
+            f = task - j * F;
+        }
         Item it;
         int64_t m_built, m_sib;
         if (root_mode) {
@@ -2820,8 +2830,18 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
     const double l1 = hp.lambda_l1, l2 = hp.lambda_l2, min_h = hp.min_sum_hessian;
     const long long min_c = hp.min_data_in_leaf;
     for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
-        const int j = task / F;
-        const int f = task - j * F;
+        // with category-set features, tasks go feature-major in scan_order
+        // (those features first: their searches run longest, so the
+        // shorter numerical tasks fill in behind them)
+        int j, f;
+        if (kCat && s.scan_order != nullptr) {
+            const int pos = task / n_items;
+            j = task - pos * n_items;
+            f = s.scan_order[pos];
+        } else {
+            j = task / F;
+            f = task - j * F;
+        }
         Item it;
         int64_t m_built, m_sib;
         if (root_mode) {

@@ -237,6 +237,7 @@ struct DevState {
     const int32_t *missing_bin;  // F
     const int32_t *widths;       // F: realized bin count bound
     const int32_t *ncat;         // F: categories of a categorical feature (bins 1..ncat), 0 numerical; null: none
+    const int32_t *scan_order;  // F, with ncat: scan task order of the features (category-set ones first)
     const uint8_t *feature_mask; // num_trees x F (1: the tree may split it)
     uint8_t *records_w;          // same buffer as records, writable view
     int64_t n;
