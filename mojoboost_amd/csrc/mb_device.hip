@@ -447,7 +447,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.prob = K > 1 ? dalloc<double>((size_t)ds->n * K, run.owned) : nullptr;
     s.grad = dalloc<float>(ds->n, run.owned);
     s.hess = dalloc<float>(ds->n, run.owned);
-    s.stats = dalloc<uint32_t>(4, run.owned);
+    s.stats = dalloc<uint32_t>(4 * mb::kStatSlots, run.owned);
     s.round = dalloc<mb::Round>(1, run.owned);
     s.rows0 = dalloc<int32_t>(ds->n, run.owned);
     s.rows1 = dalloc<int32_t>(ds->n, run.owned);
@@ -651,7 +651,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
         throw Error{MOJOTREES_ERROR_TRAINING, "internal: the feature tile exceeds one workgroup's LDS"};
     HIPX(hipMemset(s.rows0, 0, (size_t)ds->n * sizeof(int32_t)));
     HIPX(hipMemset(s.rows1, 0, (size_t)ds->n * sizeof(int32_t)));
-    HIPX(hipMemset(s.stats, 0, 4 * sizeof(uint32_t)));
+    HIPX(hipMemset(s.stats, 0, 4 * mb::kStatSlots * sizeof(uint32_t)));
     HIPX(hipMemset(s.batch, 0, sizeof(mb::Batch)));
     HIPX(hipMemset(s.grow, 0, sizeof(mb::Grow)));
     HIPX(hipMemset(s.part_items, 0, (size_t)s.kmax * sizeof(mb::PartItem)));
@@ -1036,6 +1036,11 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         fit->train_raw.resize((size_t)ds->n * K);
         HIPX(hipMemcpy(fit->train_raw.data(), s.raw, fit->train_raw.size() * sizeof(double),
                        hipMemcpyDeviceToHost));
+        if (K > 1) {  // the device's class-major scores to the row-major layout of the API
+            std::vector<double> cm(fit->train_raw);
+            for (int64_t r = 0; r < ds->n; ++r)
+                for (int k = 0; k < K; ++k) fit->train_raw[(size_t)r * K + k] = cm[(size_t)k * ds->n + r];
+        }
         const bool bagging = s.hp.bagging != 0 || s.hp.goss != 0;  // sampled rounds are skipped, not stops
         // algorithmic bytes per accumulated row: its bins plus its g/h pair
         // (int8 x 2 quantized, fp32 x 2 otherwise)

@@ -104,6 +104,20 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
+// max |g|, |h| of a tree's rows (binary32 bits: non-negative floats order
+// like their bits), by parity: the blocks of the objective kernels fold
+// their maxima into kStatSlots slots (block b into slot b mod kStatSlots),
+// so no single address takes an atomic from every block; readers fold the
+// slots.
+__device__ __forceinline__ int stat_slot(int parity, int which, int b) {
+    return (parity * 2 + which) * kStatSlots + (b & (kStatSlots - 1));
+}
+// Every lane of the wave calls it (one slot per lane).
+__device__ __forceinline__ float stats_max_wave(const DevState &s, int parity, int which) {
+    static_assert(kStatSlots == 64, "one slot per lane");
+    return __uint_as_float(wave_max_u32(s.stats[stat_slot(parity, which, lane_id())]));
+}
+
 __device__ __forceinline__ unsigned wave_min_u32(unsigned x) {
     x = min(x, dpp_u32<0xB1, 0xF>(x));
     x = min(x, dpp_u32<0x4E, 0xF>(x));
@@ -257,7 +271,7 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
         if (hp.objective == kObjMulticlass) {
             // _fill_softmax_grad_hess_at (boosting.mojo:3621-3678) on the
             // probabilities of the round's start
-            const double p = s.prob[r * K + ck];
+            const double p = s.prob[(size_t)ck * s.n + r];
             const double y = ((int)s.labels[r] == ck) ? 1.0 : 0.0;
             g = (float)(w * (p - y));
             double hh = factor * p * (1.0 - p);
@@ -295,8 +309,8 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
             mg = fmaxf(mg, red_g[i]);
             mh = fmaxf(mh, red_h[i]);
         }
-        atomicMax(&s.stats[rd.parity * 2 + 0], __float_as_uint(mg));
-        atomicMax(&s.stats[rd.parity * 2 + 1], __float_as_uint(mh));
+        atomicMax(&s.stats[stat_slot(rd.parity, 0, blockIdx.x)], __float_as_uint(mg));
+        atomicMax(&s.stats[stat_slot(rd.parity, 1, blockIdx.x)], __float_as_uint(mh));
     }
 }
 
@@ -479,24 +493,27 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
 // boosting._softmax_rows (src/mojotrees/boosting.mojo:3529-3573): per row,
 // shift by the maximum, exponentiate with the reference's exp, sum in class
 // order, divide. Run once at the start of each multiclass round; every class
-// tree of the round uses these probabilities.
+// tree of the round uses these probabilities. Raw scores and probabilities
+// of a multiclass training are class-major (class k of row r at k n + r), so
+// each class's pass reads and writes consecutive rows.
 __global__ __launch_bounds__(256) void k_softmax(DevState s) {
     if (s.round->stopped) return;
     const int K = s.hp.num_class;
+    const int64_t n = s.n;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
-        const double *x = s.raw + r * K;
-        double *p = s.prob + r * K;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+        const double *x = s.raw + r;
+        double *p = s.prob + r;
         double m = x[0];
         for (int i = 1; i < K; ++i)
-            if (x[i] > m) m = x[i];
+            if (x[(size_t)i * n] > m) m = x[(size_t)i * n];
         double total = 0.0;
         for (int i = 0; i < K; ++i) {
-            const double e = ref_exp(x[i] - m);
-            p[i] = e;
+            const double e = ref_exp(x[(size_t)i * n] - m);
+            p[(size_t)i * n] = e;
             total += e;
         }
-        for (int i = 0; i < K; ++i) p[i] = p[i] / total;
+        for (int i = 0; i < K; ++i) p[(size_t)i * n] = p[(size_t)i * n] / total;
     }
 }
 
@@ -533,12 +550,13 @@ __device__ __forceinline__ QCtx quant_ctx(const DevState &s, const Round &rd) {
     QCtx c;
     c.gs_on = goss_on(s);
     c.gmult = c.gs_on ? goss_weight(*s.gst, s.n) : 1.0;
+    const double sg = (double)stats_max_wave(s, rd.parity, 0), sh = (double)stats_max_wave(s, rd.parity, 1);
     double max_g = c.gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 0])
                    : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 0])
-                               : (double)__uint_as_float(s.stats[rd.parity * 2 + 0]);
+                               : sg;
     double max_h = c.gs_on ? __longlong_as_double((long long)s.goss_max[rd.parity * 2 + 1])
                    : hp.grad64 ? __longlong_as_double((long long)s.stats64[rd.parity * 2 + 1])
-                               : (double)__uint_as_float(s.stats[rd.parity * 2 + 1]);
+                               : sh;
     if (max_g < 1e-12) max_g = 1e-12;
     if (max_h < 1e-12) max_h = 1e-12;
     // max-abs: (B / 2) / max|g| and B / max|h| with clamps B / 2, B; the
@@ -600,8 +618,7 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
             s.round->grad_units = gu;
             s.round->hess_units = hu;
         }
-        s.stats[(1 - rd.parity) * 2 + 0] = 0u;
-        s.stats[(1 - rd.parity) * 2 + 1] = 0u;
+        for (int i = 0; i < 2 * kStatSlots; ++i) s.stats[stat_slot(1 - rd.parity, 0, 0) + i] = 0u;
         if (hp.grad64) {
             s.stats64[(1 - rd.parity) * 2 + 0] = 0ULL;
             s.stats64[(1 - rd.parity) * 2 + 1] = 0ULL;
@@ -714,7 +731,9 @@ __global__ void k_magfold(DevState s) {
     const double gu = fixed_point_scale_pow2(tg, okg);
     double hu;
     if (s.hp.const_hessian) {
-        double mh = (double)__uint_as_float(s.stats[rp->parity * 2 + 1]);
+        unsigned mb = 0u;
+        for (int i = 0; i < kStatSlots; ++i) mb = max(mb, s.stats[stat_slot(rp->parity, 1, i)]);
+        double mh = (double)__uint_as_float(mb);
         if (mh < 1e-12) mh = 1e-12;
         hu = 1.0 / mh;
     } else {
@@ -767,7 +786,7 @@ __global__ __launch_bounds__(256) void k_goss_importance(DevState s) {
         const int y = (int)s.labels[r];
         double imp = 0.0;
         for (int k = 0; k < K; ++k) {
-            const double p = s.prob[r * K + k];
+            const double p = s.prob[(size_t)k * s.n + r];
             const float g = (float)(w * (p - (y == k ? 1.0 : 0.0)));
             double hh = factor * p * (1.0 - p);
             if (hh < 1e-16) hh = 1e-16;
@@ -4518,7 +4537,7 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
             const int t = f / tf;
             return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
         });
-        double *slot = s.raw + r * K + k;
+        double *slot = s.raw + (size_t)k * s.n + r;  // class-major (k = 0 for a single output)
         *slot = fma(lr, tree.value[node], *slot);
     }
 }
@@ -4659,8 +4678,8 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
             mg = fmaxf(mg, red_g[i]);
             mh = fmaxf(mh, red_h[i]);
         }
-        atomicMax(&s.stats[np * 2 + 0], __float_as_uint(mg));
-        atomicMax(&s.stats[np * 2 + 1], __float_as_uint(mh));
+        atomicMax(&s.stats[stat_slot(np, 0, blockIdx.x)], __float_as_uint(mg));
+        atomicMax(&s.stats[stat_slot(np, 1, blockIdx.x)], __float_as_uint(mh));
     }
 }
 
@@ -4778,10 +4797,11 @@ __global__ __launch_bounds__(256) void k_predict(PredictArgs a) {
     }
 }
 
+// The initial raw scores, class-major: class k of row r at k n + r.
 __global__ __launch_bounds__(256) void k_fill_f64(double *p, int64_t n, int K, const double *base) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n * K; i += stride)
-        p[i] = base[i % K];
+        p[i] = base[i / n];
 }
 
 __global__ void k_exp_sigmoid(const double *x, double *e, double *sg, int64_t n) {

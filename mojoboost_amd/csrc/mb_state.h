@@ -153,6 +153,7 @@ constexpr int kHistBlocksPerCU = MB_HIST_BPC;
 
 // Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
 constexpr int kGossTileRows = 16384;
+constexpr int kStatSlots = 64;  // slots of each max |g|, |h| (parity x grad/hess x slot)
 constexpr int kGossDigitBlocks = 1024;  // blocks of a radix-select pass, each a contiguous row range
 
 // The state of a run before its first tree: no sampling, unit GOSS weight.
@@ -259,7 +260,7 @@ struct DevState {
     const double *rank_disc;        // 1 / log2(rank + 2) for ranks below the largest query
     int32_t n_queries;
     int32_t rank_pad;               // largest query rounded up to a power of two
-    uint32_t *stats;       // [2 parities][2]: max |g|, max |h| as float bits
+    uint32_t *stats;       // [2 parities][2][kStatSlots]: max |g|, max |h| as float bits, per slot
     // magnitude-sum lattice (hp.wide): each row's quantized (grad, hess)
     // interleaved, and the magnitude reduction's 256 + 256 binary32
     // workgroup sums (|g| then |h|)
