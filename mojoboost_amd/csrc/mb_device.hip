@@ -563,7 +563,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     if (hp.goss) {
         s.goss_nblk = (int32_t)((ds->n + 1023) / 1024);
         s.gst = dalloc<mb::GossState>(1, run.owned);
-        s.goss_hist = dalloc<uint32_t>(8 * 256, run.owned);
+        s.goss_hist = dalloc<uint32_t>(8 * mb::kGossHistSlots * 256, run.owned);
         s.goss_sel = dalloc<unsigned long long>(16, run.owned);
         s.goss_cand = dalloc<unsigned long long>(ds->n, run.owned);
         s.goss_ccnt = dalloc<int32_t>(mb::kGossDigitBlocks, run.owned);

@@ -799,7 +799,7 @@ __global__ __launch_bounds__(256) void k_goss_importance(DevState s) {
 
 __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
     if (!goss_on(s)) return;
-    for (int i = threadIdx.x; i < 8 * 256; i += blockDim.x) s.goss_hist[i] = 0u;
+    for (int i = threadIdx.x; i < 8 * kGossHistSlots * 256; i += blockDim.x) s.goss_hist[i] = 0u;
     if (threadIdx.x == 0) {
         GossState g;
         const int64_t n = s.n;
@@ -828,10 +828,21 @@ __global__ __launch_bounds__(256) void k_goss_setup(DevState s) {
 // The digit of the rank-th largest key (0-based, descending) in a 256-bin
 // digit histogram, by one wave: the highest digit whose count from the top
 // passes rank (digit 0 when none does); rank becomes the rank inside that
-// digit. Lane l holds digits 4l .. 4l + 3; counts are below n < 2^31.
+// digit. Lane l holds digits 4l .. 4l + 3; counts are below n < 2^31. h: the
+// pass's kGossHistSlots partial histograms (a block adds its counts into
+// slot blockIdx mod kGossHistSlots, so no counter takes an atomic from every
+// block), summed here.
 __device__ __forceinline__ int goss_pick_wave(const uint32_t *h, long long &rank) {
     const int lane = lane_id();
-    const uint4 c = ((const uint4 *)h)[lane];
+    uint4 c = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int k = 0; k < kGossHistSlots; ++k) {
+        const uint4 v = ((const uint4 *)(h + k * 256))[lane];
+        c.x += v.x;
+        c.y += v.y;
+        c.z += v.z;
+        c.w += v.w;
+    }
     const int t = (int)(c.x + c.y + c.z + c.w);
     const int incl = wave_incl_scan_i(t);
     const int total = __builtin_amdgcn_readlane(incl, 63);
@@ -881,7 +892,7 @@ __global__ __launch_bounds__(256) void k_goss_digits(DevState s, int pass) {
         } else {
             prefix = s.goss_sel[2 * (pass - 1)];
             rank = (long long)s.goss_sel[2 * (pass - 1) + 1];
-            const int d = goss_pick_wave(s.goss_hist + (pass - 1) * 256, rank);
+            const int d = goss_pick_wave(s.goss_hist + (pass - 1) * kGossHistSlots * 256, rank);
             prefix |= (unsigned long long)d << (56 - 8 * (pass - 1));
         }
         if (threadIdx.x == 0) {
@@ -940,7 +951,7 @@ __global__ __launch_bounds__(256) void k_goss_digits(DevState s, int pass) {
     }
     __syncthreads();
     const uint32_t v = hist[threadIdx.x];
-    if (v) atomicAdd(&s.goss_hist[pass * 256 + threadIdx.x], v);
+    if (v) atomicAdd(&s.goss_hist[(pass * kGossHistSlots + (blockIdx.x & (kGossHistSlots - 1))) * 256 + threadIdx.x], v);
     if (pass == 2 && threadIdx.x == 0) s.goss_ccnt[blockIdx.x] = s_nc;
 }
 
@@ -949,7 +960,7 @@ __global__ void k_goss_pick(DevState s) {
     if (!goss_on(s) || threadIdx.x >= 64) return;
     unsigned long long prefix = s.goss_sel[14];
     long long rank = (long long)s.goss_sel[15];
-    const int d = goss_pick_wave(s.goss_hist + 7 * 256, rank);
+    const int d = goss_pick_wave(s.goss_hist + 7 * kGossHistSlots * 256, rank);
     prefix |= (unsigned long long)d;
     if (threadIdx.x == 0) {
         GossState g = *s.gst;

@@ -153,6 +153,7 @@ constexpr int kHistBlocksPerCU = MB_HIST_BPC;
 
 // Rows per tile of the GOSS count; the kappa buffer is padded to whole tiles.
 constexpr int kGossTileRows = 16384;
+constexpr int kGossHistSlots = 8;  // partial digit histograms per radix pass
 constexpr int kStatSlots = 64;  // slots of each max |g|, |h| (parity x grad/hess x slot)
 constexpr int kGossDigitBlocks = 1024;  // blocks of a radix-select pass, each a contiguous row range
 
@@ -282,7 +283,7 @@ struct DevState {
     int64_t hist_chunk_limit;  // most rows a block may pack (field bounds)
     // GOSS (fp32 path)
     GossState *gst;
-    uint32_t *goss_hist;        // 8 passes x 256 digit counts
+    uint32_t *goss_hist;        // 8 passes x kGossHistSlots x 256 digit counts
     unsigned long long *goss_sel;   // 8 x (prefix, rank): the radix select's state after each pick
     unsigned long long *goss_cand;  // n: per select block, the keys that match the 16-bit prefix
     int32_t *goss_ccnt;         // kGossDigitBlocks: their counts
