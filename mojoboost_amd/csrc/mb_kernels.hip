@@ -4537,19 +4537,52 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     if (s.hp.num_class == 1 && n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
     const PackedTree tree = load_packed_tree(s, score_smem);
     const double lr = s.hp.learning_rate;
-    const int K = s.hp.num_class;
     const int k = s.round->class_k;
     const int rec = s.rec_bytes, tf = s.tile_f;
     const size_t tile_bytes = (size_t)s.n * rec;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < s.n; r += stride) {
+    const int64_t n = s.n;
+    double *raw = s.raw + (size_t)k * n;  // class-major (k = 0 for a single output)
+    const int64_t r0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s.n_tiles == 1 && rec <= 64) {
+        // one tile of at most 64 bytes: the row's record is copied into this
+        // thread's 64 LDS bytes and walked there, the next row's record and
+        // raw score loaded (unconditionally, the last row again past the
+        // end) while the current row walks
+        __shared__ uint4 srec[256 * 4];
+        uint4 *mine4 = srec + threadIdx.x * 4;
+        const uint8_t *mine = (const uint8_t *)mine4;
+        const uint4 *R = (const uint4 *)s.records;
+        const int per = rec / 16;  // 1, 2 or 4 uint4 per record
+        const int o1 = per > 1 ? 1 : 0, o2 = per > 2 ? 2 : per - 1, o3 = per - 1;
+        int64_t q = r0 < n ? r0 : n - 1;
+        uint4 c0 = R[q * per], c1 = R[q * per + o1], c2 = R[q * per + o2], c3 = R[q * per + o3];
+        double cv = raw[q];
+        for (int64_t r = r0; r < n; r += stride) {
+            q = r + stride < n ? r + stride : n - 1;
+            const uint4 n0 = R[q * per], n1 = R[q * per + o1], n2 = R[q * per + o2], n3 = R[q * per + o3];
+            const double nv = raw[q];
+            mine4[0] = c0;  // this thread's own bytes: no barrier
+            mine4[1] = c1;
+            mine4[2] = c2;
+            mine4[3] = c3;
+            const int node = walk_packed(tree, n_nodes, [&](int f) { return (int)mine[f]; });
+            raw[r] = fma(lr, tree.value[node], cv);
+            c0 = n0;
+            c1 = n1;
+            c2 = n2;
+            c3 = n3;
+            cv = nv;
+        }
+        return;
+    }
+    for (int64_t r = r0; r < n; r += stride) {
         const uint8_t *rb = s.records + r * rec;
         const int node = walk_packed(tree, n_nodes, [&](int f) {
             const int t = f / tf;
             return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
         });
-        double *slot = s.raw + (size_t)k * s.n + r;  // class-major (k = 0 for a single output)
-        *slot = fma(lr, tree.value[node], *slot);
+        raw[r] = fma(lr, tree.value[node], raw[r]);
     }
 }
 
