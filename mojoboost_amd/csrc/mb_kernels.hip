@@ -501,6 +501,31 @@ __global__ __launch_bounds__(256) void k_softmax(DevState s) {
     const int K = s.hp.num_class;
     const int64_t n = s.n;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    constexpr int kRegK = 16;  // up to this many classes, the exponentials stay in registers
+    if (K <= kRegK) {
+        for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
+            const double *x = s.raw + r;
+            double *p = s.prob + r;
+            double e[kRegK];
+#pragma unroll
+            for (int i = 0; i < kRegK; ++i) e[i] = i < K ? x[(size_t)i * n] : 0.0;
+            double m = e[0];
+#pragma unroll
+            for (int i = 1; i < kRegK; ++i)
+                if (i < K && e[i] > m) m = e[i];
+            double total = 0.0;
+#pragma unroll
+            for (int i = 0; i < kRegK; ++i)
+                if (i < K) {
+                    e[i] = ref_exp(e[i] - m);
+                    total += e[i];
+                }
+#pragma unroll
+            for (int i = 0; i < kRegK; ++i)
+                if (i < K) p[(size_t)i * n] = e[i] / total;
+        }
+        return;
+    }
     for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n; r += stride) {
         const double *x = s.raw + r;
         double *p = s.prob + r;
