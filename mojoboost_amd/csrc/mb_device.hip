@@ -342,7 +342,10 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     // the packed int8-lattice counters bound a block's rows; the other
     // accumulators hold whole-round sums in every field
     const int64_t limit = kind == mb::kAccQuant ? chunk_limit_for(B) : (int64_t)1 << 30;
-    int64_t grid = (int64_t)ds->n_cu * mb::kHistBlocksPerCU;  // resident root-build blocks
+    // resident root-build blocks, shared by the feature tiles (a launch runs
+    // grid x tiles blocks): every block then takes more rows, and zeroes,
+    // stores and leaves to the scan's merge one partial per tile and block
+    int64_t grid = std::max<int64_t>(1, (int64_t)ds->n_cu * mb::kHistBlocksPerCU / std::max(1, s.n_tiles));
     const int64_t need = (ds->n + limit - 1) / limit;
     if (grid < need) grid = need;
     s.hist_grid = (int32_t)grid;
