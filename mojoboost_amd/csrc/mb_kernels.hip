@@ -2672,6 +2672,16 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
     for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
         const int j = task / n_groups;
         const int f0 = (task - j * n_groups) * kNarrowFeat;
+        // the scan phase's feature (this wave's: f0 + wave / 2) metadata,
+        // requested with the task's first loads
+        const int fs = f0 + (wv >> 1);
+        int mbf_s = -1, fwidth = 0;
+        bool fmask = false;
+        if (fs < F) {
+            mbf_s = s.missing_bin[fs];
+            fwidth = s.widths[fs];
+            fmask = s.feature_mask[(size_t)rd.tree_index * F + fs];
+        }
         Item it;
         int64_t m_built, m_sib;
         if (root_mode) {
@@ -2786,10 +2796,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
             const int TG = __builtin_amdgcn_readlane(lg, 63), TH = __builtin_amdgcn_readlane(lh, 63),
                       TC = __builtin_amdgcn_readlane(lc, 63);
             const int64_t n_child = child == 0 ? m_built : m_sib;
-            const int mbf = s.missing_bin[f];
+            const int mbf = mbf_s;  // f == fs
             const bool gated = (hp.max_depth > 0 && it.depth_child >= hp.max_depth) ||
-                               n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 ||
-                               !s.feature_mask[(size_t)rd.tree_index * F + f];
+                               n_child < 2 * (int64_t)hp.min_data_in_leaf || n_child < 2 || !fmask;
             double best_gain = 0.0;
             int best_order = 0x7FFFFFFF;
             int best_left = 0;
@@ -2798,7 +2807,7 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
                           mc = mbf >= 0 ? cv[q][child][2][mbf] : 0;
                 const long long min_c = hp.min_data_in_leaf;
                 const int n_scan = mbf >= 0 ? mbf : nb;
-                int lim = n_scan < s.widths[f] ? n_scan : s.widths[f];
+                int lim = n_scan < fwidth ? n_scan : fwidth;
                 if (mc == 0 && lim > n_scan - 1) lim = n_scan - 1;
                 if (bin < lim) {
                     const double parent = qscore(TG, TH, gu, hu, l1, l2);
