@@ -2669,6 +2669,10 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
         if (fl < u) fl += 1.0;
         hmin = (long long)fl;
     }
+    // every wave holds the batch's items, lane i item i (n_items <= 64): a
+    // task reads its item's fields from registers, not from memory
+    Item my{};
+    if (!root_mode && lane < n_items) my = s.items[lane];
     for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
         const int j = task / n_groups;
         const int f0 = (task - j * n_groups) * kNarrowFeat;
@@ -2694,7 +2698,15 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
             it.hist_sib = 0;
             it.depth_child = 0;
         } else {
-            it = s.items[j];
+            it.begin = readlane_i64(my.begin, j);
+            it.end = readlane_i64(my.end, j);
+            it.n_left = readlane_i64(my.n_left, j);
+            it.builds_left = __builtin_amdgcn_readlane(my.builds_left, j);
+            it.hist_built = __builtin_amdgcn_readlane(my.hist_built, j);
+            it.hist_sib = __builtin_amdgcn_readlane(my.hist_sib, j);
+            it.depth_child = __builtin_amdgcn_readlane(my.depth_child, j);
+            it.part_off = __builtin_amdgcn_readlane(my.part_off, j);
+            it.part_cnt = __builtin_amdgcn_readlane(my.part_cnt, j);
             const int64_t m = it.end - it.begin;
             m_built = it.builds_left ? it.n_left : m - it.n_left;
             m_sib = m - m_built;
