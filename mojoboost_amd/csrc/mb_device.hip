@@ -950,7 +950,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             // the max-abs lattice quantizes in the root build, which reads
             // every record of the round's rows anyway
             const bool fuse_q = mb::acc_kind(s.hp) == mb::kAccQuant && !s.hp.grad64;
-            HIPX(mb::launch_quantize(s, grid_rows, st, !fuse_q));
+            // with the pairs written by the root build and no row list to
+            // gather (no bag, no GOSS), one block publishes the scales
+            const bool q_rows = !fuse_q || s.hp.bagging || s.hp.goss;
+            HIPX(mb::launch_quantize(s, q_rows ? grid_rows : 1, st, !fuse_q));
             if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3], fuse_q));
             else HIPX(mb::launch_hist(s, st, nullptr, nullptr, fuse_q));
             HIPX(mb::launch_scan(s, 1, st));

@@ -649,6 +649,9 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
             s.stats64[(1 - rd.parity) * 2 + 1] = 0ULL;
         }
     }
+    // no pairs to write and every row in order (no bag, no GOSS sample):
+    // nothing per row (the host then launches one block)
+    if (!(hp.quantized && write_pairs) && !gs_on && !hp.bagging) return;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int rec = s.rec_bytes;
     for (int64_t r0 = (int64_t)blockIdx.x * blockDim.x; r0 < s.n; r0 += stride) {
@@ -677,7 +680,8 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
         if (gs_on) {
             if (r < gst.bag_n) s.rows0[r] = s.goss_rows[r];
         } else if (!hp.bagging) {
-            if (valid) s.rows0[r] = (int32_t)r;
+            // every row in order: the root build and the root's partition
+            // compute the ids, no list is written
         } else {
             // Sampled rows appended with one atomic per wave; their order in
             // the root range does not matter (integer histograms).
@@ -2008,7 +2012,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         const int q = 63 - (int)__builtin_clzll(own);
         struct {
             int64_t begin, n_left, m, c0, c1;
-            int item, src_buf, feature, bin, default_left, missing_bin, cat_e;
+            int item, src_buf, feature, bin, default_left, missing_bin, cat_e, direct;
         } d;
         d.begin = readlane_i64(pit.begin, q);
         d.n_left = readlane_i64(pit.n_left, q);
@@ -2022,6 +2026,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         d.default_left = __builtin_amdgcn_readlane(pit.default_left, q);
         d.missing_bin = __builtin_amdgcn_readlane(pit.missing_bin, q);
         d.cat_e = __builtin_amdgcn_readlane(pit.cat_e, q);
+        d.direct = __builtin_amdgcn_readlane(pit.direct, q);
         const int32_t *src = (d.src_buf ? s.rows1 : s.rows0) + d.begin;
         int32_t *dst = (d.src_buf ? s.rows0 : s.rows1) + d.begin;
         const int mb = d.missing_bin, thr = d.bin, dl = d.default_left;
@@ -2039,12 +2044,21 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         uint32_t vbits = 0, lbits = 0;
         // every load unconditional (a row past the task reads id 0 and is
         // masked off), so all of them are in flight together
+        if (d.direct) {  // task-uniform: ids are positions (the root, begin 0)
 #pragma unroll
-        for (int u = 0; u < kPartRows; ++u) {
-            const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
-            vbits |= (i < d.c1 ? 1u : 0u) << u;
-            r[u] = __builtin_amdgcn_raw_buffer_load_b32(ids, (u * kPartThreads + tid) * 4, 0, 0);
-            if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the row lists
+            for (int u = 0; u < kPartRows; ++u) {
+                const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
+                vbits |= (i < d.c1 ? 1u : 0u) << u;
+                r[u] = i < d.c1 ? (int32_t)(d.begin + i) : 0;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kPartRows; ++u) {
+                const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
+                vbits |= (i < d.c1 ? 1u : 0u) << u;
+                r[u] = __builtin_amdgcn_raw_buffer_load_b32(ids, (u * kPartThreads + tid) * 4, 0, 0);
+                if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the row lists
+            }
         }
         uint32_t bin[kPartRows];
 #pragma unroll
@@ -4441,7 +4455,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         pi.default_left = sn.default_left;
         pi.missing_bin = v.mbin[sn.feature];
         pi.cat_e = sn.cat ? Xs : -1;
-        pi.pad_ = 0;
+        // the root of an unsampled round spans every row in order: its
+        // partition computes the ids instead of reading an identity list
+        pi.direct = (Xs == 0 && !rd.sampled) ? 1 : 0;
         s.part_items[jj] = pi;
         AccItem ai;
         ai.lo = bl ? b0 : b0 + nlft;

@@ -63,7 +63,7 @@ struct PartItem {
     int64_t begin, n_left, m;
     int32_t qoff, src_buf, feature, bin, default_left, missing_bin;
     int32_t cat_e;  // categorical split: the explored node whose e_cat set routes left; -1 numerical
-    int32_t pad_;
+    int32_t direct; // 1: the parent is the root over every row in order (row id = position, no list read)
 };
 
 // A batch item's accumulation work: its accumulated child, rows [lo, hi) of
