@@ -970,11 +970,11 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 group_size[slot] = n;
                 for (int c = 0; c < n; ++c) {
                     if (timed) {
-                        HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1)));
+                        HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1), k == 0 && c == 0));
                         HIPX(mb::launch_accum(s, st, ev_group(slot, c, 2), ev_group(slot, c, 3)));
                         HIPX(hipEventRecord(ev_group(slot, c, 4), st));
                     } else {
-                        HIPX(mb::launch_partition(s, st));
+                        HIPX(mb::launch_partition(s, st, nullptr, nullptr, k == 0 && c == 0));
                         HIPX(mb::launch_accum(s, st));
                     }
                     HIPX(mb::launch_scan(s, 0, st));

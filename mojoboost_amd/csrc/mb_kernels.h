@@ -36,7 +36,8 @@ size_t rank_lds_bytes(const DevState &s);
 // pairs into the records (max-abs lattice only; other kinds ignore it).
 hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr,
                        bool quantize = false);
-hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr,
+                            bool root = false);
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st);
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st, Batch *host = nullptr);

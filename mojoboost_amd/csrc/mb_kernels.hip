@@ -1988,10 +1988,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uin
 constexpr int kPartThreads = MB_PART_THREADS;
 constexpr int kPartRows = kPartChunk / kPartThreads;  // rows per thread of a task
 static_assert(kPartRows * kPartThreads == kPartChunk && kPartRows <= 32, "a task's rows fit the thread bit masks");
+// The root's batch (one leaf over every row of the round) is partitioned by
+// its own launch with kPartRowsRoot rows per thread: a quarter of the tasks,
+// so a quarter of the same-address reservations on the root's two cursors
+// (one wave of tasks holds the chip; the occupancy lost to the registers
+// costs less there).
+constexpr int kPartRowsRoot = kPartChunkRoot / kPartThreads;
+static_assert(kPartRowsRoot * kPartThreads == kPartChunkRoot && kPartRowsRoot <= 32, "root task rows fit the masks");
 
+template <int R>
 __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
     constexpr int NW = kPartThreads / 64;  // waves
-    constexpr int E = kPartRows * NW;      // (row group, wave) entries of a task
+    constexpr int E = R * NW;              // (row group, wave) entries of a task
     constexpr int SW = (E + 63) / 64;      // waves that scan one side's entries
     static_assert((E % 64 == 0 || E < 64) && 2 * SW <= NW, "one wave scans up to 64 entries");
     __shared__ int cnt_l[E], cnt_r[E];     // counts, then exclusive prefixes within a scan wave
@@ -2040,31 +2048,31 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         // 64-bit address), and any offset past the range reads 0
         const __amdgpu_buffer_rsrc_t ids = buffer_rsrc(src + d.c0, (uint32_t)(d.c1 - d.c0) * 4u);
         const __amdgpu_buffer_rsrc_t col = buffer_rsrc(s.bins_cm + (size_t)d.feature * s.n, (uint32_t)s.n);
-        int32_t r[kPartRows];
+        int32_t r[R];
         uint32_t vbits = 0, lbits = 0;
         // every load unconditional (a row past the task reads id 0 and is
         // masked off), so all of them are in flight together
         if (d.direct) {  // task-uniform: ids are positions (the root, begin 0)
 #pragma unroll
-            for (int u = 0; u < kPartRows; ++u) {
+            for (int u = 0; u < R; ++u) {
                 const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
                 vbits |= (i < d.c1 ? 1u : 0u) << u;
                 r[u] = i < d.c1 ? (int32_t)(d.begin + i) : 0;
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < kPartRows; ++u) {
+            for (int u = 0; u < R; ++u) {
                 const int64_t i = d.c0 + (int64_t)u * kPartThreads + tid;
                 vbits |= (i < d.c1 ? 1u : 0u) << u;
                 r[u] = __builtin_amdgcn_raw_buffer_load_b32(ids, (u * kPartThreads + tid) * 4, 0, 0);
                 if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the row lists
             }
         }
-        uint32_t bin[kPartRows];
+        uint32_t bin[R];
 #pragma unroll
-        for (int u = 0; u < kPartRows; ++u) bin[u] = __builtin_amdgcn_raw_buffer_load_b8(col, r[u], 0, 0);
+        for (int u = 0; u < R; ++u) bin[u] = __builtin_amdgcn_raw_buffer_load_b8(col, r[u], 0, 0);
 #pragma unroll
-        for (int u = 0; u < kPartRows; ++u) {
+        for (int u = 0; u < R; ++u) {
             const bool valid = (vbits >> u) & 1u;
             const int b = (int)bin[u];
             const unsigned long long cw = b < 64 ? cset[0] : b < 128 ? cset[1] : b < 192 ? cset[2] : cset[3];
@@ -2111,7 +2119,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
         // barriers)
         asm volatile("" : "+v"(lbits), "+v"(vbits));
 #pragma unroll
-        for (int u = 0; u < kPartRows; ++u) {
+        for (int u = 0; u < R; ++u) {
             const bool valid = (vbits >> u) & 1u;
             const bool left = (lbits >> u) & 1u;
             const unsigned long long lm = __ballot(valid && left);
@@ -4354,7 +4362,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         const int pc = lane < nsel ? (int)((mb + chunk - 1) / chunk) : 0;
         long long chunk_p = (rows_total + s.part_target - 1) / s.part_target;
         chunk_p = (chunk_p + kPartChunkStep - 1) / kPartChunkStep * kPartChunkStep;
-        chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > kPartChunk ? kPartChunk : chunk_p;
+        // the root's batch has a launch of its own with larger tasks
+        const long long cmax = root_mode ? kPartChunkRoot : kPartChunk;
+        chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > cmax ? cmax : chunk_p;
         const int qc = lane < nsel ? (int)((m + chunk_p - 1) / chunk_p) : 0;
         const int pi = wave_incl_scan_i(pc), qi = wave_incl_scan_i(qc);
         if (lane < nsel) {
@@ -5075,8 +5085,9 @@ hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEve
            : s.hp.quantized ? launch_hist_t<QAcc>(s, st, ev0, ev1)
                             : launch_hist_t<FAcc>(s, st, ev0, ev1);
 }
-hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    return launch_timed(k_partition, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
+hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, bool root) {
+    if (root) return launch_timed(k_partition<kPartRowsRoot>, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
+    return launch_timed(k_partition<kPartRows>, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
 }
 template <class Acc>
 hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {

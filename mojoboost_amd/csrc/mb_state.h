@@ -140,6 +140,7 @@ constexpr int kPartChunk = MB_PART_CHUNK;
 #endif
 constexpr int kPartChunkMin = MB_PART_CHUNK_MIN;
 constexpr int kPartChunkStep = 256;
+constexpr int kPartChunkRoot = 16384;  // at most, per task of the root's batch (its own launch)
 // Root build launch: kHistThreads per block, kHistBlocksPerCU blocks per CU
 // (each with its own LDS histogram).
 #ifndef MB_HIST_THREADS
