@@ -1977,8 +1977,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uin
 // within each side. Few rows per thread keep the kernel at 64 VGPRs or less
 // and many gathers in flight per CU; measured on C2, 4K-row chunks of 1024
 // threads partition 31 % faster than 8K-row chunks of 256 threads with 32
-// rows each, although the root split's 2.6K chunks take twice the
-// same-address atomics on the leaf's two cursors (the L2 serializes them).
+// rows each. The root's batch, one leaf over every row, is the exception
+// (below: 16K-row chunks, a quarter of the same-address reservations on its
+// two cursors, which the L2 serializes).
 // The order of rows inside a child is not the reference's (chunks land in
 // reservation order); integer histograms are order-free, fp64 sums differ
 // only in their rounding.
