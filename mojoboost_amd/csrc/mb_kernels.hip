@@ -1507,6 +1507,35 @@ __host__ __device__ constexpr int record_bytes_for(int tf) {
     return r;
 }
 
+// A lane's 16-byte record slice (dwords d0..d3) rotated right by rot bytes:
+// byte k of the result is byte (k + rot) mod 16 of the slice. The histogram
+// kinds with bin-major cells give each lane rot = (lane mod 16) xor (bit 4
+// of lane), so at every step the lanes of a wave take different byte
+// positions.
+__device__ __forceinline__ void rotate_slice(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t rot,
+                                             uint32_t (&r)[4]) {
+    if (rot & 4u) {  // one dword
+        const uint32_t t = d0;
+        d0 = d1;
+        d1 = d2;
+        d2 = d3;
+        d3 = t;
+    }
+    if (rot & 8u) {  // two dwords
+        uint32_t t = d0;
+        d0 = d2;
+        d2 = t;
+        t = d1;
+        d1 = d3;
+        d3 = t;
+    }
+    const uint32_t sh = rot & 3u;
+    r[0] = __builtin_amdgcn_alignbyte(d1, d0, sh);
+    r[1] = __builtin_amdgcn_alignbyte(d2, d1, sh);
+    r[2] = __builtin_amdgcn_alignbyte(d3, d2, sh);
+    r[3] = __builtin_amdgcn_alignbyte(d0, d3, sh);
+}
+
 struct QAcc {
     // LDS cells are bin-major: cell (byte position p of the record, bin) at
     // bin * FS + p, FS = max(32, record bytes). A 64-bit cell's banks then
@@ -1546,25 +1575,8 @@ struct QAcc {
         const uint32_t rot = ((uint32_t)lane_id() & 15u) ^ (((uint32_t)lane_id() >> 4) & 1u);
         // the g/h bytes are added as bin 0 (any bin id must be below the LDS
         // rows, n_bins); pad bytes are zero
-        uint32_t d0 = w.x, d1 = w.y, d2 = w.z, d3 = sub == LPR - 1 ? w.w & 0xFFFFu : w.w;
-        if (rot & 4u) {  // one dword
-            const uint32_t t = d0;
-            d0 = d1;
-            d1 = d2;
-            d2 = d3;
-            d3 = t;
-        }
-        if (rot & 8u) {  // two dwords
-            uint32_t t = d0;
-            d0 = d2;
-            d2 = t;
-            t = d1;
-            d1 = d3;
-            d3 = t;
-        }
-        const uint32_t sh = rot & 3u;
-        const uint32_t r[4] = {__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
-                               __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d0, d3, sh)};
+        uint32_t r[4];
+        rotate_slice(w.x, w.y, w.z, sub == LPR - 1 ? w.w & 0xFFFFu : w.w, rot, r);
         const uint32_t pb = (uint32_t)sub * 128u;  // byte offset of position sub*16
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -1600,48 +1612,60 @@ struct QAcc {
 };
 
 struct FAcc {
-    static __host__ __device__ size_t lds_bytes(int F, int ls) { return (size_t)F * ls * 20; }
+    // grad and hess cells bin-major, as QAcc's: cell (byte position p, bin)
+    // at bin * FS + p, FS = max(32, record bytes), so a binary64 cell's banks
+    // depend on p alone and, with QAcc's lane rotation, a step's 64 adds
+    // meet no bank conflict (feature-major cells lost a third of the LDS
+    // cycles to conflicts); positions past the tile's features are skipped.
+    // The counts stay feature-major (f * ls + bin): bin-major they would not
+    // fit beside the sums in one workgroup's LDS.
+    static __host__ __device__ size_t lds_bytes(int tf, int ls) {
+        return (size_t)2 * QAcc::row_cells_for(record_bytes_for(tf)) * ls * 8 + (size_t)tf * ls * 4;
+    }
     template <int LPR>
     __device__ static void zero(unsigned char *lds, int F, int ls) {
+        constexpr int FS = QAcc::row_cells_for(LPR * 16);
         double *g = (double *)lds;
-        uint32_t *c = (uint32_t *)(g + 2 * (size_t)F * ls);
-        for (int i = threadIdx.x; i < 2 * F * ls; i += blockDim.x) g[i] = 0.0;
+        uint32_t *c = (uint32_t *)(g + 2 * (size_t)FS * ls);
+        for (int i = threadIdx.x; i < 2 * FS * ls; i += blockDim.x) g[i] = 0.0;
         for (int i = threadIdx.x; i < F * ls; i += blockDim.x) c[i] = 0u;
     }
     // gv, hv: the row's derivatives in binary64 with its GOSS weight applied
     // (accumulate_rows loads them with the record)
     template <int LPR>
     __device__ static void add(unsigned char *lds, const uint4 &w, int sub, int F, int ls, double gv, double hv) {
+        constexpr int FS = QAcc::row_cells_for(LPR * 16);
         double *g = (double *)lds;
-        double *h = g + (size_t)F * ls;
-        uint32_t *c = (uint32_t *)(h + (size_t)F * ls);
-        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+        double *h = g + (size_t)FS * ls;
+        uint32_t *c = (uint32_t *)(h + (size_t)FS * ls);
+        const uint32_t rot = ((uint32_t)lane_id() & 15u) ^ (((uint32_t)lane_id() >> 4) & 1u);
+        uint32_t r[4];
+        rotate_slice(w.x, w.y, w.z, w.w, rot, r);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int f = sub * 16 + q * 4 + j;
-                if (f < F) {
-                    const int cell = f * ls + (int)((d[q] >> (8 * j)) & 255u);
-                    atomicAdd(&g[cell], gv);
-                    atomicAdd(&h[cell], hv);
-                    atomicAdd(&c[cell], 1u);
-                }
+        for (int k = 0; k < 16; ++k) {
+            const int p = sub * 16 + (int)(((uint32_t)k + rot) & 15u);
+            const int bin = (int)((r[k >> 2] >> (8 * (k & 3))) & 255u);
+            if (p < F) {
+                atomicAdd(&g[bin * FS + p], gv);
+                atomicAdd(&h[bin * FS + p], hv);
+                atomicAdd(&c[p * ls + bin], 1u);
             }
+        }
     }
     template <int LPR>
     __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
+        constexpr int FS = QAcc::row_cells_for(LPR * 16);
         const int F = s.n_features, nb = s.n_bins, ls = s.lds_stride, ps = s.part_stride;
         const double *g = (const double *)lds;
-        const double *h = g + (size_t)Ft * ls;
-        const uint32_t *c = (const uint32_t *)(h + (size_t)Ft * ls);
+        const double *h = g + (size_t)FS * ls;
+        const uint32_t *c = (const uint32_t *)(h + (size_t)FS * ls);
         const size_t base = ((size_t)blk * F + f0) * ps;
         for (int i = threadIdx.x; i < Ft * ps; i += blockDim.x) {
             const int f = i / ps;
             const int b = i - f * ps;
             const bool in = b < nb;
-            s.fpart_g[base + i] = in ? g[f * ls + b] : 0.0;
-            s.fpart_h[base + i] = in ? h[f * ls + b] : 0.0;
+            s.fpart_g[base + i] = in ? g[b * FS + f] : 0.0;
+            s.fpart_h[base + i] = in ? h[b * FS + f] : 0.0;
             s.fpart_c[base + i] = in ? c[f * ls + b] : 0u;
         }
     }
@@ -1943,8 +1967,11 @@ __global__ __launch_bounds__(1024) void k_hist(DevState s) {
         if (direct) accumulate_rows<LPR, Acc, false, true, 3>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
         else accumulate_rows<LPR, Acc, true, true, 3>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult, &qc, rec_w);
     } else {
-        if (direct) accumulate_rows<LPR, Acc, false, false, kRootUnroll>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
-        else accumulate_rows<LPR, Acc, true, false, kRootUnroll>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
+        // fp32 cells: two rows per step (four need more than the 128 VGPRs
+        // a 1024-thread block may hold)
+        constexpr int U = std::is_same<Acc, FAcc>::value ? 2 : kRootUnroll;
+        if (direct) accumulate_rows<LPR, Acc, false, false, U>(s, lds, nullptr, c0, c1, Ft, rec, goss_mult);
+        else accumulate_rows<LPR, Acc, true, false, U>(s, lds, s.rows0, c0, c1, Ft, rec, goss_mult);
     }
     __syncthreads();
     Acc::template store<LPR>(s, lds, blockIdx.x, f0, Ft);
