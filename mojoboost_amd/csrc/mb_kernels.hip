@@ -3000,34 +3000,53 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
             }
             if (bin < nb) {
                 const size_t pstride = (size_t)F * s.part_stride;
-                const size_t base = (size_t)it.part_off * pstride + (size_t)f * s.part_stride + bin;
-                const double *qg = s.fpart_g + base, *qh = s.fpart_h + base;
-                const uint32_t *qc = s.fpart_c + base;
+                // the item's partials of this feature through buffer loads
+                // (a 32-bit offset per load instead of a 64-bit address, so
+                // kMU partials' loads fit in flight); added in partial order
+                constexpr int kMU = 6;
+                const size_t ubase = (size_t)it.part_off * pstride + (size_t)f * s.part_stride;
                 const int np = it.part_cnt;
+                // byte offsets of the item's partials fit 32 bits (else
+                // the addresses are formed in 64 bits, one partial at a time)
+                const bool fits = (uint64_t)np * (uint64_t)pstride * 8ull < (1ull << 32);  // task-uniform
+                const uint32_t span = fits ? (uint32_t)((size_t)np * pstride) : 0u;  // elements
+                const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(s.fpart_g + ubase, span * 8u);
+                const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(s.fpart_h + ubase, span * 8u);
+                const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(s.fpart_c + ubase, span * 4u);
+                auto ld = [&](uint32_t e, double &xg, double &xh, uint32_t &xc) {
+                    xg = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rg, e * 8u, 0, 0));
+                    xh = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rh, e * 8u, 0, 0));
+                    xc = __builtin_amdgcn_raw_buffer_load_b32(rc, e * 4u, 0, 0);
+                };
                 int b = half;
-                // four partials' loads in flight, added in partial order
-                for (; b + 6 < np; b += 8) {
-                    double vg[4], vh[4];
-                    uint32_t vc[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const size_t at = (size_t)(b + 2 * u) * pstride;
-                        vg[u] = qg[at];
-                        vh[u] = qh[at];
-                        vc[u] = qc[at];
+                if (!fits) {
+                    for (; b < np; b += 2) {
+                        const size_t at = ubase + (size_t)b * pstride + bin;
+                        g += s.fpart_g[at];
+                        h += s.fpart_h[at];
+                        c += (int)s.fpart_c[at];
                     }
+                }
+                for (; b + 2 * kMU - 2 < np; b += 2 * kMU) {
+                    double vg[kMU], vh[kMU];
+                    uint32_t vc[kMU];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < kMU; ++u)
+                        ld((uint32_t)bin + (uint32_t)(b + 2 * u) * (uint32_t)pstride, vg[u], vh[u], vc[u]);
+#pragma unroll
+                    for (int u = 0; u < kMU; ++u) {
                         g += vg[u];
                         h += vh[u];
                         c += (int)vc[u];
                     }
                 }
                 for (; b < np; b += 2) {
-                    const size_t at = (size_t)b * pstride;
-                    g += qg[at];
-                    h += qh[at];
-                    c += (int)qc[at];
+                    double xg, xh;
+                    uint32_t xc;
+                    ld((uint32_t)bin + (uint32_t)b * (uint32_t)pstride, xg, xh, xc);
+                    g += xg;
+                    h += xh;
+                    c += (int)xc;
                 }
             }
             if (half == 1) {
