@@ -363,6 +363,10 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     s.pb_launch = std::min<int32_t>(s.pb_grid, (kind == mb::kAccFloat ? 1 : 2) * ds->n_cu);
     s.part_launch = std::min<int32_t>(s.part_grid, 8 * ds->n_cu);
     s.part_target = 2 * ds->n_cu;
+    // the root's batch gets the launch of larger tasks only where its rows
+    // fill them (C2's 10.5M: 16K-row tasks; C5's 2M rows would leave three
+    // quarters of each task's slots empty)
+    s.part_root = (int64_t)ds->n >= (int64_t)mb::kPartChunkRoot * s.part_target ? 1 : 0;
     // a root build uses at most ceil(n / chunk_min) chunks
     const int64_t parts = std::max<int64_t>(std::min<int64_t>(grid, (ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min),
                                             s.pb_grid);
@@ -970,11 +974,12 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 group_size[slot] = n;
                 for (int c = 0; c < n; ++c) {
                     if (timed) {
-                        HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1), k == 0 && c == 0));
+                        HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1),
+                                                  s.part_root && k == 0 && c == 0));
                         HIPX(mb::launch_accum(s, st, ev_group(slot, c, 2), ev_group(slot, c, 3)));
                         HIPX(hipEventRecord(ev_group(slot, c, 4), st));
                     } else {
-                        HIPX(mb::launch_partition(s, st, nullptr, nullptr, k == 0 && c == 0));
+                        HIPX(mb::launch_partition(s, st, nullptr, nullptr, s.part_root && k == 0 && c == 0));
                         HIPX(mb::launch_accum(s, st));
                     }
                     HIPX(mb::launch_scan(s, 0, st));

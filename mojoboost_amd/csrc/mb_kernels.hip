@@ -4410,7 +4410,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         long long chunk_p = (rows_total + s.part_target - 1) / s.part_target;
         chunk_p = (chunk_p + kPartChunkStep - 1) / kPartChunkStep * kPartChunkStep;
         // the root's batch has a launch of its own with larger tasks
-        const long long cmax = root_mode ? kPartChunkRoot : kPartChunk;
+        const long long cmax = root_mode && s.part_root ? kPartChunkRoot : kPartChunk;
         chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > cmax ? cmax : chunk_p;
         const int qc = lane < nsel ? (int)((m + chunk_p - 1) / chunk_p) : 0;
         const int pi = wave_incl_scan_i(pc), qi = wave_incl_scan_i(qc);

@@ -329,6 +329,7 @@ struct DevState {
     int32_t pb_launch;     // blocks of an accumulation launch (grid-strided)
     int32_t part_launch;   // blocks of a partition launch (grid-strided)
     int32_t part_target;   // partition tasks a batch is spread over
+    int32_t part_root;     // 1: the root's batch takes its own launch of kPartChunkRoot-row tasks
     // tree being grown (max 2 * num_leaves - 1 nodes)
     int32_t *t_feature, *t_threshold, *t_left, *t_right, *t_default_left, *t_missing_bin;
     double *t_value, *t_gain, *t_count;

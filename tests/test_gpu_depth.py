@@ -2,7 +2,8 @@
 100 trees (where the max-abs lattice is at its smallest), C5-shaped softmax
 with category sets as the bench runs it, every lattice width and both
 roundings, lambda_l1 > 0 on both gradient paths, the C3 shape at its full 28
-features and 255 leaves, and the empty-bag fallback of the quantizer.
+features and 255 leaves, the empty-bag fallback of the quantizer, and a root
+large enough for the root partition's own launch.
 Quantized comparisons are bit for bit; fp32-gradient ones within 1e-5
 relative."""
 import numpy as np
@@ -34,6 +35,23 @@ def test_c2_shape_1m_rows_100_trees_bit_exact(dev):
     fit = dev.Dataset(bins, n, 28, nb, y, missing_bin=mb).train(**kw)
     ref = O.train(bins, n, 28, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
     assert fit.n_trees == ref.n_trees == 100
+    _compare_fit(fit, ref, n)
+
+
+def test_root_partition_launch_of_large_tasks_bit_exact(dev):
+    """A root over at least kPartChunkRoot x (2 x CUs) rows (8.4M on 256 CUs)
+    is partitioned by its own launch of 16K-row tasks (the C2 shape takes it
+    on every tree); trees, values and raw scores bit-exact to the oracle."""
+    n = 8_700_000
+    rng = np.random.default_rng(33)
+    x = rng.normal(size=(4, n))
+    y = (rng.uniform(size=n) < 1 / (1 + np.exp(-(x[0] * x[1] + 0.5 * x[2])))).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, 4, max_bins=63)
+    del x
+    kw = dict(objective=1, num_iterations=3, num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1)
+    fit = dev.Dataset(bins, n, 4, 63, y, missing_bin=mb).train(**kw)
+    ref = O.train(bins, n, 4, 63, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    assert fit.n_trees == ref.n_trees == 3
     _compare_fit(fit, ref, n)
 
 
