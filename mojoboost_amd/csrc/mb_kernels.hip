@@ -1081,9 +1081,15 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_count(DevState s, int 
 
 // Exclusive prefix of per-block counts, in place (one block); the total
 // goes to *total when given.
-__global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, int64_t *total) {
+// blk2, total2: a second array scanned by block 1 of a two-block launch.
+__global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, int64_t *total, int32_t *blk2,
+                                                    int64_t *total2) {
     __shared__ long long wtot[16];
     if (!goss_on(s)) return;
+    if (blockIdx.x == 1) {
+        blk = blk2;
+        total = total2;
+    }
     const int nb = s.goss_nblk;
     const int per = (nb + 1023) / 1024;
     const int lo = threadIdx.x * per;
@@ -5002,22 +5008,26 @@ hipError_t launch_goss(const DevState &s, int grid_rows, hipStream_t st) {
     int64_t *bag_n = &s.gst->bag_n;
     // top rows: counts, prefix; kappa and the band's classes
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 0);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr, (int32_t *)nullptr,
+                       (int64_t *)nullptr);
     hipLaunchKernelGGL(k_goss_kappa, blocks, dim3(kGossRowThreads), 0, st, s);
     // the open rows: list, sequential count, decisions
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk_u, n_unc);
+    // the kept and the open rows' block counts, one block each
+    hipLaunchKernelGGL(k_goss_scan, dim3(2), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr, s.goss_blk_u,
+                       n_unc);
     hipLaunchKernelGGL(k_goss_compact, blocks, dim3(kGossRowThreads), 0, st, s);
     hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 1);
     hipLaunchKernelGGL(k_goss_apply, dim3(256), dim3(256), 0, st, s);
     // the check, and the full count when it fails
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 2);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, (int64_t *)nullptr, (int32_t *)nullptr,
+                       (int64_t *)nullptr);
     hipLaunchKernelGGL(k_goss_verify, blocks, dim3(kGossRowThreads), 0, st, s);
     hipLaunchKernelGGL(k_goss_walk, dim3(1), dim3(1024), walk_lds, st, s, 0);
     // the sample: top rows and kept rows, ascending
     hipLaunchKernelGGL(k_goss_count, blocks, dim3(kGossRowThreads), 0, st, s, 1);
-    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, bag_n);
+    hipLaunchKernelGGL(k_goss_scan, dim3(1), dim3(1024), 0, st, s, s.goss_blk, bag_n, (int32_t *)nullptr,
+                       (int64_t *)nullptr);
     hipLaunchKernelGGL(k_goss_scatter, blocks, dim3(kGossRowThreads), 0, st, s);
     return hipGetLastError();
 }
