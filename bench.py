@@ -19,6 +19,9 @@ root and each expansion's smaller child, speculative expansions included --
 m rows * (F + gh) (uint8 bins + the g/h pair: 2 bytes int8, 8 bytes fp32; row
 ids, LDS traffic and partial writes not counted), over the durations of the
 kernels that accumulate them (k_hist for the root, k_accum for the children).
+The root build that training runs also quantizes (max-abs lattice): the
+quantizer's own bytes (binary32 g, h in, the int8 pair out) are reported
+apart (`root_quantizer_bytes_per_tree`), never in `value`.
 The durations come from HIP events that the runtime records at each kernel's
 own start and end (hipExtLaunchKernel), on the stream the kernel runs on, so
 they are the kernel times rocprofv3's kernel trace reports. `roofline` prices
@@ -250,6 +253,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=None,
                     help="oracle sample: trees (rounds for c5); default per workload")
     ap.add_argument("--no-instrumented", action="store_true")
+    ap.add_argument("--partition-mode", type=int, default=0,
+                    help="leaf rows as 0 automatic, 1 records, 2 row ids (mbh_params.partition_mode)")
     ap.add_argument("--rocprof-summary", default=None,
                     help="only summarize a rocprofv3 CSV (kernel_stats or counter_collection) "
                          "as a markdown table")
@@ -318,6 +323,8 @@ def main():
     ds = device.Dataset(bins, args.rows, F, NB, y, missing_bin=missing, n_categories=n_cat)
     kw = dict(num_leaves=L, min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1,
               num_grad_quant_bins=4, stochastic_rounding=1, **wl["params"])
+    if args.partition_mode:
+        kw["partition_mode"] = args.partition_mode
     if args.warmup > 0:
         ds.train(num_iterations=args.warmup, **kw)
     print("[bench] warmup done", file=sys.stderr, flush=True)
@@ -358,7 +365,8 @@ def main():
         import oracle_lib as O
 
         cores, visible = host_cores()
-        oparams = {k: v for k, v in kw.items() if k not in ("num_grad_quant_bins", "stochastic_rounding")}
+        oparams = {k: v for k, v in kw.items()
+                   if k not in ("num_grad_quant_bins", "stochastic_rounding", "partition_mode")}
         p = O.default_params(num_iterations=args.cpu_trees, num_grad_quant_bins=4, n_threads=cores,
                              **oparams)
         if n_cat is not None:
@@ -389,6 +397,8 @@ def main():
         print(f"[bench] cpu oracle {args.cpu_trees} {unit_steps} in {cpu_s:.1f}s", file=sys.stderr,
               flush=True)
 
+    # the root build of stored pairs (k_hist without the quantizer), timed
+    # apart from training; training's own root build is st["root_ms"]
     algo_root = args.rows * (F + GH)
     root_gbs = algo_root / (root_mean_ms * 1e-3) / 1e9
     root_merged_gbs = algo_root / (root_merged_ms * 1e-3) / 1e9
@@ -402,7 +412,7 @@ def main():
         launches = max(1.0, st["expand_launches"])
         kernel_gbs = st["accum_bytes"] / (st["accum_ms"] * 1e-3) / 1e9
         kernel_avg_ms = st["accum_ms"] / launches
-        part_bytes = st["rows_parted"] * 9.0
+        part_bytes = st["partition_bytes"]
         per_tree = 1.0 / max(1, stat_steps)
         extra = {
             "hist_rows_features_per_s": round(acc_bytes / (F + GH) * F / (acc_ms * 1e-3), 1),
@@ -422,14 +432,20 @@ def main():
                 st["rows_built"] / max(1.0, st["hist_bytes"] / (F + GH) - st["root_bytes"] / (F + GH))
                 - 1.0, 4),
             "accum_kernel_avg_ms": round(kernel_avg_ms, 5),
+            # the root build training runs (quantizing when the lattice is
+            # max-abs), BASELINE bytes only, and the quantizer's bytes apart
+            "root_build_in_training_ms": round(st["root_ms"] * per_tree, 4),
+            "root_build_in_training_gbs": round(st["root_bytes"] / (st["root_ms"] * 1e-3) / 1e9, 1),
+            "root_quantizer_bytes_per_tree": round(st["root_quantizer_bytes"] * per_tree, 1),
+            "accum_gbs": round(kernel_gbs, 1),
         }
         note = (f"dominant histogram kernel k_accum (smaller-child accumulation from the "
                 f"partitioned row list) over the instrumented {stat_steps}-step training, "
                 f"algorithmic bytes per launch = accumulated rows * (F + {GH}) "
                 f"({st['accum_bytes'] / launches / 1e6:.2f} MB), over its average kernel duration "
                 f"({kernel_avg_ms * 1e3:.1f} us, {int(st['expand_launches'])} launches incl. empty "
-                f"tail launches); root build k_hist alone {root_gbs:.0f} GB/s "
-                f"({root_gbs / HBM_PEAK_GBS:.1%})")
+                f"tail launches); training's root build "
+                f"{st['root_bytes'] / (st['root_ms'] * 1e-3) / 1e9:.0f} GB/s on F + {GH} bytes per row")
     else:
         value = root_gbs
         kernel_gbs = root_gbs
@@ -454,10 +470,12 @@ def main():
         "full_training_trees_kept": full_fit.n_trees,
         "hist_frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         **extra,
-        "root_hist_gbs": round(root_gbs, 1),
-        "root_hist_ms": round(root_mean_ms, 4),
-        "root_hist_merged_gbs": round(root_merged_gbs, 1),
-        "root_hist_merged_ms": round(root_merged_ms, 4),
+        # k_hist over pairs already stored (not the quantizing build that
+        # training runs: root_build_in_training_*), alone and with its merge
+        "root_hist_stored_pairs_gbs": round(root_gbs, 1),
+        "root_hist_stored_pairs_ms": round(root_mean_ms, 4),
+        "root_hist_stored_pairs_merged_gbs": round(root_merged_gbs, 1),
+        "root_hist_stored_pairs_merged_ms": round(root_merged_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_per_launch(args.workload), "note": note},

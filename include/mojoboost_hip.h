@@ -106,6 +106,14 @@ typedef struct {
      * in which any value does not is refused (MOJOTREES_ERROR_TRAINING,
      * naming the count per plane). */
     int32_t quant_staging;
+    /* how a leaf holds its rows during growth: 0 automatic (default), 1 as
+     * their records, 2 as row ids. As records (int8 pairs of the max-abs
+     * lattice, one feature tile of at most 64-byte records), the partition
+     * moves each row's whole record into the child's contiguous range and
+     * the histogram streams it; as row ids, the partition moves 4-byte ids
+     * and the histogram gathers each record by id. Automatic takes row ids
+     * (measured faster end to end). The trees are the same either way. */
+    int32_t partition_mode;
 } mbh_params;
 
 /* Host binning of a column-major double matrix (NaN = missing) with the
@@ -187,7 +195,7 @@ void mbh_fit_cat_bits(const mbh_fit *fit, uint64_t *out);
 int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
                           int32_t err_len);
 /* Training statistics. Writes min(n_out, count) values and returns count
- * (17). Milliseconds are summed HIP-event times and are filled only with
+ * (22). Milliseconds are summed HIP-event times and are filled only with
  * time_histograms=1.
  *   [0] wall seconds of the training loop (enqueue to final sync)
  *   [1] ms of the histogram-accumulating kernels (root build + expansions)
@@ -206,7 +214,12 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *   [16] their algorithmic bytes: [13] * 9 (row id in, bin, row id out)
  *        + [12] * (n_features + gh)
  *   [17] ms of the partition launches   [18] ms of the accumulation launches
- *   [19] the accumulations' algorithmic bytes: [12] * (n_features + gh) */
+ *   [19] the accumulations' algorithmic bytes: [12] * (n_features + gh)
+ *   [20] bytes of the quantizer fused into the root build, not in [2] or
+ *        [5]: root rows * 10 (binary32 g, h read, int8 pair written) when
+ *        the root build quantizes (max-abs lattice), else 0
+ *   [21] the partitions' algorithmic bytes: [13] * 9 with row ids; with
+ *        records [13] * 2 * record bytes + root rows * 2 (the root's pairs) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
 /* Query groups of a resident dataset, for objective lambdarank: counts[q]

@@ -80,6 +80,7 @@ class MbhParams(C.Structure):
         ("one_hot_max_size", C.c_int32),
         ("quant_scale_rule", C.c_int32),
         ("quant_staging", C.c_int32),
+        ("partition_mode", C.c_int32),
     ]
 
 
@@ -94,7 +95,7 @@ def mbh_params(**kw) -> MbhParams:
                   lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0,
                   max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
                   min_data_per_group=100, one_hot_max_size=-1, quant_scale_rule=0,
-                  quant_staging=0)
+                  quant_staging=0, partition_mode=0)
     for k, v in kw.items():
         setattr(p, k, v)
     return p

@@ -138,7 +138,7 @@ struct mbh_dataset {
     }
 };
 
-constexpr int kNumStats = 20;
+constexpr int kNumStats = 22;
 
 struct mbh_fit {
     int num_class = 1;
@@ -682,6 +682,29 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     return tb;
 }
 
+// The leaf row representation of a training run (mbh_params.partition_mode):
+// records (s.rcp = 1) where the layout allows it -- the max-abs lattice's
+// int8 pairs, whose root build quantizes (a pair per row to the pair plane),
+// one feature tile, records of at most 64 bytes -- and the mode asks for it;
+// row ids otherwise. Automatic takes row ids: on C2 (32-byte records) the
+// records' histograms stream (k_accum 15.6 -> 10.8 us per launch) but
+// moving 64 bytes per partitioned row instead of 9 costs more than that
+// saves (0.99 -> 1.09 s per 500 trees).
+void setup_record_partition(mb::DevState &s, const mbh_dataset *ds, const mbh_params *p, Run &run) {
+    const bool eligible = mb::acc_kind(s.hp) == mb::kAccQuant && !s.hp.grad64 && s.n_tiles == 1 &&
+                          s.rec_bytes <= 64;
+    const int mode = p->partition_mode;
+    if (mode < 0 || mode > 2) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "partition_mode must be 0, 1 or 2"};
+    s.rcp = eligible && mode == 1 ? 1 : 0;
+    if (!s.rcp) return;
+    s.crec0 = dalloc<uint8_t>((size_t)ds->n * s.rec_bytes, run.owned);
+    s.crec1 = dalloc<uint8_t>((size_t)ds->n * s.rec_bytes, run.owned);
+    s.pairs = dalloc<uint16_t>(ds->n, run.owned);
+    // the root's batch shares the record partition's kPartChunk-row tasks
+    // (16K-row tasks would hold 16 records per thread)
+    s.part_root = 0;
+}
+
 // The packed int16 arm's refusal (gpu_active_rows._raise_stage16): values
 // that did not fit a signed 16-bit word were counted per plane by the
 // quantizer; any such value (the hessian plane only when it is read, not
@@ -882,6 +905,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         Run run;
         TrainBuffers tb = setup_state(ds, p, run);
         mb::DevState &s = tb.s;
+        setup_record_partition(s, ds, p, run);
         const int K = s.hp.num_class;
         fit->num_class = K;
         fit->objective = p->objective;
@@ -1126,10 +1150,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         double *o = fit->stats;
         o[0] = std::chrono::duration<double>(t1 - t0).count();
         o[1] = t_acc;
-        o[2] = useful_rows * rb + root_rows * rq;
+        o[2] = useful_rows * rb;
         o[3] = useful_rows * ds->F;
         o[4] = builds;
-        o[5] = root_rows * (rb + rq);
+        o[5] = root_rows * rb;
         o[6] = t_root;
         o[7] = grown;
         o[8] = t_root + t_root_scan + t_pb + t_scan;
@@ -1144,6 +1168,11 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         o[17] = t_part;
         o[18] = t_accum;
         o[19] = rows_built * rb;
+        o[20] = root_rows * rq;
+        // the partitions' algorithmic bytes: row ids in and out and the
+        // split column's byte, or each row's record in and out (the root's
+        // pair read from the pair plane)
+        o[21] = s.rcp ? rows_parted * 2.0 * s.rec_bytes + root_rows * 2.0 : rows_parted * 9.0;
         for (auto &e : events) (void)hipEventDestroy(e);
         events.clear();
     } catch (const Error &e) {

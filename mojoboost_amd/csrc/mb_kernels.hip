@@ -1885,9 +1885,16 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                 const uint32_t pair = (uint32_t)(uint8_t)(int8_t)qg | ((uint32_t)(uint8_t)(int8_t)qh << 8);
                 uint4 v = w[u];
                 if (sub == LPR - 1) v.w = (v.w & 0xFFFFu) | (pair << 16);
-                // every lane writes its 16 bytes back, so consecutive rows
-                // rewrite whole 128-byte lines (no partial-line update)
-                if (i < hi) rec_w[(size_t)r * LPR + sub] = v;
+                // record partition: the pair goes to the pair plane (the
+                // root's partition patches it into each record it moves);
+                // otherwise every lane writes its 16 bytes back, so
+                // consecutive rows rewrite whole 128-byte lines (no
+                // partial-line update)
+                if (s.rcp) {
+                    if (i < hi && sub == LPR - 1) s.pairs[r] = (uint16_t)pair;
+                } else if (i < hi) {
+                    rec_w[(size_t)r * LPR + sub] = v;
+                }
                 gh[u] = group_last_lane<LPR>(v.w);
             }
         } else {
@@ -2170,6 +2177,169 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
     }
 }
 
+// ------------------------------------------------------ record partition
+// The partition of the record layout (s.rcp): the same tasks, counts, scans
+// and reservations as k_partition, but a row travels as its whole record
+// (LPR x 16 bytes, with its int8 pair in the last two bytes) from the
+// parent's range of one record buffer to the child's range of the other, so
+// the split feature's bin is a byte of the record already loaded (no column
+// gather) and the children's accumulations read their records as one
+// contiguous stream. The root's batch reads the dataset's records instead
+// -- row id = position, or from the root list -- with each row's pair from
+// the plane the root build wrote. kPartRows (4) rows per thread.
+template <int LPR>
+__global__ __launch_bounds__(kPartThreads) void k_partition_rec(DevState s) {
+    constexpr int R = kPartRows;
+    constexpr int NW = kPartThreads / 64;  // waves
+    constexpr int E = R * NW;              // (row group, wave) entries of a task
+    constexpr int SW = (E + 63) / 64;      // waves that scan one side's entries
+    static_assert((E % 64 == 0 || E < 64) && 2 * SW <= NW, "one wave scans up to 64 entries");
+    __shared__ int cnt_l[E], cnt_r[E];
+    __shared__ int wtot[2][SW];
+    __shared__ long long base[2];
+    const Batch bh = *s.batch;
+    const int n_blocks = bh.n_blocks;
+    if ((int)blockIdx.x >= n_blocks) return;
+    const int tid = threadIdx.x, lane = lane_id(), w = tid >> 6;
+    const unsigned long long below = (1ULL << lane) - 1ULL;
+    const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
+    PartItem pit{};
+    if (lane < bh.n_items) pit = s.part_items[lane];
+    for (int blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const unsigned long long own = __ballot(lane < bh.n_items && pit.qoff <= blk);  // item 0 starts at 0
+        const int q = 63 - (int)__builtin_clzll(own);
+        const int64_t begin = readlane_i64(pit.begin, q);
+        const int64_t n_left = readlane_i64(pit.n_left, q);
+        const int64_t m = readlane_i64(pit.m, q);
+        const int64_t c0 = (int64_t)(blk - __builtin_amdgcn_readlane(pit.qoff, q)) * bh.chunk_p;
+        const int64_t c1 = c0 + bh.chunk_p < m ? c0 + bh.chunk_p : m;
+        const int src_buf = __builtin_amdgcn_readlane(pit.src_buf, q);
+        const int feature = __builtin_amdgcn_readlane(pit.feature, q);
+        const int thr = __builtin_amdgcn_readlane(pit.bin, q);
+        const int dl = __builtin_amdgcn_readlane(pit.default_left, q);
+        const int mbin = __builtin_amdgcn_readlane(pit.missing_bin, q);
+        const int cat_e = __builtin_amdgcn_readlane(pit.cat_e, q);
+        const int direct = __builtin_amdgcn_readlane(pit.direct, q);
+        const int root = __builtin_amdgcn_readlane(pit.root, q);
+        unsigned long long cset[4] = {0ULL, 0ULL, 0ULL, 0ULL};
+        const bool is_cat = cat_e >= 0;
+        if (is_cat)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cset[k] = s.e_cat[(size_t)cat_e * 4 + k];
+        uint4 rec[R][LPR];
+        uint32_t vbits = 0, lbits = 0;
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+            vbits |= (i < c1 ? 1u : 0u) << u;
+        }
+        // every load unconditional (a slot past the task re-reads its last
+        // row and is masked off), so all of them are in flight together
+        if (root) {
+            int32_t r[R];
+            uint32_t pr[R];
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+                i = i < c1 ? i : c1 - 1;
+                r[u] = direct ? (int32_t)(begin + i) : s.rows0[begin + i];
+                if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the root list
+            }
+            const uint4 *src = (const uint4 *)s.records;
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+#pragma unroll
+                for (int k = 0; k < LPR; ++k) rec[u][k] = src[(size_t)(uint32_t)r[u] * LPR + k];
+                pr[u] = s.pairs[(uint32_t)r[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < R; ++u) rec[u][LPR - 1].w = (rec[u][LPR - 1].w & 0xFFFFu) | (pr[u] << 16);
+        } else {
+            const uint4 *src = (const uint4 *)(src_buf ? s.crec1 : s.crec0) + (size_t)begin * LPR;
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+                i = i < c1 ? i : c1 - 1;
+#pragma unroll
+                for (int k = 0; k < LPR; ++k) rec[u][k] = src[(size_t)i * LPR + k];
+            }
+        }
+        // the split feature's byte of each record: the dword holding it is
+        // picked by a task-uniform select (no indexing into registers)
+        const int fw = feature >> 2, fsh = 8 * (feature & 3);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            uint32_t word = 0u;
+#pragma unroll
+            for (int k = 0; k < LPR; ++k) {
+                word = fw == 4 * k + 0 ? rec[u][k].x : word;
+                word = fw == 4 * k + 1 ? rec[u][k].y : word;
+                word = fw == 4 * k + 2 ? rec[u][k].z : word;
+                word = fw == 4 * k + 3 ? rec[u][k].w : word;
+            }
+            const int b = (int)((word >> fsh) & 255u);
+            const bool valid = (vbits >> u) & 1u;
+            const unsigned long long cw = b < 64 ? cset[0] : b < 128 ? cset[1] : b < 192 ? cset[2] : cset[3];
+            const bool left = is_cat ? ((cw >> (b & 63)) & 1ULL) != 0 : (b == mbin) ? (dl != 0) : (b <= thr);
+            lbits |= (left ? 1u : 0u) << u;
+            const unsigned long long lm = __ballot(valid && left);
+            const unsigned long long rm = __ballot(valid && !left);
+            if (lane == 0) {
+                cnt_l[u * NW + w] = __popcll(lm);
+                cnt_r[u * NW + w] = __popcll(rm);
+            }
+        }
+        __syncthreads();
+        if (w < 2 * SW) {
+            int *c = w < SW ? cnt_l : cnt_r;
+            const int k = (w % SW) * 64 + lane;
+            const int v = k < E ? c[k] : 0;
+            const int inc = wave_incl_scan_i(v);
+            if (k < E) c[k] = inc - v;
+            if (lane == 63) wtot[w / SW][w % SW] = inc;
+        }
+        __syncthreads();
+        if (tid < 2) {
+            int a = 0;
+            for (int j = 0; j < SW; ++j) {
+                const int t = wtot[tid][j];
+                wtot[tid][j] = a;
+                a += t;
+            }
+            unsigned long long *cur = (unsigned long long *)&s.cursor[2 + 2 * q + tid];
+            base[tid] = a ? (long long)atomicAdd(cur, (unsigned long long)a) : 0;
+        }
+        __syncthreads();
+        // positions relative to the leaf's begin (below m < 2^31); a record
+        // that would land past its side of the range is not stored, and
+        // flagged
+        const int bl = (int)base[0], br = (int)base[1];
+        const int nl = (int)n_left, mm = (int)m;
+        uint4 *dst = (uint4 *)(src_buf ? s.crec0 : s.crec1) + (size_t)begin * LPR;
+        bool overflow = false;
+        asm volatile("" : "+v"(lbits), "+v"(vbits));
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const bool valid = (vbits >> u) & 1u;
+            const bool left = (lbits >> u) & 1u;
+            const unsigned long long lm = __ballot(valid && left);
+            const unsigned long long rm = __ballot(valid && !left);
+            const int k = u * NW + w;
+            const int pl = bl + wtot[0][k >> 6] + cnt_l[k] + (int)__popcll(lm & below);
+            const int pr = nl + br + wtot[1][k >> 6] + cnt_r[k] + (int)__popcll(rm & below);
+            const int pos = left ? pl : pr;
+            const bool bad = left ? pl >= nl : pr >= mm;
+            overflow |= valid && bad;
+            if (valid && !bad) {
+#pragma unroll
+                for (int kk = 0; kk < LPR; ++kk) dst[(size_t)pos * LPR + kk] = rec[u][kk];
+            }
+        }
+        if (overflow) atomicOr(s.error, 1);
+        __syncthreads();  // counts and offsets are rewritten by the next task
+    }
+}
+
 // ---------------------------------------------------------- accumulation
 // One launch accumulates the smaller child of every leaf of the batch from
 // its rows, now contiguous in the partitioned row buffer. Each task (found
@@ -2208,6 +2378,41 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
             s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec, goss_mult);
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
+        __syncthreads();  // the LDS histogram is zeroed again for the next task
+    }
+}
+
+// The accumulation of the record layout (s.rcp): an accumulated child's
+// records are contiguous in its range of a record buffer, so a task streams
+// them (no row id, no gather), kAccUnrollRec rows per lane and step.
+#ifndef MB_ACC_UNROLL_REC
+#define MB_ACC_UNROLL_REC 2
+#endif
+constexpr int kAccUnrollRec = MB_ACC_UNROLL_REC;
+template <int LPR>
+__global__ __launch_bounds__(kAccThreads) void k_accum_rec(DevState s) {
+    extern __shared__ unsigned char lds[];
+    const Batch bh = *s.batch;
+    const int n_acc = bh.n_acc;
+    if ((int)blockIdx.x >= n_acc) return;
+    const int ls = s.lds_stride;
+    const int Ft = s.n_features;  // one tile
+    const int lane = lane_id();
+    AccItem ait{};
+    if (lane < bh.n_items) ait = s.acc_items[lane];
+    for (int blk = blockIdx.x; blk < n_acc; blk += gridDim.x) {
+        const unsigned long long own = __ballot(lane < bh.n_items && ait.poff <= blk);  // item 0 starts at 0
+        const int q = 63 - (int)__builtin_clzll(own);
+        const int64_t lo = readlane_i64(ait.lo, q) + (int64_t)(blk - __builtin_amdgcn_readlane(ait.poff, q)) * bh.chunk_a;
+        const int64_t hi_item = readlane_i64(ait.hi, q);
+        const int64_t hi = lo + bh.chunk_a < hi_item ? lo + bh.chunk_a : hi_item;
+        const int buf = __builtin_amdgcn_readlane(ait.buf, q);
+        const uint4 *rec = (const uint4 *)(buf ? s.crec1 : s.crec0);
+        QAcc::template zero<LPR>(lds, Ft, ls);
+        __syncthreads();
+        accumulate_rows<LPR, QAcc, false, false, kAccUnrollRec>(s, lds, nullptr, lo, hi, Ft, rec, 1.0);
+        __syncthreads();
+        QAcc::template store<LPR>(s, lds, blk, 0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next task
     }
 }
@@ -4521,6 +4726,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         // the root of an unsampled round spans every row in order: its
         // partition computes the ids instead of reading an identity list
         pi.direct = (Xs == 0 && !rd.sampled) ? 1 : 0;
+        pi.root = Xs == 0 ? 1 : 0;
+        pi.pad_ = 0;
         s.part_items[jj] = pi;
         AccItem ai;
         ai.lo = bl ? b0 : b0 + nlft;
@@ -5094,6 +5301,9 @@ hipError_t prepare_kernels(const DevState &s) {
         MB_SET_LDS((k_accum<2, QAcc>), h);
         MB_SET_LDS((k_accum<4, QAcc>), h);
         MB_SET_LDS((k_accum<8, QAcc>), h);
+        MB_SET_LDS(k_accum_rec<1>, h);
+        MB_SET_LDS(k_accum_rec<2>, h);
+        MB_SET_LDS(k_accum_rec<4>, h);
     } else {
         MB_SET_LDS((k_hist<1, FAcc>), h);
         MB_SET_LDS((k_hist<2, FAcc>), h);
@@ -5143,6 +5353,15 @@ hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEve
                             : launch_hist_t<FAcc>(s, st, ev0, ev1);
 }
 hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, bool root) {
+    if (s.rcp) {
+        const dim3 grid(s.part_launch), block(kPartThreads);
+        switch (s.rec_bytes / 16) {
+        case 1: return launch_timed(k_partition_rec<1>, grid, block, 0, st, s, ev0, ev1);
+        case 2: return launch_timed(k_partition_rec<2>, grid, block, 0, st, s, ev0, ev1);
+        case 4: return launch_timed(k_partition_rec<4>, grid, block, 0, st, s, ev0, ev1);
+        default: return hipErrorInvalidValue;
+        }
+    }
     if (root) return launch_timed(k_partition<kPartRowsRoot>, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
     return launch_timed(k_partition<kPartRows>, dim3(s.part_launch), dim3(kPartThreads), 0, st, s, ev0, ev1);
 }
@@ -5159,6 +5378,16 @@ hipError_t launch_accum_t(const DevState &s, hipStream_t st, hipEvent_t ev0, hip
     }
 }
 hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (s.rcp) {
+        const size_t lds = hist_lds_bytes(s);
+        const dim3 grid(s.pb_launch), block(kAccThreads);
+        switch (s.rec_bytes / 16) {
+        case 1: return launch_timed(k_accum_rec<1>, grid, block, lds, st, s, ev0, ev1);
+        case 2: return launch_timed(k_accum_rec<2>, grid, block, lds, st, s, ev0, ev1);
+        case 4: return launch_timed(k_accum_rec<4>, grid, block, lds, st, s, ev0, ev1);
+        default: return hipErrorInvalidValue;
+        }
+    }
     return s.hp.stage16     ? launch_accum_t<WAcc16>(s, st, ev0, ev1)
            : s.hp.wide      ? launch_accum_t<WAcc>(s, st, ev0, ev1)
            : s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1)

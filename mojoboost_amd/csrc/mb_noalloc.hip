@@ -163,14 +163,17 @@ extern "C" int32_t mbh_histogram_noalloc(const uint8_t *bins_cm, int64_t n_rows,
         set_err(err, err_len, "rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
         return MOJOTREES_ERROR_INVALID_ARGUMENT;
     }
-    const int cells = n_features * n_bins;
-    const size_t partial_bytes = (size_t)cells * sizeof(unsigned long long);
-    if (partial_bytes > kScratchBytes) {
+    // one partial in 64-bit arithmetic, checked before anything divides by
+    // it or narrows the cell count (n_features * n_bins may exceed int)
+    const int64_t cells64 = (int64_t)n_features * (int64_t)n_bins;
+    const uint64_t partial_bytes = (uint64_t)cells64 * sizeof(unsigned long long);
+    if (partial_bytes > (uint64_t)kScratchBytes) {
         set_err(err, err_len,
                 "n_features * n_bins exceeds the no-alloc scratch (one partial of 8 bytes per cell must fit "
                 "MBH_NOALLOC_SCRATCH_BYTES)");
         return MOJOTREES_ERROR_INVALID_ARGUMENT;
     }
+    const int cells = (int)cells64;  // at most kScratchBytes / 8 after the check
     int max_blocks = (int)(kScratchBytes / partial_bytes);
     if (max_blocks > kMaxBlocks) max_blocks = kMaxBlocks;
     const int64_t limit = chunk_limit(B);

@@ -64,6 +64,8 @@ struct PartItem {
     int32_t qoff, src_buf, feature, bin, default_left, missing_bin;
     int32_t cat_e;  // categorical split: the explored node whose e_cat set routes left; -1 numerical
     int32_t direct; // 1: the parent is the root over every row in order (row id = position, no list read)
+    int32_t root;   // 1: the parent is the round's root (record partition: read the dataset's records)
+    int32_t pad_;
 };
 
 // A batch item's accumulation work: its accumulated child, rows [lo, hi) of
@@ -243,6 +245,20 @@ struct DevState {
     const int32_t *scan_order;  // F, with ncat: scan task order of the features (category-set ones first)
     const uint8_t *feature_mask; // num_trees x F (1: the tree may split it)
     uint8_t *records_w;          // same buffer as records, writable view
+    // Record partition (rcp = 1): a leaf's rows are held as their records,
+    // contiguous in the leaf's range [begin, end) of crec0 / crec1 (the
+    // leaf's buf), each with the round's int8 pair in its last two bytes; the
+    // partition moves whole records to the children's ranges and the
+    // accumulation streams them, so no row id is read below the root. The
+    // root build writes each root row's pair to `pairs` (2 bytes per row)
+    // instead of into the dataset's records, and the root's partition reads
+    // the dataset's records (by position or through the root list) with
+    // their pairs. rcp = 0: leaves hold row ids in rows0 / rows1 and every
+    // record is gathered by id.
+    uint8_t *crec0, *crec1;      // n x rec_bytes each (rcp)
+    uint16_t *pairs;             // n: the root rows' int8 (grad, hess) pairs (rcp)
+    int32_t rcp;
+    int32_t pad_rcp_;
     int64_t n;
     int32_t n_features;
     int32_t n_bins;        // histogram stride per feature

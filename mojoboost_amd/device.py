@@ -233,7 +233,8 @@ class Fit:
                  "hist_builds", "root_bytes", "root_ms", "trees_grown", "growth_ms",
                  "root_growth_ms", "iterations", "expansions", "rows_built", "rows_parted",
                  "expand_launches", "expand_ms", "expand_bytes", "partition_ms", "accum_ms",
-                 "accum_bytes")
+                 "accum_bytes", "root_quantizer_bytes",
+                 "partition_bytes")
         st = np.zeros(len(names))
         count = L.mbh_fit_stats(handle, ptr(st), len(names))
         assert count == len(names), count
