@@ -221,6 +221,39 @@ def rocprof_summary(path):
     return 0
 
 
+SIZE_EDGES = [1, 16_384, 65_536, 262_144, 1_048_576, 4_194_304]
+
+
+def size_classes(log, rows_col, ms_col, bytes_per_row):
+    """Launches of one expansion kernel by rows per launch: count, rows,
+    mean duration, share of the kernel's time and algorithmic GB/s per
+    class. `log` is a fit's launch_log (tree, iteration, rows partitioned,
+    rows accumulated, partition ms, accumulation ms)."""
+    rows, ms = log[:, rows_col], log[:, ms_col]
+    total = max(1e-12, float(ms.sum()))
+    edges = [0] + SIZE_EDGES + [float("inf")]
+    out = []
+    for lo, hi in zip(edges[:-1], edges[1:]):
+        sel = (rows >= lo) & (rows < hi) if lo > 0 else rows == 0
+        if not sel.any():
+            continue
+        r, t = float(rows[sel].sum()), float(ms[sel].sum())
+        out.append({"rows": "0" if lo == 0 else f"{int(lo)}-{'' if hi == float('inf') else int(hi)}",
+                    "launches": int(sel.sum()), "rows_per_launch": round(r / sel.sum(), 1),
+                    "avg_us": round(t / sel.sum() * 1e3, 2), "time_share": round(t / total, 4),
+                    "gbs": round(r * bytes_per_row / (t * 1e-3) / 1e9, 1) if t > 0 else None})
+    return out
+
+
+def size_table_md(title, classes):
+    lines = [f"### {title}", "", "| rows per launch | launches | avg rows | avg us | share of time | GB/s |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for c in classes:
+        lines.append(f"| {c['rows']} | {c['launches']} | {c['rows_per_launch']:.0f} | {c['avg_us']:.2f} | "
+                     f"{c['time_share']:.1%} | {c['gbs'] if c['gbs'] is not None else '-'} |")
+    return "\n".join(lines) + "\n"
+
+
 def copy_probe(mib):
     """One hipMemcpy device-to-device of `mib` MiB: the runtime's blit kernel
     reads and writes exactly that many bytes, which calibrates the HBM byte
@@ -253,6 +286,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=None,
                     help="oracle sample: trees (rounds for c5); default per workload")
     ap.add_argument("--no-instrumented", action="store_true")
+    ap.add_argument("--launch-table", default=None,
+                    help="also write the expansion kernels' size-class tables (markdown) to this file")
     ap.add_argument("--partition-mode", type=int, default=0,
                     help="leaf rows as 0 automatic, 1 records, 2 row ids (mbh_params.partition_mode)")
     ap.add_argument("--rocprof-summary", default=None,
@@ -351,6 +386,7 @@ def main():
     if not args.no_instrumented:
         ifit = ds.train(num_iterations=full, time_histograms=1, **kw)
         st = ifit.stats
+        launch_log = ifit.launch_log
         same = np.array_equal(ifit.threshold, full_fit.threshold) and np.array_equal(
             ifit.value.view(np.uint64), full_fit.value.view(np.uint64))
         print(f"[bench] instrumented full run done (trees identical to the timed run: {same})",
@@ -438,7 +474,20 @@ def main():
             "root_build_in_training_gbs": round(st["root_bytes"] / (st["root_ms"] * 1e-3) / 1e9, 1),
             "root_quantizer_bytes_per_tree": round(st["root_quantizer_bytes"] * per_tree, 1),
             "accum_gbs": round(kernel_gbs, 1),
+            "accum_size_classes": size_classes(launch_log, 3, 5, F + GH),
         }
+        rec_mode = st["partition_bytes"] != st["rows_parted"] * 9.0
+        part_row_bytes = st["partition_bytes"] / max(1.0, st["rows_parted"])
+        if args.launch_table:
+            with open(args.launch_table, "w") as fh:
+                fh.write(f"Workload {args.workload}, {stat_steps} trees, leaf rows as "
+                         f"{'records' if rec_mode else 'row ids'}; algorithmic bytes per accumulated row "
+                         f"F + {GH} = {F + GH}, per partitioned row {part_row_bytes:.1f}\n\n")
+                fh.write(size_table_md("k_accum (accumulation) by rows accumulated per launch",
+                                       size_classes(launch_log, 3, 5, F + GH)))
+                fh.write("\n")
+                fh.write(size_table_md("k_partition by rows partitioned per launch",
+                                       size_classes(launch_log, 2, 4, part_row_bytes)))
         note = (f"dominant histogram kernel k_accum (smaller-child accumulation from the "
                 f"partitioned row list) over the instrumented {stat_steps}-step training, "
                 f"algorithmic bytes per launch = accumulated rows * (F + {GH}) "

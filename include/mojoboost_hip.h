@@ -222,6 +222,13 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err,
  *        records [13] * 2 * record bytes + root rows * 2 (the root's pairs) */
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out);
 
+/* Per expansion launch of a time_histograms=1 fit, six values each: tree,
+ * expansion iteration, rows partitioned, rows accumulated (from the
+ * planner's batch; 0 for the empty launches after a tree is done), and the
+ * partition and accumulation kernels' durations in ms. Writes min(n_out,
+ * count) values and returns count (6 per launch; 0 for untimed fits). */
+int64_t mbh_fit_launch_log(const mbh_fit *fit, double *out, int64_t n_out);
+
 /* Query groups of a resident dataset, for objective lambdarank: counts[q]
  * rows per query, in row order (LightGBM's `group`,
  * ranking.groups_from_counts, src/mojotrees/ranking.mojo:152-169); counts must

@@ -38,7 +38,7 @@ MBH_SYMBOLS = [
     "mbh_predict_binned", "mbh_dataset_set_groups", "mbh_lambdarank", "mbh_train_ranker_dense",
     "mbh_bin_dense_cat", "mbh_dataset_set_categorical", "mbh_fit_cat_bits", "mbh_dataset_set_weights",
     "mbh_histogram_noalloc", "mbh_save_model_named", "mbh_model_feature_names",
-    "mbh_objective_quantize32", "mbh_histogram32", "mbh_bin_dense_device",
+    "mbh_objective_quantize32", "mbh_histogram32", "mbh_bin_dense_device", "mbh_fit_launch_log",
 ]
 
 
@@ -156,6 +156,7 @@ def lib():
         "mbh_fit_arrays": (None, [V] * 12),
         "mbh_fit_train_raw": (I32, [V, V, C.c_char_p, I32]),
         "mbh_fit_stats": (I32, [V, V, I32]),
+        "mbh_fit_launch_log": (I64, [V, V, I64]),
         "mbh_exp_sigmoid": (I32, [V, I64, V, V, C.c_char_p, I32]),
         "mbh_objective_quantize": (I32, [V, P(MbhParams), V, I64, V, V, V, V, V, C.c_char_p, I32]),
         "mbh_histogram": (I32, [V, V, V, V, I64, I32, V, C.c_char_p, I32]),

@@ -152,6 +152,9 @@ struct mbh_fit {
     std::vector<uint64_t> cat_bits;  // 4 words per node
     std::vector<double> train_raw;
     double stats[kNumStats] = {0};
+    // time_histograms runs: per expansion launch, (tree, iteration, rows
+    // partitioned, rows accumulated, partition ms, accumulation ms)
+    std::vector<double> launch_log;
 };
 
 namespace {
@@ -941,6 +944,9 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         double t_acc = 0.0, t_root = 0.0, t_root_scan = 0.0, t_pb = 0.0, t_scan = 0.0;
         double t_part = 0.0, t_accum = 0.0;
         double pb_launches = 0.0;
+        // per launch of a group slot: its tree and iteration index
+        int group_tree[2] = {0, 0}, group_iter0[2] = {0, 0};
+        std::vector<double> launch_ms;  // tree, iteration, partition ms, accumulation ms
         auto add_group = [&](int slot, int n) {
             for (int c = 0; c < n; ++c) {
                 float a = 0.f, b = 0.f, d = 0.f;
@@ -951,8 +957,15 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 t_accum += b;
                 t_pb += a + b;
                 t_scan += d;
+                launch_ms.insert(launch_ms.end(), {(double)group_tree[slot], (double)(group_iter0[slot] + c),
+                                                   (double)a, (double)b});
             }
         };
+        if (timed) {
+            s.iter_stride = L + kMaxGroup + 4;
+            s.iter_log = dalloc<int64_t>((size_t)T * s.iter_stride * 2, run.owned);
+            HIPX(hipMemset(s.iter_log, 0, (size_t)T * s.iter_stride * 2 * sizeof(int64_t)));
+        }
         // expansion launches the previous tree needed: the first group of a
         // tree is that long, later groups kNextGroup
         int est = kFirstGroup;
@@ -996,6 +1009,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 // launches
                 const int n = k == 0 ? std::max(1, std::min(est - 2, kMaxGroup)) : kNextGroup;
                 group_size[slot] = n;
+                group_tree[slot] = t;
+                group_iter0[slot] = iters;
                 for (int c = 0; c < n; ++c) {
                     if (timed) {
                         HIPX(mb::launch_partition(s, st, ev_group(slot, c, 0), ev_group(slot, c, 1),
@@ -1063,6 +1078,20 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         HIPX(hipMemcpy(ai.data(), s.arc_int, ai.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(ad.data(), s.arc_dbl, ad.size() * sizeof(double), hipMemcpyDeviceToHost));
         HIPX(hipMemcpy(ax.data(), s.arc_aux, ax.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
+        if (timed) {
+            // each launch's rows from the planner's log (zero for the empty
+            // launches after a tree is done)
+            std::vector<int64_t> lg((size_t)T * s.iter_stride * 2);
+            HIPX(hipMemcpy(lg.data(), s.iter_log, lg.size() * sizeof(int64_t), hipMemcpyDeviceToHost));
+            for (size_t i = 0; i + 3 < launch_ms.size(); i += 4) {
+                const int t = (int)launch_ms[i], it = (int)launch_ms[i + 1];
+                const bool in = it < s.iter_stride;
+                const size_t o = 2 * ((size_t)t * s.iter_stride + (in ? it : 0));
+                fit->launch_log.insert(fit->launch_log.end(),
+                                       {(double)t, (double)it, in ? (double)lg[o] : 0.0, in ? (double)lg[o + 1] : 0.0,
+                                        launch_ms[i + 2], launch_ms[i + 3]});
+            }
+        }
         std::vector<unsigned long long> acat;
         if (s.arc_cat) {
             acat.resize((size_t)tb.T * mn * 4);
@@ -1215,6 +1244,13 @@ int32_t mbh_fit_train_raw(const mbh_fit *fit, double *out, char *err, int32_t er
     }
     std::memcpy(out, fit->train_raw.data(), fit->train_raw.size() * sizeof(double));
     return MOJOTREES_OK;
+}
+int64_t mbh_fit_launch_log(const mbh_fit *fit, double *out, int64_t n_out) {
+    if (!fit) return 0;
+    const int64_t n = (int64_t)fit->launch_log.size();
+    if (out)
+        for (int64_t i = 0; i < n && i < n_out; ++i) out[i] = fit->launch_log[(size_t)i];
+    return n;
 }
 int32_t mbh_fit_stats(const mbh_fit *fit, double *out, int32_t n_out) {
     if (fit && out)

@@ -2178,6 +2178,8 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
 }
 
 // ------------------------------------------------------ record partition
+// kPartRecThreads x kPartRows rows per task at most (the planner caps a
+// record partition's tasks at kPartRecChunk rows).
 // The partition of the record layout (s.rcp): the same tasks, counts, scans
 // and reservations as k_partition, but a row travels as its whole record
 // (LPR x 16 bytes, with its int8 pair in the last two bytes) from the
@@ -2188,9 +2190,10 @@ __global__ __launch_bounds__(kPartThreads) void k_partition(DevState s) {
 // -- row id = position, or from the root list -- with each row's pair from
 // the plane the root build wrote. kPartRows (4) rows per thread.
 template <int LPR>
-__global__ __launch_bounds__(kPartThreads) void k_partition_rec(DevState s) {
+__global__ __launch_bounds__(kPartRecThreads) void k_partition_rec(DevState s) {
     constexpr int R = kPartRows;
-    constexpr int NW = kPartThreads / 64;  // waves
+    constexpr int T = kPartRecThreads;
+    constexpr int NW = T / 64;             // waves
     constexpr int E = R * NW;              // (row group, wave) entries of a task
     constexpr int SW = (E + 63) / 64;      // waves that scan one side's entries
     static_assert((E % 64 == 0 || E < 64) && 2 * SW <= NW, "one wave scans up to 64 entries");
@@ -2230,7 +2233,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition_rec(DevState s) {
         uint32_t vbits = 0, lbits = 0;
 #pragma unroll
         for (int u = 0; u < R; ++u) {
-            const int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+            const int64_t i = c0 + (int64_t)u * T + tid;
             vbits |= (i < c1 ? 1u : 0u) << u;
         }
         // every load unconditional (a slot past the task re-reads its last
@@ -2240,7 +2243,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition_rec(DevState s) {
             uint32_t pr[R];
 #pragma unroll
             for (int u = 0; u < R; ++u) {
-                int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+                int64_t i = c0 + (int64_t)u * T + tid;
                 i = i < c1 ? i : c1 - 1;
                 r[u] = direct ? (int32_t)(begin + i) : s.rows0[begin + i];
                 if ((uint32_t)r[u] >= n32) r[u] = 0;  // never taken: ids come from the root list
@@ -2258,7 +2261,7 @@ __global__ __launch_bounds__(kPartThreads) void k_partition_rec(DevState s) {
             const uint4 *src = (const uint4 *)(src_buf ? s.crec1 : s.crec0) + (size_t)begin * LPR;
 #pragma unroll
             for (int u = 0; u < R; ++u) {
-                int64_t i = c0 + (int64_t)u * kPartThreads + tid;
+                int64_t i = c0 + (int64_t)u * T + tid;
                 i = i < c1 ? i : c1 - 1;
 #pragma unroll
                 for (int k = 0; k < LPR; ++k) rec[u][k] = src[(size_t)i * LPR + k];
@@ -4621,7 +4624,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         long long chunk_p = (rows_total + s.part_target - 1) / s.part_target;
         chunk_p = (chunk_p + kPartChunkStep - 1) / kPartChunkStep * kPartChunkStep;
         // the root's batch has a launch of its own with larger tasks
-        const long long cmax = root_mode && s.part_root ? kPartChunkRoot : kPartChunk;
+        const long long cmax = s.rcp ? (long long)kPartRecThreads * kPartRows
+                               : root_mode && s.part_root ? kPartChunkRoot : kPartChunk;
         chunk_p = chunk_p < kPartChunkMin ? kPartChunkMin : chunk_p > cmax ? cmax : chunk_p;
         const int qc = lane < nsel ? (int)((m + chunk_p - 1) / chunk_p) : 0;
         const int pi = wave_incl_scan_i(pc), qi = wave_incl_scan_i(qc);
@@ -4739,6 +4743,11 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     __syncthreads();
     __syncthreads();
     if (tid == 0) {
+        if (s.iter_log && g.iterations < s.iter_stride) {
+            int64_t *lg = s.iter_log + 2 * ((size_t)rd.tree_index * s.iter_stride + g.iterations);
+            lg[0] = (int64_t)s_rows_parted;
+            lg[1] = (int64_t)s_rows_built;
+        }
         g.n_explored = ne + 2 * nsel;
         g.n_hist += nsel;
         g.expansions += nsel;
@@ -5354,7 +5363,9 @@ hipError_t launch_hist(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEve
 }
 hipError_t launch_partition(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, bool root) {
     if (s.rcp) {
-        const dim3 grid(s.part_launch), block(kPartThreads);
+        // a CU holds several record-partition blocks: the grid is widened
+        // to keep the same rows in flight
+        const dim3 grid(s.part_launch * (kPartThreads / kPartRecThreads)), block(kPartRecThreads);
         switch (s.rec_bytes / 16) {
         case 1: return launch_timed(k_partition_rec<1>, grid, block, 0, st, s, ev0, ev1);
         case 2: return launch_timed(k_partition_rec<2>, grid, block, 0, st, s, ev0, ev1);

@@ -142,6 +142,12 @@ constexpr int kPartChunk = MB_PART_CHUNK;
 #endif
 constexpr int kPartChunkMin = MB_PART_CHUNK_MIN;
 constexpr int kPartChunkStep = 256;
+// Threads of a record-partition block (leaves holding records); its tasks
+// take at most kPartRecChunk rows (kPartRows per thread).
+#ifndef MB_PART_REC_THREADS
+#define MB_PART_REC_THREADS 512
+#endif
+constexpr int kPartRecThreads = MB_PART_REC_THREADS;
 constexpr int kPartChunkRoot = 16384;  // at most, per task of the root's batch (its own launch)
 // Root build launch: kHistThreads per block, kHistBlocksPerCU blocks per CU
 // (each with its own LDS histogram).
@@ -355,6 +361,12 @@ struct DevState {
     int32_t *arc_int;      // per tree: max_nodes x 6 ints + 2 meta
     double *arc_dbl;       // per tree: max_nodes x 3 doubles
     int64_t *arc_aux;      // per tree: rows accumulated, iterations, expansions, 0
+    // per (tree, expansion iteration): the rows the iteration's batch
+    // partitions and accumulates, written by the planner when it plans the
+    // batch (time_histograms runs only; null otherwise)
+    int64_t *iter_log;
+    int32_t iter_stride;   // iterations per tree in iter_log
+    int32_t pad_log_;
     unsigned long long *arc_cat;  // per tree: max_nodes x 4 (when a feature is categorical)
     int32_t max_nodes;
     HyperParams hp;

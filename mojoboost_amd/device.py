@@ -239,6 +239,14 @@ class Fit:
         count = L.mbh_fit_stats(handle, ptr(st), len(names))
         assert count == len(names), count
         self.stats = dict(zip(names, (float(v) for v in st)))
+        # time_histograms fits: one row per expansion launch (tree,
+        # iteration, rows partitioned, rows accumulated, partition ms,
+        # accumulation ms); empty otherwise
+        n_log = int(L.mbh_fit_launch_log(handle, None, 0))
+        log = np.zeros(n_log)
+        if n_log:
+            L.mbh_fit_launch_log(handle, ptr(log), n_log)
+        self.launch_log = log.reshape(-1, 6)
 
     def tree(self, t):
         a, b = self.off[t], self.off[t + 1]
