@@ -339,12 +339,16 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // n / kPartChunkMin + (batch size) of them at most, spread over about two
 // tasks per CU.
 constexpr int64_t kHistChunkMin = 2048;
+constexpr int64_t kHistChunkMinF = 512;  // fp32 cells
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run &run) {
     const bool quantized = kind != mb::kAccFloat;
     // the packed int8-lattice counters bound a block's rows; the other
     // accumulators hold whole-round sums in every field
-    const int64_t limit = kind == mb::kAccQuant ? chunk_limit_for(B) : (int64_t)1 << 30;
+    // the fp32 cells' 16-bit count halves bound a block's rows too
+    const int64_t limit = kind == mb::kAccQuant   ? chunk_limit_for(B)
+                          : kind == mb::kAccFloat ? mb::kFAccChunk
+                                                  : (int64_t)1 << 30;
     // resident root-build blocks, shared by the feature tiles (a launch runs
     // grid x tiles blocks): every block then takes more rows, and zeroes,
     // stores and leaves to the scan's merge one partial per tile and block
@@ -353,17 +357,21 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     if (grid < need) grid = need;
     s.hist_grid = (int32_t)grid;
     s.part_stride = (ds->nb + 1) & ~1;
-    s.hist_chunk_min = std::min<int64_t>(kHistChunkMin, limit);
+    // the fp32 cells' per-row LDS work is three times the quantized one's:
+    // smaller launches are spread over more blocks
+    s.hist_chunk_min = std::min<int64_t>(kind == mb::kAccFloat ? kHistChunkMinF : kHistChunkMin, limit);
     s.hist_chunk_limit = limit;
     s.kmax = kMaxBatch;
-    s.pb_grid = (int32_t)((ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
-    s.part_grid = (int32_t)((ds->n + mb::kPartChunkMin - 1) / mb::kPartChunkMin + s.kmax);
-    s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     // one accumulation task per resident block: two per CU where two LDS
     // histograms fit (quantized), one for the fp32 cells, whose histogram
     // fills a CU's LDS (half the partials to merge; measured 0.3 % faster on
     // C3 than two tasks per CU run one after the other)
-    s.pb_launch = std::min<int32_t>(s.pb_grid, (kind == mb::kAccFloat ? 1 : 2) * ds->n_cu);
+    s.pb_launch = (kind == mb::kAccFloat ? 1 : 2) * ds->n_cu;
+    // a batch's accumulation tasks: with chunk >= its rows / pb_launch (or
+    // = limit) an item of m rows takes at most m / chunk + 1 of them
+    s.pb_grid = (int32_t)(s.pb_launch + s.kmax + (ds->n + limit - 1) / limit);
+    s.part_grid = (int32_t)((ds->n + mb::kPartChunkMin - 1) / mb::kPartChunkMin + s.kmax);
+    s.scan_grid = std::min(s.kmax * ds->F, 4 * ds->n_cu);
     s.part_launch = std::min<int32_t>(s.part_grid, 8 * ds->n_cu);
     s.part_target = 2 * ds->n_cu;
     // the root's batch gets the launch of larger tasks only where its rows
@@ -654,6 +662,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     hp.cat_smooth = p->cat_smooth;
     hp.cat_l2 = p->cat_l2;
 
+    // the fp32 path's binary32 derivatives, interleaved per row
+    if (!quantized && !hp.grad64) s.gh2 = dalloc<float>(2 * (size_t)ds->n, run.owned);
     if (mb::plan_lds_bytes(s) > 160 * 1024)
         throw Error{MOJOTREES_ERROR_UNSUPPORTED,
                     "num_leaves * n_features too large for the planner's LDS (160 KiB)"};
@@ -683,6 +693,18 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     tb.L = L;
     tb.max_nodes = max_nodes;
     return tb;
+}
+
+// The round's binary32 derivatives to the host: the planes, or the fp32
+// path's interleaved pairs.
+void download_derivatives(const mb::DevState &s, int64_t n, float *grad, float *hess) {
+    if (s.gh2) {
+        HIPX(hipMemcpy2D(grad, sizeof(float), s.gh2, 2 * sizeof(float), sizeof(float), n, hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy2D(hess, sizeof(float), s.gh2 + 1, 2 * sizeof(float), sizeof(float), n, hipMemcpyDeviceToHost));
+    } else {
+        HIPX(hipMemcpy(grad, s.grad, n * sizeof(float), hipMemcpyDeviceToHost));
+        HIPX(hipMemcpy(hess, s.hess, n * sizeof(float), hipMemcpyDeviceToHost));
+    }
 }
 
 // The leaf row representation of a training run (mbh_params.partition_mode):
@@ -1528,8 +1550,7 @@ int32_t mbh_objective_quantize(mbh_dataset *ds, const mbh_params *p, const doubl
         HIPX(mb::launch_objective(s, grid, nullptr));
         HIPX(mb::launch_quantize(s, grid, nullptr));
         HIPX(hipDeviceSynchronize());
-        HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
-        HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        download_derivatives(s, ds->n, grad, hess);
         // the pairs of tile 0 (every tile holds the same pair)
         std::vector<uint8_t> rec((size_t)ds->n * ds->rec);
         HIPX(hipMemcpy(rec.data(), ds->d_records, rec.size(), hipMemcpyDeviceToHost));
@@ -1577,8 +1598,7 @@ int32_t mbh_objective_quantize32(mbh_dataset *ds, const mbh_params *p, const dou
         HIPX(hipMemcpy(&h_error, s.error, sizeof(int32_t), hipMemcpyDeviceToHost));
         if (h_error & 4)
             throw Error{MOJOTREES_ERROR_TRAINING, "gradient/hessian magnitudes are out of range for the fixed-point histogram"};
-        HIPX(hipMemcpy(grad, s.grad, ds->n * sizeof(float), hipMemcpyDeviceToHost));
-        HIPX(hipMemcpy(hess, s.hess, ds->n * sizeof(float), hipMemcpyDeviceToHost));
+        download_derivatives(s, ds->n, grad, hess);
         scales[4] = 0.0;
         scales[5] = 0.0;
         if (s.hp.stage16) {
@@ -1780,8 +1800,10 @@ int32_t mbh_histogram_fp32(mbh_dataset *ds, const float *grad, const float *hess
         p.use_quantized_grad = 0;
         TrainBuffers tb = setup_state(ds, &p, run);
         mb::DevState &s = tb.s;
-        HIPX(hipMemcpy(s.grad, grad, ds->n * sizeof(float), hipMemcpyHostToDevice));
-        HIPX(hipMemcpy(s.hess, hess, ds->n * sizeof(float), hipMemcpyHostToDevice));
+        // the fp32 path reads the derivatives interleaved
+        HIPX(hipMemcpy2D(s.gh2, 2 * sizeof(float), grad, sizeof(float), sizeof(float), ds->n, hipMemcpyHostToDevice));
+        HIPX(hipMemcpy2D(s.gh2 + 1, 2 * sizeof(float), hess, sizeof(float), sizeof(float), ds->n,
+                         hipMemcpyHostToDevice));
         mb::Round r0 = mb::initial_round();
         r0.sampled = rows ? 1 : 0;  // root range = rows0[0 .. cursor[0])
         HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));

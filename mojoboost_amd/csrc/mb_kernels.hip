@@ -287,8 +287,12 @@ __global__ __launch_bounds__(256) void k_objective(DevState s) {
             g = (float)(w * (s.raw[r] - s.labels[r]));
             h = (float)(w * 1.0);
         }
-        s.grad[r] = g;
-        s.hess[r] = h;
+        if (s.gh2) {
+            ((float2 *)s.gh2)[r] = make_float2(g, h);
+        } else {
+            s.grad[r] = g;
+            s.hess[r] = h;
+        }
         float ag = fabsf(g), ah = fabsf(h);
         bool sel = !hp.bagging || in_bag(s, bstream, bfall, r);
         if (sel && isfinite(ag) && isfinite(ah)) {
@@ -678,7 +682,17 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
             }
         }
         if (gs_on) {
-            if (r < gst.bag_n) s.rows0[r] = s.goss_rows[r];
+            if (r < gst.bag_n) {
+                const int32_t rr = s.goss_rows[r];
+                s.rows0[r] = rr;
+                // interleaved binary32 derivatives: the row's GOSS weight bit
+                // goes into its hessian's sign bit (hessians are >= 0), which
+                // the fp32 accumulation reads with the pair
+                if (s.gh2 && s.goss_other[rr]) {
+                    uint32_t *hw = (uint32_t *)(s.gh2 + 2 * (size_t)rr + 1);
+                    *hw = *hw | 0x80000000u;
+                }
+            }
         } else if (!hp.bagging) {
             // every row in order: the root build and the root's partition
             // compute the ids, no list is written
@@ -795,7 +809,15 @@ __global__ void k_magfold(DevState s) {
 // A row's sampling importance: goss_importance's |g h| (goss.mojo:294-305)
 // of a single-output round, the class sum of a multiclass round (goss_imp).
 __device__ __forceinline__ unsigned long long goss_key(const DevState &s, int64_t r) {
-    const double imp = s.hp.num_class > 1 ? s.goss_imp[r] : fabs((double)s.grad[r] * (double)s.hess[r]);
+    double imp;
+    if (s.hp.num_class > 1) {
+        imp = s.goss_imp[r];
+    } else if (s.gh2) {
+        const float2 gh = ((const float2 *)s.gh2)[r];
+        imp = fabs((double)gh.x * (double)gh.y);
+    } else {
+        imp = fabs((double)s.grad[r] * (double)s.hess[r]);
+    }
     return (unsigned long long)__double_as_longlong(imp);  // non-negative: ordered like its bits
 }
 
@@ -1623,18 +1645,26 @@ struct FAcc {
     // depend on p alone and, with QAcc's lane rotation, a step's 64 adds
     // meet no bank conflict (feature-major cells lost a third of the LDS
     // cycles to conflicts); positions past the tile's features are skipped.
-    // The counts stay feature-major (f * ls + bin): bin-major they would not
-    // fit beside the sums in one workgroup's LDS.
+    // The counts of two neighbouring bins share a 32-bit cell (bin b in its
+    // half b & 1, 16 bits each), bin-pair-major at (b >> 1) * FS + p: a
+    // cell's bank is p plus 32 times one bit of the bin, so the 32 lanes of
+    // a half-wave, at 32 different positions, meet no conflict either
+    // (feature-major 32-bit counts, whose banks follow the random bins, cost
+    // 43 % of the accumulation's LDS cycles in conflicts), and the pairs
+    // fit beside the sums in one workgroup's LDS. A block adds at most
+    // kFAccChunk rows, so no half overflows.
+    static __host__ __device__ int count_rows(int ls) { return (ls + 1) / 2; }
     static __host__ __device__ size_t lds_bytes(int tf, int ls) {
-        return (size_t)2 * QAcc::row_cells_for(record_bytes_for(tf)) * ls * 8 + (size_t)tf * ls * 4;
+        const int FS = QAcc::row_cells_for(record_bytes_for(tf));
+        return (size_t)2 * FS * ls * 8 + (size_t)count_rows(ls) * FS * 4;
     }
     template <int LPR>
-    __device__ static void zero(unsigned char *lds, int F, int ls) {
+    __device__ static void zero(unsigned char *lds, int, int ls) {
         constexpr int FS = QAcc::row_cells_for(LPR * 16);
         double *g = (double *)lds;
         uint32_t *c = (uint32_t *)(g + 2 * (size_t)FS * ls);
         for (int i = threadIdx.x; i < 2 * FS * ls; i += blockDim.x) g[i] = 0.0;
-        for (int i = threadIdx.x; i < F * ls; i += blockDim.x) c[i] = 0u;
+        for (int i = threadIdx.x; i < count_rows(ls) * FS; i += blockDim.x) c[i] = 0u;
     }
     // gv, hv: the row's derivatives in binary64 with its GOSS weight applied
     // (accumulate_rows loads them with the record)
@@ -1654,7 +1684,7 @@ struct FAcc {
             if (p < F) {
                 atomicAdd(&g[bin * FS + p], gv);
                 atomicAdd(&h[bin * FS + p], hv);
-                atomicAdd(&c[p * ls + bin], 1u);
+                atomicAdd(&c[(bin >> 1) * FS + p], (bin & 1) ? 0x10000u : 1u);
             }
         }
     }
@@ -1672,7 +1702,7 @@ struct FAcc {
             const bool in = b < nb;
             s.fpart_g[base + i] = in ? g[b * FS + f] : 0.0;
             s.fpart_h[base + i] = in ? h[b * FS + f] : 0.0;
-            s.fpart_c[base + i] = in ? c[f * ls + b] : 0u;
+            s.fpart_c[base + i] = in ? (c[(b >> 1) * FS + f] >> (16 * (b & 1))) & 0xFFFFu : 0u;
         }
     }
 };
@@ -1822,10 +1852,12 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     uint32_t qw = 0u, qw_nxt = 0u;
     const bool q_goss = kQ && qc->gs_on;
     // fp32 cells (FAcc): each row's derivatives (binary32 bits, or binary64
-    // with grad64) and GOSS weight bit, loaded with the record a step ahead
+    // with grad64) and GOSS weight bit, loaded with the record a step ahead;
+    // binary32 derivatives come as one interleaved (g, h) pair whose h sign
+    // bit carries the GOSS weight bit (one gather per row, not three)
     constexpr bool kF = std::is_same<Acc, FAcc>::value;
     const bool f64 = kF && s.hp.grad64;
-    const bool f_goss = kF && goss_mult != 1.0 && s.goss_other != nullptr;
+    const bool f_goss = kF && goss_mult != 1.0 && (f64 ? s.goss_other != nullptr : true);
     unsigned long long fg[U], fh[U], fg_nxt[U], fh_nxt[U];
     uint32_t fw = 0u, fw_nxt = 0u;
     auto load_recs = [&](int64_t, const int32_t *id, uint4 *w, float *v, float *v2, uint32_t &wb,
@@ -1845,11 +1877,12 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                 if (f64) {
                     xg[u] = ((const unsigned long long *)s.grad64)[r];
                     xh[u] = ((const unsigned long long *)s.hess64)[r];
+                    if (f_goss) xw |= (s.goss_other[r] ? 1u : 0u) << u;
                 } else {
-                    xg[u] = ((const uint32_t *)s.grad)[r];
-                    xh[u] = ((const uint32_t *)s.hess)[r];
+                    const uint2 gh = ((const uint2 *)s.gh2)[r];
+                    xg[u] = gh.x;
+                    xh[u] = gh.y;  // sign bit: the GOSS weight bit
                 }
-                if (f_goss) xw |= (s.goss_other[r] ? 1u : 0u) << u;
             }
         }
     };
@@ -1908,8 +1941,10 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
                 // goss.apply_goss_scaling: the sampled small-gradient rows'
                 // g and h times the GOSS weight, in binary64
                 double gv = f64 ? __longlong_as_double((long long)xg[u]) : (double)__uint_as_float((uint32_t)xg[u]);
-                double hv = f64 ? __longlong_as_double((long long)xh[u]) : (double)__uint_as_float((uint32_t)xh[u]);
-                if ((xw >> u) & 1u) {
+                double hv = f64 ? __longlong_as_double((long long)xh[u])
+                                : (double)__uint_as_float((uint32_t)xh[u] & 0x7FFFFFFFu);
+                const bool wbit = f64 ? ((xw >> u) & 1u) != 0 : (f_goss && ((uint32_t)xh[u] >> 31) != 0);
+                if (wbit) {
                     gv *= goss_mult;
                     hv *= goss_mult;
                 }
@@ -4972,8 +5007,12 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
             g = (float)(w * (raw - y));
             h = (float)(w * 1.0);
         }
-        s.grad[r] = g;
-        s.hess[r] = h;
+        if (s.gh2) {
+            ((float2 *)s.gh2)[r] = make_float2(g, h);
+        } else {
+            s.grad[r] = g;
+            s.hess[r] = h;
+        }
         const float ag = fabsf(g), ah = fabsf(h);
         const bool sel = !hp.bagging || in_bag(s, bstream, bfall, r);
         if (sel && isfinite(ag) && isfinite(ah)) {

@@ -142,6 +142,9 @@ constexpr int kPartChunk = MB_PART_CHUNK;
 #endif
 constexpr int kPartChunkMin = MB_PART_CHUNK_MIN;
 constexpr int kPartChunkStep = 256;
+// Rows one fp32-path histogram block may add: its counts are 16-bit halves
+// of 32-bit LDS cells.
+constexpr int64_t kFAccChunk = 65535;
 // Threads of a record-partition block (leaves holding records); its tasks
 // take at most kPartRecChunk rows (kPartRows per thread).
 #ifndef MB_PART_REC_THREADS
@@ -275,7 +278,11 @@ struct DevState {
     // per round
     double *raw;           // n x num_class
     double *prob;          // n x num_class softmax of raw at the start of a round (multiclass)
-    float *grad, *hess;    // n
+    float *grad, *hess;    // n (not written when gh2 is set)
+    // the fp32 path's binary32 derivatives, (g, h) interleaved per row (one
+    // gather per accumulated row); h's sign bit is set when the round's GOSS
+    // sample took the row with the GOSS weight (hessians are >= 0)
+    float *gh2;            // 2n: g at 2r, h at 2r + 1
     double *grad64, *hess64;        // n, when hp.grad64
     unsigned long long *stats64;    // [2 parities][2]: max |g|, |h| as double bits, when hp.grad64
     // lambdarank: query q owns rows [qstart[q], qstart[q + 1])
