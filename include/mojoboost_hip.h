@@ -232,7 +232,8 @@ int64_t mbh_fit_launch_log(const mbh_fit *fit, double *out, int64_t n_out);
 /* Query groups of a resident dataset, for objective lambdarank: counts[q]
  * rows per query, in row order (LightGBM's `group`,
  * ranking.groups_from_counts, src/mojotrees/ranking.mojo:152-169); counts must
- * be positive and sum to n_rows, and a query holds at most 2048 rows. */
+ * be positive and sum to n_rows, and a query holds at most 2^30 rows
+ * (queries above 2048 rows are sorted in global memory rather than LDS). */
 int32_t mbh_dataset_set_groups(mbh_dataset *ds, const int32_t *counts, int64_t n_queries,
                                char *err, int32_t err_len);
 

@@ -563,9 +563,37 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
         s.inv_max_dcg = d_inv;
         s.qstart = ds->d_qstart;
         s.n_queries = (int32_t)nq;
+        // queries the LDS sort holds go to k_lambdarank; larger ones to
+        // k_lambdarank_big, which sorts in a global slot per block
+        int max_small = 1, max_big = 0;
+        std::vector<int32_t> big;
+        for (int64_t q = 0; q < nq; ++q) {
+            const int c = (int)(ds->qstart[q + 1] - ds->qstart[q]);
+            if (c > mb::kMaxQueryRows) {
+                big.push_back((int32_t)q);
+                max_big = std::max(max_big, c);
+            } else {
+                max_small = std::max(max_small, c);
+            }
+        }
         int pad = 1;
-        while (pad < ds->max_query) pad <<= 1;
+        while (pad < max_small) pad <<= 1;
         s.rank_pad = pad;
+        if (!big.empty()) {
+            int bp = 1;
+            while (bp < max_big) bp <<= 1;
+            const size_t slot_bytes = (size_t)bp * (3 * sizeof(double) + 2 * sizeof(int32_t));
+            int slots = (int)std::min<size_t>(big.size(), (size_t)ds->n_cu);
+            slots = (int)std::max<size_t>(1, std::min<size_t>(slots, ((size_t)4 << 30) / slot_bytes));
+            s.n_big = (int32_t)big.size();
+            s.rank_big_pad = bp;
+            s.rank_big_slots = slots;
+            s.rank_scratch = dalloc<double>((size_t)slots * 3 * bp, run.owned);
+            s.rank_scratch_i = dalloc<int32_t>((size_t)slots * 2 * bp, run.owned);
+            int32_t *d_big = dalloc<int32_t>(big.size(), run.owned);
+            HIPX(hipMemcpy(d_big, big.data(), big.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+            s.rank_big = d_big;
+        }
     }
     hp.quantized = p->use_quantized_grad ? 1 : 0;
     hp.wide = wide ? 1 : 0;
@@ -1366,8 +1394,8 @@ int32_t mbh_dataset_set_groups(mbh_dataset *ds, const int32_t *counts, int64_t n
             max_q = std::max(max_q, counts[q]);
         }
         if (st[nq] != ds->n) throw Error{MOJOTREES_ERROR_INVALID_ARGUMENT, "group counts must sum to n_rows"};
-        if (max_q > mb::kMaxQueryRows)
-            throw Error{MOJOTREES_ERROR_UNSUPPORTED, "a query holds more than 2048 rows (the device sorts a query in LDS)"};
+        if (max_q > (1 << 30))
+            throw Error{MOJOTREES_ERROR_UNSUPPORTED, "a query holds more than 2^30 rows"};
         int64_t *d = dalloc<int64_t>(nq + 1, ds->owned);
         HIPX(hipMemcpy(d, st.data(), st.size() * sizeof(int64_t), hipMemcpyHostToDevice));
         ds->qstart = std::move(st);

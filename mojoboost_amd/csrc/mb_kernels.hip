@@ -361,6 +361,7 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
     for (int q = blockIdx.x; q < s.n_queries; q += gridDim.x) {
         const int64_t a = s.qstart[q];
         const int cnt = (int)(s.qstart[q + 1] - a);
+        if (cnt > kMaxQueryRows) continue;  // k_lambdarank_big's (block-uniform)
         int p2 = 1;
         while (p2 < cnt) p2 <<= 1;
         for (int i = tid; i < p2; i += nt) {
@@ -488,6 +489,182 @@ __global__ __launch_bounds__(256) void k_lambdarank(DevState s) {
             mh = fmax(mh, red_h[i]);
         }
         // non-negative doubles order like their bit patterns
+        atomicMax(&s.stats64[rd.parity * 2 + 0], (unsigned long long)__double_as_longlong(mg));
+        atomicMax(&s.stats64[rd.parity * 2 + 1], (unsigned long long)__double_as_longlong(mh));
+    }
+}
+
+// Queries of more than kMaxQueryRows documents, which the LDS sort cannot
+// hold: one block per query at a time, with the query's sort keys,
+// positions, labels and running lambdas in the block's slot of global
+// memory. The same bitonic order and the same arithmetic as k_lambdarank;
+// each rank i's pairs are evaluated kRankChunk documents at a time, their
+// values staged in LDS, and the two sequential sums (the running |lambda|
+// and rank i's own lambda and hessian) walk each chunk in document order,
+// carried from chunk to chunk, so every sum keeps
+// ranking._fill_query_lambdas' order (src/mojotrees/ranking.mojo:504-654).
+constexpr int kRankChunk = 2048;
+__global__ __launch_bounds__(256) void k_lambdarank_big(DevState s) {
+    __shared__ double PL[kRankChunk], PH[kRankChunk];
+    __shared__ uint8_t V[kRankChunk];
+    __shared__ double s_factor;
+    __shared__ double red_g[4], red_h[4];
+    const Round rd = *s.round;
+    if (rd.stopped) return;
+    const HyperParams &hp = s.hp;
+    const size_t P = (size_t)s.rank_big_pad;
+    double *key = s.rank_scratch + (size_t)blockIdx.x * 3 * P;
+    double *G = key + P;
+    double *H = G + P;
+    int32_t *idx = s.rank_scratch_i + (size_t)blockIdx.x * 2 * P;
+    int32_t *lab = idx + P;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const double sigma = hp.rank_sigma;
+    const bool norm = hp.rank_norm != 0;
+    const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
+    const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
+    double mg = 0.0, mh = 0.0;
+    for (int bq = blockIdx.x; bq < s.n_big; bq += gridDim.x) {
+        const int q = s.rank_big[bq];
+        const int64_t a = s.qstart[q];
+        const int cnt = (int)(s.qstart[q + 1] - a);
+        int p2 = 1;
+        while (p2 < cnt) p2 <<= 1;
+        for (int i = tid; i < p2; i += nt) {
+            key[i] = i < cnt ? s.raw[a + i] : -INFINITY;
+            idx[i] = i;
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (int k = 2; k <= p2; k <<= 1)
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < p2; i += nt) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        const double ki = key[i], kl = key[l];
+                        const int ii = idx[i], il = idx[l];
+                        const bool l_first = rank_before(kl, il, ki, ii);
+                        if ((i & k) == 0 ? l_first : !l_first) {
+                            key[i] = kl;
+                            key[l] = ki;
+                            idx[i] = il;
+                            idx[l] = ii;
+                        }
+                    }
+                }
+                __threadfence_block();
+                __syncthreads();
+            }
+        for (int k = tid; k < cnt; k += nt) {
+            lab[k] = (int)s.labels[a + idx[k]];
+            G[k] = 0.0;
+            H[k] = 0.0;
+        }
+        __threadfence_block();
+        __syncthreads();
+        const double best = key[0], worst = key[cnt - 1];
+        const double inv = s.inv_max_dcg[q];
+        const int top = cnt - 1 < hp.rank_trunc ? cnt - 1 : hp.rank_trunc;
+        double sum = 0.0;         // thread 0's running sum of |lambda| (ranking.mojo:565)
+        double gi = 0.0, hi = 0.0;  // thread 64's rank-i lambda and hessian
+        for (int i = 0; i < top; ++i) {
+            const int li = lab[i];
+            const double si = key[i];
+            if (tid == 64) {
+                gi = G[i];
+                hi = H[i];
+            }
+            for (int c0 = i + 1; c0 < cnt; c0 += kRankChunk) {
+                const int c1 = c0 + kRankChunk < cnt ? c0 + kRankChunk : cnt;
+                for (int j = c0 + tid; j < c1; j += nt) {
+                    const int lj = lab[j];
+                    double pl = 0.0, ph = 0.0;
+                    uint8_t v = 0;
+                    if (li != lj) {
+                        const bool ih = li > lj;  // rank i holds the more relevant document
+                        const double kj = key[j];
+                        const int hr = ih ? i : j, lr = ih ? j : i;
+                        const double delta = ih ? si - kj : kj - si;
+                        const double gap = label_gain(ih ? li : lj) - label_gain(ih ? lj : li);
+                        const double paired = fabs(s.rank_disc[hr] - s.rank_disc[lr]);
+                        double dn = gap * paired * inv;
+                        if (norm && best != worst) dn /= 0.01 + fabs(delta);
+                        double p = pair_sigmoid(delta, sigma);
+                        double phh = p * (1.0 - p);
+                        p *= -sigma * dn;
+                        phh *= sigma * sigma * dn;
+                        pl = p;
+                        ph = phh;
+                        v = ih ? 3 : 1;
+                        G[j] = ih ? G[j] - p : G[j] + p;
+                        H[j] = H[j] + phh;
+                    }
+                    PL[j - c0] = pl;
+                    PH[j - c0] = ph;
+                    V[j - c0] = v;
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    for (int j = 0; j < c1 - c0; ++j)
+                        if (V[j]) sum -= 2.0 * PL[j];
+                } else if (tid == 64) {
+                    for (int j = 0; j < c1 - c0; ++j) {
+                        const uint8_t v = V[j];
+                        if (!v) continue;
+                        gi = (v & 2) ? gi + PL[j] : gi - PL[j];
+                        hi = hi + PH[j];
+                    }
+                }
+                __syncthreads();  // the staged chunk is rewritten next
+            }
+            if (tid == 64) {
+                G[i] = gi;
+                H[i] = hi;
+            }
+            __threadfence_block();
+            __syncthreads();
+        }
+        if (tid == 0) s_factor = (norm && sum > 0.0) ? ref_log2(1.0 + sum) / sum : 0.0;
+        __syncthreads();
+        const double factor = s_factor;
+        const bool sel = !hp.bagging || in_bag(s, bstream, bfall, a);
+        for (int k = tid; k < cnt; k += nt) {
+            double g = G[k], h = H[k];
+            if (factor != 0.0) {
+                g *= factor;
+                h *= factor;
+            }
+            const int64_t r = a + idx[k];
+            if (s.weights) {
+                g *= s.weights[r];
+                h *= s.weights[r];
+            }
+            s.grad64[r] = g;
+            s.hess64[r] = h;
+            if (sel && isfinite(g) && isfinite(h)) {
+                mg = fmax(mg, fabs(g));
+                mh = fmax(mh, fabs(h));
+            }
+        }
+        __threadfence_block();
+        __syncthreads();  // the slot is the next query's
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        mg = fmax(mg, __shfl_xor(mg, d, 64));
+        mh = fmax(mh, __shfl_xor(mh, d, 64));
+    }
+    const int w = tid >> 6;
+    if (lane_id() == 0) {
+        red_g[w] = mg;
+        red_h[w] = mh;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < (nt >> 6); ++i) {
+            mg = fmax(mg, red_g[i]);
+            mh = fmax(mh, red_h[i]);
+        }
         atomicMax(&s.stats64[rd.parity * 2 + 0], (unsigned long long)__double_as_longlong(mg));
         atomicMax(&s.stats64[rd.parity * 2 + 1], (unsigned long long)__double_as_longlong(mh));
     }
@@ -5242,6 +5419,11 @@ hipError_t launch_objective(const DevState &s, int grid, hipStream_t st) {
     if (s.hp.objective == kObjLambdarank) {
         const int g = s.n_queries < 4 * grid ? s.n_queries : 4 * grid;
         hipLaunchKernelGGL(k_lambdarank, dim3(g > 0 ? g : 1), dim3(256), rank_lds_bytes(s), st, s);
+        if (s.n_big > 0) {
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(k_lambdarank_big, dim3(s.rank_big_slots), dim3(256), 0, st, s);
+        }
     } else {
         hipLaunchKernelGGL(k_objective, dim3(grid), dim3(256), 0, st, s);
     }

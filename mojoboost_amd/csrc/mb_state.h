@@ -16,7 +16,7 @@ constexpr int kObjL2 = 0;
 constexpr int kObjBinary = 1;
 constexpr int kObjMulticlass = 2;
 constexpr int kObjLambdarank = 3;
-constexpr int kMaxQueryRows = 2048;  // the largest query the LDS sort takes
+constexpr int kMaxQueryRows = 2048;  // the largest query the LDS sort takes (larger: k_lambdarank_big)
 
 // Leaf-wise growth, batched. The reference grows a tree best-first: split the
 // frontier leaf of largest gain, score both children, repeat. A leaf's best
@@ -290,7 +290,17 @@ struct DevState {
     const double *inv_max_dcg;      // per query: 1 / maxDCG at the truncation level (0: none)
     const double *rank_disc;        // 1 / log2(rank + 2) for ranks below the largest query
     int32_t n_queries;
-    int32_t rank_pad;               // largest query rounded up to a power of two
+    int32_t rank_pad;               // largest query of at most kMaxQueryRows rows, rounded up to a power of two
+    // queries of more than kMaxQueryRows rows (k_lambdarank_big): their
+    // indices, and per block slot the query's keys, G, H (binary64) and
+    // positions, labels (int32), each rank_big_pad long
+    const int32_t *rank_big;
+    int32_t n_big;
+    int32_t rank_big_pad;
+    int32_t rank_big_slots;         // blocks of k_lambdarank_big (one slot each)
+    int32_t pad_big_;
+    double *rank_scratch;           // slots x 3 x rank_big_pad
+    int32_t *rank_scratch_i;        // slots x 2 x rank_big_pad
     uint32_t *stats;       // [2 parities][2][kStatSlots]: max |g|, max |h| as float bits, per slot
     // magnitude-sum lattice (hp.wide): each row's quantized (grad, hess)
     // interleaved, and the magnitude reduction's 256 + 256 binary32

@@ -574,6 +574,47 @@ def test_lambdarank_gradients_bit_exact(dev, trunc, norm):
     assert np.array_equal(bits(h), bits(wh))
 
 
+@pytest.mark.parametrize("trunc,norm", [(30, True), (5, False)])
+def test_lambdarank_large_queries_bit_exact(dev, trunc, norm):
+    """Queries above the LDS sort's 2048 documents (one of 10000) are sorted
+    and paired in global memory, their pair values staged in LDS chunks:
+    every gradient and hessian bit still equal to the oracle's, beside small
+    queries in the same launch."""
+    rng = np.random.default_rng(71 + trunc)
+    counts = np.array([10_000, 3, 2049, 4097, 700, 2048, 1, 2050], np.int32)
+    n = int(counts.sum())
+    y = rng.integers(0, 5, size=n).astype(np.float64)
+    y[5000:5100] = rng.integers(0, 31, size=100)
+    raw = np.round(rng.normal(size=n), 1)             # many ties
+    raw[9000:9500] = 0.0
+    bins = rng.integers(0, 8, size=(2, n), dtype=np.uint8)
+    ds = dev.Dataset(bins, n, 2, 8, y)
+    ds.set_groups(counts)
+    g, h = ds.lambdarank(raw, lambdarank_truncation_level=trunc, lambdarank_norm=int(norm))
+    wg, wh = O.lambdarank(raw, y, counts, truncation=trunc, sigma=1.0, norm=norm)
+    assert np.array_equal(bits(g), bits(wg))
+    assert np.array_equal(bits(h), bits(wh))
+
+
+def test_training_lambdarank_large_queries(dev):
+    """A quantized LambdaRank fit whose queries include three above 2048
+    documents: every tree and raw score bit-exact to the oracle."""
+    rng = np.random.default_rng(77)
+    counts = np.concatenate([[3000, 5000, 2500], rng.integers(1, 200, size=60)]).astype(np.int32)
+    n = int(counts.sum())
+    x = rng.normal(size=(10, n))
+    sc = x[0] - 0.5 * x[1] + 0.3 * x[2] * x[3] + 0.5 * rng.normal(size=n)
+    y = np.clip(np.floor((sc + 2.0)), 0, 4).astype(np.float64)
+    bins, _, _, mb = O.fit_transform(x.ravel(), n, 10, max_bins=63)
+    kw = dict(num_iterations=5, num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0, learning_rate=0.1)
+    ds = dev.Dataset(bins, n, 10, 64, y, missing_bin=mb)
+    ds.set_groups(counts)
+    fit = ds.train(objective=3, use_quantized_grad=1, **kw)
+    p, st = O.rank_params(counts, use_quantized_grad=1, **kw)
+    ref = O.train(bins, n, 10, 64, y, p, missing_bin=mb)
+    _compare_fit(fit, ref, n)
+
+
 @pytest.mark.parametrize("quantized", [1, 0])
 def test_training_lambdarank(dev, quantized):
     """A LambdaRank ensemble on the device against the oracle's restatement
