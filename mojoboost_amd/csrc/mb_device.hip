@@ -265,9 +265,6 @@ void check_params(const mbh_dataset *ds, const mbh_params *p) {
             unsup("n_rows * (num_grad_quant_bins + 1) must stay below 2^31 for int32 histogram cells");
     }
     if (p->goss) {
-        if (p->use_quantized_grad && p->quant_scale_rule == 1)
-            unsup("GOSS with the magnitude-sum lattice (quant_scale_rule=magnitude_sum) is not built on the "
-                  "device path; GOSS with quantized gradients takes the max-abs lattice");
         // GossParams.validate (goss.mojo:129-145), _check_goss (boosting.mojo:346-355)
         if (p->bagging_freq > 0 && p->bagging_fraction < 1.0) bad("goss and bagging cannot both be enabled");
         if (!(p->top_rate >= 0.0 && p->top_rate <= 1.0) || !(p->other_rate >= 0.0 && p->other_rate <= 1.0) ||

@@ -907,11 +907,26 @@ __global__ __launch_bounds__(kMagThreads) void k_magsum(DevState s) {
     const HyperParams &hp = s.hp;
     const uint64_t bstream = hp.bagging ? bag_stream_of(hp, rd.round) : 0;
     const int64_t bfall = hp.bagging ? bag_fallback_of(s, rd.round) : -1;
+    // a GOSS round's sample: its top rows (kappa INT_MIN) and the rows the
+    // sampling kept, whose derivatives carry the GOSS weight (applied in
+    // binary64, then narrowed as gradient_stats' caller narrows them)
+    const bool gs = goss_on(s);
+    const double gmult = gs ? goss_weight(*s.gst, s.n) : 1.0;
     const int t = threadIdx.x;
     float ag = 0.0f, ah = 0.0f;
     for (int64_t r = (int64_t)blockIdx.x * kMagThreads + t; r < s.n; r += (int64_t)kMagBlocks * kMagThreads) {
         if (hp.bagging && !in_bag(s, bstream, bfall, r)) continue;
-        const float g = fabsf(s.grad[r]), h = fabsf(s.hess[r]);
+        float g = s.grad[r], h = s.hess[r];
+        if (gs) {
+            const bool other = s.goss_other[r] != 0;
+            if (!other && s.goss_kappa[r] != INT_MIN) continue;  // not sampled
+            if (other) {
+                g = (float)((double)g * gmult);
+                h = (float)((double)h * gmult);
+            }
+        }
+        g = fabsf(g);
+        h = fabsf(h);
         if (!(isfinite(g) && isfinite(h))) continue;
         ag += g;
         ah += h;

@@ -78,9 +78,36 @@ def test_multiclass_goss(dev, quantized):
         assert _tree_agreement(fit, ref) >= ref.n_trees - 1
 
 
-def test_goss_with_magnitude_sum_lattice_is_refused(dev):
-    n = 5_000
-    bins, y, mb, nb = c2_like(n, f=4, seed=47)
-    ds = dev.Dataset(bins, n, 4, nb, y, missing_bin=mb)
-    with pytest.raises(Exception, match="magnitude"):
-        ds.train(objective=1, num_iterations=2, num_leaves=7, quant_scale_rule=1, **GOSS)
+@pytest.mark.parametrize("objective,staging", [(1, 0), (0, 0), (1, 1)])
+def test_goss_on_the_magnitude_sum_lattice(dev, objective, staging):
+    """GOSS with the reference's magnitude-sum lattice (quant_scale_rule=1,
+    the 2^30 power-of-two scales): the magnitude sums cover the round's
+    sample with the GOSS weight applied to the kept small-gradient rows, the
+    quantizer sees the weighted derivatives; int32 and int16 staging.
+    Every tree and raw score bit-exact to the oracle. The int16 arm needs
+    rows enough for every weighted row's value to fit 16 bits at the
+    sample's scale (it refuses the fit otherwise): 1.5M rows there."""
+    n = 1_500_000 if staging else 60_000
+    bins, y, mb, nb = c2_like(n, f=8, seed=48 + objective)
+    if objective == 0:
+        y = y * 2.0 - 0.5 + 0.1 * np.random.default_rng(2).normal(size=n)
+    kw = dict(objective=objective, num_iterations=8, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.25)
+    fit = dev.Dataset(bins, n, 8, nb, y, missing_bin=mb).train(quant_scale_rule=1, quant_staging=staging,
+                                                               **GOSS, **kw)
+    ref = O.train(bins, n, 8, nb, y, O.default_params(**kw, **GOSS, use_quantized_grad=1, quant_scale_rule=1),
+                  missing_bin=mb)
+    assert ref.n_trees == 8 and ref.tree(5)["count"][0] < n  # rounds past the warmup sampled
+    _compare_fit(fit, ref, n)
+
+
+def test_multiclass_goss_on_the_magnitude_sum_lattice(dev):
+    n, K = 60_000, 3
+    bins, y, mb, nb, f = c5_like(n, K, seed=49)
+    kw = dict(objective=2, num_class=K, num_iterations=5, num_leaves=15, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.5)
+    fit = dev.Dataset(bins, n, f, nb, y, missing_bin=mb).train(quant_scale_rule=1, **GOSS, **kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, **GOSS, use_quantized_grad=1, quant_scale_rule=1),
+                  missing_bin=mb)
+    assert ref.n_trees == fit.n_trees == 5 * K
+    _compare_fit(fit, ref, n)
