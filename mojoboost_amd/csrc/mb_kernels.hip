@@ -1880,6 +1880,11 @@ struct FAcc {
             }
         }
     }
+    // every cell of the block's histogram as its partial (feature-major), as
+    // QAcc::store: a lane takes four bins of one position, so the lanes of
+    // a wave read 32 consecutive positions of a bin row (conflict-free; a
+    // lane per bin of one feature read cells FS apart, all on one bank), and
+    // writes them as contiguous runs.
     template <int LPR>
     __device__ static void store(const DevState &s, const unsigned char *lds, int blk, int f0, int Ft) {
         constexpr int FS = QAcc::row_cells_for(LPR * 16);
@@ -1888,13 +1893,30 @@ struct FAcc {
         const double *h = g + (size_t)FS * ls;
         const uint32_t *c = (const uint32_t *)(h + (size_t)FS * ls);
         const size_t base = ((size_t)blk * F + f0) * ps;
-        for (int i = threadIdx.x; i < Ft * ps; i += blockDim.x) {
-            const int f = i / ps;
-            const int b = i - f * ps;
-            const bool in = b < nb;
-            s.fpart_g[base + i] = in ? g[b * FS + f] : 0.0;
-            s.fpart_h[base + i] = in ? h[b * FS + f] : 0.0;
-            s.fpart_c[base + i] = in ? (c[(b >> 1) * FS + f] >> (16 * (b & 1))) & 0xFFFFu : 0u;
+        const int nq = (ps + 3) >> 2;
+        for (int u = threadIdx.x; u < FS * nq; u += blockDim.x) {
+            const int q = u / FS;
+            const int f = u - q * FS;
+            if (f >= Ft) continue;
+            const int b = 4 * q;
+            double vg[4], vh[4];
+            uint32_t vc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool in = b + i < nb;
+                vg[i] = in ? g[(b + i) * FS + f] : 0.0;
+                vh[i] = in ? h[(b + i) * FS + f] : 0.0;
+                vc[i] = in ? (c[((b + i) >> 1) * FS + f] >> (16 * ((b + i) & 1))) & 0xFFFFu : 0u;
+            }
+            const size_t o = base + (size_t)f * ps + b;  // ps is even: 16-byte aligned pairs
+            *(double2 *)(s.fpart_g + o) = make_double2(vg[0], vg[1]);
+            *(double2 *)(s.fpart_h + o) = make_double2(vh[0], vh[1]);
+            *(uint2 *)(s.fpart_c + o) = make_uint2(vc[0], vc[1]);
+            if (b + 2 < ps) {
+                *(double2 *)(s.fpart_g + o + 2) = make_double2(vg[2], vg[3]);
+                *(double2 *)(s.fpart_h + o + 2) = make_double2(vh[2], vh[3]);
+                *(uint2 *)(s.fpart_c + o + 2) = make_uint2(vc[2], vc[3]);
+            }
         }
     }
 };
