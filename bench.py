@@ -488,8 +488,10 @@ def main():
                 fh.write("\n")
                 fh.write(size_table_md("k_partition by rows partitioned per launch",
                                        size_classes(launch_log, 2, 4, part_row_bytes)))
-        note = (f"dominant histogram kernel k_accum (smaller-child accumulation from the "
-                f"partitioned row list) over the instrumented {stat_steps}-step training, "
+        how = ("streamed from the leaf's records" if args.partition_mode == 1
+               else "gathered through the partitioned row list")
+        note = (f"dominant histogram kernel k_accum (smaller-child accumulation, {how}) "
+                f"over the instrumented {stat_steps}-step training, "
                 f"algorithmic bytes per launch = accumulated rows * (F + {GH}) "
                 f"({st['accum_bytes'] / launches / 1e6:.2f} MB), over its average kernel duration "
                 f"({kernel_avg_ms * 1e3:.1f} us, {int(st['expand_launches'])} launches incl. empty "
@@ -527,7 +529,8 @@ def main():
         "root_hist_stored_pairs_merged_ms": round(root_merged_ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_per_launch(args.workload), "note": note},
+                     "traffic": traffic_per_launch(args.workload + ("rec" if args.partition_mode == 1 else "")),
+                     "note": note},
         "cpu_baseline": cpu,
         "parity_first_trees_bit_exact": parity,
         "binning": binning,
