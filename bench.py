@@ -30,6 +30,11 @@ counters. The conservative figure that charges every growth kernel
 (partition, accumulation, partial merge and scan, planning) against the
 committed trees' builds only is reported as `hist_gbs_committed_over_growth`.
 
+records_layout: the same full training with leaves holding their rows as
+whole records (partition_mode=1: the partition moves records, the histogram
+streams them) instead of row ids (the default, which gathers each record by
+id), timed and instrumented the same way, its trees checked identical.
+
 cpu_baseline: the CPU oracle (a C++ restatement of the reference's CPU
 trainer; the reference itself is Mojo and cannot run here) on the first
 --cpu-trees trees of the same workload on all rows (a bounded sample of
@@ -164,14 +169,24 @@ def workload_data(name, n_rows):
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo), or None."""
+    """The host CPU's model name with its family / model / stepping numbers
+    and clock (/proc/cpuinfo; a virtualized host may report only the
+    vendor's product line as the name), or None."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (t.strip() for t in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping", "cpu MHz") and k not in fields:
+                    fields[k] = v
+            elif fields:
+                break
     except OSError:
-        pass
-    return None
+        return None
+    if "model name" not in fields:
+        return None
+    extra = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping", "cpu MHz") if k in fields)
+    return f"{fields['model name']} ({extra})" if extra else fields["model name"]
 
 
 def host_cores():
@@ -391,6 +406,30 @@ def main():
             ifit.value.view(np.uint64), full_fit.value.view(np.uint64))
         print(f"[bench] instrumented full run done (trees identical to the timed run: {same})",
               file=sys.stderr, flush=True)
+    # the other leaf-row layout, measured the same way (full training, then
+    # its instrumented run): leaves holding their rows as whole records
+    # (partition_mode=1) stream the histogram, row ids (the default) gather it
+    alt = None
+    if not args.no_instrumented and not args.partition_mode and wl["params"].get("use_quantized_grad") \
+            and F + GH <= 64:
+        akw = dict(kw, partition_mode=1)
+        t3 = time.perf_counter()
+        afit = ds.train(num_iterations=full, **akw)
+        alt_wall = time.perf_counter() - t3
+        ast = ds.train(num_iterations=full, time_histograms=1, **akw).stats
+        same_alt = np.array_equal(afit.threshold, full_fit.threshold) and np.array_equal(
+            afit.value.view(np.uint64), full_fit.value.view(np.uint64))
+        alt = {"partition_mode": 1, "leaf_rows": "records",
+               f"train_sec_per_{full}_{'rounds' if K > 1 else 'trees'}": round(alt_wall, 3),
+               "value": round((ast["root_bytes"] + ast["accum_bytes"]) / ((ast["root_ms"] + ast["accum_ms"]) * 1e-3)
+                              / 1e9, 2),
+               "accum_gbs": round(ast["accum_bytes"] / (ast["accum_ms"] * 1e-3) / 1e9, 1),
+               "accum_kernel_avg_ms": round(ast["accum_ms"] / max(1.0, ast["expand_launches"]), 5),
+               "partition_ms_per_tree": round(ast["partition_ms"] / full, 4),
+               "traffic": traffic_per_launch(args.workload + "rec"),
+               "trees_identical_to_row_ids": bool(same_alt)}
+        print(f"[bench] records layout: {full} steps in {alt_wall:.3f}s (trees identical: {same_alt})",
+              file=sys.stderr, flush=True)
     root_mean_ms, root_min_ms, root_merged_ms = ds.bench_root_histogram(reps=20)
 
     # CPU baseline on the same bins: the first --cpu-trees trees of the workload.
@@ -532,6 +571,7 @@ def main():
                      "traffic": traffic_per_launch(args.workload + ("rec" if args.partition_mode == 1 else "")),
                      "note": note},
         "cpu_baseline": cpu,
+        "records_layout": alt,
         "parity_first_trees_bit_exact": parity,
         "binning": binning,
     }
