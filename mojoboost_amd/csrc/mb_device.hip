@@ -486,6 +486,8 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     s.slot_fid = dalloc<int32_t>(L, run.owned);
     s.scan = dalloc<mb::ScanResult>((size_t)s.kmax * 2 * F, run.owned);
     s.scan_gain = dalloc<double>((size_t)s.kmax * 2 * F, run.owned);
+    s.pair_gain = dalloc<double>((size_t)s.kmax * 2, run.owned);
+    s.pair_feat = dalloc<int32_t>((size_t)s.kmax * 2, run.owned);
     s.e_gain = dalloc<double>(s.e_cap, run.owned);
     s.e_left = dalloc<int32_t>(s.e_cap, run.owned);
     s.e_rows = dalloc<int32_t>(s.e_cap, run.owned);

@@ -3887,6 +3887,59 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
     }
 }
 
+// ------------------------------------------------------------- pair fold
+// With more than 64 features the planner cannot take a pair's per-feature
+// gains in one wave load: one block per (child) pair folds them here, after
+// the scan -- the feature of largest gain (gain > 0, lowest feature on equal
+// gains, as the planner's own fold) -- so the planner's single block reads
+// one (gain, feature) per pair instead of F gains (C4: 2000 features x 64
+// pairs, a megabyte through one CU).
+constexpr int kFoldThreads = 256;
+__global__ __launch_bounds__(kFoldThreads) void k_fold(DevState s, int root_mode) {
+    __shared__ double wg[kFoldThreads / 64];
+    __shared__ int wf[kFoldThreads / 64];
+    const int n_pairs = root_mode ? 1 : 2 * s.batch->n_items;
+    const int pr = blockIdx.x;
+    if (pr >= n_pairs) return;
+    const int F = s.n_features, tid = threadIdx.x, lane = lane_id(), wv = tid >> 6;
+    const double *q = s.scan_gain + (size_t)pr * F;
+    double bg = 0.0;
+    int bf = 0x7FFFFFFF;
+    // eight loads in flight per thread, ascending features per thread (strict
+    // '>' keeps the lowest of equal gains)
+    for (int f0 = tid; f0 < F; f0 += 8 * kFoldThreads) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int f = f0 + u * kFoldThreads;
+            v[u] = f < F ? q[f] : -1.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int f = f0 + u * kFoldThreads;
+            if (v[u] > 0.0 && v[u] > bg) {
+                bg = v[u];
+                bf = f;
+            }
+        }
+    }
+    wave_argmax_lex(bg, bf);
+    if (lane == 0) {
+        wg[wv] = bg;
+        wf[wv] = bf;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kFoldThreads / 64; ++w)
+            if (wg[w] > bg || (wg[w] == bg && wf[w] < bf)) {
+                bg = wg[w];
+                bf = wf[w];
+            }
+        s.pair_gain[pr] = bf != 0x7FFFFFFF ? bg : 0.0;
+        s.pair_feat[pr] = bf;
+    }
+}
+
 // ------------------------------------------------------------------ planner
 // Single block of kPlanThreads, after every scan launch.
 //
@@ -4225,8 +4278,10 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // counts are allocated, read and never used).
     constexpr int kPW = 8;  // fold: pairs per wave (16 waves x 8 >= 2 x 64)
     static_assert(kPlanThreads / 64 * kPW >= 2 * 64, "every pair of a batch in one pass");
-    const bool pre = s.e_cap <= kPlanThreads && L <= kPlanThreads && F <= 64;  // launch-uniform
-    double p_eg = 0.0, gq[kPW];
+    const bool pre = s.e_cap <= kPlanThreads && L <= kPlanThreads;  // launch-uniform
+    const bool folded = F > 64;  // k_fold left one (gain, feature) per pair
+    double p_eg = 0.0, gq[kPW], p_pg = 0.0;
+    int p_pf = 0x7FFFFFFF;
     int p_el = 0, p_ep = 0, p_rw = 0, p_se = 0, p_sf = 0, p_mb = 0;
     static_assert(sizeof(Item) == 64, "an item is four 16-byte words");
     uint4 p_i0 = make_uint4(0, 0, 0, 0), p_i1 = p_i0, p_i2 = p_i0, p_i3 = p_i0;
@@ -4249,11 +4304,16 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             p_i2 = q[2];
             p_i3 = q[3];
         }
+        if (!folded) {
 #pragma unroll
-        for (int k = 0; k < kPW; ++k) {
-            int pr = wv + k * nwaves;
-            pr = pr < 2 * s.kmax ? pr : 0;
-            gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+            for (int k = 0; k < kPW; ++k) {
+                int pr = wv + k * nwaves;
+                pr = pr < 2 * s.kmax ? pr : 0;
+                gq[k] = s.scan_gain[(size_t)pr * F + (lane < F ? lane : 0)];
+            }
+        } else if (tid < 2 * s.kmax) {
+            p_pg = s.pair_gain[tid];
+            p_pf = s.pair_feat[tid];
         }
     }
     // the batch size, the round and the growth counters in one memory round
@@ -4312,6 +4372,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
     // unconditional (a branch between dependent loads would cost a memory
     // round trip each): when F <= 64 wave w takes pairs w + 16 k, k < kPW,
     // lane = feature; the argmax keeps the lowest feature on equal gains.
+    // With more features k_fold has already folded each pair (same rule),
+    // and thread p reads pair p's (gain, feature).
     if (pre) {
         if (!root_mode && tid < n_items) {
             uint4 *q = (uint4 *)&v.it[tid];
@@ -4321,6 +4383,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             q[3] = p_i3;
         }
         if (tid < F) v.mbin[tid] = p_mb;
+        for (int f = tid + nthr; f < F; f += nthr) v.mbin[f] = s.missing_bin[f];  // F > kPlanThreads
         if (tid < ne) {
             v.eg[tid] = p_eg;
             v.el[tid] = p_el;
@@ -4332,7 +4395,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             v.sl_fid[tid] = p_sf;
         }
     } else {
-        if (F <= 64) {
+        if (folded) {
+            if (tid < n_pairs) {
+                p_pg = s.pair_gain[tid];
+                p_pf = s.pair_feat[tid];
+            }
+        } else {
 #pragma unroll
             for (int k = 0; k < kPW; ++k) {
                 int pr = wv + k * nwaves;
@@ -4370,7 +4438,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
         }
         if (lane == 0) s_vf = vf;
     }
-    if (F <= 64) {
+    if (folded) {
+        if (tid < n_pairs) {
+            v.wg[tid] = p_pg;
+            v.wf[tid] = p_pf;
+        }
+    } else {  // F <= 64
 #pragma unroll
         for (int k = 0; k < kPW; ++k) {
             const int pr = wv + k * nwaves;
@@ -4378,23 +4451,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_plan(DevState s, int root_mode
             const bool ok = lane < F && gq[k] > 0.0;
             double bg = ok ? gq[k] : 0.0;
             int bf = ok ? lane : 0x7FFFFFFF;
-            wave_argmax_lex(bg, bf);
-            if (lane == 0) {
-                v.wg[pr] = bg;
-                v.wf[pr] = bf;
-            }
-        }
-    } else {
-        for (int pr = wv; pr < n_pairs; pr += nwaves) {
-            double bg = 0.0;
-            int bf = 0x7FFFFFFF;
-            for (int ff = lane; ff < F; ff += 64) {
-                const double q = s.scan_gain[(size_t)pr * F + ff];
-                if (q > bg) {
-                    bg = q;
-                    bf = ff;
-                }
-            }
             wave_argmax_lex(bg, bf);
             if (lane == 0) {
                 v.wg[pr] = bg;
@@ -5662,12 +5718,18 @@ hipError_t launch_accum(const DevState &s, hipStream_t st, hipEvent_t ev0, hipEv
            : s.hp.quantized ? launch_accum_t<QAcc>(s, st, ev0, ev1)
                             : launch_accum_t<FAcc>(s, st, ev0, ev1);
 }
+hipError_t launch_fold(const DevState &s, int root_mode, hipStream_t st) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || s.n_features <= 64) return e;
+    hipLaunchKernelGGL(k_fold, dim3(root_mode ? 1 : 2 * s.kmax), dim3(kFoldThreads), 0, st, s, root_mode);
+    return hipGetLastError();
+}
 hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
     if (s.hp.quantized && !s.ncat && s.n_bins <= 64) {
         const int groups = (s.n_features + kNarrowFeat - 1) / kNarrowFeat;
         const int grid = root_mode ? groups : std::min(s.scan_grid, s.kmax * groups);
         hipLaunchKernelGGL(k_scan_narrow, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
-        return hipGetLastError();
+        return launch_fold(s, root_mode, st);
     }
     const int grid = root_mode ? s.n_features : s.scan_grid;
     if (s.hp.quantized && s.ncat)
@@ -5678,7 +5740,7 @@ hipError_t launch_scan(const DevState &s, int root_mode, hipStream_t st) {
         hipLaunchKernelGGL(k_scan_f<true>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
     else
         hipLaunchKernelGGL(k_scan_f<false>, dim3(grid), dim3(kScanThreads), 0, st, s, root_mode);
-    return hipGetLastError();
+    return launch_fold(s, root_mode, st);
 }
 hipError_t launch_plan(const DevState &s, int root_mode, hipStream_t st, Batch *host) {
     hipLaunchKernelGGL(k_plan, dim3(1), dim3(kPlanThreads), plan_lds_bytes(s), st, s, root_mode, host);

@@ -355,6 +355,10 @@ struct DevState {
     int32_t *slot_fid;     // num_leaves: its node id in the committed tree
     ScanResult *scan;      // kmax x 2 x F
     double *scan_gain;     // kmax x 2 x F: a result's gain when found, else -1 (all the planner's fold reads)
+    // more than 64 features: each pair's best gain (0: none) and its feature
+    // (0x7FFFFFFF: none), folded by k_fold for the planner
+    double *pair_gain;     // 2 x kmax
+    int32_t *pair_feat;    // 2 x kmax
     unsigned long long *scan_cat;  // kmax x 2 x F x 4: a categorical result's left set
     unsigned long long *e_cat;     // e_cap x 4: an explored node's categorical left set
     int64_t *cursor;       // [0] root bag size; [2 + 2j], [3 + 2j]: item j's output cursors
