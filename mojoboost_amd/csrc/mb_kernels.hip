@@ -4083,10 +4083,20 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x)
 // lane's row of 16); a swizzle within 32 lanes for 16; a crossbar shuffle
 // for 32; through LDS for 64 and more, alternating between two buffers so
 // that each such step takes one barrier (a buffer is rewritten two steps
-// later, after every thread has passed the barrier between).
+// later, after every thread has passed the barrier between). Only the waves
+// that hold the 2^LOGN positions compare and exchange (a position's partners
+// are all below 2^LOGN); the others take the LDS steps' barriers and nothing
+// else, so they leave the SIMDs to the sorting waves.
 template <int LOGN>
 __device__ __forceinline__ unsigned bitonic_desc(unsigned x, unsigned (*keys)[kPlanThreads]) {
     const int tid = threadIdx.x, lane = lane_id();
+    constexpr int kWaves = (1 << LOGN) > 64 ? (1 << LOGN) / 64 : 1;
+    if ((tid >> 6) >= kWaves) {  // wave-uniform
+        constexpr int kLdsSteps = LOGN > 6 ? (LOGN - 6) * (LOGN - 5) / 2 : 0;  // steps with j >= 64
+#pragma unroll
+        for (int i = 0; i < kLdsSteps; ++i) __syncthreads();
+        return x;
+    }
     int buf = 1;
 #pragma unroll
     for (int lk = 1; lk <= LOGN; ++lk) {
