@@ -969,6 +969,9 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         const int grid_rows = 8 * ds->n_cu;
         HIPX(mb::launch_fill_f64(s.raw, ds->n, K, d_base, grid_rows, nullptr));
         HIPX(mb::prepare_kernels(s));
+        const int grid_score = mb::rows_grid(s, mb::kRowsScore, ds->n_cu);
+        const int grid_score_obj = mb::rows_grid(s, mb::kRowsScoreObjective, ds->n_cu);
+        const int grid_softmax = mb::rows_grid(s, mb::kRowsSoftmax, ds->n_cu);
         HIPX(hipDeviceSynchronize());
         const int L = tb.L;
         const int T = p->num_iterations * K;
@@ -1030,7 +1033,7 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             // single output, once per round from the softmax probabilities
             // for multiclass (every class tree of the round on that sample)
             if (K > 1 && t % K == 0) {
-                HIPX(mb::launch_softmax(s, grid_rows, st));
+                HIPX(mb::launch_softmax(s, grid_softmax, st));
                 if (s.hp.goss) HIPX(mb::launch_goss(s, grid_rows, st));
             }
             if (!(fuse_objective && t > 0)) HIPX(mb::launch_objective(s, grid_rows, st));
@@ -1102,8 +1105,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
                 t_root += a;
                 t_root_scan += b;
             }
-            if (fuse_objective && t + 1 < T) HIPX(mb::launch_score_objective(s, grid_rows, st));
-            else HIPX(mb::launch_score(s, grid_rows, st));
+            if (fuse_objective && t + 1 < T) HIPX(mb::launch_score_objective(s, grid_score_obj, st));
+            else HIPX(mb::launch_score(s, grid_score, st));
             HIPX(mb::launch_round_end(s, st));
         }
         HIPX(hipStreamSynchronize(st));

@@ -46,6 +46,12 @@ hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
 // and binary): after it, the next tree skips launch_objective.
 hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_round_end(const DevState &s, hipStream_t st);
+// Grid of a grid-stride rows kernel: as many blocks per CU as its registers
+// and LDS let stay resident (at most 8), times n_cu, so that every block runs
+// from the start instead of a partial second round of blocks following the
+// first.
+enum RowsKernel { kRowsScore = 0, kRowsScoreObjective = 1, kRowsSoftmax = 2 };
+int rows_grid(const DevState &s, RowsKernel k, int n_cu);
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
                                 int tile_f, int n_tiles, int grid, hipStream_t st);
 hipError_t launch_fill_f64(double *p, int64_t n, int K, const double *base, int grid, hipStream_t st);

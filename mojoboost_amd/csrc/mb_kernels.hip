@@ -5767,6 +5767,17 @@ hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st) {
         hipLaunchKernelGGL(k_score_objective<false>, dim3(grid), dim3(256), score_lds_bytes(s), st, s);
     return hipGetLastError();
 }
+int rows_grid(const DevState &s, RowsKernel k, int n_cu) {
+    const void *fn = k == kRowsScore            ? (const void *)k_score
+                     : k == kRowsSoftmax        ? (const void *)k_softmax
+                     : s.labels8 != nullptr     ? (const void *)k_score_objective<true>
+                                                : (const void *)k_score_objective<false>;
+    const size_t lds = k == kRowsSoftmax ? 0 : score_lds_bytes(s);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) per_cu = 8;
+    per_cu = per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu;
+    return per_cu * (n_cu < 1 ? 1 : n_cu);
+}
 hipError_t launch_round_end(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_round_end, dim3(1), dim3(256), 0, st, s);
     return hipGetLastError();
