@@ -5103,13 +5103,27 @@ struct PackedTree {
 
 // tree.goes_left for a packed node: bit 50 marks a categorical node, routed
 // by its set (bin 0, missing or unseen, is in no set); otherwise the missing
-// bin follows default_left and bin <= threshold goes left.
+// bin follows default_left and bin <= threshold goes left. kCat: the tree may
+// hold categorical nodes (a dataset with categorical features); without them
+// the rule is selects only, no branch that splits the wave.
+template <bool kCat>
 __device__ __forceinline__ bool packed_goes_left(const PackedTree &t, unsigned long long w, int node, int b) {
-    if ((w >> 50) & 1ULL) return (t.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1ULL;
+    if (kCat && ((w >> 50) & 1ULL)) return (t.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1ULL;
     const int thr = (int)((w >> 16) & 255ULL);
     const int mbin = (int)((w >> 24) & 511ULL) - 1;
     const bool dl = (w >> 33) & 1ULL;
     return (b == mbin) ? dl : (b <= thr);
+}
+// The numerical rule in integer arithmetic, 1 when bin b goes left:
+// le ^ (miss & (le ^ dl)) is dl for the missing bin and le otherwise (no
+// boolean select for the compiler to turn into a branch).
+__device__ __forceinline__ unsigned packed_left_bit(unsigned long long w, int b) {
+    const unsigned thr = (unsigned)(w >> 16) & 255u;
+    const unsigned mbin = ((unsigned)(w >> 24) & 511u) - 1u;  // 0xFFFFFFFF: no missing bin
+    const unsigned dl = (unsigned)(w >> 33) & 1u;
+    const unsigned le = (unsigned)b <= thr ? 1u : 0u;
+    const unsigned miss = (unsigned)b == mbin ? 1u : 0u;
+    return le ^ (miss & (le ^ dl));
 }
 
 __device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsigned char *smem) {
@@ -5142,8 +5156,21 @@ __device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsign
 // follows default_left, otherwise bin <= threshold goes left
 // (tree.goes_left, src/mojotrees/tree.mojo:483-505). Children always have
 // larger ids than their parent, so a walk ends within n_nodes steps.
-template <class BinOf>
+template <bool kCat, class BinOf>
 __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, BinOf bin) {
+    if (!kCat) {
+        // no branch inside the step (a lane leaves the loop at its leaf)
+        int node = 0;
+        unsigned long long w = t.node[0];
+        for (int d = 0; d < n_nodes; ++d) {
+            const int f = (int)(w & 0xFFFFULL);
+            if (f == 0xFFFF) break;
+            const int c = (int)((w >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(w, bin(f));
+            node = (unsigned)c < (unsigned)n_nodes ? c : 0;
+            w = t.node[node];
+        }
+        return node;
+    }
     int node = 0;
     for (int d = 0; d < n_nodes; ++d) {
         const unsigned long long w = t.node[node];
@@ -5151,7 +5178,7 @@ __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, Bin
         if (f == 0xFFFF) break;
         const int b = bin(f);
         const int left = (int)((w >> 34) & 0xFFFFULL);
-        node = packed_goes_left(t, w, node, b) ? left : left + 1;
+        node = packed_goes_left<kCat>(t, w, node, b) ? left : left + 1;
         if ((unsigned)node >= (unsigned)n_nodes) node = 0;
     }
     return node;
@@ -5159,9 +5186,30 @@ __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, Bin
 
 // Two independent walks advanced together, so each level's LDS round trips
 // of one row overlap the other's.
-template <class BinA, class BinB>
+template <bool kCat, class BinA, class BinB>
 __device__ __forceinline__ void walk_packed2(const PackedTree &t, int n_nodes, BinA bin_a, BinB bin_b, int &na,
                                              int &nb) {
+    if (!kCat) {
+        // both rows step until both reach their leaves; a row at its leaf
+        // keeps it and reads feature 0 (selects, no branch inside the step)
+        int a = 0, b = 0;
+        unsigned long long wa = t.node[0], wb = wa;
+        for (int d = 0; d < n_nodes; ++d) {
+            const int fa = (int)(wa & 0xFFFFULL), fb = (int)(wb & 0xFFFFULL);
+            const bool la = fa == 0xFFFF, lb = fb == 0xFFFF;
+            if (la && lb) break;
+            const int ba = bin_a(la ? 0 : fa), bb = bin_b(lb ? 0 : fb);
+            const int ca = (int)((wa >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(wa, ba);
+            const int cb = (int)((wb >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(wb, bb);
+            a = la ? a : ((unsigned)ca < (unsigned)n_nodes ? ca : 0);
+            b = lb ? b : ((unsigned)cb < (unsigned)n_nodes ? cb : 0);
+            wa = t.node[a];
+            wb = t.node[b];
+        }
+        na = a;
+        nb = b;
+        return;
+    }
     int a = 0, b = 0;
     bool da = false, db = false;
     for (int d = 0; d < n_nodes && !(da && db); ++d) {
@@ -5172,11 +5220,12 @@ __device__ __forceinline__ void walk_packed2(const PackedTree &t, int n_nodes, B
         const int ba = da ? 0 : bin_a(fa), bb = db ? 0 : bin_b(fb);
         auto next = [&t](unsigned long long w, int bin, int node, int n) {
             const int left = (int)((w >> 34) & 0xFFFFULL);
-            const int c = packed_goes_left(t, w, node, bin) ? left : left + 1;
+            const int c = packed_goes_left<kCat>(t, w, node, bin) ? left : left + 1;
             return (unsigned)c < (unsigned)n ? c : 0;
         };
-        if (!da) a = next(wa, ba, a, n_nodes);
-        if (!db) b = next(wb, bb, b, n_nodes);
+        const int a1 = next(wa, ba, a, n_nodes), b1 = next(wb, bb, b, n_nodes);
+        a = da ? a : a1;
+        b = db ? b : b1;
     }
     na = a;
     nb = b;
@@ -5192,6 +5241,7 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     // (boosting.mojo:2898-2907, :3876-4165)
     if (s.hp.num_class == 1 && n_leaves == 1 && fabs(s.t_value[0]) < 1e-12) return;
     const PackedTree tree = load_packed_tree(s, score_smem);
+    const bool has_cat = s.t_cat != nullptr;  // categorical nodes possible (launch-uniform)
     const double lr = s.hp.learning_rate;
     const int k = s.round->class_k;
     const int rec = s.rec_bytes, tf = s.tile_f;
@@ -5222,7 +5272,8 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
             mine4[1] = c1;
             mine4[2] = c2;
             mine4[3] = c3;
-            const int node = walk_packed(tree, n_nodes, [&](int f) { return (int)mine[f]; });
+            auto bin = [&](int f) { return (int)mine[f]; };
+            const int node = has_cat ? walk_packed<true>(tree, n_nodes, bin) : walk_packed<false>(tree, n_nodes, bin);
             raw[r] = fma(lr, tree.value[node], cv);
             c0 = n0;
             c1 = n1;
@@ -5234,10 +5285,11 @@ __global__ __launch_bounds__(256) void k_score(DevState s) {
     }
     for (int64_t r = r0; r < n; r += stride) {
         const uint8_t *rb = s.records + r * rec;
-        const int node = walk_packed(tree, n_nodes, [&](int f) {
+        auto bin = [&](int f) {
             const int t = f / tf;
             return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
-        });
+        };
+        const int node = has_cat ? walk_packed<true>(tree, n_nodes, bin) : walk_packed<false>(tree, n_nodes, bin);
         raw[r] = fma(lr, tree.value[node], raw[r]);
     }
 }
@@ -5263,6 +5315,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
     const int n_nodes = s.t_meta[0];
     const bool add = !(s.t_meta[1] == 1 && fabs(s.t_value[0]) < 1e-12);
     const PackedTree tree = load_packed_tree(s, score_smem);
+    const bool has_cat = s.t_cat != nullptr;  // categorical nodes possible (launch-uniform)
     const double lr = hp.learning_rate;
     const int rec = s.rec_bytes;
     const bool in_regs = s.n_tiles == 1 && rec <= 32;
@@ -5334,8 +5387,10 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
                 srec[256 * 2 + threadIdx.x * 2] = ca2;
                 srec[256 * 2 + threadIdx.x * 2 + 1] = cb2;
                 int n1, n2;
-                walk_packed2(tree, n_nodes, [&](int f) { return (int)mine[f]; },
-                             [&](int f) { return (int)mine2[f]; }, n1, n2);
+                auto bin1 = [&](int f) { return (int)mine[f]; };
+                auto bin2 = [&](int f) { return (int)mine2[f]; };
+                if (has_cat) walk_packed2<true>(tree, n_nodes, bin1, bin2, n1, n2);
+                else walk_packed2<false>(tree, n_nodes, bin1, bin2, n1, n2);
                 raw = fma(lr, tree.value[n1], raw);
                 s.raw[r] = raw;
                 raw2 = fma(lr, tree.value[n2], raw2);
@@ -5359,10 +5414,12 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
             double raw = s.raw[r];
             if (add) {
                 const uint8_t *rb = s.records + r * rec;
-                const int node = walk_packed(tree, n_nodes, [&](int f) {
+                auto bin = [&](int f) {
                     const int t = f / tf;
                     return (int)rb[(size_t)t * tile_bytes + (f - t * tf)];
-                });
+                };
+                const int node =
+                    has_cat ? walk_packed<true>(tree, n_nodes, bin) : walk_packed<false>(tree, n_nodes, bin);
                 raw = fma(lr, tree.value[node], raw);
                 s.raw[r] = raw;
             }
