@@ -5103,20 +5103,10 @@ struct PackedTree {
 
 // tree.goes_left for a packed node: bit 50 marks a categorical node, routed
 // by its set (bin 0, missing or unseen, is in no set); otherwise the missing
-// bin follows default_left and bin <= threshold goes left. kCat: the tree may
-// hold categorical nodes (a dataset with categorical features); without them
-// the rule is selects only, no branch that splits the wave.
-template <bool kCat>
-__device__ __forceinline__ bool packed_goes_left(const PackedTree &t, unsigned long long w, int node, int b) {
-    if (kCat && ((w >> 50) & 1ULL)) return (t.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1ULL;
-    const int thr = (int)((w >> 16) & 255ULL);
-    const int mbin = (int)((w >> 24) & 511ULL) - 1;
-    const bool dl = (w >> 33) & 1ULL;
-    return (b == mbin) ? dl : (b <= thr);
-}
-// The numerical rule in integer arithmetic, 1 when bin b goes left:
-// le ^ (miss & (le ^ dl)) is dl for the missing bin and le otherwise (no
-// boolean select for the compiler to turn into a branch).
+// bin follows default_left and bin <= threshold goes left. The numerical rule
+// in integer arithmetic, 1 when bin b goes left: le ^ (miss & (le ^ dl)) is
+// dl for the missing bin and le otherwise (no boolean select for the compiler
+// to turn into a branch).
 __device__ __forceinline__ unsigned packed_left_bit(unsigned long long w, int b) {
     const unsigned thr = (unsigned)(w >> 16) & 255u;
     const unsigned mbin = ((unsigned)(w >> 24) & 511u) - 1u;  // 0xFFFFFFFF: no missing bin
@@ -5156,30 +5146,28 @@ __device__ __forceinline__ PackedTree load_packed_tree(const DevState &s, unsign
 // follows default_left, otherwise bin <= threshold goes left
 // (tree.goes_left, src/mojotrees/tree.mojo:483-505). Children always have
 // larger ids than their parent, so a walk ends within n_nodes steps.
+// 1 when bin b goes left at node `node` (word w): with kCat, a categorical
+// node's set bit is read for every node (in bounds; used only where bit 50
+// marks the node categorical) and selected, so the step has no branch.
+template <bool kCat>
+__device__ __forceinline__ unsigned packed_left(const PackedTree &t, unsigned long long w, int node, int b) {
+    const unsigned num = packed_left_bit(w, b);
+    if (!kCat) return num;
+    const unsigned set = (unsigned)(t.cat[(size_t)node * 4 + (b >> 6)] >> (b & 63)) & 1u;
+    return ((w >> 50) & 1ULL) ? set : num;
+}
+
 template <bool kCat, class BinOf>
 __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, BinOf bin) {
-    if (!kCat) {
-        // no branch inside the step (a lane leaves the loop at its leaf)
-        int node = 0;
-        unsigned long long w = t.node[0];
-        for (int d = 0; d < n_nodes; ++d) {
-            const int f = (int)(w & 0xFFFFULL);
-            if (f == 0xFFFF) break;
-            const int c = (int)((w >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(w, bin(f));
-            node = (unsigned)c < (unsigned)n_nodes ? c : 0;
-            w = t.node[node];
-        }
-        return node;
-    }
+    // no branch inside the step (a lane leaves the loop at its leaf)
     int node = 0;
+    unsigned long long w = t.node[0];
     for (int d = 0; d < n_nodes; ++d) {
-        const unsigned long long w = t.node[node];
         const int f = (int)(w & 0xFFFFULL);
         if (f == 0xFFFF) break;
-        const int b = bin(f);
-        const int left = (int)((w >> 34) & 0xFFFFULL);
-        node = packed_goes_left<kCat>(t, w, node, b) ? left : left + 1;
-        if ((unsigned)node >= (unsigned)n_nodes) node = 0;
+        const int c = (int)((w >> 34) & 0xFFFFULL) + 1 - (int)packed_left<kCat>(t, w, node, bin(f));
+        node = (unsigned)c < (unsigned)n_nodes ? c : 0;
+        w = t.node[node];
     }
     return node;
 }
@@ -5189,43 +5177,21 @@ __device__ __forceinline__ int walk_packed(const PackedTree &t, int n_nodes, Bin
 template <bool kCat, class BinA, class BinB>
 __device__ __forceinline__ void walk_packed2(const PackedTree &t, int n_nodes, BinA bin_a, BinB bin_b, int &na,
                                              int &nb) {
-    if (!kCat) {
-        // both rows step until both reach their leaves; a row at its leaf
-        // keeps it and reads feature 0 (selects, no branch inside the step)
-        int a = 0, b = 0;
-        unsigned long long wa = t.node[0], wb = wa;
-        for (int d = 0; d < n_nodes; ++d) {
-            const int fa = (int)(wa & 0xFFFFULL), fb = (int)(wb & 0xFFFFULL);
-            const bool la = fa == 0xFFFF, lb = fb == 0xFFFF;
-            if (la && lb) break;
-            const int ba = bin_a(la ? 0 : fa), bb = bin_b(lb ? 0 : fb);
-            const int ca = (int)((wa >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(wa, ba);
-            const int cb = (int)((wb >> 34) & 0xFFFFULL) + 1 - (int)packed_left_bit(wb, bb);
-            a = la ? a : ((unsigned)ca < (unsigned)n_nodes ? ca : 0);
-            b = lb ? b : ((unsigned)cb < (unsigned)n_nodes ? cb : 0);
-            wa = t.node[a];
-            wb = t.node[b];
-        }
-        na = a;
-        nb = b;
-        return;
-    }
+    // both rows step until both reach their leaves; a row at its leaf keeps
+    // it and reads feature 0 (selects, no branch inside the step)
     int a = 0, b = 0;
-    bool da = false, db = false;
-    for (int d = 0; d < n_nodes && !(da && db); ++d) {
-        const unsigned long long wa = t.node[a], wb = t.node[b];
+    unsigned long long wa = t.node[0], wb = wa;
+    for (int d = 0; d < n_nodes; ++d) {
         const int fa = (int)(wa & 0xFFFFULL), fb = (int)(wb & 0xFFFFULL);
-        da |= fa == 0xFFFF;
-        db |= fb == 0xFFFF;
-        const int ba = da ? 0 : bin_a(fa), bb = db ? 0 : bin_b(fb);
-        auto next = [&t](unsigned long long w, int bin, int node, int n) {
-            const int left = (int)((w >> 34) & 0xFFFFULL);
-            const int c = packed_goes_left<kCat>(t, w, node, bin) ? left : left + 1;
-            return (unsigned)c < (unsigned)n ? c : 0;
-        };
-        const int a1 = next(wa, ba, a, n_nodes), b1 = next(wb, bb, b, n_nodes);
-        a = da ? a : a1;
-        b = db ? b : b1;
+        const bool la = fa == 0xFFFF, lb = fb == 0xFFFF;
+        if (la && lb) break;
+        const int ba = bin_a(la ? 0 : fa), bb = bin_b(lb ? 0 : fb);
+        const int ca = (int)((wa >> 34) & 0xFFFFULL) + 1 - (int)packed_left<kCat>(t, wa, a, ba);
+        const int cb = (int)((wb >> 34) & 0xFFFFULL) + 1 - (int)packed_left<kCat>(t, wb, b, bb);
+        a = la ? a : ((unsigned)ca < (unsigned)n_nodes ? ca : 0);
+        b = lb ? b : ((unsigned)cb < (unsigned)n_nodes ? cb : 0);
+        wa = t.node[a];
+        wb = t.node[b];
     }
     na = a;
     nb = b;
