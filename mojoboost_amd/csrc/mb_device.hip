@@ -363,7 +363,11 @@ void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run
     // histograms fit (quantized), one for the fp32 cells, whose histogram
     // fills a CU's LDS (half the partials to merge; measured 0.3 % faster on
     // C3 than two tasks per CU run one after the other)
-    s.pb_launch = (kind == mb::kAccFloat ? 1 : 2) * ds->n_cu;
+    // (no more blocks than a batch can have tasks: n / hist_chunk_min + one
+    // per item; every block of a launch, empty or not, is dispatched -- times
+    // the feature tiles)
+    s.pb_launch = (int32_t)std::min<int64_t>((kind == mb::kAccFloat ? 1 : 2) * ds->n_cu,
+                                             (ds->n + s.hist_chunk_min - 1) / s.hist_chunk_min + s.kmax);
     // a batch's accumulation tasks: with chunk >= its rows / pb_launch (or
     // = limit) an item of m rows takes at most m / chunk + 1 of them
     s.pb_grid = (int32_t)(s.pb_launch + s.kmax + (ds->n + limit - 1) / limit);
