@@ -173,6 +173,31 @@ struct PinnedFlags {
     }
 };
 
+// A state growing its share of a multiclass round's class trees on its own
+// stream (mbh_train with several states side by side): the device state, the
+// two pinned batch headers and group markers of its iteration groups, and
+// where the tree it grows stands.
+struct ClassState {
+    mb::DevState s{};
+    hipStream_t st = nullptr;
+    PinnedFlags flags;
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipEvent_t done = nullptr;
+    int est = 0;          // expansion iterations its previous tree needed
+    int cls = 0;          // class of the tree it grows next
+    bool growing = false; // a tree is in flight
+    int pending = 0;      // slot of the iteration group whose header is read next
+    int iters = 0;        // iterations enqueued for the tree in flight
+    ClassState() = default;
+    ClassState(const ClassState &) = delete;
+    ClassState &operator=(const ClassState &) = delete;
+    ~ClassState() {
+        for (hipEvent_t e : {ev[0], ev[1], done})
+            if (e) (void)hipEventDestroy(e);
+        if (st) (void)hipStreamDestroy(st);
+    }
+};
+
 // LDS a histogram block leaves free beside its histogram (scheduling slack).
 constexpr size_t kPbStaticLds = 2048;
 // Leaves expanded per launch, at most (the best-first replay of C2-shaped
@@ -190,6 +215,10 @@ constexpr int kFirstGroup = 8;
 // Most classes of a multiclass objective.
 constexpr int kMaxClass = 1024;
 constexpr int kNextGroup = 1;
+#ifndef MB_STATE_NEXT_GROUP
+#define MB_STATE_NEXT_GROUP 1
+#endif
+constexpr int kStateNextGroup = MB_STATE_NEXT_GROUP;  // later groups of a side-by-side class state
 constexpr int kMaxGroup = 64;
 
 int64_t chunk_limit_for(int B) {
@@ -525,6 +554,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
     mb::HyperParams &hp = s.hp;
     hp.objective = p->objective;
     hp.num_class = K;
+    hp.class_stride = 1;
     hp.num_leaves = L;
     hp.min_data_in_leaf = p->min_data_in_leaf;
     hp.max_depth = p->max_depth;
@@ -759,6 +789,98 @@ void setup_record_partition(mb::DevState &s, const mbh_dataset *ds, const mbh_pa
     // the root's batch shares the record partition's kPartChunk-row tasks
     // (16K-row tasks would hold 16 records per thread)
     s.part_root = 0;
+}
+
+// One more state for a multiclass round's class trees grown side by side:
+// a copy of s0 sharing the dataset, the scores and probabilities, the
+// archive, the feature masks, the bag tables, the error word and the
+// round-level GOSS sample, with its own copy of everything one tree's growth
+// writes -- the records (each tree's quantized pairs land in them), the
+// derivatives and their magnitude statistics, the round state, the row
+// lists, histograms, partials, explored nodes, batch, frontier, scan
+// results and the tree being grown. Its first class is `first`; it grows
+// classes first, first + stride, ... of every round.
+mb::DevState clone_class_state(const mb::DevState &s0, const mbh_dataset *ds, int first, int stride,
+                               int L, int max_nodes, Run &run) {
+    mb::DevState s = s0;
+    const int64_t n = ds->n;
+    const int F = ds->F;
+    s.hp.class_stride = stride;
+    const size_t rec_total = (size_t)s0.n_tiles * (size_t)n * (size_t)s0.rec_bytes;
+    uint8_t *rec = dalloc<uint8_t>(rec_total, run.owned);
+    HIPX(hipMemcpy(rec, s0.records, rec_total, hipMemcpyDeviceToDevice));
+    s.records = rec;
+    s.records_w = rec;
+    s.grad = dalloc<float>(n, run.owned);
+    s.hess = dalloc<float>(n, run.owned);
+    if (s0.gh2) s.gh2 = dalloc<float>(2 * (size_t)n, run.owned);
+    s.stats = dalloc<uint32_t>(4 * mb::kStatSlots, run.owned);
+    s.round = dalloc<mb::Round>(1, run.owned);
+    s.rows0 = dalloc<int32_t>(n, run.owned);
+    s.rows1 = dalloc<int32_t>(n, run.owned);
+    if (s0.hist) s.hist = dalloc<int32_t>((size_t)(1 + s0.max_exp) * F * ds->nb * 3, run.owned);
+    if (s0.histf) s.histf = dalloc<mb::HistF>((size_t)(1 + s0.max_exp) * F * ds->nb, run.owned);
+    const int kind = s0.hp.wide ? mb::kAccWide : s0.hp.quantized ? mb::kAccQuant : mb::kAccFloat;
+    s.part = nullptr;
+    s.part_c = nullptr;
+    s.fpart_g = s.fpart_h = nullptr;
+    s.fpart_c = nullptr;
+    configure_hist(s, ds, s0.hp.quantized ? s0.hp.quant_bins : 4, kind, run);
+    if (s0.gq) s.gq = dalloc<int32_t>(2 * (size_t)n, run.owned);
+    if (s0.magpart) s.magpart = dalloc<float>(2 * 256, run.owned);
+    if (s0.stage16_over) {
+        s.stage16_over = dalloc<unsigned long long>(2, run.owned);
+        HIPX(hipMemset(s.stage16_over, 0, 2 * sizeof(unsigned long long)));
+    }
+    if (s0.goss_max) {
+        s.goss_max = dalloc<unsigned long long>(4, run.owned);
+        HIPX(hipMemset(s.goss_max, 0, 4 * sizeof(unsigned long long)));
+    }
+    s.enodes = dalloc<mb::ENode>(s.e_cap, run.owned);
+    s.items = dalloc<mb::Item>(s.kmax, run.owned);
+    s.batch = dalloc<mb::Batch>(1, run.owned);
+    s.grow = dalloc<mb::Grow>(1, run.owned);
+    s.slot_e = dalloc<int32_t>(L, run.owned);
+    s.slot_fid = dalloc<int32_t>(L, run.owned);
+    s.scan = dalloc<mb::ScanResult>((size_t)s.kmax * 2 * F, run.owned);
+    s.scan_gain = dalloc<double>((size_t)s.kmax * 2 * F, run.owned);
+    s.pair_gain = dalloc<double>((size_t)s.kmax * 2, run.owned);
+    s.pair_feat = dalloc<int32_t>((size_t)s.kmax * 2, run.owned);
+    s.e_gain = dalloc<double>(s.e_cap, run.owned);
+    s.e_left = dalloc<int32_t>(s.e_cap, run.owned);
+    s.e_rows = dalloc<int32_t>(s.e_cap, run.owned);
+    s.e_parent = dalloc<int32_t>(s.e_cap, run.owned);
+    s.cursor = dalloc<int64_t>(2 + 2 * (size_t)s.kmax, run.owned);
+    s.t_feature = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_threshold = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_left = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_right = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_default_left = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_missing_bin = dalloc<int32_t>(max_nodes, run.owned);
+    s.t_value = dalloc<double>(max_nodes, run.owned);
+    s.t_gain = dalloc<double>(max_nodes, run.owned);
+    s.t_count = dalloc<double>(max_nodes, run.owned);
+    s.t_meta = dalloc<int32_t>(2, run.owned);
+    if (s0.scan_cat) {
+        s.scan_cat = dalloc<unsigned long long>((size_t)s.kmax * 2 * F * 4, run.owned);
+        s.e_cat = dalloc<unsigned long long>((size_t)s.e_cap * 4, run.owned);
+        s.t_cat = dalloc<unsigned long long>((size_t)max_nodes * 4, run.owned);
+        HIPX(hipMemset(s.t_cat, 0, (size_t)max_nodes * 4 * sizeof(unsigned long long)));
+    }
+    HIPX(hipMemset(s.rows0, 0, (size_t)n * sizeof(int32_t)));
+    HIPX(hipMemset(s.rows1, 0, (size_t)n * sizeof(int32_t)));
+    HIPX(hipMemset(s.stats, 0, 4 * mb::kStatSlots * sizeof(uint32_t)));
+    HIPX(hipMemset(s.batch, 0, sizeof(mb::Batch)));
+    HIPX(hipMemset(s.grow, 0, sizeof(mb::Grow)));
+    HIPX(hipMemset(s.part_items, 0, (size_t)s.kmax * sizeof(mb::PartItem)));
+    HIPX(hipMemset(s.acc_items, 0, (size_t)s.kmax * sizeof(mb::AccItem)));
+    HIPX(hipMemset(s.cursor, 0, (2 + 2 * (size_t)s.kmax) * sizeof(int64_t)));
+    HIPX(hipMemset(s.t_meta, 0, 2 * sizeof(int32_t)));
+    mb::Round r0 = mb::initial_round();
+    r0.class_k = first;
+    r0.tree_index = first;
+    HIPX(hipMemcpy(s.round, &r0, sizeof(r0), hipMemcpyHostToDevice));
+    return s;
 }
 
 // The packed int16 arm's refusal (gpu_active_rows._raise_stage16): values
@@ -1029,8 +1151,116 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
         // objective of tree t + 1 in the same pass
         const bool fuse_objective =
             K == 1 && (p->objective == MBH_OBJ_BINARY || p->objective == MBH_OBJ_REGRESSION);
+        // Multiclass: the K trees of a round are independent (each reads the
+        // round's probabilities and writes only its class's scores), so S
+        // states grow them side by side, each on its own stream, and the
+        // latency-bound launches of several trees overlap on the chip. A
+        // state grows classes j, j + S, ...; every round starts with the
+        // softmax (and the GOSS sample) on state 0's stream, and state 0
+        // joins the others' streams before the round's stop rule. Timed
+        // runs and the record partition keep the single stream.
+        const int S = (K > 1 && !timed && !s.rcp) ? std::min(K, mb::kMaxClassStates) : 1;
+        std::vector<ClassState> cs(S > 1 ? S : 0);
+        if (S > 1) {
+            s.hp.class_stride = S;
+            for (int j = 0; j < S; ++j) {
+                ClassState &c = cs[j];
+                c.s = j == 0 ? s : clone_class_state(s, ds, j, S, L, tb.max_nodes, run);
+                c.est = kFirstGroup;
+                HIPX(hipStreamCreateWithFlags(&c.st, hipStreamNonBlocking));
+                HIPX(hipHostMalloc((void **)&c.flags.p, 2 * sizeof(mb::Batch), hipHostMallocDefault));
+                for (int e = 0; e < 2; ++e) HIPX(hipEventCreateWithFlags(&c.ev[e], hipEventDisableTiming));
+                HIPX(hipEventCreateWithFlags(&c.done, hipEventDisableTiming));
+            }
+            HIPX(hipDeviceSynchronize());
+        }
         auto t0 = std::chrono::steady_clock::now();
-        for (int t = 0; t < T; ++t) {
+        if (S > 1) {
+            // one iteration group of state c in header slot `slot`: its last
+            // planning launch writes the batch header there
+            auto enqueue_group = [&](ClassState &c, int slot, int n, bool first) {
+                for (int i = 0; i < n; ++i) {
+                    HIPX(mb::launch_partition(c.s, c.st, nullptr, nullptr, c.s.part_root && first && i == 0));
+                    HIPX(mb::launch_accum(c.s, c.st));
+                    HIPX(mb::launch_scan(c.s, 0, c.st));
+                    HIPX(mb::launch_plan(c.s, 0, c.st, i == n - 1 ? &c.flags.p[slot] : nullptr));
+                }
+                pb_launches += n;
+                HIPX(hipEventRecord(c.ev[slot], c.st));
+            };
+            // a class tree's objective, quantizer and root, then two
+            // iteration groups in flight (as the single-stream loop)
+            auto start_tree = [&](ClassState &c) {
+                mb::DevState &z = c.s;
+                HIPX(mb::launch_objective(z, grid_rows, c.st));
+                if (z.hp.goss && z.hp.quantized) HIPX(mb::launch_goss_stats(z, grid_rows, c.st));
+                if (z.hp.wide) HIPX(mb::launch_magnitude(z, c.st));
+                const bool fuse_q = mb::acc_kind(z.hp) == mb::kAccQuant && !z.hp.grad64;
+                const bool q_rows = !fuse_q || z.hp.bagging || z.hp.goss;
+                HIPX(mb::launch_quantize(z, q_rows ? grid_rows : 1, c.st, !fuse_q));
+                HIPX(mb::launch_hist(z, c.st, nullptr, nullptr, fuse_q));
+                HIPX(mb::launch_scan(z, 1, c.st));
+                HIPX(mb::launch_plan(z, 1, c.st));
+                const int n0 = std::max(1, std::min(c.est - 2, kMaxGroup));
+                enqueue_group(c, 0, n0, true);
+                enqueue_group(c, 1, kStateNextGroup, false);
+                c.pending = 0;
+                c.iters = n0 + kStateNextGroup;
+                c.growing = true;
+            };
+            // reads the header of the group in flight longest once its
+            // marker completed: the tree is finished (score update, round
+            // end) or one more group is enqueued in the freed slot
+            auto poll = [&](ClassState &c) {
+                const hipError_t q = hipEventQuery(c.ev[c.pending]);
+                if (q == hipErrorNotReady) return;
+                HIPX(q);
+                if (c.flags.p[c.pending].done) {
+                    c.est = c.flags.p[c.pending].iters;
+                    HIPX(mb::launch_score(c.s, grid_score, c.st));
+                    HIPX(mb::launch_round_end(c.s, c.st));
+                    c.growing = false;
+                    c.cls += S;
+                    return;
+                }
+                if (c.iters > L + kMaxGroup + 2)
+                    throw Error{MOJOTREES_ERROR_TRAINING, "tree growth did not finish (internal error)"};
+                enqueue_group(c, c.pending, kStateNextGroup, false);
+                c.iters += kStateNextGroup;
+                c.pending = 1 - c.pending;
+            };
+            mb::RoundStates rs{};
+            rs.n = S;
+            for (int j = 0; j < S; ++j) rs.r[j] = cs[j].s.round;
+            const int sampling = (s.hp.bagging || s.hp.goss) ? 1 : 0;
+            for (int rr = 0; rr < T / K; ++rr) {
+                ClassState &c0 = cs[0];
+                HIPX(mb::launch_softmax(c0.s, grid_softmax, c0.st));
+                if (c0.s.hp.goss) HIPX(mb::launch_goss(c0.s, grid_rows, c0.st));
+                HIPX(hipEventRecord(c0.done, c0.st));
+                for (int j = 1; j < S; ++j) HIPX(hipStreamWaitEvent(cs[j].st, c0.done, 0));
+                for (int j = 0; j < S; ++j) cs[j].cls = j;
+                for (;;) {
+                    bool active = false;
+                    for (ClassState &c : cs) {
+                        if (!c.growing && c.cls < K) start_tree(c);
+                        if (c.growing) {
+                            active = true;
+                            poll(c);
+                        }
+                    }
+                    if (!active) break;
+                }
+                for (int j = 1; j < S; ++j) {
+                    HIPX(hipEventRecord(cs[j].done, cs[j].st));
+                    HIPX(hipStreamWaitEvent(c0.st, cs[j].done, 0));
+                }
+                HIPX(mb::launch_round_combine(rs, sampling, c0.st));
+            }
+            HIPX(hipDeviceSynchronize());
+            for (int j = 1; j < S; ++j) check_stage16(cs[j].s, ds->n);
+        }
+        for (int t = 0; S == 1 && t < T; ++t) {
             // GOSS draws its sample after the derivatives it ranks rows by
             // and before the quantizer, which sees the weighted derivatives
             // (goss_round, then the grower's quantizer): per tree for a

@@ -5452,19 +5452,42 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
             if (K == 1) {
                 if (degenerate && !sampling) nr.stopped = 1;
             } else {
-                nr.progress = (rd.class_k == 0 ? 0 : rd.progress) | (degenerate ? 0 : 1);
-                if (rd.class_k == K - 1 && !nr.progress && !sampling) nr.stopped = 1;
+                // progress over this state's trees of the round; with several
+                // states side by side, k_round_combine judges the round
+                const bool first = rd.class_k < s.hp.class_stride;
+                nr.progress = (first ? 0 : rd.progress) | (degenerate ? 0 : 1);
+                if (s.hp.class_stride == 1 && rd.class_k == K - 1 && !nr.progress && !sampling) nr.stopped = 1;
             }
         }
-        nr.tree_index = rd.tree_index + 1;
-        nr.class_k = rd.class_k + 1;
+        // this state's next class tree: class_k + stride, or its first class
+        // of the next round
+        const int S = s.hp.class_stride;
+        nr.class_k = rd.class_k + S;
         if (nr.class_k >= s.hp.num_class) {
-            nr.class_k = 0;
+            nr.class_k = rd.class_k % S;
             nr.round = rd.round + 1;
         }
+        nr.tree_index = (int32_t)(nr.round * s.hp.num_class + nr.class_k);
         nr.parity = 1 - rd.parity;
         *s.round = nr;
     }
+}
+
+// The round's stop rule when several states grow its class trees side by
+// side (one thread, after every state finished the round): boosting.
+// train_multiclass judges the round's K trees together -- a round none of
+// whose trees split or moved ends training unless rows are sampled
+// (boosting.mojo:3876-4165) -- so the states' progress flags are combined
+// and every state stops.
+__global__ void k_round_combine(RoundStates rs, int sampling) {
+    if (threadIdx.x != 0) return;
+    bool stopped = false, progress = false;
+    for (int i = 0; i < rs.n; ++i) {
+        stopped |= rs.r[i]->stopped != 0;
+        progress |= rs.r[i]->progress != 0;
+    }
+    if (!stopped && !progress && !sampling)
+        for (int i = 0; i < rs.n; ++i) rs.r[i]->stopped = 1;
 }
 
 // Bins column-major -> tile-major row records (each tile: its features' bin
@@ -5800,6 +5823,10 @@ int rows_grid(const DevState &s, RowsKernel k, int n_cu) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess) per_cu = 8;
     per_cu = per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu;
     return per_cu * (n_cu < 1 ? 1 : n_cu);
+}
+hipError_t launch_round_combine(const RoundStates &rs, int sampling, hipStream_t st) {
+    hipLaunchKernelGGL(k_round_combine, dim3(1), dim3(64), 0, st, rs, sampling);
+    return hipGetLastError();
 }
 hipError_t launch_round_end(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_round_end, dim3(1), dim3(256), 0, st, s);
