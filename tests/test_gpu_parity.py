@@ -239,6 +239,25 @@ def test_training_multiclass_bit_exact(dev, bagging):
     _compare_fit(fit, ref, n)
 
 
+@pytest.mark.parametrize("K,bagging", [(2, False), (7, True)])
+def test_training_multiclass_side_by_side_states(dev, K, bagging):
+    """A round's class trees are grown by up to three states side by side,
+    each on its own stream: two states for two classes, three for seven
+    (growing classes 0, 3, 6 / 1, 4 / 2, 5). The oracle grows the classes in
+    turn; every tree and training score must be identical."""
+    n = 60_000
+    bins, y, mb, nb, f = c5_like(n, K, seed=11)
+    kw = dict(objective=2, num_class=K, num_iterations=3, num_leaves=31, min_data_in_leaf=20,
+              lambda_l2=1.0, learning_rate=0.1)
+    if bagging:
+        kw.update(bagging_fraction=0.6, bagging_freq=1, bagging_seed=4)
+    ds = dev.Dataset(bins, n, f, nb, y, missing_bin=mb)
+    fit = ds.train(**kw)
+    ref = O.train(bins, n, f, nb, y, O.default_params(**kw, use_quantized_grad=1), missing_bin=mb)
+    assert fit.num_class == K and fit.n_trees == 3 * K
+    _compare_fit(fit, ref, n)
+
+
 def test_estimator_multiclass_through_c_abi_bit_exact(dev, tmp_path):
     """MojoTreesClassifier with 4 classes -> objective=multiclass through the
     C ABI; raw scores equal the oracle's on its own bins, and survive
