@@ -3390,9 +3390,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan_narrow(DevState s, int
 
 template <bool kCat>
 __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState s, int root_mode) {
-    __shared__ double cg[2][256], ch[2][256];
+    __shared__ __align__(16) double cg[2][256], ch[2][256];
     __shared__ int cc[2][256];
-    __shared__ double pg_[2][256], ph_[2][256];
+    __shared__ __align__(16) double pg_[2][256], ph_[2][256];
     __shared__ int pc_[2][256];
     __shared__ double accg[256], acch[256];
     __shared__ double ckey[2][256];
@@ -3549,85 +3549,100 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
         }
         const int child = tid >> 8;
         const int bin = tid & 255;
-        // ---- the reference's sequential sums per child: lane 0 of the
-        // child's first wave sums the grad cells, lane 1 the hess cells, both
-        // the counts (the last count prefix is the total); the next four
-        // cells are requested before the current four are added
-        if ((tid & 255) < 2) {
-            constexpr int W = 8;
-            const int q = tid & 1;
-            const double *src = q ? ch[child] : cg[child];
-            double *dst = q ? ph_[child] : pg_[child];
-            const int *csrc = cc[child];
-            int *cdst = pc_[child];
-            double lw[W];
+        // ---- the reference's sums per child, split over four waves:
+        //  wave 0: the sequential prefix sums (lane 2c + q: child c, grad
+        //    cells for q = 0, hess for q = 1), eight cells per step with the
+        //    next eight in flight;
+        //  wave 1: the eight-way totals (lane 16c + 8q + k sums cells k,
+        //    k + 8, ... of the full 8-cell blocks in order, then the lanes
+        //    pair up as (k, k + 4), (k, k + 2), (0, 1) and the last partial
+        //    block is added in order);
+        //  waves 2, 3: the count prefixes of child 0, 1 (integers: a wave
+        //    scan gives the same values as the sequential sum; the last
+        //    prefix is the total).
+        if (wv == 0) {
+            if (lane < 4) {
+                const int c = lane >> 1, q = lane & 1;
+                const double *src = q ? ch[c] : cg[c];
+                double *dst = q ? ph_[c] : pg_[c];
+                double r = 0.0;
+                int b = 0;
+                if (nb >= 8) {
+                    double2 x[4];
 #pragma unroll
-            for (int k = 0; k < W; ++k) lw[k] = 0.0;
-            double r = 0.0;
-            int rc = 0;
-            int b = 0;
-            if (nb >= W) {
-                // four cells per register block, the next four in flight
-                constexpr int H = W / 2;
-                double x[H];
-                int y[H];
+                    for (int u = 0; u < 4; ++u) x[u] = ((const double2 *)src)[u];
+                    for (; b + 8 <= nb; b += 8) {
+                        // the next block's cells (clamped in bounds of the
+                        // 256-cell rows; past the last full block unused)
+                        const int nx = b + 8 <= 248 ? b + 8 : 248;
+                        double2 xn[4];
 #pragma unroll
-                for (int u = 0; u < H; ++u) {
-                    x[u] = src[u];
-                    y[u] = csrc[u];
+                        for (int u = 0; u < 4; ++u) xn[u] = ((const double2 *)(src + nx))[u];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            r += x[u].x;
+                            const double r0 = r;
+                            r += x[u].y;
+                            ((double2 *)(dst + b))[u] = make_double2(r0, r);
+                            x[u] = xn[u];
+                        }
+                    }
                 }
-                auto step = [&](int at, int lo) {
-                    // the next block's cells (clamped in bounds of the
-                    // 256-cell rows; past the last full block unused)
-                    const int nx = at + H <= 256 - H ? at + H : 256 - H;
-                    double xn[H];
-                    int yn[H];
-#pragma unroll
-                    for (int u = 0; u < H; ++u) {
-                        xn[u] = src[nx + u];
-                        yn[u] = csrc[nx + u];
-                    }
-#pragma unroll
-                    for (int u = 0; u < H; ++u) {
-                        lw[lo + u] += x[u];
-                        r += x[u];
-                        rc += y[u];
-                        dst[at + u] = r;
-                        cdst[at + u] = rc;  // both lanes, the same value
-                    }
-#pragma unroll
-                    for (int u = 0; u < H; ++u) {
-                        x[u] = xn[u];
-                        y[u] = yn[u];
-                    }
-                };
-                for (; b + W <= nb; b += W) {
-                    step(b, 0);
-                    step(b + H, H);
+                for (; b < nb; ++b) {
+                    r += src[b];
+                    dst[b] = r;
                 }
+                if (q == 0) s_sg[c] = r;
+                else s_sh[c] = r;
             }
+        } else if (wv == 1) {
+            const int c = (lane >> 4) & 1, q = (lane >> 3) & 1, kk = lane & 7;
+            const double *src = q ? ch[c] : cg[c];
+            const int full = nb & ~7;  // cells in full 8-cell blocks
+            double a = 0.0;
+            int j = kk;
+            for (; j + 24 < full; j += 32) {
+                const double v0 = src[j], v1 = src[j + 8], v2 = src[j + 16], v3 = src[j + 24];
+                a += v0;
+                a += v1;
+                a += v2;
+                a += v3;
+            }
+            for (; j < full; j += 8) a += src[j];
+            a += __shfl_down(a, 4, 64);
+            a += __shfl_down(a, 2, 64);
+            a += __shfl_down(a, 1, 64);
+            if (lane < 32 && kk == 0) {
+                double t = a;
+                for (int bb = full; bb < nb; ++bb) t += src[bb];
+                if (q == 0) s_tg[c] = t;
+                else s_th[c] = t;
+            }
+        } else if (wv < 4) {
+            const int c = wv - 2;
+            const int *csrc = cc[c];
+            int *cdst = pc_[c];
+            int pfx[4];
+            int run = 0;
 #pragma unroll
-            for (int w2 = W / 2; w2 >= 1; w2 >>= 1)
+            for (int i = 0; i < 4; ++i) {
+                const int cell = 4 * lane + i;
+                run += cell < nb ? csrc[cell] : 0;
+                pfx[i] = run;
+            }
+            int incl = run;
 #pragma unroll
-                for (int k = 0; k < w2; ++k) lw[k] = lw[k] + lw[k + w2];
-            double t = lw[0];
-            for (; b < nb; ++b) {
-                const double xv = src[b];
-                const int yv = csrc[b];
-                t += xv;
-                r += xv;
-                rc += yv;
-                dst[b] = r;
-                cdst[b] = rc;
+            for (int d = 1; d < 64; d <<= 1) {
+                const int o = __shfl_up(incl, d, 64);
+                incl += lane >= d ? o : 0;
             }
-            if (q == 0) {
-                s_tg[child] = t;
-                s_tc[child] = rc;  // the count total is the last prefix
-                s_sg[child] = r;
-            } else {
-                s_th[child] = t;
-                s_sh[child] = r;
+            const int excl = incl - run;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int cell = 4 * lane + i;
+                if (cell < nb) cdst[cell] = excl + pfx[i];
             }
+            if (lane == 63) s_tc[c] = incl;
         }
         __syncthreads();
         const double TG = s_tg[child], TH = s_th[child];
