@@ -3568,24 +3568,35 @@ __global__ __launch_bounds__(kScanThreads, kCat ? 1 : 4) void k_scan_f(DevState 
                 double r = 0.0;
                 int b = 0;
                 if (nb >= 8) {
-                    double2 x[4];
+                    // two register blocks of eight cells taking turns: one is
+                    // added while the other's cells are requested (loads
+                    // clamped in bounds of the 256-cell rows; past the last
+                    // full block unused)
+                    double2 xa[4], xb[4];
+                    auto ld8 = [&](double2 *x, int at) {
+                        const int c8 = at <= 248 ? at : 248;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) x[u] = ((const double2 *)src)[u];
-                    for (; b + 8 <= nb; b += 8) {
-                        // the next block's cells (clamped in bounds of the
-                        // 256-cell rows; past the last full block unused)
-                        const int nx = b + 8 <= 248 ? b + 8 : 248;
-                        double2 xn[4];
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) xn[u] = ((const double2 *)(src + nx))[u];
+                        for (int u = 0; u < 4; ++u) x[u] = ((const double2 *)(src + c8))[u];
+                    };
+                    auto add8 = [&](const double2 *x, int at) {
 #pragma unroll
                         for (int u = 0; u < 4; ++u) {
                             r += x[u].x;
                             const double r0 = r;
                             r += x[u].y;
-                            ((double2 *)(dst + b))[u] = make_double2(r0, r);
-                            x[u] = xn[u];
+                            ((double2 *)(dst + at))[u] = make_double2(r0, r);
                         }
+                    };
+                    ld8(xa, 0);
+                    for (; b + 16 <= nb; b += 16) {
+                        ld8(xb, b + 8);
+                        add8(xa, b);
+                        ld8(xa, b + 16);
+                        add8(xb, b + 8);
+                    }
+                    if (b + 8 <= nb) {
+                        add8(xa, b);
+                        b += 8;
                     }
                 }
                 for (; b < nb; ++b) {
