@@ -2685,6 +2685,11 @@ __global__ __launch_bounds__(kAccThreads) void k_accum_rec(DevState s) {
 constexpr int kScanThreads = 512;
 
 
+// Lane l's binary64 value on every lane (l wave-uniform).
+__device__ __forceinline__ double readlane_f64_early(double d, int l) {
+    return __longlong_as_double((long long)readlane_i64((int64_t)__double_as_longlong(d), l));
+}
+
 // kCat: the dataset has categorical features (the category-set search is
 // compiled in). At most 128 VGPRs (4 waves per SIMD): two 512-thread blocks
 // per CU, so a batch's (leaf, feature) tasks need half the block rounds.
@@ -2911,12 +2916,20 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                 if (lane == 0) cwcnt[wv] = __popcll(cm);
                 csort[child][bin] = cand ? 1 : 0;  // candidate flags until ranked
                 __syncthreads();
+                // rank = the candidates ordered before this one: the wave
+                // reads 64 categories' keys and flags per LDS load, then
+                // compares with each candidate's key read from its lane
                 int rank = 0;
-                if (cand)
-                    for (int u = 1; u <= ncf; ++u) {
-                        const double ku = ckey[child][u];
-                        rank += (csort[child][u] != 0 && (ku < key || (ku == key && u < bin))) ? 1 : 0;
+                for (int u0 = 1; u0 <= ncf; u0 += 64) {
+                    const int u = u0 + lane;
+                    const bool ok = u <= ncf && csort[child][u] != 0;
+                    const double ku = ok ? ckey[child][u] : 0.0;
+                    for (unsigned long long m = __ballot(ok); m; m &= m - 1ULL) {
+                        const int l = (int)__builtin_ctzll(m);
+                        const double kl = readlane_f64_early(ku, l);
+                        rank += (kl < key || (kl == key && u0 + l < bin)) ? 1 : 0;
                     }
+                }
                 const int used = cwcnt[child << 2] + cwcnt[(child << 2) + 1] + cwcnt[(child << 2) + 2] +
                                  cwcnt[(child << 2) + 3];
                 __syncthreads();
@@ -2939,6 +2952,12 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                         if (max_num_cat < 0) max_num_cat = 0;
                         const int steps = used < max_num_cat ? used : max_num_cat;
                         const double l2c = l2 + hp.cat_l2;
+                        // lane = step of the walk (64 per pass): the running
+                        // sums are integer prefix sums (exact in any order);
+                        // the walk stops at the first step that leaves too
+                        // little on the other side, and the groups of
+                        // min_data_per_group rows are a scalar pass over the
+                        // steps' counts before it
                         long long ag = 0, ah = 0;
                         long long ac = 0, agg = 0;
                         bool stop = false;
@@ -2948,35 +2967,29 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                             const int tb = in ? csort[child][d == 0 ? i : used - 1 - i] : 0;
                             const int xg = in ? cg[child][tb] : 0, xh = in ? ch[child][tb] : 0;
                             const int xc = in ? cc[child][tb] : 0;
-                            long long mg = 0, mh = 0;
-                            long long mc = 0;
-                            bool mev = false;
+                            const long long mg = ag + wave_incl_scan((long long)xg);
+                            const long long mh = ah + wave_incl_scan((long long)xh);
+                            const long long mc = ac + wave_incl_scan((long long)xc);
+                            const bool valid = in && !(mc < min_c || mh < hmin);
+                            const long long rc = TC - mc;
+                            const unsigned long long sm =
+                                __ballot(valid && (rc < min_c || rc < hp.min_data_per_group || TH - mh < hmin));
                             const int n_here = steps - c0 < 64 ? steps - c0 : 64;
-                            for (int k = 0; k < n_here; ++k) {
-                                ag += __builtin_amdgcn_readlane(xg, k);
-                                ah += __builtin_amdgcn_readlane(xh, k);
-                                const long long kc = __builtin_amdgcn_readlane(xc, k);
-                                ac += kc;
-                                agg += kc;
-                                bool ev = false;
-                                if (!(ac < min_c || ah < hmin)) {
-                                    const long long rc = TC - ac;
-                                    if (rc < min_c || rc < hp.min_data_per_group || TH - ah < hmin) {
-                                        stop = true;
-                                        break;
-                                    }
-                                    if (agg >= hp.min_data_per_group) {
-                                        ev = true;
-                                        agg = 0;
-                                    }
-                                }
-                                if (lane == k) {
-                                    mg = ag;
-                                    mh = ah;
-                                    mc = ac;
-                                    mev = ev;
+                            const int s_at = sm ? (int)__builtin_ctzll(sm) : n_here;  // first stop, else the pass's end
+                            const unsigned long long vm = __ballot(valid);
+                            unsigned long long evm = 0ULL;
+                            for (int k = 0; k < s_at; ++k) {
+                                agg += __builtin_amdgcn_readlane(xc, k);
+                                if (((vm >> k) & 1ULL) && agg >= hp.min_data_per_group) {
+                                    evm |= 1ULL << k;
+                                    agg = 0;
                                 }
                             }
+                            const bool mev = (evm >> lane) & 1ULL;
+                            stop = sm != 0ULL;
+                            ag = readlane_i64(mg, 63);
+                            ah = readlane_i64(mh, 63);
+                            ac = readlane_i64(mc, 63);
                             double bg = 0.0;
                             int bo = 0x7FFFFFFF;
                             if (mev) {
