@@ -2705,6 +2705,7 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
     // count, and each walk direction's best (gain, step, left rows)
     __shared__ double ckey[2][256];
     __shared__ int csort[2][256];
+    __shared__ int rpart[2][4][64];  // rank counts of bins 0-63 per wave of a half (below 64 categories)
     __shared__ int cwcnt[8];
     __shared__ double cdg[2][2];
     __shared__ int cdi[2][2];
@@ -2916,23 +2917,37 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                 if (lane == 0) cwcnt[wv] = __popcll(cm);
                 csort[child][bin] = cand ? 1 : 0;  // candidate flags until ranked
                 __syncthreads();
-                // rank = the candidates ordered before this one: the wave
+                // rank = the candidates ordered before this one: a wave
                 // reads 64 categories' keys and flags per LDS load, then
-                // compares with each candidate's key read from its lane
+                // compares with each candidate's key read from its lane.
+                // Below 64 categories every candidate is in the half's
+                // first wave: the half's four waves each compare the keys
+                // of bins 0-63 with a quarter of the candidates, and the
+                // quarters' counts are added up.
+                const bool few = ncf < 64;  // block-uniform
                 int rank = 0;
-                for (int u0 = 1; u0 <= ncf; u0 += 64) {
-                    const int u = u0 + lane;
-                    const bool ok = u <= ncf && csort[child][u] != 0;
-                    const double ku = ok ? ckey[child][u] : 0.0;
-                    for (unsigned long long m = __ballot(ok); m; m &= m - 1ULL) {
-                        const int l = (int)__builtin_ctzll(m);
-                        const double kl = readlane_f64_early(ku, l);
-                        rank += (kl < key || (kl == key && u0 + l < bin)) ? 1 : 0;
+                {
+                    const double kt = few ? ckey[child][lane] : key;  // the target: bin `lane`, or the own bin
+                    const int bt = few ? lane : bin;
+                    for (int u0 = 1; u0 <= ncf; u0 += 64) {
+                        const int u = u0 + lane;
+                        const bool ok = u <= ncf && csort[child][u] != 0;
+                        const double ku = ok ? ckey[child][u] : 0.0;
+                        unsigned long long m = __ballot(ok);
+                        if (few) m &= 0xFFFFULL << (16 * cw);
+                        for (; m; m &= m - 1ULL) {
+                            const int l = (int)__builtin_ctzll(m);
+                            const double kl = readlane_f64_early(ku, l);
+                            rank += (kl < kt || (kl == kt && u0 + l < bt)) ? 1 : 0;
+                        }
                     }
+                    if (few) rpart[child][cw][lane] = rank;
                 }
                 const int used = cwcnt[child << 2] + cwcnt[(child << 2) + 1] + cwcnt[(child << 2) + 2] +
                                  cwcnt[(child << 2) + 3];
                 __syncthreads();
+                if (few && cw == 0)
+                    rank = rpart[child][0][lane] + rpart[child][1][lane] + rpart[child][2][lane] + rpart[child][3][lane];
                 if (cand) csort[child][rank] = bin;
                 __syncthreads();
                 // each direction's wave: its lanes load the steps' cells, a
@@ -2953,7 +2968,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                         const int steps = used < max_num_cat ? used : max_num_cat;
                         const double l2c = l2 + hp.cat_l2;
                         // lane = step of the walk (64 per pass): the running
-                        // sums are integer prefix sums (exact in any order);
+                        // sums are 32-bit integer prefix sums (exact in any
+                        // order: every subset of a round's rows sums within
+                        // int32, as the histogram cells do);
                         // the walk stops at the first step that leaves too
                         // little on the other side, and the groups of
                         // min_data_per_group rows are a scalar pass over the
@@ -2967,9 +2984,9 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                             const int tb = in ? csort[child][d == 0 ? i : used - 1 - i] : 0;
                             const int xg = in ? cg[child][tb] : 0, xh = in ? ch[child][tb] : 0;
                             const int xc = in ? cc[child][tb] : 0;
-                            const long long mg = ag + wave_incl_scan((long long)xg);
-                            const long long mh = ah + wave_incl_scan((long long)xh);
-                            const long long mc = ac + wave_incl_scan((long long)xc);
+                            const long long mg = ag + (long long)wave_incl_scan_i(xg);
+                            const long long mh = ah + (long long)wave_incl_scan_i(xh);
+                            const long long mc = ac + (long long)wave_incl_scan_i(xc);
                             const bool valid = in && !(mc < min_c || mh < hmin);
                             const long long rc = TC - mc;
                             const unsigned long long sm =
