@@ -2967,6 +2967,7 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                         if (max_num_cat < 0) max_num_cat = 0;
                         const int steps = used < max_num_cat ? used : max_num_cat;
                         const double l2c = l2 + hp.cat_l2;
+                        const int mdpg = hp.min_data_per_group;
                         // lane = step of the walk (64 per pass): the running
                         // sums are 32-bit integer prefix sums (exact in any
                         // order: every subset of a round's rows sums within
@@ -2994,12 +2995,24 @@ __global__ __launch_bounds__(kScanThreads, 4) void k_scan(DevState s, int root_m
                             const int n_here = steps - c0 < 64 ? steps - c0 : 64;
                             const int s_at = sm ? (int)__builtin_ctzll(sm) : n_here;  // first stop, else the pass's end
                             const unsigned long long vm = __ballot(valid);
+                            const unsigned long long before = s_at < 64 ? (1ULL << s_at) - 1ULL : ~0ULL;
                             unsigned long long evm = 0ULL;
-                            for (int k = 0; k < s_at; ++k) {
-                                agg += __builtin_amdgcn_readlane(xc, k);
-                                if (((vm >> k) & 1ULL) && agg >= hp.min_data_per_group) {
-                                    evm |= 1ULL << k;
-                                    agg = 0;
+                            if ((~__ballot(xc >= mdpg) & before) == 0ULL) {
+                                // every step before the stop holds a group on
+                                // its own: each valid one closes a group, and
+                                // the open count is what follows the last
+                                evm = vm & before;
+                                if (s_at > 0) {
+                                    const long long last = readlane_i64(mc, s_at - 1);
+                                    agg = evm ? last - readlane_i64(mc, 63 - (int)__builtin_clzll(evm)) : agg + (last - ac);
+                                }
+                            } else {
+                                for (int k = 0; k < s_at; ++k) {
+                                    agg += __builtin_amdgcn_readlane(xc, k);
+                                    if (((vm >> k) & 1ULL) && agg >= mdpg) {
+                                        evm |= 1ULL << k;
+                                        agg = 0;
+                                    }
                                 }
                             }
                             const bool mev = (evm >> lane) & 1ULL;
