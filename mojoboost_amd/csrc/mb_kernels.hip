@@ -1305,11 +1305,26 @@ __global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, in
         total = total2;
     }
     const int nb = s.goss_nblk;
+    // a thread's run of `per` counts, kC loads in flight at a time (the
+    // runs of up to 16M rows' blocks are one round of loads); the counts of
+    // the first kC stay in registers for the write-back
+    constexpr int kC = 16;
     const int per = (nb + 1023) / 1024;
     const int lo = threadIdx.x * per;
     const int hi = lo + per < nb ? lo + per : nb;
     long long sum = 0;
-    for (int i = lo; i < hi; ++i) sum += blk[i];
+    int v0[kC];
+#pragma unroll
+    for (int u = 0; u < kC; ++u) v0[u] = lo + u < hi ? blk[lo + u] : 0;
+#pragma unroll
+    for (int u = 0; u < kC; ++u) sum += v0[u];
+    for (int c = lo + kC; c < hi; c += kC) {
+        int v[kC];
+#pragma unroll
+        for (int u = 0; u < kC; ++u) v[u] = c + u < hi ? blk[c + u] : 0;
+#pragma unroll
+        for (int u = 0; u < kC; ++u) sum += v[u];
+    }
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const long long inc = wave_incl_scan(sum);
     if (lane == 63) wtot[w] = inc;
@@ -1318,10 +1333,20 @@ __global__ __launch_bounds__(1024) void k_goss_scan(DevState s, int32_t *blk, in
     for (int i = 0; i < w; ++i) before += wtot[i];
     if (total != nullptr && threadIdx.x == 1023) *total = before + inc;
     long long acc = before + inc - sum;
-    for (int i = lo; i < hi; ++i) {
-        const int v = blk[i];
-        blk[i] = (int32_t)acc;
-        acc += v;
+#pragma unroll
+    for (int u = 0; u < kC; ++u) {
+        if (lo + u < hi) blk[lo + u] = (int32_t)acc;
+        acc += v0[u];
+    }
+    for (int c = lo + kC; c < hi; c += kC) {
+        int v[kC];
+#pragma unroll
+        for (int u = 0; u < kC; ++u) v[u] = c + u < hi ? blk[c + u] : 0;
+#pragma unroll
+        for (int u = 0; u < kC; ++u) {
+            if (c + u < hi) blk[c + u] = (int32_t)acc;
+            acc += v[u];
+        }
     }
 }
 
