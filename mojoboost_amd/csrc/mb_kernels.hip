@@ -2062,17 +2062,27 @@ __device__ __forceinline__ uint32_t group_last_lane(uint32_t x) {
 // would apply) instead of read from the record, and the row's record is
 // written back with the pair in place, for the expansions' accumulations;
 // rec_w is the record tile being read.
-template <int LPR, class Acc, bool kList, bool kQ, int U>
+struct NoPre {
+    __device__ void operator()() const {}
+};
+// pre: run by every thread once the first step's loads are in flight (and
+// on an empty range): the caller's zeroing of the LDS histogram and its
+// barrier, so they overlap the first records' latency.
+template <int LPR, class Acc, bool kList, bool kQ, int U, class Pre = NoPre>
 __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char *lds, const int32_t *rows,
                                                 int64_t lo, int64_t hi, int Ft, const uint4 *rec,
-                                                double goss_mult, const QCtx *qc = nullptr, uint4 *rec_w = nullptr) {
+                                                double goss_mult, const QCtx *qc = nullptr, uint4 *rec_w = nullptr,
+                                                Pre pre = Pre()) {
     const int ls = s.lds_stride;
     const int sub = threadIdx.x % LPR;
     const int rr = threadIdx.x / LPR;
     const int rpp = blockDim.x / LPR;
     const int64_t step = (int64_t)U * rpp;
     const uint32_t n32 = (uint32_t)s.n;  // n < 2^31
-    if (lo >= hi) return;
+    if (lo >= hi) {
+        pre();
+        return;
+    }
     // Every load is unconditional (an entry past the range loads the last
     // row again and is masked off when added): branches around loads would
     // make the compiler wait for every load in flight at each of them.
@@ -2200,6 +2210,7 @@ __device__ __forceinline__ void accumulate_rows(const DevState &s, unsigned char
     load_ids(i0, id_cur);
     load_recs(i0, id_cur, w_cur, qv, qv2, qw, fg, fh, fw);
     load_ids(i0 + step, id_nxt);
+    pre();
     // The next step's loads are issued unconditionally (past the range they
     // re-read the last row): under a branch, the compiler's wait for the
     // current records at the join would also wait for them, and loads would
@@ -2649,10 +2660,12 @@ __global__ __launch_bounds__(kAccThreads) void k_accum(DevState s) {
         const int64_t hi_item = readlane_i64(ait.hi, q);
         const int64_t hi = lo + bh.chunk_a < hi_item ? lo + bh.chunk_a : hi_item;
         const int buf = __builtin_amdgcn_readlane(ait.buf, q);
-        Acc::template zero<LPR>(lds, Ft, ls);
-        __syncthreads();
+        // the histogram is zeroed while the task's first records load
         accumulate_rows<LPR, Acc, true, false, std::is_same<Acc, FAcc>::value ? kAccUnrollF : kAccUnroll>(
-            s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec, goss_mult);
+            s, lds, buf ? s.rows1 : s.rows0, lo, hi, Ft, rec, goss_mult, nullptr, nullptr, [&]() {
+                Acc::template zero<LPR>(lds, Ft, ls);
+                __syncthreads();
+            });
         __syncthreads();
         Acc::template store<LPR>(s, lds, blk, f0, Ft);
         __syncthreads();  // the LDS histogram is zeroed again for the next task
