@@ -365,7 +365,7 @@ void ensure_records(mbh_dataset *ds, const RecLayout &l) {
 // n / kPartChunkMin + (batch size) of them at most, spread over about two
 // tasks per CU.
 constexpr int64_t kHistChunkMin = 2048;
-constexpr int64_t kHistChunkMinF = 512;  // fp32 cells
+constexpr int64_t kHistChunkMinF = 1536;  // fp32 cells
 
 void configure_hist(mb::DevState &s, const mbh_dataset *ds, int B, int kind, Run &run) {
     const bool quantized = kind != mb::kAccFloat;
