@@ -101,6 +101,41 @@ def test_training_categorical_onehot_and_small_groups(dev):
         compare(fit, ref, n)
 
 
+def test_training_categorical_tied_keys_around_64_categories(dev):
+    """Twin categories with equal sort keys, on both sides of the search's
+    64-category boundary (below it a half's four waves rank bins 0-63
+    together, from 64 on each lane ranks its own bin): rows come in pairs
+    identical but for their category (c and c + 32), so with nearest
+    rounding the twins' gradient sums, keys and counts are equal wherever
+    both sit in one leaf, and the rank must keep the lower bin first."""
+    m = 30_000
+    rng = np.random.default_rng(21)
+    num = np.repeat(rng.normal(size=(2, m)), 2, axis=1)          # twins share the numbers
+    a = rng.integers(0, 32, size=m)
+    b = rng.integers(0, 33, size=m)
+    twin = np.arange(2 * m) % 2
+    col64 = np.repeat(a, 2) + 32 * twin                           # 64 categories
+    col65 = np.repeat(b, 2) + 32 * twin                           # 65 categories
+    col63 = rng.integers(0, 63, size=2 * m)                       # 63 categories, no twins
+    eff_a, eff_b = rng.normal(size=32), rng.normal(size=33)
+    z = num[0] - 0.5 * num[1] + np.repeat(eff_a[a] + 0.7 * eff_b[b], 2)
+    y = z + 0.1 * np.repeat(rng.normal(size=m), 2)
+    x = np.vstack([num, col64, col65, col63]).astype(np.float64)
+    n, f = 2 * m, x.shape[0]
+    cat_idx = [2, 3, 4]
+    bins, mb, nc = dev.bin_dense(x.ravel(), n, f, max_bins=255, categorical=cat_idx)
+    assert nc.tolist() == [0, 0, 64, 65, 63]
+    extra = dict(max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=5.0, cat_l2=1.0,
+                 min_data_per_group=20)
+    kw = dict(objective=0, num_iterations=5, num_leaves=31, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.2, stochastic_rounding=0)
+    fit = dev.Dataset(bins, n, f, 255, y, missing_bin=mb, n_categories=nc).train(**kw, **extra)
+    p, keep = O.categorical_params(nc, **kw, **extra, use_quantized_grad=1)
+    ref = O.train(bins, n, f, 255, y, p, missing_bin=mb)
+    assert ((fit.feature >= 2) & (fit.threshold < 0)).sum() > 0
+    compare(fit, ref, n)
+
+
 def test_training_categorical_fp32(dev):
     """fp32 gradients with fp64 histogram sums (the reference's own path):
     the sums differ from the oracle's only in rounding order, so the bar is
