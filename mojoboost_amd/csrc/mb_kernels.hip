@@ -830,9 +830,11 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
             s.stats64[(1 - rd.parity) * 2 + 1] = 0ULL;
         }
     }
-    // no pairs to write and every row in order (no bag, no GOSS sample):
-    // nothing per row (the host then launches one block)
-    if (!(hp.quantized && write_pairs) && !gs_on && !hp.bagging) return;
+    // the round's GOSS sample is copied into the root list per class tree
+    // (one tree per round: k_goss_scatter wrote it there)
+    const bool copy_sample = gs_on && hp.num_class > 1;
+    // no pairs to write and no list to fill: nothing per row
+    if (!(hp.quantized && write_pairs) && !copy_sample && !(hp.bagging && !gs_on)) return;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int rec = s.rec_bytes;
     for (int64_t r0 = (int64_t)blockIdx.x * blockDim.x; r0 < s.n; r0 += stride) {
@@ -859,7 +861,7 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
             }
         }
         if (gs_on) {
-            if (r < gst.bag_n) {
+            if (copy_sample && r < gst.bag_n) {
                 const int32_t rr = s.goss_rows[r];
                 s.rows0[r] = rr;
                 // interleaved binary32 derivatives: the row's GOSS weight bit
@@ -1661,12 +1663,21 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_scatter(DevState s) {
     int pre[4];
     goss_block_prefix(in, pre, wc);
     const int64_t base = s.goss_blk[blockIdx.x];
+    // one tree per round: the sample goes straight into the root's row list
+    // (several class trees each copy it from goss_rows instead), and a kept
+    // small-gradient row's weight bit into its interleaved hessian's sign bit
+    const bool direct = s.hp.num_class == 1;
+    int32_t *dst = direct ? s.rows0 : s.goss_rows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t r = r0 + j * 256;
         if (r < n) {
-            if (in[j]) s.goss_rows[base + pre[j]] = (int32_t)r;
+            if (in[j]) dst[base + pre[j]] = (int32_t)r;
             s.goss_other[r] = other[j] ? 1 : 0;
+            if (direct && other[j] && s.gh2) {
+                uint32_t *hw = (uint32_t *)(s.gh2 + 2 * (size_t)r + 1);
+                *hw = *hw | 0x80000000u;
+            }
         }
     }
 }
@@ -1686,7 +1697,7 @@ __global__ __launch_bounds__(256) void k_goss_stats(DevState s) {
     double mg = 0.0, mh = 0.0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < g.bag_n; j += stride) {
-        const int32_t r = s.goss_rows[j];
+        const int32_t r = (s.hp.num_class == 1 ? s.rows0 : s.goss_rows)[j];
         const double m = s.goss_other[r] ? mult : 1.0;
         const double ag = fabs((double)s.grad[r] * m), ah = fabs((double)s.hess[r] * m);
         if (isfinite(ag) && isfinite(ah)) {
