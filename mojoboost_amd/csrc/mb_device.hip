@@ -655,6 +655,7 @@ TrainBuffers setup_state(mbh_dataset *ds, const mbh_params *p, Run &run, int64_t
             HIPX(hipMemcpy(s.goss_kappa + ds->n, pad.data(), pad.size() * sizeof(int32_t), hipMemcpyHostToDevice));
         }
         s.goss_mask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
+        s.goss_topmask = dalloc<unsigned long long>((ds->n + 63) / 64, run.owned);
         s.goss_blk = dalloc<int32_t>(s.goss_nblk, run.owned);
         s.goss_blk_u = dalloc<int32_t>(s.goss_nblk, run.owned);
         s.goss_ukappa = dalloc<int32_t>(padded, run.owned);  // whole count tiles

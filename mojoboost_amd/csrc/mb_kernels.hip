@@ -1291,6 +1291,17 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_count(DevState s, int 
             }
         }
     }
+    if (mode == 0) {
+        // the top rows' bits, for the kappa pass (it need not read the
+        // derivatives again): slot j of the wave's lanes is one 64-row word
+        const int lane = lane_id(), w = threadIdx.x >> 6;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned long long m = __ballot(in[j]);
+            const int64_t rw = (int64_t)blockIdx.x * 1024 + j * 256 + w * 64;
+            if (lane == 0 && rw < n) s.goss_topmask[rw >> 6] = m;
+        }
+    }
     const int t = goss_block_count(in, wc);
     if (threadIdx.x == 0) s.goss_blk[blockIdx.x] = t;
 }
@@ -1380,12 +1391,12 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_kappa(DevState s) {
     const int64_t r0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
     const int lane = lane_id(), w = threadIdx.x >> 6;
     const int64_t top_before_blk = s.goss_blk[blockIdx.x];
-    const unsigned long long thr = (unsigned long long)__double_as_longlong(g.threshold);
     bool top[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t r = r0 + j * 256;
-        top[j] = r < n && goss_top(s, r, thr);
+        const int64_t rw = (int64_t)blockIdx.x * 1024 + j * 256 + w * 64;
+        top[j] = r < n && ((s.goss_topmask[rw >> 6] >> lane) & 1ULL);  // k_goss_count(0)'s bits
     }
     int pre[4];
     goss_block_prefix(top, pre, wc);

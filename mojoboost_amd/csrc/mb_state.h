@@ -348,6 +348,7 @@ struct DevState {
     int32_t *goss_ccnt;         // kGossDigitBlocks: their counts
     int32_t *goss_kappa;        // n: top row -> INT_MIN, else the count bound of the sampling
     unsigned long long *goss_mask;  // ceil(n / 64): rows kept by the sampling
+    unsigned long long *goss_topmask;  // ceil(n / 64): top rows (importance at or above the threshold)
     int32_t *goss_blk;          // per 1024-row block counts, then their exclusive prefix
     int32_t *goss_blk_u;        // per block: rows the band leaves open, then their prefix
     int32_t *goss_ukappa;       // the open rows in row order: kappa - certain keeps before it
