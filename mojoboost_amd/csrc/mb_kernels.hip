@@ -1287,7 +1287,8 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_count(DevState s, int 
                 in[j] = goss_top(s, r, thr);
             } else {
                 const bool other = goss_kept_bit(s, r);
-                in[j] = mode == 2 ? other : (s.goss_kappa[r] == INT_MIN || other);
+                // a top row: its bit of k_goss_count(0)'s words (its kappa is INT_MIN)
+                in[j] = mode == 2 ? other : (((s.goss_topmask[r >> 6] >> (r & 63)) & 1ULL) != 0 || other);
             }
         }
     }
@@ -1666,7 +1667,7 @@ __global__ __launch_bounds__(kGossRowThreads) void k_goss_scatter(DevState s) {
         bool top = false;
         other[j] = false;
         if (r < n) {
-            top = s.goss_kappa[r] == INT_MIN;
+            top = ((s.goss_topmask[r >> 6] >> (r & 63)) & 1ULL) != 0;  // its kappa is INT_MIN
             other[j] = !top && goss_kept_bit(s, r);
         }
         in[j] = top || other[j];
