@@ -1622,19 +1622,25 @@ __global__ __launch_bounds__(1024) void k_goss_walk(DevState s, int list) {
                 const int o = st + 1 < kGossTile / kGossStep ? (st + 1) * kGossStep : 0;
                 const int n0 = cur[o + lane], n1 = cur[o + 64 + lane], n2 = cur[o + 128 + lane],
                           n3 = cur[o + 192 + lane];
-                const int hi = cnt + kGossStep - 1;
-                const unsigned long long a0 = __ballot(k0 > hi), a1 = __ballot(k1 > hi),
-                                         a2 = __ballot(k2 > hi), a3 = __ballot(k3 > hi);
-                const unsigned long long z0 = __ballot(k0 <= cnt), z1 = __ballot(k1 <= cnt),
-                                         z2 = __ballot(k2 <= cnt), z3 = __ballot(k3 <= cnt);
                 unsigned long long m0, m1, m2, m3;
-                if (((a0 | z0) & (a1 | z1) & (a2 | z2) & (a3 | z3)) == ~0ULL) {
+                bool whole = false;
+                if (!list) {  // launch-uniform
+                    // the whole step at once when no kappa lies within
+                    // 256 above the count (the open rows' kappas, within
+                    // the band around the count, almost never allow it)
+                    const int hi = cnt + kGossStep - 1;
+                    const unsigned long long a0 = __ballot(k0 > hi), a1 = __ballot(k1 > hi),
+                                             a2 = __ballot(k2 > hi), a3 = __ballot(k3 > hi);
+                    const unsigned long long z0 = __ballot(k0 <= cnt), z1 = __ballot(k1 <= cnt),
+                                             z2 = __ballot(k2 <= cnt), z3 = __ballot(k3 <= cnt);
+                    whole = ((a0 | z0) & (a1 | z1) & (a2 | z2) & (a3 | z3)) == ~0ULL;
                     m0 = a0;
                     m1 = a1;
                     m2 = a2;
                     m3 = a3;
-                    cnt += __popcll(a0) + __popcll(a1) + __popcll(a2) + __popcll(a3);
-                } else {
+                    if (whole) cnt += __popcll(a0) + __popcll(a1) + __popcll(a2) + __popcll(a3);
+                }
+                if (!whole) {
                     m0 = goss_slice(k0, cnt);
                     m1 = goss_slice(k1, cnt);
                     m2 = goss_slice(k2, cnt);
