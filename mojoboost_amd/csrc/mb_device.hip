@@ -1281,7 +1281,10 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             // with the pairs written by the root build and no row list to
             // gather (no bag, no GOSS), one block publishes the scales
             const bool q_rows = !fuse_q || s.hp.bagging || s.hp.goss;
-            HIPX(mb::launch_quantize(s, q_rows ? grid_rows : 1, st, !fuse_q));
+            // ... in the previous tree's round-end launch when nothing is
+            // launched between the two
+            const bool merge_rq = K == 1 && fuse_objective && !s.hp.goss && !s.hp.wide && !q_rows;
+            if (!(merge_rq && t > 0)) HIPX(mb::launch_quantize(s, q_rows ? grid_rows : 1, st, !fuse_q));
             if (timed) HIPX(mb::launch_hist(s, st, events[2], events[3], fuse_q));
             else HIPX(mb::launch_hist(s, st, nullptr, nullptr, fuse_q));
             HIPX(mb::launch_scan(s, 1, st));
@@ -1342,7 +1345,8 @@ int32_t mbh_train(mbh_dataset *ds, const mbh_params *p, mbh_fit **out, char *err
             }
             if (fuse_objective && t + 1 < T) HIPX(mb::launch_score_objective(s, grid_score_obj, st));
             else HIPX(mb::launch_score(s, grid_score, st));
-            HIPX(mb::launch_round_end(s, st));
+            if (merge_rq && t + 1 < T) HIPX(mb::launch_round_end_quantize(s, st));
+            else HIPX(mb::launch_round_end(s, st));
         }
         HIPX(hipStreamSynchronize(st));
         auto t1 = std::chrono::steady_clock::now();

@@ -46,6 +46,7 @@ hipError_t launch_score(const DevState &s, int grid, hipStream_t st);
 // and binary): after it, the next tree skips launch_objective.
 hipError_t launch_score_objective(const DevState &s, int grid, hipStream_t st);
 hipError_t launch_round_end(const DevState &s, hipStream_t st);
+hipError_t launch_round_end_quantize(const DevState &s, hipStream_t st);
 hipError_t launch_round_combine(const RoundStates &rs, int sampling, hipStream_t st);
 // Grid of a grid-stride rows kernel: as many blocks per CU as its registers
 // and LDS let stay resident (at most 8), times n_cu, so that every block runs

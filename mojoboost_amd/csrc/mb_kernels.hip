@@ -800,7 +800,7 @@ __device__ __forceinline__ int32_t quant_value(const QCtx &c, float v, bool w, i
 // write_pairs = 0: the max-abs int8 pairs are left to the root build
 // (k_hist quantizes the rows it reads, k_hist<.., kQuant>); the scales and
 // the root row list are still published here.
-__global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
+__device__ __forceinline__ void quantize_body(const DevState &s, int write_pairs) {
     const Round rd = *s.round;
     if (rd.stopped) return;
     const HyperParams &hp = s.hp;
@@ -891,6 +891,8 @@ __global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) {
         }
     }
 }
+
+__global__ __launch_bounds__(256) void k_quantize(DevState s, int write_pairs) { quantize_body(s, write_pairs); }
 
 // ------------------------------------------------ magnitude-sum lattice
 // The magnitude reduction of the reference's device histogram, in its fixed
@@ -5547,7 +5549,7 @@ __global__ __launch_bounds__(256) void k_score_objective(DevState s) {
 }
 
 // Archive the finished tree and advance the round state (one block).
-__global__ __launch_bounds__(256) void k_round_end(DevState s) {
+__device__ __forceinline__ void round_end_body(const DevState &s) {
     const Round rd = *s.round;
     const int mn = s.max_nodes;
     int32_t *ai = s.arc_int + (size_t)rd.tree_index * (6 * mn + 2);
@@ -5607,6 +5609,18 @@ __global__ __launch_bounds__(256) void k_round_end(DevState s) {
         nr.parity = 1 - rd.parity;
         *s.round = nr;
     }
+}
+
+__global__ __launch_bounds__(256) void k_round_end(DevState s) { round_end_body(s); }
+
+// The end of a tree and the next tree's one-block quantizer launch in one
+// (both one block, in order): used when no launch comes between them (one
+// output, the objective fused into the score update, no GOSS, no
+// magnitude-sum lattice, the pairs written by the root build).
+__global__ __launch_bounds__(256) void k_round_end_quantize(DevState s) {
+    round_end_body(s);
+    __syncthreads();  // the advanced round state, written by thread 0
+    quantize_body(s, 0);
 }
 
 // The round's stop rule when several states grow its class trees side by
@@ -5966,6 +5980,10 @@ hipError_t launch_round_combine(const RoundStates &rs, int sampling, hipStream_t
 }
 hipError_t launch_round_end(const DevState &s, hipStream_t st) {
     hipLaunchKernelGGL(k_round_end, dim3(1), dim3(256), 0, st, s);
+    return hipGetLastError();
+}
+hipError_t launch_round_end_quantize(const DevState &s, hipStream_t st) {
+    hipLaunchKernelGGL(k_round_end_quantize, dim3(1), dim3(256), 0, st, s);
     return hipGetLastError();
 }
 hipError_t launch_build_records(const uint8_t *bins_cm, uint8_t *records, int64_t n, int F, int rec,
