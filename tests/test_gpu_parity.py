@@ -374,6 +374,23 @@ def test_training_fp32_c1(dev):
     assert _tree_agreement(fit, ref) >= 95
 
 
+@pytest.mark.parametrize("nb", [5, 13, 64])
+def test_training_fp32_few_bins(dev, nb):
+    """fp32 path at bin counts that take the scan's short paths: fewer than
+    eight cells (no full eight-cell block: the totals are the remainder's
+    sequential sum), one full block and a remainder, and whole blocks only;
+    the same splits as the oracle, raw scores within 1e-5."""
+    n, f = 40_000, 8
+    bins, y, mb, nbb = c2_like(n, f=f, seed=31 + nb, nb=nb)
+    kw = dict(objective=1, num_iterations=8, num_leaves=15, min_data_in_leaf=20, lambda_l2=1.0,
+              learning_rate=0.2)
+    fit = dev.Dataset(bins, n, f, nbb, y, missing_bin=mb).train(use_quantized_grad=0, **kw)
+    ref = O.train(bins, n, f, nbb, y, O.default_params(**kw, use_quantized_grad=0), missing_bin=mb)
+    assert fit.n_trees == ref.n_trees
+    assert _tree_agreement(fit, ref) >= ref.n_trees - 1
+    assert _rel_err(fit.train_raw(), ref.train_raw(n)) < 1e-5
+
+
 def test_training_fp32_binary_bagging(dev):
     n = 150_000
     bins, y, mb, nb = c2_like(n, f=16)
