@@ -167,7 +167,9 @@ constexpr int kHistBlocksPerCU = MB_HIST_BPC;
 constexpr int kGossTileRows = 16384;
 constexpr int kGossHistSlots = 8;  // partial digit histograms per radix pass
 constexpr int kStatSlots = 64;  // slots of each max |g|, |h| (parity x grad/hess x slot)
-constexpr int kGossDigitBlocks = 1024;  // blocks of a radix-select pass, each a contiguous row range
+// blocks of a radix-select pass, each a contiguous row range (C3: 2048 ran
+// 0.5 % faster per 500 trees than 1024 or 4096)
+constexpr int kGossDigitBlocks = 2048;
 
 // The state of a run before its first tree: no sampling, unit GOSS weight.
 inline Round initial_round() {
