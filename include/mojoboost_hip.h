@@ -71,7 +71,9 @@ typedef struct {
     /* GOSS count: decisions outside a band of goss_band standard deviations
      * (+64) around the count's expectation are taken in parallel and checked
      * exactly; goss_exact_walk = 1 always runs the full sequential count.
-     * Both give the reference's sample. Defaults 10 and 0. */
+     * Both give the reference's sample. Defaults 6 and 0 (at 6 the
+     * check fails in well under one round in 10^5; C3 ran 0.5 % faster per
+     * 500 trees than at 10). */
     double goss_band;
     int32_t goss_exact_walk;
     /* lambdarank (LightGBM names): pairs whose better-ranked member sits

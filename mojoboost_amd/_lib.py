@@ -91,7 +91,7 @@ def mbh_params(**kw) -> MbhParams:
                   feature_fraction_seed=2, bagging_fraction=1.0, bagging_freq=0,
                   bagging_seed=3, num_grad_quant_bins=4, stochastic_rounding=1,
                   quant_seed=11, time_histograms=0, use_quantized_grad=1, goss=0,
-                  top_rate=0.2, other_rate=0.1, goss_band=10.0, goss_exact_walk=0,
+                  top_rate=0.2, other_rate=0.1, goss_band=6.0, goss_exact_walk=0,
                   lambdarank_truncation_level=30, lambdarank_norm=1, lambdarank_sigmoid=1.0,
                   max_cat_to_onehot=4, max_cat_threshold=32, cat_smooth=10.0, cat_l2=10.0,
                   min_data_per_group=100, one_hot_max_size=-1, quant_scale_rule=0,

@@ -175,7 +175,7 @@ Config parse(const char *spec) {
     p.objective = MBH_OBJ_REGRESSION;
     p.num_class = 1;
     p.goss = 0;
-    p.goss_band = 10.0;
+    p.goss_band = 6.0;
     p.goss_exact_walk = 0;
     p.top_rate = 0.2;    // LightGBM / GossParams defaults
     p.other_rate = 0.1;
